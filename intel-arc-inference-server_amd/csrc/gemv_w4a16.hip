@@ -1,0 +1,233 @@
+// gemv_w4a16.hip - the W4A16 GPTQ group-64 linear for M = 1..16 rows on gfx950.
+//
+// Replaces the reference's `gemv` (src/kernels/gemv.cl:124-221) and, for M >= 2, its
+// small-M `gemm_sm` (src/kernels/gemm_sm.cl:161): same operands and the same output
+// contract - fp32 split-K partials [S][M][N] that the consumer folds in slice order
+// (tests/kernels/gemm_sm_ref.h:106-136) - with an MI355X-native inner loop.
+//
+// Weights stay in GPTQ layout 0 (qweight u32 [K/8][N], nibble i of word (r, n) is
+// k = 8r + i; scales f16 [K/64][N]; zero point 8), which already streams coalesced:
+//
+//   * A work-group is 4 wave64s on one 64-column tile; grid (N / 64, S). Slice s owns
+//     k-groups [s G/S, (s+1) G/S); wave w takes every 4th of them.
+//   * Lane l reads one 16-byte uint4 = 4 adjacent columns (n0 + 4 (l % 16) .. + 3) of word
+//     row (l / 16) of a 4-row quarter group: each 16-lane quarter-wave reads 256 contiguous
+//     bytes, the wave 1 KB, with non-temporal loads (weights are read once per token).
+//   * The contraction runs on the matrix cores: v_mfma_f32_16x16x32_f16 with A = the M
+//     activation rows (zero-padded to 16) and B = 32 k x 16 columns of dequantised
+//     weights. Lane l's B operand is exactly its word: 8 consecutive k of one column, so
+//     the dequant is register-local - two v_and_or_b32 of the word (and of word >> 8)
+//     against the fp16 magic 0x6400 give (1024 + q) or (1024 + 16 q) in each half, and
+//     one packed f16 add / fma takes them to q - 8 exactly. The halves come out paired
+//     (k0,k4)(k1,k5)(k2,k6)(k3,k7); the activation octet is permuted the same way
+//     (v_perm_b32), so the MFMA sums the right products.
+//   * Per k-group the 16x16 fp32 tile starts from zero, then acc = fma(tile, scale, acc)
+//     per column (the reference's acc += gacc * scale per group); the 4 waves' partials
+//     are summed in wave order through LDS and written as one slice.
+//
+// Property R (gemm_sm.cl:36-41): row m's result does not depend on M or on the other
+// rows - every output element is its own MFMA dot and the same fixed merges - so S and
+// the wave split are functions of the shape only (mi_gemv_pick_s).
+//
+// No atomics: replays are bitwise identical.
+#include "mi_common.h"
+#include "mi_capi_internal.h"
+
+namespace mi {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kCols = 64;
+
+// 8 dequantised int4 weights of one word, in the pair order (q0,q4)(q1,q5)(q2,q6)(q3,q7).
+__device__ __forceinline__ h8_t dequant_word(uint32_t w, uint32_t m_lo, uint32_t m_hi,
+                                             uint32_t magic) {
+  const h2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
+  const h2_t s16 = {(half_t)0.0625f, (half_t)0.0625f};
+  const h2_t b72 = {(half_t)-72.0f, (half_t)-72.0f};
+  const uint32_t t = w >> 8;
+  const h2_t p0 = as_h2(and_or(w, m_lo, magic)) - b1032;                          // 1024+q   -> q-8
+  const h2_t p1 = __builtin_elementwise_fma(as_h2(and_or(w, m_hi, magic)), s16, b72);  // 1024+16q -> q-8
+  const h2_t p2 = as_h2(and_or(t, m_lo, magic)) - b1032;
+  const h2_t p3 = __builtin_elementwise_fma(as_h2(and_or(t, m_hi, magic)), s16, b72);
+  return h8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// 8 natural-order activations (x0..x7 in four u32) into the same pair order.
+__device__ __forceinline__ h8_t perm_x(u4_t v) {
+  const uint32_t a0 = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);  // (x0, x4)
+  const uint32_t a1 = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);  // (x1, x5)
+  const uint32_t a2 = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);  // (x2, x6)
+  const uint32_t a3 = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);  // (x3, x7)
+  const h2_t b0 = as_h2(a0), b1 = as_h2(a1), b2 = as_h2(a2), b3 = as_h2(a3);
+  return h8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+}
+
+// MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together.
+template <int MR, int U>
+__global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ x,
+                                                         float* __restrict__ partials, uint32_t M,
+                                                         uint32_t K, uint32_t N, uint32_t gps) {
+  constexpr int RR = MR < 4 ? MR : 4;  // accumulator rows a lane holds (rows 4*(l/16) + r)
+  __shared__ float red[kWaves][MR][kCols];
+
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t c4 = lane & 15u, q = lane >> 4;
+  const uint32_t n0 = blockIdx.x * kCols;
+  const uint32_t ncol = n0 + 4u * c4;
+  const uint32_t s = blockIdx.y;
+  const uint32_t g_begin = s * gps + wave;
+  const uint32_t g_end = (s + 1) * gps;
+  const bool xrow = c4 < M;  // this lane feeds activation row c4 of the A operand
+
+  const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
+
+  float acc[4][RR];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < RR; ++r) acc[c][r] = 0.f;
+
+  for (uint32_t g0 = g_begin; g0 < g_end; g0 += kWaves * U) {
+    u4_t wv[U][2];
+    u2_t sv[U];
+    u4_t xv[U][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = g0 + u * kWaves;
+      if (g < g_end) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t row = g * 8u + 4u * h + q;
+          wv[u][h] = load_stream16(qweight + (size_t)row * N + ncol);
+          if (xrow)
+            xv[u][h] = *reinterpret_cast<const u4_t*>(x + (size_t)c4 * K + g * 64u + 32u * h + 8u * q);
+          else
+            xv[u][h] = u4_t{0u, 0u, 0u, 0u};
+        }
+        sv[u] = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + ncol);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = g0 + u * kWaves;
+      if (g < g_end) {
+        f4_t d[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d[c] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const h8_t a = perm_x(xv[u][h]);
+          const uint32_t ws[4] = {wv[u][h].x, wv[u][h].y, wv[u][h].z, wv[u][h].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            d[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, dequant_word(ws[c], m_lo, m_hi, magic), d[c], 0, 0, 0);
+        }
+        const float sc[4] = {h2f((uint16_t)(sv[u].x & 0xFFFFu)), h2f((uint16_t)(sv[u].x >> 16)),
+                             h2f((uint16_t)(sv[u].y & 0xFFFFu)), h2f((uint16_t)(sv[u].y >> 16))};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < RR; ++r) acc[c][r] = __builtin_fmaf(d[c][r], sc[c], acc[c][r]);
+      }
+    }
+  }
+
+  // Lane l holds rows 4 q + r of columns ncol .. ncol+3: stage them, then sum the waves.
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    const uint32_t row = 4u * q + r;
+    if (row < (uint32_t)MR) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[wave][row][4u * c4 + c] = acc[c][r];
+    }
+  }
+  __syncthreads();
+  const uint32_t total = M * kCols;
+  for (uint32_t i = threadIdx.x; i < total; i += 256u) {
+    const uint32_t row = i / kCols, col = i % kCols;
+    float v = red[0][row][col];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += red[w][row][col];
+    partials[((size_t)s * M + row) * N + n0 + col] = v;
+  }
+}
+
+// out[m][n] (fp16 or fp32) = sum over s ascending of partials[s][m][n], from 0.f.
+__global__ __launch_bounds__(256) void fold_partials_kernel(const float* __restrict__ partials,
+                                                            uint16_t* __restrict__ out16,
+                                                            float* __restrict__ out32,
+                                                            uint32_t S, uint32_t MN) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= MN) return;
+  float t = 0.f;
+  for (uint32_t s = 0; s < S; ++s) t += partials[(size_t)s * MN + i];
+  if (out16) out16[i] = f2h(t);
+  if (out32) out32[i] = t;
+}
+
+template <int MR>
+int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part,
+                uint32_t M, uint32_t K, uint32_t N, uint32_t S, hipStream_t st) {
+  const uint32_t G = K / 64, gps = G / S;
+  dim3 grid(N / kCols, S);
+  if (gps >= 16)
+    gemv_w4a16_kernel<MR, 4><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps);
+  else
+    gemv_w4a16_kernel<MR, 2><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
+  // The split-K width for a shape: enough waves to keep every CU's load queues full
+  // (about 2048 or more), at least 2 k-groups per wave where the shape allows; S | K/64.
+  const uint32_t G = K / 64, tiles = N / kCols;
+  uint32_t best = 1;
+  for (uint32_t S = 1; S <= G; ++S) {
+    if (G % S) continue;
+    const uint32_t gpw = (G / S + kWaves - 1) / kWaves;
+    if (gpw < 2 && S > 1) break;
+    best = S;
+    if (tiles * S * kWaves >= 2048 && gpw <= 8) break;
+  }
+  return best;
+}
+
+extern "C" int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
+                             float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,
+                             void* stream) {
+  if (!qweight || !scales || !x || !partials) return mi_fail(MI_ERR_ARG, "gemv_w4a16: null pointer");
+  if (M < 1 || M > 16) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: M must be 1..16");
+  if (K == 0 || K % 64 || N == 0 || N % 64)
+    return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: K and N must be non-zero multiples of 64");
+  if (S == 0 || (K / 64) % S) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: S must divide K/64");
+  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(scales) % 8)
+    return mi_fail(MI_ERR_ARG, "gemv_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int e;
+  if (M == 1)
+    e = launch_gemv<1>(qweight, scales, x, partials, M, K, N, S, st);
+  else if (M <= 4)
+    e = launch_gemv<4>(qweight, scales, x, partials, M, K, N, S, st);
+  else
+    e = launch_gemv<16>(qweight, scales, x, partials, M, K, N, S, st);
+  return mi_hip(e, "gemv_w4a16 launch");
+}
+
+extern "C" int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,
+                                uint32_t M, uint32_t N, void* stream) {
+  if (!partials || (!out_f16 && !out_f32) || S == 0)
+    return mi_fail(MI_ERR_ARG, "fold_partials: bad arguments");
+  const uint32_t MN = M * N;
+  fold_partials_kernel<<<(MN + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      partials, out_f16, out_f32, S, MN);
+  return mi_hip((int)hipGetLastError(), "fold_partials launch");
+}

@@ -1,0 +1,10 @@
+// mi_capi_internal.h - error plumbing shared by the C-ABI entry points.
+#pragma once
+#include <stdint.h>
+
+#include "../../include/mi355x_decode.h"
+
+// Records `msg` as the calling thread's last error and returns `code`.
+int mi_fail(int code, const char* msg);
+// Returns `e` (a hipError_t value); records `where` and the HIP error string when non-zero.
+int mi_hip(int e, const char* where);
