@@ -93,6 +93,135 @@ uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N);
 int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,
                      uint32_t M, uint32_t N, void* stream);
 
+
+/* ---- the between-GEMV kernels (src/kernels/prep.cl). Residual stream and normed
+ * activations are f16 [M][K]; norm weights fp32 [K] (the reference bakes fp32 weights,
+ * src/loader/small_layout.h). ---- */
+/* prep_res_fold (prep.cl:288): resid = rne(resid + rne(sum_s partials)) (S_PREV = 0: no
+ * fold), sumsq[g][m] = the chunk's sum of squares, G chunks of ceil(K/G), 256-lane tree. */
+int mi_res_fold(const float* partials, uint16_t* resid, float* sumsq, uint32_t M, uint32_t K,
+                uint32_t S_PREV, uint32_t G, void* stream);
+/* prep_norm_finish (prep.cl:350): x = rne(r * (1/sqrt(sum_g sumsq / K + eps)) * w) */
+int mi_norm_finish(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                   uint32_t M, uint32_t K, uint32_t G, float eps, void* stream);
+/* prep_res_norm (tests/kernels/prep_ref.h:59-92): both halves in one launch per row */
+int mi_res_norm(const float* partials, uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                uint32_t M, uint32_t K, uint32_t S_PREV, float eps, void* stream);
+/* prep_silu_mul (prep.cl:384): gate||up partials [S][M][2N] interleaved in 16-column blocks
+ * (src/common/repack.h:64-73) -> x = rne(rne(silu(rne(g))) * rne(u)), [M][N] */
+int mi_silu_mul(const float* partials, uint16_t* x_out, uint32_t M, uint32_t N, uint32_t S,
+                void* stream);
+
+/* Attention shape. The fused qkv linear's columns: q heads (interleaved [q_h | gate_h]
+ * per head when gated, src/kernels/attn.cl header) then k at k_off, v at v_off. */
+typedef struct mi_attn_shape {
+  uint32_t q_heads, kv_heads, head_dim, rot_dim;
+  uint32_t gated;
+  uint32_t qkv_n, k_off, v_off;
+  float scale; /* score scale, fp32(1/sqrt(head_dim)) */
+  float eps;   /* q/k RMSNorm epsilon */
+} mi_attn_shape;
+
+/* attn_prep (attn.cl:361-372): fold the qkv partials [S][M][qkv_n], per-head q/k RMSNorm
+ * (q_norm/k_norm fp32 [head_dim], NULL = none), RoPE (rope fp32 [max_len][2][rot_dim/2],
+ * rotate_half pairs), q -> attn_q fp32 [M][q_heads][head_dim], gate -> attn_gate (gated
+ * only), K/V f16 written at the row of position pos + m: element (row, head, d) at
+ * row*row_stride + head*head_stride + d; row = pages[p/page]*page + p%page when pages.
+ * kv_len (positions the cache holds, 0 = unchecked): a position >= kv_len writes nothing
+ * and sets ctrl[MI_CTRL_DEBUG] = 0xDEAD0002. */
+int mi_attn_prep(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
+                 const mi_attn_shape* shape, const float* q_norm, const float* k_norm,
+                 const float* rope, float* attn_q, float* attn_gate, uint16_t* kv_k,
+                 uint16_t* kv_v, size_t row_stride, size_t head_stride, const uint32_t* pages,
+                 uint32_t page, uint32_t kv_len, void* stream);
+/* Positions per attention block for a row attending to `len` keys (attn_v2.cl:138-142). */
+uint32_t mi_attn_ppw(uint32_t len, uint32_t tgt);
+/* attn_decode_v2 (attn_v2.cl:172-188) / attn_decode_v2_kv8 (kv8.cl:535-548): grid
+ * (kv_heads, tgt, M); kv_kind 0 = f16 KV, 1 = int8 KV with f16 scales at
+ * row*sc_row_stride + head*sc_head_stride; attn_part fp32 [q_heads][tgt][M][head_dim+2];
+ * keys at positions >= kv_len are never read (0 = unchecked). */
+int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, const void* kv_k,
+                   const void* kv_v, const uint16_t* k_scale, const uint16_t* v_scale,
+                   size_t row_stride, size_t head_stride, size_t sc_row_stride,
+                   size_t sc_head_stride, const uint32_t* pages, uint32_t page, uint32_t kv_len,
+                   float* attn_part, uint32_t M, uint32_t tgt, const mi_attn_shape* shape,
+                   void* stream);
+/* attn_reduce_v2 (attn_v2.cl:383-386): ascending block merge -> attn_out f16
+ * [M][q_heads*head_dim] (gated: rne(rne(o) * sigmoid(gate))) */
+int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate,
+                   uint16_t* attn_out, uint32_t M, uint32_t tgt, const mi_attn_shape* shape,
+                   void* stream);
+
+/* ---- the token boundary ---- */
+/* embed_gather (embed_gather.cl:47-49): resid[m] = embed[cur_token[m]]; an id >= vocab
+ * writes nothing and sets ctrl[MI_CTRL_DEBUG] = 0xDEAD0001 */
+int mi_embed_gather(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, uint32_t M,
+                    uint32_t hidden, uint32_t vocab, void* stream);
+/* argmax_stage1/2 (argmax.cl:82-83, 133-134): per active row the arg-max of logits fp32
+ * [M][vocab] (ties -> lower index; index >= vocab_used never wins) into out_token[m]; then
+ * cur_token[0] = out_token[n-1], history[steps] = it (when history != NULL and
+ * steps < history_len), steps += 1, pos += n_active. part: mi_argmax_groups(vocab) * M * 8
+ * bytes of scratch. */
+uint32_t mi_argmax_groups(uint32_t vocab);
+int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history,
+              uint32_t history_len, uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
+
+
+/* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
+ * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the
+ * dense GQA decoder this build runs: every layer is attention + SwiGLU MLP, all linears
+ * int4 g64 layout 0, fp16 activations and KV. */
+typedef struct mi_model_desc {
+  uint32_t layers, hidden, q_heads, kv_heads, head_dim, rot_dim, inter, vocab, vocab_used;
+  uint32_t max_len;  /* KV cache rows per layer (positions) */
+  uint32_t qk_norm;  /* 1: per-head RMSNorm on q and k (attn.cl attn_prep) */
+  uint32_t max_rows; /* largest verify step (rows) the engine captures, 1..8 */
+  uint32_t attn_tgt; /* attention blocks per kv head (the v2 grid's TGT) */
+  float rope_theta, rms_eps;
+} mi_model_desc;
+
+typedef struct mi_engine mi_engine;
+
+/* Weight and buffer kinds for mi_engine_tensor (per layer below MI_T_EMBED). */
+enum {
+  MI_T_QKV_Q = 0, MI_T_QKV_S, MI_T_O_Q, MI_T_O_S, MI_T_GU_Q, MI_T_GU_S, MI_T_DOWN_Q, MI_T_DOWN_S,
+  MI_T_IN_NORM, MI_T_POST_NORM, MI_T_Q_NORM, MI_T_K_NORM,
+  MI_T_EMBED = 32, MI_T_FINAL_NORM, MI_T_LM_Q, MI_T_LM_S, MI_T_ROPE, MI_T_KV_K, MI_T_KV_V,
+  MI_T_LOGITS, MI_T_CTRL, MI_T_HISTORY
+};
+
+/* Allocates weights (random-init on the device from `seed`, BASELINE config 2's
+ * distributions: uniform nibbles, scales U(0.002, 0.02), gammas N(1, 0.02) in fp16, embed
+ * and KV N(0, 1)), the KV cache [layers][kv_heads][max_len][head_dim] f16 and all step
+ * buffers. stream NULL: the engine owns a stream. Returns NULL on failure (mi_last_error). */
+mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stream);
+void mi_engine_destroy(mi_engine* e);
+void* mi_engine_stream(mi_engine* e);
+/* Device pointer and size of a weight or buffer (for loading real weights or checks). */
+int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes);
+/* Split-K width of linear `which` (0 qkv, 1 o, 2 gate||up, 3 down, 4 lm_head). */
+int mi_engine_linear_s(mi_engine* e, uint32_t which, uint32_t* S);
+/* runtime::build / build_verify (capture.cc:2135-2144): record the M-row step as a graph. */
+int mi_engine_capture(mi_engine* e, uint32_t M);
+/* Engine::reset: control block cleared, pos and cur_token[0] set, n_active 1. */
+int mi_engine_reset(mi_engine* e, uint32_t pos, uint32_t token);
+/* Engine::replay (engine.cc:702-713): enqueue one captured M-row step (no sync). */
+int mi_engine_replay(mi_engine* e, uint32_t M);
+/* Engine::generate (engine.cc:726-750): n greedy tokens; the ids land in `tokens`. */
+int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens);
+/* Engine::ingest (engine.cc:715-724): one step per prompt id. */
+int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
+int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
+/* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
+ * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. */
+int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);
+/* Engine::commit (engine.cc:927-960): pos = verify_pos + j + 1, cur_token[0] = next. */
+int mi_engine_commit(mi_engine* e, uint32_t verify_pos, uint32_t j, uint32_t next);
+/* server::accept_greedy (src/server/spec_accept.cc:81-85): the accepted draft count j;
+ * *next = verify_argmax[j]. */
+uint32_t mi_accept_greedy(const uint32_t* verify_argmax, const uint32_t* drafts, uint32_t k,
+                          uint32_t* next);
+
 /* ---- measurement: a plain streaming read of `bytes` (the probe_bw rate,
  * tools/probe/probe_bw) ---- */
 int mi_stream_read(const void* p, size_t bytes, uint32_t* sink, void* stream);

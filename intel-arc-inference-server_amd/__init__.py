@@ -41,6 +41,31 @@ SIGNATURES = {
     "mi_gemv_pick_s": (u32, [u32, u32]),
     "mi_fold_partials": (i32, [vp, vp, vp, u32, u32, u32, vp]),
     "mi_stream_read": (i32, [vp, sz, vp, vp]),
+    "mi_res_fold": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "mi_norm_finish": (i32, [vp, vp, vp, vp, u32, u32, u32, f32, vp]),
+    "mi_res_norm": (i32, [vp, vp, vp, vp, u32, u32, u32, f32, vp]),
+    "mi_silu_mul": (i32, [vp, vp, u32, u32, u32, vp]),
+    "mi_attn_prep": (i32, [vp, vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, u32, vp]),
+    "mi_attn_ppw": (u32, [u32, u32]),
+    "mi_attn_decode": (i32, [vp, vp, u32, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, vp, u32, u32, vp, vp]),
+    "mi_attn_reduce": (i32, [vp, vp, vp, vp, u32, u32, vp, vp]),
+    "mi_embed_gather": (i32, [vp, vp, vp, u32, u32, u32, vp]),
+    "mi_argmax_groups": (u32, [u32]),
+    "mi_argmax": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
+    "mi_engine_create": (vp, [vp, u64, vp]),
+    "mi_engine_destroy": (None, [vp]),
+    "mi_engine_stream": (vp, [vp]),
+    "mi_engine_tensor": (i32, [vp, u32, u32, C.POINTER(vp), C.POINTER(sz)]),
+    "mi_engine_linear_s": (i32, [vp, u32, C.POINTER(u32)]),
+    "mi_engine_capture": (i32, [vp, u32]),
+    "mi_engine_reset": (i32, [vp, u32, u32]),
+    "mi_engine_replay": (i32, [vp, u32]),
+    "mi_engine_generate": (i32, [vp, u32, vp]),
+    "mi_engine_ingest": (i32, [vp, vp, u32]),
+    "mi_engine_read_ctrl": (i32, [vp, vp]),
+    "mi_engine_verify": (i32, [vp, vp, u32, vp]),
+    "mi_engine_commit": (i32, [vp, u32, u32, u32]),
+    "mi_accept_greedy": (u32, [vp, vp, u32, vp]),
 }
 
 
@@ -81,3 +106,138 @@ def header_functions():
         text = f.read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+# ---- the decode loop (host-side mirror of src/runtime/engine.h) -------------------------
+class ModelDesc(C.Structure):
+    """mi_model_desc: the model's shape as data (model::ModelDesc)."""
+    _fields_ = [("layers", u32), ("hidden", u32), ("q_heads", u32), ("kv_heads", u32),
+                ("head_dim", u32), ("rot_dim", u32), ("inter", u32), ("vocab", u32),
+                ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
+                ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32)]
+
+
+def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
+               rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
+               rope_theta=1e6, rms_eps=1e-6):
+    return ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
+                     head_dim if rot_dim is None else rot_dim, inter, vocab,
+                     vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
+                     attn_tgt, rope_theta, rms_eps)
+
+
+def desc_27b(max_len=4096 + 512):
+    """the 27B-shape dense decoder (64 layers, hidden 5120, 40 q / 8 kv
+    heads of 128, SwiGLU 17408, vocab 151936, RoPE theta 1e6)."""
+    return dense_desc(64, 5120, 40, 8, 128, 17408, 151936, max_len)
+
+
+# tensor kinds (mi_engine_tensor)
+(T_QKV_Q, T_QKV_S, T_O_Q, T_O_S, T_GU_Q, T_GU_S, T_DOWN_Q, T_DOWN_S, T_IN_NORM, T_POST_NORM,
+ T_Q_NORM, T_K_NORM) = range(12)
+(T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
+ T_HISTORY) = range(32, 42)
+CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
+
+
+class Engine:
+    """Owns a mi_engine: weights, KV cache, the captured step graphs."""
+
+    def __init__(self, desc, seed=1234, stream=None):
+        self.desc = desc
+        self._h = lib().mi_engine_create(C.byref(desc), seed, stream)
+        if not self._h:
+            raise MiError("mi_engine_create: " + lib().mi_last_error().decode(errors="replace"))
+
+    def close(self):
+        if self._h:
+            lib().mi_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self):
+        return lib().mi_engine_stream(self._h)
+
+    def tensor(self, kind, layer=0):
+        p, b = vp(), sz()
+        check(lib().mi_engine_tensor(self._h, kind, layer, C.byref(p), C.byref(b)), "engine_tensor")
+        return p.value, b.value
+
+    def to_host(self, kind, layer=0, dtype="uint8"):
+        import numpy as np
+        p, b = self.tensor(kind, layer)
+        out = np.empty(b, np.uint8)
+        if b:
+            check(lib().mi_memcpy_d2h(out.ctypes.data, p, b, self.stream), "d2h")
+        return out.view(dtype)
+
+    def from_host(self, kind, arr, layer=0):
+        import numpy as np
+        p, b = self.tensor(kind, layer)
+        a = np.ascontiguousarray(arr)
+        assert a.nbytes == b, (a.nbytes, b)
+        check(lib().mi_memcpy_h2d(p, a.ctypes.data, b, self.stream), "h2d")
+        check(lib().mi_stream_sync(self.stream), "sync")
+
+    def linear_s(self, which):
+        s = u32()
+        check(lib().mi_engine_linear_s(self._h, which, C.byref(s)), "linear_s")
+        return s.value
+
+    def capture(self, M=1):
+        check(lib().mi_engine_capture(self._h, M), "engine_capture")
+
+    def reset(self, pos, token):
+        check(lib().mi_engine_reset(self._h, pos, token), "engine_reset")
+
+    def replay(self, M=1):
+        check(lib().mi_engine_replay(self._h, M), "engine_replay")
+
+    def generate(self, n):
+        import numpy as np
+        out = np.zeros(n, np.uint32)
+        check(lib().mi_engine_generate(self._h, n, out.ctypes.data), "engine_generate")
+        return out
+
+    def ingest(self, ids):
+        import numpy as np
+        a = np.ascontiguousarray(ids, np.uint32)
+        check(lib().mi_engine_ingest(self._h, a.ctypes.data, a.size), "engine_ingest")
+
+    def ctrl(self):
+        import numpy as np
+        out = np.zeros(CTRL_WORDS, np.uint32)
+        check(lib().mi_engine_read_ctrl(self._h, out.ctypes.data), "engine_read_ctrl")
+        return out
+
+    def verify(self, drafts):
+        import numpy as np
+        d = np.ascontiguousarray(drafts, np.uint32)
+        out = np.zeros(d.size + 1, np.uint32)
+        check(lib().mi_engine_verify(self._h, d.ctypes.data if d.size else None, d.size, out.ctypes.data),
+              "engine_verify")
+        return out
+
+    def commit(self, verify_pos, j, nxt):
+        check(lib().mi_engine_commit(self._h, verify_pos, j, nxt), "engine_commit")
+
+    def logits(self, rows=1):
+        import numpy as np
+        lg = self.to_host(T_LOGITS, dtype=np.float32)
+        return lg[:rows * self.desc.vocab].reshape(rows, self.desc.vocab)
+
+
+def accept_greedy(verify_argmax, drafts):
+    """server::accept_greedy through the library: (accepted count j, next token)."""
+    import numpy as np
+    va = np.ascontiguousarray(verify_argmax, np.uint32)
+    d = np.ascontiguousarray(drafts, np.uint32)
+    nxt = u32()
+    j = lib().mi_accept_greedy(va.ctypes.data, d.ctypes.data if d.size else None, d.size, C.byref(nxt))
+    return int(j), int(nxt.value)

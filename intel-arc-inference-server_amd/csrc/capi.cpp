@@ -77,3 +77,13 @@ int mi_event_elapsed_ms(void* start, void* stop, float* ms) {
 int mi_event_destroy(void* ev) { return mi_hip(static_cast<int>(hipEventDestroy(static_cast<hipEvent_t>(ev))), "hipEventDestroy"); }
 
 }  // extern "C"
+
+// server::accept_greedy (src/server/spec_accept.cc:81-85): accept d_i while it equals the
+// verify argmax of the row before it; the next token is the argmax at the first mismatch.
+extern "C" uint32_t mi_accept_greedy(const uint32_t* verify_argmax, const uint32_t* drafts, uint32_t k,
+                                     uint32_t* next) {
+  uint32_t j = 0;
+  while (j < k && drafts[j] == verify_argmax[j]) ++j;
+  if (next) *next = verify_argmax[j];
+  return j;
+}

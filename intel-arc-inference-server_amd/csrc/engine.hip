@@ -1,0 +1,446 @@
+// engine.cpp - the decode loop: weights, buffers, one captured step replayed per token.
+//
+// Mirrors the reference runtime (src/runtime/engine.h:52, engine.cc:702-960, capture.cc):
+//   * the model is shape-as-data (mi_model_desc ~ model::ModelDesc, model_desc.h:67-229);
+//   * one step is recorded once into a hipGraph (the L0 regular command list of
+//     runtime::build, capture.cc:2135-2142) and replayed per token (Engine::replay,
+//     engine.cc:702-713);
+//   * everything that changes per token lives in the device control block (Control,
+//     control.h:13-44): embed_gather reads cur_token, argmax writes out_token /
+//     cur_token / the token history and advances pos - so `generate(n)` is n graph
+//     launches and one synchronisation, with no host work between tokens;
+//   * verify(k drafts) replays an (k+1)-row graph, accept_greedy picks the accepted
+//     prefix on the host, commit() moves pos and cur_token (engine.cc:868-960,
+//     spec_accept.cc:81-85).
+// The layer walk is capture.cc's dense-attention layer (fa_layer :1370 + mlp :1247):
+//   res_fold + norm_finish, qkv GEMV, attn_prep, attn_decode, attn_reduce, o GEMV,
+//   res_fold + norm_finish, gate||up GEMV, silu_mul, down GEMV; then head() (:1461):
+//   res_fold + norm_finish, lm_head GEMV, fold to logits, argmax.
+// Weights are synthetic (random-init on the device) - the loader is outside this build -
+// and every weight tensor is reachable through mi_engine_tensor for checks or loading.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "mi_capi_internal.h"
+
+namespace {
+
+#define MI_TRY(expr)              \
+  do {                            \
+    const int _e = (expr);        \
+    if (_e != 0) return _e;       \
+  } while (0)
+
+struct Linear {
+  uint32_t* q = nullptr;  // [K/8][N]
+  uint16_t* s = nullptr;  // [K/64][N]
+  uint32_t K = 0, N = 0, S = 1;
+};
+
+struct Layer {
+  Linear qkv, o, gate_up, down;
+  float* in_norm = nullptr;
+  float* post_norm = nullptr;
+  float* q_norm = nullptr;
+  float* k_norm = nullptr;
+};
+
+__global__ void ctrl_set_kernel(uint32_t* ctrl, uint32_t word, uint32_t value) {
+  if (threadIdx.x == 0) ctrl[word] = value;
+}
+__global__ void ctrl_set_rows_kernel(uint32_t* ctrl, uint32_t pos, uint32_t n_act, const uint32_t* ids,
+                                     uint32_t n_ids) {
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {
+    ctrl[MI_CTRL_POS] = pos;
+    ctrl[MI_CTRL_NACT] = n_act;
+  }
+  if (t < n_ids) ctrl[MI_CTRL_CUR + t] = ids[t];
+}
+
+}  // namespace
+
+struct mi_engine {
+  mi_model_desc d{};
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  std::vector<void*> allocs;
+  std::vector<Layer> layer;
+  uint16_t* embed = nullptr;
+  float* final_norm = nullptr;
+  Linear lm_head;
+  float* rope = nullptr;
+  uint16_t* kv_k = nullptr;  // [layers][kv_heads][max_len][head_dim]
+  uint16_t* kv_v = nullptr;
+  // activations / scratch
+  uint32_t* ctrl = nullptr;
+  uint32_t* history = nullptr;
+  uint32_t* ids_dev = nullptr;
+  uint16_t* resid = nullptr;
+  uint16_t* x = nullptr;
+  uint16_t* hbuf = nullptr;
+  uint16_t* attn_out = nullptr;
+  float* part = nullptr;
+  float* sumsq = nullptr;
+  float* attn_q = nullptr;
+  float* attn_part = nullptr;
+  float* logits = nullptr;
+  void* argmax_part = nullptr;
+  uint32_t norm_g = 20;
+  mi_attn_shape ash{};
+  hipGraphExec_t graphs[17] = {};
+
+  ~mi_engine() {
+    for (auto& g : graphs)
+      if (g) hipGraphExecDestroy(g);
+    for (void* p : allocs) hipFree(p);
+    if (own_stream && stream) hipStreamDestroy(stream);
+  }
+
+  template <typename T>
+  int alloc(T** p, size_t count) {
+    void* v = nullptr;
+    const int e = static_cast<int>(hipMalloc(&v, count * sizeof(T) + 256));
+    if (e != 0) return mi_hip(e, "engine hipMalloc");
+    allocs.push_back(v);
+    *p = static_cast<T*>(v);
+    return 0;
+  }
+
+  int alloc_linear(Linear& l, uint32_t K, uint32_t N) {
+    l.K = K;
+    l.N = N;
+    l.S = mi_gemv_pick_s(K, N);
+    MI_TRY(alloc(&l.q, size_t(K / 8) * N));
+    MI_TRY(alloc(&l.s, size_t(K / 64) * N));
+    return 0;
+  }
+
+  int init_linear(Linear& l, uint64_t& seed) {
+    MI_TRY(mi_fill_u32(l.q, size_t(l.K / 8) * l.N, seed++, stream));
+    MI_TRY(mi_fill_f16(l.s, size_t(l.K / 64) * l.N, seed++, 0, 0.002f, 0.02f, stream));
+    return 0;
+  }
+
+  int build(uint64_t seed) {
+    const mi_model_desc& m = d;
+    const uint32_t H = m.hidden, HD = m.head_dim, QH = m.q_heads, KVH = m.kv_heads;
+    const uint32_t R = m.max_rows;
+    const uint32_t qkv_n = (QH + 2 * KVH) * HD;
+    ash = mi_attn_shape{QH, KVH, HD, m.rot_dim, 0u, qkv_n, QH * HD, (QH + KVH) * HD,
+                        1.0f / std::sqrt(float(HD)), m.rms_eps};
+    ash.scale = float(1.0 / std::sqrt(double(HD)));
+    norm_g = (H % 256 == 0) ? H / 256 : (H + 255) / 256;
+    layer.resize(m.layers);
+    size_t part_max = 0;
+    for (Layer& L : layer) {
+      MI_TRY(alloc_linear(L.qkv, H, qkv_n));
+      MI_TRY(alloc_linear(L.o, QH * HD, H));
+      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter));
+      MI_TRY(alloc_linear(L.down, m.inter, H));
+      MI_TRY(alloc(&L.in_norm, H));
+      MI_TRY(alloc(&L.post_norm, H));
+      if (m.qk_norm) {
+        MI_TRY(alloc(&L.q_norm, HD));
+        MI_TRY(alloc(&L.k_norm, HD));
+      }
+      for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
+        part_max = std::max(part_max, size_t(l->S) * R * l->N);
+    }
+    MI_TRY(alloc_linear(lm_head, H, m.vocab));
+    part_max = std::max(part_max, size_t(lm_head.S) * R * m.vocab);
+    MI_TRY(alloc(&embed, size_t(m.vocab) * H));
+    MI_TRY(alloc(&final_norm, H));
+    MI_TRY(alloc(&rope, size_t(m.max_len) * m.rot_dim));
+    const size_t kv_elems = size_t(m.layers) * KVH * m.max_len * HD;
+    MI_TRY(alloc(&kv_k, kv_elems));
+    MI_TRY(alloc(&kv_v, kv_elems));
+    MI_TRY(alloc(&ctrl, MI_CTRL_WORDS));
+    MI_TRY(alloc(&history, m.max_len));
+    MI_TRY(alloc(&ids_dev, 32));
+    MI_TRY(alloc(&resid, size_t(R) * H));
+    MI_TRY(alloc(&x, size_t(R) * std::max(H, QH * HD)));
+    MI_TRY(alloc(&hbuf, size_t(R) * m.inter));
+    MI_TRY(alloc(&attn_out, size_t(R) * QH * HD));
+    MI_TRY(alloc(&part, part_max));
+    MI_TRY(alloc(&sumsq, size_t(norm_g) * R));
+    MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
+    MI_TRY(alloc(&attn_part, size_t(QH) * m.attn_tgt * R * (HD + 2)));
+    MI_TRY(alloc(&logits, size_t(R) * m.vocab));
+    MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * mi_argmax_groups(m.vocab)));
+
+    // synthetic weights (BASELINE config 2's distributions)
+    for (Layer& L : layer) {
+      for (Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down}) MI_TRY(init_linear(*l, seed));
+      MI_TRY(mi_fill_f32(L.in_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
+      MI_TRY(mi_fill_f32(L.post_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
+      if (m.qk_norm) {
+        MI_TRY(mi_fill_f32(L.q_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+        MI_TRY(mi_fill_f32(L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+      }
+    }
+    MI_TRY(init_linear(lm_head, seed));
+    MI_TRY(mi_fill_f16(embed, size_t(m.vocab) * H, seed++, 1, 0.0f, 1.0f, stream));
+    MI_TRY(mi_fill_f32(final_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
+    MI_TRY(mi_fill_f16(kv_k, kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+    MI_TRY(mi_fill_f16(kv_v, kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+    // RoPE table in double, stored fp32 (src/loader/loader.cc:702-716)
+    {
+      const uint32_t half = m.rot_dim / 2;
+      std::vector<float> t(size_t(m.max_len) * 2 * half);
+      for (uint32_t p = 0; p < m.max_len; ++p)
+        for (uint32_t i = 0; i < half; ++i) {
+          const double a = double(p) * std::pow(double(m.rope_theta), -2.0 * double(i) / double(m.rot_dim));
+          t[(size_t(p) * 2 + 0) * half + i] = float(std::cos(a));
+          t[(size_t(p) * 2 + 1) * half + i] = float(std::sin(a));
+        }
+      MI_TRY(mi_hip(static_cast<int>(hipMemcpy(rope, t.data(), t.size() * 4, hipMemcpyHostToDevice)),
+                    "rope upload"));
+    }
+    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(ctrl, 0, MI_CTRL_WORDS * 4, stream)), "ctrl clear"));
+    MI_TRY(mi_hip(static_cast<int>(hipStreamSynchronize(stream)), "engine init"));
+    return 0;
+  }
+
+  // res_fold + norm_finish: the residual fold of the previous linear and the next norm
+  int res_norm(const float* partials, uint32_t s_prev, const float* w, uint32_t M) {
+    MI_TRY(mi_res_fold(partials, resid, sumsq, M, d.hidden, s_prev, norm_g, stream));
+    MI_TRY(mi_norm_finish(sumsq, resid, w, x, M, d.hidden, norm_g, d.rms_eps, stream));
+    return 0;
+  }
+
+  int gemv(const Linear& l, const uint16_t* in, uint32_t M) {
+    return mi_gemv_w4a16(l.q, l.s, in, part, M, l.K, l.N, l.S, stream);
+  }
+
+  // One step over M rows, enqueued on `stream` (recorded into a graph by capture()).
+  int enqueue_step(uint32_t M) {
+    const uint32_t HD = d.head_dim, KVH = d.kv_heads;
+    const size_t layer_kv = size_t(KVH) * d.max_len * HD;
+    MI_TRY(mi_embed_gather(ctrl, embed, resid, M, d.hidden, d.vocab, stream));
+    uint32_t s_prev = 0;
+    for (uint32_t li = 0; li < d.layers; ++li) {
+      const Layer& L = layer[li];
+      MI_TRY(res_norm(part, s_prev, L.in_norm, M));
+      MI_TRY(gemv(L.qkv, x, M));
+      uint16_t* lk = kv_k + li * layer_kv;
+      uint16_t* lv = kv_v + li * layer_kv;
+      MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv, HD,
+                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+      MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
+                            nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+      MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, &ash, stream));
+      MI_TRY(gemv(L.o, attn_out, M));
+      MI_TRY(res_norm(part, L.o.S, L.post_norm, M));
+      MI_TRY(gemv(L.gate_up, x, M));
+      MI_TRY(mi_silu_mul(part, hbuf, M, d.inter, L.gate_up.S, stream));
+      MI_TRY(gemv(L.down, hbuf, M));
+      s_prev = L.down.S;
+    }
+    MI_TRY(res_norm(part, s_prev, final_norm, M));
+    MI_TRY(gemv(lm_head, x, M));
+    MI_TRY(mi_fold_partials(part, nullptr, logits, lm_head.S, M, d.vocab, stream));
+    MI_TRY(mi_argmax(ctrl, logits, argmax_part, history, d.max_len, M, d.vocab, d.vocab_used, stream));
+    return 0;
+  }
+
+  int capture(uint32_t M) {
+    if (graphs[M]) return 0;
+    hipGraph_t g = nullptr;
+    MI_TRY(mi_hip(static_cast<int>(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal)),
+                  "hipStreamBeginCapture"));
+    const int e = enqueue_step(M);
+    const int e2 = static_cast<int>(hipStreamEndCapture(stream, &g));
+    if (e != 0) {
+      if (g) hipGraphDestroy(g);
+      return e;
+    }
+    MI_TRY(mi_hip(e2, "hipStreamEndCapture"));
+    const int e3 = static_cast<int>(hipGraphInstantiate(&graphs[M], g, nullptr, nullptr, 0));
+    hipGraphDestroy(g);
+    return mi_hip(e3, "hipGraphInstantiate");
+  }
+
+  int set_rows(uint32_t pos, uint32_t n_act, const uint32_t* ids, uint32_t n_ids) {
+    if (n_ids) {
+      MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(ids_dev, ids, n_ids * 4, hipMemcpyHostToDevice, stream)),
+                    "ids upload"));
+    }
+    ctrl_set_rows_kernel<<<1, 64, 0, stream>>>(ctrl, pos, n_act, ids_dev, n_ids);
+    return mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set_rows");
+  }
+
+  int read_ctrl(uint32_t* out) {
+    return mi_memcpy_d2h(out, ctrl, MI_CTRL_WORDS * 4, stream);
+  }
+};
+
+extern "C" {
+
+mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stream) {
+  if (!desc) {
+    mi_fail(MI_ERR_ARG, "engine_create: null desc");
+    return nullptr;
+  }
+  const mi_model_desc& m = *desc;
+  if (m.layers == 0 || m.hidden % 256 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
+      m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
+      m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
+      m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64) {
+    mi_fail(MI_ERR_SHAPE, "engine_create: unsupported model shape");
+    return nullptr;
+  }
+  std::unique_ptr<mi_engine> e(new (std::nothrow) mi_engine);
+  if (!e) {
+    mi_fail(MI_ERR_OOM, "engine_create: out of host memory");
+    return nullptr;
+  }
+  e->d = m;
+  if (stream) {
+    e->stream = static_cast<hipStream_t>(stream);
+  } else {
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) {
+      mi_fail(MI_ERR_STATE, "engine_create: stream");
+      return nullptr;
+    }
+    e->own_stream = true;
+  }
+  if (e->build(seed) != 0) return nullptr;
+  return e.release();
+}
+
+void mi_engine_destroy(mi_engine* e) { delete e; }
+
+void* mi_engine_stream(mi_engine* e) { return e ? e->stream : nullptr; }
+
+int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes) {
+  if (!e || !ptr) return mi_fail(MI_ERR_ARG, "engine_tensor: null");
+  const mi_model_desc& m = e->d;
+  if (kind < MI_T_EMBED && layer >= m.layers) return mi_fail(MI_ERR_ARG, "engine_tensor: layer out of range");
+  const Layer* L = kind < MI_T_EMBED ? &e->layer[layer] : nullptr;
+  auto lin_q = [](const Linear& l, void** p, size_t* b) { *p = l.q; if (b) *b = size_t(l.K / 8) * l.N * 4; };
+  auto lin_s = [](const Linear& l, void** p, size_t* b) { *p = l.s; if (b) *b = size_t(l.K / 64) * l.N * 2; };
+  size_t b = 0;
+  const size_t kvb = size_t(m.layers) * m.kv_heads * m.max_len * m.head_dim * 2;
+  switch (kind) {
+    case MI_T_QKV_Q: lin_q(L->qkv, ptr, &b); break;
+    case MI_T_QKV_S: lin_s(L->qkv, ptr, &b); break;
+    case MI_T_O_Q: lin_q(L->o, ptr, &b); break;
+    case MI_T_O_S: lin_s(L->o, ptr, &b); break;
+    case MI_T_GU_Q: lin_q(L->gate_up, ptr, &b); break;
+    case MI_T_GU_S: lin_s(L->gate_up, ptr, &b); break;
+    case MI_T_DOWN_Q: lin_q(L->down, ptr, &b); break;
+    case MI_T_DOWN_S: lin_s(L->down, ptr, &b); break;
+    case MI_T_IN_NORM: *ptr = L->in_norm; b = size_t(m.hidden) * 4; break;
+    case MI_T_POST_NORM: *ptr = L->post_norm; b = size_t(m.hidden) * 4; break;
+    case MI_T_Q_NORM: *ptr = L->q_norm; b = L->q_norm ? size_t(m.head_dim) * 4 : 0; break;
+    case MI_T_K_NORM: *ptr = L->k_norm; b = L->k_norm ? size_t(m.head_dim) * 4 : 0; break;
+    case MI_T_EMBED: *ptr = e->embed; b = size_t(m.vocab) * m.hidden * 2; break;
+    case MI_T_FINAL_NORM: *ptr = e->final_norm; b = size_t(m.hidden) * 4; break;
+    case MI_T_LM_Q: lin_q(e->lm_head, ptr, &b); break;
+    case MI_T_LM_S: lin_s(e->lm_head, ptr, &b); break;
+    case MI_T_ROPE: *ptr = e->rope; b = size_t(m.max_len) * m.rot_dim * 4; break;
+    case MI_T_KV_K: *ptr = e->kv_k; b = kvb; break;
+    case MI_T_KV_V: *ptr = e->kv_v; b = kvb; break;
+    case MI_T_LOGITS: *ptr = e->logits; b = size_t(m.max_rows) * m.vocab * 4; break;
+    case MI_T_CTRL: *ptr = e->ctrl; b = MI_CTRL_WORDS * 4; break;
+    case MI_T_HISTORY: *ptr = e->history; b = size_t(m.max_len) * 4; break;
+    default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
+  }
+  if (bytes) *bytes = b;
+  return 0;
+}
+
+int mi_engine_linear_s(mi_engine* e, uint32_t which, uint32_t* S) {
+  if (!e || !S) return mi_fail(MI_ERR_ARG, "engine_linear_s: null");
+  const Layer& L = e->layer[0];
+  switch (which) {
+    case 0: *S = L.qkv.S; break;
+    case 1: *S = L.o.S; break;
+    case 2: *S = L.gate_up.S; break;
+    case 3: *S = L.down.S; break;
+    case 4: *S = e->lm_head.S; break;
+    default: return mi_fail(MI_ERR_ARG, "engine_linear_s: which 0..4");
+  }
+  return 0;
+}
+
+int mi_engine_capture(mi_engine* e, uint32_t M) {
+  if (!e || M == 0 || M > e->d.max_rows) return mi_fail(MI_ERR_ARG, "engine_capture: M out of range");
+  return e->capture(M);
+}
+
+int mi_engine_reset(mi_engine* e, uint32_t pos, uint32_t token) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_reset: null");
+  if (pos >= e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_reset: pos beyond the KV cache");
+  MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(e->ctrl, 0, MI_CTRL_WORDS * 4, e->stream)), "ctrl clear"));
+  return e->set_rows(pos, 1, &token, 1);
+}
+
+int mi_engine_replay(mi_engine* e, uint32_t M) {
+  if (!e || M == 0 || M > e->d.max_rows || !e->graphs[M]) return mi_fail(MI_ERR_STATE, "engine_replay: not captured");
+  return mi_hip(static_cast<int>(hipGraphLaunch(e->graphs[M], e->stream)), "hipGraphLaunch");
+}
+
+int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens) {
+  if (!e || !e->graphs[1]) return mi_fail(MI_ERR_STATE, "engine_generate: capture(1) first");
+  uint32_t c[MI_CTRL_WORDS];
+  MI_TRY(e->read_ctrl(c));
+  if (c[MI_CTRL_POS] + n > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_generate: past the KV cache");
+  if (c[MI_CTRL_NACT] != 1) return mi_fail(MI_ERR_STATE, "engine_generate: n_active must be 1");
+  const uint32_t first = c[MI_CTRL_STEPS];
+  for (uint32_t i = 0; i < n; ++i) MI_TRY(mi_engine_replay(e, 1));
+  if (tokens) MI_TRY(mi_memcpy_d2h(tokens, e->history + first, size_t(n) * 4, e->stream));
+  return mi_stream_sync(e->stream);
+}
+
+int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
+  if (!e || !e->graphs[1]) return mi_fail(MI_ERR_STATE, "engine_ingest: capture(1) first");
+  uint32_t c[MI_CTRL_WORDS];
+  MI_TRY(e->read_ctrl(c));
+  if (c[MI_CTRL_POS] + n > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_ingest: past the KV cache");
+  for (uint32_t i = 0; i < n; ++i) {
+    ctrl_set_kernel<<<1, 64, 0, e->stream>>>(e->ctrl, MI_CTRL_CUR, ids[i]);
+    MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
+    MI_TRY(mi_engine_replay(e, 1));
+  }
+  return mi_stream_sync(e->stream);
+}
+
+int mi_engine_read_ctrl(mi_engine* e, uint32_t* out) {
+  if (!e || !out) return mi_fail(MI_ERR_ARG, "engine_read_ctrl: null");
+  return e->read_ctrl(out);
+}
+
+// Engine::verify (engine.cc:868-926): rows = [cur_token, drafts...] at pos .. pos+k.
+int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows) {
+  if (!e || (k && !drafts) || k + 1 > e->d.max_rows) return mi_fail(MI_ERR_ARG, "engine_verify: bad k");
+  if (!e->graphs[k + 1]) MI_TRY(e->capture(k + 1));
+  uint32_t c[MI_CTRL_WORDS];
+  MI_TRY(e->read_ctrl(c));
+  if (c[MI_CTRL_POS] + k + 1 > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_verify: past the KV cache");
+  std::vector<uint32_t> ids(k + 1);
+  ids[0] = c[MI_CTRL_CUR];
+  for (uint32_t i = 0; i < k; ++i) ids[i + 1] = drafts[i];
+  MI_TRY(e->set_rows(c[MI_CTRL_POS], k + 1, ids.data(), k + 1));
+  MI_TRY(mi_engine_replay(e, k + 1));
+  uint32_t c2[MI_CTRL_WORDS];
+  MI_TRY(e->read_ctrl(c2));
+  if (argmax_rows) std::memcpy(argmax_rows, c2 + MI_CTRL_OUT, (k + 1) * 4);
+  // leave pos at the verify position until commit (Engine::commit decides the advance)
+  return e->set_rows(c[MI_CTRL_POS], 1, nullptr, 0);
+}
+
+// Engine::commit (engine.cc:927-960): j accepted drafts, next token = argmax row j.
+int mi_engine_commit(mi_engine* e, uint32_t verify_pos, uint32_t j, uint32_t next) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_commit: null");
+  return e->set_rows(verify_pos + j + 1, 1, &next, 1);
+}
+
+}  // extern "C"

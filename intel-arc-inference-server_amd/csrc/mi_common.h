@@ -35,7 +35,14 @@ enum : uint32_t {
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(half_t, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (half_t)f); }
+// fp32 -> f16 RNE of an fp32 value that has been rounded to fp32 first. The empty asm
+// pins `f` in a VGPR, so the backend cannot fold the producing multiply or add into a
+// v_fma_mix*_f16 (which rounds once, straight to f16: a double-rounding difference
+// from the reference's fp32 op followed by the conversion).
+__device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (half_t)f);
+}
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 

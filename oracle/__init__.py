@@ -161,7 +161,7 @@ class DenseModel(C.Structure):
                 ("vocab", C.c_uint32), ("vocab_used", C.c_uint32), ("max_len", C.c_uint32),
                 ("attn", AttnShape), ("rms_eps", C.c_float), ("layer", C.c_void_p),
                 ("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", Linear),
-                ("rope", C.c_void_p), ("tgt", C.c_uint32)]
+                ("rope", C.c_void_p), ("tgt", C.c_uint32), ("norm_g", C.c_uint32)]
 
 
 # ---- numpy helpers ----------------------------------------------------------------------

@@ -853,6 +853,15 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
   std::vector<float> xf(std::max<size_t>(size_t(H), std::max<size_t>(size_t(QH) * HD, md->inter)));
   std::vector<float> part, attn_q(size_t(QH) * HD), attn_part;
   orc_embed_gather(&tok, 1, md->embed, md->vocab, H, resid.data());
+  std::vector<float> sumsq(std::max<uint32_t>(md->norm_g, 1));
+  auto norm = [&](const float* partials, uint32_t s_prev, const float* w) {
+    if (md->norm_g == 0) {
+      orc_res_norm(act, partials, resid.data(), w, x.data(), 1, H, s_prev, md->rms_eps);
+    } else {
+      orc_res_fold(act, partials, resid.data(), sumsq.data(), 1, H, s_prev, md->norm_g);
+      orc_norm_finish(act, sumsq.data(), resid.data(), w, x.data(), 1, H, md->norm_g, md->rms_eps);
+    }
+  };
   auto widen = [&](const uint16_t* v, uint32_t n) {
     for (uint32_t i = 0; i < n; ++i) xf[i] = A.w(v[i]);
   };
@@ -866,7 +875,7 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
   std::vector<float> prev;  // the previous down projection's partials
   for (uint32_t li = 0; li < nl; ++li) {
     const orc_layer& ly = md->layer[li];
-    orc_res_norm(act, prev.data(), resid.data(), ly.in_norm, x.data(), 1, H, s_prev, md->rms_eps);
+    norm(prev.data(), s_prev, ly.in_norm);
     linear(ly.qkv, x.data());
     uint16_t* lk = kv_k + size_t(li) * KVH * L * HD;
     uint16_t* lv = kv_v + size_t(li) * KVH * L * HD;
@@ -877,7 +886,7 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
                        HD, size_t(L) * HD, 0, 0, nullptr, 0, attn_part.data());
     orc_attn_reduce_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
     linear(ly.o, attn_out.data());
-    orc_res_norm(act, part.data(), resid.data(), ly.post_norm, x.data(), 1, H, ly.o.S, md->rms_eps);
+    norm(part.data(), ly.o.S, ly.post_norm);
     linear(ly.gate_up, x.data());
     orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
     linear(ly.down, hbuf.data());
@@ -885,7 +894,7 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
     s_prev = ly.down.S;
   }
   if (nl < md->layers) return 0;
-  orc_res_norm(act, prev.data(), resid.data(), md->final_norm, x.data(), 1, H, s_prev, md->rms_eps);
+  norm(prev.data(), s_prev, md->final_norm);
   widen(x.data(), H);
   orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1,
                 md->lm_head.S, logits);

@@ -165,6 +165,7 @@ typedef struct orc_dense_model {
   orc_linear lm_head;
   const float* rope; /* [max_len][2][rot_dim/2] */
   uint32_t tgt;      /* attention blocks per kv head (the v2 grid) */
+  uint32_t norm_g;   /* 0: single-launch res_norm tree; G > 0: res_fold over G chunks + norm_finish */
 } orc_dense_model;
 /* One step for token `tok` at position pos. kv_k/kv_v: [layers][kv_heads][max_len][hd] act
  * (this build's layout), updated in place. Writes logits fp32 [vocab] and returns argmax. */

@@ -15,6 +15,8 @@ def torch():
 
 def dev(a):
     """numpy array -> torch device tensor with the same bytes."""
+    if a is None:
+        return None
     T = torch()
     a = np.ascontiguousarray(a)
     if a.dtype == np.uint16:

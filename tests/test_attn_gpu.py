@@ -1,0 +1,149 @@
+"""GQA decode attention on the GPU (fp16 and int8 KV, contiguous and paged) vs the oracle.
+
+Bars: softmax attention within rel 2e-3 of the fp64 reference (the reference holds its
+readers to the fp64 attend by cosine, tests/kernels/kv8_ref.h:1-12) and of the oracle's
+restatement of attn_decode_v2's order; cosine >= 0.99999; KV paging bitwise equal to the
+contiguous cache (attn_v2.cl:123-131); row m of an M-row step bitwise the 1-row step at
+pos + m; replays bitwise."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mipkg import dev, empty, host, mi, ptr, stream, sync
+
+pytestmark = pytest.mark.gpu
+F16 = O.ORC_F16
+L = O.lib
+
+
+def ctrl_dev(pos, n_act):
+    c = np.zeros(64, np.uint32)
+    c[0], c[1] = pos, n_act
+    return dev(c)
+
+
+def make_kv(kind, KVH, Lm, HD, seed):
+    rng = np.random.default_rng(seed)
+    if kind == 0:
+        k = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+        v = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+        return k, v, None, None
+    k = rng.integers(-127, 128, size=(KVH, Lm, HD)).astype(np.int8)
+    v = rng.integers(-127, 128, size=(KVH, Lm, HD)).astype(np.int8)
+    ks = O.f32_to_f16_bits(rng.uniform(0.005, 0.05, (KVH, Lm)).astype(np.float32))
+    vs = O.f32_to_f16_bits(rng.uniform(0.005, 0.05, (KVH, Lm)).astype(np.float32))
+    return k, v, ks, vs
+
+
+def gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, pages=None, page=0):
+    HD, QH = sh.head_dim, sh.q_heads
+    Lm = k.shape[1]
+    print(f"attn kind={kind} HD={HD} QH={QH} pos={pos} M={M} tgt={tgt} paged={pages is not None}", flush=True)
+    ctrl = ctrl_dev(pos, M)
+    part = empty((QH, tgt, M, HD + 2), np.float32)
+    out = empty((M, QH * HD), np.uint16)
+    dk, dv, dks, dvs, dq = dev(k), dev(v), dev(ks), dev(vs), dev(q)
+    dpg = dev(pages)
+    shp = C.byref(sh)
+    mi.call("mi_attn_decode", ptr(ctrl), ptr(dq), kind, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD,
+            1, Lm, ptr(dpg), page, Lm, ptr(part), M, tgt, shp, stream())
+    mi.call("mi_attn_reduce", ptr(ctrl), ptr(part), None, ptr(out), M, tgt, shp, stream())
+    sync()
+    return host(out, np.uint16), host(part, np.float32)
+
+
+def fp64_attention(sh, q, kind, k, v, ks, vs, n, pages=None, page=0):
+    HD, QH, G = sh.head_dim, sh.q_heads, sh.q_heads // sh.kv_heads
+    Lm = k.shape[1]
+    o = np.zeros((QH, HD))
+    for h in range(QH):
+        L().orc_attend64(C.byref(sh), O._p(np.ascontiguousarray(q[h])), h // G, n, kind, F16, O._p(k), O._p(v),
+                         O._p(ks), O._p(vs), HD, Lm * HD, 1, Lm, O._p(pages), page, O._p(o[h]))
+    return o
+
+
+def check_close(got16, want, rtol=2e-3):
+    g = O.f16_bits_to_f32(got16).astype(np.float64).reshape(want.shape)
+    err = np.abs(g - want)
+    assert np.all(err <= rtol * np.abs(want) + 2e-3 * np.abs(want).max(axis=-1, keepdims=True)), err.max()
+    cos = (g * want).sum(-1) / np.sqrt((g * g).sum(-1) * (want * want).sum(-1))
+    assert cos.min() >= 0.99999
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("QH,KVH,HD", [(40, 8, 128), (16, 2, 256)])
+@pytest.mark.parametrize("pos", [0, 77, 4095])
+def test_decode_vs_fp64_and_oracle(kind, QH, KVH, HD, pos):
+    Lm, tgt = 4096, 128
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(kind, KVH, Lm, HD, pos + HD)
+    q = np.random.default_rng(pos).standard_normal((1, QH, HD)).astype(np.float32)
+    got, _ = gpu_attention(sh, q, kind, k, v, ks, vs, pos, 1, tgt)
+    want = fp64_attention(sh, q[0], kind, k, v, ks, vs, pos + 1)
+    check_close(got[0].reshape(QH, HD), want)
+    # the oracle's restatement of attn_decode_v2 + attn_reduce_v2 at the same grid
+    part = np.zeros((QH, tgt, 1, HD + 2), np.float32)
+    L().orc_attn_decode_v2(F16, C.byref(sh), pos, 1, 1, tgt, O._p(q), kind, O._p(k), O._p(v), O._p(ks),
+                           O._p(vs), HD, Lm * HD, 1, Lm, None, 0, O._p(part))
+    ref = np.zeros((1, QH * HD), np.uint16)
+    L().orc_attn_reduce_v2(F16, C.byref(sh), pos, 1, 1, tgt, O._p(part), None, O._p(ref))
+    check_close(got[0].reshape(QH, HD), O.f16_bits_to_f32(ref[0]).astype(np.float64).reshape(QH, HD))
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_long_context_paged_bitwise(kind):
+    """BASELINE config 3 shape (40 q / 8 kv, hd 128) at L = 32768, 64-token pages in a
+    shuffled table: the paged cache gives the same bits as the contiguous one."""
+    QH, KVH, HD, Lm, P, tgt = 40, 8, 128, 32768, 64, 128
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(kind, KVH, Lm, HD, 7)
+    q = np.random.default_rng(8).standard_normal((1, QH, HD)).astype(np.float32)
+    pos = Lm - 1
+    a, pa = gpu_attention(sh, q, kind, k, v, ks, vs, pos, 1, tgt)
+    rng = np.random.default_rng(9)
+    pages = rng.permutation(Lm // P).astype(np.uint32)
+    phys = np.concatenate([np.arange(pg * P, pg * P + P) for pg in pages])
+    kp, vp = np.empty_like(k), np.empty_like(v)
+    kp[:, phys], vp[:, phys] = k, v
+    ksp = vsp = None
+    if kind:
+        ksp, vsp = np.empty_like(ks), np.empty_like(vs)
+        ksp[:, phys], vsp[:, phys] = ks, vs
+    b, pb = gpu_attention(sh, q, kind, kp, vp, ksp, vsp, pos, 1, tgt, pages, P)
+    assert np.array_equal(a, b)
+    assert np.array_equal(pa.view(np.uint32), pb.view(np.uint32))
+    # and against fp64 for a few heads (the full fp64 pass over 32k keys is slow on the host)
+    want = fp64_attention(sh, q[0], kind, k, v, ks, vs, pos + 1)
+    check_close(a[0].reshape(QH, HD), want)
+
+
+def test_rows_are_bitwise_their_single_row_steps():
+    QH, KVH, HD, Lm, tgt = 40, 8, 128, 4096, 128
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(0, KVH, Lm, HD, 3)
+    M, pos = 4, 2045  # rows straddle the 2048-key stride change of ppw at tgt 32 ... and 128
+    q = np.random.default_rng(4).standard_normal((M, QH, HD)).astype(np.float32)
+    full, _ = gpu_attention(sh, q, 0, k, v, ks, vs, pos, M, tgt)
+    for m in range(M):
+        one, _ = gpu_attention(sh, np.ascontiguousarray(q[m:m + 1]), 0, k, v, ks, vs, pos + m, 1, tgt)
+        assert np.array_equal(one[0], full[m])
+    again, _ = gpu_attention(sh, q, 0, k, v, ks, vs, pos, M, tgt)
+    assert np.array_equal(full, again)
+
+
+def test_reduce_matches_oracle_merge_on_device_partials():
+    """attn_reduce_v2's merge (the reference's formula, ascending blocks) on the GPU's own
+    partials: within 1 fp16 ulp of the oracle's merge (exp differs by <= 1 ulp)."""
+    QH, KVH, HD, Lm, tgt = 40, 8, 128, 8192, 32
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(0, KVH, Lm, HD, 5)
+    q = np.random.default_rng(6).standard_normal((1, QH, HD)).astype(np.float32)
+    pos = 6000
+    got, part = gpu_attention(sh, q, 0, k, v, ks, vs, pos, 1, tgt)
+    ref = np.zeros((1, QH * HD), np.uint16)
+    L().orc_attn_reduce_v2(F16, C.byref(sh), pos, 1, 1, tgt, O._p(np.ascontiguousarray(part)), None, O._p(ref))
+    a = O.f16_bits_to_f32(got).astype(np.float64)
+    b = O.f16_bits_to_f32(ref).astype(np.float64)
+    assert np.all(np.abs(a - b) <= np.maximum(np.abs(b), 2.0 ** -14) * 2.0 ** -10 * 1.01)

@@ -1,0 +1,170 @@
+"""The captured decode step (hipGraph replay, control block on the device) against the
+oracle's whole dense step, plus speculative verify + greedy accept + commit.
+
+Bars: logits within rel 2e-3 of the oracle's step on the same weights, KV and token
+(teacher forcing, several steps); argmax equal unless the oracle's top two are closer than
+the tolerance; the RoPE table bit-exact; verify rows bitwise the plain steps at the same
+positions (tests/kernels/attn_v2_test.cc's "verify rows bitwise the plain step");
+accept_greedy's count and next token exact; replays deterministic."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mipkg import mi
+
+pytestmark = pytest.mark.gpu
+F16 = O.ORC_F16
+
+
+def small_desc(**kw):
+    d = dict(layers=2, hidden=512, q_heads=8, kv_heads=2, head_dim=128, inter=1024, vocab=4096,
+             max_len=512, max_rows=4, attn_tgt=4)
+    d.update(kw)
+    return mi.dense_desc(d.pop("layers"), d.pop("hidden"), d.pop("q_heads"), d.pop("kv_heads"),
+                         d.pop("head_dim"), d.pop("inter"), d.pop("vocab"), d.pop("max_len"), **d)
+
+
+class OracleModel:
+    """Host copies of the engine's weights wired into orc_dense_model."""
+
+    def __init__(self, eng):
+        d = eng.desc
+        self.d = d
+        self.keep = []
+        H, HD, QH, KVH, I = d.hidden, d.head_dim, d.q_heads, d.kv_heads, d.inter
+        S = [eng.linear_s(w) for w in range(5)]
+        dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
+        layers = (O.Layer * d.layers)()
+        for li in range(d.layers):
+            lins = []
+            for w, (K, N) in enumerate(dims):
+                q = self._h(eng.to_host(2 * w, li, np.uint32))
+                s = self._h(eng.to_host(2 * w + 1, li, np.uint16))
+                lins.append(O.Linear(q.ctypes.data, s.ctypes.data, K, N, S[w]))
+            L = layers[li]
+            L.qkv, L.o, L.gate_up, L.down = lins
+            L.in_norm = self._h(eng.to_host(mi.T_IN_NORM, li, np.float32)).ctypes.data
+            L.post_norm = self._h(eng.to_host(mi.T_POST_NORM, li, np.float32)).ctypes.data
+            if d.qk_norm:
+                L.q_norm = self._h(eng.to_host(mi.T_Q_NORM, li, np.float32)).ctypes.data
+                L.k_norm = self._h(eng.to_host(mi.T_K_NORM, li, np.float32)).ctypes.data
+        self.keep.append(layers)
+        self.rope = self._h(eng.to_host(mi.T_ROPE, 0, np.float32))
+        want_rope = O.rope_table(d.rope_theta, d.rot_dim, d.max_len)
+        assert np.array_equal(self.rope.view(np.uint32), want_rope.ravel().view(np.uint32))
+        embed = self._h(eng.to_host(mi.T_EMBED, 0, np.uint16))
+        fnorm = self._h(eng.to_host(mi.T_FINAL_NORM, 0, np.float32))
+        lmq = self._h(eng.to_host(mi.T_LM_Q, 0, np.uint32))
+        lms = self._h(eng.to_host(mi.T_LM_S, 0, np.uint16))
+        self.kv_k = eng.to_host(mi.T_KV_K, 0, np.uint16).copy()
+        self.kv_v = eng.to_host(mi.T_KV_V, 0, np.uint16).copy()
+        sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
+        self.m = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
+                              C.cast(layers, C.c_void_p), embed.ctypes.data, fnorm.ctypes.data,
+                              O.Linear(lmq.ctypes.data, lms.ctypes.data, H, d.vocab, S[4]),
+                              self.rope.ctypes.data, d.attn_tgt, H // 256)
+
+    def _h(self, a):
+        a = np.ascontiguousarray(a)
+        self.keep.append(a)
+        return a
+
+    def step(self, tok, pos):
+        logits = np.zeros(self.d.vocab, np.float32)
+        am = O.lib().orc_dense_step(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
+                                    O._p(logits), self.d.layers)
+        return am, logits
+
+
+def close(got, want):
+    err = np.abs(got.astype(np.float64) - want)
+    return np.all(err <= 2e-3 * np.abs(want) + 2e-3 * np.abs(want).max())
+
+
+def argmax_ok(gpu_tok, want_logits):
+    top = np.sort(want_logits)[::-1]
+    if gpu_tok == int(np.argmax(want_logits)):
+        return True
+    # an oracle near-tie: the two leading logits closer than the tolerance
+    return (top[0] - want_logits[gpu_tok]) <= 2e-3 * np.abs(want_logits).max() * 2
+
+
+@pytest.mark.parametrize("qk_norm", [1, 0])
+def test_decode_steps_vs_oracle_teacher_forced(qk_norm):
+    eng = mi.Engine(small_desc(qk_norm=qk_norm), seed=42)
+    print(f"engine qk_norm={qk_norm} S={[eng.linear_s(w) for w in range(5)]}", flush=True)
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 300, 7
+    eng.reset(pos, tok)
+    for step in range(4):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert argmax_ok(got_tok, want)
+        c = eng.ctrl()
+        assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_CUR] == got_tok and c[mi.CTRL_OUT] == got_tok
+        tok, pos = got_tok, pos + 1
+    eng.close()
+
+
+def test_generate_deterministic_and_history():
+    eng = mi.Engine(small_desc(), seed=3)
+    eng.capture(1)
+    eng.reset(10, 5)
+    a = eng.generate(6)
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == 16 and c[mi.CTRL_STEPS] == 6 and c[mi.CTRL_CUR] == a[-1]
+    eng.reset(10, 5)  # same start: the replayed list recomputes the same KV rows and tokens
+    b = eng.generate(6)
+    assert np.array_equal(a, b)
+    eng.close()
+
+
+def test_verify_rows_bitwise_plain_steps_and_accept():
+    eng = mi.Engine(small_desc(), seed=11)
+    eng.capture(1)
+    P, t0 = 200, 9
+    eng.reset(P, t0)
+    plain_tok, plain_logits = [], []
+    for _ in range(4):
+        plain_tok.append(int(eng.generate(1)[0]))
+        plain_logits.append(eng.logits(1)[0].copy())
+    # verify the first three as drafts from the same start
+    eng.reset(P, t0)
+    rows = eng.verify(plain_tok[:3])
+    assert list(rows) == plain_tok
+    lg = eng.logits(4)
+    for m in range(4):
+        assert np.array_equal(lg[m].view(np.uint32), plain_logits[m].view(np.uint32))
+    j, nxt = mi.accept_greedy(rows, plain_tok[:3])
+    assert (j, nxt) == (3, plain_tok[3])
+    eng.commit(P, j, nxt)
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == P + 4 and c[mi.CTRL_CUR] == plain_tok[3] and c[mi.CTRL_NACT] == 1
+    # a rejected draft: accept stops at the first mismatch and takes that row's argmax
+    eng.reset(P, t0)
+    bad = [plain_tok[0], (plain_tok[1] + 1) % 4096, plain_tok[2]]
+    rows = eng.verify(bad)
+    assert rows[0] == plain_tok[0] and rows[1] == plain_tok[1]
+    j, nxt = mi.accept_greedy(rows, bad)
+    assert (j, nxt) == (1, plain_tok[1])
+    assert O.accept_greedy(rows, bad) == (j, nxt)
+    eng.commit(P, j, nxt)
+    assert eng.ctrl()[mi.CTRL_POS] == P + 2
+    eng.close()
+
+
+def test_ingest_then_generate():
+    eng = mi.Engine(small_desc(), seed=5)
+    eng.capture(1)
+    eng.reset(0, 1)
+    eng.ingest([1, 2, 3, 4])
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == 4
+    toks = eng.generate(3)
+    assert eng.ctrl()[mi.CTRL_POS] == 7 and len(toks) == 3
+    eng.close()
