@@ -1,0 +1,288 @@
+#!/usr/bin/env python3
+"""bench.py - batch-1 decode tokens/s of the 27B-shape W4A16 g64 model on one MI355X.
+
+Workload (the metric's configuration): a dense 64-layer decoder,
+hidden 5120, 40 q / 8 kv heads of 128, SwiGLU 17408, vocab 151936, int4 g64 weights for
+every linear and the lm_head, fp16 KV cache pre-filled N(0,1) to 4096 positions, RoPE
+theta 1e6, greedy argmax. Random-init weights of that architecture (no checkpoint).
+
+A "step" is one replay of the captured decode step (one token). The timed region is K
+back-to-back graph launches on the engine's stream, bracketed by device synchronisation,
+timed with HIP events on that stream; inputs (weights, KV, control block) are resident in
+HBM before it starts.
+
+Also printed in the same JSON line:
+  roofline     the int4 GEMV (the step's dominant kernel): algorithmic bytes of every GEMV
+               launch of one step / their measured time, HIP events on the engine's stream;
+  cpu_baseline this repository's CPU oracle (the reference's scalar twins restated) running
+               one full decode step of the same model on the host's cores;
+  parity       GPU vs oracle logits of that same step (rel 2e-3 bar) and their argmax.
+"""
+import argparse
+import ctypes as C
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+mi = importlib.import_module("intel-arc-inference-server_amd")
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E vendor peak
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Events:
+    def __init__(self, stream):
+        self.L = mi.lib()
+        self.stream = stream
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        mi.check(self.L.mi_event_create(C.byref(self.a)))
+        mi.check(self.L.mi_event_create(C.byref(self.b)))
+
+    def start(self):
+        mi.check(self.L.mi_event_record(self.a, self.stream))
+
+    def stop_ms(self):
+        mi.check(self.L.mi_event_record(self.b, self.stream))
+        ms = C.c_float()
+        mi.check(self.L.mi_event_elapsed_ms(self.a, self.b, C.byref(ms)))
+        return float(ms.value)
+
+
+def gemv_roofline(eng, reps=3):
+    """Every int4 GEMV launch of one step (4 per layer + lm_head), each on the engine's own
+    weights and split-K width, back to back on the engine's stream; HIP events around
+    `reps` such sweeps. Algorithmic bytes per launch = int4 weights + fp16 scales + fp16 x
+    in + fp32 y out (K N / 2 + (K / 64) N 2 + 2 K + 4 N)."""
+    L = mi.lib()
+    d = eng.desc
+    st = eng.stream
+    H, I, V = d.hidden, d.inter, d.vocab
+    qkv_n = (d.q_heads + 2 * d.kv_heads) * d.head_dim
+    dims = [(H, qkv_n), (d.q_heads * d.head_dim, H), (H, 2 * I), (I, H)]
+    S = [eng.linear_s(w) for w in range(5)]
+    kmax = max(H, I, d.q_heads * d.head_dim)
+    nmax = max(s * n for s, (_, n) in zip(S, dims + [(H, V)]))
+    xbuf, pbuf = C.c_void_p(), C.c_void_p()
+    mi.check(L.mi_malloc(C.byref(xbuf), kmax * 2))
+    mi.check(L.mi_malloc(C.byref(pbuf), nmax * 4))
+    mi.check(L.mi_fill_f16(xbuf, kmax, 99, 1, 0.0, 1.0, st))
+    launches = []
+    for li in range(d.layers):
+        for w, (K, N) in enumerate(dims):
+            q, _ = eng.tensor(2 * w, li)
+            s, _ = eng.tensor(2 * w + 1, li)
+            launches.append((q, s, K, N, S[w]))
+    lq, _ = eng.tensor(mi.T_LM_Q)
+    ls, _ = eng.tensor(mi.T_LM_S)
+    launches.append((lq, ls, H, V, S[4]))
+    alg = sum(K * N // 2 + (K // 64) * N * 2 + 2 * K + 4 * N for _, _, K, N, _ in launches)
+
+    def sweep():
+        for q, s, K, N, Sx in launches:
+            mi.check(L.mi_gemv_w4a16(q, s, xbuf, pbuf, 1, K, N, Sx, st))
+
+    sweep()
+    mi.check(L.mi_stream_sync(st))
+    ev = Events(st)
+    ev.start()
+    for _ in range(reps):
+        sweep()
+    ms = ev.stop_ms()
+    mi.check(L.mi_free(xbuf))
+    mi.check(L.mi_free(pbuf))
+    per_launch_s = ms * 1e-3 / (reps * len(launches))
+    bytes_per_launch = alg / len(launches)
+    achieved = bytes_per_launch / per_launch_s / 1e9
+    return {
+        "kernel": "gemv_w4a16_kernel (int4 g64 GEMV, M=1)",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "launches_per_step": len(launches),
+        "alg_bytes_per_step": alg,
+        "gemv_ms_per_step": round(per_launch_s * len(launches) * 1e3, 4),
+        "avg_launch_us": round(per_launch_s * 1e6, 3),
+    }, alg
+
+
+def stream_read_rate(st):
+    L = mi.lib()
+    nbytes = 2 << 30
+    buf, sink = C.c_void_p(), C.c_void_p()
+    mi.check(L.mi_malloc(C.byref(buf), nbytes))
+    mi.check(L.mi_malloc(C.byref(sink), 8192 * 4))
+    mi.check(L.mi_fill_u32(buf, nbytes // 4, 5, st))
+    mi.check(L.mi_stream_read(buf, nbytes, sink, st))
+    mi.check(L.mi_stream_sync(st))
+    ev = Events(st)
+    ev.start()
+    for _ in range(5):
+        mi.check(L.mi_stream_read(buf, nbytes, sink, st))
+    ms = ev.stop_ms()
+    mi.check(L.mi_free(buf))
+    mi.check(L.mi_free(sink))
+    return nbytes * 5 / (ms * 1e-3) / 1e9
+
+
+def cpu_oracle_step(eng, tok, pos):
+    """One full decode step of the same model through the CPU oracle (the reference's
+    scalar twins restated; OpenMP over columns in the GEMV twins). Returns (seconds,
+    logits, argmax, threads)."""
+    import oracle as O
+    d = eng.desc
+    H, I, HD, QH, KVH = d.hidden, d.inter, d.head_dim, d.q_heads, d.kv_heads
+    S = [eng.linear_s(w) for w in range(5)]
+    dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
+    keep = []
+
+    def h(kind, layer, dt):
+        a = eng.to_host(kind, layer, dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    layers = (O.Layer * d.layers)()
+    for li in range(d.layers):
+        lins = [O.Linear(h(2 * w, li, np.uint32), h(2 * w + 1, li, np.uint16), K, N, S[w])
+                for w, (K, N) in enumerate(dims)]
+        Ly = layers[li]
+        Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+        Ly.in_norm = h(mi.T_IN_NORM, li, np.float32)
+        Ly.post_norm = h(mi.T_POST_NORM, li, np.float32)
+        if d.qk_norm:
+            Ly.q_norm = h(mi.T_Q_NORM, li, np.float32)
+            Ly.k_norm = h(mi.T_K_NORM, li, np.float32)
+    kv_k = eng.to_host(mi.T_KV_K, 0, np.uint16).copy()
+    kv_v = eng.to_host(mi.T_KV_V, 0, np.uint16).copy()
+    sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
+    model = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
+                         C.cast(layers, C.c_void_p), h(mi.T_EMBED, 0, np.uint16),
+                         h(mi.T_FINAL_NORM, 0, np.float32),
+                         O.Linear(h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab, S[4]),
+                         h(mi.T_ROPE, 0, np.float32), d.attn_tgt, H // 64)
+    logits = np.zeros(d.vocab, np.float32)
+    t0 = time.perf_counter()
+    am = O.lib().orc_dense_step(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(logits),
+                                d.layers)
+    dt = time.perf_counter() - t0
+    return dt, logits, int(am), int(O.lib().orc_threads())
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline and parity step")
+    ap.add_argument("--eager", action="store_true",
+                    help="enqueue each step kernel by kernel instead of replaying the captured graph")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    max_len = ((args.context + args.warmup + args.steps + 1 + 63) // 64) * 64
+    desc = mi.desc_27b(max_len=max_len)
+    log(f"bench: building 27B-shape engine (max_len {max_len}) ...")
+    t0 = time.time()
+    eng = mi.Engine(desc, seed=args.seed)
+    eng.capture(1)
+    log(f"bench: engine ready in {time.time() - t0:.1f} s; S per linear {[eng.linear_s(w) for w in range(5)]}")
+    st = eng.stream
+    tok0 = 1000
+
+    parity = None
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU oracle step (one full 64-layer step on the host) ...")
+        eng.reset(args.context, tok0)
+        dt, cpu_logits, cpu_am, threads = cpu_oracle_step(eng, tok0, args.context)
+        eng.reset(args.context, tok0)
+        gpu_tok = int(eng.generate(1)[0])
+        g = eng.logits(1)[0].astype(np.float64)
+        w = cpu_logits.astype(np.float64)
+        err = np.abs(g - w)
+        parity = {
+            "max_abs_err": float(err.max()),
+            "max_err_over_max_logit": float(err.max() / np.abs(w).max()),
+            "within_rel_2e-3": bool(np.all(err <= 2e-3 * np.abs(w) + 2e-3 * np.abs(w).max())),
+            "argmax_gpu": gpu_tok, "argmax_oracle": cpu_am,
+        }
+        cpu = {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"one full decode step of the same 64-layer model at context {args.context} "
+                         f"(oracle/oracle.cpp orc_dense_step, twin GEMV order, {threads} OpenMP threads), "
+                         f"{dt:.2f} s"}
+        log(f"bench: cpu step {dt:.2f} s on {threads} threads; parity {parity}")
+
+    eng.reset(args.context, tok0)
+    step = eng.step_eager if args.eager else eng.replay
+    for _ in range(max(1, args.warmup)):
+        step(1)
+    mi.check(mi.lib().mi_device_sync())
+    ev = Events(st)
+    tw = time.perf_counter()
+    ev.start()
+    for _ in range(args.steps):
+        step(1)
+    ms = ev.stop_ms()
+    mi.check(mi.lib().mi_device_sync())
+    wall = time.perf_counter() - tw
+    ms_per_step = ms / args.steps
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == args.context + args.warmup + args.steps, c[:20]
+    assert c[mi.CTRL_DEBUG] == 0, hex(c[mi.CTRL_DEBUG])
+    tok_s = 1000.0 / ms_per_step
+    log(f"bench: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms wall -> {tok_s:.1f} tok/s")
+
+    roof, alg_gemv = gemv_roofline(eng)
+    stream_gbs = stream_read_rate(st)
+    kv_bytes = 2 * desc.layers * desc.kv_heads * (args.context + 1) * desc.head_dim * 2
+    step_alg = alg_gemv + kv_bytes
+    roof["stream_read_gbs"] = round(stream_gbs, 1)
+    roof["frac_of_stream"] = round(roof["achieved"] / stream_gbs, 4)
+    log(f"bench: gemv roofline {roof}")
+
+    out = {
+        "metric": "batch-1 decode tokens/s (27B-shape W4A16); int4 GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (int4 g64 weights, f16 activations, fp32 accumulate)",
+        "data": "synthetic (random-init 27B-shape weights; fp16 KV pre-filled N(0,1))",
+        "config": {"workload": "BASELINE configs[1]: dense 27B-shape decode step, batch 1, context 4096",
+                   "launch": "eager" if args.eager else "hipGraph replay",
+                   "layers": desc.layers, "hidden": desc.hidden, "q_heads": desc.q_heads,
+                   "kv_heads": desc.kv_heads, "head_dim": desc.head_dim, "intermediate": desc.inter,
+                   "vocab": desc.vocab, "context": args.context, "rope_theta": 1e6},
+        "step_alg_bytes": step_alg,
+        "step_hbm_gbs": round(step_alg / (ms_per_step * 1e-3) / 1e9, 1),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -85,6 +85,35 @@ int mi_int4_dequant(const uint32_t* qweight, const uint16_t* scales, float* out,
  * partials fp32 [S][M][N]. 1 <= M <= 16, 64 | K, 64 | N, S | K/64. ---- */
 int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                   float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S, void* stream);
+/* The same linear with the step's next operation fused into its last work-group per
+ * 64-column tile (the reference's consumers prep_res_fold + prep_norm_finish, prep_silu_mul
+ * and the lm_head fold + argmax_stage1, src/kernels/prep.cl:288-384, argmax.cl:82).
+ * `counters`: >= N/64 + 1 zeroed uint32 words; every launch leaves them zeroed again.
+ * Launches that share one counter array must not overlap. */
+enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3 };
+typedef struct mi_gemv_epilogue {
+  uint32_t kind;
+  uint32_t* counters;
+  /* RESID (N = hidden): resid [M][N] += rne(sum_s partials) (rounded as prep_res_fold);
+   * sumsq [N/64][M] the 64-column tiles' sums of squares; then rstd [M] =
+   * 1/sqrt(sum_g sumsq / N + eps) and x_next [M][N] = rne(resid * rstd * next_norm_w). */
+  uint16_t* resid;
+  float* sumsq;
+  float* rstd;
+  const float* next_norm_w;
+  uint16_t* x_next;
+  float eps;
+  /* SILU (N = 2 * inter, interleave16 gate||up): h [M][N/2] = rne(rne(silu(g)) * u) */
+  uint16_t* h;
+  /* LOGITS: logits [M][N] fp32; argmax_part [M][N/64] of 8 bytes (value, index) for
+   * mi_argmax_finish, indices >= vocab_used never win (NULL: no argmax part) */
+  float* logits;
+  void* argmax_part;
+  uint32_t vocab_used;
+} mi_gemv_epilogue;
+int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
+                     float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,
+                     const mi_gemv_epilogue* epilogue, void* stream);
 /* The split-K width this library uses for a shape (the role of kQwen38Tuning,
  * src/model/model_desc.cc:32, and kSmallMTuning, src/kernels/kernels.h:140-170). */
 uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N);
@@ -149,8 +178,8 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
 /* attn_reduce_v2 (attn_v2.cl:383-386): ascending block merge -> attn_out f16
  * [M][q_heads*head_dim] (gated: rne(rne(o) * sigmoid(gate))) */
 int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate,
-                   uint16_t* attn_out, uint32_t M, uint32_t tgt, const mi_attn_shape* shape,
-                   void* stream);
+                   uint16_t* attn_out, uint32_t M, uint32_t tgt, uint32_t kv_len,
+                   const mi_attn_shape* shape, void* stream);
 
 /* ---- the token boundary ---- */
 /* embed_gather (embed_gather.cl:47-49): resid[m] = embed[cur_token[m]]; an id >= vocab
@@ -163,6 +192,16 @@ int mi_embed_gather(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, uint
  * steps < history_len), steps += 1, pos += n_active. part: mi_argmax_groups(vocab) * M * 8
  * bytes of scratch. */
 uint32_t mi_argmax_groups(uint32_t vocab);
+/* argmax_stage2 alone (argmax.cl:133-172) over `groups` (value, index) winners per row, as
+ * written by mi_gemv_w4a16_ex's LOGITS epilogue (groups = vocab / 64) or by stage 1. */
+int mi_argmax_finish(uint32_t* ctrl, const void* part, uint32_t groups, uint32_t* history,
+                     uint32_t history_len, void* stream);
+/* embed_gather + the first RMSNorm in one launch per row: resid[m] = embed[cur_token[m]],
+ * rstd[m] from 64-element chunk sums (prep_res_fold's tree at chunk 64, chunks ascending),
+ * x = rne(resid * rstd * norm_w). Bad ids as embed_gather. hidden % 64 == 0. */
+int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w,
+                  uint16_t* x_out, float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab,
+                  float eps, void* stream);
 int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history,
               uint32_t history_len, uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
 
@@ -207,6 +246,8 @@ int mi_engine_capture(mi_engine* e, uint32_t M);
 int mi_engine_reset(mi_engine* e, uint32_t pos, uint32_t token);
 /* Engine::replay (engine.cc:702-713): enqueue one captured M-row step (no sync). */
 int mi_engine_replay(mi_engine* e, uint32_t M);
+/* The same M-row step enqueued launch by launch, without the graph (no sync). */
+int mi_engine_step_eager(mi_engine* e, uint32_t M);
 /* Engine::generate (engine.cc:726-750): n greedy tokens; the ids land in `tokens`. */
 int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens);
 /* Engine::ingest (engine.cc:715-724): one step per prompt id. */

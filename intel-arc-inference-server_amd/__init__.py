@@ -48,10 +48,13 @@ SIGNATURES = {
     "mi_attn_prep": (i32, [vp, vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, u32, vp]),
     "mi_attn_ppw": (u32, [u32, u32]),
     "mi_attn_decode": (i32, [vp, vp, u32, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, vp, u32, u32, vp, vp]),
-    "mi_attn_reduce": (i32, [vp, vp, vp, vp, u32, u32, vp, vp]),
+    "mi_attn_reduce": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, vp]),
     "mi_embed_gather": (i32, [vp, vp, vp, u32, u32, u32, vp]),
     "mi_argmax_groups": (u32, [u32]),
     "mi_argmax": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
+    "mi_argmax_finish": (i32, [vp, vp, u32, vp, u32, vp]),
+    "mi_embed_norm": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, f32, vp]),
+    "mi_gemv_w4a16_ex": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
     "mi_engine_create": (vp, [vp, u64, vp]),
     "mi_engine_destroy": (None, [vp]),
     "mi_engine_stream": (vp, [vp]),
@@ -60,6 +63,7 @@ SIGNATURES = {
     "mi_engine_capture": (i32, [vp, u32]),
     "mi_engine_reset": (i32, [vp, u32, u32]),
     "mi_engine_replay": (i32, [vp, u32]),
+    "mi_engine_step_eager": (i32, [vp, u32]),
     "mi_engine_generate": (i32, [vp, u32, vp]),
     "mi_engine_ingest": (i32, [vp, vp, u32]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),
@@ -67,6 +71,16 @@ SIGNATURES = {
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
     "mi_accept_greedy": (u32, [vp, vp, u32, vp]),
 }
+
+
+EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS = 0, 1, 2, 3
+
+
+class GemvEpilogue(C.Structure):
+    """mi_gemv_epilogue"""
+    _fields_ = [("kind", u32), ("counters", vp), ("resid", vp), ("sumsq", vp), ("rstd", vp),
+                ("next_norm_w", vp), ("x_next", vp), ("eps", f32), ("h", vp), ("logits", vp),
+                ("argmax_part", vp), ("vocab_used", u32)]
 
 
 class MiError(RuntimeError):
@@ -198,6 +212,9 @@ class Engine:
 
     def replay(self, M=1):
         check(lib().mi_engine_replay(self._h, M), "engine_replay")
+
+    def step_eager(self, M=1):
+        check(lib().mi_engine_step_eager(self._h, M), "engine_step_eager")
 
     def generate(self, n):
         import numpy as np

@@ -21,10 +21,9 @@
 //     256/512-byte row reads; the block's rows of one kv head are contiguous in the
 //     head-major layout;
 //   * all GQA q heads of the kv head share each K/V load (q held in registers, fp32);
-//   * the block is walked in chunks of 256 positions: pass 1 writes the chunk's scores to
-//     LDS, the chunk max updates the running max (an online softmax per chunk, not per
-//     16-position wave), weights exp(s - m) go back to LDS, pass 2 accumulates
-//     sum_p w_p v_p per lane; the position slots are merged at the end in a fixed order.
+//   * the block is walked in chunks of 64 positions, each a single HBM round trip; the
+//     q.K scores run on the matrix cores, the online softmax per chunk (not per 16-position
+//     wave) in LDS, and P.V on the vector ALUs (kernel comment below).
 // Scores and the softmax are fp32; no atomics, so replays are bitwise.
 #include "mi_capi_internal.h"
 #include "mi_common.h"
@@ -32,8 +31,6 @@
 namespace mi {
 namespace {
 
-constexpr uint32_t kChunkP = 256;  // positions per score chunk
-constexpr uint32_t kGqaMax = 8;
 
 __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
   uint32_t p = (len + tgt - 1) / tgt;
@@ -60,38 +57,90 @@ struct AttnDecodeArgs {
   float scale;
 };
 
-// 8 consecutive KV elements of one row as fp32
+// 8 consecutive KV elements of one row, raw (f16: 16 bytes; int8: 8 bytes)
 template <int KV8>
-__device__ __forceinline__ void load8(const void* base, const uint16_t* sc, size_t off, size_t soff,
-                                      float (&v)[8]) {
+struct KvChunk {
+  u4_t w;
+};
+template <>
+struct KvChunk<1> {
+  u2_t w;
+  uint16_t s;
+};
+
+template <int KV8>
+__device__ __forceinline__ KvChunk<KV8> load_chunk(const void* base, const uint16_t* sc, size_t off, size_t soff) {
+  KvChunk<KV8> c;
   if constexpr (KV8 == 0) {
-    const u4_t w = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(base) + off);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    c.w = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(base) + off);
+  } else {
+    c.w = *reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(base) + off);
+    c.s = sc[soff];
+  }
+  return c;
+}
+template <int KV8>
+__device__ __forceinline__ void zero_chunk(KvChunk<KV8>& c) {
+  if constexpr (KV8 == 0) c.w = u4_t{0u, 0u, 0u, 0u};
+  else { c.w = u2_t{0u, 0u}; c.s = 0; }
+}
+// the 8 values as fp32: f16 widened exactly, or int8 * f16(scale) (exact in fp32, kv8.h:126)
+template <int KV8>
+__device__ __forceinline__ void widen_chunk(const KvChunk<KV8>& c, float (&v)[8]) {
+  if constexpr (KV8 == 0) {
+    const uint32_t ws[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = h2f((uint16_t)(ws[i] & 0xFFFFu));
       v[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
     }
   } else {
-    const u2_t w = *reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(base) + off);
-    const float s = h2f(sc[soff]);
-    const uint32_t ws[2] = {w.x, w.y};
+    const float s = h2f(c.s);
+    const uint32_t ws[2] = {c.w.x, c.w.y};
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((ws[i / 4] >> (8 * (i % 4))) & 0xFFu) * s;
   }
 }
 
-// HD: head dim (128 or 256); LP = HD / 8 lanes per row; SLOTS = 256 / LP rows per pass.
-template <int HD, int KV8>
+// 8 KV values of one row as the f16 B operand of an MFMA (int8 values are exact in f16;
+// their row scale is applied to the score afterwards)
+template <int KV8>
+__device__ __forceinline__ h8_t chunk_h8(const KvChunk<KV8>& c) {
+  if constexpr (KV8 == 0) {
+    return __builtin_bit_cast(h8_t, c.w);
+  } else {
+    h8_t r;
+    const uint32_t ws[2] = {c.w.x, c.w.y};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (half_t)(float)(int8_t)((ws[i / 4] >> (8 * (i % 4))) & 0xFFu);
+    return r;
+  }
+}
+
+// HD: head dim; KV8: int8 KV; GQA: q heads per kv head. A work-group walks its block in
+// chunks of 64 positions; every thread issues all of its K and V loads for the chunk
+// before using any, so a chunk costs one HBM round trip.
+//   scores  on the matrix cores: wave w computes the 16 x 16 tile (q heads padded to 16) x
+//           (positions 16w .. 16w+15) with v_mfma_f32_16x16x32_f16, A = q split into an f16
+//           high part and the f16 rounding of the remainder (two MFMAs: the dot is fp32
+//           accurate), B = the K rows, read 16 bytes per lane (lane l: position l % 16,
+//           dims 8 (l / 16) + 32 kk) - no cross-lane reduction at all;
+//   softmax per chunk per head in LDS (max, exp, sum), an online rescale between chunks;
+//   P V     on the vector ALUs: HD / 8 lanes own a V row (8 dims, 16 bytes each), the
+//           256 / (HD / 8) row slots accumulate sum_p w_p v_p and are merged in LDS in slot
+//           order at the end.
+template <int HD, int KV8, int GQA>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
-  constexpr uint32_t LP = HD / 8, SLOTS = 256 / LP, WSLOTS = 64 / LP;
-  __shared__ float sc[kGqaMax][kChunkP];
-  __shared__ float st_alpha[kGqaMax], st_m[kGqaMax], st_l[kGqaMax];
-  __shared__ float red[4][kGqaMax][HD];
+  constexpr uint32_t CH = 64, KK = HD / 32;
+  constexpr uint32_t LP = HD / 8, SLOTS = 256 / LP, VU = CH / SLOTS;
+  __shared__ float sc[GQA][CH];
+  __shared__ float st_alpha[GQA], st_m[GQA], st_l[GQA];
+  __shared__ float red[SLOTS][GQA][HD];
 
   const uint32_t j = blockIdx.x, blk = blockIdx.y, m = blockIdx.z;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t slot = t / LP, dg = t % LP, d0 = dg * 8;
+  const uint32_t qi = lane & 15u, qq = lane >> 4;
   const uint32_t n_act = a.ctrl[CTRL_NACT];
   if (m >= n_act) return;
   const uint32_t pos = a.ctrl[CTRL_POS];
@@ -102,68 +151,92 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   if (nb > a.tgt) nb = a.tgt;
   if (blk >= nb) return;
   const uint32_t p_begin = blk * s, p_end = min(p_begin + s, L);
-  const uint32_t gqa = a.q_heads / a.kv_heads;
 
-  float q[kGqaMax][8];
+  // q as the MFMA A operand: row qi = head (zero past GQA), k = 32 kk + 8 qq + e
+  h8_t qhi[KK], qlo[KK];
 #pragma unroll
-  for (uint32_t g = 0; g < kGqaMax; ++g) {
-    if (g < gqa) {
-      const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * gqa + g) * HD + d0;
+  for (uint32_t kk = 0; kk < KK; ++kk) {
+    float v[8];
+    if (qi < GQA) {
+      const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
       const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
       const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
-      q[g][0] = q0.x; q[g][1] = q0.y; q[g][2] = q0.z; q[g][3] = q0.w;
-      q[g][4] = q1.x; q[g][5] = q1.y; q[g][6] = q1.z; q[g][7] = q1.w;
+      v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+      v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) q[g][i] = 0.f;
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half_t h = (half_t)v[e];
+      qhi[kk][e] = h;
+      qlo[kk][e] = (half_t)(v[e] - (float)h);
     }
   }
-  float acc[kGqaMax][8];
+  float acc[GQA][8];
 #pragma unroll
-  for (uint32_t g = 0; g < kGqaMax; ++g)
+  for (uint32_t g = 0; g < GQA; ++g)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-  if (t < kGqaMax) {
+  if (t < GQA) {
     st_m[t] = -INFINITY;
     st_l[t] = 0.f;
   }
 
-  const size_t hoff = (size_t)j * a.head_stride + d0;
+  const size_t hoff = (size_t)j * a.head_stride;
   const size_t shoff = (size_t)j * a.sc_head_stride;
-  for (uint32_t c0 = p_begin; c0 < p_end; c0 += kChunkP) {
-    const uint32_t clen = min(kChunkP, p_end - c0);
-    // pass 1: scores of the chunk
-    for (uint32_t pl = slot; pl < clen; pl += SLOTS) {
-      const size_t row = kv_row(c0 + pl, a.pages, a.page);
-      float k[8];
-      load8<KV8>(a.kv_k, a.k_scale, row * a.row_stride + hoff, row * a.sc_row_stride + shoff, k);
+  const uint32_t pk = 16u * wave + qi;  // this lane's score position within the chunk
+  for (uint32_t c0 = p_begin; c0 < p_end; c0 += CH) {
+    const uint32_t clen = min(CH, p_end - c0);
+    KvChunk<KV8> kc[KK], vc[VU];
+    if (pk < clen) {
+      const size_t row = kv_row(c0 + pk, a.pages, a.page);
 #pragma unroll
-      for (uint32_t g = 0; g < kGqaMax; ++g) {
-        if (g < gqa) {
-          float d = 0.f;
+      for (uint32_t kk = 0; kk < KK; ++kk)
+        kc[kk] = load_chunk<KV8>(a.kv_k, a.k_scale, row * a.row_stride + hoff + 32 * kk + 8 * qq,
+                                 row * a.sc_row_stride + shoff);
+    } else {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[g][i], k[i], d);
+      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(kc[kk]);
+    }
 #pragma unroll
-          for (uint32_t o = LP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-          if (dg == 0) sc[g][pl] = d * a.scale;
-        }
+    for (uint32_t u = 0; u < VU; ++u) {
+      const uint32_t pl = u * SLOTS + slot;
+      if (pl < clen) {
+        const size_t row = kv_row(c0 + pl, a.pages, a.page);
+        vc[u] = load_chunk<KV8>(a.kv_v, a.v_scale, row * a.row_stride + hoff + d0, row * a.sc_row_stride + shoff);
+      } else {
+        zero_chunk<KV8>(vc[u]);
       }
+    }
+    // scores
+    f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t kk = 0; kk < KK; ++kk) {
+      const h8_t b = chunk_h8<KV8>(kc[kk]);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[kk], b, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[kk], b, d, 0, 0, 0);
+    }
+    float rs = a.scale;
+    if constexpr (KV8 == 1) rs = a.scale * h2f(kc[0].s);
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      const uint32_t head = 4u * qq + r;
+      if (head < GQA && pk < clen) sc[head][pk] = d[r] * rs;
     }
     __syncthreads();
     // chunk max, weights and chunk sum: wave w owns heads w, w + 4
-    for (uint32_t g = wave; g < gqa; g += 4) {
-      float mx = -INFINITY;
-      for (uint32_t p = lane; p < clen; p += 64) mx = fmaxf(mx, sc[g][p]);
+    for (uint32_t g = wave; g < GQA; g += 4) {
+      const float v = lane < clen ? sc[g][lane] : -INFINITY;
+      float mx = v;
 #pragma unroll
       for (uint32_t o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
       const float m_old = st_m[g];
       const float m_new = fmaxf(m_old, mx);
-      float sum = 0.f;
-      for (uint32_t p = lane; p < clen; p += 64) {
-        const float w = expf(sc[g][p] - m_new);
-        sc[g][p] = w;
-        sum += w;
-      }
+      const float w = lane < clen ? expf(v - m_new) : 0.f;
+      if (lane < clen) sc[g][lane] = w;
+      float sum = w;
 #pragma unroll
       for (uint32_t o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
       if (lane == 0) {
@@ -174,22 +247,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
       }
     }
     __syncthreads();
-    // pass 2: rescale, then accumulate w * v
+    // rescale, then accumulate w * v from the registers loaded above
 #pragma unroll
-    for (uint32_t g = 0; g < kGqaMax; ++g) {
-      if (g < gqa) {
-        const float al = st_alpha[g];
+    for (uint32_t g = 0; g < GQA; ++g) {
+      const float al = st_alpha[g];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] *= al;
-      }
+      for (int i = 0; i < 8; ++i) acc[g][i] *= al;
     }
-    for (uint32_t pl = slot; pl < clen; pl += SLOTS) {
-      const size_t row = kv_row(c0 + pl, a.pages, a.page);
-      float v[8];
-      load8<KV8>(a.kv_v, a.v_scale, row * a.row_stride + hoff, row * a.sc_row_stride + shoff, v);
 #pragma unroll
-      for (uint32_t g = 0; g < kGqaMax; ++g) {
-        if (g < gqa) {
+    for (uint32_t u = 0; u < VU; ++u) {
+      const uint32_t pl = u * SLOTS + slot;
+      if (pl < clen) {
+        float v[8];
+        widen_chunk<KV8>(vc[u], v);
+#pragma unroll
+        for (uint32_t g = 0; g < GQA; ++g) {
           const float w = sc[g][pl];
 #pragma unroll
           for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(w, v[i], acc[g][i]);
@@ -198,68 +270,97 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     }
     __syncthreads();
   }
-  // merge the position slots: within the wave (xor over the slot bits), then the 4 waves
+  // merge the row slots in slot order through LDS
 #pragma unroll
-  for (uint32_t g = 0; g < kGqaMax; ++g) {
-    if (g < gqa) {
+  for (uint32_t g = 0; g < GQA; ++g)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float v = acc[g][i];
-#pragma unroll
-        for (uint32_t o = LP; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-        acc[g][i] = v;
-      }
-      if (lane < LP) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) red[wave][g][d0 + i] = acc[g][i];
-      }
-    }
-  }
-  (void)WSLOTS;
+    for (int i = 0; i < 8; ++i) red[slot][g][d0 + i] = acc[g][i];
   __syncthreads();
-  for (uint32_t idx = t; idx < gqa * HD; idx += 256) {
-    const uint32_t g = idx / HD, d = idx % HD;
-    const float v = ((red[0][g][d] + red[1][g][d]) + red[2][g][d]) + red[3][g][d];
-    float* out = a.attn_part + (((size_t)(j * gqa + g) * a.tgt + blk) * a.M + m) * (HD + 2);
-    out[2 + d] = v;
-    if (d == 0) {
+  for (uint32_t idx = t; idx < GQA * HD; idx += 256) {
+    const uint32_t g = idx / HD, dd = idx % HD;
+    float v = red[0][g][dd];
+#pragma unroll
+    for (uint32_t sl = 1; sl < SLOTS; ++sl) v += red[sl][g][dd];
+    float* out = a.attn_part + (((size_t)(j * GQA + g) * a.tgt + blk) * a.M + m) * (HD + 2);
+    out[2 + dd] = v;
+    if (dd == 0) {
       out[0] = st_m[g];
       out[1] = st_l[g];
     }
   }
 }
 
-// grid (q_heads, M), HD lanes: attn_v2.cl:383-428.
+// grid (q_heads, M), HD lanes: attn_v2.cl:383-428's merge of a row's nb block partials.
+// Phase 1 reads every block's (mx, sm) in parallel and forms the common max M = max mx
+// and each block's factor exp(mx_b - M); phase 2 sums acc_b * factor_b in ascending b with
+// all the loads independent of each other. Mathematically the reference's sequential
+// rescaling merge; the roundings differ at the last place only.
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __restrict__ ctrl,
                                                           const float* __restrict__ attn_part,
                                                           const float* __restrict__ attn_gate,
                                                           uint16_t* __restrict__ attn_out, uint32_t M,
                                                           uint32_t q_heads, uint32_t HD, uint32_t tgt,
-                                                          uint32_t gated) {
+                                                          uint32_t gated, uint32_t kv_len) {
+  __shared__ float fac[1024];
+  __shared__ float s_sm;
   const uint32_t h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
   if (m >= ctrl[CTRL_NACT]) return;
   const uint32_t pos = ctrl[CTRL_POS];
-  uint32_t nb = (pos + m) / v2_ppw(pos + m + 1, tgt) + 1;
+  uint32_t L = pos + m + 1;
+  if (kv_len && L > kv_len) L = kv_len;
+  uint32_t nb = (L - 1) / v2_ppw(L, tgt) + 1;
   if (nb > tgt) nb = tgt;
-  float mx = -INFINITY, sm = 0.f, acc = 0.f;
   const size_t PART = HD + 2;
-  for (uint32_t b = 0; b < nb; ++b) {
-    const float* p = attn_part + (((size_t)h * tgt + b) * M + m) * PART;
-    const float bmx = p[0], bsm = p[1], bacc = p[2 + d];
-    const float nmx = fmaxf(mx, bmx);
-    const float al = expf(mx - nmx);
-    const float bs = expf(bmx - nmx);
-    sm = __builtin_fmaf(sm, al, bsm * bs);
-    acc = __builtin_fmaf(acc, al, bacc * bs);
-    mx = nmx;
+  const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
+  const size_t bstride = (size_t)M * PART;
+  // phase 1 (wave 0): the common max and the per-block factors
+  if (d < 64) {
+    float mx = -INFINITY;
+    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, base[b * bstride]);
+#pragma unroll
+    for (uint32_t o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sm = 0.f;
+    for (uint32_t b = d; b < nb; b += 64) {
+      const float f = expf(base[b * bstride] - mx);
+      fac[b] = f;
+      sm = __builtin_fmaf(base[b * bstride + 1], f, sm);
+    }
+#pragma unroll
+    for (uint32_t o = 32; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+    if (d == 0) s_sm = sm;
   }
-  const float o = acc / sm;
+  __syncthreads();
+  float acc = 0.f;
+  uint32_t b = 0;
+  for (; b + 8 <= nb; b += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = base[(b + u) * bstride + 2 + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(v[u], fac[b + u], acc);
+  }
+  for (; b < nb; ++b) acc = __builtin_fmaf(base[b * bstride + 2 + d], fac[b], acc);
+  const float o = acc / s_sm;
   uint16_t r;
   if (gated && attn_gate)
     r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
   else
     r = f2h(o);
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
+}
+
+template <int HD, int KV8>
+int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
+  switch (gqa) {
+    case 1: attn_decode_kernel<HD, KV8, 1><<<grid, 256, 0, st>>>(a); break;
+    case 2: attn_decode_kernel<HD, KV8, 2><<<grid, 256, 0, st>>>(a); break;
+    case 4: attn_decode_kernel<HD, KV8, 4><<<grid, 256, 0, st>>>(a); break;
+    case 5: attn_decode_kernel<HD, KV8, 5><<<grid, 256, 0, st>>>(a); break;
+    case 6: attn_decode_kernel<HD, KV8, 6><<<grid, 256, 0, st>>>(a); break;
+    case 8: attn_decode_kernel<HD, KV8, 8><<<grid, 256, 0, st>>>(a); break;
+    default: return -1;
+  }
+  return 0;
 }
 
 }  // namespace
@@ -286,8 +387,10 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
     return mi_fail(MI_ERR_ARG, "attn_decode: kv_kind 0 (fp16) or 1 (int8 + fp16 scales)");
   const uint32_t HD = shape->head_dim;
   if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_decode: head_dim must be 128 or 256");
-  if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads || shape->q_heads / shape->kv_heads > kGqaMax)
-    return mi_fail(MI_ERR_SHAPE, "attn_decode: q_heads / kv_heads must be an integer <= 8");
+  const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
+  if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads ||
+      !(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 5 || gqa == 6 || gqa == 8))
+    return mi_fail(MI_ERR_SHAPE, "attn_decode: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
   if (pages && (page == 0 || page % 16))
     return mi_fail(MI_ERR_SHAPE, "attn_decode: a KV page holds a multiple of 16 positions");
   if ((row_stride % 8) || (head_stride % 8))
@@ -299,23 +402,23 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
   dim3 grid(shape->kv_heads, tgt, M);
   hipStream_t st = (hipStream_t)stream;
   if (HD == 128) {
-    if (kv_kind == 0) attn_decode_kernel<128, 0><<<grid, 256, 0, st>>>(a);
-    else attn_decode_kernel<128, 1><<<grid, 256, 0, st>>>(a);
+    if (kv_kind == 0) launch_decode<128, 0>(a, gqa, grid, st);
+    else launch_decode<128, 1>(a, gqa, grid, st);
   } else {
-    if (kv_kind == 0) attn_decode_kernel<256, 0><<<grid, 256, 0, st>>>(a);
-    else attn_decode_kernel<256, 1><<<grid, 256, 0, st>>>(a);
+    if (kv_kind == 0) launch_decode<256, 0>(a, gqa, grid, st);
+    else launch_decode<256, 1>(a, gqa, grid, st);
   }
   return mi_hip((int)hipGetLastError(), "attn_decode");
 }
 
 int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate, uint16_t* attn_out,
-                   uint32_t M, uint32_t tgt, const mi_attn_shape* shape, void* stream) {
-  if (!ctrl || !attn_part || !attn_out || !shape || M == 0 || tgt == 0)
-    return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments");
+                   uint32_t M, uint32_t tgt, uint32_t kv_len, const mi_attn_shape* shape, void* stream) {
+  if (!ctrl || !attn_part || !attn_out || !shape || M == 0 || tgt == 0 || tgt > 1024)
+    return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
   attn_reduce_kernel<<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
-      ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated);
+      ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
 }
 

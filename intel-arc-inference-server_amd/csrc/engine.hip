@@ -92,6 +92,8 @@ struct mi_engine {
   float* attn_part = nullptr;
   float* logits = nullptr;
   void* argmax_part = nullptr;
+  uint32_t* counters = nullptr;  // the fused GEMV epilogues' tile counters (self-resetting)
+  float* rstd = nullptr;
   uint32_t norm_g = 20;
   mi_attn_shape ash{};
   hipGraphExec_t graphs[17] = {};
@@ -136,7 +138,7 @@ struct mi_engine {
     ash = mi_attn_shape{QH, KVH, HD, m.rot_dim, 0u, qkv_n, QH * HD, (QH + KVH) * HD,
                         1.0f / std::sqrt(float(HD)), m.rms_eps};
     ash.scale = float(1.0 / std::sqrt(double(HD)));
-    norm_g = (H % 256 == 0) ? H / 256 : (H + 255) / 256;
+    norm_g = H / 64;  // the fused epilogues take the residual's sum of squares in 64-element chunks
     layer.resize(m.layers);
     size_t part_max = 0;
     for (Layer& L : layer) {
@@ -173,7 +175,11 @@ struct mi_engine {
     MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
     MI_TRY(alloc(&attn_part, size_t(QH) * m.attn_tgt * R * (HD + 2)));
     MI_TRY(alloc(&logits, size_t(R) * m.vocab));
-    MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * mi_argmax_groups(m.vocab)));
+    MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * (m.vocab / 64 + mi_argmax_groups(m.vocab))));
+    const size_t max_tiles = std::max<size_t>({qkv_n, 2 * size_t(m.inter), size_t(m.vocab), size_t(H)}) / 64 + 1;
+    MI_TRY(alloc(&counters, max_tiles));
+    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(counters, 0, max_tiles * 4, stream)), "counters clear"));
+    MI_TRY(alloc(&rstd, R));
 
     // synthetic weights (BASELINE config 2's distributions)
     for (Layer& L : layer) {
@@ -208,26 +214,33 @@ struct mi_engine {
     return 0;
   }
 
-  // res_fold + norm_finish: the residual fold of the previous linear and the next norm
-  int res_norm(const float* partials, uint32_t s_prev, const float* w, uint32_t M) {
-    MI_TRY(mi_res_fold(partials, resid, sumsq, M, d.hidden, s_prev, norm_g, stream));
-    MI_TRY(mi_norm_finish(sumsq, resid, w, x, M, d.hidden, norm_g, d.rms_eps, stream));
-    return 0;
-  }
-
   int gemv(const Linear& l, const uint16_t* in, uint32_t M) {
     return mi_gemv_w4a16(l.q, l.s, in, part, M, l.K, l.N, l.S, stream);
   }
 
+  mi_gemv_epilogue resid_epi(const float* next_w) const {
+    mi_gemv_epilogue e{};
+    e.kind = MI_EPI_RESID;
+    e.counters = counters;
+    e.resid = resid;
+    e.sumsq = sumsq;
+    e.rstd = rstd;
+    e.next_norm_w = next_w;
+    e.x_next = x;
+    e.eps = d.rms_eps;
+    return e;
+  }
+
   // One step over M rows, enqueued on `stream` (recorded into a graph by capture()).
+  // Seven launches per layer: qkv GEMV; attn_prep; attn_decode; attn_reduce; o GEMV with
+  // the residual fold + post-attention norm fused; gate||up GEMV with silu*up fused;
+  // down GEMV with the residual fold + next norm fused.
   int enqueue_step(uint32_t M) {
     const uint32_t HD = d.head_dim, KVH = d.kv_heads;
     const size_t layer_kv = size_t(KVH) * d.max_len * HD;
-    MI_TRY(mi_embed_gather(ctrl, embed, resid, M, d.hidden, d.vocab, stream));
-    uint32_t s_prev = 0;
+    MI_TRY(mi_embed_norm(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      MI_TRY(res_norm(part, s_prev, L.in_norm, M));
       MI_TRY(gemv(L.qkv, x, M));
       uint16_t* lk = kv_k + li * layer_kv;
       uint16_t* lv = kv_v + li * layer_kv;
@@ -235,18 +248,26 @@ struct mi_engine {
                           size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
       MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
                             nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
-      MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, &ash, stream));
-      MI_TRY(gemv(L.o, attn_out, M));
-      MI_TRY(res_norm(part, L.o.S, L.post_norm, M));
-      MI_TRY(gemv(L.gate_up, x, M));
-      MI_TRY(mi_silu_mul(part, hbuf, M, d.inter, L.gate_up.S, stream));
-      MI_TRY(gemv(L.down, hbuf, M));
-      s_prev = L.down.S;
+      MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+      const mi_gemv_epilogue eo = resid_epi(L.post_norm);
+      MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part, M, L.o.K, L.o.N, L.o.S, &eo, stream));
+      mi_gemv_epilogue eg{};
+      eg.kind = MI_EPI_SILU;
+      eg.counters = counters;
+      eg.h = hbuf;
+      MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
+                              stream));
+      const mi_gemv_epilogue ed = resid_epi(li + 1 < d.layers ? layer[li + 1].in_norm : final_norm);
+      MI_TRY(mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part, M, L.down.K, L.down.N, L.down.S, &ed, stream));
     }
-    MI_TRY(res_norm(part, s_prev, final_norm, M));
-    MI_TRY(gemv(lm_head, x, M));
-    MI_TRY(mi_fold_partials(part, nullptr, logits, lm_head.S, M, d.vocab, stream));
-    MI_TRY(mi_argmax(ctrl, logits, argmax_part, history, d.max_len, M, d.vocab, d.vocab_used, stream));
+    mi_gemv_epilogue el{};
+    el.kind = MI_EPI_LOGITS;
+    el.counters = counters;
+    el.logits = logits;
+    el.argmax_part = argmax_part;
+    el.vocab_used = d.vocab_used;
+    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
+    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
     return 0;
   }
 
@@ -289,7 +310,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
     return nullptr;
   }
   const mi_model_desc& m = *desc;
-  if (m.layers == 0 || m.hidden % 256 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
+  if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64) {
@@ -386,6 +407,13 @@ int mi_engine_reset(mi_engine* e, uint32_t pos, uint32_t token) {
 int mi_engine_replay(mi_engine* e, uint32_t M) {
   if (!e || M == 0 || M > e->d.max_rows || !e->graphs[M]) return mi_fail(MI_ERR_STATE, "engine_replay: not captured");
   return mi_hip(static_cast<int>(hipGraphLaunch(e->graphs[M], e->stream)), "hipGraphLaunch");
+}
+
+// The same step enqueued kernel by kernel, without the graph (for tools that trace kernel
+// launches, and for comparing against the graph replay).
+int mi_engine_step_eager(mi_engine* e, uint32_t M) {
+  if (!e || M == 0 || M > e->d.max_rows) return mi_fail(MI_ERR_ARG, "engine_step_eager: M out of range");
+  return e->enqueue_step(M);
 }
 
 int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens) {

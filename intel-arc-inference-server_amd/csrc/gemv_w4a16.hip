@@ -29,7 +29,24 @@
 // rows - every output element is its own MFMA dot and the same fixed merges - so S and
 // the wave split are functions of the shape only (mi_gemv_pick_s).
 //
-// No atomics: replays are bitwise identical.
+// Fused epilogues (mi_gemv_w4a16_ex). The work-groups of one 64-column tile count
+// themselves in a self-resetting counter; the last one to finish folds the tile's S
+// partials in ascending s (the consumer's fold of gemv.cl:1-10, so the result does not
+// depend on which work-group is last) and applies the step's next operation:
+//   RESID   resid = rne(resid + rne(sum_s part)) and the tile's sum of squares (the
+//           reference's res_fold at 64-element chunks, prep_ref.h:120-156); the last tile
+//           of the launch then forms rstd = 1/sqrt(sum_g sumsq / N + eps) and the next
+//           RMSNorm's x = rne(r * rstd * w) (norm_finish, prep_ref.h:158-168);
+//   SILU    h = rne(rne(silu(rne(g))) * rne(u)) over the interleave16 gate||up columns
+//           (prep_silu_mul, prep_ref.h:170-189);
+//   LOGITS  fp32 logits and the tile's (max, lowest index) for argmax_stage2
+//           (argmax.cl:63-65's comparator; the vocab_used mask).
+// Hand-off between the work-groups of one launch: the partials, the tiles' sums of squares
+// and the folded residual are written and read with device-coherent (sc1) accesses; each
+// thread waits for its own stores to complete before the work-group increments the
+// counter (a relaxed device-scope integer atomic), so the last arrival reads complete data.
+// No whole-L2 writeback or invalidate is needed (an agent-scope fence would emit both in
+// every work-group). No float atomics: replays stay bitwise identical.
 #include "mi_common.h"
 #include "mi_capi_internal.h"
 
@@ -63,15 +80,52 @@ __device__ __forceinline__ h8_t perm_x(u4_t v) {
   return h8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
 }
 
-// MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together.
-template <int MR, int U>
+struct GemvEpi {
+  uint32_t* counters;     // >= N/64 + 1 words, zero between launches
+  uint16_t* resid;        // RESID: [M][N]
+  float* sumsq;           // RESID: [N/64][M]
+  float* rstd;            // RESID: [M]
+  const float* next_w;    // RESID: the next RMSNorm's fp32 weights [N]
+  uint16_t* x_next;       // RESID: [M][N]
+  uint16_t* h;            // SILU: [M][N/2]
+  float* out32;           // LOGITS: [M][N]
+  u2_t* argmax_part;      // LOGITS: [M][N/64] (value bits, index), or NULL
+  uint32_t vocab_used;    // LOGITS
+  float eps;              // RESID
+};
+
+enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
+
+// argmax.cl:63-65: strictly greater wins, an exact tie keeps the lower index
+__device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
+  return (av > bv) || (av == bv && ai < bi);
+}
+
+// true in the work-group that arrives last at counter `c` (`total` arrivals); resets it.
+// Callers write everything the last arrival reads with st_agent before calling.
+__device__ __forceinline__ bool last_arrival(uint32_t* c, uint32_t total, uint32_t* s_flag) {
+  wait_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == total - 1u;
+    if (*s_flag) st_agent(c, 0u);
+  }
+  __syncthreads();
+  return *s_flag != 0u;
+}
+
+// MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue.
+template <int MR, int U, int EPI>
 __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ x,
                                                          float* __restrict__ partials, uint32_t M,
-                                                         uint32_t K, uint32_t N, uint32_t gps) {
+                                                         uint32_t K, uint32_t N, uint32_t gps,
+                                                         GemvEpi epi) {
   constexpr int RR = MR < 4 ? MR : 4;  // accumulator rows a lane holds (rows 4*(l/16) + r)
   __shared__ float red[kWaves][MR][kCols];
+  __shared__ uint32_t s_flag;
 
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t c4 = lane & 15u, q = lane >> 4;
@@ -151,7 +205,108 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     float v = red[0][row][col];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) v += red[w][row][col];
-    partials[((size_t)s * M + row) * N + n0 + col] = v;
+    if constexpr (EPI == EPI_PARTIALS)
+      partials[((size_t)s * M + row) * N + n0 + col] = v;
+    else
+      st_agent(partials + ((size_t)s * M + row) * N + n0 + col, v);
+  }
+  if constexpr (EPI == EPI_PARTIALS) return;
+
+  // ---- the tile's last work-group folds the S partials and applies the epilogue ----
+  const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
+  if (!last_arrival(epi.counters + tile, S, &s_flag)) return;
+  const uint32_t t = threadIdx.x;
+  // sum_s partials[s][row][n] from 0.f in ascending s; the loads go out 8 at a time
+  auto fold = [&](uint32_t row, uint32_t n) {
+    const float* p = partials + (size_t)row * N + n;
+    const size_t step = (size_t)M * N;
+    float a = 0.f;
+    uint32_t ss = 0;
+    for (; ss + 8 <= S; ss += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = ld_agent(p + (ss + u) * step);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a += v[u];
+    }
+    for (; ss < S; ++ss) a += ld_agent(p + ss * step);
+    return a;
+  };
+  if constexpr (EPI == EPI_RESID) {
+    // one row per wave per pass, a column per lane; the 64-lane tree is the reference's
+    // 256-lane tree over a 64-element chunk (lanes 64..255 add exact zeros)
+    for (uint32_t row = wave; row < M; row += kWaves) {
+      const uint32_t n = n0 + lane;
+      uint16_t* rp = epi.resid + (size_t)row * N + n;
+      const uint16_t rb = f2h(h2f(*rp) + h2f(f2h(fold(row, n))));
+      st_agent(rp, rb);
+      const float v = h2f(rb);
+      float a = __builtin_fmaf(v, v, 0.f);
+#pragma unroll
+      for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
+      if (lane == 0) st_agent(epi.sumsq + (size_t)tile * M + row, a);
+    }
+    // the launch's last tile: rstd per row and the next norm's input
+    if (!last_arrival(epi.counters + ntiles, ntiles, &s_flag)) return;
+    // the tiles' sums, loaded in parallel, then added in ascending tile order
+    __shared__ float s_ss[1024];
+    __shared__ float s_rstd[16];
+    for (uint32_t row = 0; row < M; ++row) {
+      for (uint32_t g = t; g < ntiles; g += 256u) s_ss[g] = ld_agent(epi.sumsq + (size_t)g * M + row);
+      __syncthreads();
+      if (t == 0) {
+        float tot = 0.f;
+        for (uint32_t g = 0; g < ntiles; ++g) tot += s_ss[g];
+        const float r = 1.0f / sqrtf(tot / (float)N + epi.eps);
+        s_rstd[row] = r;
+        epi.rstd[row] = r;
+      }
+      __syncthreads();
+    }
+    for (uint32_t row = 0; row < M; ++row) {
+      const float r = s_rstd[row];
+      const uint16_t* rr = epi.resid + (size_t)row * N;
+      uint16_t* xo = epi.x_next + (size_t)row * N;
+      uint32_t n = t;
+      for (; n + 3u * 256u < N; n += 4u * 256u) {
+        uint16_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ld_agent(rr + n + u * 256u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xo[n + u * 256u] = f2h(h2f(v[u]) * r * epi.next_w[n + u * 256u]);
+      }
+      for (; n < N; n += 256u) xo[n] = f2h(h2f(ld_agent(rr + n)) * r * epi.next_w[n]);
+    }
+  } else if constexpr (EPI == EPI_SILU) {
+    // 64 interleave16 columns = 32 outputs k = 32 tile + i (gate at gflat, up at gflat + 16)
+    for (uint32_t i = t; i < 32u * M; i += 256u) {
+      const uint32_t row = i / 32u, k = tile * 32u + i % 32u;
+      const uint32_t gflat = (k / 16u) * 32u + (k % 16u);
+      const uint16_t g_b = f2h(fold(row, gflat)), u_b = f2h(fold(row, gflat + 16u));
+      const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
+      epi.h[(size_t)row * (N / 2) + k] = f2h(h2f(s_b) * h2f(u_b));
+    }
+  } else if constexpr (EPI == EPI_LOGITS) {
+    for (uint32_t row = wave; row < M; row += kWaves) {
+      const uint32_t n = n0 + lane;
+      const float v = fold(row, n);
+      epi.out32[(size_t)row * N + n] = v;
+      if (epi.argmax_part) {
+        float bv = n < epi.vocab_used ? v : -INFINITY;
+        uint32_t bi = n;
+#pragma unroll
+        for (int st = 32; st > 0; st >>= 1) {
+          const float ov = __shfl_down(bv, st, 64);
+          const uint32_t oi = __shfl_down(bi, st, 64);
+          if (lane + st < 64 && better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (lane == 0)
+          epi.argmax_part[(size_t)row * ntiles + tile] = u2_t{__builtin_bit_cast(uint32_t, bv), bi};
+      }
+    }
   }
 }
 
@@ -168,16 +323,37 @@ __global__ __launch_bounds__(256) void fold_partials_kernel(const float* __restr
   if (out32) out32[i] = t;
 }
 
-template <int MR>
-int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part,
-                uint32_t M, uint32_t K, uint32_t N, uint32_t S, hipStream_t st) {
+template <int MR, int EPI>
+int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part, uint32_t M,
+                uint32_t K, uint32_t N, uint32_t S, const GemvEpi& epi, hipStream_t st) {
   const uint32_t G = K / 64, gps = G / S;
   dim3 grid(N / kCols, S);
   if (gps >= 16)
-    gemv_w4a16_kernel<MR, 4><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps);
+    gemv_w4a16_kernel<MR, 4, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, epi);
   else
-    gemv_w4a16_kernel<MR, 2><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps);
+    gemv_w4a16_kernel<MR, 2, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, epi);
   return (int)hipGetLastError();
+}
+
+template <int EPI>
+int launch_rows(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part, uint32_t M,
+                uint32_t K, uint32_t N, uint32_t S, const GemvEpi& epi, hipStream_t st) {
+  if (M == 1) return launch_gemv<1, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
+  if (M <= 4) return launch_gemv<4, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
+  return launch_gemv<16, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
+}
+
+int check_gemv(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, const float* partials,
+               uint32_t M, uint32_t K, uint32_t N, uint32_t S) {
+  if (!qweight || !scales || !x || !partials) return mi_fail(MI_ERR_ARG, "gemv_w4a16: null pointer");
+  if (M < 1 || M > 16) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: M must be 1..16");
+  if (K == 0 || K % 64 || N == 0 || N % 64)
+    return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: K and N must be non-zero multiples of 64");
+  if (S == 0 || (K / 64) % S) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: S must divide K/64");
+  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(scales) % 8)
+    return mi_fail(MI_ERR_ARG, "gemv_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
+  return 0;
 }
 
 }  // namespace
@@ -203,23 +379,44 @@ extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
 extern "C" int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                              float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,
                              void* stream) {
-  if (!qweight || !scales || !x || !partials) return mi_fail(MI_ERR_ARG, "gemv_w4a16: null pointer");
-  if (M < 1 || M > 16) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: M must be 1..16");
-  if (K == 0 || K % 64 || N == 0 || N % 64)
-    return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: K and N must be non-zero multiples of 64");
-  if (S == 0 || (K / 64) % S) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16: S must divide K/64");
-  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(scales) % 8)
-    return mi_fail(MI_ERR_ARG, "gemv_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
+  if (int e = check_gemv(qweight, scales, x, partials, M, K, N, S)) return e;
+  const GemvEpi none{};
+  return mi_hip(launch_rows<EPI_PARTIALS>(qweight, scales, x, partials, M, K, N, S, none,
+                                          static_cast<hipStream_t>(stream)),
+                "gemv_w4a16 launch");
+}
+
+extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
+                                float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,
+                                const mi_gemv_epilogue* ep, void* stream) {
+  if (int e = check_gemv(qweight, scales, x, partials, M, K, N, S)) return e;
+  if (!ep) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: null epilogue");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int e;
-  if (M == 1)
-    e = launch_gemv<1>(qweight, scales, x, partials, M, K, N, S, st);
-  else if (M <= 4)
-    e = launch_gemv<4>(qweight, scales, x, partials, M, K, N, S, st);
-  else
-    e = launch_gemv<16>(qweight, scales, x, partials, M, K, N, S, st);
-  return mi_hip(e, "gemv_w4a16 launch");
+  GemvEpi e{ep->counters, ep->resid, ep->sumsq, ep->rstd, ep->next_norm_w, ep->x_next, ep->h,
+            ep->logits, reinterpret_cast<u2_t*>(ep->argmax_part), ep->vocab_used, ep->eps};
+  int r;
+  switch (ep->kind) {
+    case MI_EPI_PARTIALS:
+      r = launch_rows<EPI_PARTIALS>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    case MI_EPI_RESID:
+      if (!e.counters || !e.resid || !e.sumsq || !e.rstd || !e.next_w || !e.x_next || N / kCols > 1024)
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex RESID: counters, resid, sumsq, rstd, next_norm_w, x_next; N <= 65536");
+      r = launch_rows<EPI_RESID>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    case MI_EPI_SILU:
+      if (!e.counters || !e.h || N % 32) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex SILU: counters, h");
+      r = launch_rows<EPI_SILU>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    case MI_EPI_LOGITS:
+      if (!e.counters || !e.out32 || e.vocab_used > N)
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex LOGITS: counters, logits, vocab_used <= N");
+      r = launch_rows<EPI_LOGITS>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    default:
+      return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: unknown epilogue");
+  }
+  return mi_hip(r, "gemv_w4a16_ex launch");
 }
 
 extern "C" int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,

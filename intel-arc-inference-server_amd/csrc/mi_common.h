@@ -63,6 +63,21 @@ __device__ __forceinline__ u4_t load_stream16(const uint32_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
 }
 
+// Device-coherent (agent scope) accesses for data that work-groups of one launch hand to
+// each other: relaxed atomics, which the compiler emits as sc1 loads and stores that are
+// coherent across the XCDs' L2s without any cache writeback or invalidate.
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this thread's memory operations have completed (vector memory counter 0),
+// and keeps the compiler from moving memory operations across the wait.
+__device__ __forceinline__ void wait_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Launch helper: returns the launch error as an int.
 #define MI_LAUNCH_CHECK() return (int)hipGetLastError()
 

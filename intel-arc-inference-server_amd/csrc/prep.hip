@@ -253,6 +253,49 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(uint32_t* __restrict_
   }
 }
 
+
+// grid (M), 256 lanes: embed_gather followed by the first RMSNorm, with the residual's
+// sum of squares taken in 64-element chunks (the reference's res_fold tree at chunk 64:
+// one element per lane, then the pairwise tree; chunks summed in ascending order).
+__global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ ctrl,
+                                                         const uint16_t* __restrict__ embed,
+                                                         uint16_t* __restrict__ resid,
+                                                         const float* __restrict__ norm_w,
+                                                         uint16_t* __restrict__ x_out,
+                                                         float* __restrict__ rstd_out, uint32_t hidden,
+                                                         uint32_t vocab, float eps) {
+  __shared__ float chunk[1024];
+  const uint32_t m = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t row = ctrl[CTRL_CUR + m];
+  if (row >= vocab) {
+    if (t == 0) ctrl[CTRL_DEBUG] = 0xDEAD0001u;
+    return;
+  }
+  const uint16_t* src = embed + (size_t)row * hidden;
+  uint16_t* dst = resid + (size_t)m * hidden;
+  const uint32_t nch = hidden / 64;
+  for (uint32_t c = wave; c < nch; c += 4) {
+    const uint16_t v16 = src[c * 64 + lane];
+    dst[c * 64 + lane] = v16;
+    const float v = h2f(v16);
+    float a = __builtin_fmaf(v, v, 0.f);
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
+    if (lane == 0) chunk[c] = a;
+  }
+  __syncthreads();
+  __shared__ float s_rstd;
+  if (t == 0) {
+    float tot = 0.f;
+    for (uint32_t c = 0; c < nch; ++c) tot += chunk[c];
+    s_rstd = 1.0f / sqrtf(tot / (float)hidden + eps);
+    if (rstd_out) rstd_out[m] = s_rstd;
+  }
+  __syncthreads();
+  const float r = s_rstd;
+  for (uint32_t k = t; k < hidden; k += kWG) x_out[(size_t)m * hidden + k] = f2h(h2f(src[k]) * r * norm_w[k]);
+}
+
 // The comparator (argmax.cl:63-65): strictly greater wins, an exact tie keeps the lower index.
 __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
   return (av > bv) || (av == bv && ai < bi);
@@ -400,7 +443,23 @@ int mi_embed_gather(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, uint
   return mi_hip((int)hipGetLastError(), "embed_gather");
 }
 
+int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                  float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab, float eps, void* stream) {
+  if (!ctrl || !embed || !resid || !norm_w || !x_out || M == 0 || M > 8 || hidden % 64 || hidden > 65536)
+    return mi_fail(MI_ERR_ARG, "embed_norm: bad arguments (M <= 8, hidden a multiple of 64)");
+  embed_norm_kernel<<<M, kWG, 0, (hipStream_t)stream>>>(ctrl, embed, resid, norm_w, x_out, rstd, hidden, vocab,
+                                                         eps);
+  return mi_hip((int)hipGetLastError(), "embed_norm");
+}
+
 uint32_t mi_argmax_groups(uint32_t vocab) { return (vocab + kChunk - 1) / kChunk; }
+
+int mi_argmax_finish(uint32_t* ctrl, const void* part, uint32_t groups, uint32_t* history, uint32_t history_len,
+                     void* stream) {
+  if (!ctrl || !part || groups == 0) return mi_fail(MI_ERR_ARG, "argmax_finish: bad arguments");
+  argmax_stage2_kernel<<<1, kWG, 0, (hipStream_t)stream>>>(ctrl, (const u2_t*)part, history, history_len, groups);
+  return mi_hip((int)hipGetLastError(), "argmax_finish");
+}
 
 int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history, uint32_t history_len,
               uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream) {

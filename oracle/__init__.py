@@ -71,6 +71,7 @@ def lib():
             "orc_moe_block": (None, [i32, u32, u32, u32, u32, u32, vp, vp, vp, vp, sz, sz, vp,
                                      vp, sz, sz, u32, u32, vp, vp]),
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
+            "orc_threads": (i32, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

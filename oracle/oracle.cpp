@@ -157,6 +157,14 @@ struct KvRead {
 
 extern "C" {
 
+int orc_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
 // ---- conversions -----------------------------------------------------------------------
 // src/common/bf16.h:8-16
 float orc_bf16_to_f32(uint16_t h) { return bitsf(uint32_t(h) << 16); }

@@ -49,7 +49,7 @@ def gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, pages=None, page=0):
     shp = C.byref(sh)
     mi.call("mi_attn_decode", ptr(ctrl), ptr(dq), kind, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD,
             1, Lm, ptr(dpg), page, Lm, ptr(part), M, tgt, shp, stream())
-    mi.call("mi_attn_reduce", ptr(ctrl), ptr(part), None, ptr(out), M, tgt, shp, stream())
+    mi.call("mi_attn_reduce", ptr(ctrl), ptr(part), None, ptr(out), M, tgt, Lm, shp, stream())
     sync()
     return host(out, np.uint16), host(part, np.float32)
 
@@ -134,8 +134,9 @@ def test_rows_are_bitwise_their_single_row_steps():
 
 
 def test_reduce_matches_oracle_merge_on_device_partials():
-    """attn_reduce_v2's merge (the reference's formula, ascending blocks) on the GPU's own
-    partials: within 1 fp16 ulp of the oracle's merge (exp differs by <= 1 ulp)."""
+    """attn_reduce_v2's merge on the GPU's own partials: within 1 fp16 ulp of the oracle's
+    sequential merge (the device forms the same sum with a common max; exp differs by <= 1
+    ulp)."""
     QH, KVH, HD, Lm, tgt = 40, 8, 128, 8192, 32
     sh = O.attn_shape(QH, KVH, HD)
     k, v, ks, vs = make_kv(0, KVH, Lm, HD, 5)

@@ -64,7 +64,7 @@ class OracleModel:
         self.m = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
                               C.cast(layers, C.c_void_p), embed.ctypes.data, fnorm.ctypes.data,
                               O.Linear(lmq.ctypes.data, lms.ctypes.data, H, d.vocab, S[4]),
-                              self.rope.ctypes.data, d.attn_tgt, H // 256)
+                              self.rope.ctypes.data, d.attn_tgt, H // 64)
 
     def _h(self, a):
         a = np.ascontiguousarray(a)

@@ -1,0 +1,139 @@
+"""The GEMV's fused epilogues (last work-group per 64-column tile) and the fused
+embed + first norm, against the separate-kernel chain they replace, bit for bit on the
+same partials: prep_res_fold at 64-element chunks + prep_norm_finish, prep_silu_mul,
+the lm_head fold + argmax (tests/kernels/prep_test.cc, argmax_test.cc's bars)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mipkg import dev, empty, host, mi, ptr, stream, sync
+
+pytestmark = pytest.mark.gpu
+F16 = O.ORC_F16
+L = O.lib
+
+
+def rand_w(K, N, seed):
+    rng = np.random.default_rng(seed)
+    qw = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
+    sc = O.f32_to_f16_bits(rng.uniform(0.002, 0.02, size=(K // 64, N)).astype(np.float32))
+    return qw, sc
+
+
+def partials_of(dq, ds, dx, M, K, N, S):
+    part = empty((S, M, N), np.float32)
+    mi.call("mi_gemv_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(part), M, K, N, S, stream())
+    sync()
+    return host(part, np.float32).copy()
+
+
+@pytest.mark.parametrize("M,S", [(1, 8), (3, 4), (16, 1)])
+def test_resid_epilogue_bitwise(M, S):
+    K, N = 2048, 1024  # N = hidden
+    qw, sc = rand_w(K, N, 10 + M)
+    rng = np.random.default_rng(M)
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    resid = O.f32_to_f16_bits(rng.standard_normal((M, N)).astype(np.float32))
+    w = (1 + 0.02 * rng.standard_normal(N)).astype(np.float32)
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    part = partials_of(dq, ds, dx, M, K, N, S)
+    print(f"resid epilogue M={M} S={S}", flush=True)
+    G = N // 64
+    ctr = dev(np.zeros(G + 1, np.uint32))
+    dr, dw = dev(resid), dev(w)
+    dss = empty((G, M), np.float32)
+    drs = empty((M,), np.float32)
+    dxn = empty((M, N), np.uint16)
+    dpart = empty((S, M, N), np.float32)
+    ep = mi.GemvEpilogue(mi.EPI_RESID, ptr(ctr), ptr(dr), ptr(dss), ptr(drs), ptr(dw), ptr(dxn), 1e-6,
+                         None, None, None, 0)
+    for rep in range(2):  # a replay must find the counters reset
+        if rep:
+            dr.copy_(dev(resid))
+        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        sync()
+        assert not host(ctr, np.uint32).any()
+        r_ref = resid.copy()
+        s_ref = np.zeros((G, M), np.float32)
+        x_ref = np.zeros((M, N), np.uint16)
+        L().orc_res_fold(F16, O._p(part), O._p(r_ref), O._p(s_ref), M, N, S, G)
+        L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, N, G, 1e-6)
+        assert np.array_equal(host(dr, np.uint16), r_ref)
+        assert np.array_equal(host(dss, np.uint32), s_ref.view(np.uint32))
+        assert np.array_equal(host(dxn, np.uint16), x_ref)
+
+
+@pytest.mark.parametrize("M,S", [(1, 4), (4, 2)])
+def test_silu_epilogue(M, S):
+    K, I = 1024, 1536
+    N = 2 * I
+    qw, sc = rand_w(K, N, 20 + M)
+    x = O.f32_to_f16_bits(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    part = partials_of(dq, ds, dx, M, K, N, S)
+    ctr = dev(np.zeros(N // 64 + 1, np.uint32))
+    dh = empty((M, I), np.uint16)
+    dpart = empty((S, M, N), np.float32)
+    ep = mi.GemvEpilogue(mi.EPI_SILU, ptr(ctr), None, None, None, None, None, 0.0, ptr(dh), None, None, 0)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    sync()
+    assert not host(ctr, np.uint32).any()
+    got = host(dh, np.uint16)
+    want = O.silu_mul(F16, part, M, I, S)
+    a = O.f16_bits_to_f32(got).astype(np.float64)
+    b = O.f16_bits_to_f32(want).astype(np.float64)
+    assert np.all(np.abs(a - b) <= 2 * np.maximum(np.abs(b), 2.0 ** -14) * 2.0 ** -10)
+    assert np.mean(got == want) >= 0.95
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_logits_epilogue_and_argmax(M):
+    K, V, used = 1024, 8192, 8000
+    qw, sc = rand_w(K, V, 30 + M)
+    x = O.f32_to_f16_bits(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    S = 4
+    part = partials_of(dq, ds, dx, M, K, V, S)
+    ctr = dev(np.zeros(V // 64 + 1, np.uint32))
+    dl = empty((M, V), np.float32)
+    dap = empty((M * (V // 64) * 2,), np.uint32)
+    dpart = empty((S, M, V), np.float32)
+    ep = mi.GemvEpilogue(mi.EPI_LOGITS, ptr(ctr), None, None, None, None, None, 0.0, None, ptr(dl), ptr(dap), used)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, V, S, C.byref(ep), stream())
+    c = np.zeros(64, np.uint32)
+    c[1] = M
+    ctrl = dev(c)
+    mi.call("mi_argmax_finish", ptr(ctrl), ptr(dap), V // 64, None, 0, stream())
+    sync()
+    want = np.zeros((M, V), np.float32)
+    for s in range(S):
+        want = want + part[s]  # ascending s from 0.f
+    got = host(dl, np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    cc = host(ctrl, np.uint32)
+    assert list(cc[10:10 + M]) == [O.argmax(want[m], used) for m in range(M)]
+
+
+def test_embed_norm_bitwise():
+    V, H, M = 512, 5120, 2
+    rng = np.random.default_rng(4)
+    emb = O.f32_to_f16_bits(rng.standard_normal((V, H)).astype(np.float32))
+    w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    c = np.zeros(64, np.uint32)
+    c[1], c[2], c[3] = M, 17, 300
+    ctrl, demb, dw = dev(c), dev(emb), dev(w)
+    dr = empty((M, H), np.uint16)
+    dx = empty((M, H), np.uint16)
+    drs = empty((M,), np.float32)
+    mi.call("mi_embed_norm", ptr(ctrl), ptr(demb), ptr(dr), ptr(dw), ptr(dx), ptr(drs), M, H, V, 1e-6, stream())
+    sync()
+    r_ref = emb[[17, 300]].copy()
+    G = H // 64
+    s_ref = np.zeros((G, M), np.float32)
+    x_ref = np.zeros((M, H), np.uint16)
+    L().orc_res_fold(F16, None, O._p(r_ref), O._p(s_ref), M, H, 0, G)
+    L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, H, G, 1e-6)
+    assert np.array_equal(host(dr, np.uint16), r_ref)
+    assert np.array_equal(host(dx, np.uint16), x_ref)
