@@ -10,7 +10,7 @@ import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-LIB_PATH = os.path.join(HERE, "libmi355x_decode.so")
+LIB_PATH = os.environ.get("MI355X_DECODE_LIB") or os.path.join(HERE, "libmi355x_decode.so")
 HEADER = os.path.join(ROOT, "include", "mi355x_decode.h")
 
 _lib = None

@@ -274,14 +274,26 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
   const uint16_t* src = embed + (size_t)row * hidden;
   uint16_t* dst = resid + (size_t)m * hidden;
   const uint32_t nch = hidden / 64;
-  for (uint32_t c = wave; c < nch; c += 4) {
-    const uint16_t v16 = src[c * 64 + lane];
-    dst[c * 64 + lane] = v16;
-    const float v = h2f(v16);
-    float a = __builtin_fmaf(v, v, 0.f);
+  // wave w takes chunks w, w + 4, ...; the loads of up to 8 chunks go out together
+  for (uint32_t c0 = wave; c0 < nch; c0 += 32) {
+    uint16_t v16[8];
 #pragma unroll
-    for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
-    if (lane == 0) chunk[c] = a;
+    for (uint32_t u = 0; u < 8; ++u) {
+      const uint32_t c = c0 + 4 * u;
+      v16[u] = c < nch ? src[c * 64 + lane] : (uint16_t)0;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+      const uint32_t c = c0 + 4 * u;
+      if (c < nch) {
+        dst[c * 64 + lane] = v16[u];
+        const float v = h2f(v16[u]);
+        float a = __builtin_fmaf(v, v, 0.f);
+#pragma unroll
+        for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
+        if (lane == 0) chunk[c] = a;
+      }
+    }
   }
   __syncthreads();
   __shared__ float s_rstd;
@@ -293,7 +305,16 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
   }
   __syncthreads();
   const float r = s_rstd;
-  for (uint32_t k = t; k < hidden; k += kWG) x_out[(size_t)m * hidden + k] = f2h(h2f(src[k]) * r * norm_w[k]);
+  for (uint32_t k0 = t; k0 < hidden; k0 += 8 * kWG) {
+    uint16_t v16[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) v16[u] = k0 + u * kWG < hidden ? src[k0 + u * kWG] : (uint16_t)0;
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+      const uint32_t k = k0 + u * kWG;
+      if (k < hidden) x_out[(size_t)m * hidden + k] = f2h(h2f(v16[u]) * r * norm_w[k]);
+    }
+  }
 }
 
 // The comparator (argmax.cl:63-65): strictly greater wins, an exact tie keeps the lower index.
