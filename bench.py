@@ -188,7 +188,9 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline and parity step")
     ap.add_argument("--eager", action="store_true",
-                    help="enqueue each step kernel by kernel instead of replaying the captured graph")
+                    help="enqueue each step kernel by kernel instead of replaying the captured graph "
+                         "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
+                         "the stream-read probe run, which is the command the kernel profiles use")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
@@ -200,14 +202,15 @@ def main():
     log(f"bench: building 27B-shape engine (max_len {max_len}) ...")
     t0 = time.time()
     eng = mi.Engine(desc, seed=args.seed)
-    eng.capture(1)
+    if not args.eager:
+        eng.capture(1)
     log(f"bench: engine ready in {time.time() - t0:.1f} s; S per linear {[eng.linear_s(w) for w in range(5)]}")
     st = eng.stream
     tok0 = 1000
 
     parity = None
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.eager:
         log("bench: CPU oracle step (one full 64-layer step on the host) ...")
         eng.reset(args.context, tok0)
         dt, cpu_logits, cpu_am, threads = cpu_oracle_step(eng, tok0, args.context)
@@ -230,23 +233,25 @@ def main():
 
     eng.reset(args.context, tok0)
     step = eng.step_eager if args.eager else eng.replay
-    for _ in range(max(1, args.warmup)):
-        step(1)
-    mi.check(mi.lib().mi_device_sync())
-    ev = Events(st)
-    tw = time.perf_counter()
-    ev.start()
-    for _ in range(args.steps):
-        step(1)
-    ms = ev.stop_ms()
-    mi.check(mi.lib().mi_device_sync())
-    wall = time.perf_counter() - tw
-    ms_per_step = ms / args.steps
-    c = eng.ctrl()
-    assert c[mi.CTRL_POS] == args.context + args.warmup + args.steps, c[:20]
-    assert c[mi.CTRL_DEBUG] == 0, hex(c[mi.CTRL_DEBUG])
-    tok_s = 1000.0 / ms_per_step
-    log(f"bench: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms wall -> {tok_s:.1f} tok/s")
+    ms_per_step = tok_s = None
+    if args.steps > 0:
+        for _ in range(args.warmup):
+            step(1)
+        mi.check(mi.lib().mi_device_sync())
+        ev = Events(st)
+        tw = time.perf_counter()
+        ev.start()
+        for _ in range(args.steps):
+            step(1)
+        ms = ev.stop_ms()
+        mi.check(mi.lib().mi_device_sync())
+        wall = time.perf_counter() - tw
+        ms_per_step = ms / args.steps
+        c = eng.ctrl()
+        assert c[mi.CTRL_POS] == args.context + args.warmup + args.steps, c[:20]
+        assert c[mi.CTRL_DEBUG] == 0, hex(c[mi.CTRL_DEBUG])
+        tok_s = 1000.0 / ms_per_step
+        log(f"bench: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms wall -> {tok_s:.1f} tok/s")
 
     roof, alg_gemv = gemv_roofline(eng)
     stream_gbs = stream_read_rate(st)
@@ -258,12 +263,12 @@ def main():
 
     out = {
         "metric": "batch-1 decode tokens/s (27B-shape W4A16); int4 GEMV HBM GB/s vs peak",
-        "value": round(tok_s, 2),
+        "value": None if tok_s is None else round(tok_s, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": None if ms_per_step is None else round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -275,7 +280,7 @@ def main():
                    "kv_heads": desc.kv_heads, "head_dim": desc.head_dim, "intermediate": desc.inter,
                    "vocab": desc.vocab, "context": args.context, "rope_theta": 1e6},
         "step_alg_bytes": step_alg,
-        "step_hbm_gbs": round(step_alg / (ms_per_step * 1e-3) / 1e9, 1),
+        "step_hbm_gbs": None if ms_per_step is None else round(step_alg / (ms_per_step * 1e-3) / 1e9, 1),
         "roofline": roof,
         "cpu_baseline": cpu,
         "parity": parity,

@@ -117,6 +117,9 @@ int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint
 /* The split-K width this library uses for a shape (the role of kQwen38Tuning,
  * src/model/model_desc.cc:32, and kSmallMTuning, src/kernels/kernels.h:140-170). */
 uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N);
+/* The split-K width for a launch with epilogue kind `epilogue` (MI_EPI_*): the plain
+ * choice for MI_EPI_PARTIALS, at most 8 for the fused epilogues (same role as above). */
+uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue);
 /* out = sum_s partials[s] (ascending from 0.f), as fp16 and/or fp32 (the host fold of
  * tests/kernels/gemv_harness.h:59-120, on the device) */
 int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,

@@ -39,6 +39,7 @@ SIGNATURES = {
     "mi_int4_dequant": (i32, [vp, vp, vp, u32, u32, vp]),
     "mi_gemv_w4a16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_gemv_pick_s": (u32, [u32, u32]),
+    "mi_gemv_pick_s_ex": (u32, [u32, u32, u32]),
     "mi_fold_partials": (i32, [vp, vp, vp, u32, u32, u32, vp]),
     "mi_stream_read": (i32, [vp, sz, vp, vp]),
     "mi_res_fold": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),

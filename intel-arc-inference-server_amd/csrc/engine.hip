@@ -115,10 +115,11 @@ struct mi_engine {
     return 0;
   }
 
-  int alloc_linear(Linear& l, uint32_t K, uint32_t N) {
+  // epi: the epilogue the step runs this linear with (its split-K width depends on it)
+  int alloc_linear(Linear& l, uint32_t K, uint32_t N, uint32_t epi) {
     l.K = K;
     l.N = N;
-    l.S = mi_gemv_pick_s(K, N);
+    l.S = mi_gemv_pick_s_ex(K, N, epi);
     MI_TRY(alloc(&l.q, size_t(K / 8) * N));
     MI_TRY(alloc(&l.s, size_t(K / 64) * N));
     return 0;
@@ -142,10 +143,10 @@ struct mi_engine {
     layer.resize(m.layers);
     size_t part_max = 0;
     for (Layer& L : layer) {
-      MI_TRY(alloc_linear(L.qkv, H, qkv_n));
-      MI_TRY(alloc_linear(L.o, QH * HD, H));
-      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter));
-      MI_TRY(alloc_linear(L.down, m.inter, H));
+      MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_PARTIALS));
+      MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
+      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
+      MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
       MI_TRY(alloc(&L.in_norm, H));
       MI_TRY(alloc(&L.post_norm, H));
       if (m.qk_norm) {
@@ -155,7 +156,7 @@ struct mi_engine {
       for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
         part_max = std::max(part_max, size_t(l->S) * R * l->N);
     }
-    MI_TRY(alloc_linear(lm_head, H, m.vocab));
+    MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
     part_max = std::max(part_max, size_t(lm_head.S) * R * m.vocab);
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
     MI_TRY(alloc(&final_norm, H));

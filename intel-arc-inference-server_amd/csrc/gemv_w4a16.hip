@@ -249,14 +249,22 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     // the launch's last tile: rstd per row and the next norm's input
     if (!last_arrival(epi.counters + ntiles, ntiles, &s_flag)) return;
     // the tiles' sums, loaded in parallel, then added in ascending tile order
-    __shared__ float s_ss[1024];
+    __shared__ __align__(16) float s_ss[1024];
     __shared__ float s_rstd[16];
     for (uint32_t row = 0; row < M; ++row) {
       for (uint32_t g = t; g < ntiles; g += 256u) s_ss[g] = ld_agent(epi.sumsq + (size_t)g * M + row);
       __syncthreads();
       if (t == 0) {
         float tot = 0.f;
-        for (uint32_t g = 0; g < ntiles; ++g) tot += s_ss[g];
+        uint32_t g = 0;
+        for (; g + 16u <= ntiles; g += 16u) {
+          f4_t v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f4_t*>(s_ss + g + 4u * u);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) tot = ((tot + v[u][0]) + v[u][1] + v[u][2]) + v[u][3];
+        }
+        for (; g < ntiles; ++g) tot += s_ss[g];
         const float r = 1.0f / sqrtf(tot / (float)N + epi.eps);
         s_rstd[row] = r;
         epi.rstd[row] = r;
@@ -267,15 +275,25 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       const float r = s_rstd[row];
       const uint16_t* rr = epi.resid + (size_t)row * N;
       uint16_t* xo = epi.x_next + (size_t)row * N;
-      uint32_t n = t;
-      for (; n + 3u * 256u < N; n += 4u * 256u) {
-        uint16_t v[4];
+      const uint32_t nq = N / 4u;
+      const uint64_t* rq = reinterpret_cast<const uint64_t*>(rr);
+      for (uint32_t q0 = t; q0 < nq; q0 += 8u * 256u) {
+        uint64_t v[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = ld_agent(rr + n + u * 256u);
+        for (uint32_t u = 0; u < 8; ++u) v[u] = ld_agent(rq + min(q0 + u * 256u, nq - 1u));
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xo[n + u * 256u] = f2h(h2f(v[u]) * r * epi.next_w[n + u * 256u]);
+        for (uint32_t u = 0; u < 8; ++u) {
+          const uint32_t q = q0 + u * 256u;
+          if (q < nq) {
+            const f4_t wv = *reinterpret_cast<const f4_t*>(epi.next_w + 4u * q);
+            uint64_t o = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              o |= (uint64_t)f2h(h2f((uint16_t)(v[u] >> (16 * j))) * r * wv[j]) << (16 * j);
+            reinterpret_cast<uint64_t*>(xo)[q] = o;
+          }
+        }
       }
-      for (; n < N; n += 256u) xo[n] = f2h(h2f(ld_agent(rr + n)) * r * epi.next_w[n]);
     }
   } else if constexpr (EPI == EPI_SILU) {
     // 64 interleave16 columns = 32 outputs k = 32 tile + i (gate at gflat, up at gflat + 16)
@@ -362,17 +380,31 @@ int check_gemv(const uint32_t* qweight, const uint16_t* scales, const uint16_t* 
 using namespace mi;
 
 extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
-  // The split-K width for a shape: enough waves to keep every CU's load queues full
-  // (about 2048 or more), at least 2 k-groups per wave where the shape allows; S | K/64.
+  // The split-K width for a plain launch (measured on MI355X over the 27B shapes at M = 1):
+  // the smallest S | K/64 that gives at most 8 k-groups per split and at least 2048
+  // work-groups, never going below 4 k-groups per split.
   const uint32_t G = K / 64, tiles = N / kCols;
   uint32_t best = 1;
   for (uint32_t S = 1; S <= G; ++S) {
     if (G % S) continue;
-    const uint32_t gpw = (G / S + kWaves - 1) / kWaves;
-    if (gpw < 2 && S > 1) break;
+    const uint32_t gps = G / S;
+    if (gps < 4 && S > 1) break;
     best = S;
-    if (tiles * S * kWaves >= 2048 && gpw <= 8) break;
+    if (gps <= 8 && tiles * S >= 2048) break;
   }
+  return best;
+}
+
+extern "C" uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue) {
+  // A fused epilogue's last work-group per tile folds S partials with device-coherent
+  // loads, so larger S lengthens the launch's serial tail; the fused launches keep S at the
+  // largest divisor of K/64 no larger than 8 (and no larger than the plain choice).
+  const uint32_t plain = mi_gemv_pick_s(K, N);
+  if (epilogue == MI_EPI_PARTIALS) return plain;
+  const uint32_t G = K / 64, cap = plain < 8u ? plain : 8u;
+  uint32_t best = 1;
+  for (uint32_t S = 1; S <= cap; ++S)
+    if (G % S == 0) best = S;
   return best;
 }
 

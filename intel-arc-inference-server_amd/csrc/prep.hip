@@ -189,9 +189,20 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   const float* nw = is_q ? a.q_norm : a.k_norm;
   const size_t base = is_q ? (a.gated ? (size_t)h * 2 * HD : (size_t)h * HD)
                            : (size_t)a.k_off + (size_t)h * HD;
+  // sum_s partials in ascending s from 0.f; the loads go out 8 at a time (past S they reload
+  // the last partial and add +0.f, which leaves the sum's bits unchanged: it starts at +0.f
+  // and a round-to-nearest sum of nonzero terms is never -0)
   auto qkv_sum = [&](size_t col) {
+    const float* p = a.partials + (size_t)m * a.qkv_n + col;
+    const size_t step = (size_t)a.M * a.qkv_n;
     float v = 0.0f;
-    for (uint32_t s = 0; s < a.S; ++s) v += a.partials[((size_t)s * a.M + m) * a.qkv_n + col];
+    for (uint32_t s = 0; s < a.S; s += 8u) {
+      float t8[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) t8[u] = p[min(s + u, a.S - 1u) * step];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) v += s + u < a.S ? t8[u] : 0.f;
+    }
     return v;
   };
   const float xf = h2f(f2h(qkv_sum(base + i)));
