@@ -117,6 +117,22 @@ def gemv_roofline(eng, reps=3):
     }, alg
 
 
+def profiled_traffic(eng):
+    """HBM bytes per GEMV launch of the sweep from the committed PMC summary (FETCH_SIZE and
+    WRITE_SIZE runs of `bench.py --eager --steps 0`, each scaled by a kernel of known size),
+    provided it was measured at the split-K widths this engine uses; else None."""
+    path = os.path.join(ROOT, "profiles", "gemv_w4a16_27b_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        prof = json.load(f)
+    mine = dict(zip(["qkv", "o", "gate_up", "down", "lm_head"], [eng.linear_s(w) for w in range(5)]))
+    if prof.get("split_k") != mine:
+        log(f"bench: profiled traffic was measured at S {prof.get('split_k')}, engine uses {mine}: not reported")
+        return None
+    return prof["traffic_bytes_per_launch"]
+
+
 def stream_read_rate(st):
     L = mi.lib()
     nbytes = 2 << 30
@@ -257,6 +273,7 @@ def main():
     stream_gbs = stream_read_rate(st)
     kv_bytes = 2 * desc.layers * desc.kv_heads * (args.context + 1) * desc.head_dim * 2
     step_alg = alg_gemv + kv_bytes
+    roof["traffic"] = profiled_traffic(eng)
     roof["stream_read_gbs"] = round(stream_gbs, 1)
     roof["frac_of_stream"] = round(roof["achieved"] / stream_gbs, 4)
     log(f"bench: gemv roofline {roof}")

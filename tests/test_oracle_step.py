@@ -1,0 +1,169 @@
+"""Pins the oracle's whole dense decode step (orc_dense_step: the layer walk of
+src/runtime/capture.cc:997, 1247-1263, 1370-1423, 1461-1480) against an independent fp64
+forward of the same model written here from the model's definition: RMSNorm, q/k-norm,
+half-split RoPE, GQA softmax attention over positions 0..pos, interleave16 SwiGLU
+(src/common/repack.h:64-73), two residual adds per layer, final norm, int4 lm_head.
+
+The per-kernel pieces are pinned bit-exactly elsewhere; this test catches wiring mistakes
+that those cannot see (a transposed operand, a wrong residual, a mis-indexed KV row or head
+group). Bar: fp16 activations round at every kernel boundary, so the oracle's logits sit
+within 5e-3 of the largest fp64 logit (measured: 1e-3) and correlate > 0.9999; the argmax agrees unless the
+fp64 top two are closer than that."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+F16 = O.ORC_F16
+
+
+def f16(a):
+    return O.f32_to_f16_bits(np.asarray(a, np.float32))
+
+
+class TinyModel:
+    def __init__(self, seed, layers=2, H=256, QH=4, KVH=2, HD=64, rot=64, I=256, V=512, L=64,
+                 qk_norm=True, theta=1e4):
+        rng = np.random.default_rng(seed)
+        self.d = dict(layers=layers, H=H, QH=QH, KVH=KVH, HD=HD, rot=rot, I=I, V=V, L=L, qk_norm=qk_norm)
+        self.keep = []
+        self.lin = []
+        dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
+        S = [2, 2, 2, 2]
+        layers_c = (O.Layer * layers)()
+        self.w = []
+        for li in range(layers):
+            ws = {}
+            lins = []
+            for (K, N), s in zip(dims, S):
+                q = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
+                sc = f16(rng.uniform(0.004, 0.03, (K // 64, N)))
+                self.keep += [q, sc]
+                lins.append(O.Linear(q.ctypes.data, sc.ctypes.data, K, N, s))
+                ws[len(ws)] = O.int4_dequant(q, sc, K, N).astype(np.float64)
+            Ly = layers_c[li]
+            Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+            norms = {}
+            for name, n in (("in_norm", H), ("post_norm", H), ("q_norm", HD), ("k_norm", HD)):
+                a = (1.0 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+                self.keep.append(a)
+                norms[name] = a
+                if name in ("q_norm", "k_norm") and not qk_norm:
+                    continue
+                setattr(Ly, name, a.ctypes.data)
+            ws["norms"] = norms
+            self.w.append(ws)
+        self.embed = f16(rng.standard_normal((V, H)))
+        self.fnorm = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+        lq = rng.integers(0, 2**32, size=(H // 8, V), dtype=np.uint64).astype(np.uint32)
+        ls = f16(rng.uniform(0.004, 0.03, (H // 64, V)))
+        self.lm = O.int4_dequant(lq, ls, H, V).astype(np.float64)
+        self.rope = O.rope_table(theta, rot, L)
+        self.keep += [self.embed, self.fnorm, lq, ls, self.rope, layers_c]
+        sh = O.attn_shape(QH, KVH, HD, rot_dim=rot)
+        self.m = O.DenseModel(layers, H, I, V, V, L, sh, 1e-6, C.cast(layers_c, C.c_void_p),
+                              self.embed.ctypes.data, self.fnorm.ctypes.data,
+                              O.Linear(lq.ctypes.data, ls.ctypes.data, H, V, 2), self.rope.ctypes.data, 4,
+                              H // 64)
+        self.kv_k = f16(rng.standard_normal((layers, KVH, L, HD)))
+        self.kv_v = f16(rng.standard_normal((layers, KVH, L, HD)))
+
+    def oracle_step(self, tok, pos):
+        kk, vv = self.kv_k.copy(), self.kv_v.copy()
+        logits = np.zeros(self.d["V"], np.float32)
+        am = O.lib().orc_dense_step(F16, C.byref(self.m), tok, pos, O._p(kk), O._p(vv), O._p(logits),
+                                    self.d["layers"])
+        return int(am), logits, kk, vv
+
+    def fp64_step(self, tok, pos, mistake=None):
+        d = self.d
+        H, QH, KVH, HD, rot, I = d["H"], d["QH"], d["KVH"], d["HD"], d["rot"], d["I"]
+        eps = 1e-6
+
+        def rms(v, w):
+            return v / np.sqrt(np.mean(v * v) + eps) * w
+
+        half = rot // 2
+        cos = self.rope[pos, 0].astype(np.float64)
+        sin = self.rope[pos, 1].astype(np.float64)
+
+        def rope(v):
+            out = v.copy()
+            a, b = v[:half], v[half:rot]
+            out[:half] = a * cos - b * sin if mistake != "rope_sign" else a * cos + b * sin
+            out[half:rot] = b * cos + a * sin
+            return out
+
+        resid = O.f16_bits_to_f32(self.embed[tok]).astype(np.float64)
+        kc = O.f16_bits_to_f32(self.kv_k).astype(np.float64)
+        vc = O.f16_bits_to_f32(self.kv_v).astype(np.float64)
+        G = QH // KVH
+        for li, ws in enumerate(self.w):
+            nm = ws["norms"]
+            x = rms(resid, nm["in_norm"])
+            qkv = x @ ws[0]
+            q = qkv[:QH * HD].reshape(QH, HD)
+            k = qkv[QH * HD:(QH + KVH) * HD].reshape(KVH, HD)
+            v = qkv[(QH + KVH) * HD:].reshape(KVH, HD)
+            if d["qk_norm"]:
+                q = np.stack([rms(h, nm["q_norm"]) for h in q])
+                k = np.stack([rms(h, nm["k_norm"]) for h in k])
+            q = np.stack([rope(h) for h in q])
+            k = np.stack([rope(h) for h in k])
+            kc[li, :, pos] = k
+            vc[li, :, pos] = v
+            att = np.empty((QH, HD))
+            for h in range(QH):
+                kvh = h // G if mistake != "gqa_map" else h % KVH
+                sc = kc[li, kvh, :pos + 1] @ q[h] / np.sqrt(HD)
+                p = np.exp(sc - sc.max())
+                att[h] = (p / p.sum()) @ vc[li, kvh, :pos + 1]
+            resid = resid + att.reshape(-1) @ ws[1] if mistake != "no_attn_resid" else att.reshape(-1) @ ws[1]
+            x = rms(resid, nm["post_norm"])
+            gu = x @ ws[2]
+            j = np.arange(I)
+            g = gu[(j // 16) * 32 + j % 16]
+            u = gu[(j // 16) * 32 + j % 16 + 16]
+            if mistake == "gate_up_swap":
+                g, u = u, g
+            h_ = g / (1.0 + np.exp(-g)) * u
+            resid = resid + h_ @ ws[3]
+        x = rms(resid, self.fnorm)
+        return x @ self.lm, kc, vc
+
+
+@pytest.mark.parametrize("seed,pos,qk_norm", [(1, 0, True), (2, 37, True), (3, 63, False)])
+def test_dense_step_vs_independent_fp64_forward(seed, pos, qk_norm):
+    m = TinyModel(seed, qk_norm=qk_norm)
+    tok = (seed * 97) % m.d["V"]
+    am, got, kk, vv = m.oracle_step(tok, pos)
+    want, kc, vc = m.fp64_step(tok, pos)
+    scale = np.abs(want).max()
+    err = np.abs(got.astype(np.float64) - want)
+    assert err.max() <= 5e-3 * scale, (err.max(), scale)
+    assert np.corrcoef(got, want)[0, 1] > 0.9999
+    top = np.sort(want)[::-1]
+    assert am == int(np.argmax(want)) or top[0] - want[am] <= 1e-2 * scale
+    # the step wrote this position's K and V rows (fp16 of the fp64 values, to the same bar),
+    # and nothing else
+    for li in range(m.d["layers"]):
+        gk = O.f16_bits_to_f32(kk[li, :, pos]).astype(np.float64)
+        assert np.abs(gk - kc[li, :, pos]).max() <= 2e-2 * np.abs(kc[li, :, pos]).max()
+        gv = O.f16_bits_to_f32(vv[li, :, pos]).astype(np.float64)
+        assert np.abs(gv - vc[li, :, pos]).max() <= 2e-2 * np.abs(vc[li, :, pos]).max()
+    mask = np.ones(m.d["L"], bool)
+    mask[pos] = False
+    assert np.array_equal(kk[:, :, mask], m.kv_k[:, :, mask])
+    assert np.array_equal(vv[:, :, mask], m.kv_v[:, :, mask])
+
+
+@pytest.mark.parametrize("mistake", ["rope_sign", "gqa_map", "gate_up_swap", "no_attn_resid"])
+def test_bar_rejects_plausible_wiring_mistakes(mistake):
+    """The comparison is not vacuous: the same fp64 forward with one plausible mistake
+    (RoPE sign, GQA head mapping, gate/up swapped, a dropped residual) misses the bar."""
+    m = TinyModel(2)
+    _, got, _, _ = m.oracle_step(194, 37)
+    want = m.fp64_step(194, 37, mistake=mistake)[0]
+    assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
