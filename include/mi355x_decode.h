@@ -209,6 +209,35 @@ int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history
               uint32_t history_len, uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
 
 
+/* ---- mixture of experts (src/kernels/moe.cl, src/kernels/gemv_bf16.cl) ----
+ * A MoE block is four launches, as the reference's list (moe.cl:1-13): the router || shared
+ * gate GEMV, routing, expert gate||up, expert down + combine + residual. Expert ids stay on
+ * the device in a route row of MI_MOE_ROUTE_WORDS u32 per token (moe.cl:49-56): [0..7] ids,
+ * [8..15] w_k and [16] the shared gate (fp32 bits of fp16 values), [17..24] p_k, [25] p of
+ * rank top_k. The shared expert is weight block `experts` and slot top_k. */
+#define MI_MOE_ROUTE_WORDS 32
+/* gemv_bf16 (gemv_bf16.cl:103-200) with fp16 weights: out [M][N] fp32 = x [M][K] . w, w in
+ * the tile layout [N/16][K/8][8][16] (common/repack.h:118); per column `ksplit` K slices
+ * (power of two <= 16) each summed in ascending k, merged by the pairwise tree. */
+int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* out, uint32_t M, uint32_t K,
+                 uint32_t N, uint32_t ksplit, void* stream);
+/* moe_route (moe.cl:192-262): logits [M][router_n] (experts router rows, then the shared
+ * gate's row) -> route [M][MI_MOE_ROUTE_WORDS]. experts: power of two in [16, 256]. */
+int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts,
+                 uint32_t top_k, uint32_t router_n, void* stream);
+/* moe_gate_up (moe.cl:335-381): h [M][top_k + 1][inter] fp16 = rne(silu(g)) * u of each slot's
+ * expert, gate||up in layout-1 int4 g64 blocks of (2 inter / 16) * (hidden / 64) * 136 u32
+ * per expert (experts + 1 blocks); K split in 4 slices merged pairwise (kernels.h:591). */
+int mi_moe_gate_up(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks,
+                   uint16_t* h, uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                   uint32_t inter, void* stream);
+/* moe_down (moe.cl:383-470): resid [M][hidden] += the slot-ordered combine of each slot's
+ * down projection (layout-1 blocks of (hidden / 16) * (inter / 64) * 136 u32 per expert, K
+ * split in 2 slices) weighted by w_k, plus the shared expert's times its gate. */
+int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks,
+                uint16_t* resid, uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                uint32_t inter, void* stream);
+
 /* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
  * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the
  * dense GQA decoder this build runs: every layer is attention + SwiGLU MLP, all linears

@@ -71,6 +71,10 @@ SIGNATURES = {
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
     "mi_accept_greedy": (u32, [vp, vp, u32, vp]),
+    "mi_gemv_f16w": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "mi_moe_route": (i32, [vp, vp, u32, u32, u32, u32, vp]),
+    "mi_moe_gate_up": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "mi_moe_down": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
 }
 
 

@@ -1,0 +1,323 @@
+// moe.hip - the mixture-of-experts block of a decode step: router || shared-gate GEMV,
+// top-k routing, expert gate||up and down over int4 g64 layout-1 expert blocks, and the
+// slot-ordered combine with the residual (src/kernels/moe.cl, src/kernels/gemv_bf16.cl;
+// host twins tests/kernels/moe_ref.h:62-177).
+//
+// Four launches per block, as the reference's list (moe.cl:1-13): ids are produced and
+// consumed on the device through the 32-word route row (moe.cl:49-56):
+//   [0..7] expert id of slot k, [8..15] w_k (fp32 bits of an fp16 value), [16] shared gate
+//   s (same), [17..24] p_k before renormalisation, [25] p of rank top_k.
+//
+// Arithmetic is the twins' order, so results are bitwise the oracle's where no exp is
+// involved: a k-group's dot is (sum over its 8 words of the word's 8 ascending products)
+// in word order; a K slice is `acc += gdot * scale` over its groups in ascending order; the
+// slices merge by the pairwise tree (moe_ref.h:98-132). On MI355X the per-group dots run on
+// separate lanes (each is independent) and one lane per (column, slice) then adds them in
+// order from LDS: the same operations in the same order, spread over 256 lanes so the
+// expert weights stream at HBM rate instead of one lane per column walking K.
+#include "mi_common.h"
+#include "mi_capi_internal.h"
+
+namespace mi {
+namespace {
+
+constexpr uint32_t kRouteWords = 32, R_IDS = 0, R_W = 8, R_SG = 16, R_P = 17, R_P9 = 25;
+constexpr uint32_t kUpKs = 4, kDnKs = 2;  // the reference's in-work-group K splits (kernels.h:591)
+constexpr uint32_t kTileU32 = 136;        // layout 1: 128 words of nibbles + 16 f16 scales
+constexpr uint32_t kMaxHidden = 4096, kMaxSlotsInter = 9 * 1024, kMaxGroups = kMaxHidden / 64;
+
+__device__ __forceinline__ float rf(float v) { return h2f(f2h(v)); }
+
+// ---- router || shared-gate GEMV (gemv_bf16.cl:103-200), fp16 weights --------------------
+// grid (N/16, M), 16 * ksplit lanes: lane l of slice q sums column n_tile*16 + l over k8 in
+// [q*per, (q+1)*per), 8 products per k8 in k order; slices merge by the pairwise tree.
+__global__ __launch_bounds__(256) void gemv_f16w_kernel(const uint16_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ x,
+                                                        float* __restrict__ out, uint32_t K,
+                                                        uint32_t N, uint32_t ksplit) {
+  __shared__ float red[16][16];
+  const uint32_t lane = threadIdx.x & 15u, q = threadIdx.x >> 4;
+  const uint32_t nt = blockIdx.x, m = blockIdx.y;
+  const uint32_t K8 = K / 8, per = K8 / ksplit;
+  const uint16_t* tile = w + (size_t)nt * K8 * 128 + (size_t)q * per * 128 + lane;
+  const uint16_t* xr = x + (size_t)m * K + (size_t)q * per * 8;
+  float acc = 0.f;
+  uint32_t k8 = 0;
+  for (; k8 + 4 <= per; k8 += 4) {
+    uint16_t wv[4][8];
+    u4_t xv[4];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+#pragma unroll
+      for (uint32_t j = 0; j < 8; ++j) wv[u][j] = tile[(size_t)(k8 + u) * 128 + j * 16];
+      xv[u] = *reinterpret_cast<const u4_t*>(xr + (k8 + u) * 8);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+      for (uint32_t j = 0; j < 8; ++j)
+        acc += h2f(wv[u][j]) * h2f((uint16_t)(xw[j / 2] >> (16 * (j % 2))));
+    }
+  }
+  for (; k8 < per; ++k8)
+    for (uint32_t j = 0; j < 8; ++j) acc += h2f(tile[(size_t)k8 * 128 + j * 16]) * h2f(xr[k8 * 8 + j]);
+  red[q][lane] = acc;
+  __syncthreads();
+  for (uint32_t stride = ksplit / 2; stride > 0; stride >>= 1) {
+    if (q < stride) red[q][lane] += red[q + stride][lane];
+    __syncthreads();
+  }
+  if (q == 0) out[(size_t)m * N + nt * 16 + lane] = red[0][lane];
+}
+
+// ---- routing (moe.cl:192-262; twin moe_ref.h:62-96) ----------------------------------------
+// one work-group of E lanes per row: l = rne(logit); p = exp(l - max) / (pairwise sum);
+// rank = #{j : p_j > p_e or (p_j == p_e and j < e)}; slots 0..top_k-1 take ranks 0..top_k-1;
+// w_k = rne(p_k / sum of the top_k p in rank order); s = rne(sigmoid(rne(logit_E))).
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits,
+                                                        uint32_t* __restrict__ route, uint32_t E,
+                                                        uint32_t top_k, uint32_t router_n) {
+  __shared__ float s_l[256], s_red[256], s_p[256], s_top_p[9];
+  __shared__ uint32_t s_top_id[9];
+  const uint32_t e = threadIdx.x, m = blockIdx.x;
+  const float* lg = logits + (size_t)m * router_n;
+  const float l = rf(lg[e]);
+  s_l[e] = l;
+  __syncthreads();
+  // max: exact whatever the order
+  s_red[e] = l;
+  __syncthreads();
+  for (uint32_t st = E / 2; st > 0; st >>= 1) {
+    if (e < st) s_red[e] = fmaxf(s_red[e], s_red[e + st]);
+    __syncthreads();
+  }
+  const float mx = s_red[0];
+  __syncthreads();
+  const float ex = expf(l - mx);
+  s_red[e] = ex;
+  __syncthreads();
+  for (uint32_t st = E / 2; st > 0; st >>= 1) {
+    if (e < st) s_red[e] += s_red[e + st];
+    __syncthreads();
+  }
+  const float p = ex / s_red[0];
+  s_p[e] = p;
+  __syncthreads();
+  uint32_t rank = 0;
+  for (uint32_t j = 0; j < E; ++j) {
+    const float pj = s_p[j];
+    rank += (pj > p || (pj == p && j < e)) ? 1u : 0u;
+  }
+  const uint32_t slots = top_k + 1;
+  if (e < slots) {  // defaults the twin starts from (top_id[k] = k, top_p[k] = 0)
+    s_top_id[e] = e;
+    s_top_p[e] = 0.f;
+  }
+  __syncthreads();
+  if (rank < slots) {
+    s_top_id[rank] = e;
+    s_top_p[rank] = p;
+  }
+  __syncthreads();
+  uint32_t* row = route + (size_t)m * kRouteWords;
+  if (e == 0) {
+    float s8 = 0.f;
+    for (uint32_t k = 0; k < top_k; ++k) s8 += s_top_p[k];
+    for (uint32_t k = 0; k < 8; ++k) {
+      const bool on = k < top_k;
+      row[R_IDS + k] = on ? s_top_id[k] : 0u;
+      row[R_W + k] = on ? __builtin_bit_cast(uint32_t, rf(s_top_p[k] / s8)) : 0u;
+      row[R_P + k] = on ? __builtin_bit_cast(uint32_t, s_top_p[k]) : 0u;
+    }
+    row[R_P9] = __builtin_bit_cast(uint32_t, s_top_p[top_k]);
+    row[R_SG] = __builtin_bit_cast(uint32_t, rf(sigmoid_f32(rf(lg[E]))));
+    for (uint32_t k = R_P9 + 1; k < kRouteWords; ++k) row[k] = 0u;
+  }
+}
+
+// expert block of slot `slot` (the shared expert is block E, slot top_k); an out-of-range id
+// in a malformed route row reads the shared block rather than past the weights
+__device__ __forceinline__ uint32_t slot_expert(const uint32_t* row, uint32_t slot, uint32_t E,
+                                                uint32_t top_k) {
+  if (slot >= top_k) return E;
+  const uint32_t id = row[R_IDS + slot];
+  return id < E ? id : E;
+}
+
+// one k-group's dot for column c of a layout-1 tile (moe_ref.h:98-116's tile_dot body):
+// sum over words j of (sum over nibbles i of (q - 8) * x) in ascending order, then * scale
+__device__ __forceinline__ float group_term(const uint32_t* __restrict__ tile, uint32_t c,
+                                            const float* __restrict__ xs) {
+  uint32_t wd[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wd[j] = tile[j * 16 + c];
+  const uint16_t sc = reinterpret_cast<const uint16_t*>(tile + 128)[c];
+  float g = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a += (float)((int)((wd[j] >> (4 * i)) & 0xFu) - 8) * xs[j * 8 + i];
+    g += a;
+  }
+  return g * h2f(sc);
+}
+
+// ---- gate||up + SiLU (moe.cl:335-381; twin moe_ref.h:154-168) ------------------------------
+// grid (slots * inter/16, M): work-group (slot, ib) makes h[m][slot][16 ib .. 16 ib + 15] from
+// the expert's gate tile 2 ib and up tile 2 ib + 1 (interleave16 columns).
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(const uint32_t* __restrict__ route,
+                                                          const uint16_t* __restrict__ x,
+                                                          const uint32_t* __restrict__ gu,
+                                                          uint16_t* __restrict__ h, uint32_t E,
+                                                          uint32_t top_k, uint32_t hidden,
+                                                          uint32_t inter) {
+  __shared__ float s_x[kMaxHidden];
+  __shared__ float s_t[2][16][kMaxGroups];
+  __shared__ float s_r[2][16][kUpKs];
+  const uint32_t t = threadIdx.x, m = blockIdx.y;
+  const uint32_t nib = inter / 16, slot = blockIdx.x / nib, ib = blockIdx.x % nib;
+  const uint32_t G = hidden / 64, slots = top_k + 1;
+  const uint32_t e = slot_expert(route + (size_t)m * kRouteWords, slot, E, top_k);
+  for (uint32_t k = t; k < hidden; k += 256u) s_x[k] = h2f(x[(size_t)m * hidden + k]);
+  __syncthreads();
+  const size_t block = (size_t)(2 * inter / 16) * G * kTileU32;
+  const uint32_t c = t & 15u, gsub = (t >> 4) & 7u, tl = t >> 7;
+  const uint32_t* tiles = gu + (size_t)e * block + (size_t)(2 * ib + tl) * G * kTileU32;
+  for (uint32_t g = gsub; g < G; g += 8u) s_t[tl][c][g] = group_term(tiles + (size_t)g * kTileU32, c, s_x + g * 64);
+  __syncthreads();
+  if (t < 2u * 16u * kUpKs) {  // (tile, column, slice): the slice's groups in order
+    const uint32_t tl2 = t / (16u * kUpKs), c2 = (t / kUpKs) % 16u, q = t % kUpKs;
+    const uint32_t per = G / kUpKs;
+    float acc = 0.f;
+    for (uint32_t g = q * per; g < (q + 1) * per; ++g) acc += s_t[tl2][c2][g];
+    s_r[tl2][c2][q] = acc;
+  }
+  __syncthreads();
+  if (t < 16u) {
+    float r[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      // the tree of moe_ref.h:127-131 at 4 slices: (q0 + q2) + (q1 + q3)
+      const float a0 = s_r[u][t][0] + s_r[u][t][2];
+      const float a1 = s_r[u][t][1] + s_r[u][t][3];
+      r[u] = a0 + a1;
+    }
+    const uint16_t g_b = f2h(r[0]), u_b = f2h(r[1]);
+    const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
+    h[((size_t)m * slots + slot) * inter + ib * 16 + t] = f2h(h2f(s_b) * h2f(u_b));
+  }
+}
+
+// ---- down + combine + residual (moe.cl:383-470; twin moe_ref.h:140-177) ---------------------
+// grid (hidden/16, M): work-group nb makes resid[m][16 nb .. 16 nb + 15] from every slot's
+// down tile nb, combined in slot order.
+__global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restrict__ route,
+                                                       const uint16_t* __restrict__ h,
+                                                       const uint32_t* __restrict__ dn,
+                                                       uint16_t* __restrict__ resid, uint32_t E,
+                                                       uint32_t top_k, uint32_t hidden,
+                                                       uint32_t inter) {
+  __shared__ float s_h[kMaxSlotsInter];
+  __shared__ float s_t[9][16][16];  // [slot][column][group], inter <= 1024
+  __shared__ float s_d[9][16];
+  const uint32_t t = threadIdx.x, m = blockIdx.y, nb = blockIdx.x;
+  const uint32_t G = inter / 64, slots = top_k + 1;
+  const uint32_t* row = route + (size_t)m * kRouteWords;
+  for (uint32_t k = t; k < slots * inter; k += 256u) s_h[k] = h2f(h[(size_t)m * slots * inter + k]);
+  __syncthreads();
+  const size_t block = (size_t)(hidden / 16) * G * kTileU32;
+  const uint32_t tasks = slots * 16u * G;
+  for (uint32_t i = t; i < tasks; i += 256u) {
+    const uint32_t slot = i / (16u * G), rem = i % (16u * G), g = rem / 16u, c = rem % 16u;
+    const uint32_t e = slot_expert(row, slot, E, top_k);
+    const uint32_t* tile = dn + (size_t)e * block + ((size_t)nb * G + g) * kTileU32;
+    s_t[slot][c][g] = group_term(tile, c, s_h + slot * inter + g * 64);
+  }
+  __syncthreads();
+  if (t < slots * 16u) {
+    const uint32_t slot = t / 16u, c = t % 16u, per = G / kDnKs;
+    float r[kDnKs];
+#pragma unroll
+    for (uint32_t q = 0; q < kDnKs; ++q) {
+      float acc = 0.f;
+      for (uint32_t g = q * per; g < (q + 1) * per; ++g) acc += s_t[slot][c][g];
+      r[q] = acc;
+    }
+    s_d[slot][c] = r[0] + r[1];
+  }
+  __syncthreads();
+  if (t < 16u) {
+    // moe_ref.h:144-152: sum_k rne(rne(d_k) * w_k) in slot order; + rne(rne(d_shared) * s)
+    float sum = 0.f;
+    for (uint32_t k = 0; k < top_k; ++k) {
+      const float wk = __builtin_bit_cast(float, row[R_W + k]);
+      sum += h2f(f2h(h2f(f2h(s_d[k][t])) * wk));
+    }
+    const uint16_t r_b = f2h(sum);
+    const float sg = __builtin_bit_cast(float, row[R_SG]);
+    const uint16_t sh_b = f2h(h2f(f2h(s_d[top_k][t])) * sg);
+    const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
+    uint16_t* rp = resid + (size_t)m * hidden + nb * 16 + t;
+    *rp = f2h(h2f(*rp) + h2f(o_b));
+  }
+}
+
+int check_moe(uint32_t M, uint32_t E, uint32_t top_k, uint32_t hidden, uint32_t inter) {
+  if (M == 0 || M > 16) return mi_fail(MI_ERR_SHAPE, "moe: M must be 1..16");
+  if (E < 16 || E > 256 || (E & (E - 1))) return mi_fail(MI_ERR_SHAPE, "moe: experts must be a power of two in [16, 256]");
+  if (top_k < 1 || top_k > 8) return mi_fail(MI_ERR_SHAPE, "moe: top_k must be 1..8");
+  if (hidden == 0 || hidden % 512 || hidden > kMaxHidden)
+    return mi_fail(MI_ERR_SHAPE, "moe: hidden must be a multiple of 512 up to 4096");
+  if (inter == 0 || inter % 128 || inter > 1024)
+    return mi_fail(MI_ERR_SHAPE, "moe: inter must be a multiple of 128 up to 1024");
+  return 0;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* out, uint32_t M, uint32_t K,
+                            uint32_t N, uint32_t ksplit, void* stream) {
+  if (!w_tiled || !x || !out) return mi_fail(MI_ERR_ARG, "gemv_f16w: null pointer");
+  if (M == 0 || M > 16 || K == 0 || N == 0 || N % 16 || K % 64)
+    return mi_fail(MI_ERR_SHAPE, "gemv_f16w: M 1..16, K a multiple of 64, N a multiple of 16");
+  if (ksplit == 0 || ksplit > 16 || (ksplit & (ksplit - 1)) || (K / 8) % ksplit)
+    return mi_fail(MI_ERR_SHAPE, "gemv_f16w: ksplit must be a power of two <= 16 dividing K/8");
+  if (reinterpret_cast<uintptr_t>(x) % 16) return mi_fail(MI_ERR_ARG, "gemv_f16w: x needs 16-byte alignment");
+  gemv_f16w_kernel<<<dim3(N / 16, M), 16 * ksplit, 0, static_cast<hipStream_t>(stream)>>>(w_tiled, x, out, K, N,
+                                                                                          ksplit);
+  return mi_hip(static_cast<int>(hipGetLastError()), "gemv_f16w launch");
+}
+
+extern "C" int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts, uint32_t top_k,
+                            uint32_t router_n, void* stream) {
+  if (!logits || !route) return mi_fail(MI_ERR_ARG, "moe_route: null pointer");
+  if (int e = check_moe(M, experts, top_k, 512, 128)) return e;
+  if (router_n < experts + 1) return mi_fail(MI_ERR_SHAPE, "moe_route: router_n must hold experts + 1 rows");
+  moe_route_kernel<<<M, experts, 0, static_cast<hipStream_t>(stream)>>>(logits, route, experts, top_k, router_n);
+  return mi_hip(static_cast<int>(hipGetLastError()), "moe_route launch");
+}
+
+extern "C" int mi_moe_gate_up(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks, uint16_t* h,
+                              uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                              void* stream) {
+  if (!route || !x || !gu_blocks || !h) return mi_fail(MI_ERR_ARG, "moe_gate_up: null pointer");
+  if (int e = check_moe(M, experts, top_k, hidden, inter)) return e;
+  moe_gate_up_kernel<<<dim3((top_k + 1) * (inter / 16), M), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      route, x, gu_blocks, h, experts, top_k, hidden, inter);
+  return mi_hip(static_cast<int>(hipGetLastError()), "moe_gate_up launch");
+}
+
+extern "C" int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks, uint16_t* resid,
+                           uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                           void* stream) {
+  if (!route || !h || !dn_blocks || !resid) return mi_fail(MI_ERR_ARG, "moe_down: null pointer");
+  if (int e = check_moe(M, experts, top_k, hidden, inter)) return e;
+  moe_down_kernel<<<dim3(hidden / 16, M), 256, 0, static_cast<hipStream_t>(stream)>>>(route, h, dn_blocks, resid,
+                                                                                      experts, top_k, hidden, inter);
+  return mi_hip(static_cast<int>(hipGetLastError()), "moe_down launch");
+}

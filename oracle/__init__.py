@@ -71,6 +71,8 @@ def lib():
             "orc_moe_block": (None, [i32, u32, u32, u32, u32, u32, vp, vp, vp, vp, sz, sz, vp,
                                      vp, sz, sz, u32, u32, vp, vp]),
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
+            "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
+            "orc_f16w_tile": (None, [vp, u32, u32, vp]),
             "orc_threads": (i32, []),
         }
         for name, (res, args) in sig.items():
@@ -115,6 +117,7 @@ def ref():
             "ref_moe_silu_up": (u16, [f32, f32]),
             "ref_moe_combine": (u16, [vp, vp, u32, u32, u16]),
             "ref_moe_block": (None, [vp, u32, u32, u32, u32, u32, vp, vp, vp, u32, u32, vp]),
+            "ref_repack_bf16_tiled": (None, [vp, u32, u32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(R, name)

@@ -851,6 +851,36 @@ void orc_moe_block(int act, uint32_t layout, uint32_t experts, uint32_t top_k, u
   }
 }
 
+// ---- fp16-weight GEMV (src/kernels/gemv_bf16.cl:103-200, weights fp16 in this build) -------
+// The kernel's per-lane chain: acc = 0; per 8-k step `a += w * x` eight times in k order
+// (gemv_bf16.cl:149-157, BF16_STEP); slices merged by the tree of :185-192.
+void orc_gemv_f16w(int act, const uint16_t* w, const uint16_t* x, uint32_t M, uint32_t K, uint32_t N,
+                   uint32_t ksplit, float* out) {
+  const Act A{act};
+  const uint32_t K8 = K / 8, per = K8 / ksplit;
+  std::vector<float> red(ksplit);
+  for (uint32_t m = 0; m < M; ++m)
+    for (uint32_t n = 0; n < N; ++n) {
+      const uint16_t* tile = w + size_t(n / 16) * K8 * 128;
+      for (uint32_t q = 0; q < ksplit; ++q) {
+        float acc = 0.f;
+        for (uint32_t k8 = q * per; k8 < (q + 1) * per; ++k8)
+          for (uint32_t j = 0; j < 8; ++j)
+            acc += orc_f16_to_f32(tile[size_t(k8) * 128 + j * 16 + n % 16]) * A.w(x[size_t(m) * K + k8 * 8 + j]);
+        red[q] = acc;
+      }
+      for (uint32_t stride = ksplit / 2; stride > 0; stride >>= 1)
+        for (uint32_t q = 0; q < stride; ++q) red[q] += red[q + stride];
+      out[size_t(m) * N + n] = red[0];
+    }
+}
+// common::Bf16Tiled::from_rowmajor's element map (the layout gemv_bf16.cl reads)
+void orc_f16w_tile(const uint16_t* w_rm, uint32_t K, uint32_t N, uint16_t* wt) {
+  for (uint32_t n = 0; n < N; ++n)
+    for (uint32_t k = 0; k < K; ++k)
+      wt[(size_t(n / 16) * (K / 8) + k / 8) * 128 + (k % 8) * 16 + n % 16] = w_rm[size_t(n) * K + k];
+}
+
 // ---- dense decode step (src/runtime/capture.cc:997, 1247-1263, 1370-1423, 1461-1480) --------
 uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos,
                         uint16_t* kv_k, uint16_t* kv_v, float* logits, uint32_t n_layers_run) {

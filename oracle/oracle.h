@@ -146,6 +146,17 @@ void orc_moe_block(int act, uint32_t layout, uint32_t experts, uint32_t top_k, u
                    size_t dn_stride_words, size_t dn_stride_scales, uint32_t up_ks,
                    uint32_t dn_ks, uint16_t* h_out, uint16_t* resid);
 
+/* ---- fp16-weight GEMV for the MoE router || shared gate (src/kernels/gemv_bf16.cl:103-200)
+ * w: the canonical tile layout [N/16][K/8][8][16] (element k, n at
+ * ((n/16)*(K/8) + k/8)*128 + (k%8)*16 + n%16), fp16 (the reference: bf16) weights;
+ * x [M][K] activations (act). Per column, each of `ksplit` K slices sums w*x in ascending
+ * k from 0.f (product and sum each rounded); the slices merge by the pairwise tree
+ * stride = ksplit/2 .. 1, slice q < stride adding slice q + stride. out [M][N] fp32. */
+void orc_gemv_f16w(int act, const uint16_t* w, const uint16_t* x, uint32_t M, uint32_t K,
+                   uint32_t N, uint32_t ksplit, float* out);
+/* row-major [N][K] fp16 -> the tile layout above */
+void orc_f16w_tile(const uint16_t* w_rowmajor, uint32_t K, uint32_t N, uint16_t* w_tiled);
+
 /* ---- a whole dense decode step (src/runtime/capture.cc:1247-1480 layer walk) ---- */
 typedef struct orc_linear {
   const uint32_t* qweight; /* [K/8][N] */

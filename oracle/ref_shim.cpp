@@ -160,4 +160,9 @@ void ref_moe_block(const float* logits, uint32_t experts, uint32_t top_k, uint32
   std::memcpy(resid_inout, out.data(), out.size() * 2);
 }
 
+// common/repack.h:118 (the bf16 tile layout gemv_bf16.cl reads; element type agnostic)
+void ref_repack_bf16_tiled(const uint16_t* w_rowmajor, uint32_t K, uint32_t N, uint16_t* out) {
+  common::repack_bf16_tiled(w_rowmajor, K, N, out);
+}
+
 }  // extern "C"

@@ -47,3 +47,15 @@ def test_split_k_choices_for_the_27b_shapes():
             for epi in range(4):
                 s = L.mi_gemv_pick_s_ex(K, N, epi)
                 assert 1 <= s <= K // 64 and (K // 64) % s == 0
+
+
+def test_moe_argument_errors_without_a_gpu():
+    L = mi.lib()
+    assert L.mi_moe_route(None, None, 1, 256, 8, 272, None) == -1
+    assert L.mi_moe_route(8, 8, 1, 100, 8, 272, None) == -2      # experts not a power of two
+    assert L.mi_moe_route(8, 8, 1, 256, 9, 272, None) == -2      # top_k > 8
+    assert L.mi_moe_route(8, 8, 1, 256, 8, 256, None) == -2      # router_n < experts + 1
+    assert L.mi_moe_gate_up(8, 8, 8, 8, 1, 256, 8, 2000, 512, None) == -2  # hidden % 512
+    assert L.mi_moe_down(8, 8, 8, 8, 1, 256, 8, 2048, 2048, None) == -2    # inter > 1024
+    assert L.mi_gemv_f16w(8, 16, 8, 1, 2048, 272, 3, None) == -2           # ksplit not 2^n
+    assert b"ksplit" in L.mi_last_error()

@@ -494,3 +494,44 @@ def test_moe_block_vs_fp64():
         ulp = np.maximum(np.abs(b_), 2.0 ** -14) * 2.0 ** -10
         worst = max(worst, float(np.max(np.abs(a - b_) / ulp)))
     assert worst <= 2.0
+
+
+def _f16w_tiled(w_rm, K, N):
+    wt = np.empty(K * N, np.uint16)
+    O.lib().orc_f16w_tile(O._p(np.ascontiguousarray(w_rm)), K, N, O._p(wt))
+    return wt
+
+
+def test_gemv_f16w_merge_order_known_answer():
+    """gemv_bf16.cl:37-41 documents the KSPLIT merge: at KSPLIT = 4 the column sum is
+    (p0 + p2) + (p1 + p3). Slices 2^24, 1, -2^24, 1 give 2 that way; an ascending chain or an
+    adjacent-pair tree gives 1."""
+    K, N = 32, 16
+    w = np.zeros((N, K), np.float32)
+    x = np.zeros(K, np.float32)
+    for q, (wv, xv) in enumerate([(4096.0, 4096.0), (1.0, 1.0), (-4096.0, 4096.0), (1.0, 1.0)]):
+        w[:, 8 * q] = wv
+        x[8 * q] = xv
+    wt = _f16w_tiled(O.f32_to_f16_bits(w), K, N)
+    out = np.empty(N, np.float32)
+    O.lib().orc_gemv_f16w(O.ORC_F16, O._p(wt), O._p(O.f32_to_f16_bits(x)), 1, K, N, 4, O._p(out))
+    assert np.all(out == 2.0)
+    O.lib().orc_gemv_f16w(O.ORC_F16, O._p(wt), O._p(O.f32_to_f16_bits(x)), 1, K, N, 1, O._p(out))
+    assert np.all(out == 1.0)
+
+
+@pytest.mark.parametrize("ksplit", [1, 4, 16])
+def test_gemv_f16w_vs_fp64(ksplit):
+    """Router || shared-gate GEMV at config 4's shape (K 2048, N 272, M 2): within the
+    sequential fp32 bound (K/ksplit + log2 ksplit) 2^-24 sum|w x| of fp64."""
+    K, N, M = 2048, 272, 2
+    rng = np.random.default_rng(ksplit)
+    w = O.f32_to_f16_bits((0.02 * rng.standard_normal((N, K))).astype(np.float32))
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    out = np.empty((M, N), np.float32)
+    O.lib().orc_gemv_f16w(O.ORC_F16, O._p(_f16w_tiled(w, K, N)), O._p(x), M, K, N, ksplit, O._p(out))
+    wf = O.f16_bits_to_f32(w).astype(np.float64)
+    xf = O.f16_bits_to_f32(x).astype(np.float64)
+    want = xf @ wf.T
+    bound = (K / ksplit + np.log2(ksplit) + 1) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)
+    assert np.all(np.abs(out - want) <= bound)

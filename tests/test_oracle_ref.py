@@ -248,3 +248,13 @@ def test_moe_split_dot_silu_combine_block():
         C.memmove(C.byref(b), C.byref(a), C.sizeof(a))
         assert L().orc_moe_combine(BF, P(d), C.byref(a), K, int(resid[0])) == \
             R.ref_moe_combine(P(d), C.byref(b), E, K, int(resid[0]))
+
+
+def test_f16w_tile_layout_matches_reference_repack():
+    K, N = 256, 48
+    w = np.random.default_rng(3).integers(0, 65536, size=(N, K), dtype=np.uint32).astype(np.uint16)
+    a = np.empty(K * N, np.uint16)
+    b = np.empty(K * N, np.uint16)
+    O.lib().orc_f16w_tile(O._p(w), K, N, O._p(a))
+    R.ref_repack_bf16_tiled(O._p(w), K, N, O._p(b))
+    assert np.array_equal(a, b)
