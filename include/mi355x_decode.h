@@ -73,6 +73,9 @@ int mi_fill_f16(uint16_t* p, size_t n, uint64_t seed, int kind, float a, float b
 int mi_fill_f32(float* p, size_t n, uint64_t seed, int kind, float a, float b, int round16,
                 void* stream);
 int mi_fill_i8(int8_t* p, size_t n, uint64_t seed, int lo, int hi, void* stream);
+/* `tiles` int4 g64 layout-1 tiles of 136 u32 (common/repack.h:17-30): random nibble words and
+ * fp16 scales uniform in [lo, hi) (synthetic expert weights) */
+int mi_fill_layout1(uint32_t* p, size_t tiles, uint64_t seed, float lo, float hi, void* stream);
 
 /* ---- int4 GPTQ g64 unpack: replaces common::Int4Gptq::at (src/common/int4.h:19-23) as
  * a device pass; out[k][n] = (q - 8) * scale, fp32, exact ---- */
@@ -205,6 +208,12 @@ int mi_argmax_finish(uint32_t* ctrl, const void* part, uint32_t groups, uint32_t
 int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w,
                   uint16_t* x_out, float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab,
                   float eps, void* stream);
+/* The norm of the residual as it stands, rows [M][hidden]: the sum of squares in 64-element
+ * chunks added in chunk order, rstd = 1/sqrt(sum / hidden + eps), x = rne(r * rstd * w)
+ * (prep_res_fold with S_PREV 0 then prep_norm_finish, prep.cl:288/350) - the norm after a
+ * block that folds its own output into the residual (moe_down, moe.cl:36-38). */
+int mi_norm_rows(const uint16_t* resid, const float* norm_w, uint16_t* x_out, float* rstd,
+                 uint32_t M, uint32_t hidden, float eps, void* stream);
 int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history,
               uint32_t history_len, uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
 
@@ -240,8 +249,8 @@ int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blo
 
 /* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
  * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the
- * dense GQA decoder this build runs: every layer is attention + SwiGLU MLP, all linears
- * int4 g64 layout 0, fp16 activations and KV. */
+ * GQA decoders this build runs: every layer is attention + a SwiGLU MLP (int4 g64 layout 0)
+ * or a mixture-of-experts block (layout-1 experts); fp16 activations and KV. */
 typedef struct mi_model_desc {
   uint32_t layers, hidden, q_heads, kv_heads, head_dim, rot_dim, inter, vocab, vocab_used;
   uint32_t max_len;  /* KV cache rows per layer (positions) */
@@ -249,6 +258,11 @@ typedef struct mi_model_desc {
   uint32_t max_rows; /* largest verify step (rows) the engine captures, 1..8 */
   uint32_t attn_tgt; /* attention blocks per kv head (the v2 grid's TGT) */
   float rope_theta, rms_eps;
+  /* experts > 0: every layer's MLP is a mixture-of-experts block (moe.cl) of `experts`
+   * routed experts (power of two, 16..256), top_k of them per token plus one shared
+   * expert, expert intermediate moe_inter; the router || shared gate is an fp16 linear of
+   * roundup16(experts + 1) rows. `inter` is then unused. */
+  uint32_t experts, top_k, moe_inter;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;
@@ -257,6 +271,7 @@ typedef struct mi_engine mi_engine;
 enum {
   MI_T_QKV_Q = 0, MI_T_QKV_S, MI_T_O_Q, MI_T_O_S, MI_T_GU_Q, MI_T_GU_S, MI_T_DOWN_Q, MI_T_DOWN_S,
   MI_T_IN_NORM, MI_T_POST_NORM, MI_T_Q_NORM, MI_T_K_NORM,
+  MI_T_ROUTER, MI_T_MOE_GU, MI_T_MOE_DN, /* MoE layers: router tiles, expert blocks */
   MI_T_EMBED = 32, MI_T_FINAL_NORM, MI_T_LM_Q, MI_T_LM_S, MI_T_ROPE, MI_T_KV_K, MI_T_KV_V,
   MI_T_LOGITS, MI_T_CTRL, MI_T_HISTORY
 };

@@ -35,6 +35,7 @@ SIGNATURES = {
     "mi_fill_u32": (i32, [vp, sz, u64, vp]),
     "mi_fill_f16": (i32, [vp, sz, u64, i32, f32, f32, vp]),
     "mi_fill_f32": (i32, [vp, sz, u64, i32, f32, f32, i32, vp]),
+    "mi_fill_layout1": (i32, [vp, sz, u64, f32, f32, vp]),
     "mi_fill_i8": (i32, [vp, sz, u64, i32, i32, vp]),
     "mi_int4_dequant": (i32, [vp, vp, vp, u32, u32, vp]),
     "mi_gemv_w4a16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
@@ -71,6 +72,7 @@ SIGNATURES = {
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
     "mi_accept_greedy": (u32, [vp, vp, u32, vp]),
+    "mi_norm_rows": (i32, [vp, vp, vp, vp, u32, u32, f32, vp]),
     "mi_gemv_f16w": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_route": (i32, [vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_gate_up": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
@@ -133,7 +135,8 @@ class ModelDesc(C.Structure):
     _fields_ = [("layers", u32), ("hidden", u32), ("q_heads", u32), ("kv_heads", u32),
                 ("head_dim", u32), ("rot_dim", u32), ("inter", u32), ("vocab", u32),
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
-                ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32)]
+                ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
+                ("experts", u32), ("top_k", u32), ("moe_inter", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
@@ -145,6 +148,22 @@ def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_le
                      attn_tgt, rope_theta, rms_eps)
 
 
+def moe_desc(layers, hidden, q_heads, kv_heads, head_dim, experts, top_k, moe_inter, vocab, max_len,
+             **kw):
+    """A mixture-of-experts decoder: every layer is attention + the MoE block (experts routed,
+    top_k per token, one shared expert, expert intermediate moe_inter)."""
+    d = dense_desc(layers, hidden, q_heads, kv_heads, head_dim, 0, vocab, max_len, **kw)
+    d.experts, d.top_k, d.moe_inter = experts, top_k, moe_inter
+    return d
+
+
+def desc_moe_cfg4(max_len=4096 + 512):
+    """a 40-layer MoE decoder, hidden 2048, 256 experts top 8 + 1 shared,
+    expert intermediate 512, attention 16 q / 2 kv heads of 256, vocab 151936 (assumed; the
+    config does not state it), RoPE theta 1e6."""
+    return moe_desc(40, 2048, 16, 2, 256, 256, 8, 512, 151936, max_len)
+
+
 def desc_27b(max_len=4096 + 512):
     """the 27B-shape dense decoder (64 layers, hidden 5120, 40 q / 8 kv
     heads of 128, SwiGLU 17408, vocab 151936, RoPE theta 1e6)."""
@@ -153,7 +172,7 @@ def desc_27b(max_len=4096 + 512):
 
 # tensor kinds (mi_engine_tensor)
 (T_QKV_Q, T_QKV_S, T_O_Q, T_O_S, T_GU_Q, T_GU_S, T_DOWN_Q, T_DOWN_S, T_IN_NORM, T_POST_NORM,
- T_Q_NORM, T_K_NORM) = range(12)
+ T_Q_NORM, T_K_NORM, T_ROUTER, T_MOE_GU, T_MOE_DN) = range(15)
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY) = range(32, 42)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64

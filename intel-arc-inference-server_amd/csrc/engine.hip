@@ -12,7 +12,8 @@
 //   * verify(k drafts) replays an (k+1)-row graph, accept_greedy picks the accepted
 //     prefix on the host, commit() moves pos and cur_token (engine.cc:868-960,
 //     spec_accept.cc:81-85).
-// The layer walk is capture.cc's dense-attention layer (fa_layer :1370 + mlp :1247):
+// The layer walk is capture.cc's dense-attention layer (fa_layer :1370 + mlp :1247, or
+// moe_block :1295 for a mixture-of-experts model):
 //   res_fold + norm_finish, qkv GEMV, attn_prep, attn_decode, attn_reduce, o GEMV,
 //   res_fold + norm_finish, gate||up GEMV, silu_mul, down GEMV; then head() (:1461):
 //   res_fold + norm_finish, lm_head GEMV, fold to logits, argmax.
@@ -44,7 +45,10 @@ struct Linear {
 };
 
 struct Layer {
-  Linear qkv, o, gate_up, down;
+  Linear qkv, o, gate_up, down;  // gate_up / down unused in a MoE layer
+  uint16_t* router = nullptr;    // MoE: fp16 [router_n][hidden] in the gemv_bf16 tile layout
+  uint32_t* moe_gu = nullptr;    // MoE: experts + 1 layout-1 gate||up blocks
+  uint32_t* moe_dn = nullptr;    // MoE: experts + 1 layout-1 down blocks
   float* in_norm = nullptr;
   float* post_norm = nullptr;
   float* q_norm = nullptr;
@@ -94,6 +98,11 @@ struct mi_engine {
   void* argmax_part = nullptr;
   uint32_t* counters = nullptr;  // the fused GEMV epilogues' tile counters (self-resetting)
   float* rstd = nullptr;
+  float* moe_logits = nullptr;   // [max_rows][router_n]
+  uint32_t* moe_route = nullptr; // [max_rows][MI_MOE_ROUTE_WORDS]
+  uint16_t* moe_h = nullptr;     // [max_rows][top_k + 1][moe_inter]
+  uint32_t router_n = 0;
+  size_t gu_block = 0, dn_block = 0;  // u32 per expert block
   uint32_t norm_g = 20;
   mi_attn_shape ash{};
   hipGraphExec_t graphs[17] = {};
@@ -142,11 +151,23 @@ struct mi_engine {
     norm_g = H / 64;  // the fused epilogues take the residual's sum of squares in 64-element chunks
     layer.resize(m.layers);
     size_t part_max = 0;
+    const bool moe = m.experts > 0;
+    if (moe) {
+      router_n = (m.experts + 1 + 15) / 16 * 16;
+      gu_block = size_t(2 * m.moe_inter / 16) * (H / 64) * 136;
+      dn_block = size_t(H / 16) * (m.moe_inter / 64) * 136;
+    }
     for (Layer& L : layer) {
       MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_PARTIALS));
       MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
-      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
-      MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
+      if (moe) {
+        MI_TRY(alloc(&L.router, size_t(router_n) * H));
+        MI_TRY(alloc(&L.moe_gu, (m.experts + 1) * gu_block));
+        MI_TRY(alloc(&L.moe_dn, (m.experts + 1) * dn_block));
+      } else {
+        MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
+        MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
+      }
       MI_TRY(alloc(&L.in_norm, H));
       MI_TRY(alloc(&L.post_norm, H));
       if (m.qk_norm) {
@@ -154,7 +175,7 @@ struct mi_engine {
         MI_TRY(alloc(&L.k_norm, HD));
       }
       for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
-        part_max = std::max(part_max, size_t(l->S) * R * l->N);
+        if (l->q) part_max = std::max(part_max, size_t(l->S) * R * l->N);
     }
     MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
     part_max = std::max(part_max, size_t(lm_head.S) * R * m.vocab);
@@ -181,10 +202,21 @@ struct mi_engine {
     MI_TRY(alloc(&counters, max_tiles));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(counters, 0, max_tiles * 4, stream)), "counters clear"));
     MI_TRY(alloc(&rstd, R));
+    if (moe) {
+      MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
+      MI_TRY(alloc(&moe_route, size_t(R) * MI_MOE_ROUTE_WORDS));
+      MI_TRY(alloc(&moe_h, size_t(R) * (m.top_k + 1) * m.moe_inter));
+    }
 
     // synthetic weights (BASELINE config 2's distributions)
     for (Layer& L : layer) {
-      for (Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down}) MI_TRY(init_linear(*l, seed));
+      for (Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
+        if (l->q) MI_TRY(init_linear(*l, seed));
+      if (moe) {  // router N(0, 0.02), int4 g64 experts
+        MI_TRY(mi_fill_f16(L.router, size_t(router_n) * H, seed++, 1, 0.0f, 0.02f, stream));
+        MI_TRY(mi_fill_layout1(L.moe_gu, (m.experts + 1) * gu_block / 136, seed++, 0.002f, 0.02f, stream));
+        MI_TRY(mi_fill_layout1(L.moe_dn, (m.experts + 1) * dn_block / 136, seed++, 0.002f, 0.02f, stream));
+      }
       MI_TRY(mi_fill_f32(L.in_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
       MI_TRY(mi_fill_f32(L.post_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
       if (m.qk_norm) {
@@ -213,6 +245,13 @@ struct mi_engine {
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(ctrl, 0, MI_CTRL_WORDS * 4, stream)), "ctrl clear"));
     MI_TRY(mi_hip(static_cast<int>(hipStreamSynchronize(stream)), "engine init"));
     return 0;
+  }
+
+  // the router GEMV's K split: gemv_bf16's {16, 16} tiling (kernels.h gemv_bf16_tiling)
+  uint32_t router_ksplit() const {
+    uint32_t k = 16;
+    while (k > 1 && (d.hidden / 8) % k) k /= 2;
+    return k;
   }
 
   int gemv(const Linear& l, const uint16_t* in, uint32_t M) {
@@ -252,13 +291,24 @@ struct mi_engine {
       MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
       const mi_gemv_epilogue eo = resid_epi(L.post_norm);
       MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part, M, L.o.K, L.o.N, L.o.S, &eo, stream));
+      const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
+      if (d.experts) {
+        // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
+        // into the residual, then the next norm with nothing left to fold
+        MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
+        MI_TRY(mi_moe_route(moe_logits, moe_route, M, d.experts, d.top_k, router_n, stream));
+        MI_TRY(mi_moe_gate_up(moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
+        MI_TRY(mi_moe_down(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
+        MI_TRY(mi_norm_rows(resid, next_w, x, rstd, M, d.hidden, d.rms_eps, stream));
+        continue;
+      }
       mi_gemv_epilogue eg{};
       eg.kind = MI_EPI_SILU;
       eg.counters = counters;
       eg.h = hbuf;
       MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                               stream));
-      const mi_gemv_epilogue ed = resid_epi(li + 1 < d.layers ? layer[li + 1].in_norm : final_norm);
+      const mi_gemv_epilogue ed = resid_epi(next_w);
       MI_TRY(mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part, M, L.down.K, L.down.N, L.down.S, &ed, stream));
     }
     mi_gemv_epilogue el{};
@@ -314,7 +364,10 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
   if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
-      m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64) {
+      m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 ||
+      (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
+                     m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
+                     m.hidden % 512 || m.hidden > 4096))) {
     mi_fail(MI_ERR_SHAPE, "engine_create: unsupported model shape");
     return nullptr;
   }
@@ -363,6 +416,9 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_POST_NORM: *ptr = L->post_norm; b = size_t(m.hidden) * 4; break;
     case MI_T_Q_NORM: *ptr = L->q_norm; b = L->q_norm ? size_t(m.head_dim) * 4 : 0; break;
     case MI_T_K_NORM: *ptr = L->k_norm; b = L->k_norm ? size_t(m.head_dim) * 4 : 0; break;
+    case MI_T_ROUTER: *ptr = L->router; b = L->router ? size_t(e->router_n) * m.hidden * 2 : 0; break;
+    case MI_T_MOE_GU: *ptr = L->moe_gu; b = L->moe_gu ? (m.experts + 1) * e->gu_block * 4 : 0; break;
+    case MI_T_MOE_DN: *ptr = L->moe_dn; b = L->moe_dn ? (m.experts + 1) * e->dn_block * 4 : 0; break;
     case MI_T_EMBED: *ptr = e->embed; b = size_t(m.vocab) * m.hidden * 2; break;
     case MI_T_FINAL_NORM: *ptr = e->final_norm; b = size_t(m.hidden) * 4; break;
     case MI_T_LM_Q: lin_q(e->lm_head, ptr, &b); break;
@@ -385,8 +441,8 @@ int mi_engine_linear_s(mi_engine* e, uint32_t which, uint32_t* S) {
   switch (which) {
     case 0: *S = L.qkv.S; break;
     case 1: *S = L.o.S; break;
-    case 2: *S = L.gate_up.S; break;
-    case 3: *S = L.down.S; break;
+    case 2: *S = L.gate_up.q ? L.gate_up.S : 0; break;  // 0: a MoE model has no dense MLP
+    case 3: *S = L.down.q ? L.down.S : 0; break;
     case 4: *S = e->lm_head.S; break;
     default: return mi_fail(MI_ERR_ARG, "engine_linear_s: which 0..4");
   }

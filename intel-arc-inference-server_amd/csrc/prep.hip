@@ -268,6 +268,9 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(uint32_t* __restrict_
 // grid (M), 256 lanes: embed_gather followed by the first RMSNorm, with the residual's
 // sum of squares taken in 64-element chunks (the reference's res_fold tree at chunk 64:
 // one element per lane, then the pairwise tree; chunks summed in ascending order).
+// GATHER: resid[m] = embed[cur_token[m]] first (embed_gather), else the norm of resid[m] as it
+// is (prep_res_fold with S_PREV 0, then prep_norm_finish).
+template <bool GATHER>
 __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ ctrl,
                                                          const uint16_t* __restrict__ embed,
                                                          uint16_t* __restrict__ resid,
@@ -277,12 +280,15 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
                                                          uint32_t vocab, float eps) {
   __shared__ float chunk[1024];
   const uint32_t m = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-  const uint32_t row = ctrl[CTRL_CUR + m];
-  if (row >= vocab) {
-    if (t == 0) ctrl[CTRL_DEBUG] = 0xDEAD0001u;
-    return;
+  const uint16_t* src = resid + (size_t)m * hidden;
+  if constexpr (GATHER) {
+    const uint32_t row = ctrl[CTRL_CUR + m];
+    if (row >= vocab) {
+      if (t == 0) ctrl[CTRL_DEBUG] = 0xDEAD0001u;
+      return;
+    }
+    src = embed + (size_t)row * hidden;
   }
-  const uint16_t* src = embed + (size_t)row * hidden;
   uint16_t* dst = resid + (size_t)m * hidden;
   const uint32_t nch = hidden / 64;
   // wave w takes chunks w, w + 4, ...; the loads of up to 8 chunks go out together
@@ -297,7 +303,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
     for (uint32_t u = 0; u < 8; ++u) {
       const uint32_t c = c0 + 4 * u;
       if (c < nch) {
-        dst[c * 64 + lane] = v16[u];
+        if constexpr (GATHER) dst[c * 64 + lane] = v16[u];
         const float v = h2f(v16[u]);
         float a = __builtin_fmaf(v, v, 0.f);
 #pragma unroll
@@ -479,9 +485,18 @@ int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const 
                   float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab, float eps, void* stream) {
   if (!ctrl || !embed || !resid || !norm_w || !x_out || M == 0 || M > 8 || hidden % 64 || hidden > 65536)
     return mi_fail(MI_ERR_ARG, "embed_norm: bad arguments (M <= 8, hidden a multiple of 64)");
-  embed_norm_kernel<<<M, kWG, 0, (hipStream_t)stream>>>(ctrl, embed, resid, norm_w, x_out, rstd, hidden, vocab,
-                                                         eps);
+  embed_norm_kernel<true><<<M, kWG, 0, (hipStream_t)stream>>>(ctrl, embed, resid, norm_w, x_out, rstd, hidden,
+                                                               vocab, eps);
   return mi_hip((int)hipGetLastError(), "embed_norm");
+}
+
+int mi_norm_rows(const uint16_t* resid, const float* norm_w, uint16_t* x_out, float* rstd, uint32_t M,
+                 uint32_t hidden, float eps, void* stream) {
+  if (!resid || !norm_w || !x_out || M == 0 || M > 16 || hidden % 64 || hidden > 65536)
+    return mi_fail(MI_ERR_ARG, "norm_rows: bad arguments (M <= 16, hidden a multiple of 64)");
+  embed_norm_kernel<false><<<M, kWG, 0, (hipStream_t)stream>>>(nullptr, nullptr, const_cast<uint16_t*>(resid),
+                                                                norm_w, x_out, rstd, hidden, 0, eps);
+  return mi_hip((int)hipGetLastError(), "norm_rows");
 }
 
 uint32_t mi_argmax_groups(uint32_t vocab) { return (vocab + kChunk - 1) / kChunk; }

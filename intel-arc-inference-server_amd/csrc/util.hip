@@ -47,6 +47,20 @@ __global__ void fill_f32_kernel(float* p, size_t n, uint64_t seed, int kind, flo
     p[i] = v;
   }
 }
+// int4 g64 layout-1 tiles (common/repack.h:17-30): 128 random nibble words, then 16 fp16
+// scales uniform in [lo, hi) packed two per word
+__global__ void fill_layout1_kernel(uint32_t* p, size_t n_words, uint64_t seed, float lo, float hi) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_words; i += (size_t)gridDim.x * 256) {
+    const uint64_t h = mix64(seed, i);
+    const uint32_t w = (uint32_t)(i % 136u);
+    if (w < 128u) {
+      p[i] = (uint32_t)h;
+    } else {
+      const float a = lo + (hi - lo) * unit01((uint32_t)h), b = lo + (hi - lo) * unit01((uint32_t)(h >> 32));
+      p[i] = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+    }
+  }
+}
 // int8 uniform in [lo, hi]
 __global__ void fill_i8_kernel(int8_t* p, size_t n, uint64_t seed, int lo, int hi) {
   const uint32_t span = (uint32_t)(hi - lo + 1);
@@ -105,6 +119,10 @@ int mi_fill_f32(float* p, size_t n, uint64_t seed, int kind, float a, float b, i
 int mi_fill_i8(int8_t* p, size_t n, uint64_t seed, int lo, int hi, void* stream) {
   fill_i8_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(p, n, seed, lo, hi);
   return mi_hip((int)hipGetLastError(), "fill_i8");
+}
+int mi_fill_layout1(uint32_t* p, size_t tiles, uint64_t seed, float lo, float hi, void* stream) {
+  fill_layout1_kernel<<<grid_for(tiles * 136), 256, 0, (hipStream_t)stream>>>(p, tiles * 136, seed, lo, hi);
+  return mi_hip((int)hipGetLastError(), "fill_layout1");
 }
 int mi_int4_dequant(const uint32_t* qweight, const uint16_t* scales, float* out, uint32_t K, uint32_t N,
                     void* stream) {

@@ -157,7 +157,8 @@ class Linear(C.Structure):
 class Layer(C.Structure):
     _fields_ = [("qkv", Linear), ("o", Linear), ("gate_up", Linear), ("down", Linear),
                 ("in_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
-                ("k_norm", C.c_void_p)]
+                ("k_norm", C.c_void_p), ("router", C.c_void_p), ("moe_gu", C.c_void_p),
+                ("moe_dn", C.c_void_p)]
 
 
 class DenseModel(C.Structure):
@@ -165,7 +166,9 @@ class DenseModel(C.Structure):
                 ("vocab", C.c_uint32), ("vocab_used", C.c_uint32), ("max_len", C.c_uint32),
                 ("attn", AttnShape), ("rms_eps", C.c_float), ("layer", C.c_void_p),
                 ("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", Linear),
-                ("rope", C.c_void_p), ("tgt", C.c_uint32), ("norm_g", C.c_uint32)]
+                ("rope", C.c_void_p), ("tgt", C.c_uint32), ("norm_g", C.c_uint32),
+                ("experts", C.c_uint32), ("top_k", C.c_uint32), ("moe_inter", C.c_uint32),
+                ("router_n", C.c_uint32), ("router_ksplit", C.c_uint32)]
 
 
 # ---- numpy helpers ----------------------------------------------------------------------

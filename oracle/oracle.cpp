@@ -925,6 +925,22 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
     orc_attn_reduce_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
     linear(ly.o, attn_out.data());
     norm(part.data(), ly.o.S, ly.post_norm);
+    if (md->experts) {
+      // capture.cc:1295 moe_block: router || shared gate, route, experts; moe_down folds its
+      // output into the residual itself, so the next norm folds nothing (moe.cl:36-38)
+      const uint32_t H2 = md->hidden;
+      std::vector<float> lg(md->router_n);
+      orc_gemv_f16w(act, ly.router, x.data(), 1, H2, md->router_n, md->router_ksplit, lg.data());
+      orc_moe_route r;
+      orc_moe_route_fn(act, lg.data(), md->experts, md->top_k, &r);
+      const size_t gub = size_t(2 * md->moe_inter / 16) * (H2 / 64) * 136;
+      const size_t dnb = size_t(H2 / 16) * (md->moe_inter / 64) * 136;
+      orc_moe_block(act, 1, md->experts, md->top_k, H2, md->moe_inter, &r, x.data(), ly.moe_gu, nullptr, gub, 0,
+                    ly.moe_dn, nullptr, dnb, 0, 4, 2, nullptr, resid.data());
+      prev.clear();
+      s_prev = 0;
+      continue;
+    }
     linear(ly.gate_up, x.data());
     orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
     linear(ly.down, hbuf.data());

@@ -169,6 +169,11 @@ typedef struct orc_layer {
   const float* post_norm;
   const float* q_norm; /* may be NULL (no q/k norm) */
   const float* k_norm;
+  /* a mixture-of-experts layer (the model's experts > 0): router || shared gate fp16 in the
+   * gemv_bf16 tile layout, experts + 1 layout-1 gate||up and down blocks */
+  const uint16_t* router;
+  const uint32_t* moe_gu;
+  const uint32_t* moe_dn;
 } orc_layer;
 typedef struct orc_dense_model {
   uint32_t layers, hidden, inter, vocab, vocab_used, max_len;
@@ -181,6 +186,8 @@ typedef struct orc_dense_model {
   const float* rope; /* [max_len][2][rot_dim/2] */
   uint32_t tgt;      /* attention blocks per kv head (the v2 grid) */
   uint32_t norm_g;   /* 0: single-launch res_norm tree; G > 0: res_fold over G chunks + norm_finish */
+  /* experts > 0: every layer's MLP is the MoE block (moe.cl), router K split router_ksplit */
+  uint32_t experts, top_k, moe_inter, router_n, router_ksplit;
 } orc_dense_model;
 /* One step for token `tok` at position pos. kv_k/kv_v: [layers][kv_heads][max_len][hd] act
  * (this build's layout), updated in place. Writes logits fp32 [vocab] and returns argmax. */

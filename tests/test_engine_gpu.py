@@ -36,15 +36,23 @@ class OracleModel:
         H, HD, QH, KVH, I = d.hidden, d.head_dim, d.q_heads, d.kv_heads, d.inter
         S = [eng.linear_s(w) for w in range(5)]
         dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
+        moe = d.experts > 0
         layers = (O.Layer * d.layers)()
         for li in range(d.layers):
             lins = []
             for w, (K, N) in enumerate(dims):
+                if moe and w >= 2:
+                    lins.append(O.Linear(None, None, K, N, 1))
+                    continue
                 q = self._h(eng.to_host(2 * w, li, np.uint32))
                 s = self._h(eng.to_host(2 * w + 1, li, np.uint16))
                 lins.append(O.Linear(q.ctypes.data, s.ctypes.data, K, N, S[w]))
             L = layers[li]
             L.qkv, L.o, L.gate_up, L.down = lins
+            if moe:
+                L.router = self._h(eng.to_host(mi.T_ROUTER, li, np.uint16)).ctypes.data
+                L.moe_gu = self._h(eng.to_host(mi.T_MOE_GU, li, np.uint32)).ctypes.data
+                L.moe_dn = self._h(eng.to_host(mi.T_MOE_DN, li, np.uint32)).ctypes.data
             L.in_norm = self._h(eng.to_host(mi.T_IN_NORM, li, np.float32)).ctypes.data
             L.post_norm = self._h(eng.to_host(mi.T_POST_NORM, li, np.float32)).ctypes.data
             if d.qk_norm:
@@ -65,6 +73,10 @@ class OracleModel:
                               C.cast(layers, C.c_void_p), embed.ctypes.data, fnorm.ctypes.data,
                               O.Linear(lmq.ctypes.data, lms.ctypes.data, H, d.vocab, S[4]),
                               self.rope.ctypes.data, d.attn_tgt, H // 64)
+        if moe:
+            self.m.experts, self.m.top_k, self.m.moe_inter = d.experts, d.top_k, d.moe_inter
+            self.m.router_n = (d.experts + 1 + 15) // 16 * 16
+            self.m.router_ksplit = 16
 
     def _h(self, a):
         a = np.ascontiguousarray(a)
@@ -108,6 +120,52 @@ def test_decode_steps_vs_oracle_teacher_forced(qk_norm):
         c = eng.ctrl()
         assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_CUR] == got_tok and c[mi.CTRL_OUT] == got_tok
         tok, pos = got_tok, pos + 1
+    eng.close()
+
+
+def moe_small_desc(**kw):
+    d = dict(layers=2, hidden=512, q_heads=8, kv_heads=2, head_dim=256, experts=16, top_k=4, moe_inter=128,
+             vocab=4096, max_len=512, max_rows=4, attn_tgt=4)
+    d.update(kw)
+    return mi.moe_desc(d.pop("layers"), d.pop("hidden"), d.pop("q_heads"), d.pop("kv_heads"), d.pop("head_dim"),
+                       d.pop("experts"), d.pop("top_k"), d.pop("moe_inter"), d.pop("vocab"), d.pop("max_len"), **d)
+
+
+@pytest.mark.parametrize("top_k", [4, 8])
+def test_moe_decode_steps_vs_oracle(top_k):
+    """A mixture-of-experts model (config 4's layer kind at a small size, head_dim 256):
+    the captured step against the oracle's step, teacher forced."""
+    eng = mi.Engine(moe_small_desc(top_k=top_k, experts=32 if top_k == 8 else 16), seed=77)
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 100, 11
+    eng.reset(pos, tok)
+    for step in range(3):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert argmax_ok(got_tok, want)
+        assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+        tok, pos = got_tok, pos + 1
+    eng.close()
+
+
+def test_moe_verify_rows_bitwise_plain_steps():
+    eng = mi.Engine(moe_small_desc(), seed=12)
+    eng.capture(1)
+    P, t0 = 50, 3
+    eng.reset(P, t0)
+    toks, lg = [], []
+    for _ in range(3):
+        toks.append(int(eng.generate(1)[0]))
+        lg.append(eng.logits(1)[0].copy())
+    eng.reset(P, t0)
+    rows = eng.verify(toks[:2])
+    assert list(rows) == toks
+    got = eng.logits(3)
+    for m in range(3):
+        assert np.array_equal(got[m].view(np.uint32), lg[m].view(np.uint32))
     eng.close()
 
 

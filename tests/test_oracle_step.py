@@ -167,3 +167,133 @@ def test_bar_rejects_plausible_wiring_mistakes(mistake):
     _, got, _, _ = m.oracle_step(194, 37)
     want = m.fp64_step(194, 37, mistake=mistake)[0]
     assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
+
+
+def layout1_dequant(blocks, K, N):
+    """fp64 [K][N] of one int4 g64 layout-1 block, from the format's definition: tile
+    (n/16, k/64) of 136 words; word (k%64)/8 * 16 + n%16 holds k's nibble k%8 (low first);
+    the 16 fp16 scales follow the 128 nibble words."""
+    G, NT = K // 64, N // 16
+    t = blocks[:NT * G * 136].reshape(NT, G, 136)
+    nib = (t[:, :, :128].reshape(NT, G, 8, 16)[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF
+    # nib [nt][g][j][n16][i] -> k = g*64 + j*8 + i, n = nt*16 + n16
+    q = nib.astype(np.float64) - 8.0
+    sc = O.f16_bits_to_f32(t[:, :, 128:].copy().view(np.uint16).reshape(NT, G, 16)).astype(np.float64)
+    w = q * sc[:, :, None, :, None]
+    return w.transpose(1, 2, 4, 0, 3).reshape(K, N)
+
+
+class TinyMoe(TinyModel):
+    """TinyModel whose MLPs are the MoE block: E routed experts, top_k + a shared one."""
+
+    def __init__(self, seed, E=16, top_k=4, moe_inter=128, H=512, **kw):
+        super().__init__(seed, H=H, I=256, **kw)
+        rng = np.random.default_rng(seed + 1000)
+        self.E, self.top_k, self.mi_ = E, top_k, moe_inter
+        self.router_n = (E + 1 + 15) // 16 * 16
+        layers_c = C.cast(self.m.layer, C.POINTER(O.Layer))
+        gub = (2 * moe_inter // 16) * (H // 64) * 136
+        dnb = (H // 16) * (moe_inter // 64) * 136
+        for li in range(self.d["layers"]):
+            rw = np.zeros((self.router_n, H), np.float32)
+            rw[:E + 1] = 0.05 * rng.standard_normal((E + 1, H))
+            rw16 = f16(rw)
+            rt = np.empty(self.router_n * H, np.uint16)
+            O.lib().orc_f16w_tile(O._p(rw16), H, self.router_n, O._p(rt))
+
+            def blocks(n_blocks, K, N):
+                tiles = n_blocks * (N // 16) * (K // 64)
+                b = rng.integers(0, 2**32, size=(tiles, 136), dtype=np.uint64).astype(np.uint32)
+                b[:, 128:] = f16(rng.uniform(0.004, 0.03, (tiles, 16))).view(np.uint32).reshape(tiles, 8)
+                return b.reshape(-1)
+            gu, dn = blocks(E + 1, H, 2 * moe_inter), blocks(E + 1, moe_inter, H)
+            self.keep += [rt, gu, dn]
+            L = layers_c[li]
+            L.router, L.moe_gu, L.moe_dn = rt.ctypes.data, gu.ctypes.data, dn.ctypes.data
+            self.w[li]["router"] = O.f16_bits_to_f32(rw16).astype(np.float64)
+            self.w[li]["gu"] = [layout1_dequant(gu[e * gub:(e + 1) * gub], H, 2 * moe_inter) for e in range(E + 1)]
+            self.w[li]["dn"] = [layout1_dequant(dn[e * dnb:(e + 1) * dnb], moe_inter, H) for e in range(E + 1)]
+        self.m.experts, self.m.top_k, self.m.moe_inter = E, top_k, moe_inter
+        self.m.router_n, self.m.router_ksplit = self.router_n, 16
+        self.ids = []
+
+    def mlp(self, ws, x, mistake=None):
+        E, k = self.E, self.top_k
+        lg = ws["router"] @ x
+        p = np.exp(lg[:E] - lg[:E].max())
+        p /= p.sum()
+        ids = sorted(range(E), key=lambda e: (-p[e], e))[:k]
+        self.ids.append(ids)
+        w = p[ids] / p[ids].sum()
+        j = np.arange(self.mi_)
+
+        def expert(e):
+            gu = x @ ws["gu"][e]
+            g, u = gu[(j // 16) * 32 + j % 16], gu[(j // 16) * 32 + j % 16 + 16]
+            if mistake == "moe_gate_up_swap":
+                g, u = u, g
+            return (g / (1.0 + np.exp(-g)) * u) @ ws["dn"][e]
+        out = sum(wk * expert(e) for wk, e in zip(w, ids))
+        sg = 1.0 / (1.0 + np.exp(-lg[E]))
+        return out + (sg if mistake != "moe_no_shared" else 0.0) * expert(E)
+
+
+def _fp64_moe_step(m, tok, pos, mistake=None):
+    """TinyModel.fp64_step with each layer's MLP replaced by TinyMoe.mlp."""
+    orig = m.w
+    d = m.d
+    H, QH, KVH, HD = d["H"], d["QH"], d["KVH"], d["HD"]
+    eps = 1e-6
+
+    def rms(v, w):
+        return v / np.sqrt(np.mean(v * v) + eps) * w
+    half = d["rot"] // 2
+    cos, sin = m.rope[pos, 0].astype(np.float64), m.rope[pos, 1].astype(np.float64)
+
+    def rope(v):
+        out = v.copy()
+        a, b = v[:half], v[half:d["rot"]]
+        out[:half] = a * cos - b * sin
+        out[half:d["rot"]] = b * cos + a * sin
+        return out
+    resid = O.f16_bits_to_f32(m.embed[tok]).astype(np.float64)
+    kc = O.f16_bits_to_f32(m.kv_k).astype(np.float64)
+    vc = O.f16_bits_to_f32(m.kv_v).astype(np.float64)
+    G = QH // KVH
+    for li, ws in enumerate(orig):
+        nm = ws["norms"]
+        x = rms(resid, nm["in_norm"])
+        qkv = x @ ws[0]
+        q = qkv[:QH * HD].reshape(QH, HD)
+        k = qkv[QH * HD:(QH + KVH) * HD].reshape(KVH, HD)
+        v = qkv[(QH + KVH) * HD:].reshape(KVH, HD)
+        q = np.stack([rope(rms(h, nm["q_norm"])) for h in q])
+        k = np.stack([rope(rms(h, nm["k_norm"])) for h in k])
+        kc[li, :, pos], vc[li, :, pos] = k, v
+        att = np.empty((QH, HD))
+        for h in range(QH):
+            sc = kc[li, h // G, :pos + 1] @ q[h] / np.sqrt(HD)
+            p = np.exp(sc - sc.max())
+            att[h] = (p / p.sum()) @ vc[li, h // G, :pos + 1]
+        resid = resid + att.reshape(-1) @ ws[1]
+        resid = resid + m.mlp(ws, rms(resid, nm["post_norm"]), mistake)
+    return rms(resid, m.fnorm) @ m.lm
+
+
+@pytest.mark.parametrize("seed,pos", [(7, 0), (8, 33)])
+def test_moe_step_vs_independent_fp64_forward(seed, pos):
+    m = TinyMoe(seed)
+    tok = seed * 13
+    am, got, _, _ = m.oracle_step(tok, pos)
+    want = _fp64_moe_step(m, tok, pos)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= 5e-3 * scale, np.abs(got - want).max() / scale
+    assert np.corrcoef(got, want)[0, 1] > 0.9999
+
+
+@pytest.mark.parametrize("mistake", ["moe_gate_up_swap", "moe_no_shared"])
+def test_moe_bar_rejects_plausible_mistakes(mistake):
+    m = TinyMoe(7)
+    _, got, _, _ = m.oracle_step(91, 33)
+    want = _fp64_moe_step(m, 91, 33, mistake)
+    assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
