@@ -152,6 +152,185 @@ def stream_read_rate(st):
     return nbytes * 5 / (ms * 1e-3) / 1e9
 
 
+class Dev:
+    """Device buffers for the secondary measurements (freed together)."""
+
+    def __init__(self):
+        self.L = mi.lib()
+        self.ptrs = []
+
+    def alloc(self, nbytes):
+        p = C.c_void_p()
+        mi.check(self.L.mi_malloc(C.byref(p), nbytes))
+        self.ptrs.append(p)
+        return p
+
+    def upload(self, arr):
+        p = self.alloc(arr.nbytes)
+        mi.check(self.L.mi_memcpy_h2d(p, arr.ctypes.data, arr.nbytes, None))
+        return p
+
+    def free(self):
+        for p in self.ptrs:
+            mi.check(self.L.mi_free(p))
+        self.ptrs = []
+
+
+def time_calls(st, fn, reps, warm=5):
+    for i in range(warm):
+        fn(i)
+    mi.check(mi.lib().mi_stream_sync(st))
+    ev = Events(st)
+    ev.start()
+    for i in range(reps):
+        fn(i)
+    return ev.stop_ms() / reps * 1e3  # us per call
+
+
+def measure_cfg1(st):
+    """one W4A16 GEMV, K = N = 4096, M = 1, x N(0,1), scales
+    U(0.002, 0.02), out fp16; >= 100 launches cycling over 96 weight copies (> 3x the 256 MB
+    MALL). A call = the split-K GEMV + the fold of its partials to fp16."""
+    L, D = mi.lib(), Dev()
+    K = N = 4096
+    copies = 96
+    S = L.mi_gemv_pick_s(K, N)
+    qw, sc = [], []
+    for c in range(copies):
+        q = D.alloc(K // 8 * N * 4)
+        s = D.alloc(K // 64 * N * 2)
+        mi.check(L.mi_fill_u32(q, K // 8 * N, 1000 + c, st))
+        mi.check(L.mi_fill_f16(s, K // 64 * N, 5000 + c, 0, 0.002, 0.02, st))
+        qw.append(q)
+        sc.append(s)
+    x = D.alloc(K * 2)
+    mi.check(L.mi_fill_f16(x, K, 1234, 1, 0.0, 1.0, st))
+    part = D.alloc(S * N * 4)
+    out = D.alloc(N * 2)
+    gemv = lambda i: mi.check(L.mi_gemv_w4a16(qw[i % copies], sc[i % copies], x, part, 1, K, N, S, st))
+
+    def call(i):
+        gemv(i)
+        mi.check(L.mi_fold_partials(part, out, None, S, 1, N, st))
+    t_call = time_calls(st, call, 192)
+    t_gemv = time_calls(st, gemv, 192)
+    D.free()
+    alg = K * N // 2 + (K // 64) * N * 2 + 2 * K + 2 * N  # 8,929,280 B
+    return {"workload": "BASELINE configs[0]: W4A16 GEMV K=N=4096, M=1, fp16 out", "split_k": S,
+            "us_per_call": round(t_call, 3), "us_gemv_kernel_only": round(t_gemv, 3), "alg_bytes": alg,
+            "gbs_per_call": round(alg / t_call / 1e3, 1), "gbs_gemv_kernel": round(alg / t_gemv / 1e3, 1),
+            "frac_of_peak_gemv": round(alg / t_gemv / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def measure_cfg3(st, ctx):
+    """one layer's decode attention at context `ctx`, 40 q / 8 kv heads
+    of 128, int8 K/V uniform [-127, 127] with fp16 scales U(0.005, 0.05) per (pos, kv head),
+    64-token pages in a shuffled table; attn_decode + attn_reduce per call."""
+    L, D = mi.lib(), Dev()
+    QH, KVH, HD, P, tgt = 40, 8, 128, 64, 128
+    rng = np.random.default_rng(ctx)
+    k8, v8 = D.alloc(KVH * ctx * HD), D.alloc(KVH * ctx * HD)
+    ks, vs = D.alloc(KVH * ctx * 2), D.alloc(KVH * ctx * 2)
+    mi.check(L.mi_fill_i8(k8, KVH * ctx * HD, 31, -127, 127, st))
+    mi.check(L.mi_fill_i8(v8, KVH * ctx * HD, 32, -127, 127, st))
+    mi.check(L.mi_fill_f16(ks, KVH * ctx, 33, 0, 0.005, 0.05, st))
+    mi.check(L.mi_fill_f16(vs, KVH * ctx, 34, 0, 0.005, 0.05, st))
+    pages = D.upload(rng.permutation(ctx // P).astype(np.uint32))
+    q = D.alloc(QH * HD * 4)
+    mi.check(L.mi_fill_f32(q, QH * HD, 35, 1, 0.0, 1.0, 1, st))
+    ctrl_h = np.zeros(64, np.uint32)
+    ctrl_h[0], ctrl_h[1] = ctx - 1, 1
+    ctrl = D.upload(ctrl_h)
+    part = D.alloc(QH * tgt * (HD + 2) * 4)
+    out = D.alloc(QH * HD * 2)
+    sh = mi.AttnShape(QH, KVH, HD, HD, 0, (QH + 2 * KVH) * HD, QH * HD, (QH + KVH) * HD,
+                      float(np.float32(1 / np.sqrt(HD))), 1e-6)
+
+    def call(i):
+        mi.check(L.mi_attn_decode(ctrl, q, 1, k8, v8, ks, vs, HD, ctx * HD, 1, ctx, pages, P, ctx, part, 1, tgt,
+                                  C.byref(sh), st))
+        mi.check(L.mi_attn_reduce(ctrl, part, None, out, 1, tgt, ctx, C.byref(sh), st))
+    t = time_calls(st, call, 50)
+    D.free()
+    alg = 2 * KVH * HD * ctx + 2 * KVH * ctx * 2
+    return {"context": ctx, "us_per_layer": round(t, 2), "alg_bytes": alg, "gbs": round(alg / t / 1e3, 1),
+            "frac_of_peak": round(alg / t / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def measure_cfg5(st):
+    """the small-M verify GEMV, M in {4, 8, 16} on the 27B shapes
+    (gate||up 5120->34816, down 17408->5120, qkv 5120->7168), activations N(0,1); weight
+    copies cycled past the MALL. Reports HBM rate and MFMA rate (2 M K N flops)."""
+    L, D = mi.lib(), Dev()
+    rows = []
+    for name, K, N in (("gate_up", 5120, 34816), ("down", 17408, 5120), ("qkv", 5120, 7168)):
+        wb = K * N // 2 + (K // 64) * N * 2
+        copies = max(3, -(-768 * 2**20 // wb))
+        S = L.mi_gemv_pick_s(K, N)
+        qw = [D.alloc(K // 8 * N * 4) for _ in range(copies)]
+        sc = [D.alloc(K // 64 * N * 2) for _ in range(copies)]
+        for c in range(copies):
+            mi.check(L.mi_fill_u32(qw[c], K // 8 * N, 70 + c, st))
+            mi.check(L.mi_fill_f16(sc[c], K // 64 * N, 170 + c, 0, 0.002, 0.02, st))
+        x = D.alloc(16 * K * 2)
+        mi.check(L.mi_fill_f16(x, 16 * K, 9, 1, 0.0, 1.0, st))
+        part = D.alloc(S * 16 * N * 4)
+        for M in (1, 4, 8, 16):
+            fn = lambda i: mi.check(L.mi_gemv_w4a16(qw[i % copies], sc[i % copies], x, part, M, K, N, S, st))
+            t = time_calls(st, fn, 60)
+            alg = wb + 2 * M * K + 4 * M * N
+            tf = 2 * M * K * N / t / 1e6
+            rows.append({"linear": name, "K": K, "N": N, "M": M, "split_k": S, "us": round(t, 2),
+                         "gbs": round(alg / t / 1e3, 1), "hbm_frac": round(alg / t / 1e3 / HBM_PEAK_GBS, 4),
+                         "tflops": round(tf, 2), "mfma_frac_fp16": round(tf / 2500.0, 5)})
+        D.free()
+    return rows
+
+
+def measure_cfg4(args):
+    """a 40-layer MoE decoder (hidden 2048, 256 experts top 8 + shared,
+    expert inter 512, attention 16 q / 2 kv of 256, vocab 151936 assumed) at context 4096:
+    tokens/s of the captured step, and one step against the CPU oracle."""
+    max_len = ((args.context + 64 + 1 + 63) // 64) * 64
+    desc = mi.desc_moe_cfg4(max_len=max_len)
+    eng = mi.Engine(desc, seed=args.seed + 1)
+    eng.capture(1)
+    st = eng.stream
+    out = {"workload": "BASELINE configs[3]: MoE decode step (40 layers, 256 experts top 8 + shared)"}
+    if not args.no_cpu:
+        eng.reset(args.context, 1000)
+        dt, cpu_logits, cpu_am, threads = cpu_oracle_step(eng, 1000, args.context)
+        eng.reset(args.context, 1000)
+        gpu_tok = int(eng.generate(1)[0])
+        g = eng.logits(1)[0].astype(np.float64)
+        w = cpu_logits.astype(np.float64)
+        err = np.abs(g - w)
+        out["parity"] = {"max_err_over_max_logit": float(err.max() / np.abs(w).max()),
+                         "within_rel_2e-3": bool(np.all(err <= 2e-3 * np.abs(w) + 2e-3 * np.abs(w).max())),
+                         "argmax_gpu": gpu_tok, "argmax_oracle": cpu_am}
+        out["cpu_tokens_per_s"] = round(1.0 / dt, 4)
+    eng.reset(args.context, 1000)
+    for _ in range(4):
+        eng.replay(1)
+    mi.check(mi.lib().mi_device_sync())
+    ev = Events(st)
+    ev.start()
+    n = 32
+    for _ in range(n):
+        eng.replay(1)
+    ms = ev.stop_ms() / n
+    c = eng.ctrl()
+    assert c[mi.CTRL_DEBUG] == 0, hex(c[mi.CTRL_DEBUG])
+    eng.close()
+    H, E, I, QH, KVH, HD, V = 2048, 256, 512, 16, 2, 256, 151936
+    per_layer = 9 * (2 * I * H + I * H) * 17 // 32 + (E + 1 + 15) // 16 * 16 * H * 2 \
+        + ((QH + 2 * KVH) * HD * H + QH * HD * H) * 17 // 32 + 2 * KVH * (args.context + 1) * HD * 2
+    alg = 40 * per_layer + H * V * 17 // 32
+    out.update({"ms_per_step": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 2), "alg_bytes_per_token": alg,
+                "gbs": round(alg / ms / 1e6, 1)})
+    return out
+
+
 def cpu_oracle_step(eng, tok, pos):
     """One full decode step of the same model through the CPU oracle (the reference's
     scalar twins restated; OpenMP over columns in the GEMV twins). Returns (seconds,
@@ -168,12 +347,18 @@ def cpu_oracle_step(eng, tok, pos):
         keep.append(a)
         return a.ctypes.data
 
+    moe = d.experts > 0
     layers = (O.Layer * d.layers)()
     for li in range(d.layers):
         lins = [O.Linear(h(2 * w, li, np.uint32), h(2 * w + 1, li, np.uint16), K, N, S[w])
+                if not (moe and w >= 2) else O.Linear(None, None, K, N, 1)
                 for w, (K, N) in enumerate(dims)]
         Ly = layers[li]
         Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+        if moe:
+            Ly.router = h(mi.T_ROUTER, li, np.uint16)
+            Ly.moe_gu = h(mi.T_MOE_GU, li, np.uint32)
+            Ly.moe_dn = h(mi.T_MOE_DN, li, np.uint32)
         Ly.in_norm = h(mi.T_IN_NORM, li, np.float32)
         Ly.post_norm = h(mi.T_POST_NORM, li, np.float32)
         if d.qk_norm:
@@ -187,6 +372,9 @@ def cpu_oracle_step(eng, tok, pos):
                          h(mi.T_FINAL_NORM, 0, np.float32),
                          O.Linear(h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab, S[4]),
                          h(mi.T_ROPE, 0, np.float32), d.attn_tgt, H // 64)
+    if moe:
+        model.experts, model.top_k, model.moe_inter = d.experts, d.top_k, d.moe_inter
+        model.router_n, model.router_ksplit = (d.experts + 1 + 15) // 16 * 16, 16
     logits = np.zeros(d.vocab, np.float32)
     t0 = time.perf_counter()
     am = O.lib().orc_dense_step(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(logits),
@@ -203,6 +391,8 @@ def main():
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline and parity step")
+    ap.add_argument("--no-other", action="store_true",
+                    help="skip the secondary measurements of BASELINE configs 1, 3, 4 and 5")
     ap.add_argument("--eager", action="store_true",
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
@@ -277,6 +467,19 @@ def main():
     roof["stream_read_gbs"] = round(stream_gbs, 1)
     roof["frac_of_stream"] = round(roof["achieved"] / stream_gbs, 4)
     log(f"bench: gemv roofline {roof}")
+    eng.close()
+
+    other = None
+    if not args.eager and not args.no_other:
+        log("bench: other configurations (cfg1 GEMV, cfg3 attention, cfg5 small-M, cfg4 MoE step) ...")
+        other = {"cfg1_gemv": measure_cfg1(None)}
+        log(f"bench: cfg1 {other['cfg1_gemv']}")
+        other["cfg3_attention_int8_paged"] = [measure_cfg3(None, L) for L in (32768, 131072)]
+        log(f"bench: cfg3 {other['cfg3_attention_int8_paged']}")
+        other["cfg5_small_m_gemv"] = measure_cfg5(None)
+        log(f"bench: cfg5 {other['cfg5_small_m_gemv']}")
+        other["cfg4_moe_step"] = measure_cfg4(args)
+        log(f"bench: cfg4 {other['cfg4_moe_step']}")
 
     out = {
         "metric": "batch-1 decode tokens/s (27B-shape W4A16); int4 GEMV HBM GB/s vs peak",
@@ -301,9 +504,9 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "parity": parity,
+        "other_configs": other,
     }
     print(json.dumps(out), flush=True)
-    eng.close()
 
 
 if __name__ == "__main__":

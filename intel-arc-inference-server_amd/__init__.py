@@ -129,6 +129,13 @@ def header_functions():
     return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
 
 
+class AttnShape(C.Structure):
+    """mi_attn_shape: heads, head_dim, rotary dims, gate on/off, the fused qkv column map."""
+    _fields_ = [("q_heads", u32), ("kv_heads", u32), ("head_dim", u32), ("rot_dim", u32),
+                ("gated", u32), ("qkv_n", u32), ("k_off", u32), ("v_off", u32), ("scale", f32),
+                ("eps", f32)]
+
+
 # ---- the decode loop (host-side mirror of src/runtime/engine.h) -------------------------
 class ModelDesc(C.Structure):
     """mi_model_desc: the model's shape as data (model::ModelDesc)."""

@@ -38,9 +38,9 @@ __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
   return p < 64u ? 64u : p;
 }
 
-__device__ __forceinline__ size_t kv_row(uint32_t p, const uint32_t* pages, uint32_t page) {
-  return pages ? (size_t)pages[p / page] * page + p % page : (size_t)p;
-}
+// page-table entries one work-group stages (a block of ppw positions spans at most
+// ppw / page + 1 pages)
+constexpr uint32_t kMaxBlockPages = 256;
 
 struct AttnDecodeArgs {
   const uint32_t* ctrl;
@@ -118,8 +118,8 @@ __device__ __forceinline__ h8_t chunk_h8(const KvChunk<KV8>& c) {
 }
 
 // HD: head dim; KV8: int8 KV; GQA: q heads per kv head. A work-group walks its block in
-// chunks of 64 positions; every thread issues all of its K and V loads for the chunk
-// before using any, so a chunk costs one HBM round trip.
+// chunks of 64 positions; every thread issues all of its K and V loads for a chunk
+// together, one chunk ahead of the one it computes when DB is set.
 //   scores  on the matrix cores: wave w computes the 16 x 16 tile (q heads padded to 16) x
 //           (positions 16w .. 16w+15) with v_mfma_f32_16x16x32_f16, A = q split into an f16
 //           high part and the f16 rounding of the remainder (two MFMAs: the dot is fp32
@@ -129,13 +129,16 @@ __device__ __forceinline__ h8_t chunk_h8(const KvChunk<KV8>& c) {
 //   P V     on the vector ALUs: HD / 8 lanes own a V row (8 dims, 16 bytes each), the
 //           256 / (HD / 8) row slots accumulate sum_p w_p v_p and are merged in LDS in slot
 //           order at the end.
-template <int HD, int KV8, int GQA>
+// DB: double-buffer the chunks (blocks longer than one chunk); without it the registers of
+// one chunk's K and V are all a thread holds.
+template <int HD, int KV8, int GQA, bool DB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   constexpr uint32_t CH = 64, KK = HD / 32;
   constexpr uint32_t LP = HD / 8, SLOTS = 256 / LP, VU = CH / SLOTS;
   __shared__ float sc[GQA][CH];
   __shared__ float st_alpha[GQA], st_m[GQA], st_l[GQA];
   __shared__ float red[SLOTS][GQA][HD];
+  __shared__ uint32_t s_pages[kMaxBlockPages];  // the block's page-table entries (paged KV)
 
   const uint32_t j = blockIdx.x, blk = blockIdx.y, m = blockIdx.z;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
@@ -152,6 +155,58 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   if (blk >= nb) return;
   const uint32_t p_begin = blk * s, p_end = min(p_begin + s, L);
 
+  float acc[GQA][8];
+#pragma unroll
+  for (uint32_t g = 0; g < GQA; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  if (t < GQA) {
+    st_m[t] = -INFINITY;
+    st_l[t] = 0.f;
+  }
+
+  // A paged cache's entries for this block are read once, into LDS, so a chunk's K/V loads
+  // never wait on a page-table load first.
+  const uint32_t pg0 = a.pages ? p_begin / a.page : 0u;
+  if (a.pages) {
+    const uint32_t np = (p_end - 1) / a.page - pg0 + 1;
+    for (uint32_t i = t; i < np; i += 256u) s_pages[i] = a.pages[pg0 + i];
+    __syncthreads();
+  }
+  auto row_of = [&](uint32_t p) -> size_t {
+    return a.pages ? (size_t)s_pages[p / a.page - pg0] * a.page + p % a.page : (size_t)p;
+  };
+  const size_t hoff = (size_t)j * a.head_stride;
+  const size_t shoff = (size_t)j * a.sc_head_stride;
+  const uint32_t pk = 16u * wave + qi;  // this lane's score position within the chunk
+  // chunk c's K and V rows into registers (zeros past the block's end)
+  auto load_kv = [&](uint32_t c0, KvChunk<KV8> (&kc)[KK], KvChunk<KV8> (&vc)[VU]) {
+    const uint32_t clen = c0 < p_end ? min(CH, p_end - c0) : 0u;
+    if (pk < clen) {
+      const size_t row = row_of(c0 + pk);
+#pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk)
+        kc[kk] = load_chunk<KV8>(a.kv_k, a.k_scale, row * a.row_stride + hoff + 32 * kk + 8 * qq,
+                                 row * a.sc_row_stride + shoff);
+    } else {
+#pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(kc[kk]);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < VU; ++u) {
+      const uint32_t pl = u * SLOTS + slot;
+      if (pl < clen) {
+        const size_t row = row_of(c0 + pl);
+        vc[u] = load_chunk<KV8>(a.kv_v, a.v_scale, row * a.row_stride + hoff + d0, row * a.sc_row_stride + shoff);
+      } else {
+        zero_chunk<KV8>(vc[u]);
+      }
+    }
+  };
+  // DB: chunk c + 1's loads are issued before chunk c is used, and the barriers in the loop
+  // order LDS only, so those loads stay in flight across them.
+  KvChunk<KV8> kc[KK], vc[VU];
+  load_kv(p_begin, kc, vc);  // the first chunk's loads go out before q is read
   // q as the MFMA A operand: row qi = head (zero past GQA), k = 32 kk + 8 qq + e
   h8_t qhi[KK], qlo[KK];
 #pragma unroll
@@ -174,42 +229,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
       qlo[kk][e] = (half_t)(v[e] - (float)h);
     }
   }
-  float acc[GQA][8];
-#pragma unroll
-  for (uint32_t g = 0; g < GQA; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-  if (t < GQA) {
-    st_m[t] = -INFINITY;
-    st_l[t] = 0.f;
-  }
-
-  const size_t hoff = (size_t)j * a.head_stride;
-  const size_t shoff = (size_t)j * a.sc_head_stride;
-  const uint32_t pk = 16u * wave + qi;  // this lane's score position within the chunk
   for (uint32_t c0 = p_begin; c0 < p_end; c0 += CH) {
     const uint32_t clen = min(CH, p_end - c0);
-    KvChunk<KV8> kc[KK], vc[VU];
-    if (pk < clen) {
-      const size_t row = kv_row(c0 + pk, a.pages, a.page);
-#pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk)
-        kc[kk] = load_chunk<KV8>(a.kv_k, a.k_scale, row * a.row_stride + hoff + 32 * kk + 8 * qq,
-                                 row * a.sc_row_stride + shoff);
-    } else {
-#pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(kc[kk]);
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < VU; ++u) {
-      const uint32_t pl = u * SLOTS + slot;
-      if (pl < clen) {
-        const size_t row = kv_row(c0 + pl, a.pages, a.page);
-        vc[u] = load_chunk<KV8>(a.kv_v, a.v_scale, row * a.row_stride + hoff + d0, row * a.sc_row_stride + shoff);
-      } else {
-        zero_chunk<KV8>(vc[u]);
-      }
-    }
+    KvChunk<KV8> kn[KK], vn[VU];
+    if constexpr (DB) load_kv(c0 + CH, kn, vn);
     // scores
     f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -225,20 +248,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
       const uint32_t head = 4u * qq + r;
       if (head < GQA && pk < clen) sc[head][pk] = d[r] * rs;
     }
-    __syncthreads();
+    lds_barrier();
     // chunk max, weights and chunk sum: wave w owns heads w, w + 4
     for (uint32_t g = wave; g < GQA; g += 4) {
       const float v = lane < clen ? sc[g][lane] : -INFINITY;
-      float mx = v;
-#pragma unroll
-      for (uint32_t o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float mx = wave_max(v);
       const float m_old = st_m[g];
       const float m_new = fmaxf(m_old, mx);
       const float w = lane < clen ? expf(v - m_new) : 0.f;
       if (lane < clen) sc[g][lane] = w;
-      float sum = w;
-#pragma unroll
-      for (uint32_t o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      const float sum = wave_sum(w);
       if (lane == 0) {
         const float alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
         st_alpha[g] = alpha;
@@ -246,7 +265,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         st_m[g] = m_new;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // rescale, then accumulate w * v from the registers loaded above
 #pragma unroll
     for (uint32_t g = 0; g < GQA; ++g) {
@@ -268,7 +287,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
+    if constexpr (DB) {
+#pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk) kc[kk] = kn[kk];
+#pragma unroll
+      for (uint32_t u = 0; u < VU; ++u) vc[u] = vn[u];
+    } else if (c0 + CH < p_end) {
+      load_kv(c0 + CH, kc, vc);
+    }
   }
   // merge the row slots in slot order through LDS
 #pragma unroll
@@ -349,18 +376,25 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
-template <int HD, int KV8>
-int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
+template <int HD, int KV8, bool DB>
+int launch_decode_db(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
   switch (gqa) {
-    case 1: attn_decode_kernel<HD, KV8, 1><<<grid, 256, 0, st>>>(a); break;
-    case 2: attn_decode_kernel<HD, KV8, 2><<<grid, 256, 0, st>>>(a); break;
-    case 4: attn_decode_kernel<HD, KV8, 4><<<grid, 256, 0, st>>>(a); break;
-    case 5: attn_decode_kernel<HD, KV8, 5><<<grid, 256, 0, st>>>(a); break;
-    case 6: attn_decode_kernel<HD, KV8, 6><<<grid, 256, 0, st>>>(a); break;
-    case 8: attn_decode_kernel<HD, KV8, 8><<<grid, 256, 0, st>>>(a); break;
+    case 1: attn_decode_kernel<HD, KV8, 1, DB><<<grid, 256, 0, st>>>(a); break;
+    case 2: attn_decode_kernel<HD, KV8, 2, DB><<<grid, 256, 0, st>>>(a); break;
+    case 4: attn_decode_kernel<HD, KV8, 4, DB><<<grid, 256, 0, st>>>(a); break;
+    case 5: attn_decode_kernel<HD, KV8, 5, DB><<<grid, 256, 0, st>>>(a); break;
+    case 6: attn_decode_kernel<HD, KV8, 6, DB><<<grid, 256, 0, st>>>(a); break;
+    case 8: attn_decode_kernel<HD, KV8, 8, DB><<<grid, 256, 0, st>>>(a); break;
     default: return -1;
   }
   return 0;
+}
+// A cache of kv_len rows never gives a block more than one 64-position chunk when
+// kv_len <= 64 tgt (ppw stays 64); otherwise the double-buffered kernel runs.
+template <int HD, int KV8>
+int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
+  if (a.kv_len && a.kv_len <= 64u * a.tgt) return launch_decode_db<HD, KV8, false>(a, gqa, grid, st);
+  return launch_decode_db<HD, KV8, true>(a, gqa, grid, st);
 }
 
 }  // namespace
@@ -393,6 +427,8 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
     return mi_fail(MI_ERR_SHAPE, "attn_decode: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
   if (pages && (page == 0 || page % 16))
     return mi_fail(MI_ERR_SHAPE, "attn_decode: a KV page holds a multiple of 16 positions");
+  if (pages && (!kv_len || mi_attn_ppw(kv_len, tgt) / page + 1 > kMaxBlockPages))
+    return mi_fail(MI_ERR_SHAPE, "attn_decode: a paged cache needs kv_len, and at most 256 pages per block");
   if ((row_stride % 8) || (head_stride % 8))
     return mi_fail(MI_ERR_ARG, "attn_decode: KV strides must keep 8-element alignment");
   AttnDecodeArgs a{ctrl,  attn_q,       kv_k,           kv_v,   k_scale,         v_scale,

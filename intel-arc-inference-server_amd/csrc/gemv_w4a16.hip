@@ -267,7 +267,6 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
         for (; g < ntiles; ++g) tot += s_ss[g];
         const float r = 1.0f / sqrtf(tot / (float)N + epi.eps);
         s_rstd[row] = r;
-        epi.rstd[row] = r;
       }
       __syncthreads();
     }
@@ -295,6 +294,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
         }
       }
     }
+    // rstd goes out last: a global store before a barrier would make the barrier wait for it
+    if (t < M) epi.rstd[t] = s_rstd[t];
   } else if constexpr (EPI == EPI_SILU) {
     // 64 interleave16 columns = 32 outputs k = 32 tile + i (gate at gflat, up at gflat + 16)
     for (uint32_t i = t; i < 32u * M; i += 256u) {

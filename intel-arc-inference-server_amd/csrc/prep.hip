@@ -318,10 +318,10 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
     float tot = 0.f;
     for (uint32_t c = 0; c < nch; ++c) tot += chunk[c];
     s_rstd = 1.0f / sqrtf(tot / (float)hidden + eps);
-    if (rstd_out) rstd_out[m] = s_rstd;
   }
   __syncthreads();
   const float r = s_rstd;
+  if (t == 0 && rstd_out) rstd_out[m] = r;  // after the barrier, which would otherwise wait for it
   for (uint32_t k0 = t; k0 < hidden; k0 += 8 * kWG) {
     uint16_t v16[8];
 #pragma unroll

@@ -92,6 +92,20 @@ def test_decode_vs_fp64_and_oracle(kind, QH, KVH, HD, pos):
     check_close(got[0].reshape(QH, HD), O.f16_bits_to_f32(ref[0]).astype(np.float64).reshape(QH, HD))
 
 
+@pytest.mark.parametrize("QH,KVH,HD", [(8, 8, 128), (8, 4, 128), (8, 2, 128), (12, 2, 128), (16, 2, 256),
+                                      (8, 2, 256)])
+@pytest.mark.parametrize("Lm,tgt,pos", [(512, 4, 300), (512, 4, 45), (4096, 128, 3000)])
+def test_decode_every_gqa_and_block_length(QH, KVH, HD, Lm, tgt, pos):
+    """Every GQA ratio the kernel instantiates, blocks of one and of several 16-position
+    chunks per wave (tgt 4 at 512 cached rows: the double-buffered variant), partial blocks."""
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(0, KVH, Lm, HD, pos + QH)
+    q = np.random.default_rng(pos + KVH).standard_normal((1, QH, HD)).astype(np.float32)
+    got, _ = gpu_attention(sh, q, 0, k, v, ks, vs, pos, 1, tgt)
+    want = fp64_attention(sh, q[0], 0, k, v, ks, vs, pos + 1)
+    check_close(got[0].reshape(QH, HD), want)
+
+
 @pytest.mark.parametrize("kind", [0, 1])
 def test_long_context_paged_bitwise(kind):
     """BASELINE config 3 shape (40 q / 8 kv, hd 128) at L = 32768, 64-token pages in a
