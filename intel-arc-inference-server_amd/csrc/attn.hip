@@ -340,6 +340,11 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   const size_t PART = HD + 2;
   const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
   const size_t bstride = (size_t)M * PART;
+  // the first 64 blocks' acc values do not depend on phase 1: their loads go out first
+  // (a block past nb reloads block nb - 1 and is not added)
+  float v64[64];
+#pragma unroll
+  for (uint32_t u = 0; u < 64; ++u) v64[u] = base[min(u, nb - 1) * bstride + 2 + d];
   // phase 1 (wave 0): the common max and the per-block factors
   if (d < 64) {
     float mx = -INFINITY;
@@ -357,16 +362,19 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
     if (d == 0) s_sm = sm;
   }
   __syncthreads();
+  // added in ascending block order: the preloaded 64, then the rest 8 loads at a time
   float acc = 0.f;
-  uint32_t b = 0;
-  for (; b + 8 <= nb; b += 8) {
+#pragma unroll
+  for (uint32_t u = 0; u < 64; ++u)
+    if (u < nb) acc = __builtin_fmaf(v64[u], fac[u], acc);
+  for (uint32_t b = 64; b < nb; b += 8) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = base[(b + u) * bstride + 2 + d];
+    for (uint32_t u = 0; u < 8; ++u) v[u] = base[min(b + u, nb - 1) * bstride + 2 + d];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(v[u], fac[b + u], acc);
+    for (uint32_t u = 0; u < 8; ++u)
+      if (b + u < nb) acc = __builtin_fmaf(v[u], fac[b + u], acc);
   }
-  for (; b < nb; ++b) acc = __builtin_fmaf(base[b * bstride + 2 + d], fac[b], acc);
   const float o = acc / s_sm;
   uint16_t r;
   if (gated && attn_gate)

@@ -189,56 +189,65 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   const float* nw = is_q ? a.q_norm : a.k_norm;
   const size_t base = is_q ? (a.gated ? (size_t)h * 2 * HD : (size_t)h * HD)
                            : (size_t)a.k_off + (size_t)h * HD;
-  // sum_s partials in ascending s from 0.f; the loads go out 8 at a time (past S they reload
+  // sum_s partials in ascending s from 0.f; the loads go out 32 at a time (past S they reload
   // the last partial and add +0.f, which leaves the sum's bits unchanged: it starts at +0.f
   // and a round-to-nearest sum of nonzero terms is never -0)
   auto qkv_sum = [&](size_t col) {
     const float* p = a.partials + (size_t)m * a.qkv_n + col;
     const size_t step = (size_t)a.M * a.qkv_n;
     float v = 0.0f;
-    for (uint32_t s = 0; s < a.S; s += 8u) {
-      float t8[8];
+    for (uint32_t s = 0; s < a.S; s += 32u) {
+      float t8[32];
 #pragma unroll
-      for (uint32_t u = 0; u < 8; ++u) t8[u] = p[min(s + u, a.S - 1u) * step];
+      for (uint32_t u = 0; u < 32; ++u) t8[u] = p[min(s + u, a.S - 1u) * step];
 #pragma unroll
-      for (uint32_t u = 0; u < 8; ++u) v += s + u < a.S ? t8[u] : 0.f;
+      for (uint32_t u = 0; u < 32; ++u) v += s + u < a.S ? t8[u] : 0.f;
     }
     return v;
   };
+  // Everything this lane reads goes out before the norm's barriers (loads cannot move
+  // across them): the head's partials, the V (or gate) partials, the RoPE pair, the norm
+  // weight, the page-table entry. The arithmetic and its order are unchanged.
+  const uint32_t half = a.rot_dim / 2;
+  const float* cs = a.rope + (size_t)(pos + m) * 2 * half;
+  float rc = 1.f, rsn = 0.f;
+  if (i < a.rot_dim) {
+    const uint32_t ii = i < half ? i : i - half;
+    rc = cs[ii];
+    rsn = cs[half + ii];
+  }
+  const float wn = nw ? nw[i] : 0.f;
+  const size_t row = is_q ? 0 : kv_row(pos + m, a.pages, a.page);
+  float vg = 0.f;
+  if (!is_q) vg = qkv_sum((size_t)a.v_off + (size_t)h * HD + i);
+  else if (a.gated && a.attn_gate) vg = qkv_sum(base + HD + i);
   const float xf = h2f(f2h(qkv_sum(base + i)));
   float nv;
   if (nw) {
     const float tot = tree_hd(xf * xf, red, HD);
     const float rstd = 1.0f / sqrtf(tot / (float)HD + a.eps);
-    nv = h2f(f2h(xf * rstd * nw[i]));
+    nv = h2f(f2h(xf * rstd * wn));
   } else {
     nv = xf;
   }
   nrm[i] = nv;
   __syncthreads();
-  const uint32_t half = a.rot_dim / 2;
-  const float* cs = a.rope + (size_t)(pos + m) * 2 * half;
   float outv;
   if (i < half) {
-    const float c = cs[i], s = cs[half + i];
-    const float t = nrm[i + half] * s;
-    outv = __builtin_fmaf(nv, c, -t);
+    const float t = nrm[i + half] * rsn;
+    outv = __builtin_fmaf(nv, rc, -t);
   } else if (i < a.rot_dim) {
-    const uint32_t ii = i - half;
-    const float c = cs[ii], s = cs[half + ii];
-    const float t = nrm[ii] * s;
-    outv = __builtin_fmaf(nv, c, t);
+    const float t = nrm[i - half] * rsn;
+    outv = __builtin_fmaf(nv, rc, t);
   } else {
     outv = nv;
   }
   if (is_q) {
     a.attn_q[((size_t)m * a.q_heads + h) * HD + i] = outv;
-    if (a.gated && a.attn_gate)
-      a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(qkv_sum(base + HD + i)));
+    if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(vg));
   } else {
-    const size_t row = kv_row(pos + m, a.pages, a.page);
     a.kv_k[row * a.row_stride + h * a.head_stride + i] = f2h(outv);
-    a.kv_v[row * a.row_stride + h * a.head_stride + i] = f2h(qkv_sum((size_t)a.v_off + (size_t)h * HD + i));
+    a.kv_v[row * a.row_stride + h * a.head_stride + i] = f2h(vg);
   }
 }
 
