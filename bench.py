@@ -390,6 +390,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--attn-tgt", type=int, default=None,
+                    help="attention blocks per kv head (the v2 grid's TGT); default: the model description's")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline and parity step")
     ap.add_argument("--no-other", action="store_true",
                     help="skip the secondary measurements of BASELINE configs 1, 3, 4 and 5")
@@ -405,6 +407,8 @@ def main():
 
     max_len = ((args.context + args.warmup + args.steps + 1 + 63) // 64) * 64
     desc = mi.desc_27b(max_len=max_len)
+    if args.attn_tgt:
+        desc.attn_tgt = args.attn_tgt
     log(f"bench: building 27B-shape engine (max_len {max_len}) ...")
     t0 = time.time()
     eng = mi.Engine(desc, seed=args.seed)
