@@ -169,6 +169,17 @@ int mi_attn_prep(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
                  const float* rope, float* attn_q, float* attn_gate, uint16_t* kv_k,
                  uint16_t* kv_v, size_t row_stride, size_t head_stride, const uint32_t* pages,
                  uint32_t page, uint32_t kv_len, void* stream);
+/* attn_prep_kv8 (kv8.cl:287-300, the int8 KV writer; scheme src/common/kv8.h:1-26): the
+ * mi_attn_prep chain at head_dim 256, then q rotated (attn_q fp32, R = H_256 diag(s) / 16),
+ * and the K row (f16 rounding of the roped k) and V row (f16 rounding of v) rotated and
+ * quantised: int8 at row*row_stride + head*head_stride + d, the row's fp16 scale
+ * f16(amax / 127) at row*sc_row_stride + head*sc_head_stride. */
+int mi_attn_prep_kv8(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
+                     const mi_attn_shape* shape, const float* q_norm, const float* k_norm,
+                     const float* rope, float* attn_q, float* attn_gate, int8_t* kv_k,
+                     int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale, size_t row_stride,
+                     size_t head_stride, size_t sc_row_stride, size_t sc_head_stride,
+                     const uint32_t* pages, uint32_t page, uint32_t kv_len, void* stream);
 /* Positions per attention block for a row attending to `len` keys (attn_v2.cl:138-142). */
 uint32_t mi_attn_ppw(uint32_t len, uint32_t tgt);
 /* attn_decode_v2 (attn_v2.cl:172-188) / attn_decode_v2_kv8 (kv8.cl:535-548): grid
@@ -186,6 +197,12 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
 int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate,
                    uint16_t* attn_out, uint32_t M, uint32_t tgt, uint32_t kv_len,
                    const mi_attn_shape* shape, void* stream);
+
+/* attn_reduce_v2_kv8 (kv8.cl:814-821): mi_attn_reduce's merge over partials of the rotated
+ * int8 cache, the head's output un-rotated (FWHT(s * o) / 16) before the gate; head_dim 256. */
+int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float* attn_gate,
+                       uint16_t* attn_out, uint32_t M, uint32_t tgt, uint32_t kv_len,
+                       const mi_attn_shape* shape, void* stream);
 
 /* ---- the token boundary ---- */
 /* embed_gather (embed_gather.cl:47-49): resid[m] = embed[cur_token[m]]; an id >= vocab

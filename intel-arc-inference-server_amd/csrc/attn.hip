@@ -322,6 +322,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
 // and each block's factor exp(mx_b - M); phase 2 sums acc_b * factor_b in ascending b with
 // all the loads independent of each other. Mathematically the reference's sequential
 // rescaling merge; the roundings differ at the last place only.
+// ROT (attn_reduce_v2_kv8, kv8.cl:814-860; head_dim 256): the merged output is in the int8
+// cache's rotated basis and is un-rotated per head before the gate.
+template <bool ROT>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __restrict__ ctrl,
                                                           const float* __restrict__ attn_part,
                                                           const float* __restrict__ attn_gate,
@@ -375,7 +378,13 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
     for (uint32_t u = 0; u < 8; ++u)
       if (b + u < nb) acc = __builtin_fmaf(v[u], fac[b + u], acc);
   }
-  const float o = acc / s_sm;
+  float o = acc / s_sm;
+  if constexpr (ROT) {
+    __shared__ float xch[256];
+    float v1[1] = {kv8_flip(o, kv8_sign_neg(d))};
+    fwht256<1>(v1, d, xch);
+    o = v1[0] * 0.0625f;
+  }
   uint16_t r;
   if (gated && attn_gate)
     r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
@@ -461,9 +470,20 @@ int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* at
     return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
-  attn_reduce_kernel<<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
+  attn_reduce_kernel<false><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
       ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
+}
+
+int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float* attn_gate, uint16_t* attn_out,
+                       uint32_t M, uint32_t tgt, uint32_t kv_len, const mi_attn_shape* shape, void* stream) {
+  if (!ctrl || !attn_part || !attn_out || !shape || M == 0 || tgt == 0 || tgt > 1024)
+    return mi_fail(MI_ERR_ARG, "attn_reduce_kv8: bad arguments (tgt <= 1024)");
+  if (shape->head_dim != 256)
+    return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: the rotation is defined for head_dim 256 only");
+  attn_reduce_kernel<true><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
+      ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
+  return mi_hip((int)hipGetLastError(), "attn_reduce_kv8");
 }
 
 }  // extern "C"

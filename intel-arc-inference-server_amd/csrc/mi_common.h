@@ -122,6 +122,65 @@ __device__ __forceinline__ void lds_barrier() {
 // and keeps the compiler from moving memory operations across the wait.
 __device__ __forceinline__ void wait_memory() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---- the int8 KV cache's rotation and quantiser (src/common/kv8.h:1-26, :56-156) ----
+// R = H_256 diag(s) / 16 with Sylvester H in natural order and s the fixed sign vector (bit j
+// of word j / 32 set when s[j] = -1); rotate(x)[j] = s[j] FWHT(x)[j] / 16, unrotate(y)[i] =
+// FWHT(s * y)[i] / 16. The FWHT's stages run h = 1, 2, ..., 128, the pair (i, i + h) with
+// i & h == 0 becoming (a + c, a - c): each element's chain of fp32 operations is fixed, so any
+// schedule that performs the same operations gives the same bits.
+__device__ __forceinline__ bool kv8_sign_neg(uint32_t j) {
+  constexpr uint32_t kSigns[8] = {0xA197D809u, 0xA6850592u, 0xB205A73Eu, 0x20AFA769u,
+                                  0x45C2CF64u, 0xBEAEAACBu, 0x75F39ADDu, 0x2385A70Cu};
+  uint32_t w = kSigns[0];
+#pragma unroll
+  for (uint32_t k = 1; k < 8; ++k) w = (j >> 5) == k ? kSigns[k] : w;  // no memory lookup
+  return (w >> (j & 31u)) & 1u;
+}
+__device__ __forceinline__ float kv8_flip(float v, bool neg) {
+  return __uint_as_float(__float_as_uint(v) ^ (neg ? 0x80000000u : 0u));
+}
+// N independent 256-point FWHTs across a 256-thread work-group, thread i holding element i of
+// each. Stages 1..32 stay inside the wave (lane exchanges); stages 64 and 128 take one LDS
+// round: every thread reads the four elements i & 63 + 64 k and performs the two stages'
+// operations on them in the same form (a + c for the lower index, a - c for the upper).
+// Every thread of the work-group must call it; `xch` is N * 256 floats of LDS, free on entry
+// and on return.
+template <int N>
+__device__ __forceinline__ void fwht256(float (&v)[N], uint32_t i, float* xch) {
+#pragma unroll
+  for (uint32_t h = 1; h < 64; h <<= 1)
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const float o = __shfl_xor(v[n], (int)h, 64);
+      v[n] = (i & h) ? (o - v[n]) : (v[n] + o);
+    }
+#pragma unroll
+  for (int n = 0; n < N; ++n) xch[n * 256 + i] = v[n];
+  lds_barrier();
+  const uint32_t lo = i & 63u, q = i >> 6;
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    const float a0 = xch[n * 256 + lo], a1 = xch[n * 256 + lo + 64];
+    const float a2 = xch[n * 256 + lo + 128], a3 = xch[n * 256 + lo + 192];
+    // stage 64: elements lo, lo+64 from (a0, a1); lo+128, lo+192 from (a2, a3)
+    const float w_lo = (q & 1u) ? (a0 - a1) : (a0 + a1);    // this thread's slot within its pair
+    const float w_hi = (q & 1u) ? (a2 - a3) : (a2 + a3);
+    // stage 128: the lower half adds its partner 128 up, the upper half subtracts itself
+    v[n] = (q & 2u) ? (w_lo - w_hi) : (w_lo + w_hi);
+  }
+  lds_barrier();
+}
+// binary16 round-to-nearest-even of a non-negative finite scale, subnormals kept, values at or
+// above 65504 saturated (kv8.h:56-72's f32_to_f16_rne)
+__device__ __forceinline__ uint16_t kv8_f16_sat(float f) { return f2h(fminf(f, 65504.0f)); }
+// kv8.h:103-114: the row's amax (exact in any order), s16 = f16(amax / 127) correctly
+// rounded, q = s16 == 0 ? 0 : clamp(rint(y / f16f(s16)), -127, 127). `amax` is the row's max.
+__device__ __forceinline__ int8_t kv8_quant(float y, float sf) {
+  float r = sf == 0.0f ? 0.0f : rintf(y / sf);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int8_t)(int)r;
+}
+
 // Launch helper: returns the launch error as an int.
 #define MI_LAUNCH_CHECK() return (int)hipGetLastError()
 

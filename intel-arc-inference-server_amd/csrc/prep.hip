@@ -166,13 +166,21 @@ struct AttnPrepArgs {
   uint32_t page, S, M, q_heads, kv_heads, head_dim, rot_dim, gated, qkv_n, k_off, v_off;
   uint32_t kv_len;  // positions the cache (or page table) holds; 0 = unchecked
   float eps;
+  // int8 cache (attn_prep_kv8): rows of int8 at kv_k / kv_v's element offsets, fp16 scales
+  // at row * sc_row_stride + head * sc_head_stride
+  uint16_t* k_scale;
+  uint16_t* v_scale;
+  size_t sc_row_stride, sc_head_stride;
 };
 
 __device__ __forceinline__ size_t kv_row(uint32_t p, const uint32_t* pages, uint32_t page) {
   return pages ? (size_t)pages[p / page] * page + p % page : (size_t)p;
 }
 
-// grid (q_heads + kv_heads, M), HD lanes.
+// grid (q_heads + kv_heads, M), HD lanes. KV8 (attn_prep_kv8, kv8.cl:287-408; head_dim 256):
+// the same chain, then q rotated in fp32, and the K row as the f16 cache would hold it and
+// the V row rotated and quantised into the int8 cache.
+template <bool KV8>
 __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   __shared__ float red[256];
   __shared__ float nrm[256];
@@ -242,12 +250,45 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   } else {
     outv = nv;
   }
-  if (is_q) {
-    a.attn_q[((size_t)m * a.q_heads + h) * HD + i] = outv;
-    if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(vg));
+  if constexpr (KV8) {
+    __shared__ float xch[2 * 256];
+    __shared__ float s_am[2][4];
+    const bool neg = kv8_sign_neg(i);
+    if (is_q) {  // uniform: every thread of the work-group reaches the barriers inside
+      float v1[1] = {outv};
+      fwht256<1>(v1, i, xch);
+      a.attn_q[((size_t)m * a.q_heads + h) * HD + i] = kv8_flip(v1[0], neg) * 0.0625f;
+      if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(vg));
+    } else {
+      float v2[2] = {h2f(f2h(outv)), h2f(f2h(vg))};
+      fwht256<2>(v2, i, xch);
+      const float yk = kv8_flip(v2[0], neg) * 0.0625f, yv = kv8_flip(v2[1], neg) * 0.0625f;
+      const float mk = wave_max(fabsf(yk)), mv = wave_max(fabsf(yv));
+      if ((i & 63u) == 0) {
+        s_am[0][i >> 6] = mk;
+        s_am[1][i >> 6] = mv;
+      }
+      lds_barrier();
+      const float ak = fmaxf(fmaxf(s_am[0][0], s_am[0][1]), fmaxf(s_am[0][2], s_am[0][3]));
+      const float av = fmaxf(fmaxf(s_am[1][0], s_am[1][1]), fmaxf(s_am[1][2], s_am[1][3]));
+      const uint16_t sk = kv8_f16_sat(ak / 127.0f), sv = kv8_f16_sat(av / 127.0f);
+      int8_t* k8 = reinterpret_cast<int8_t*>(a.kv_k);
+      int8_t* v8 = reinterpret_cast<int8_t*>(a.kv_v);
+      k8[row * a.row_stride + h * a.head_stride + i] = kv8_quant(yk, h2f(sk));
+      v8[row * a.row_stride + h * a.head_stride + i] = kv8_quant(yv, h2f(sv));
+      if (i == 0) {
+        a.k_scale[row * a.sc_row_stride + h * a.sc_head_stride] = sk;
+        a.v_scale[row * a.sc_row_stride + h * a.sc_head_stride] = sv;
+      }
+    }
   } else {
-    a.kv_k[row * a.row_stride + h * a.head_stride + i] = f2h(outv);
-    a.kv_v[row * a.row_stride + h * a.head_stride + i] = f2h(vg);
+    if (is_q) {
+      a.attn_q[((size_t)m * a.q_heads + h) * HD + i] = outv;
+      if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(vg));
+    } else {
+      a.kv_k[row * a.row_stride + h * a.head_stride + i] = f2h(outv);
+      a.kv_v[row * a.row_stride + h * a.head_stride + i] = f2h(vg);
+    }
   }
 }
 
@@ -477,9 +518,35 @@ int mi_attn_prep(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
     return mi_fail(MI_ERR_SHAPE, "attn_prep: a KV page holds a multiple of 16 positions");
   AttnPrepArgs a{ctrl, partials, q_norm, k_norm, rope, attn_q, attn_gate, kv_k, kv_v, pages, row_stride,
                  head_stride, page, S, M, shape->q_heads, shape->kv_heads, HD, shape->rot_dim,
-                 shape->gated, shape->qkv_n, shape->k_off, shape->v_off, kv_len, shape->eps};
-  attn_prep_kernel<<<dim3(shape->q_heads + shape->kv_heads, M), HD, 0, (hipStream_t)stream>>>(a);
+                 shape->gated, shape->qkv_n, shape->k_off, shape->v_off, kv_len, shape->eps,
+                 nullptr, nullptr, 0, 0};
+  attn_prep_kernel<false><<<dim3(shape->q_heads + shape->kv_heads, M), HD, 0, (hipStream_t)stream>>>(a);
   return mi_hip((int)hipGetLastError(), "attn_prep");
+}
+
+int mi_attn_prep_kv8(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
+                     const mi_attn_shape* shape, const float* q_norm, const float* k_norm, const float* rope,
+                     float* attn_q, float* attn_gate, int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale,
+                     uint16_t* v_scale, size_t row_stride, size_t head_stride, size_t sc_row_stride,
+                     size_t sc_head_stride, const uint32_t* pages, uint32_t page, uint32_t kv_len,
+                     void* stream) {
+  if (!ctrl || !partials || !shape || !rope || !attn_q || !kv_k || !kv_v || !k_scale || !v_scale || S == 0 ||
+      M == 0)
+    return mi_fail(MI_ERR_ARG, "attn_prep_kv8: bad arguments");
+  if (shape->head_dim != 256)
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_kv8: the rotation is defined for head_dim 256 only");
+  if (shape->rot_dim > 256 || shape->rot_dim % 2 || shape->q_heads == 0 || shape->kv_heads == 0 ||
+      shape->q_heads % shape->kv_heads)
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_kv8: inconsistent heads / rotary dims");
+  if (pages && (page == 0 || page % 16))
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_kv8: a KV page holds a multiple of 16 positions");
+  AttnPrepArgs a{ctrl, partials, q_norm, k_norm, rope, attn_q, attn_gate,
+                 reinterpret_cast<uint16_t*>(kv_k), reinterpret_cast<uint16_t*>(kv_v), pages, row_stride,
+                 head_stride, page, S, M, shape->q_heads, shape->kv_heads, 256, shape->rot_dim,
+                 shape->gated, shape->qkv_n, shape->k_off, shape->v_off, kv_len, shape->eps,
+                 k_scale, v_scale, sc_row_stride, sc_head_stride};
+  attn_prep_kernel<true><<<dim3(shape->q_heads + shape->kv_heads, M), 256, 0, (hipStream_t)stream>>>(a);
+  return mi_hip((int)hipGetLastError(), "attn_prep_kv8");
 }
 
 int mi_embed_gather(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, uint32_t M, uint32_t hidden,

@@ -61,6 +61,9 @@ def lib():
             "orc_kv8_rotate256": (None, [vp, vp]), "orc_kv8_unrotate256": (None, [vp, vp]),
             "orc_kv8_quantise": (u16, [vp, vp, u32]), "orc_kv8_encode256": (u16, [vp, vp]),
             "orc_kv8_dequant": (f32, [C.c_int8, u16]),
+            "orc_attn_prep_kv8": (None, [i32, vp, u32, u32, u32, vp, u32, vp, vp, vp, vp, vp, vp,
+                                         vp, vp, vp, sz, sz, sz, sz, vp, u32]),
+            "orc_attn_reduce_v2_kv8": (None, [i32, vp, u32, u32, u32, u32, vp, vp, vp]),
             "orc_embed_gather": (i32, [vp, u32, vp, u32, u32, vp]),
             "orc_argmax": (u32, [vp, u32, u32]),
             "orc_accept_greedy": (u32, [vp, vp, u32, vp]),
@@ -112,6 +115,8 @@ def ref():
             "ref_attn_reduce": (None, [u32, u32, u32, u32, vp, vp, vp]),
             "ref_kv8_rotate": (None, [vp, vp]), "ref_kv8_unrotate": (None, [vp, vp]),
             "ref_kv8_encode": (u16, [vp, vp]), "ref_kv8_dequant": (f32, [C.c_int8, u16]),
+            "ref_kv8_prep": (None, [u32, u32, u32, vp, vp, vp, u32, vp, vp, vp, vp, vp, vp]),
+            "ref_kv8_attend": (None, [vp, u32, vp, vp, vp, vp, u32, u32, vp, vp]),
             "ref_moe_route": (None, [vp, u32, u32, u32, u32, u32, vp]),
             "ref_moe_split_dot": (f32, [vp, u32, u32, vp, u32]),
             "ref_moe_silu_up": (u16, [f32, f32]),

@@ -717,6 +717,80 @@ uint16_t orc_kv8_encode256(const float* x, int8_t* q) {
 }
 float orc_kv8_dequant(int8_t q, uint16_t s16) { return float(q) * orc_f16_to_f32(s16); }
 
+// attn_prep_kv8 (src/kernels/kv8.cl:287-408): attn_prep's chain unchanged, then q rotated
+// in fp32, and the K row as the 16-bit cache would store it (rne of the roped value) and
+// the V row (rne of the folded v) rotated and quantised into the int8 cache. head_dim 256.
+void orc_attn_prep_kv8(int act, const orc_attn_shape* sh, uint32_t pos, uint32_t n_act,
+                       uint32_t M, const float* partials, uint32_t S, const float* q_norm,
+                       const float* k_norm, const float* rope, float* attn_q, float* attn_gate,
+                       int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
+                       size_t rs, size_t hs, size_t srs, size_t shs, const uint32_t* pages,
+                       uint32_t page) {
+  const Act A{act};
+  const uint32_t HD = sh->head_dim, QH = sh->q_heads, KVH = sh->kv_heads;
+  if (HD != 256) return;
+  // the 16-bit values the fp16 cache would hold, at rows pos .. pos + n_act - 1
+  const size_t rows = size_t(pos) + n_act;
+  std::vector<uint16_t> k16(rows * KVH * HD), v16(rows * KVH * HD);
+  orc_attn_prep(act, sh, pos, n_act, M, partials, S, q_norm, k_norm, rope, attn_q, attn_gate, k16.data(),
+                v16.data(), size_t(KVH) * HD, HD, nullptr, 0);
+  float x[256], y[256];
+  for (uint32_t m = 0; m < n_act; ++m) {
+    for (uint32_t h = 0; h < QH; ++h) {
+      float* q = attn_q + (size_t(m) * QH + h) * HD;
+      orc_kv8_rotate256(q, y);
+      std::memcpy(q, y, sizeof y);
+    }
+    const size_t row = kv_row(pos + m, pages, page);
+    for (uint32_t h = 0; h < KVH; ++h) {
+      const size_t src = (size_t(pos + m) * KVH + h) * HD;
+      for (uint32_t i = 0; i < HD; ++i) x[i] = A.w(k16[src + i]);
+      k_scale[row * srs + h * shs] = orc_kv8_encode256(x, kv_k + row * rs + h * hs);
+      for (uint32_t i = 0; i < HD; ++i) x[i] = A.w(v16[src + i]);
+      v_scale[row * srs + h * shs] = orc_kv8_encode256(x, kv_v + row * rs + h * hs);
+    }
+  }
+}
+
+// attn_reduce_v2_kv8 (src/kernels/kv8.cl:814-860): attn_reduce_v2's merge, then the head's
+// output un-rotated before the gate (or the plain rounding when ungated). head_dim 256.
+void orc_attn_reduce_v2_kv8(int act, const orc_attn_shape* sh, uint32_t pos, uint32_t n_act,
+                            uint32_t M, uint32_t tgt, const float* attn_part, const float* attn_gate,
+                            uint16_t* attn_out) {
+  const Act A{act};
+  const uint32_t HD = sh->head_dim, QH = sh->q_heads, PART = HD + 2, OUT_N = QH * HD;
+  if (HD != 256) return;
+  float o[256], x[256];
+  for (uint32_t h = 0; h < QH; ++h)
+    for (uint32_t m = 0; m < n_act; ++m) {
+      uint32_t nb = (pos + m) / orc_v2_ppw(pos + m + 1, tgt) + 1;
+      if (nb > tgt) nb = tgt;
+      for (uint32_t d = 0; d < HD; ++d) {
+        float mx = ninf(), sm = 0.f, acc = 0.f;
+        for (uint32_t b = 0; b < nb; ++b) {
+          const float* p = attn_part + ((size_t(h) * tgt + b) * M + m) * PART;
+          const float bmx = p[0], bsm = p[1], bacc = p[2 + d];
+          const float nmx = std::fmax(mx, bmx);
+          const float a = std::exp(mx - nmx);
+          const float bs = std::exp(bmx - nmx);
+          sm = std::fma(sm, a, bsm * bs);
+          acc = std::fma(acc, a, bacc * bs);
+          mx = nmx;
+        }
+        o[d] = acc / sm;
+      }
+      orc_kv8_unrotate256(o, x);
+      for (uint32_t d = 0; d < HD; ++d) {
+        uint16_t r;
+        if (sh->gated && attn_gate)
+          r = A.rne(A.w(A.rne(x[d])) * sigmoid_f32(attn_gate[(size_t(m) * QH + h) * HD + d]));
+        else
+          r = A.rne(x[d]);
+        attn_out[size_t(m) * OUT_N + size_t(h) * HD + d] = r;
+      }
+    }
+}
+
 // ---- token boundary -----------------------------------------------------------------------
 // src/kernels/embed_gather.cl:47-69: returns 0xDEAD0001 (and writes nothing) on a bad id
 int orc_embed_gather(const uint32_t* ids, uint32_t M, const uint16_t* embed, uint32_t vocab,

@@ -112,6 +112,18 @@ void orc_kv8_unrotate256(const float* y, float* out);
 uint16_t orc_kv8_quantise(const float* y, int8_t* q, uint32_t n);
 uint16_t orc_kv8_encode256(const float* x, int8_t* q);
 float orc_kv8_dequant(int8_t q, uint16_t s16);
+/* attn_prep_kv8 (kv8.cl:287-408): orc_attn_prep's chain, q rotated (fp32), K = rne(roped k)
+ * and V = rne(v) rotated and quantised: int8 at row*rs + h*hs, fp16 scale at row*srs + h*shs */
+void orc_attn_prep_kv8(int act, const orc_attn_shape* sh, uint32_t pos, uint32_t n_act,
+                       uint32_t M, const float* partials, uint32_t S, const float* q_norm,
+                       const float* k_norm, const float* rope, float* attn_q, float* attn_gate,
+                       int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
+                       size_t rs, size_t hs, size_t srs, size_t shs, const uint32_t* pages,
+                       uint32_t page);
+/* attn_reduce_v2_kv8 (kv8.cl:814-860): the merge, un-rotation per head, then the gate */
+void orc_attn_reduce_v2_kv8(int act, const orc_attn_shape* sh, uint32_t pos, uint32_t n_act,
+                            uint32_t M, uint32_t tgt, const float* attn_part,
+                            const float* attn_gate, uint16_t* attn_out);
 
 /* ---- token boundary (src/kernels/embed_gather.cl:47-69, argmax.cl:63-172,
  *      src/server/spec_accept.cc:81-85) ---- */

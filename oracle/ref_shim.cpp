@@ -117,6 +117,34 @@ void ref_kv8_unrotate(const float* y, float* out) { common::kv8::unrotate(y, out
 uint16_t ref_kv8_encode(const float* x, int8_t* q) { return common::kv8::encode(x, q); }
 float ref_kv8_dequant(int8_t q, uint16_t s) { return common::kv8::dequant(q, s); }
 
+// kv8_ref::prep (attn_prep_kv8's twin, 24/4 heads of 256, bf16): the int8 cache
+// [max_len][4][256] with scales [max_len][4] copied out of its host Cache.
+void ref_kv8_prep(uint32_t pos, uint32_t n_act, uint32_t M, const float* partials, const float* fa_small,
+                  const float* rope, uint32_t max_len, float* attn_q, float* attn_gate, int8_t* k, int8_t* v,
+                  uint16_t* ks, uint16_t* vs) {
+  kv8_ref::Cache c(max_len);
+  std::memcpy(c.k.data(), k, c.k.size());
+  std::memcpy(c.v.data(), v, c.v.size());
+  std::memcpy(c.ks.data(), ks, c.ks.size() * 2);
+  std::memcpy(c.vs.data(), vs, c.vs.size() * 2);
+  kv8_ref::prep(pos, n_act, M, partials, fa_small, rope, max_len, attn_q, nullptr, attn_gate, c);
+  std::memcpy(k, c.k.data(), c.k.size());
+  std::memcpy(v, c.v.data(), c.v.size());
+  std::memcpy(ks, c.ks.data(), c.ks.size() * 2);
+  std::memcpy(vs, c.vs.data(), c.vs.size() * 2);
+}
+// kv8_ref::attend: the fp64 reader of one (q head, query) over keys [0, n) of kv head j,
+// un-rotated (o) and rotated (o_rot) outputs.
+void ref_kv8_attend(const float* q_rot, uint32_t max_len, const int8_t* k, const int8_t* v, const uint16_t* ks,
+                    const uint16_t* vs, uint32_t j, uint32_t n, double* o, double* o_rot) {
+  kv8_ref::Cache c(max_len);
+  std::memcpy(c.k.data(), k, c.k.size());
+  std::memcpy(c.v.data(), v, c.v.size());
+  std::memcpy(c.ks.data(), ks, c.ks.size() * 2);
+  std::memcpy(c.vs.data(), vs, c.vs.size() * 2);
+  kv8_ref::attend(q_rot, c, j, n, o, o_rot);
+}
+
 struct RefRoute {
   uint32_t ids[8];
   float w[8];

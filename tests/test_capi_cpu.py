@@ -59,3 +59,17 @@ def test_moe_argument_errors_without_a_gpu():
     assert L.mi_moe_down(8, 8, 8, 8, 1, 256, 8, 2048, 2048, None) == -2    # inter > 1024
     assert L.mi_gemv_f16w(8, 16, 8, 1, 2048, 272, 3, None) == -2           # ksplit not 2^n
     assert b"ksplit" in L.mi_last_error()
+
+
+def test_kv8_argument_errors_without_a_gpu():
+    """The int8 writer and the rotated reduce are defined for head_dim 256 only
+    (src/common/kv8.h kHeadDim); the checks run before any launch."""
+    L = mi.lib()
+    sh = mi.AttnShape(40, 8, 128, 128, 0, 7168, 5120, 6144, 0.08838835, 1e-6)
+    assert L.mi_attn_reduce_kv8(8, 8, None, 8, 1, 8, 0, C.byref(sh), None) == -2
+    assert b"head_dim 256" in L.mi_last_error()
+    assert L.mi_attn_prep_kv8(8, 8, 1, 1, C.byref(sh), None, None, 8, 8, None, 8, 8, 8, 8, 128, 128, 1, 1,
+                              None, 0, 0, None) == -2
+    sh.head_dim = 256
+    assert L.mi_attn_prep_kv8(8, 8, 1, 1, C.byref(sh), None, None, 8, 8, None, 8, 8, None, 8, 256, 256, 1, 1,
+                              None, 0, 0, None) == -1   # no k_scale

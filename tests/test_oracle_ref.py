@@ -185,6 +185,89 @@ def test_kv8_bitwise():
         assert np.array_equal(q1, q2)
 
 
+def _kv8_prep_case(pos, n_act, M, max_len, seed):
+    sh = _qwen_shape()
+    rng = np.random.default_rng(seed)
+    part = np.ascontiguousarray(rng.standard_normal((2, M, sh.qkv_n)).astype(np.float32))
+    fa_small = np.ascontiguousarray((1 + 0.05 * rng.standard_normal(512)).astype(np.float32))
+    rope = O.rope_table(1e7, ROT, max_len)
+    return sh, part, fa_small, rope
+
+
+@pytest.mark.parametrize("pos,n_act,paged", [(41, 2, False), (0, 1, False), (100, 3, True)])
+def test_attn_prep_kv8_bitwise(pos, n_act, paged):
+    """orc_attn_prep_kv8 (bf16, Qwen3.8's shape) against kv8_ref::prep: q rotated, K/V int8
+    and scales bit for bit; a page table moves only the rows."""
+    M, max_len = 3, 256
+    sh, part, fa_small, rope = _kv8_prep_case(pos, n_act, M, max_len, 30 + pos)
+    rng = np.random.default_rng(pos)
+    k0 = rng.integers(-127, 128, (max_len, KVH, HD), dtype=np.int8)
+    v0 = rng.integers(-127, 128, (max_len, KVH, HD), dtype=np.int8)
+    ks0 = rng.integers(0, 0x3C00, (max_len, KVH), dtype=np.uint16)
+    vs0 = rng.integers(0, 0x3C00, (max_len, KVH), dtype=np.uint16)
+    pages = rng.permutation(max_len // 64).astype(np.uint32) if paged else None
+    aq1 = np.zeros((M, QH, HD), np.float32); aq2 = np.zeros_like(aq1)
+    g1 = np.zeros_like(aq1); g2 = np.zeros_like(aq1)
+    rows = np.arange(max_len)
+    if paged:  # logical position p of the reference's contiguous cache sits at the paged row
+        rows = pages[rows // 64] * 64 + rows % 64
+    k1, v1, ks1, vs1 = (np.empty_like(a) for a in (k0, v0, ks0, vs0))
+    k1[rows], v1[rows], ks1[rows], vs1[rows] = k0, v0, ks0, vs0
+    k2, v2, ks2, vs2 = k0.copy(), v0.copy(), ks0.copy(), vs0.copy()
+    L().orc_attn_prep_kv8(BF, C.byref(sh), pos, n_act, M, P(part), 2, P(fa_small), P(fa_small[256:].copy()),
+                          P(rope), P(aq1), P(g1), P(k1), P(v1), P(ks1), P(vs1), KVH * HD, HD, KVH, 1,
+                          P(pages) if paged else None, 64 if paged else 0)
+    R.ref_kv8_prep(pos, n_act, M, P(part), P(fa_small), P(rope), max_len, P(aq2), P(g2), P(k2), P(v2), P(ks2),
+                   P(vs2))
+    assert np.array_equal(bits(aq1[:n_act]), bits(aq2[:n_act]))
+    assert np.array_equal(bits(g1[:n_act]), bits(g2[:n_act]))
+    assert np.array_equal(k1[rows], k2) and np.array_equal(v1[rows], v2)
+    assert np.array_equal(ks1[rows], ks2) and np.array_equal(vs1[rows], vs2)
+    written = np.arange(pos, pos + n_act)
+    assert not np.array_equal(k2[written], k0[written])  # the rows were rewritten
+
+
+def test_attn_reduce_kv8_vs_reference_fp64_reader():
+    """The rotated pair (orc_attn_decode_v2 on the int8 cache + orc_attn_reduce_v2_kv8)
+    against kv8_ref::attend's fp64 reader with its fp64 un-rotation and the gated chain:
+    cosine >= 0.99999 and within 2e-3 relative per head (the reference's reader bar)."""
+    sh = _qwen_shape()
+    M, max_len, pos, n_act = 1, 512, 300, 1
+    tgt = 8
+    rng = np.random.default_rng(5)
+    q = np.ascontiguousarray(rng.standard_normal((M, QH, HD)).astype(np.float32))
+    k = np.zeros((max_len, KVH, HD), np.int8); v = np.zeros_like(k)
+    ks = np.zeros((max_len, KVH), np.uint16); vs = np.zeros_like(ks)
+    for p in range(pos + 1):
+        for j in range(KVH):
+            x = O.bf16_bits_to_f32(O.f32_to_bf16_bits(rng.standard_normal(HD).astype(np.float32)))
+            ks[p, j] = L().orc_kv8_encode256(P(np.ascontiguousarray(x)), P(k[p, j]))
+            x = O.bf16_bits_to_f32(O.f32_to_bf16_bits(rng.standard_normal(HD).astype(np.float32)))
+            vs[p, j] = L().orc_kv8_encode256(P(np.ascontiguousarray(x)), P(v[p, j]))
+    gate = np.ascontiguousarray(rng.standard_normal((M, QH, HD)).astype(np.float32))
+    part = np.zeros((QH, tgt, M, HD + 2), np.float32)
+    L().orc_attn_decode_v2(BF, C.byref(sh), pos, n_act, M, tgt, P(q), 1, P(k), P(v), P(ks), P(vs),
+                           KVH * HD, HD, KVH, 1, None, 0, P(part))
+    out = np.zeros((M, QH * HD), np.uint16)
+    L().orc_attn_reduce_v2_kv8(BF, C.byref(sh), pos, n_act, M, tgt, P(part), P(gate), P(out))
+    got = O.bf16_bits_to_f32(out[0]).astype(np.float64).reshape(QH, HD)
+    rot = np.zeros((QH, HD))
+    L().orc_attn_reduce_v2(BF, C.byref(sh), pos, n_act, M, tgt, P(part), P(gate), P(out))
+    rot[:] = O.bf16_bits_to_f32(out[0]).reshape(QH, HD)  # the same merge, left rotated
+    o = np.zeros(HD); orot = np.zeros(HD)
+    for h in range(QH):
+        R.ref_kv8_attend(P(np.ascontiguousarray(q[0, h])), max_len, P(k), P(v), P(ks), P(vs), h // (QH // KVH),
+                         pos + 1, P(o), P(orot))
+        ob = O.bf16_bits_to_f32(O.f32_to_bf16_bits(o.astype(np.float32)))
+        sg = np.float32(1) / (np.float32(1) + np.exp(-gate[0, h]))
+        want = O.bf16_bits_to_f32(O.f32_to_bf16_bits((ob * sg).astype(np.float32))).astype(np.float64)
+        cos = got[h] @ want / np.sqrt((got[h] @ got[h]) * (want @ want))
+        assert cos >= 0.99999, (h, cos)
+        assert np.max(np.abs(got[h] - want)) <= 2e-3 * np.max(np.abs(want)) + 1e-6, h
+        # without the un-rotation the same partials miss the answer by far
+        assert np.max(np.abs(rot[h] - want)) > 0.1 * np.max(np.abs(want)), h
+
+
 class RefRoute(C.Structure):
     _fields_ = O.MoeRoute._fields_
 
