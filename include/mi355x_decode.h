@@ -280,6 +280,10 @@ typedef struct mi_model_desc {
    * expert, expert intermediate moe_inter; the router || shared gate is an fp16 linear of
    * roundup16(experts + 1) rows. `inter` is then unused. */
   uint32_t experts, top_k, moe_inter;
+  /* 1: the int8 KV cache with the Hadamard rotation (kv8.cl under --kv-cache int8;
+   * head_dim 256): int8 rows [layers][kv_heads][max_len][head_dim] and fp16 scales
+   * [layers][kv_heads][max_len]; the step runs attn_prep_kv8 and the rotated reader pair. */
+  uint32_t kv_int8;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;
@@ -290,13 +294,15 @@ enum {
   MI_T_IN_NORM, MI_T_POST_NORM, MI_T_Q_NORM, MI_T_K_NORM,
   MI_T_ROUTER, MI_T_MOE_GU, MI_T_MOE_DN, /* MoE layers: router tiles, expert blocks */
   MI_T_EMBED = 32, MI_T_FINAL_NORM, MI_T_LM_Q, MI_T_LM_S, MI_T_ROPE, MI_T_KV_K, MI_T_KV_V,
-  MI_T_LOGITS, MI_T_CTRL, MI_T_HISTORY
+  MI_T_LOGITS, MI_T_CTRL, MI_T_HISTORY,
+  MI_T_KV_KS, MI_T_KV_VS /* the int8 cache's fp16 row scales (kv_int8) */
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's
  * distributions: uniform nibbles, scales U(0.002, 0.02), gammas N(1, 0.02) in fp16, embed
- * and KV N(0, 1)), the KV cache [layers][kv_heads][max_len][head_dim] f16 and all step
- * buffers. stream NULL: the engine owns a stream. Returns NULL on failure (mi_last_error). */
+ * and KV N(0, 1); an int8 cache holds uniform [-127, 127] with scales U(0.005, 0.05), config
+ * 3's), the KV cache [layers][kv_heads][max_len][head_dim] (f16, or int8 + scales) and all
+ * step buffers. stream NULL: the engine owns a stream. Returns NULL on failure (mi_last_error). */
 mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stream);
 void mi_engine_destroy(mi_engine* e);
 void* mi_engine_stream(mi_engine* e);

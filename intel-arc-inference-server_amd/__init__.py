@@ -103,6 +103,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise MiError(f"{LIB_PATH} is missing: run `python __graft_entry__.py` (build()) first")
+        # One HIP runtime per process: PyTorch ships its own libamdhip64 under the same soname,
+        # and the one loaded first serves both. Loading torch first makes that its runtime, so
+        # torch tensors (device buffers, streams) work whatever this library is called with.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
@@ -146,16 +153,18 @@ class ModelDesc(C.Structure):
                 ("head_dim", u32), ("rot_dim", u32), ("inter", u32), ("vocab", u32),
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
                 ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
-                ("experts", u32), ("top_k", u32), ("moe_inter", u32)]
+                ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
                rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
-               rope_theta=1e6, rms_eps=1e-6):
-    return ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
-                     head_dim if rot_dim is None else rot_dim, inter, vocab,
-                     vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
-                     attn_tgt, rope_theta, rms_eps)
+               rope_theta=1e6, rms_eps=1e-6, kv_int8=0):
+    d = ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
+                  head_dim if rot_dim is None else rot_dim, inter, vocab,
+                  vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
+                  attn_tgt, rope_theta, rms_eps)
+    d.kv_int8 = kv_int8
+    return d
 
 
 def moe_desc(layers, hidden, q_heads, kv_heads, head_dim, experts, top_k, moe_inter, vocab, max_len,
@@ -184,7 +193,7 @@ def desc_27b(max_len=4096 + 512):
 (T_QKV_Q, T_QKV_S, T_O_Q, T_O_S, T_GU_Q, T_GU_S, T_DOWN_Q, T_DOWN_S, T_IN_NORM, T_POST_NORM,
  T_Q_NORM, T_K_NORM, T_ROUTER, T_MOE_GU, T_MOE_DN) = range(15)
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
- T_HISTORY) = range(32, 42)
+ T_HISTORY, T_KV_KS, T_KV_VS) = range(32, 44)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 

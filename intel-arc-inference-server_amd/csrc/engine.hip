@@ -80,8 +80,10 @@ struct mi_engine {
   float* final_norm = nullptr;
   Linear lm_head;
   float* rope = nullptr;
-  uint16_t* kv_k = nullptr;  // [layers][kv_heads][max_len][head_dim]
-  uint16_t* kv_v = nullptr;
+  void* kv_k = nullptr;  // [layers][kv_heads][max_len][head_dim] f16, or int8 (kv_int8)
+  void* kv_v = nullptr;
+  uint16_t* kv_ks = nullptr;  // kv_int8: fp16 row scales [layers][kv_heads][max_len]
+  uint16_t* kv_vs = nullptr;
   // activations / scratch
   uint32_t* ctrl = nullptr;
   uint32_t* history = nullptr;
@@ -183,8 +185,16 @@ struct mi_engine {
     MI_TRY(alloc(&final_norm, H));
     MI_TRY(alloc(&rope, size_t(m.max_len) * m.rot_dim));
     const size_t kv_elems = size_t(m.layers) * KVH * m.max_len * HD;
-    MI_TRY(alloc(&kv_k, kv_elems));
-    MI_TRY(alloc(&kv_v, kv_elems));
+    const size_t kv_rows = size_t(m.layers) * KVH * m.max_len;
+    if (m.kv_int8) {
+      MI_TRY(alloc(reinterpret_cast<int8_t**>(&kv_k), kv_elems));
+      MI_TRY(alloc(reinterpret_cast<int8_t**>(&kv_v), kv_elems));
+      MI_TRY(alloc(&kv_ks, kv_rows));
+      MI_TRY(alloc(&kv_vs, kv_rows));
+    } else {
+      MI_TRY(alloc(reinterpret_cast<uint16_t**>(&kv_k), kv_elems));
+      MI_TRY(alloc(reinterpret_cast<uint16_t**>(&kv_v), kv_elems));
+    }
     MI_TRY(alloc(&ctrl, MI_CTRL_WORDS));
     MI_TRY(alloc(&history, m.max_len));
     MI_TRY(alloc(&ids_dev, 32));
@@ -227,8 +237,15 @@ struct mi_engine {
     MI_TRY(init_linear(lm_head, seed));
     MI_TRY(mi_fill_f16(embed, size_t(m.vocab) * H, seed++, 1, 0.0f, 1.0f, stream));
     MI_TRY(mi_fill_f32(final_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
-    MI_TRY(mi_fill_f16(kv_k, kv_elems, seed++, 1, 0.0f, 1.0f, stream));
-    MI_TRY(mi_fill_f16(kv_v, kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+    if (m.kv_int8) {  // BASELINE config 3's int8 cache: uniform [-127, 127], scales U(0.005, 0.05)
+      MI_TRY(mi_fill_i8(static_cast<int8_t*>(kv_k), kv_elems, seed++, -127, 127, stream));
+      MI_TRY(mi_fill_i8(static_cast<int8_t*>(kv_v), kv_elems, seed++, -127, 127, stream));
+      MI_TRY(mi_fill_f16(kv_ks, kv_rows, seed++, 0, 0.005f, 0.05f, stream));
+      MI_TRY(mi_fill_f16(kv_vs, kv_rows, seed++, 0, 0.005f, 0.05f, stream));
+    } else {
+      MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_k), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+      MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_v), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+    }
     // RoPE table in double, stored fp32 (src/loader/loader.cc:702-716)
     {
       const uint32_t half = m.rot_dim / 2;
@@ -282,13 +299,26 @@ struct mi_engine {
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
       MI_TRY(gemv(L.qkv, x, M));
-      uint16_t* lk = kv_k + li * layer_kv;
-      uint16_t* lv = kv_v + li * layer_kv;
-      MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv, HD,
-                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
-      MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
-                            nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
-      MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+      if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
+        int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
+        int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
+        uint16_t* lks = kv_ks + size_t(li) * KVH * d.max_len;
+        uint16_t* lvs = kv_vs + size_t(li) * KVH * d.max_len;
+        MI_TRY(mi_attn_prep_kv8(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
+                                lks, lvs, HD, size_t(d.max_len) * HD, 1, d.max_len, nullptr, 0, d.max_len,
+                                stream));
+        MI_TRY(mi_attn_decode(ctrl, attn_q, 1, lk, lv, lks, lvs, HD, size_t(d.max_len) * HD, 1, d.max_len,
+                              nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+        MI_TRY(mi_attn_reduce_kv8(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+      } else {
+        uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
+        uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+        MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
+                            HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+        MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
+                              nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+        MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+      }
       const mi_gemv_epilogue eo = resid_epi(L.post_norm);
       MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part, M, L.o.K, L.o.N, L.o.S, &eo, stream));
       const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
@@ -364,7 +394,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
   if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
-      m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 ||
+      m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {
@@ -402,7 +432,8 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
   auto lin_q = [](const Linear& l, void** p, size_t* b) { *p = l.q; if (b) *b = size_t(l.K / 8) * l.N * 4; };
   auto lin_s = [](const Linear& l, void** p, size_t* b) { *p = l.s; if (b) *b = size_t(l.K / 64) * l.N * 2; };
   size_t b = 0;
-  const size_t kvb = size_t(m.layers) * m.kv_heads * m.max_len * m.head_dim * 2;
+  const size_t kvb = size_t(m.layers) * m.kv_heads * m.max_len * m.head_dim * (m.kv_int8 ? 1 : 2);
+  const size_t kvsb = m.kv_int8 ? size_t(m.layers) * m.kv_heads * m.max_len * 2 : 0;
   switch (kind) {
     case MI_T_QKV_Q: lin_q(L->qkv, ptr, &b); break;
     case MI_T_QKV_S: lin_s(L->qkv, ptr, &b); break;
@@ -429,6 +460,8 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_LOGITS: *ptr = e->logits; b = size_t(m.max_rows) * m.vocab * 4; break;
     case MI_T_CTRL: *ptr = e->ctrl; b = MI_CTRL_WORDS * 4; break;
     case MI_T_HISTORY: *ptr = e->history; b = size_t(m.max_len) * 4; break;
+    case MI_T_KV_KS: *ptr = e->kv_ks; b = kvsb; break;
+    case MI_T_KV_VS: *ptr = e->kv_vs; b = kvsb; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;

@@ -74,6 +74,7 @@ def lib():
             "orc_moe_block": (None, [i32, u32, u32, u32, u32, u32, vp, vp, vp, vp, sz, sz, vp,
                                      vp, sz, sz, u32, u32, vp, vp]),
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
+            "orc_dense_step_kv8": (u32, [i32, vp, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
             "orc_threads": (i32, []),

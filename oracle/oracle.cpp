@@ -956,8 +956,11 @@ void orc_f16w_tile(const uint16_t* w_rm, uint32_t K, uint32_t N, uint16_t* wt) {
 }
 
 // ---- dense decode step (src/runtime/capture.cc:997, 1247-1263, 1370-1423, 1461-1480) --------
-uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos,
-                        uint16_t* kv_k, uint16_t* kv_v, float* logits, uint32_t n_layers_run) {
+// k_scale != NULL: the int8 rotated cache (kv8.cl's writer and readers, head_dim 256), int8 rows
+// [layers][kv_heads][max_len][hd] and fp16 scales [layers][kv_heads][max_len]
+static uint32_t dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos, void* kv_k,
+                           void* kv_v, uint16_t* k_scale, uint16_t* v_scale, float* logits,
+                           uint32_t n_layers_run) {
   const Act A{act};
   const uint32_t H = md->hidden, HD = md->attn.head_dim, QH = md->attn.q_heads;
   const uint32_t KVH = md->attn.kv_heads, L = md->max_len;
@@ -989,14 +992,27 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
     const orc_layer& ly = md->layer[li];
     norm(prev.data(), s_prev, ly.in_norm);
     linear(ly.qkv, x.data());
-    uint16_t* lk = kv_k + size_t(li) * KVH * L * HD;
-    uint16_t* lv = kv_v + size_t(li) * KVH * L * HD;
-    orc_attn_prep(act, &md->attn, pos, 1, 1, part.data(), ly.qkv.S, ly.q_norm, ly.k_norm, md->rope,
-                  attn_q.data(), nullptr, lk, lv, HD, size_t(L) * HD, nullptr, 0);
+    const size_t lo = size_t(li) * KVH * L * HD;
     attn_part.assign(size_t(QH) * md->tgt * (HD + 2), 0.f);
-    orc_attn_decode_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_q.data(), 0, lk, lv, nullptr, nullptr,
-                       HD, size_t(L) * HD, 0, 0, nullptr, 0, attn_part.data());
-    orc_attn_reduce_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
+    if (k_scale) {  // capture.cc fa_layer under --kv-cache int8 (kv8.cl KV8_PREP / KV8_DEC)
+      int8_t* lk = static_cast<int8_t*>(kv_k) + lo;
+      int8_t* lv = static_cast<int8_t*>(kv_v) + lo;
+      uint16_t* lks = k_scale + size_t(li) * KVH * L;
+      uint16_t* lvs = v_scale + size_t(li) * KVH * L;
+      orc_attn_prep_kv8(act, &md->attn, pos, 1, 1, part.data(), ly.qkv.S, ly.q_norm, ly.k_norm, md->rope,
+                        attn_q.data(), nullptr, lk, lv, lks, lvs, HD, size_t(L) * HD, 1, L, nullptr, 0);
+      orc_attn_decode_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_q.data(), 1, lk, lv, lks, lvs, HD,
+                         size_t(L) * HD, 1, L, nullptr, 0, attn_part.data());
+      orc_attn_reduce_v2_kv8(act, &md->attn, pos, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
+    } else {
+      uint16_t* lk = static_cast<uint16_t*>(kv_k) + lo;
+      uint16_t* lv = static_cast<uint16_t*>(kv_v) + lo;
+      orc_attn_prep(act, &md->attn, pos, 1, 1, part.data(), ly.qkv.S, ly.q_norm, ly.k_norm, md->rope,
+                    attn_q.data(), nullptr, lk, lv, HD, size_t(L) * HD, nullptr, 0);
+      orc_attn_decode_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_q.data(), 0, lk, lv, nullptr, nullptr,
+                         HD, size_t(L) * HD, 0, 0, nullptr, 0, attn_part.data());
+      orc_attn_reduce_v2(act, &md->attn, pos, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
+    }
     linear(ly.o, attn_out.data());
     norm(part.data(), ly.o.S, ly.post_norm);
     if (md->experts) {
@@ -1027,6 +1043,17 @@ uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32
   orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1,
                 md->lm_head.S, logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);
+}
+
+uint32_t orc_dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos, uint16_t* kv_k,
+                        uint16_t* kv_v, float* logits, uint32_t n_layers_run) {
+  return dense_step(act, md, tok, pos, kv_k, kv_v, nullptr, nullptr, logits, n_layers_run);
+}
+uint32_t orc_dense_step_kv8(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos, int8_t* kv_k,
+                            int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale, float* logits,
+                            uint32_t n_layers_run) {
+  if (md->attn.head_dim != 256 || !k_scale || !v_scale) return 0xFFFFFFFFu;
+  return dense_step(act, md, tok, pos, kv_k, kv_v, k_scale, v_scale, logits, n_layers_run);
 }
 
 }  // extern "C"

@@ -205,6 +205,11 @@ typedef struct orc_dense_model {
  * (this build's layout), updated in place. Writes logits fp32 [vocab] and returns argmax. */
 uint32_t orc_dense_step(int act, const orc_dense_model* m, uint32_t tok, uint32_t pos,
                         uint16_t* kv_k, uint16_t* kv_v, float* logits, uint32_t n_layers_run);
+/* The same step over the int8 rotated cache (head_dim 256): kv_k/kv_v int8
+ * [layers][kv_heads][max_len][hd], k_scale/v_scale fp16 [layers][kv_heads][max_len]. */
+uint32_t orc_dense_step_kv8(int act, const orc_dense_model* m, uint32_t tok, uint32_t pos,
+                            int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
+                            float* logits, uint32_t n_layers_run);
 
 #ifdef __cplusplus
 }

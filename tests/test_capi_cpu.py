@@ -73,3 +73,11 @@ def test_kv8_argument_errors_without_a_gpu():
     sh.head_dim = 256
     assert L.mi_attn_prep_kv8(8, 8, 1, 1, C.byref(sh), None, None, 8, 8, None, 8, 8, None, 8, 256, 256, 1, 1,
                               None, 0, 0, None) == -1   # no k_scale
+
+
+def test_engine_rejects_int8_kv_off_head_dim_256():
+    """The int8 rotated cache needs head_dim 256; the shape check runs before any HIP call."""
+    L = mi.lib()
+    d = mi.dense_desc(2, 512, 8, 2, 128, 1024, 4096, 512, kv_int8=1)
+    assert not L.mi_engine_create(C.byref(d), 1, None)
+    assert b"unsupported model shape" in L.mi_last_error()

@@ -66,8 +66,13 @@ class OracleModel:
         fnorm = self._h(eng.to_host(mi.T_FINAL_NORM, 0, np.float32))
         lmq = self._h(eng.to_host(mi.T_LM_Q, 0, np.uint32))
         lms = self._h(eng.to_host(mi.T_LM_S, 0, np.uint16))
-        self.kv_k = eng.to_host(mi.T_KV_K, 0, np.uint16).copy()
-        self.kv_v = eng.to_host(mi.T_KV_V, 0, np.uint16).copy()
+        self.kv8 = bool(d.kv_int8)
+        kv_t = np.int8 if self.kv8 else np.uint16
+        self.kv_k = eng.to_host(mi.T_KV_K, 0, kv_t).copy()
+        self.kv_v = eng.to_host(mi.T_KV_V, 0, kv_t).copy()
+        if self.kv8:
+            self.kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
+            self.kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
         sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
         self.m = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
                               C.cast(layers, C.c_void_p), embed.ctypes.data, fnorm.ctypes.data,
@@ -85,8 +90,12 @@ class OracleModel:
 
     def step(self, tok, pos):
         logits = np.zeros(self.d.vocab, np.float32)
-        am = O.lib().orc_dense_step(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
-                                    O._p(logits), self.d.layers)
+        if self.kv8:
+            am = O.lib().orc_dense_step_kv8(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
+                                            O._p(self.kv_ks), O._p(self.kv_vs), O._p(logits), self.d.layers)
+        else:
+            am = O.lib().orc_dense_step(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
+                                        O._p(logits), self.d.layers)
         return am, logits
 
 
@@ -225,4 +234,66 @@ def test_ingest_then_generate():
     assert c[mi.CTRL_POS] == 4
     toks = eng.generate(3)
     assert eng.ctrl()[mi.CTRL_POS] == 7 and len(toks) == 3
+    eng.close()
+
+
+@pytest.mark.parametrize("moe", [False, True])
+def test_int8_kv_decode_steps_vs_oracle(moe):
+    """The int8 rotated KV cache in the captured step (attn_prep_kv8, the int8 reader, the
+    rotated reduce; head_dim 256): teacher forced against the oracle's step over the same
+    int8 cache, and the cache rows the steps wrote bitwise the oracle's."""
+    if moe:
+        desc = moe_small_desc(kv_int8=1)
+    else:
+        desc = small_desc(head_dim=256, kv_int8=1)
+    eng = mi.Engine(desc, seed=91)
+    print(f"engine int8 KV moe={moe}", flush=True)
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 200, 5
+    eng.reset(pos, tok)
+    for step in range(3):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert argmax_ok(got_tok, want)
+        tok, pos = got_tok, pos + 1
+    # the cache: rows the steps did not write unchanged; the written rows (from the device
+    # GEMV's qkv, which matches the oracle's within its rounding bound, not bitwise) decode to
+    # the oracle's within a quantisation step
+    d = eng.desc
+    shp = (d.layers, d.kv_heads, d.max_len)
+    written = np.zeros(d.max_len, bool)
+    written[200:pos] = True
+    for k8, ks, r8, rs in ((mi.T_KV_K, mi.T_KV_KS, orc.kv_k, orc.kv_ks), (mi.T_KV_V, mi.T_KV_VS, orc.kv_v,
+                                                                          orc.kv_vs)):
+        g8 = eng.to_host(k8, 0, np.int8).reshape(shp + (256,))
+        gs = eng.to_host(ks, 0, np.uint16).reshape(shp)
+        r8, rs = r8.reshape(shp + (256,)), rs.reshape(shp)
+        assert np.array_equal(g8[:, :, ~written], r8[:, :, ~written])
+        assert np.array_equal(gs[:, :, ~written], rs[:, :, ~written])
+        gd = g8[:, :, written] * O.f16_bits_to_f32(gs[:, :, written])[..., None].astype(np.float64)
+        rd = r8[:, :, written] * O.f16_bits_to_f32(rs[:, :, written])[..., None].astype(np.float64)
+        step_ = O.f16_bits_to_f32(rs[:, :, written]).astype(np.float64)[..., None]
+        assert np.all(np.abs(gd - rd) <= 1.5 * step_ + 1e-6)
+        assert np.mean(g8[:, :, written] == r8[:, :, written]) > 0.5
+    eng.close()
+
+
+def test_int8_kv_verify_rows_bitwise_plain_steps():
+    eng = mi.Engine(small_desc(head_dim=256, kv_int8=1), seed=13)
+    eng.capture(1)
+    P, t0 = 70, 4
+    eng.reset(P, t0)
+    toks, lg = [], []
+    for _ in range(3):
+        toks.append(int(eng.generate(1)[0]))
+        lg.append(eng.logits(1)[0].copy())
+    eng.reset(P, t0)
+    rows = eng.verify(toks[:2])
+    assert list(rows) == toks
+    got = eng.logits(3)
+    for m in range(3):
+        assert np.array_equal(got[m].view(np.uint32), lg[m].view(np.uint32))
     eng.close()

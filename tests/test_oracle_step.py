@@ -77,7 +77,8 @@ class TinyModel:
                                     self.d["layers"])
         return int(am), logits, kk, vv
 
-    def fp64_step(self, tok, pos, mistake=None):
+    def fp64_step(self, tok, pos, mistake=None, cache=None):
+        """cache: the fp64 K and V rows to attend over (default: the model's fp16 cache)"""
         d = self.d
         H, QH, KVH, HD, rot, I = d["H"], d["QH"], d["KVH"], d["HD"], d["rot"], d["I"]
         eps = 1e-6
@@ -97,8 +98,11 @@ class TinyModel:
             return out
 
         resid = O.f16_bits_to_f32(self.embed[tok]).astype(np.float64)
-        kc = O.f16_bits_to_f32(self.kv_k).astype(np.float64)
-        vc = O.f16_bits_to_f32(self.kv_v).astype(np.float64)
+        if cache is None:
+            kc = O.f16_bits_to_f32(self.kv_k).astype(np.float64)
+            vc = O.f16_bits_to_f32(self.kv_v).astype(np.float64)
+        else:
+            kc, vc = cache[0].copy(), cache[1].copy()
         G = QH // KVH
         for li, ws in enumerate(self.w):
             nm = ws["norms"]
@@ -296,4 +300,85 @@ def test_moe_bar_rejects_plausible_mistakes(mistake):
     m = TinyMoe(7)
     _, got, _, _ = m.oracle_step(91, 33)
     want = _fp64_moe_step(m, 91, 33, mistake)
+    assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
+
+
+SIGN_WORDS = [0xA197D809, 0xA6850592, 0xB205A73E, 0x20AFA769, 0x45C2CF64, 0xBEAEAACB, 0x75F39ADD, 0x2385A70C]
+
+
+def unrotate64(y):
+    """R^T in fp64 along the last axis (R = H_256 diag(s) / 16, src/common/kv8.h:1-26)."""
+    from scipy.linalg import hadamard
+    s = np.array([-1.0 if (SIGN_WORDS[j >> 5] >> (j & 31)) & 1 else 1.0 for j in range(256)])
+    return (y * s) @ hadamard(256).astype(np.float64) / 16.0
+
+
+class TinyKv8(TinyModel):
+    """TinyModel with head_dim 256 and the int8 rotated KV cache: rows [0, L) hold the
+    writer's encoding of N(0, 1) fp16 rows."""
+
+    def __init__(self, seed, **kw):
+        super().__init__(seed, H=256, QH=4, KVH=2, HD=256, rot=64, **kw)
+        rng = np.random.default_rng(seed + 77)
+        d = self.d
+        shape = (d["layers"], d["KVH"], d["L"])
+        self.k8 = np.zeros(shape + (256,), np.int8)
+        self.v8 = np.zeros_like(self.k8)
+        self.ks = np.zeros(shape, np.uint16)
+        self.vs = np.zeros_like(self.ks)
+        for idx in np.ndindex(*shape):
+            for c8, cs in ((self.k8, self.ks), (self.v8, self.vs)):
+                x = np.ascontiguousarray(O.f16_bits_to_f32(f16(rng.standard_normal(256))))
+                cs[idx] = O.lib().orc_kv8_encode256(O._p(x), O._p(c8[idx]))
+
+    def oracle_step_kv8(self, tok, pos):
+        k8, v8, ks, vs = self.k8.copy(), self.v8.copy(), self.ks.copy(), self.vs.copy()
+        logits = np.zeros(self.d["V"], np.float32)
+        am = O.lib().orc_dense_step_kv8(F16, C.byref(self.m), tok, pos, O._p(k8), O._p(v8), O._p(ks), O._p(vs),
+                                        O._p(logits), self.d["layers"])
+        return int(am), logits, (k8, v8, ks, vs)
+
+    def dequant(self, c8, cs):
+        return c8.astype(np.float64) * O.f16_bits_to_f32(cs).astype(np.float64)[..., None]
+
+    def fp64_step_kv8(self, tok, pos, mistake=None):
+        """The fp64 forward over the cache in the model's own basis: a cached row's value
+        is the un-rotation of its dequantised int8 row (q.k and sum p v are invariant under
+        the orthogonal R); the current position's K and V are the exact fp64 values."""
+        kd, vd = self.dequant(self.k8, self.ks), self.dequant(self.v8, self.vs)
+        if mistake != "kv8_rotated_basis":
+            kd, vd = unrotate64(kd), unrotate64(vd)
+        return self.fp64_step(tok, pos, cache=(kd, vd))
+
+
+@pytest.mark.parametrize("seed,pos", [(4, 0), (5, 41)])
+def test_kv8_step_vs_independent_fp64_forward(seed, pos):
+    """orc_dense_step_kv8 (attn_prep_kv8 + the int8 reader + the rotated reduce in the layer
+    walk) against the fp64 forward in the un-rotated basis; the written rows decode, after
+    un-rotation, to the step's K and V within the int8 quantiser's bound."""
+    m = TinyKv8(seed)
+    tok = seed * 31
+    am, got, (k8, v8, ks, vs) = m.oracle_step_kv8(tok, pos)
+    want, kc, vc = m.fp64_step_kv8(tok, pos)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= 5e-3 * scale, np.abs(got - want).max() / scale
+    assert np.corrcoef(got, want)[0, 1] > 0.9999
+    for li in range(m.d["layers"]):
+        for c8, cs, ref in ((k8, ks, kc), (v8, vs, vc)):
+            dec = unrotate64(m.dequant(c8[li, :, pos], cs[li, :, pos]))
+            step = O.f16_bits_to_f32(cs[li, :, pos])  # the rows' scales
+            # per element in the rotated basis |err| <= scale / 2 (+ the 16-bit rounding of
+            # the row); R is orthogonal, so the row's 2-norm error is at most 16 * scale / 2
+            err = np.linalg.norm(dec - ref[li, :, pos], axis=-1)
+            bound = 16 * step.astype(np.float64) / 2 + 2e-3 * np.linalg.norm(ref[li, :, pos], axis=-1)
+            assert np.all(err <= bound), (err, bound)
+    mask = np.ones(m.d["L"], bool)
+    mask[pos] = False
+    assert np.array_equal(k8[:, :, mask], m.k8[:, :, mask]) and np.array_equal(vs[:, :, mask], m.vs[:, :, mask])
+
+
+def test_kv8_bar_rejects_a_missing_unrotation():
+    m = TinyKv8(5)
+    _, got, _ = m.oracle_step_kv8(155, 41)
+    want = m.fp64_step_kv8(155, 41, mistake="kv8_rotated_basis")[0]
     assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
