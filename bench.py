@@ -287,16 +287,19 @@ def measure_cfg5(st):
     return rows
 
 
-def measure_cfg4(args):
+def measure_cfg4(args, kv_int8=0):
     """a 40-layer MoE decoder (hidden 2048, 256 experts top 8 + shared,
     expert inter 512, attention 16 q / 2 kv of 256, vocab 151936 assumed) at context 4096:
-    tokens/s of the captured step, and one step against the CPU oracle."""
+    tokens/s of the captured step, and one step against the CPU oracle. kv_int8: the same
+    model over the int8 rotated KV cache (the reference's --kv-cache int8)."""
     max_len = ((args.context + 64 + 1 + 63) // 64) * 64
     desc = mi.desc_moe_cfg4(max_len=max_len)
+    desc.kv_int8 = kv_int8
     eng = mi.Engine(desc, seed=args.seed + 1)
     eng.capture(1)
     st = eng.stream
-    out = {"workload": "BASELINE configs[3]: MoE decode step (40 layers, 256 experts top 8 + shared)"}
+    out = {"workload": "BASELINE configs[3]: MoE decode step (40 layers, 256 experts top 8 + shared)"
+                       + (", int8 rotated KV cache" if kv_int8 else "")}
     if not args.no_cpu:
         eng.reset(args.context, 1000)
         dt, cpu_logits, cpu_am, threads = cpu_oracle_step(eng, 1000, args.context)
@@ -324,7 +327,8 @@ def measure_cfg4(args):
     eng.close()
     H, E, I, QH, KVH, HD, V = 2048, 256, 512, 16, 2, 256, 151936
     per_layer = 9 * (2 * I * H + I * H) * 17 // 32 + (E + 1 + 15) // 16 * 16 * H * 2 \
-        + ((QH + 2 * KVH) * HD * H + QH * HD * H) * 17 // 32 + 2 * KVH * (args.context + 1) * HD * 2
+        + ((QH + 2 * KVH) * HD * H + QH * HD * H) * 17 // 32 \
+        + 2 * KVH * (args.context + 1) * (HD + 2 if kv_int8 else HD * 2)
     alg = 40 * per_layer + H * V * 17 // 32
     out.update({"ms_per_step": round(ms, 4), "tokens_per_s": round(1000.0 / ms, 2), "alg_bytes_per_token": alg,
                 "gbs": round(alg / ms / 1e6, 1)})
@@ -364,8 +368,9 @@ def cpu_oracle_step(eng, tok, pos):
         if d.qk_norm:
             Ly.q_norm = h(mi.T_Q_NORM, li, np.float32)
             Ly.k_norm = h(mi.T_K_NORM, li, np.float32)
-    kv_k = eng.to_host(mi.T_KV_K, 0, np.uint16).copy()
-    kv_v = eng.to_host(mi.T_KV_V, 0, np.uint16).copy()
+    kv_t = np.int8 if d.kv_int8 else np.uint16
+    kv_k = eng.to_host(mi.T_KV_K, 0, kv_t).copy()
+    kv_v = eng.to_host(mi.T_KV_V, 0, kv_t).copy()
     sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
     model = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
                          C.cast(layers, C.c_void_p), h(mi.T_EMBED, 0, np.uint16),
@@ -377,8 +382,14 @@ def cpu_oracle_step(eng, tok, pos):
         model.router_n, model.router_ksplit = (d.experts + 1 + 15) // 16 * 16, 16
     logits = np.zeros(d.vocab, np.float32)
     t0 = time.perf_counter()
-    am = O.lib().orc_dense_step(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(logits),
-                                d.layers)
+    if d.kv_int8:
+        kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
+        kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
+        am = O.lib().orc_dense_step_kv8(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(kv_ks),
+                                        O._p(kv_vs), O._p(logits), d.layers)
+    else:
+        am = O.lib().orc_dense_step(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(logits),
+                                    d.layers)
     dt = time.perf_counter() - t0
     return dt, logits, int(am), int(O.lib().orc_threads())
 
@@ -483,6 +494,7 @@ def main():
         other["cfg5_small_m_gemv"] = measure_cfg5(None)
         log(f"bench: cfg5 {other['cfg5_small_m_gemv']}")
         other["cfg4_moe_step"] = measure_cfg4(args)
+        other["cfg4_moe_step_int8_kv"] = measure_cfg4(args, kv_int8=1)
         log(f"bench: cfg4 {other['cfg4_moe_step']}")
 
     out = {

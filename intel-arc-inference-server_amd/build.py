@@ -21,11 +21,17 @@ HIP_ONLY = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-
             "-munsafe-fp-atomics"]
 
 
+# Per-file code generation options. attn.hip: the attention accumulators live in ordinary
+# VGPRs (they are rescaled by the vector ALUs between matrix-core products, which AGPRs would
+# turn into copies back and forth).
+PER_FILE = {"attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
     cmd = [HIPCC, *COMMON]
     if src.endswith(".hip"):
-        cmd += ["-x", "hip", *HIP_ONLY]
+        cmd += ["-x", "hip", *HIP_ONLY, *PER_FILE.get(os.path.basename(src), [])]
     cmd += ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in (r.stderr or "").splitlines()

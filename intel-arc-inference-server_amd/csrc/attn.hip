@@ -15,15 +15,9 @@
 //     layout and this build's head-major [kvh][rows][hd] are expressible;
 //   * int8 KV (kv8.h:126): k = float(q8) * f16(scale[row][kvh]), exact in fp32.
 //
-// Inside a block the work is MI355X-shaped rather than the B70's waves of 16:
-//   * one K or V row of HD dims is read by HD/8 lanes, 16 bytes (fp16) or 8 bytes (int8)
-//     each - a 64-lane wave covers 4 (HD 128) or 2 (HD 256) positions with coalesced
-//     256/512-byte row reads; the block's rows of one kv head are contiguous in the
-//     head-major layout;
-//   * all GQA q heads of the kv head share each K/V load (q held in registers, fp32);
-//   * the block is walked in chunks of 64 positions, each a single HBM round trip; the
-//     q.K scores run on the matrix cores, the online softmax per chunk (not per 16-position
-//     wave) in LDS, and P.V on the vector ALUs (kernel comment below).
+// Inside a block the work is MI355X-shaped rather than the B70's waves of 16: each of the
+// four waves runs its own online softmax over 16-position groups with both products (q.K and
+// P.V) on the matrix cores, and the waves merge once at the end (kernel comment below).
 // Scores and the softmax are fp32; no atomics, so replays are bitwise.
 #include "mi_capi_internal.h"
 #include "mi_common.h"
@@ -38,9 +32,9 @@ __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
   return p < 64u ? 64u : p;
 }
 
-// page-table entries one work-group stages (a block of ppw positions spans at most
-// ppw / page + 1 pages)
-constexpr uint32_t kMaxBlockPages = 256;
+// 16-position groups whose cache rows one work-group stages for a paged cache (a block of
+// ppw positions holds ppw / 16 groups; ppw is a multiple of 64)
+constexpr uint32_t kMaxBlockGroups = 512;
 
 struct AttnDecodeArgs {
   const uint32_t* ctrl;
@@ -57,7 +51,7 @@ struct AttnDecodeArgs {
   float scale;
 };
 
-// 8 consecutive KV elements of one row, raw (f16: 16 bytes; int8: 8 bytes)
+// 8 consecutive K elements of one row, raw (f16: 16 bytes; int8: 8 bytes)
 template <int KV8>
 struct KvChunk {
   u4_t w;
@@ -65,84 +59,69 @@ struct KvChunk {
 template <>
 struct KvChunk<1> {
   u2_t w;
-  uint16_t s;
 };
-
-template <int KV8>
-__device__ __forceinline__ KvChunk<KV8> load_chunk(const void* base, const uint16_t* sc, size_t off, size_t soff) {
-  KvChunk<KV8> c;
-  if constexpr (KV8 == 0) {
-    c.w = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(base) + off);
-  } else {
-    c.w = *reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(base) + off);
-    c.s = sc[soff];
-  }
-  return c;
-}
 template <int KV8>
 __device__ __forceinline__ void zero_chunk(KvChunk<KV8>& c) {
   if constexpr (KV8 == 0) c.w = u4_t{0u, 0u, 0u, 0u};
-  else { c.w = u2_t{0u, 0u}; c.s = 0; }
-}
-// the 8 values as fp32: f16 widened exactly, or int8 * f16(scale) (exact in fp32, kv8.h:126)
-template <int KV8>
-__device__ __forceinline__ void widen_chunk(const KvChunk<KV8>& c, float (&v)[8]) {
-  if constexpr (KV8 == 0) {
-    const uint32_t ws[4] = {c.w.x, c.w.y, c.w.z, c.w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = h2f((uint16_t)(ws[i] & 0xFFFFu));
-      v[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
-    }
-  } else {
-    const float s = h2f(c.s);
-    const uint32_t ws[2] = {c.w.x, c.w.y};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((ws[i / 4] >> (8 * (i % 4))) & 0xFFu) * s;
-  }
+  else c.w = u2_t{0u, 0u};
 }
 
-// 8 KV values of one row as the f16 B operand of an MFMA (int8 values are exact in f16;
-// their row scale is applied to the score afterwards)
+// 8 K values of one row as an f16 MFMA operand (int8 values are exact in f16; their row
+// scale is applied to the score afterwards)
 template <int KV8>
 __device__ __forceinline__ h8_t chunk_h8(const KvChunk<KV8>& c) {
   if constexpr (KV8 == 0) {
     return __builtin_bit_cast(h8_t, c.w);
   } else {
-    h8_t r;
-    const uint32_t ws[2] = {c.w.x, c.w.y};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (half_t)(float)(int8_t)((ws[i / 4] >> (8 * (i % 4))) & 0xFFu);
-    return r;
+    // byte permute: each biased byte u = q8 + 128 under an f16 exponent byte 0x64 is the f16
+    // 1024 + u; subtracting 1152 leaves q8 exactly (f16 integers up to 2048 are exact)
+    const uint32_t x0 = c.w.x ^ 0x80808080u, x1 = c.w.y ^ 0x80808080u, hi = 0x64646464u;
+    const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+    const h2_t p0 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04010400u)) - bias;
+    const h2_t p1 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04030402u)) - bias;
+    const h2_t p2 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04010400u)) - bias;
+    const h2_t p3 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04030402u)) - bias;
+    return h8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   }
 }
 
-// HD: head dim; KV8: int8 KV; GQA: q heads per kv head. A work-group walks its block in
-// chunks of 64 positions; every thread issues all of its K and V loads for a chunk
-// together, one chunk ahead of the one it computes when DB is set.
-//   scores  on the matrix cores: wave w computes the 16 x 16 tile (q heads padded to 16) x
-//           (positions 16w .. 16w+15) with v_mfma_f32_16x16x32_f16, A = q split into an f16
-//           high part and the f16 rounding of the remainder (two MFMAs: the dot is fp32
-//           accurate), B = the K rows, read 16 bytes per lane (lane l: position l % 16,
-//           dims 8 (l / 16) + 32 kk) - no cross-lane reduction at all;
-//   softmax per chunk per head in LDS (max, exp, sum), an online rescale between chunks;
-//   P V     on the vector ALUs: HD / 8 lanes own a V row (8 dims, 16 bytes each), the
-//           256 / (HD / 8) row slots accumulate sum_p w_p v_p and are merged in LDS in slot
-//           order at the end.
-// DB: double-buffer the chunks (blocks longer than one chunk); without it the registers of
-// one chunk's K and V are all a thread holds.
-template <int HD, int KV8, int GQA, bool DB>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
-  constexpr uint32_t CH = 64, KK = HD / 32;
-  constexpr uint32_t LP = HD / 8, SLOTS = 256 / LP, VU = CH / SLOTS;
-  __shared__ float sc[GQA][CH];
-  __shared__ float st_alpha[GQA], st_m[GQA], st_l[GQA];
-  __shared__ float red[SLOTS][GQA][HD];
-  __shared__ uint32_t s_pages[kMaxBlockPages];  // the block's page-table entries (paged KV)
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
+// HD: head dim; KV8: int8 KV; GQA: q heads per kv head. Per-wave flash decoding: the block's
+// positions are cut into 16-position groups and wave w takes groups w, w + 4, ..., keeping its
+// own online softmax state (running max, sum, accumulator) per q head; the four waves' states
+// are merged once, at the end, into the block's partial. No work-group barrier inside the loop.
+// Per group, both products run on the matrix cores:
+//   scores  S^T = K Q^T with v_mfma_f32_16x16x32_f16: A = the 16 K rows (lane l: position
+//           l % 16, dims 8 (l / 16) + 32 kk; int8 widened exactly to f16 by a byte permute),
+//           B = q split into an f16 high part and the f16 rounding of the remainder (two
+//           MFMAs: the dot is fp32 accurate), padded to 16 heads. Lane l receives the scores of
+//           positions 4 (l / 16) + r, r < 4, for head l % 16;
+//   softmax per head over those 4 scores and the 4 lanes l % 16 + 16 k (two lane exchanges);
+//           the weights w = exp(s - max) stay in the lanes that hold the scores, which is the
+//           B operand layout of the next product;
+//   P V     O^T = V^T W^T with v_mfma_f32_16x16x16_f16 per 16-dim tile: A = V^T (lane l: dim
+//           l % 16, positions 4 (l / 16) + j) read from the group's V rows staged in LDS with a
+//           swizzle that keeps the four row groups on distinct banks; B = the weights (times the
+//           row's V scale for int8), split into f16 high and low parts like q. The int8 (or f16)
+//           V values are exact in f16.
+// Prefetch (PF): the next group's K and V registers are loaded before the current group is used.
+template <int HD, int KV8, int GQA>
+__global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a) {
+  constexpr uint32_t KK = HD / 32, NT = HD / 16;
+  constexpr uint32_t EB = KV8 ? 1u : 2u, ROWB = HD * EB;  // bytes per row
+  constexpr uint32_t VLD = ROWB / 64u;                     // 16-byte V loads per lane (4 lanes per row)
+  constexpr uint32_t CW = 16u * EB;                        // bytes of one 16-dim column
+  constexpr bool PF = (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;
+  constexpr uint32_t SV = 16u * ROWB;                      // one wave's staged V group
+  constexpr uint32_t RED = 4u * GQA * HD * 4u;             // the end merge's accumulators
+  __shared__ __align__(16) unsigned char s_buf[(4u * SV > RED ? 4u * SV : RED)];
+  __shared__ float st_m[4][16], st_l[4][16];
+  __shared__ uint32_t s_grow[kMaxBlockGroups];
+  __shared__ h8_t s_q[2][KK][64];  // q as the B operand, per lane: f16 high and low parts
 
   const uint32_t j = blockIdx.x, blk = blockIdx.y, m = blockIdx.z;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-  const uint32_t slot = t / LP, dg = t % LP, d0 = dg * 8;
   const uint32_t qi = lane & 15u, qq = lane >> 4;
   const uint32_t n_act = a.ctrl[CTRL_NACT];
   if (m >= n_act) return;
@@ -154,187 +133,252 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
   if (nb > a.tgt) nb = a.tgt;
   if (blk >= nb) return;
   const uint32_t p_begin = blk * s, p_end = min(p_begin + s, L);
+  const uint32_t ng = (p_end - p_begin + 15u) / 16u;
 
-  float acc[GQA][8];
-#pragma unroll
-  for (uint32_t g = 0; g < GQA; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-  if (t < GQA) {
-    st_m[t] = -INFINITY;
-    st_l[t] = 0.f;
-  }
-
-  // A paged cache's entries for this block are read once, into LDS, so a chunk's K/V loads
-  // never wait on a page-table load first.
-  const uint32_t pg0 = a.pages ? p_begin / a.page : 0u;
-  if (a.pages) {
-    const uint32_t np = (p_end - 1) / a.page - pg0 + 1;
-    for (uint32_t i = t; i < np; i += 256u) s_pages[i] = a.pages[pg0 + i];
-    __syncthreads();
-  }
-  auto row_of = [&](uint32_t p) -> size_t {
-    return a.pages ? (size_t)s_pages[p / a.page - pg0] * a.page + p % a.page : (size_t)p;
-  };
   const size_t hoff = (size_t)j * a.head_stride;
   const size_t shoff = (size_t)j * a.sc_head_stride;
-  const uint32_t pk = 16u * wave + qi;  // this lane's score position within the chunk
-  // chunk c's K and V rows into registers (zeros past the block's end)
-  auto load_kv = [&](uint32_t c0, KvChunk<KV8> (&kc)[KK], KvChunk<KV8> (&vc)[VU]) {
-    const uint32_t clen = c0 < p_end ? min(CH, p_end - c0) : 0u;
-    if (pk < clen) {
-      const size_t row = row_of(c0 + pk);
+  struct Group {
+    KvChunk<KV8> k[KK];
+    u4_t v[VLD];
+    uint16_t ks, vs;
+  };
+  const uint32_t vrow = lane >> 2, vpart = lane & 3u;  // the V row and quarter this lane loads
+  // group gi whose first cache row is rb (uniform)
+  auto load_group = [&](uint32_t gi, uint32_t rb, Group& g) {
+    const uint32_t p0 = p_begin + 16u * gi;
+    const uint32_t glen = min(16u, p_end - p0);
+    if (qi < glen) {
+      const size_t row = (size_t)rb + qi;
 #pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk)
-        kc[kk] = load_chunk<KV8>(a.kv_k, a.k_scale, row * a.row_stride + hoff + 32 * kk + 8 * qq,
-                                 row * a.sc_row_stride + shoff);
+      for (uint32_t kk = 0; kk < KK; ++kk) {
+        const size_t off = row * a.row_stride + hoff + 32 * kk + 8 * qq;
+        if constexpr (KV8 == 0) g.k[kk].w = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(a.kv_k) + off);
+        else g.k[kk].w = *reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(a.kv_k) + off);
+      }
+      if constexpr (KV8 == 1) {
+        g.ks = a.k_scale[row * a.sc_row_stride + shoff];
+        g.vs = a.v_scale[row * a.sc_row_stride + shoff];
+      }
     } else {
 #pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(kc[kk]);
+      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(g.k[kk]);
+      g.ks = 0;
+      g.vs = 0;
     }
+    if (vrow < glen) {
+      const unsigned char* vb = static_cast<const unsigned char*>(a.kv_v) +
+                                (((size_t)rb + vrow) * a.row_stride + hoff) * EB + vpart * (ROWB / 4u);
 #pragma unroll
-    for (uint32_t u = 0; u < VU; ++u) {
-      const uint32_t pl = u * SLOTS + slot;
-      if (pl < clen) {
-        const size_t row = row_of(c0 + pl);
-        vc[u] = load_chunk<KV8>(a.kv_v, a.v_scale, row * a.row_stride + hoff + d0, row * a.sc_row_stride + shoff);
-      } else {
-        zero_chunk<KV8>(vc[u]);
-      }
+      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = *reinterpret_cast<const u4_t*>(vb + 16u * i);
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = u4_t{0u, 0u, 0u, 0u};
     }
   };
-  // DB: chunk c + 1's loads are issued before chunk c is used, and the barriers in the loop
-  // order LDS only, so those loads stay in flight across them.
-  KvChunk<KV8> kc[KK], vc[VU];
-  load_kv(p_begin, kc, vc);  // the first chunk's loads go out before q is read
-  // q as the MFMA A operand: row qi = head (zero past GQA), k = 32 kk + 8 qq + e
-  h8_t qhi[KK], qlo[KK];
-#pragma unroll
-  for (uint32_t kk = 0; kk < KK; ++kk) {
-    float v[8];
-    if (qi < GQA) {
-      const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
-      const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
-      const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
-      v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-      v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const half_t h = (half_t)v[e];
-      qhi[kk][e] = h;
-      qlo[kk][e] = (half_t)(v[e] - (float)h);
+
+
+  // this wave's first group goes out before anything else: its row straight from the page
+  // table, the later groups' rows staged in LDS below
+  Group cur, nxt;
+  uint32_t gi = wave;
+  if (gi < ng) {
+    const uint32_t p0 = p_begin + 16u * gi;
+    const uint32_t rb = a.pages ? a.pages[p0 / a.page] * a.page + p0 % a.page : p0;
+    load_group(gi, __builtin_amdgcn_readfirstlane(rb), cur);
+  }
+  // A paged cache: a page holds whole 16-position groups, so a group's rows are consecutive.
+  // Each group's first cache row is looked up once, into LDS (the only divisions by the page
+  // size), so no later K/V load waits on a page-table load.
+  if (a.pages) {
+    for (uint32_t i = t; i < ng; i += 256u) {
+      const uint32_t p = p_begin + 16u * i;
+      s_grow[i] = a.pages[p / a.page] * a.page + p % a.page;
     }
   }
-  for (uint32_t c0 = p_begin; c0 < p_end; c0 += CH) {
-    const uint32_t clen = min(CH, p_end - c0);
-    KvChunk<KV8> kn[KK], vn[VU];
-    if constexpr (DB) load_kv(c0 + CH, kn, vn);
-    // scores
+  // q as the MFMA B operand, staged once by wave 0: column qi = head (zero past GQA),
+  // k = 32 kk + 8 qq + e; the waves read it from LDS per group rather than holding it
+  if (wave == 0) {
+#pragma unroll
+    for (uint32_t kk = 0; kk < KK; ++kk) {
+      float v[8];
+      if (qi < GQA) {
+        const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
+        const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
+        const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
+        v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+        v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+      h8_t hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const half_t h = (half_t)v[e];
+        hi[e] = h;
+        lo[e] = (half_t)(v[e] - (float)h);
+      }
+      s_q[0][kk][lane] = hi;
+      s_q[1][kk][lane] = lo;
+    }
+  }
+  __syncthreads();
+
+  // this wave's running state for head qi; acc[tt][r] = O^T[16 tt + 4 qq + r][qi]
+  float m_run = -INFINITY, l_run = 0.f;
+  f4_t acc[NT];
+#pragma unroll
+  for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  unsigned char* sv = s_buf + wave * SV;
+  // the swizzled byte offset of (row r, 16-dim column c): the four row groups 4 k + j that one
+  // A-operand read touches land on distinct banks
+  auto sv_off = [](uint32_t r, uint32_t c) -> uint32_t { return r * ROWB + ((c ^ ((r >> 2) & 3u)) * CW); };
+
+  auto group_row = [&](uint32_t g) -> uint32_t {
+    return __builtin_amdgcn_readfirstlane(a.pages ? s_grow[g] : p_begin + 16u * g);
+  };
+  for (; gi < ng; gi += 4u) {
+    if constexpr (PF) {
+      if (gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);
+    }
+    const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
+    // stage this group's V rows (the previous group's reads of this wave's area are done:
+    // one wave's LDS operations complete in order, and the fence keeps the compiler's too)
+    wave_lds_sync();
+#pragma unroll
+    for (uint32_t i = 0; i < VLD; ++i) {
+      const uint32_t byte = vpart * (ROWB / 4u) + 16u * i;  // within the row
+      *reinterpret_cast<u4_t*>(sv + sv_off(vrow, byte / CW) + byte % CW) = cur.v[i];
+    }
+    wave_lds_sync();
+    // scores S^T[position 4 qq + r][head qi]
     f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (uint32_t kk = 0; kk < KK; ++kk) {
-      const h8_t b = chunk_h8<KV8>(kc[kk]);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[kk], b, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[kk], b, d, 0, 0, 0);
+      const h8_t kh = chunk_h8<KV8>(cur.k[kk]);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[0][kk][lane], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[1][kk][lane], d, 0, 0, 0);
     }
-    float rs = a.scale;
-    if constexpr (KV8 == 1) rs = a.scale * h2f(kc[0].s);
+    float sc[4];
+    float mx = -INFINITY;
 #pragma unroll
     for (uint32_t r = 0; r < 4; ++r) {
-      const uint32_t head = 4u * qq + r;
-      if (head < GQA && pk < clen) sc[head][pk] = d[r] * rs;
+      float rs = a.scale;
+      if constexpr (KV8 == 1) rs = a.scale * h2f((uint16_t)__shfl((int)cur.ks, (int)(4u * qq + r), 64));
+      sc[r] = 4u * qq + r < glen ? d[r] * rs : -INFINITY;
+      mx = fmaxf(mx, sc[r]);
     }
-    lds_barrier();
-    // chunk max, weights and chunk sum: wave w owns heads w, w + 4
-    for (uint32_t g = wave; g < GQA; g += 4) {
-      const float v = lane < clen ? sc[g][lane] : -INFINITY;
-      const float mx = wave_max(v);
-      const float m_old = st_m[g];
-      const float m_new = fmaxf(m_old, mx);
-      const float w = lane < clen ? expf(v - m_new) : 0.f;
-      if (lane < clen) sc[g][lane] = w;
-      const float sum = wave_sum(w);
-      if (lane == 0) {
-        const float alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
-        st_alpha[g] = alpha;
-        st_l[g] = __builtin_fmaf(st_l[g], alpha, sum);
-        st_m[g] = m_new;
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = expf(m_run - m_new);  // 0 on the first group (m_run = -inf)
+    float w[4];
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) w[r] = expf(sc[r] - m_new);
+    l_run = __builtin_fmaf(l_run, alpha, (w[0] + w[1]) + (w[2] + w[3]));
+    m_run = m_new;
+    if (__ballot(alpha != 1.0f)) {  // a head's max moved (a factor of 1 leaves acc unchanged)
+#pragma unroll
+      for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+    }
+    // B operand: the weights (int8: times the row's V scale), f16 high and low parts
+    h4_t bh, bl;
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      float wv = w[r];
+      if constexpr (KV8 == 1) wv *= h2f((uint16_t)__shfl((int)cur.vs, (int)(4u * qq + r), 64));
+      const half_t h = (half_t)wv;
+      bh[r] = h;
+      bl[r] = (half_t)(wv - (float)h);
+    }
+    // P V per 16-dim tile: A[dim qi][position 4 qq + jj] from the staged rows
+#pragma unroll
+    for (uint32_t tt = 0; tt < NT; ++tt) {
+      h4_t av;
+      if constexpr (KV8 == 1) {
+        uint32_t b[4];
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; ++jj) b[jj] = sv[sv_off(4u * qq + jj, tt) + qi];
+        const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+        const h2_t lo = as_h2((b[0] | (b[1] << 16)) ^ 0x64806480u) - bias;
+        const h2_t hi = as_h2((b[2] | (b[3] << 16)) ^ 0x64806480u) - bias;
+        av = h4_t{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; ++jj)
+          av[jj] = *reinterpret_cast<const half_t*>(sv + sv_off(4u * qq + jj, tt) + 2u * qi);
       }
+      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, acc[tt], 0, 0, 0);
+      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, acc[tt], 0, 0, 0);
     }
-    lds_barrier();
-    // rescale, then accumulate w * v from the registers loaded above
-#pragma unroll
-    for (uint32_t g = 0; g < GQA; ++g) {
-      const float al = st_alpha[g];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] *= al;
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < VU; ++u) {
-      const uint32_t pl = u * SLOTS + slot;
-      if (pl < clen) {
-        float v[8];
-        widen_chunk<KV8>(vc[u], v);
-#pragma unroll
-        for (uint32_t g = 0; g < GQA; ++g) {
-          const float w = sc[g][pl];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(w, v[i], acc[g][i]);
-        }
-      }
-    }
-    lds_barrier();
-    if constexpr (DB) {
-#pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) kc[kk] = kn[kk];
-#pragma unroll
-      for (uint32_t u = 0; u < VU; ++u) vc[u] = vn[u];
-    } else if (c0 + CH < p_end) {
-      load_kv(c0 + CH, kc, vc);
+    if constexpr (PF) {
+      cur = nxt;
+    } else {
+      if (gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), cur);
     }
   }
-  // merge the row slots in slot order through LDS
+  // merge the four waves: M = max m_w, f_w = exp(m_w - M), sum and acc weighted by f_w in
+  // wave order
+  float l = l_run + __shfl_xor(l_run, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  if (qq == 0) {
+    st_m[wave][qi] = m_run;
+    st_l[wave][qi] = l;
+  }
+  lds_barrier();  // every wave has finished with its staging area, which the merge reuses
+  float* red = reinterpret_cast<float*>(s_buf);  // [4][GQA][HD]
+  if (qi < GQA) {
 #pragma unroll
-  for (uint32_t g = 0; g < GQA; ++g)
+    for (uint32_t tt = 0; tt < NT; ++tt)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) red[slot][g][d0 + i] = acc[g][i];
-  __syncthreads();
-  for (uint32_t idx = t; idx < GQA * HD; idx += 256) {
+      for (uint32_t r = 0; r < 4; ++r) red[(wave * GQA + qi) * HD + 16u * tt + 4u * qq + r] = acc[tt][r];
+  }
+  lds_barrier();
+  for (uint32_t idx = t; idx < GQA * HD; idx += 256u) {
     const uint32_t g = idx / HD, dd = idx % HD;
-    float v = red[0][g][dd];
+    float M = st_m[0][g];
 #pragma unroll
-    for (uint32_t sl = 1; sl < SLOTS; ++sl) v += red[sl][g][dd];
+    for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][g]);
+    float sm = 0.f, v = 0.f;
+#pragma unroll
+    for (uint32_t w2 = 0; w2 < 4; ++w2) {
+      const float f = expf(st_m[w2][g] - M);  // a wave without positions: exp(-inf) = 0
+      sm = __builtin_fmaf(st_l[w2][g], f, sm);
+      v = __builtin_fmaf(red[(w2 * GQA + g) * HD + dd], f, v);
+    }
     float* out = a.attn_part + (((size_t)(j * GQA + g) * a.tgt + blk) * a.M + m) * (HD + 2);
     out[2 + dd] = v;
     if (dd == 0) {
-      out[0] = st_m[g];
-      out[1] = st_l[g];
+      out[0] = M;
+      out[1] = sm;
     }
   }
 }
 
-// grid (q_heads, M), HD lanes: attn_v2.cl:383-428's merge of a row's nb block partials.
-// Phase 1 reads every block's (mx, sm) in parallel and forms the common max M = max mx
-// and each block's factor exp(mx_b - M); phase 2 sums acc_b * factor_b in ascending b with
-// all the loads independent of each other. Mathematically the reference's sequential
-// rescaling merge; the roundings differ at the last place only.
+// attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,
+// factors f_b = exp(mx_b - M), sum = sum_b sm_b f_b and acc = sum_b acc_b f_b: mathematically
+// the reference's sequential rescaling merge, the roundings differing at the last place.
+// grid (q_heads, M, NZ), 256 threads. Wave w sums the blocks of its quarter of [0, nb) in
+// ascending order; the four quarter sums are added in wave order. Lane l owns dims
+// 64 z + l (NZ = HD / 64 work-groups per head, DPT = 1), or, for ROT, dims l + 64 k for
+// k < HD / 64 (NZ = 1, DPT = HD / 64), since the un-rotation needs the whole head. Every
+// partial load of a batch is issued before the factors are formed, so the merge takes a
+// few memory round trips whatever nb is.
 // ROT (attn_reduce_v2_kv8, kv8.cl:814-860; head_dim 256): the merged output is in the int8
 // cache's rotated basis and is un-rotated per head before the gate.
-template <bool ROT>
+template <bool ROT, int DPT>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __restrict__ ctrl,
                                                           const float* __restrict__ attn_part,
                                                           const float* __restrict__ attn_gate,
                                                           uint16_t* __restrict__ attn_out, uint32_t M,
                                                           uint32_t q_heads, uint32_t HD, uint32_t tgt,
                                                           uint32_t gated, uint32_t kv_len) {
+  constexpr uint32_t BATCH = 64 / DPT;  // blocks per load batch (64 loads in flight per thread)
   __shared__ float fac[1024];
-  __shared__ float s_sm;
-  const uint32_t h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
-  if (m >= ctrl[CTRL_NACT]) return;
+  __shared__ float s_red[2][4];
+  __shared__ float s_acc[4][DPT * 64];
+  const uint32_t h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  if (m >= ctrl[CTRL_NACT]) return;  // uniform
   const uint32_t pos = ctrl[CTRL_POS];
   uint32_t L = pos + m + 1;
   if (kv_len && L > kv_len) L = kv_len;
@@ -343,75 +387,98 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   const size_t PART = HD + 2;
   const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
   const size_t bstride = (size_t)M * PART;
-  // the first 64 blocks' acc values do not depend on phase 1: their loads go out first
-  // (a block past nb reloads block nb - 1 and is not added)
-  float v64[64];
+  const uint32_t dbase = ROT ? 0u : blockIdx.z * 64u;
+  // this wave's quarter of the blocks
+  const uint32_t qn = (nb + 3) / 4, b0 = min(w * qn, nb), b1 = min(b0 + qn, nb);
+  // the first batch's partial values do not depend on the factors: their loads go first
+  // (a block past b1 reloads block nb - 1 and is not added)
+  float v[BATCH][DPT];
 #pragma unroll
-  for (uint32_t u = 0; u < 64; ++u) v64[u] = base[min(u, nb - 1) * bstride + 2 + d];
-  // phase 1 (wave 0): the common max and the per-block factors
-  if (d < 64) {
-    float mx = -INFINITY;
-    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, base[b * bstride]);
+  for (uint32_t u = 0; u < BATCH; ++u)
 #pragma unroll
-    for (uint32_t o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float sm = 0.f;
-    for (uint32_t b = d; b < nb; b += 64) {
-      const float f = expf(base[b * bstride] - mx);
+    for (int k = 0; k < DPT; ++k) v[u][k] = base[min(b0 + u, nb - 1) * bstride + 2 + dbase + lane + 64 * k];
+  // factors: the common max over every block, then f_b and the weighted block sums
+  float mxs[4], sms[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t b = t + 256 * i;
+    mxs[i] = b < nb ? base[b * bstride] : -INFINITY;
+    sms[i] = b < nb ? base[b * bstride + 1] : 0.f;
+    mx = fmaxf(mx, mxs[i]);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) s_red[0][w] = mx;
+  lds_barrier();
+  mx = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+  float sm = 0.f;
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t b = t + 256 * i;
+    if (b < nb) {
+      const float f = expf(mxs[i] - mx);
       fac[b] = f;
-      sm = __builtin_fmaf(base[b * bstride + 1], f, sm);
+      sm = __builtin_fmaf(sms[i], f, sm);
+    }
+  }
+  sm = wave_sum(sm);
+  if (lane == 0) s_red[1][w] = sm;
+  lds_barrier();
+  sm = ((s_red[1][0] + s_red[1][1]) + s_red[1][2]) + s_red[1][3];
+  // this wave's quarter in ascending block order
+  float acc[DPT];
+#pragma unroll
+  for (int k = 0; k < DPT; ++k) acc[k] = 0.f;
+  for (uint32_t b = b0; b < b1; b += BATCH) {
+    if (b != b0) {
+#pragma unroll
+      for (uint32_t u = 0; u < BATCH; ++u)
+#pragma unroll
+        for (int k = 0; k < DPT; ++k) v[u][k] = base[min(b + u, nb - 1) * bstride + 2 + dbase + lane + 64 * k];
     }
 #pragma unroll
-    for (uint32_t o = 32; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
-    if (d == 0) s_sm = sm;
-  }
-  __syncthreads();
-  // added in ascending block order: the preloaded 64, then the rest 8 loads at a time
-  float acc = 0.f;
+    for (uint32_t u = 0; u < BATCH; ++u)
+      if (b + u < b1) {
+        const float f = fac[b + u];
 #pragma unroll
-  for (uint32_t u = 0; u < 64; ++u)
-    if (u < nb) acc = __builtin_fmaf(v64[u], fac[u], acc);
-  for (uint32_t b = 64; b < nb; b += 8) {
-    float v[8];
-#pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) v[u] = base[min(b + u, nb - 1) * bstride + 2 + d];
-#pragma unroll
-    for (uint32_t u = 0; u < 8; ++u)
-      if (b + u < nb) acc = __builtin_fmaf(v[u], fac[b + u], acc);
+        for (int k = 0; k < DPT; ++k) acc[k] = __builtin_fmaf(v[u][k], f, acc[k]);
+      }
   }
-  float o = acc / s_sm;
-  if constexpr (ROT) {
-    __shared__ float xch[256];
-    float v1[1] = {kv8_flip(o, kv8_sign_neg(d))};
-    fwht256<1>(v1, d, xch);
-    o = v1[0] * 0.0625f;
+#pragma unroll
+  for (int k = 0; k < DPT; ++k) s_acc[w][lane + 64 * k] = acc[k];
+  lds_barrier();
+  // thread t now owns dim dbase + t (t < 64 DPT)
+  if (t < 64u * DPT) {
+    const float tot = ((s_acc[0][t] + s_acc[1][t]) + s_acc[2][t]) + s_acc[3][t];
+    float o = tot / sm;
+    if constexpr (ROT) {
+      __shared__ float xch[256];
+      float v1[1] = {kv8_flip(o, kv8_sign_neg(t))};
+      fwht256<1>(v1, t, xch);  // DPT = 4: all 256 threads are here
+      o = v1[0] * 0.0625f;
+    }
+    const uint32_t d = dbase + t;
+    uint16_t r;
+    if (gated && attn_gate)
+      r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
+    else
+      r = f2h(o);
+    attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
   }
-  uint16_t r;
-  if (gated && attn_gate)
-    r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
-  else
-    r = f2h(o);
-  attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
-template <int HD, int KV8, bool DB>
-int launch_decode_db(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
+template <int HD, int KV8>
+int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
   switch (gqa) {
-    case 1: attn_decode_kernel<HD, KV8, 1, DB><<<grid, 256, 0, st>>>(a); break;
-    case 2: attn_decode_kernel<HD, KV8, 2, DB><<<grid, 256, 0, st>>>(a); break;
-    case 4: attn_decode_kernel<HD, KV8, 4, DB><<<grid, 256, 0, st>>>(a); break;
-    case 5: attn_decode_kernel<HD, KV8, 5, DB><<<grid, 256, 0, st>>>(a); break;
-    case 6: attn_decode_kernel<HD, KV8, 6, DB><<<grid, 256, 0, st>>>(a); break;
-    case 8: attn_decode_kernel<HD, KV8, 8, DB><<<grid, 256, 0, st>>>(a); break;
+    case 1: attn_decode_wave_kernel<HD, KV8, 1><<<grid, 256, 0, st>>>(a); break;
+    case 2: attn_decode_wave_kernel<HD, KV8, 2><<<grid, 256, 0, st>>>(a); break;
+    case 4: attn_decode_wave_kernel<HD, KV8, 4><<<grid, 256, 0, st>>>(a); break;
+    case 5: attn_decode_wave_kernel<HD, KV8, 5><<<grid, 256, 0, st>>>(a); break;
+    case 6: attn_decode_wave_kernel<HD, KV8, 6><<<grid, 256, 0, st>>>(a); break;
+    case 8: attn_decode_wave_kernel<HD, KV8, 8><<<grid, 256, 0, st>>>(a); break;
     default: return -1;
   }
   return 0;
-}
-// A cache of kv_len rows never gives a block more than one 64-position chunk when
-// kv_len <= 64 tgt (ppw stays 64); otherwise the double-buffered kernel runs.
-template <int HD, int KV8>
-int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
-  if (a.kv_len && a.kv_len <= 64u * a.tgt) return launch_decode_db<HD, KV8, false>(a, gqa, grid, st);
-  return launch_decode_db<HD, KV8, true>(a, gqa, grid, st);
 }
 
 }  // namespace
@@ -444,8 +511,8 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
     return mi_fail(MI_ERR_SHAPE, "attn_decode: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
   if (pages && (page == 0 || page % 16))
     return mi_fail(MI_ERR_SHAPE, "attn_decode: a KV page holds a multiple of 16 positions");
-  if (pages && (!kv_len || mi_attn_ppw(kv_len, tgt) / page + 1 > kMaxBlockPages))
-    return mi_fail(MI_ERR_SHAPE, "attn_decode: a paged cache needs kv_len, and at most 256 pages per block");
+  if (pages && (!kv_len || mi_attn_ppw(kv_len, tgt) / 16 > kMaxBlockGroups))
+    return mi_fail(MI_ERR_SHAPE, "attn_decode: a paged cache needs kv_len, and at most 8192 positions per block");
   if ((row_stride % 8) || (head_stride % 8))
     return mi_fail(MI_ERR_ARG, "attn_decode: KV strides must keep 8-element alignment");
   AttnDecodeArgs a{ctrl,  attn_q,       kv_k,           kv_v,   k_scale,         v_scale,
@@ -470,7 +537,7 @@ int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* at
     return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
-  attn_reduce_kernel<false><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
+  attn_reduce_kernel<false, 1><<<dim3(shape->q_heads, M, HD / 64), 256, 0, (hipStream_t)stream>>>(
       ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
 }
@@ -481,7 +548,7 @@ int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float
     return mi_fail(MI_ERR_ARG, "attn_reduce_kv8: bad arguments (tgt <= 1024)");
   if (shape->head_dim != 256)
     return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: the rotation is defined for head_dim 256 only");
-  attn_reduce_kernel<true><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
+  attn_reduce_kernel<true, 4><<<dim3(shape->q_heads, M, 1), 256, 0, (hipStream_t)stream>>>(
       ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce_kv8");
 }
