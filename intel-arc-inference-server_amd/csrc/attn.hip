@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
   constexpr uint32_t SV = 16u * ROWB;                      // one wave's staged V group
   constexpr uint32_t RED = 4u * GQA * HD * 4u;             // the end merge's accumulators
   __shared__ __align__(16) unsigned char s_buf[(4u * SV > RED ? 4u * SV : RED)];
-  __shared__ float st_m[4][16], st_l[4][16];
+  __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
   __shared__ uint32_t s_grow[kMaxBlockGroups];
   __shared__ h8_t s_q[2][KK][64];  // q as the B operand, per lane: f16 high and low parts
 
@@ -333,51 +333,54 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
 #pragma unroll
       for (uint32_t r = 0; r < 4; ++r) red[(wave * GQA + qi) * HD + 16u * tt + 4u * qq + r] = acc[tt][r];
   }
+  if (t < GQA) {  // per head, once: the common max, the waves' factors, the weighted sum
+    float M = st_m[0][t];
+#pragma unroll
+    for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][t]);
+    float sm = 0.f;
+#pragma unroll
+    for (uint32_t w2 = 0; w2 < 4; ++w2) {
+      const float f = expf(st_m[w2][t] - M);  // a wave without positions: exp(-inf) = 0
+      sm = __builtin_fmaf(st_l[w2][t], f, sm);
+      st_f[w2][t] = f;
+    }
+    st_hm[t] = M;
+    st_hs[t] = sm;
+  }
   lds_barrier();
   for (uint32_t idx = t; idx < GQA * HD; idx += 256u) {
     const uint32_t g = idx / HD, dd = idx % HD;
-    float M = st_m[0][g];
+    float v = 0.f;
 #pragma unroll
-    for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][g]);
-    float sm = 0.f, v = 0.f;
-#pragma unroll
-    for (uint32_t w2 = 0; w2 < 4; ++w2) {
-      const float f = expf(st_m[w2][g] - M);  // a wave without positions: exp(-inf) = 0
-      sm = __builtin_fmaf(st_l[w2][g], f, sm);
-      v = __builtin_fmaf(red[(w2 * GQA + g) * HD + dd], f, v);
-    }
+    for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * GQA + g) * HD + dd], st_f[w2][g], v);
     float* out = a.attn_part + (((size_t)(j * GQA + g) * a.tgt + blk) * a.M + m) * (HD + 2);
     out[2 + dd] = v;
     if (dd == 0) {
-      out[0] = M;
-      out[1] = sm;
+      out[0] = st_hm[g];
+      out[1] = st_hs[g];
     }
   }
 }
 
 // attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,
-// factors f_b = exp(mx_b - M), sum = sum_b sm_b f_b and acc = sum_b acc_b f_b: mathematically
-// the reference's sequential rescaling merge, the roundings differing at the last place.
-// grid (q_heads, M, NZ), 256 threads. Wave w sums the blocks of its quarter of [0, nb) in
-// ascending order; the four quarter sums are added in wave order. Lane l owns dims
-// 64 z + l (NZ = HD / 64 work-groups per head, DPT = 1), or, for ROT, dims l + 64 k for
-// k < HD / 64 (NZ = 1, DPT = HD / 64), since the un-rotation needs the whole head. Every
-// partial load of a batch is issued before the factors are formed, so the merge takes a
-// few memory round trips whatever nb is.
+// factors f_b = exp(mx_b - M), sum = sum_b sm_b f_b and acc = sum_b acc_b f_b added in
+// ascending b: mathematically the reference's sequential rescaling merge, the roundings
+// differing at the last place. grid (q_heads, M), HD threads, one dim each. The first 64
+// blocks' values do not depend on the factors and are loaded before them, together with
+// wave 0's (mx, sm) loads, so a merge of up to 64 blocks is one memory round trip; further
+// blocks follow 64 at a time.
 // ROT (attn_reduce_v2_kv8, kv8.cl:814-860; head_dim 256): the merged output is in the int8
 // cache's rotated basis and is un-rotated per head before the gate.
-template <bool ROT, int DPT>
+template <bool ROT>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __restrict__ ctrl,
                                                           const float* __restrict__ attn_part,
                                                           const float* __restrict__ attn_gate,
                                                           uint16_t* __restrict__ attn_out, uint32_t M,
                                                           uint32_t q_heads, uint32_t HD, uint32_t tgt,
                                                           uint32_t gated, uint32_t kv_len) {
-  constexpr uint32_t BATCH = 64 / DPT;  // blocks per load batch (64 loads in flight per thread)
   __shared__ float fac[1024];
-  __shared__ float s_red[2][4];
-  __shared__ float s_acc[4][DPT * 64];
-  const uint32_t h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  __shared__ float s_sm;
+  const uint32_t h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
   if (m >= ctrl[CTRL_NACT]) return;  // uniform
   const uint32_t pos = ctrl[CTRL_POS];
   uint32_t L = pos + m + 1;
@@ -387,84 +390,59 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   const size_t PART = HD + 2;
   const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
   const size_t bstride = (size_t)M * PART;
-  const uint32_t dbase = ROT ? 0u : blockIdx.z * 64u;
-  // this wave's quarter of the blocks
-  const uint32_t qn = (nb + 3) / 4, b0 = min(w * qn, nb), b1 = min(b0 + qn, nb);
-  // the first batch's partial values do not depend on the factors: their loads go first
-  // (a block past b1 reloads block nb - 1 and is not added)
-  float v[BATCH][DPT];
+  // (a load past nb re-reads block nb - 1 and is not added)
+  constexpr uint32_t PRE = 64, BAT = 64;
+  // loads go out in runs of 16 behind a uniform bound, so a short merge issues few of them
+  float v[PRE];
 #pragma unroll
-  for (uint32_t u = 0; u < BATCH; ++u)
+  for (uint32_t c = 0; c < PRE; c += 16)
+    if (c < nb) {
 #pragma unroll
-    for (int k = 0; k < DPT; ++k) v[u][k] = base[min(b0 + u, nb - 1) * bstride + 2 + dbase + lane + 64 * k];
-  // factors: the common max over every block, then f_b and the weighted block sums
-  float mxs[4], sms[4];
-  float mx = -INFINITY;
-#pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t b = t + 256 * i;
-    mxs[i] = b < nb ? base[b * bstride] : -INFINITY;
-    sms[i] = b < nb ? base[b * bstride + 1] : 0.f;
-    mx = fmaxf(mx, mxs[i]);
-  }
-  mx = wave_max(mx);
-  if (lane == 0) s_red[0][w] = mx;
-  lds_barrier();
-  mx = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
-  float sm = 0.f;
-#pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t b = t + 256 * i;
-    if (b < nb) {
-      const float f = expf(mxs[i] - mx);
+      for (uint32_t u = c; u < c + 16; ++u) v[u] = base[min(u, nb - 1) * bstride + 2 + d];
+    }
+  // wave 0: the common max and the per-block factors
+  if (d < 64) {
+    float mx = -INFINITY;
+    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, base[b * bstride]);
+    mx = wave_max(mx);
+    float sm = 0.f;
+    for (uint32_t b = d; b < nb; b += 64) {
+      const float f = expf(base[b * bstride] - mx);
       fac[b] = f;
-      sm = __builtin_fmaf(sms[i], f, sm);
+      sm = __builtin_fmaf(base[b * bstride + 1], f, sm);
     }
+    sm = wave_sum(sm);
+    if (d == 0) s_sm = sm;
   }
-  sm = wave_sum(sm);
-  if (lane == 0) s_red[1][w] = sm;
-  lds_barrier();
-  sm = ((s_red[1][0] + s_red[1][1]) + s_red[1][2]) + s_red[1][3];
-  // this wave's quarter in ascending block order
-  float acc[DPT];
+  __syncthreads();
+  float acc = 0.f;
 #pragma unroll
-  for (int k = 0; k < DPT; ++k) acc[k] = 0.f;
-  for (uint32_t b = b0; b < b1; b += BATCH) {
-    if (b != b0) {
+  for (uint32_t u = 0; u < PRE; ++u)
+    if (u < nb) acc = __builtin_fmaf(v[u], fac[u], acc);
+  for (uint32_t b = PRE; b < nb; b += BAT) {
 #pragma unroll
-      for (uint32_t u = 0; u < BATCH; ++u)
+    for (uint32_t c = 0; c < BAT; c += 16)
+      if (b + c < nb) {
 #pragma unroll
-        for (int k = 0; k < DPT; ++k) v[u][k] = base[min(b + u, nb - 1) * bstride + 2 + dbase + lane + 64 * k];
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < BATCH; ++u)
-      if (b + u < b1) {
-        const float f = fac[b + u];
-#pragma unroll
-        for (int k = 0; k < DPT; ++k) acc[k] = __builtin_fmaf(v[u][k], f, acc[k]);
+        for (uint32_t u = c; u < c + 16; ++u) v[u] = base[min(b + u, nb - 1) * bstride + 2 + d];
       }
-  }
 #pragma unroll
-  for (int k = 0; k < DPT; ++k) s_acc[w][lane + 64 * k] = acc[k];
-  lds_barrier();
-  // thread t now owns dim dbase + t (t < 64 DPT)
-  if (t < 64u * DPT) {
-    const float tot = ((s_acc[0][t] + s_acc[1][t]) + s_acc[2][t]) + s_acc[3][t];
-    float o = tot / sm;
-    if constexpr (ROT) {
-      __shared__ float xch[256];
-      float v1[1] = {kv8_flip(o, kv8_sign_neg(t))};
-      fwht256<1>(v1, t, xch);  // DPT = 4: all 256 threads are here
-      o = v1[0] * 0.0625f;
-    }
-    const uint32_t d = dbase + t;
-    uint16_t r;
-    if (gated && attn_gate)
-      r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
-    else
-      r = f2h(o);
-    attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
+    for (uint32_t u = 0; u < BAT; ++u)
+      if (b + u < nb) acc = __builtin_fmaf(v[u], fac[b + u], acc);
   }
+  float o = acc / s_sm;
+  if constexpr (ROT) {
+    __shared__ float xch[256];
+    float v1[1] = {kv8_flip(o, kv8_sign_neg(d))};
+    fwht256<1>(v1, d, xch);  // HD = 256: every thread of the work-group is here
+    o = v1[0] * 0.0625f;
+  }
+  uint16_t r;
+  if (gated && attn_gate)
+    r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
+  else
+    r = f2h(o);
+  attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
 template <int HD, int KV8>
@@ -537,7 +515,7 @@ int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* at
     return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
-  attn_reduce_kernel<false, 1><<<dim3(shape->q_heads, M, HD / 64), 256, 0, (hipStream_t)stream>>>(
+  attn_reduce_kernel<false><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
       ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
 }
@@ -548,7 +526,7 @@ int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float
     return mi_fail(MI_ERR_ARG, "attn_reduce_kv8: bad arguments (tgt <= 1024)");
   if (shape->head_dim != 256)
     return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: the rotation is defined for head_dim 256 only");
-  attn_reduce_kernel<true, 4><<<dim3(shape->q_heads, M, 1), 256, 0, (hipStream_t)stream>>>(
+  attn_reduce_kernel<true><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
       ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce_kv8");
 }
