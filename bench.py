@@ -514,7 +514,8 @@ def main():
                    "launch": "eager" if args.eager else "hipGraph replay",
                    "layers": desc.layers, "hidden": desc.hidden, "q_heads": desc.q_heads,
                    "kv_heads": desc.kv_heads, "head_dim": desc.head_dim, "intermediate": desc.inter,
-                   "vocab": desc.vocab, "context": args.context, "rope_theta": 1e6},
+                   "vocab": desc.vocab, "context": args.context, "rope_theta": 1e6,
+                   "attn_blocks_per_kv_head": desc.attn_tgt},
         "step_alg_bytes": step_alg,
         "step_hbm_gbs": None if ms_per_step is None else round(step_alg / (ms_per_step * 1e-3) / 1e9, 1),
         "roofline": roof,

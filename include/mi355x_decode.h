@@ -192,6 +192,16 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
                    size_t sc_head_stride, const uint32_t* pages, uint32_t page, uint32_t kv_len,
                    float* attn_part, uint32_t M, uint32_t tgt, const mi_attn_shape* shape,
                    void* stream);
+/* attn_prep (attn.cl:361-372) and attn_decode_v2 (attn_v2.cl:172-188) in one launch, f16 cache
+ * only: the decode's work-groups compute q of their heads and the new K/V rows of their block
+ * from the qkv partials themselves (the same chain as mi_attn_prep, bitwise), write each new
+ * K/V row once and the gate (gated shapes) once, and leave the same partials as
+ * mi_attn_prep followed by mi_attn_decode. M <= 8. No q is written (attn_q is internal). */
+int mi_attn_prep_decode(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
+                        const mi_attn_shape* shape, const float* q_norm, const float* k_norm,
+                        const float* rope, float* attn_gate, uint16_t* kv_k, uint16_t* kv_v,
+                        size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page,
+                        uint32_t kv_len, float* attn_part, uint32_t tgt, void* stream);
 /* attn_reduce_v2 (attn_v2.cl:383-386): ascending block merge -> attn_out f16
  * [M][q_heads*head_dim] (gated: rne(rne(o) * sigmoid(gate))) */
 int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate,

@@ -49,6 +49,16 @@ struct AttnDecodeArgs {
   uint32_t page, M, q_heads, kv_heads, tgt;
   uint32_t kv_len;  // positions the cache holds; keys past it are never read (0 = unchecked)
   float scale;
+  // the fused prep (attn_prep's work done by the decode kernel; f16 cache): the qkv partials
+  // [S][M][qkv_n] and attn_prep's parameters
+  const float* partials;
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope;
+  float* attn_gate;
+  uint32_t* ctrl_w;
+  uint32_t S, qkv_n, k_off, v_off, rot_dim, gated;
+  float eps;
 };
 
 // 8 consecutive K elements of one row, raw (f16: 16 bytes; int8: 8 bytes)
@@ -106,7 +116,15 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 //           row's V scale for int8), split into f16 high and low parts like q. The int8 (or f16)
 //           V values are exact in f16.
 // Prefetch (PF): the next group's K and V registers are loaded before the current group is used.
-template <int HD, int KV8, int GQA>
+// FP (fused prep, f16 cache): the kernel also does attn_prep's work (attn.cl:361-372) for the
+// rows it needs: q of its GQA heads from the qkv partials (fold, q-norm, RoPE), and the K and V
+// rows of the step's new positions that fall in its block (fold, k-norm, RoPE, f16), which it
+// uses in place of the cache rows; the work-group whose row owns a new position (the last block
+// of that row) writes that K/V row to the cache, block 0 writes the gate. Every value follows
+// attn_prep_kernel's chain operation for operation (the same fold order, the same 256-lane
+// norm tree, the same RoPE fma), so the partials, the cache rows and the gate are bitwise those
+// of attn_prep followed by the plain decode.
+template <int HD, int KV8, int GQA, bool FP>
 __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a) {
   constexpr uint32_t KK = HD / 32, NT = HD / 16;
   constexpr uint32_t EB = KV8 ? 1u : 2u, ROWB = HD * EB;  // bytes per row
@@ -119,6 +137,10 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
   __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
   __shared__ uint32_t s_grow[kMaxBlockGroups];
   __shared__ h8_t s_q[2][KK][64];  // q as the B operand, per lane: f16 high and low parts
+  constexpr uint32_t FPQ = FP ? GQA * HD : 1u, FPN = FP ? 8u * HD : 1u, FPW = FP ? 4u * HD : 1u;
+  __shared__ float s_q32[FPQ];                       // FP: the roped q of the GQA heads
+  __shared__ __align__(16) uint16_t s_newk[FPN], s_newv[FPN];  // FP: new K/V rows, f16
+  __shared__ float s_nrm[FPW];                       // FP: one wave's normed row (RoPE pairs)
 
   const uint32_t j = blockIdx.x, blk = blockIdx.y, m = blockIdx.z;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
@@ -195,6 +217,129 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
       s_grow[i] = a.pages[p / a.page] * a.page + p % a.page;
     }
   }
+  uint32_t pn0 = 0xFFFFFFFFu;  // FP: the block's first new position (none: past every position)
+  if constexpr (FP) {
+    // attn_prep's chain for one row of HD values, one wave: lane l holds elements l + 64 k
+    constexpr uint32_t EPL = HD / 64u;
+    const size_t pstep = (size_t)a.M * a.qkv_n;
+    auto fold = [&](uint32_t r, size_t col) {  // sum_s partials in ascending s from +0
+      const float* pp = a.partials + (size_t)r * a.qkv_n + col;
+      float v = 0.0f;
+      for (uint32_t s0 = 0; s0 < a.S; s0 += 16u) {
+        float tv[16];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) tv[u] = pp[min(s0 + u, a.S - 1u) * pstep];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) v += s0 + u < a.S ? tv[u] : 0.f;
+      }
+      return v;
+    };
+    // the normed, roped row (fp32) of partial row r at column base, RoPE row rp
+    auto prep_row = [&](uint32_t r, size_t base, const float* nw, uint32_t rp, float (&out)[EPL]) {
+      const uint32_t half = a.rot_dim / 2u;
+      const float* cs = a.rope + (size_t)rp * 2u * half;
+      // the norm weights and the RoPE pairs go out with the partials' loads
+      float wn[EPL], rc[EPL], rsn[EPL];
+#pragma unroll
+      for (uint32_t k = 0; k < EPL; ++k) {
+        const uint32_t e = lane + 64u * k;
+        wn[k] = nw ? nw[e] : 0.f;
+        rc[k] = 1.f;
+        rsn[k] = 0.f;
+        if (e < a.rot_dim) {
+          const uint32_t ii = e < half ? e : e - half;
+          rc[k] = cs[ii];
+          rsn[k] = cs[half + ii];
+        }
+      }
+      float xf[EPL], nv[EPL];
+#pragma unroll
+      for (uint32_t k = 0; k < EPL; ++k) xf[k] = h2f(f2h(fold(r, base + lane + 64u * k)));
+      if (nw) {
+        // tree_hd's order: the LDS steps (v[i] + v[i + st], st >= 64) are this lane's own
+        // elements, then the 64-lane shuffle tree; lane 0's total is broadcast
+        float sq[EPL];
+#pragma unroll
+        for (uint32_t k = 0; k < EPL; ++k) sq[k] = xf[k] * xf[k];
+        float acc;
+        if constexpr (EPL == 4) acc = (sq[0] + sq[2]) + (sq[1] + sq[3]);
+        else if constexpr (EPL == 2) acc = sq[0] + sq[1];
+        else acc = sq[0];
+#pragma unroll
+        for (int st = 32; st > 0; st >>= 1) acc += __shfl_down(acc, st, 64);
+        const float tot = __shfl(acc, 0, 64);
+        const float rstd = 1.0f / sqrtf(tot / (float)HD + a.eps);
+#pragma unroll
+        for (uint32_t k = 0; k < EPL; ++k) nv[k] = h2f(f2h(xf[k] * rstd * wn[k]));
+      } else {
+#pragma unroll
+        for (uint32_t k = 0; k < EPL; ++k) nv[k] = xf[k];
+      }
+      float* nrm = s_nrm + wave * HD;
+      wave_lds_sync();
+#pragma unroll
+      for (uint32_t k = 0; k < EPL; ++k) nrm[lane + 64u * k] = nv[k];
+      wave_lds_sync();
+#pragma unroll
+      for (uint32_t k = 0; k < EPL; ++k) {
+        const uint32_t e = lane + 64u * k;
+        if (e < half) {
+          const float tt = nrm[e + half] * rsn[k];
+          out[k] = __builtin_fmaf(nv[k], rc[k], -tt);
+        } else if (e < a.rot_dim) {
+          const float tt = nrm[e - half] * rsn[k];
+          out[k] = __builtin_fmaf(nv[k], rc[k], tt);
+        } else {
+          out[k] = nv[k];
+        }
+      }
+    };
+    // the step's new positions pos .. pos + m that fall in this block (row r = p - pos)
+    const uint32_t first_new = max(pos, p_begin);
+    const uint32_t n_new = p_end > first_new ? p_end - first_new : 0u;
+    pn0 = first_new;
+    const uint32_t QH = a.q_heads;
+    for (uint32_t it = wave; it < GQA + n_new; it += 4u) {  // uniform per wave
+      float out[EPL];
+      if (it < GQA) {  // q head j GQA + it of row m
+        const uint32_t h = j * GQA + it;
+        const size_t base = a.gated ? (size_t)h * 2u * HD : (size_t)h * HD;
+        prep_row(m, base, a.q_norm, pos + m, out);
+#pragma unroll
+        for (uint32_t k = 0; k < EPL; ++k) s_q32[it * HD + lane + 64u * k] = out[k];
+        if (a.gated && a.attn_gate && blk == 0) {
+#pragma unroll
+          for (uint32_t k = 0; k < EPL; ++k)
+            a.attn_gate[((size_t)m * QH + h) * HD + lane + 64u * k] = h2f(f2h(fold(m, base + HD + lane + 64u * k)));
+        }
+      } else {  // the new K/V row of position first_new + (it - GQA), kv head j
+        const uint32_t rl = it - GQA, r = first_new + rl - pos;
+        prep_row(r, (size_t)a.k_off + (size_t)j * HD, a.k_norm, pos + r, out);
+        uint16_t vk[EPL], vv[EPL];
+#pragma unroll
+        for (uint32_t k = 0; k < EPL; ++k) {
+          vk[k] = f2h(out[k]);
+          vv[k] = f2h(fold(r, (size_t)a.v_off + (size_t)j * HD + lane + 64u * k));
+          s_newk[rl * HD + lane + 64u * k] = vk[k];
+          s_newv[rl * HD + lane + 64u * k] = vv[k];
+        }
+        if (r == m) {  // this row's own new position: the cache row is written here, once
+          const uint32_t p = pos + r;
+          const size_t row = a.pages ? (size_t)a.pages[p / a.page] * a.page + p % a.page : (size_t)p;
+          uint16_t* kw = static_cast<uint16_t*>(const_cast<void*>(a.kv_k)) + row * a.row_stride + hoff;
+          uint16_t* vw = static_cast<uint16_t*>(const_cast<void*>(a.kv_v)) + row * a.row_stride + hoff;
+#pragma unroll
+          for (uint32_t k = 0; k < EPL; ++k) {
+            kw[lane + 64u * k] = vk[k];
+            vw[lane + 64u * k] = vv[k];
+          }
+        }
+      }
+    }
+    if (a.kv_len && pos + m >= a.kv_len && j == 0 && blk == 0 && t == 0)
+      a.ctrl_w[CTRL_DEBUG] = 0xDEAD0002u;  // attn_prep's flag: the row's position is past the cache
+    __syncthreads();
+  }
   // q as the MFMA B operand, staged once by wave 0: column qi = head (zero past GQA),
   // k = 32 kk + 8 qq + e; the waves read it from LDS per group rather than holding it
   if (wave == 0) {
@@ -202,11 +347,16 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
     for (uint32_t kk = 0; kk < KK; ++kk) {
       float v[8];
       if (qi < GQA) {
-        const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
-        const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
-        const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
-        v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-        v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+        if constexpr (FP) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = s_q32[qi * HD + 32 * kk + 8 * qq + e];
+        } else {
+          const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
+          const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
+          const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
+          v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+          v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+        }
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = 0.f;
@@ -242,6 +392,22 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
       if (gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);
     }
     const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
+    if constexpr (FP) {
+      // the step's new positions take the rows computed above (the cache may not hold them yet)
+      const uint32_t p0 = p_begin + 16u * gi;
+      if (p0 + glen > pn0) {  // uniform
+        if (qi < glen && p0 + qi >= pn0) {
+          const uint16_t* nk = s_newk + (p0 + qi - pn0) * HD;
+#pragma unroll
+          for (uint32_t kk = 0; kk < KK; ++kk) cur.k[kk].w = *reinterpret_cast<const u4_t*>(nk + 32 * kk + 8 * qq);
+        }
+        if (vrow < glen && p0 + vrow >= pn0) {
+          const unsigned char* nv = reinterpret_cast<const unsigned char*>(s_newv + (p0 + vrow - pn0) * HD);
+#pragma unroll
+          for (uint32_t i = 0; i < VLD; ++i) cur.v[i] = *reinterpret_cast<const u4_t*>(nv + vpart * (ROWB / 4u) + 16u * i);
+        }
+      }
+    }
     // stage this group's V rows (the previous group's reads of this wave's area are done:
     // one wave's LDS operations complete in order, and the fence keeps the compiler's too)
     wave_lds_sync();
@@ -445,15 +611,15 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
-template <int HD, int KV8>
+template <int HD, int KV8, bool FP>
 int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
   switch (gqa) {
-    case 1: attn_decode_wave_kernel<HD, KV8, 1><<<grid, 256, 0, st>>>(a); break;
-    case 2: attn_decode_wave_kernel<HD, KV8, 2><<<grid, 256, 0, st>>>(a); break;
-    case 4: attn_decode_wave_kernel<HD, KV8, 4><<<grid, 256, 0, st>>>(a); break;
-    case 5: attn_decode_wave_kernel<HD, KV8, 5><<<grid, 256, 0, st>>>(a); break;
-    case 6: attn_decode_wave_kernel<HD, KV8, 6><<<grid, 256, 0, st>>>(a); break;
-    case 8: attn_decode_wave_kernel<HD, KV8, 8><<<grid, 256, 0, st>>>(a); break;
+    case 1: attn_decode_wave_kernel<HD, KV8, 1, FP><<<grid, 256, 0, st>>>(a); break;
+    case 2: attn_decode_wave_kernel<HD, KV8, 2, FP><<<grid, 256, 0, st>>>(a); break;
+    case 4: attn_decode_wave_kernel<HD, KV8, 4, FP><<<grid, 256, 0, st>>>(a); break;
+    case 5: attn_decode_wave_kernel<HD, KV8, 5, FP><<<grid, 256, 0, st>>>(a); break;
+    case 6: attn_decode_wave_kernel<HD, KV8, 6, FP><<<grid, 256, 0, st>>>(a); break;
+    case 8: attn_decode_wave_kernel<HD, KV8, 8, FP><<<grid, 256, 0, st>>>(a); break;
     default: return -1;
   }
   return 0;
@@ -493,20 +659,57 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
     return mi_fail(MI_ERR_SHAPE, "attn_decode: a paged cache needs kv_len, and at most 8192 positions per block");
   if ((row_stride % 8) || (head_stride % 8))
     return mi_fail(MI_ERR_ARG, "attn_decode: KV strides must keep 8-element alignment");
-  AttnDecodeArgs a{ctrl,  attn_q,       kv_k,           kv_v,   k_scale,         v_scale,
-                   pages, attn_part,    row_stride,     head_stride, sc_row_stride, sc_head_stride,
-                   page,  M,            shape->q_heads, shape->kv_heads, tgt,    kv_len,
-                   shape->scale};
+  AttnDecodeArgs a{};
+  a.ctrl = ctrl; a.attn_q = attn_q; a.kv_k = kv_k; a.kv_v = kv_v; a.k_scale = k_scale; a.v_scale = v_scale;
+  a.pages = pages; a.attn_part = attn_part; a.row_stride = row_stride; a.head_stride = head_stride;
+  a.sc_row_stride = sc_row_stride; a.sc_head_stride = sc_head_stride; a.page = page; a.M = M;
+  a.q_heads = shape->q_heads; a.kv_heads = shape->kv_heads; a.tgt = tgt; a.kv_len = kv_len; a.scale = shape->scale;
   dim3 grid(shape->kv_heads, tgt, M);
   hipStream_t st = (hipStream_t)stream;
   if (HD == 128) {
-    if (kv_kind == 0) launch_decode<128, 0>(a, gqa, grid, st);
-    else launch_decode<128, 1>(a, gqa, grid, st);
+    if (kv_kind == 0) launch_decode<128, 0, false>(a, gqa, grid, st);
+    else launch_decode<128, 1, false>(a, gqa, grid, st);
   } else {
-    if (kv_kind == 0) launch_decode<256, 0>(a, gqa, grid, st);
-    else launch_decode<256, 1>(a, gqa, grid, st);
+    if (kv_kind == 0) launch_decode<256, 0, false>(a, gqa, grid, st);
+    else launch_decode<256, 1, false>(a, gqa, grid, st);
   }
   return mi_hip((int)hipGetLastError(), "attn_decode");
+}
+
+int mi_attn_prep_decode(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M, const mi_attn_shape* shape,
+                        const float* q_norm, const float* k_norm, const float* rope, float* attn_gate,
+                        uint16_t* kv_k, uint16_t* kv_v, size_t row_stride, size_t head_stride,
+                        const uint32_t* pages, uint32_t page, uint32_t kv_len, float* attn_part, uint32_t tgt,
+                        void* stream) {
+  if (!ctrl || !partials || !shape || !rope || !kv_k || !kv_v || !attn_part || S == 0 || M == 0 || M > 8 ||
+      tgt == 0)
+    return mi_fail(MI_ERR_ARG, "attn_prep_decode: bad arguments (M <= 8)");
+  const uint32_t HD = shape->head_dim;
+  if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: head_dim must be 128 or 256");
+  const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
+  if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads ||
+      !(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 5 || gqa == 6 || gqa == 8))
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
+  if (shape->rot_dim > HD || shape->rot_dim % 2)
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: inconsistent rotary dims");
+  if (pages && (page == 0 || page % 16))
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: a KV page holds a multiple of 16 positions");
+  if (pages && (!kv_len || mi_attn_ppw(kv_len, tgt) / 16 > kMaxBlockGroups))
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: a paged cache needs kv_len, and at most 8192 positions per block");
+  if ((row_stride % 8) || (head_stride % 8))
+    return mi_fail(MI_ERR_ARG, "attn_prep_decode: KV strides must keep 8-element alignment");
+  AttnDecodeArgs a{};
+  a.ctrl = ctrl; a.kv_k = kv_k; a.kv_v = kv_v; a.pages = pages; a.attn_part = attn_part;
+  a.row_stride = row_stride; a.head_stride = head_stride; a.page = page; a.M = M; a.q_heads = shape->q_heads;
+  a.kv_heads = shape->kv_heads; a.tgt = tgt; a.kv_len = kv_len; a.scale = shape->scale;
+  a.partials = partials; a.q_norm = q_norm; a.k_norm = k_norm; a.rope = rope; a.attn_gate = attn_gate;
+  a.ctrl_w = ctrl; a.S = S; a.qkv_n = shape->qkv_n; a.k_off = shape->k_off; a.v_off = shape->v_off;
+  a.rot_dim = shape->rot_dim; a.gated = shape->gated; a.eps = shape->eps;
+  dim3 grid(shape->kv_heads, tgt, M);
+  hipStream_t st = (hipStream_t)stream;
+  if (HD == 128) launch_decode<128, 0, true>(a, gqa, grid, st);
+  else launch_decode<256, 0, true>(a, gqa, grid, st);
+  return mi_hip((int)hipGetLastError(), "attn_prep_decode");
 }
 
 int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* attn_gate, uint16_t* attn_out,

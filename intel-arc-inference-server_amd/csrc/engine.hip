@@ -289,9 +289,9 @@ struct mi_engine {
   }
 
   // One step over M rows, enqueued on `stream` (recorded into a graph by capture()).
-  // Seven launches per layer: qkv GEMV; attn_prep; attn_decode; attn_reduce; o GEMV with
-  // the residual fold + post-attention norm fused; gate||up GEMV with silu*up fused;
-  // down GEMV with the residual fold + next norm fused.
+  // Seven launches per layer: qkv GEMV; attn_prep (or attn_prep_kv8); attn_decode;
+  // attn_reduce; o GEMV with the residual fold + post-attention norm fused; gate||up GEMV with
+  // silu*up fused; down GEMV with the residual fold + next norm fused.
   int enqueue_step(uint32_t M) {
     const uint32_t HD = d.head_dim, KVH = d.kv_heads;
     const size_t layer_kv = size_t(KVH) * d.max_len * HD;
@@ -311,6 +311,9 @@ struct mi_engine {
                               nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
         MI_TRY(mi_attn_reduce_kv8(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
       } else {
+        // attn_prep then the decode. (mi_attn_prep_decode does both in one launch with the same
+        // values, but every decode block then folds q from the qkv partials again: at context
+        // 4096, 33 blocks per kv head, that costs more than the separate launch saves.)
         uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
         uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
         MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,

@@ -162,3 +162,63 @@ def test_reduce_matches_oracle_merge_on_device_partials():
     a = O.f16_bits_to_f32(got).astype(np.float64)
     b = O.f16_bits_to_f32(ref).astype(np.float64)
     assert np.all(np.abs(a - b) <= np.maximum(np.abs(b), 2.0 ** -14) * 2.0 ** -10 * 1.01)
+
+
+@pytest.mark.parametrize("QH,KVH,HD,rot,gated,qk,paged,M,n_act,pos,tgt", [
+    (40, 8, 128, 128, False, True, False, 1, 1, 4096, 64),
+    (40, 8, 128, 128, False, False, True, 4, 3, 2045, 32),
+    (16, 2, 256, 256, False, True, False, 2, 2, 700, 128),
+    (24, 4, 256, 64, True, True, True, 3, 3, 130, 8),
+    (8, 8, 128, 64, False, True, False, 8, 8, 63, 16),
+])
+def test_prep_decode_fused_is_prep_then_decode(QH, KVH, HD, rot, gated, qk, paged, M, n_act, pos, tgt):
+    """mi_attn_prep_decode against mi_attn_prep followed by mi_attn_decode on the same inputs:
+    the partials of every active row, the whole cache (each new K/V row written once, nothing
+    else touched) and the gate, bit for bit."""
+    sh = O.attn_shape(QH, KVH, HD, rot_dim=rot, gated=gated)
+    Lm, S, P = 4224, 3, 64
+    rng = np.random.default_rng(pos + M)
+    part = rng.standard_normal((S, M, sh.qkv_n)).astype(np.float32)
+    qn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk else None
+    kn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk else None
+    rope = O.rope_table(1e6, rot, Lm)
+    pages = rng.permutation(Lm // P).astype(np.uint32) if paged else None
+    kk = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    vv = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    print(f"prep_decode QH={QH} KVH={KVH} HD={HD} rot={rot} gated={gated} M={M} n={n_act} pos={pos}", flush=True)
+    c = np.zeros(64, np.uint32)
+    c[0], c[1] = pos, n_act
+    keep = [dev(part), dev(qn), dev(kn), dev(rope), dev(pages)]
+    shp = C.byref(sh)
+    outs = []
+    for fused in (False, True):
+        ctrl = dev(c)
+        dk, dv = dev(kk), dev(vv)
+        dq = empty((M, QH, HD), np.float32)
+        dg = empty((M, QH, HD), np.float32)
+        dg.zero_()
+        dp = empty((QH, tgt, M, HD + 2), np.float32)
+        dp.zero_()
+        if fused:
+            mi.call("mi_attn_prep_decode", ptr(ctrl), ptr(keep[0]), S, M, shp, ptr(keep[1]), ptr(keep[2]),
+                    ptr(keep[3]), ptr(dg), ptr(dk), ptr(dv), HD, Lm * HD, ptr(keep[4]), P if paged else 0, Lm,
+                    ptr(dp), tgt, stream())
+        else:
+            mi.call("mi_attn_prep", ptr(ctrl), ptr(keep[0]), S, M, shp, ptr(keep[1]), ptr(keep[2]), ptr(keep[3]),
+                    ptr(dq), ptr(dg), ptr(dk), ptr(dv), HD, Lm * HD, ptr(keep[4]), P if paged else 0, Lm, stream())
+            mi.call("mi_attn_decode", ptr(ctrl), ptr(dq), 0, ptr(dk), ptr(dv), None, None, HD, Lm * HD, 0, 0,
+                    ptr(keep[4]), P if paged else 0, Lm, ptr(dp), M, tgt, shp, stream())
+        sync()
+        outs.append((host(dp, np.uint32), host(dk, np.uint16), host(dv, np.uint16), host(dg, np.uint32),
+                     host(ctrl, np.uint32)))
+    (p0, k0, v0, g0, c0), (p1, k1, v1, g1, c1) = outs
+    for m in range(n_act):
+        L = pos + m + 1
+        nb = (L - 1) // O.lib().orc_v2_ppw(L, tgt) + 1
+        nb = min(nb, tgt)
+        assert np.array_equal(p0[:, :nb, m], p1[:, :nb, m]), m
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    assert not np.array_equal(k0, kk)  # the new rows were written
+    if gated:
+        assert np.array_equal(g0[:n_act], g1[:n_act])
+    assert c0[18] == c1[18] == 0
