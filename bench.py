@@ -410,11 +410,20 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5"], default=None,
+                    help="run only that secondary measurement and print its JSON (the command the "
+                         "attention and single-GEMV kernel profiles use)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
               "use --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        fn = {"cfg1": lambda: measure_cfg1(None),
+              "cfg3": lambda: [measure_cfg3(None, L) for L in (32768, 131072)],
+              "cfg5": lambda: measure_cfg5(None)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return
 
     max_len = ((args.context + args.warmup + args.steps + 1 + 63) // 64) * 64
     desc = mi.desc_27b(max_len=max_len)

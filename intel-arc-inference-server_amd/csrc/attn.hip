@@ -531,13 +531,13 @@ __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a)
 // attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,
 // factors f_b = exp(mx_b - M), sum = sum_b sm_b f_b and acc = sum_b acc_b f_b added in
 // ascending b: mathematically the reference's sequential rescaling merge, the roundings
-// differing at the last place. grid (q_heads, M), HD threads, one dim each. The first 64
+// differing at the last place. grid (q_heads, M), HD threads, one dim each. The first PRE
 // blocks' values do not depend on the factors and are loaded before them, together with
-// wave 0's (mx, sm) loads, so a merge of up to 64 blocks is one memory round trip; further
-// blocks follow 64 at a time.
+// wave 0's (mx, sm) loads, so a merge of up to PRE blocks is one memory round trip; further
+// blocks follow 64 at a time. PRE = 64 when tgt <= 64, else 128.
 // ROT (attn_reduce_v2_kv8, kv8.cl:814-860; head_dim 256): the merged output is in the int8
 // cache's rotated basis and is un-rotated per head before the gate.
-template <bool ROT>
+template <bool ROT, uint32_t PRE>
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __restrict__ ctrl,
                                                           const float* __restrict__ attn_part,
                                                           const float* __restrict__ attn_gate,
@@ -557,7 +557,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
   const size_t bstride = (size_t)M * PART;
   // (a load past nb re-reads block nb - 1 and is not added)
-  constexpr uint32_t PRE = 64, BAT = 64;
+  constexpr uint32_t BAT = 64;
   // loads go out in runs of 16 behind a uniform bound, so a short merge issues few of them
   float v[PRE];
 #pragma unroll
@@ -718,8 +718,12 @@ int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* at
     return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
-  attn_reduce_kernel<false><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
-      ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
+  if (tgt <= 64)
+    attn_reduce_kernel<false, 64><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
+  else
+    attn_reduce_kernel<false, 128><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
 }
 
@@ -729,8 +733,12 @@ int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float
     return mi_fail(MI_ERR_ARG, "attn_reduce_kv8: bad arguments (tgt <= 1024)");
   if (shape->head_dim != 256)
     return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: the rotation is defined for head_dim 256 only");
-  attn_reduce_kernel<true><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
-      ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
+  if (tgt <= 64)
+    attn_reduce_kernel<true, 64><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
+  else
+    attn_reduce_kernel<true, 128><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
   return mi_hip((int)hipGetLastError(), "attn_reduce_kv8");
 }
 
