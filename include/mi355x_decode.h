@@ -338,6 +338,23 @@ int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
 int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);
 /* Engine::commit (engine.cc:927-960): pos = verify_pos + j + 1, cur_token[0] = next. */
 int mi_engine_commit(mi_engine* e, uint32_t verify_pos, uint32_t j, uint32_t next);
+/* ---- checkpoints (src/loader/loader.cc, quant.cc, repack.h, moe.cc; docs/13-loader.md) ----
+ * A directory with config.json and *.safetensors of a GPTQ / AutoRound int4 g64 symmetric
+ * checkpoint (quantization_config: bits 4, group_size 64, sym true, desc_act false or absent)
+ * of a Qwen3-style GQA decoder, dense or MoE with one shared expert. */
+/* The model description config.json gives (vocab padded to a multiple of 64, vocab_used the
+ * real size; attn_tgt 64; qk_norm when the checkpoint has q_norm tensors). */
+int mi_checkpoint_desc(const char* dir, uint32_t max_len, uint32_t max_rows, mi_model_desc* desc);
+/* The quantisation checks alone (quant.cc assert_quant_invariants): the config's
+ * quantization_config, then every int4 linear's shapes, qzeros, g_idx and scales; no GPU. */
+int mi_checkpoint_check(const char* dir, char* report, size_t report_len);
+/* Loads the checkpoint into an engine created from that description: q/k/v fused by columns,
+ * gate/up interleaved in 16-column blocks, MoE experts as layout-1 tiles, the router and the
+ * shared-expert gate as f16 tiles, norms fp32, embeddings f16; qzeros (all 0x77777777),
+ * g_idx (the identity) and scales (finite) checked and the first two dropped; a 16-bit or
+ * tied lm_head quantised to int4 g64 (GPTQ symmetric round-to-nearest). `report` (may be
+ * NULL) receives a one-line summary. The KV cache and the control block are untouched. */
+int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_len);
 /* server::accept_greedy (src/server/spec_accept.cc:81-85): the accepted draft count j;
  * *next = verify_argmax[j]. */
 uint32_t mi_accept_greedy(const uint32_t* verify_argmax, const uint32_t* drafts, uint32_t k,

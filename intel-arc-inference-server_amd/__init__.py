@@ -62,6 +62,9 @@ SIGNATURES = {
     "mi_embed_norm": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, f32, vp]),
     "mi_gemv_w4a16_ex": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
     "mi_engine_create": (vp, [vp, u64, vp]),
+    "mi_checkpoint_desc": (i32, [C.c_char_p, u32, u32, vp]),
+    "mi_engine_load": (i32, [vp, C.c_char_p, C.c_char_p, sz]),
+    "mi_checkpoint_check": (i32, [C.c_char_p, C.c_char_p, sz]),
     "mi_engine_destroy": (None, [vp]),
     "mi_engine_stream": (vp, [vp]),
     "mi_engine_tensor": (i32, [vp, u32, u32, C.POINTER(vp), C.POINTER(sz)]),
@@ -177,6 +180,20 @@ def moe_desc(layers, hidden, q_heads, kv_heads, head_dim, experts, top_k, moe_in
     return d
 
 
+def checkpoint_check(ckpt_dir):
+    """mi_checkpoint_check: the quantisation checks of a checkpoint directory; its report."""
+    buf = C.create_string_buffer(512)
+    check(lib().mi_checkpoint_check(os.fsencode(ckpt_dir), buf, len(buf)), "checkpoint_check")
+    return buf.value.decode()
+
+
+def checkpoint_desc(ckpt_dir, max_len, max_rows=8):
+    """mi_checkpoint_desc: the model description a checkpoint's config.json gives."""
+    d = ModelDesc()
+    check(lib().mi_checkpoint_desc(os.fsencode(ckpt_dir), max_len, max_rows, C.byref(d)), "checkpoint_desc")
+    return d
+
+
 def desc_moe_cfg4(max_len=4096 + 512):
     """a 40-layer MoE decoder, hidden 2048, 256 experts top 8 + 1 shared,
     expert intermediate 512, attention 16 q / 2 kv heads of 256, vocab 151936 (assumed; the
@@ -223,6 +240,13 @@ class Engine:
     @property
     def stream(self):
         return lib().mi_engine_stream(self._h)
+
+    def load(self, ckpt_dir):
+        """mi_engine_load: a GPTQ / AutoRound int4 g64 checkpoint directory; returns the
+        loader's one-line report."""
+        buf = C.create_string_buffer(512)
+        check(lib().mi_engine_load(self._h, os.fsencode(ckpt_dir), buf, len(buf)), "engine_load")
+        return buf.value.decode()
 
     def tensor(self, kind, layer=0):
         p, b = vp(), sz()

@@ -1,0 +1,141 @@
+"""Loading a synthetic GPTQ / AutoRound checkpoint into an engine on the GPU (mi_engine_load):
+every device tensor against the layout its format defines, computed here from the
+checkpoint's arrays (q||k||v by columns; gate/up interleaved in 16-column blocks with the
+oracle's repack.h restatement; experts as layout-1 tiles; the router as f16 tiles; norms fp32;
+embeddings f16), the int4 head quantised at load within half a scale step, and a decode step
+of the loaded model against the CPU oracle's step on the same weights."""
+import numpy as np
+import pytest
+
+import oracle as O
+from ckpt_synth import Synth
+from mipkg import mi
+from test_engine_gpu import OracleModel, argmax_ok, close
+
+pytestmark = pytest.mark.gpu
+F16 = O.ORC_F16
+
+
+def expect_interleave(a, b):
+    """repack.h interleave16 of two [rows][Np] arrays (column n: a's (n/32)16 + n%16 when
+    n % 32 < 16, else b's)"""
+    rows, Np = a.shape
+    n = np.arange(2 * Np)
+    src = (n // 32) * 16 + n % 16
+    return np.where((n % 32 < 16)[None, :], a[:, src], b[:, src])
+
+
+def load(syn, max_len=512, max_rows=4):
+    path = syn.write(split=2)
+    desc = mi.checkpoint_desc(path, max_len=max_len, max_rows=max_rows)
+    eng = mi.Engine(desc, seed=5)
+    print(f"engine_load {path}: {eng.load(path)}", flush=True)
+    return eng
+
+
+def test_dense_tensors_and_step(tmp_path):
+    syn = Synth(str(tmp_path / "d"), V=4000)
+    eng = load(syn)
+    d = eng.desc
+    H, I, Vp = d.hidden, d.inter, d.vocab
+    for li, L in enumerate(syn.layers):
+        qkv_q = np.concatenate([L["q"][0], L["k"][0], L["v"][0]], axis=1)
+        qkv_s = np.concatenate([L["q"][1], L["k"][1], L["v"][1]], axis=1)
+        assert np.array_equal(eng.to_host(mi.T_QKV_Q, li, np.uint32), qkv_q.ravel())
+        assert np.array_equal(eng.to_host(mi.T_QKV_S, li, np.uint16), qkv_s.ravel())
+        assert np.array_equal(eng.to_host(mi.T_O_Q, li, np.uint32), L["o"][0].ravel())
+        assert np.array_equal(eng.to_host(mi.T_O_S, li, np.uint16), L["o"][1].ravel())
+        gu_q = expect_interleave(L["gate"][0], L["up"][0])
+        gu_s = expect_interleave(L["gate"][1], L["up"][1])
+        # the same map as the oracle's repack.h restatement (itself pinned by the reference's twin)
+        oq = np.empty(gu_q.size, np.uint32)
+        os_ = np.empty(gu_s.size, np.uint16)
+        O.lib().orc_interleave16_l0(O._p(L["gate"][0]), O._p(L["gate"][1]), O._p(L["up"][0]), O._p(L["up"][1]),
+                                    H, I, O._p(oq), O._p(os_))
+        assert np.array_equal(oq, gu_q.ravel()) and np.array_equal(os_, gu_s.ravel())
+        assert np.array_equal(eng.to_host(mi.T_GU_Q, li, np.uint32), gu_q.ravel())
+        assert np.array_equal(eng.to_host(mi.T_GU_S, li, np.uint16), gu_s.ravel())
+        assert np.array_equal(eng.to_host(mi.T_DOWN_Q, li, np.uint32), L["down"][0].ravel())
+        for kind, key in ((mi.T_IN_NORM, "in_norm"), (mi.T_POST_NORM, "post_norm"), (mi.T_Q_NORM, "q_norm"),
+                          (mi.T_K_NORM, "k_norm")):
+            assert np.array_equal(eng.to_host(kind, li, np.float32), L[key].astype(np.float32)), key
+    emb = eng.to_host(mi.T_EMBED, 0, np.uint16).reshape(Vp, H)
+    assert np.array_equal(emb[:syn.d["V"]], O.f32_to_f16_bits(syn.embed))
+    assert not emb[syn.d["V"]:].any()
+    lmq = eng.to_host(mi.T_LM_Q, 0, np.uint32).reshape(H // 8, Vp)
+    assert np.array_equal(lmq[:, :syn.d["V"]], syn.lm[0])
+    assert np.array_equal(eng.to_host(mi.T_FINAL_NORM, 0, np.float32), syn.final_norm)
+    # a decode step of the loaded model against the oracle's on the same weights
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 100, 17
+    eng.reset(pos, tok)
+    for step in range(2):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        assert close(got[:syn.d["V"]], want[:syn.d["V"]]), step
+        assert got_tok < syn.d["V"] and argmax_ok(got_tok, want)
+        tok, pos = got_tok, pos + 1
+    eng.close()
+
+
+@pytest.mark.parametrize("tie", [False, True])
+def test_bf16_head_quantised_at_load(tmp_path, tie):
+    syn = Synth(str(tmp_path / "h"), layers=1, V=2048, head="bf16", tie=tie)
+    eng = load(syn)
+    H, V = eng.desc.hidden, 2048
+    q = eng.to_host(mi.T_LM_Q, 0, np.uint32).reshape(H // 8, V)
+    s = O.f16_bits_to_f32(eng.to_host(mi.T_LM_S, 0, np.uint16).reshape(H // 64, V)).astype(np.float64)
+    k = np.arange(H)
+    nib = ((q[k // 8, :] >> (4 * (k % 8))[:, None]) & 0xF).astype(np.float64)  # [H][V]
+    deq = (nib - 8.0) * s[k // 64, :]
+    w = syn.lm_w.astype(np.float64).T  # [H][V]
+    amax = np.abs(w).reshape(H // 64, 64, V).max(axis=1)
+    want_s = O.f16_bits_to_f32(O.f32_to_f16_bits((2 * amax / 15).astype(np.float32))).astype(np.float64)
+    assert np.array_equal(s, want_s)
+    # round to nearest within the clamp range [-8, 7] s: |w - deq| <= s / 2, plus 7.5 times the
+    # f16 rounding of s at a group's positive extreme (amax = 7.5 s exactly before rounding)
+    err = np.abs(w - deq)
+    assert np.all(err <= 0.5 * s[k // 64, :] * (1 + 2 * 7.5 * 2.0 ** -11) + 1e-12)
+    eng.close()
+
+
+def test_moe_tensors(tmp_path):
+    syn = Synth(str(tmp_path / "m"), layers=1, H=512, experts=16, top_k=4, moe_inter=128, V=2048)
+    eng = load(syn)
+    H, E, MI = 512, 16, 128
+    L = syn.layers[0]
+    rn = (E + 1 + 15) // 16 * 16
+    rows = np.zeros((rn, H), np.float32)
+    rows[:E + 1] = L["router"]
+    rt = np.empty(rn * H, np.uint16)
+    O.lib().orc_f16w_tile(O._p(O.f32_to_f16_bits(rows)), H, rn, O._p(rt))
+    assert np.array_equal(eng.to_host(mi.T_ROUTER, 0, np.uint16), rt)
+    gu = eng.to_host(mi.T_MOE_GU, 0, np.uint32)
+    dn = eng.to_host(mi.T_MOE_DN, 0, np.uint32)
+    gub = (2 * MI // 16) * (H // 64) * 136
+    dnb = (H // 16) * (MI // 64) * 136
+    for e in (0, 7, E):  # two routed experts and the shared one (block E)
+        (gq, gs), (uq, us), (dq, ds) = L["experts"][e]
+        iq = np.ascontiguousarray(expect_interleave(gq, uq))
+        is_ = np.ascontiguousarray(expect_interleave(gs, us))
+        want = np.empty(gub, np.uint32)
+        O.lib().orc_repack_layout1(O._p(iq), O._p(is_), H, 2 * MI, O._p(want))
+        assert np.array_equal(gu[e * gub:(e + 1) * gub], want), e
+        want = np.empty(dnb, np.uint32)
+        O.lib().orc_repack_layout1(O._p(np.ascontiguousarray(dq)), O._p(np.ascontiguousarray(ds)), MI, H, O._p(want))
+        assert np.array_equal(dn[e * dnb:(e + 1) * dnb], want), e
+    eng.close()
+
+
+def test_mismatched_engine_is_refused(tmp_path):
+    syn = Synth(str(tmp_path / "x"), layers=1, V=2048)
+    path = syn.write()
+    desc = mi.checkpoint_desc(path, max_len=256)
+    desc.inter = 2048  # not the checkpoint's
+    eng = mi.Engine(desc, seed=1)
+    with pytest.raises(mi.MiError) as e:
+        eng.load(path)
+    assert "does not match config.json" in str(e.value)
+    eng.close()
