@@ -93,7 +93,7 @@ int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_
  * and the lm_head fold + argmax_stage1, src/kernels/prep.cl:288-384, argmax.cl:82).
  * `counters`: >= N/64 + 1 zeroed uint32 words; every launch leaves them zeroed again.
  * Launches that share one counter array must not overlap. */
-enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3 };
+enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3, MI_EPI_F16OUT = 4 };
 typedef struct mi_gemv_epilogue {
   uint32_t kind;
   uint32_t* counters;
@@ -113,6 +113,9 @@ typedef struct mi_gemv_epilogue {
   float* logits;
   void* argmax_part;
   uint32_t vocab_used;
+  /* F16OUT: out16 [M][N] = rne_f16(sum_s partials), the fold of mi_fold_partials in the
+   * GEMV launch (a plain linear with 16-bit output) */
+  uint16_t* out16;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,

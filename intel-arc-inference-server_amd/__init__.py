@@ -87,14 +87,14 @@ SIGNATURES = {
 }
 
 
-EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS = 0, 1, 2, 3
+EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS, EPI_F16OUT = 0, 1, 2, 3, 4
 
 
 class GemvEpilogue(C.Structure):
     """mi_gemv_epilogue"""
     _fields_ = [("kind", u32), ("counters", vp), ("resid", vp), ("sumsq", vp), ("rstd", vp),
                 ("next_norm_w", vp), ("x_next", vp), ("eps", f32), ("h", vp), ("logits", vp),
-                ("argmax_part", vp), ("vocab_used", u32)]
+                ("argmax_part", vp), ("vocab_used", u32), ("out16", vp)]
 
 
 class MiError(RuntimeError):

@@ -92,9 +92,10 @@ struct GemvEpi {
   u2_t* argmax_part;      // LOGITS: [M][N/64] (value bits, index), or NULL
   uint32_t vocab_used;    // LOGITS
   float eps;              // RESID
+  uint16_t* out16;        // F16OUT: [M][N]
 };
 
-enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3 };
+enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3, EPI_F16OUT = 4 };
 
 // argmax.cl:63-65: strictly greater wins, an exact tie keeps the lower index
 __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
@@ -305,6 +306,11 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
       epi.h[(size_t)row * (N / 2) + k] = f2h(h2f(s_b) * h2f(u_b));
     }
+  } else if constexpr (EPI == EPI_F16OUT) {
+    for (uint32_t row = wave; row < M; row += kWaves) {
+      const uint32_t n = n0 + lane;
+      epi.out16[(size_t)row * N + n] = f2h(fold(row, n));
+    }
   } else if constexpr (EPI == EPI_LOGITS) {
     for (uint32_t row = wave; row < M; row += kWaves) {
       const uint32_t n = n0 + lane;
@@ -426,7 +432,7 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   if (!ep) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: null epilogue");
   hipStream_t st = static_cast<hipStream_t>(stream);
   GemvEpi e{ep->counters, ep->resid, ep->sumsq, ep->rstd, ep->next_norm_w, ep->x_next, ep->h,
-            ep->logits, reinterpret_cast<u2_t*>(ep->argmax_part), ep->vocab_used, ep->eps};
+            ep->logits, reinterpret_cast<u2_t*>(ep->argmax_part), ep->vocab_used, ep->eps, ep->out16};
   int r;
   switch (ep->kind) {
     case MI_EPI_PARTIALS:
@@ -445,6 +451,10 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
       if (!e.counters || !e.out32 || e.vocab_used > N)
         return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex LOGITS: counters, logits, vocab_used <= N");
       r = launch_rows<EPI_LOGITS>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    case MI_EPI_F16OUT:
+      if (!e.counters || !e.out16) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex F16OUT: counters, out16");
+      r = launch_rows<EPI_F16OUT>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     default:
       return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: unknown epilogue");

@@ -116,6 +116,29 @@ def test_logits_epilogue_and_argmax(M):
     assert list(cc[10:10 + M]) == [O.argmax(want[m], used) for m in range(M)]
 
 
+@pytest.mark.parametrize("M,S", [(1, 8), (3, 4)])
+def test_f16out_epilogue_is_gemv_then_fold(M, S):
+    """MI_EPI_F16OUT: the fold of the S partials to fp16 inside the GEMV launch, bitwise
+    mi_gemv_w4a16 followed by mi_fold_partials (the oracle's fold: ascending s from +0)."""
+    K = N = 4096
+    qw, sc = rand_w(K, N, 50 + M)
+    x = O.f32_to_f16_bits(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    part = partials_of(dq, ds, dx, M, K, N, S)
+    want = np.zeros((M, N), np.float32)
+    for s in range(S):
+        want = want + part[s]
+    ctr = dev(np.zeros(N // 64 + 1, np.uint32))
+    out = empty((M, N), np.uint16)
+    dpart = empty((S, M, N), np.float32)
+    ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, counters=ptr(ctr), out16=ptr(out))
+    for _ in range(2):  # the counters reset themselves: a second launch gives the same bits
+        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        sync()
+        assert not host(ctr, np.uint32).any()
+        assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want))
+
+
 def test_embed_norm_bitwise():
     V, H, M = 512, 5120, 2
     rng = np.random.default_rng(4)
