@@ -214,9 +214,9 @@ def measure_cfg1(st):
         mi.check(L.mi_fold_partials(part, out, None, S, 1, N, st))
     # one launch: the GEMV with the fp16 fold as its epilogue (split-K capped for the fold)
     S1 = L.mi_gemv_pick_s_ex(K, N, mi.EPI_F16OUT)
-    ctr = D.upload(np.zeros(N // 64 + 1, np.uint32))  # the tile counters start (and stay) at zero
     part1 = D.alloc(S1 * N * 4)
-    ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, counters=ctr.value, out16=out.value)
+    mi.check(L.mi_gemv_handoff_init(part1, S1 * N, st))  # hand-off words: empty on entry and after each call
+    ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, out16=out.value)
     fused = lambda i: mi.check(L.mi_gemv_w4a16_ex(qw[i % copies], sc[i % copies], x, part1, 1, K, N, S1,
                                                   C.byref(ep), st))
     t_call = time_calls(st, call, 192)

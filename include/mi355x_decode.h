@@ -88,18 +88,19 @@ int mi_int4_dequant(const uint32_t* qweight, const uint16_t* scales, float* out,
  * partials fp32 [S][M][N]. 1 <= M <= 16, 64 | K, 64 | N, S | K/64. ---- */
 int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                   float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S, void* stream);
-/* The same linear with the step's next operation fused into its last work-group per
+/* The same linear with the step's next operation fused into one consumer work-group per
  * 64-column tile (the reference's consumers prep_res_fold + prep_norm_finish, prep_silu_mul
  * and the lm_head fold + argmax_stage1, src/kernels/prep.cl:288-384, argmax.cl:82).
- * `counters`: >= N/64 + 1 zeroed uint32 words; every launch leaves them zeroed again.
- * Launches that share one counter array must not overlap. */
+ * Hand-off words: for a fused kind, partials[0 .. (S-1)*M*N) (and RESID's sumsq) must hold
+ * the empty pattern of mi_gemv_handoff_init on entry; every launch leaves them so. Launches
+ * that share hand-off words must not overlap. */
 enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3, MI_EPI_F16OUT = 4 };
 typedef struct mi_gemv_epilogue {
   uint32_t kind;
-  uint32_t* counters;
-  /* RESID (N = hidden): resid [M][N] += rne(sum_s partials) (rounded as prep_res_fold);
-   * sumsq [N/64][M] the 64-column tiles' sums of squares; then rstd [M] =
-   * 1/sqrt(sum_g sumsq / N + eps) and x_next [M][N] = rne(resid * rstd * next_norm_w). */
+  /* RESID (N = hidden <= 16384): resid [M][N] += rne(sum_s partials) (rounded as
+   * prep_res_fold); the 64-column tiles' sums of squares go through sumsq, hand-off words
+   * [N/64][M][N/64]; then rstd [M] = 1/sqrt(sum_g sumsq_g / N + eps) and x_next [M][N] =
+   * rne(resid * rstd * next_norm_w). */
   uint16_t* resid;
   float* sumsq;
   float* rstd;
@@ -123,9 +124,12 @@ int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint
 /* The split-K width this library uses for a shape (the role of kQwen38Tuning,
  * src/model/model_desc.cc:32, and kSmallMTuning, src/kernels/kernels.h:140-170). */
 uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N);
-/* The split-K width for a launch with epilogue kind `epilogue` (MI_EPI_*): the plain
- * choice for MI_EPI_PARTIALS, at most 8 for the fused epilogues (same role as above). */
+/* The split-K width for a launch with epilogue kind `epilogue` (MI_EPI_*); today the plain
+ * choice for every kind (same role as above). */
 uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue);
+/* Writes the empty pattern into n hand-off words (a fused launch's partials, RESID's sumsq).
+ * Needed once per buffer: every fused launch leaves its words empty again. */
+int mi_gemv_handoff_init(float* words, size_t n, void* stream);
 /* out = sum_s partials[s] (ascending from 0.f), as fp16 and/or fp32 (the host fold of
  * tests/kernels/gemv_harness.h:59-120, on the device) */
 int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,

@@ -42,6 +42,7 @@ SIGNATURES = {
     "mi_gemv_pick_s": (u32, [u32, u32]),
     "mi_gemv_pick_s_ex": (u32, [u32, u32, u32]),
     "mi_fold_partials": (i32, [vp, vp, vp, u32, u32, u32, vp]),
+    "mi_gemv_handoff_init": (i32, [vp, sz, vp]),
     "mi_stream_read": (i32, [vp, sz, vp, vp]),
     "mi_res_fold": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_norm_finish": (i32, [vp, vp, vp, vp, u32, u32, u32, f32, vp]),
@@ -92,7 +93,7 @@ EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS, EPI_F16OUT = 0, 1, 2, 3, 4
 
 class GemvEpilogue(C.Structure):
     """mi_gemv_epilogue"""
-    _fields_ = [("kind", u32), ("counters", vp), ("resid", vp), ("sumsq", vp), ("rstd", vp),
+    _fields_ = [("kind", u32), ("resid", vp), ("sumsq", vp), ("rstd", vp),
                 ("next_norm_w", vp), ("x_next", vp), ("eps", f32), ("h", vp), ("logits", vp),
                 ("argmax_part", vp), ("vocab_used", u32), ("out16", vp)]
 

@@ -92,20 +92,19 @@ struct mi_engine {
   uint16_t* x = nullptr;
   uint16_t* hbuf = nullptr;
   uint16_t* attn_out = nullptr;
-  float* part = nullptr;
-  float* sumsq = nullptr;
+  float* part = nullptr;     // the plain launches' split-K partials (qkv)
+  float* part_ex = nullptr;  // the fused launches' hand-off words (empty between launches)
+  float* sumsq = nullptr;    // RESID's hand-off words for the tiles' sums of squares
   float* attn_q = nullptr;
   float* attn_part = nullptr;
   float* logits = nullptr;
   void* argmax_part = nullptr;
-  uint32_t* counters = nullptr;  // the fused GEMV epilogues' tile counters (self-resetting)
   float* rstd = nullptr;
   float* moe_logits = nullptr;   // [max_rows][router_n]
   uint32_t* moe_route = nullptr; // [max_rows][MI_MOE_ROUTE_WORDS]
   uint16_t* moe_h = nullptr;     // [max_rows][top_k + 1][moe_inter]
   uint32_t router_n = 0;
   size_t gu_block = 0, dn_block = 0;  // u32 per expert block
-  uint32_t norm_g = 20;
   mi_attn_shape ash{};
   hipGraphExec_t graphs[17] = {};
 
@@ -150,9 +149,8 @@ struct mi_engine {
     ash = mi_attn_shape{QH, KVH, HD, m.rot_dim, 0u, qkv_n, QH * HD, (QH + KVH) * HD,
                         1.0f / std::sqrt(float(HD)), m.rms_eps};
     ash.scale = float(1.0 / std::sqrt(double(HD)));
-    norm_g = H / 64;  // the fused epilogues take the residual's sum of squares in 64-element chunks
     layer.resize(m.layers);
-    size_t part_max = 0;
+    size_t part_max = 0, part_ex_max = 1;
     const bool moe = m.experts > 0;
     if (moe) {
       router_n = (m.experts + 1 + 15) / 16 * 16;
@@ -176,11 +174,12 @@ struct mi_engine {
         MI_TRY(alloc(&L.q_norm, HD));
         MI_TRY(alloc(&L.k_norm, HD));
       }
-      for (const Linear* l : {&L.qkv, &L.o, &L.gate_up, &L.down})
-        if (l->q) part_max = std::max(part_max, size_t(l->S) * R * l->N);
+      if (L.qkv.q) part_max = std::max(part_max, size_t(L.qkv.S) * R * L.qkv.N);
+      for (const Linear* l : {&L.o, &L.gate_up, &L.down})
+        if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S - 1) * R * l->N);
     }
     MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
-    part_max = std::max(part_max, size_t(lm_head.S) * R * m.vocab);
+    part_ex_max = std::max(part_ex_max, size_t(lm_head.S - 1) * R * m.vocab);
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
     MI_TRY(alloc(&final_norm, H));
     MI_TRY(alloc(&rope, size_t(m.max_len) * m.rot_dim));
@@ -203,14 +202,15 @@ struct mi_engine {
     MI_TRY(alloc(&hbuf, size_t(R) * m.inter));
     MI_TRY(alloc(&attn_out, size_t(R) * QH * HD));
     MI_TRY(alloc(&part, part_max));
-    MI_TRY(alloc(&sumsq, size_t(norm_g) * R));
+    MI_TRY(alloc(&part_ex, part_ex_max));
+    MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_max, stream));
+    const size_t sumsq_n = size_t(H / 64) * R * (H / 64);
+    MI_TRY(alloc(&sumsq, sumsq_n));
+    MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
     MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
     MI_TRY(alloc(&attn_part, size_t(QH) * m.attn_tgt * R * (HD + 2)));
     MI_TRY(alloc(&logits, size_t(R) * m.vocab));
     MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * (m.vocab / 64 + mi_argmax_groups(m.vocab))));
-    const size_t max_tiles = std::max<size_t>({qkv_n, 2 * size_t(m.inter), size_t(m.vocab), size_t(H)}) / 64 + 1;
-    MI_TRY(alloc(&counters, max_tiles));
-    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(counters, 0, max_tiles * 4, stream)), "counters clear"));
     MI_TRY(alloc(&rstd, R));
     if (moe) {
       MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
@@ -278,7 +278,6 @@ struct mi_engine {
   mi_gemv_epilogue resid_epi(const float* next_w) const {
     mi_gemv_epilogue e{};
     e.kind = MI_EPI_RESID;
-    e.counters = counters;
     e.resid = resid;
     e.sumsq = sumsq;
     e.rstd = rstd;
@@ -323,7 +322,7 @@ struct mi_engine {
         MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
       }
       const mi_gemv_epilogue eo = resid_epi(L.post_norm);
-      MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part, M, L.o.K, L.o.N, L.o.S, &eo, stream));
+      MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream));
       const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
       if (d.experts) {
         // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
@@ -337,20 +336,18 @@ struct mi_engine {
       }
       mi_gemv_epilogue eg{};
       eg.kind = MI_EPI_SILU;
-      eg.counters = counters;
       eg.h = hbuf;
-      MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
+      MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                               stream));
       const mi_gemv_epilogue ed = resid_epi(next_w);
-      MI_TRY(mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part, M, L.down.K, L.down.N, L.down.S, &ed, stream));
+      MI_TRY(mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream));
     }
     mi_gemv_epilogue el{};
     el.kind = MI_EPI_LOGITS;
-    el.counters = counters;
     el.logits = logits;
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
-    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
+    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
     MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
     return 0;
   }

@@ -29,24 +29,35 @@
 // rows - every output element is its own MFMA dot and the same fixed merges - so S and
 // the wave split are functions of the shape only (mi_gemv_pick_s).
 //
-// Fused epilogues (mi_gemv_w4a16_ex). The work-groups of one 64-column tile count
-// themselves in a self-resetting counter; the last one to finish folds the tile's S
-// partials in ascending s (the consumer's fold of gemv.cl:1-10, so the result does not
-// depend on which work-group is last) and applies the step's next operation:
+// Fused epilogues (mi_gemv_w4a16_ex). Slice S-1 of each 64-column tile is its consumer:
+// the other slices write their partials and exit, and the consumer, dispatched after all of
+// them, folds the tile's S partials in ascending s (the consumer's fold of gemv.cl:1-10; its
+// own slice is the last term and never leaves LDS) and applies the step's next operation:
 //   RESID   resid = rne(resid + rne(sum_s part)) and the tile's sum of squares (the
-//           reference's res_fold at 64-element chunks, prep_ref.h:120-156); the last tile
-//           of the launch then forms rstd = 1/sqrt(sum_g sumsq / N + eps) and the next
-//           RMSNorm's x = rne(r * rstd * w) (norm_finish, prep_ref.h:158-168);
+//           reference's res_fold at 64-element chunks, prep_ref.h:120-156); every consumer
+//           then sums all tiles' sums in ascending tile order, forms rstd = 1/sqrt(sum / N +
+//           eps) and writes its own tile of the next RMSNorm's x = rne(r * rstd * w)
+//           (norm_finish, prep_ref.h:158-168);
 //   SILU    h = rne(rne(silu(rne(g))) * rne(u)) over the interleave16 gate||up columns
 //           (prep_silu_mul, prep_ref.h:170-189);
 //   LOGITS  fp32 logits and the tile's (max, lowest index) for argmax_stage2
-//           (argmax.cl:63-65's comparator; the vocab_used mask).
-// Hand-off between the work-groups of one launch: the partials, the tiles' sums of squares
-// and the folded residual are written and read with device-coherent (sc1) accesses; each
-// thread waits for its own stores to complete before the work-group increments the
-// counter (a relaxed device-scope integer atomic), so the last arrival reads complete data.
-// No whole-L2 writeback or invalidate is needed (an agent-scope fence would emit both in
-// every work-group). No float atomics: replays stay bitwise identical.
+//           (argmax.cl:63-65's comparator; the vocab_used mask);
+//   F16OUT  the fold rounded to fp16.
+// Hand-off without counters or fences: the hand-off words (partials; RESID's per-consumer
+// copies of the tile sums) hold the empty pattern 0xFFFFFFFF between launches - a NaN that
+// fp32 arithmetic on fp16 data never produces (a computed value with those bits is stored as
+// the canonical NaN). Producers store with device-coherent (sc1) single-word stores and
+// exit without waiting; a consumer polls each word with device-coherent loads until it is
+// not empty, then writes the empty pattern back, so every launch leaves the words as it
+// found them. A polled word is either empty or final, so no ordering between words is
+// needed. Deadlock freedom: each XCD dispatches its share of the grid in linear order and
+// the consumers are the grid's last row, so every producer is resident or done before a
+// consumer on its XCD waits; RESID's consumers also wait on each other, which needs all N/64
+// of them resident at once (N <= 16384: at most 256 work-groups). A bounded poll ends a
+// wait that never completes with the empty NaN in the result instead of a hang.
+// No float atomics: replays stay bitwise identical.
+#include <algorithm>
+
 #include "mi_common.h"
 #include "mi_capi_internal.h"
 
@@ -81,9 +92,8 @@ __device__ __forceinline__ h8_t perm_x(u4_t v) {
 }
 
 struct GemvEpi {
-  uint32_t* counters;     // >= N/64 + 1 words, zero between launches
   uint16_t* resid;        // RESID: [M][N]
-  float* sumsq;           // RESID: [N/64][M]
+  float* sumsq;           // RESID: [N/64][M][N/64], empty between launches
   float* rstd;            // RESID: [M]
   const float* next_w;    // RESID: the next RMSNorm's fp32 weights [N]
   uint16_t* x_next;       // RESID: [M][N]
@@ -102,18 +112,57 @@ __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t
   return (av > bv) || (av == bv && ai < bi);
 }
 
-// true in the work-group that arrives last at counter `c` (`total` arrivals); resets it.
-// Callers write everything the last arrival reads with st_agent before calling.
-__device__ __forceinline__ bool last_arrival(uint32_t* c, uint32_t total, uint32_t* s_flag) {
-  wait_memory();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = prev == total - 1u;
-    if (*s_flag) st_agent(c, 0u);
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;  // a hand-off word with no value yet
+// floats of LDS a consumer polls into per round (16 KB at 16 rows: two slices a round at 2048)
+template <int MR>
+constexpr int fold_buf() { return 2048; }
+constexpr uint32_t kPollLimit = 1u << 21; // polls of one word before giving up (~seconds)
+
+__device__ __forceinline__ float empty_f() { return __builtin_bit_cast(float, kEmpty); }
+__device__ __forceinline__ bool is_empty(float v) { return __builtin_bit_cast(uint32_t, v) == kEmpty; }
+// a computed value never goes out with the empty pattern (it stays a NaN)
+__device__ __forceinline__ float publishable(float v) {
+  return is_empty(v) ? __builtin_bit_cast(float, 0x7FC00000u) : v;
+}
+
+// dst[e] = the hand-off word of element e < cnt (cnt <= BUF) once it is not empty; then the
+// word is emptied again. Element e = t + 256 u (t = threadIdx.x) sits at byte offset
+// voff + u * ustride from base: buffer accesses with a per-thread 32-bit offset and a uniform
+// one per u keep the addresses out of 64-bit registers. sc1 makes them the device-coherent
+// accesses of ld_agent / st_agent. The whole work-group calls this; dst is LDS.
+template <int BUF>
+__device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base, uint32_t voff,
+                                          uint32_t ustride) {
+  constexpr int PER = BUF / 256;
+  constexpr int kSc1 = 16;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7FFFFFFF, 0x00020000);
+  const uint32_t t = threadIdx.x;
+  uint32_t v[PER];
+  uint32_t pending = 0;  // bit u: element t + 256 u still empty
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (t + 256u * u < cnt) v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, u * ustride, kSc1);
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (t + 256u * u < cnt && v[u] == kEmpty) pending |= 1u << u;
+  // re-poll every still-empty word together, so a wait costs one round trip per poll, not per word
+  for (uint32_t n = 0; pending && n < kPollLimit; ++n) {
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      if (pending & (1u << u)) v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, u * ustride, kSc1);
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      if ((pending & (1u << u)) && v[u] != kEmpty) pending &= ~(1u << u);
   }
-  __syncthreads();
-  return *s_flag != 0u;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const uint32_t e = t + 256u * u;
+    if (e < cnt) {
+      dst[e] = __builtin_bit_cast(float, v[u]);
+      __builtin_amdgcn_raw_buffer_store_b32(kEmpty, rs, voff, u * ustride, kSc1);
+    }
+  }
 }
 
 // MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue.
@@ -126,7 +175,6 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
                                                          GemvEpi epi) {
   constexpr int RR = MR < 4 ? MR : 4;  // accumulator rows a lane holds (rows 4*(l/16) + r)
   __shared__ float red[kWaves][MR][kCols];
-  __shared__ uint32_t s_flag;
 
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t c4 = lane & 15u, q = lane >> 4;
@@ -201,6 +249,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   }
   __syncthreads();
   const uint32_t total = M * kCols;
+  const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
+  const bool consumer = EPI != EPI_PARTIALS && s + 1 == S;
   for (uint32_t i = threadIdx.x; i < total; i += 256u) {
     const uint32_t row = i / kCols, col = i % kCols;
     float v = red[0][row][col];
@@ -208,113 +258,115 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     for (int w = 1; w < kWaves; ++w) v += red[w][row][col];
     if constexpr (EPI == EPI_PARTIALS)
       partials[((size_t)s * M + row) * N + n0 + col] = v;
+    else if (consumer)
+      red[0][row][col] = v;  // the consumer's own slice stays in LDS
     else
-      st_agent(partials + ((size_t)s * M + row) * N + n0 + col, v);
+      st_agent(partials + ((size_t)s * M + row) * N + n0 + col, publishable(v));
   }
-  if constexpr (EPI == EPI_PARTIALS) return;
+  if (!consumer) return;
 
-  // ---- the tile's last work-group folds the S partials and applies the epilogue ----
-  const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
-  if (!last_arrival(epi.counters + tile, S, &s_flag)) return;
-  const uint32_t t = threadIdx.x;
-  // sum_s partials[s][row][n] from 0.f in ascending s; the loads go out 8 at a time
-  auto fold = [&](uint32_t row, uint32_t n) {
-    const float* p = partials + (size_t)row * N + n;
-    const size_t step = (size_t)M * N;
-    float a = 0.f;
-    uint32_t ss = 0;
-    for (; ss + 8 <= S; ss += 8) {
-      float v[8];
+  // ---- the tile's consumer folds the S partials and applies the epilogue ----
+  // RESID: the residual and the next norm's weights for rows wave, wave + 4, ... (at most 4
+  // of them) go out before the fold's round trips
+  uint16_t r_pre[(MR + kWaves - 1) / kWaves];
+  float w_pre = 0.f;
+  if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = ld_agent(p + (ss + u) * step);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) a += v[u];
+    for (int k = 0; k < (MR + kWaves - 1) / kWaves; ++k) {
+      const uint32_t row = wave + kWaves * k;
+      if (row < M) r_pre[k] = epi.resid[(size_t)row * N + n0 + lane];
     }
-    for (; ss < S; ++ss) a += ld_agent(p + ss * step);
-    return a;
-  };
+    w_pre = epi.next_w[n0 + lane];
+  }
+  constexpr int kFoldBuf = fold_buf<MR>();
+  __shared__ float s_fold[kFoldBuf];
+  const uint32_t t = threadIdx.x;
+  {
+    // sum_s partials[s][row][n] from 0.f in ascending s; slices 0 .. S-2 are polled in rounds
+    // of `per_round` slices, slice S-1 is this work-group's own (red[0])
+    // (thread t folds elements t + 256 u of the tile's M x 64)
+    constexpr int EL = MR * kCols / 256 > 0 ? MR * kCols / 256 : 1;
+    const uint32_t per_round = kFoldBuf / total;
+    float a[EL];
+#pragma unroll
+    for (int u = 0; u < EL; ++u) a[u] = 0.f;
+    for (uint32_t s0 = 0; s0 + 1 < S; s0 += per_round) {
+      const uint32_t ns = min(per_round, S - 1 - s0);
+      // element e: row-slice e / 64 of slices s0.., column e % 64 (e / 64 = t / 64 + 4 u)
+      poll_into<kFoldBuf>(s_fold, ns * total, partials + (size_t)s0 * M * N,
+                          ((t / kCols) * N + n0 + t % kCols) * 4u, 4u * N * 4u);
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < EL; ++u) {
+        const uint32_t i = t + 256u * u;
+        if (i < total)
+          for (uint32_t j = 0; j < ns; ++j) a[u] += s_fold[j * total + i];
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < EL; ++u) {
+      const uint32_t i = t + 256u * u;
+      if (i < total) red[0][i / kCols][i % kCols] = a[u] + red[0][i / kCols][i % kCols];
+    }
+    __syncthreads();
+  }
+  auto folded = [&](uint32_t row, uint32_t col) { return red[0][row][col]; };
+
   if constexpr (EPI == EPI_RESID) {
     // one row per wave per pass, a column per lane; the 64-lane tree is the reference's
     // 256-lane tree over a 64-element chunk (lanes 64..255 add exact zeros)
-    for (uint32_t row = wave; row < M; row += kWaves) {
-      const uint32_t n = n0 + lane;
-      uint16_t* rp = epi.resid + (size_t)row * N + n;
-      const uint16_t rb = f2h(h2f(*rp) + h2f(f2h(fold(row, n))));
-      st_agent(rp, rb);
+#pragma unroll
+    for (int k = 0; k < (MR + kWaves - 1) / kWaves; ++k) {
+      const uint32_t row = wave + kWaves * k;
+      if (row >= M) break;
+      const uint16_t rb = f2h(h2f(r_pre[k]) + h2f(f2h(folded(row, lane))));
+      epi.resid[(size_t)row * N + n0 + lane] = rb;
       const float v = h2f(rb);
+      red[1][row][lane] = v;
       float a = __builtin_fmaf(v, v, 0.f);
 #pragma unroll
       for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
-      if (lane == 0) st_agent(epi.sumsq + (size_t)tile * M + row, a);
+      a = publishable(__shfl(a, 0, 64));
+      // every consumer c gets its own copy: sumsq[c][row][tile]
+      for (uint32_t c = lane; c < ntiles; c += 64u) st_agent(epi.sumsq + ((size_t)c * M + row) * ntiles + tile, a);
     }
-    // the launch's last tile: rstd per row and the next norm's input
-    if (!last_arrival(epi.counters + ntiles, ntiles, &s_flag)) return;
-    // the tiles' sums, loaded in parallel, then added in ascending tile order
-    __shared__ __align__(16) float s_ss[1024];
+    // all tiles' sums of this launch: sumsq[tile][row][g], g ascending, polled in rounds of rows
     __shared__ float s_rstd[16];
-    for (uint32_t row = 0; row < M; ++row) {
-      for (uint32_t g = t; g < ntiles; g += 256u) s_ss[g] = ld_agent(epi.sumsq + (size_t)g * M + row);
+    const uint32_t rows_per_round = kFoldBuf / ntiles;
+    for (uint32_t r0 = 0; r0 < M; r0 += rows_per_round) {
+      const uint32_t nr = min(rows_per_round, M - r0);
+      poll_into<kFoldBuf>(s_fold, nr * ntiles, epi.sumsq + ((size_t)tile * M + r0) * ntiles, t * 4u, 1024u);
       __syncthreads();
-      if (t == 0) {
+      if (t < nr) {
+        const float* ss = s_fold + t * ntiles;
         float tot = 0.f;
-        uint32_t g = 0;
-        for (; g + 16u <= ntiles; g += 16u) {
-          f4_t v[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f4_t*>(s_ss + g + 4u * u);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) tot = ((tot + v[u][0]) + v[u][1] + v[u][2]) + v[u][3];
-        }
-        for (; g < ntiles; ++g) tot += s_ss[g];
-        const float r = 1.0f / sqrtf(tot / (float)N + epi.eps);
-        s_rstd[row] = r;
+        for (uint32_t g = 0; g < ntiles; ++g) tot += ss[g];
+        s_rstd[r0 + t] = 1.0f / sqrtf(tot / (float)N + epi.eps);
       }
       __syncthreads();
     }
-    for (uint32_t row = 0; row < M; ++row) {
-      const float r = s_rstd[row];
-      const uint16_t* rr = epi.resid + (size_t)row * N;
-      uint16_t* xo = epi.x_next + (size_t)row * N;
-      const uint32_t nq = N / 4u;
-      const uint64_t* rq = reinterpret_cast<const uint64_t*>(rr);
-      for (uint32_t q0 = t; q0 < nq; q0 += 8u * 256u) {
-        uint64_t v[8];
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) v[u] = ld_agent(rq + min(q0 + u * 256u, nq - 1u));
-#pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) {
-          const uint32_t q = q0 + u * 256u;
-          if (q < nq) {
-            const f4_t wv = *reinterpret_cast<const f4_t*>(epi.next_w + 4u * q);
-            uint64_t o = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              o |= (uint64_t)f2h(h2f((uint16_t)(v[u] >> (16 * j))) * r * wv[j]) << (16 * j);
-            reinterpret_cast<uint64_t*>(xo)[q] = o;
-          }
-        }
-      }
+    for (uint32_t row = wave; row < M; row += kWaves) {
+      const uint32_t n = n0 + lane;
+      epi.x_next[(size_t)row * N + n] = f2h(red[1][row][lane] * s_rstd[row] * w_pre);
     }
-    // rstd goes out last: a global store before a barrier would make the barrier wait for it
-    if (t < M) epi.rstd[t] = s_rstd[t];
+    if (tile == 0 && t < M) epi.rstd[t] = s_rstd[t];
   } else if constexpr (EPI == EPI_SILU) {
     // 64 interleave16 columns = 32 outputs k = 32 tile + i (gate at gflat, up at gflat + 16)
     for (uint32_t i = t; i < 32u * M; i += 256u) {
-      const uint32_t row = i / 32u, k = tile * 32u + i % 32u;
-      const uint32_t gflat = (k / 16u) * 32u + (k % 16u);
-      const uint16_t g_b = f2h(fold(row, gflat)), u_b = f2h(fold(row, gflat + 16u));
+      const uint32_t row = i / 32u, kk = i % 32u, k = tile * 32u + kk;
+      const uint32_t gcol = (kk / 16u) * 32u + (kk % 16u);
+      const uint16_t g_b = f2h(folded(row, gcol)), u_b = f2h(folded(row, gcol + 16u));
       const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
       epi.h[(size_t)row * (N / 2) + k] = f2h(h2f(s_b) * h2f(u_b));
     }
   } else if constexpr (EPI == EPI_F16OUT) {
-    for (uint32_t row = wave; row < M; row += kWaves) {
-      const uint32_t n = n0 + lane;
-      epi.out16[(size_t)row * N + n] = f2h(fold(row, n));
-    }
+    for (uint32_t i = t; i < total; i += 256u)
+      epi.out16[(size_t)(i / kCols) * N + n0 + i % kCols] = f2h(folded(i / kCols, i % kCols));
   } else if constexpr (EPI == EPI_LOGITS) {
     for (uint32_t row = wave; row < M; row += kWaves) {
       const uint32_t n = n0 + lane;
-      const float v = fold(row, n);
+      const float v = folded(row, lane);
       epi.out32[(size_t)row * N + n] = v;
       if (epi.argmax_part) {
         float bv = n < epi.vocab_used ? v : -INFINITY;
@@ -346,6 +398,10 @@ __global__ __launch_bounds__(256) void fold_partials_kernel(const float* __restr
   for (uint32_t s = 0; s < S; ++s) t += partials[(size_t)s * MN + i];
   if (out16) out16[i] = f2h(t);
   if (out32) out32[i] = t;
+}
+
+__global__ __launch_bounds__(256) void handoff_init_kernel(uint32_t* __restrict__ p, size_t n) {
+  for (size_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += (size_t)gridDim.x * 256u) p[i] = kEmpty;
 }
 
 template <int MR, int EPI>
@@ -403,16 +459,11 @@ extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
 }
 
 extern "C" uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue) {
-  // A fused epilogue's last work-group per tile folds S partials with device-coherent
-  // loads, so larger S lengthens the launch's serial tail; the fused launches keep S at the
-  // largest divisor of K/64 no larger than 8 (and no larger than the plain choice).
-  const uint32_t plain = mi_gemv_pick_s(K, N);
-  if (epilogue == MI_EPI_PARTIALS) return plain;
-  const uint32_t G = K / 64, cap = plain < 8u ? plain : 8u;
-  uint32_t best = 1;
-  for (uint32_t S = 1; S <= cap; ++S)
-    if (G % S == 0) best = S;
-  return best;
+  // The consumer folds the tile's slices after one poll round trip whatever S is, and the
+  // producers do not wait, so the fused launches keep the plain choice (measured on MI355X
+  // over the 27B shapes: o 20, gate_up 10 and down 34 beat the largest S <= 8).
+  (void)epilogue;
+  return mi_gemv_pick_s(K, N);
 }
 
 extern "C" int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
@@ -431,7 +482,7 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   if (int e = check_gemv(qweight, scales, x, partials, M, K, N, S)) return e;
   if (!ep) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: null epilogue");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  GemvEpi e{ep->counters, ep->resid, ep->sumsq, ep->rstd, ep->next_norm_w, ep->x_next, ep->h,
+  GemvEpi e{ep->resid, ep->sumsq, ep->rstd, ep->next_norm_w, ep->x_next, ep->h,
             ep->logits, reinterpret_cast<u2_t*>(ep->argmax_part), ep->vocab_used, ep->eps, ep->out16};
   int r;
   switch (ep->kind) {
@@ -439,27 +490,37 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
       r = launch_rows<EPI_PARTIALS>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     case MI_EPI_RESID:
-      if (!e.counters || !e.resid || !e.sumsq || !e.rstd || !e.next_w || !e.x_next || N / kCols > 1024)
-        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex RESID: counters, resid, sumsq, rstd, next_norm_w, x_next; N <= 65536");
+      if (!e.resid || !e.sumsq || !e.rstd || !e.next_w || !e.x_next)
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex RESID: resid, sumsq, rstd, next_norm_w and x_next are required");
+      if (N > 16384)  // every tile's consumer must be resident at once (N/64 <= 256 work-groups)
+        return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex RESID: N must be <= 16384");
       r = launch_rows<EPI_RESID>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     case MI_EPI_SILU:
-      if (!e.counters || !e.h || N % 32) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex SILU: counters, h");
+      if (!e.h) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex SILU: h is required");
       r = launch_rows<EPI_SILU>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     case MI_EPI_LOGITS:
-      if (!e.counters || !e.out32 || e.vocab_used > N)
-        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex LOGITS: counters, logits, vocab_used <= N");
+      if (!e.out32 || e.vocab_used > N)
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex LOGITS: logits is required, vocab_used <= N");
       r = launch_rows<EPI_LOGITS>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     case MI_EPI_F16OUT:
-      if (!e.counters || !e.out16) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex F16OUT: counters, out16");
+      if (!e.out16) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex F16OUT: out16 is required");
       r = launch_rows<EPI_F16OUT>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     default:
       return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: unknown epilogue");
   }
   return mi_hip(r, "gemv_w4a16_ex launch");
+}
+
+extern "C" int mi_gemv_handoff_init(float* words, size_t n, void* stream) {
+  if (!words || n == 0) return mi_fail(MI_ERR_ARG, "gemv_handoff_init: bad arguments");
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  handoff_init_kernel<<<(uint32_t)blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<uint32_t*>(words), n);
+  return mi_hip((int)hipGetLastError(), "gemv_handoff_init launch");
 }
 
 extern "C" int mi_fold_partials(const float* partials, uint16_t* out_f16, float* out_f32, uint32_t S,

@@ -1,7 +1,8 @@
-"""The GEMV's fused epilogues (last work-group per 64-column tile) and the fused
+"""The GEMV's fused epilogues (one consumer work-group per 64-column tile) and the fused
 embed + first norm, against the separate-kernel chain they replace, bit for bit on the
 same partials: prep_res_fold at 64-element chunks + prep_norm_finish, prep_silu_mul,
-the lm_head fold + argmax (tests/kernels/prep_test.cc, argmax_test.cc's bars)."""
+the lm_head fold + argmax (tests/kernels/prep_test.cc, argmax_test.cc's bars). Every
+launch must leave its hand-off words empty again, so a replay gives the same bits."""
 import ctypes as C
 
 import numpy as np
@@ -22,6 +23,21 @@ def rand_w(K, N, seed):
     return qw, sc
 
 
+EMPTY = 0xFFFFFFFF
+
+
+def handoff(n):
+    """n hand-off words set empty by the library's own initialiser"""
+    d = empty((n,), np.float32)
+    mi.call("mi_gemv_handoff_init", ptr(d), n, stream())
+    return d
+
+
+def all_empty(d, n=None):
+    h = host(d, np.uint32).ravel()
+    return bool(np.all(h[:n] == EMPTY))
+
+
 def partials_of(dq, ds, dx, M, K, N, S):
     part = empty((S, M, N), np.float32)
     mi.call("mi_gemv_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(part), M, K, N, S, stream())
@@ -29,9 +45,11 @@ def partials_of(dq, ds, dx, M, K, N, S):
     return host(part, np.float32).copy()
 
 
-@pytest.mark.parametrize("M,S", [(1, 8), (3, 4), (16, 1)])
-def test_resid_epilogue_bitwise(M, S):
-    K, N = 2048, 1024  # N = hidden
+@pytest.mark.parametrize("M,S,K,N", [(1, 8, 2048, 1024), (3, 4, 2048, 1024), (16, 1, 2048, 1024),
+                                     (16, 8, 2048, 1024), (1, 34, 17408 // 8, 1024), (16, 2, 1024, 16384)])
+def test_resid_epilogue_bitwise(M, S, K, N):
+    # N = hidden; (1, 34): down's split width over 34 k-groups; (16, 2, N 16384): the
+    # consumers' sums of squares polled in two rounds of rows
     qw, sc = rand_w(K, N, 10 + M)
     rng = np.random.default_rng(M)
     x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
@@ -39,30 +57,35 @@ def test_resid_epilogue_bitwise(M, S):
     w = (1 + 0.02 * rng.standard_normal(N)).astype(np.float32)
     dq, ds, dx = dev(qw), dev(sc), dev(x)
     part = partials_of(dq, ds, dx, M, K, N, S)
-    print(f"resid epilogue M={M} S={S}", flush=True)
+    print(f"resid epilogue M={M} S={S} K={K} N={N}", flush=True)
     G = N // 64
-    ctr = dev(np.zeros(G + 1, np.uint32))
     dr, dw = dev(resid), dev(w)
-    dss = empty((G, M), np.float32)
+    dss = handoff(G * M * G)
     drs = empty((M,), np.float32)
     dxn = empty((M, N), np.uint16)
-    dpart = empty((S, M, N), np.float32)
-    ep = mi.GemvEpilogue(mi.EPI_RESID, ptr(ctr), ptr(dr), ptr(dss), ptr(drs), ptr(dw), ptr(dxn), 1e-6,
+    dpart = handoff(S * M * N)
+    ep = mi.GemvEpilogue(mi.EPI_RESID, ptr(dr), ptr(dss), ptr(drs), ptr(dw), ptr(dxn), 1e-6,
                          None, None, None, 0)
-    for rep in range(2):  # a replay must find the counters reset
+    r_ref = resid.copy()
+    s_ref = np.zeros((G, M), np.float32)
+    x_ref = np.zeros((M, N), np.uint16)
+    L().orc_res_fold(F16, O._p(part), O._p(r_ref), O._p(s_ref), M, N, S, G)
+    L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, N, G, 1e-6)
+    rstd_ref = np.zeros(M, np.float32)
+    for m in range(M):
+        tot = np.float32(0)
+        for g in range(G):
+            tot = np.float32(tot + s_ref[g, m])
+        rstd_ref[m] = np.float32(1) / np.sqrt(np.float32(tot / np.float32(N) + np.float32(1e-6)))
+    for rep in range(2):  # a replay must find the hand-off words empty again
         if rep:
             dr.copy_(dev(resid))
         mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
         sync()
-        assert not host(ctr, np.uint32).any()
-        r_ref = resid.copy()
-        s_ref = np.zeros((G, M), np.float32)
-        x_ref = np.zeros((M, N), np.uint16)
-        L().orc_res_fold(F16, O._p(part), O._p(r_ref), O._p(s_ref), M, N, S, G)
-        L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, N, G, 1e-6)
+        assert all_empty(dpart) and all_empty(dss)
         assert np.array_equal(host(dr, np.uint16), r_ref)
-        assert np.array_equal(host(dss, np.uint32), s_ref.view(np.uint32))
         assert np.array_equal(host(dxn, np.uint16), x_ref)
+        assert np.array_equal(host(drs, np.uint32), rstd_ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("M,S", [(1, 4), (4, 2)])
@@ -73,13 +96,12 @@ def test_silu_epilogue(M, S):
     x = O.f32_to_f16_bits(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32))
     dq, ds, dx = dev(qw), dev(sc), dev(x)
     part = partials_of(dq, ds, dx, M, K, N, S)
-    ctr = dev(np.zeros(N // 64 + 1, np.uint32))
     dh = empty((M, I), np.uint16)
-    dpart = empty((S, M, N), np.float32)
-    ep = mi.GemvEpilogue(mi.EPI_SILU, ptr(ctr), None, None, None, None, None, 0.0, ptr(dh), None, None, 0)
+    dpart = handoff(S * M * N)
+    ep = mi.GemvEpilogue(mi.EPI_SILU, None, None, None, None, None, 0.0, ptr(dh), None, None, 0)
     mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
     sync()
-    assert not host(ctr, np.uint32).any()
+    assert all_empty(dpart)
     got = host(dh, np.uint16)
     want = O.silu_mul(F16, part, M, I, S)
     a = O.f16_bits_to_f32(got).astype(np.float64)
@@ -96,17 +118,17 @@ def test_logits_epilogue_and_argmax(M):
     dq, ds, dx = dev(qw), dev(sc), dev(x)
     S = 4
     part = partials_of(dq, ds, dx, M, K, V, S)
-    ctr = dev(np.zeros(V // 64 + 1, np.uint32))
     dl = empty((M, V), np.float32)
     dap = empty((M * (V // 64) * 2,), np.uint32)
-    dpart = empty((S, M, V), np.float32)
-    ep = mi.GemvEpilogue(mi.EPI_LOGITS, ptr(ctr), None, None, None, None, None, 0.0, None, ptr(dl), ptr(dap), used)
+    dpart = handoff(S * M * V)
+    ep = mi.GemvEpilogue(mi.EPI_LOGITS, None, None, None, None, None, 0.0, None, ptr(dl), ptr(dap), used)
     mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, V, S, C.byref(ep), stream())
     c = np.zeros(64, np.uint32)
     c[1] = M
     ctrl = dev(c)
     mi.call("mi_argmax_finish", ptr(ctrl), ptr(dap), V // 64, None, 0, stream())
     sync()
+    assert all_empty(dpart)
     want = np.zeros((M, V), np.float32)
     for s in range(S):
         want = want + part[s]  # ascending s from 0.f
@@ -128,15 +150,37 @@ def test_f16out_epilogue_is_gemv_then_fold(M, S):
     want = np.zeros((M, N), np.float32)
     for s in range(S):
         want = want + part[s]
-    ctr = dev(np.zeros(N // 64 + 1, np.uint32))
     out = empty((M, N), np.uint16)
-    dpart = empty((S, M, N), np.float32)
-    ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, counters=ptr(ctr), out16=ptr(out))
-    for _ in range(2):  # the counters reset themselves: a second launch gives the same bits
+    dpart = handoff(S * M * N)
+    ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, out16=ptr(out))
+    for _ in range(2):  # the hand-off words are empty again: a second launch gives the same bits
         mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
         sync()
-        assert not host(ctr, np.uint32).any()
+        assert all_empty(dpart)
         assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want))
+
+
+def test_launches_share_handoff_words():
+    """The engine's pattern: fused launches of different shapes and split widths take turns
+    on one hand-off buffer; each finds it empty and leaves it so."""
+    K, N = 1024, 2048
+    rng = np.random.default_rng(77)
+    shapes = [(K, N, 8), (K, 2 * N, 4), (2 * K, N, 16), (K, N, 1), (K, N, 8)]
+    dpart = handoff(16 * 2 * N)
+    for i, (k, n, S) in enumerate(shapes):
+        qw, sc = rand_w(k, n, 90 + i)
+        x = O.f32_to_f16_bits(rng.standard_normal((1, k)).astype(np.float32))
+        dq, ds, dx = dev(qw), dev(sc), dev(x)
+        part = partials_of(dq, ds, dx, 1, k, n, S)
+        want = np.zeros((1, n), np.float32)
+        for s_ in range(S):
+            want = want + part[s_]
+        out = empty((1, n), np.uint16)
+        ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, out16=ptr(out))
+        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), 1, k, n, S, C.byref(ep), stream())
+        sync()
+        assert all_empty(dpart), i
+        assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want)), i
 
 
 def test_embed_norm_bitwise():
