@@ -91,10 +91,11 @@ int mi_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_
 /* The same linear with the step's next operation fused into one consumer work-group per
  * 64-column tile (the reference's consumers prep_res_fold + prep_norm_finish, prep_silu_mul
  * and the lm_head fold + argmax_stage1, src/kernels/prep.cl:288-384, argmax.cl:82).
- * Hand-off words: for a fused kind, partials[0 .. (S-1)*M*N) (and RESID's sumsq) must hold
+ * Hand-off words: for a fused kind, partials[0 .. (S-1)*M*N) (S*M*N for QKV; and RESID's sumsq) must hold
  * the empty pattern of mi_gemv_handoff_init on entry; every launch leaves them so. Launches
  * that share hand-off words must not overlap. */
-enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3, MI_EPI_F16OUT = 4 };
+enum { MI_EPI_PARTIALS = 0, MI_EPI_RESID = 1, MI_EPI_SILU = 2, MI_EPI_LOGITS = 3, MI_EPI_F16OUT = 4,
+       MI_EPI_QKV = 5 };
 typedef struct mi_gemv_epilogue {
   uint32_t kind;
   /* RESID (N = hidden <= 16384): resid [M][N] += rne(sum_s partials) (rounded as
@@ -117,6 +118,23 @@ typedef struct mi_gemv_epilogue {
   /* F16OUT: out16 [M][N] = rne_f16(sum_s partials), the fold of mi_fold_partials in the
    * GEMV launch (a plain linear with 16-bit output) */
   uint16_t* out16;
+  /* QKV (N = shape->qkv_n, M <= 4, not gated, head_dim 128 or 256): mi_attn_prep on the
+   * folded q||k||v row in the same launch - q/k RMSNorm, RoPE, q -> attn_q fp32
+   * [M][q_heads][head_dim], K/V f16 at the cache row of position pos + m (the arguments of
+   * mi_attn_prep, whose output this is bit for bit). The launch takes S slices plus one
+   * consumer work-group per head; partials[0 .. S*M*N) are its hand-off words. */
+  uint32_t* ctrl;
+  const struct mi_attn_shape* shape;
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope;
+  float* attn_q;
+  uint16_t* kv_k;
+  uint16_t* kv_v;
+  size_t row_stride, head_stride;
+  const uint32_t* pages;
+  uint32_t page;
+  uint32_t kv_len;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,

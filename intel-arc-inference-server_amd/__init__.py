@@ -88,14 +88,17 @@ SIGNATURES = {
 }
 
 
-EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS, EPI_F16OUT = 0, 1, 2, 3, 4
+EPI_PARTIALS, EPI_RESID, EPI_SILU, EPI_LOGITS, EPI_F16OUT, EPI_QKV = 0, 1, 2, 3, 4, 5
 
 
 class GemvEpilogue(C.Structure):
     """mi_gemv_epilogue"""
     _fields_ = [("kind", u32), ("resid", vp), ("sumsq", vp), ("rstd", vp),
                 ("next_norm_w", vp), ("x_next", vp), ("eps", f32), ("h", vp), ("logits", vp),
-                ("argmax_part", vp), ("vocab_used", u32), ("out16", vp)]
+                ("argmax_part", vp), ("vocab_used", u32), ("out16", vp),
+                ("ctrl", vp), ("shape", vp), ("q_norm", vp), ("k_norm", vp), ("rope", vp), ("attn_q", vp),
+                ("kv_k", vp), ("kv_v", vp), ("row_stride", sz), ("head_stride", sz), ("pages", vp),
+                ("page", u32), ("kv_len", u32)]
 
 
 class MiError(RuntimeError):

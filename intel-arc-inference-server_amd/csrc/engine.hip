@@ -177,6 +177,7 @@ struct mi_engine {
       if (L.qkv.q) part_max = std::max(part_max, size_t(L.qkv.S) * R * L.qkv.N);
       for (const Linear* l : {&L.o, &L.gate_up, &L.down})
         if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S - 1) * R * l->N);
+      part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(R, 4u) * L.qkv.N);  // QKV: all S slices
     }
     MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
     part_ex_max = std::max(part_ex_max, size_t(lm_head.S - 1) * R * m.vocab);
@@ -297,7 +298,26 @@ struct mi_engine {
     MI_TRY(mi_embed_norm(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      MI_TRY(gemv(L.qkv, x, M));
+      const bool qkv_fused = !d.kv_int8 && (HD == 128 || HD == 256) && M <= 4;
+      if (qkv_fused) {
+        // attn_prep inside the qkv launch (one consumer work-group per head)
+        mi_gemv_epilogue eq{};
+        eq.kind = MI_EPI_QKV;
+        eq.ctrl = ctrl;
+        eq.shape = &ash;
+        eq.q_norm = L.q_norm;
+        eq.k_norm = L.k_norm;
+        eq.rope = rope;
+        eq.attn_q = attn_q;
+        eq.kv_k = static_cast<uint16_t*>(kv_k) + li * layer_kv;
+        eq.kv_v = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+        eq.row_stride = HD;
+        eq.head_stride = size_t(d.max_len) * HD;
+        eq.kv_len = d.max_len;
+        MI_TRY(mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream));
+      } else {
+        MI_TRY(gemv(L.qkv, x, M));
+      }
       if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
         int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
         int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
@@ -315,8 +335,9 @@ struct mi_engine {
         // 4096, 33 blocks per kv head, that costs more than the separate launch saves.)
         uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
         uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
-        MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
-                            HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+        if (!qkv_fused)
+          MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
+                              HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
         MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
                               nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
         MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));

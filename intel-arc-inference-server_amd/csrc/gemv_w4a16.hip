@@ -103,9 +103,21 @@ struct GemvEpi {
   uint32_t vocab_used;    // LOGITS
   float eps;              // RESID
   uint16_t* out16;        // F16OUT: [M][N]
+  // QKV: attn_prep's chain on the folded q||k||v row (f16 cache, not gated)
+  uint32_t* ctrl;
+  const float* rope;
+  const float* q_norm;
+  const float* k_norm;
+  float* attn_q;
+  uint16_t* kv_k;
+  uint16_t* kv_v;
+  const uint32_t* pages;
+  size_t row_stride, head_stride;
+  uint32_t page, kv_len, q_heads, kv_heads, head_dim, rot_dim;
+  float qk_eps;
 };
 
-enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3, EPI_F16OUT = 4 };
+enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3, EPI_F16OUT = 4, EPI_QKV = 5 };
 
 // argmax.cl:63-65: strictly greater wins, an exact tie keeps the lower index
 __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
@@ -116,6 +128,7 @@ constexpr uint32_t kEmpty = 0xFFFFFFFFu;  // a hand-off word with no value yet
 // floats of LDS a consumer polls into per round (16 KB at 16 rows: two slices a round at 2048)
 template <int MR>
 constexpr int fold_buf() { return 2048; }
+constexpr int kFoldBuf_QKV = 2048;
 constexpr uint32_t kPollLimit = 1u << 21; // polls of one word before giving up (~seconds)
 
 __device__ __forceinline__ float empty_f() { return __builtin_bit_cast(float, kEmpty); }
@@ -165,6 +178,136 @@ __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base,
   }
 }
 
+// EPI_QKV's consumer: work-group (tile, S) of grid (N/64, S + 1), no slice of its own. The last
+// tile of each head folds the head's HD columns over all S slices (ascending s from +0, as
+// attn_prep's fold) and runs attn_prep's chain on them (prep.cl attn_prep, attn.cl:361-372):
+// q/k rounded to f16, the per-head RMSNorm with the 256-lane tree's order, RoPE's
+// rotate_half pairs, then q -> attn_q (fp32) and k, v -> the f16 cache row of position pos + m.
+// One wave per row (M <= 4); lane l holds elements l + 64 k.
+template <int HD>
+__device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, uint32_t N, uint32_t S,
+                                             uint32_t tile, const GemvEpi& epi, float* s_fold) {
+  constexpr uint32_t TPH = HD / 64u, EPL = HD / 64u;
+  if ((tile + 1u) % TPH) return;  // uniform
+  __shared__ float s_row[4][HD];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t hh = tile / TPH, nh0 = (tile + 1u - TPH) * kCols;
+  const uint32_t QH = epi.q_heads, KVH = epi.kv_heads;
+  const bool is_q = hh < QH, is_k = !is_q && hh < QH + KVH;
+  const uint32_t h = is_q ? hh : (is_k ? hh - QH : hh - QH - KVH);
+  const uint32_t n_act = epi.ctrl[CTRL_NACT], pos = epi.ctrl[CTRL_POS];
+  const uint32_t m = wave;
+  const bool live = m < M && m < n_act;
+  const bool past = live && epi.kv_len && pos + m >= epi.kv_len;
+  // this wave's row: norm weights, RoPE pairs and the cache row go out before the fold
+  const float* nw = is_q ? epi.q_norm : (is_k ? epi.k_norm : nullptr);
+  const uint32_t half = epi.rot_dim / 2u;
+  float wn[EPL], rc[EPL], rsn[EPL];
+  size_t crow = 0;
+  if (live && !past) {
+    const float* cs = epi.rope + (size_t)(pos + m) * 2u * half;
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) {
+      const uint32_t e = lane + 64u * k;
+      wn[k] = nw ? nw[e] : 0.f;
+      rc[k] = 1.f;
+      rsn[k] = 0.f;
+      if (!is_q && !is_k) continue;
+      if (e < epi.rot_dim) {
+        const uint32_t ii = e < half ? e : e - half;
+        rc[k] = cs[ii];
+        rsn[k] = cs[half + ii];
+      }
+    }
+    if (!is_q) {
+      const uint32_t p = pos + m;
+      crow = epi.pages ? (size_t)epi.pages[p / epi.page] * epi.page + p % epi.page : (size_t)p;
+    }
+  }
+  // the fold: element e of the head's M x HD block, e = t + 256 u (rows-slices e / HD)
+  constexpr int EL = 4 * HD / 256;
+  const uint32_t total = M * HD;
+  const uint32_t per_round = kFoldBuf_QKV / total;
+  float a[EL];
+#pragma unroll
+  for (int u = 0; u < EL; ++u) a[u] = 0.f;
+  for (uint32_t s0 = 0; s0 < S; s0 += per_round) {
+    const uint32_t ns = min(per_round, S - s0);
+    poll_into<kFoldBuf_QKV>(s_fold, ns * total, const_cast<float*>(partials) + (size_t)s0 * M * N,
+                            ((t / HD) * N + nh0 + t % HD) * 4u, (256u / HD) * N * 4u);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < EL; ++u) {
+      const uint32_t i = t + 256u * u;
+      if (i < total)
+        for (uint32_t j = 0; j < ns; ++j) a[u] += s_fold[j * total + i];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < EL; ++u) {
+    const uint32_t i = t + 256u * u;
+    if (i < total) s_fold[i] = a[u];
+  }
+  __syncthreads();
+  if (!live) return;  // uniform per wave; no barriers below
+  if (past) {  // past the cache: write nothing, flag the step (attn_prep's rule)
+    if (hh == 0 && lane == 0) epi.ctrl[CTRL_DEBUG] = 0xDEAD0002u;
+    return;
+  }
+  const float* fr = s_fold + m * HD;
+  if (!is_q && !is_k) {
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k)
+      epi.kv_v[crow * epi.row_stride + h * epi.head_stride + lane + 64u * k] = f2h(fr[lane + 64u * k]);
+    return;
+  }
+  float xf[EPL], nv[EPL];
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) xf[k] = h2f(f2h(fr[lane + 64u * k]));
+  if (nw) {
+    // tree_hd's order: the LDS steps (v[i] + v[i + st], st >= 64) are this lane's own
+    // elements, then the 64-lane shuffle tree; lane 0's total is broadcast
+    float sq[EPL];
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) sq[k] = xf[k] * xf[k];
+    float acc;
+    if constexpr (EPL == 4) acc = (sq[0] + sq[2]) + (sq[1] + sq[3]);
+    else acc = sq[0] + sq[1];
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) acc += __shfl_down(acc, st, 64);
+    const float tot = __shfl(acc, 0, 64);
+    const float rstd = 1.0f / sqrtf(tot / (float)HD + epi.qk_eps);
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) nv[k] = h2f(f2h(xf[k] * rstd * wn[k]));
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) nv[k] = xf[k];
+  }
+  float* nrm = s_row[wave];
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) nrm[lane + 64u * k] = nv[k];
+  wave_lds_sync();
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) {
+    const uint32_t e = lane + 64u * k;
+    float out;
+    if (e < half) {
+      const float tt = nrm[e + half] * rsn[k];
+      out = __builtin_fmaf(nv[k], rc[k], -tt);
+    } else if (e < epi.rot_dim) {
+      const float tt = nrm[e - half] * rsn[k];
+      out = __builtin_fmaf(nv[k], rc[k], tt);
+    } else {
+      out = nv[k];
+    }
+    if (is_q)
+      epi.attn_q[((size_t)m * QH + h) * HD + e] = out;
+    else
+      epi.kv_k[crow * epi.row_stride + h * epi.head_stride + e] = f2h(out);
+  }
+}
+
 // MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue.
 template <int MR, int U, int EPI>
 __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
@@ -182,7 +325,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   const uint32_t ncol = n0 + 4u * c4;
   const uint32_t s = blockIdx.y;
   const uint32_t g_begin = s * gps + wave;
-  const uint32_t g_end = (s + 1) * gps;
+  // QKV's consumer row (s = S) has no slice of its own
+  const uint32_t g_end = (EPI == EPI_QKV && s + 1 == gridDim.y) ? 0u : (s + 1) * gps;
   const bool xrow = c4 < M;  // this lane feeds activation row c4 of the A operand
 
   const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
@@ -248,9 +392,19 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     }
   }
   __syncthreads();
+  if constexpr (EPI == EPI_QKV) {
+    if (s + 1 == gridDim.y) {  // the consumer row (uniform)
+      __shared__ float s_qfold[kFoldBuf_QKV];
+      if (epi.head_dim == 128)
+        qkv_consumer<128>(partials, M, N, gridDim.y - 1, blockIdx.x, epi, s_qfold);
+      else
+        qkv_consumer<256>(partials, M, N, gridDim.y - 1, blockIdx.x, epi, s_qfold);
+      return;
+    }
+  }
   const uint32_t total = M * kCols;
   const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
-  const bool consumer = EPI != EPI_PARTIALS && s + 1 == S;
+  const bool consumer = EPI != EPI_PARTIALS && EPI != EPI_QKV && s + 1 == S;
   for (uint32_t i = threadIdx.x; i < total; i += 256u) {
     const uint32_t row = i / kCols, col = i % kCols;
     float v = red[0][row][col];
@@ -263,6 +417,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     else
       st_agent(partials + ((size_t)s * M + row) * N + n0 + col, publishable(v));
   }
+  if constexpr (EPI == EPI_QKV) return;
   if (!consumer) return;
 
   // ---- the tile's consumer folds the S partials and applies the epilogue ----
@@ -408,7 +563,7 @@ template <int MR, int EPI>
 int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part, uint32_t M,
                 uint32_t K, uint32_t N, uint32_t S, const GemvEpi& epi, hipStream_t st) {
   const uint32_t G = K / 64, gps = G / S;
-  dim3 grid(N / kCols, S);
+  dim3 grid(N / kCols, EPI == EPI_QKV ? S + 1 : S);  // QKV: one more row, the heads' consumers
   if (gps >= 16)
     gemv_w4a16_kernel<MR, 4, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, epi);
   else
@@ -509,6 +664,27 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
       if (!e.out16) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex F16OUT: out16 is required");
       r = launch_rows<EPI_F16OUT>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
+    case MI_EPI_QKV: {
+      const mi_attn_shape* sh = ep->shape;
+      if (!ep->ctrl || !sh || !ep->rope || !ep->attn_q || !ep->kv_k || !ep->kv_v)
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex QKV: ctrl, shape, rope, attn_q, kv_k and kv_v are required");
+      if (M > 4) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: M must be <= 4");
+      if (sh->gated) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: gated attention is not fused");
+      const uint32_t HD = sh->head_dim;
+      if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: head_dim must be 128 or 256");
+      if (sh->kv_heads == 0 || N != (sh->q_heads + 2 * sh->kv_heads) * HD || sh->qkv_n != N ||
+          sh->k_off != sh->q_heads * HD || sh->v_off != (sh->q_heads + sh->kv_heads) * HD)
+        return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: N must be the q||k||v width of the shape");
+      if (sh->rot_dim > HD || sh->rot_dim % 2) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: bad rot_dim");
+      if (ep->pages && ep->page == 0) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex QKV: page size 0");
+      e.ctrl = ep->ctrl; e.rope = ep->rope; e.q_norm = ep->q_norm; e.k_norm = ep->k_norm;
+      e.attn_q = ep->attn_q; e.kv_k = ep->kv_k; e.kv_v = ep->kv_v; e.pages = ep->pages;
+      e.row_stride = ep->row_stride; e.head_stride = ep->head_stride; e.page = ep->page; e.kv_len = ep->kv_len;
+      e.q_heads = sh->q_heads; e.kv_heads = sh->kv_heads; e.head_dim = HD; e.rot_dim = sh->rot_dim;
+      e.qk_eps = sh->eps;
+      r = launch_rows<EPI_QKV>(qweight, scales, x, partials, M, K, N, S, e, st);
+      break;
+    }
     default:
       return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: unknown epilogue");
   }

@@ -183,6 +183,85 @@ def test_launches_share_handoff_words():
         assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want)), i
 
 
+@pytest.mark.parametrize("QH,KVH,HD,rot,M,n_act,paged,qk_norm,S", [
+    (40, 8, 128, 128, 1, 1, False, True, 20), (40, 8, 128, 128, 3, 2, True, True, 8),
+    (16, 2, 256, 64, 1, 1, False, False, 4), (16, 2, 256, 256, 4, 4, True, True, 2)])
+def test_qkv_epilogue_is_gemv_then_attn_prep(QH, KVH, HD, rot, M, n_act, paged, qk_norm, S):
+    """MI_EPI_QKV: attn_prep on the folded q||k||v inside the GEMV launch, bitwise the plain
+    GEMV followed by mi_attn_prep (attn_q, the K/V cache rows written, nothing else touched)."""
+    sh = O.attn_shape(QH, KVH, HD, rot_dim=rot)
+    K, N = 64 * S * max(1, 16 // S), sh.qkv_n
+    pos, Lm, P = 517, 1024, 64
+    rng = np.random.default_rng(QH + M)
+    qw, sc = rand_w(K, N, 60 + M)
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    qn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk_norm else None
+    kn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk_norm else None
+    rope = O.rope_table(1e6, rot, Lm)
+    pages = rng.permutation(Lm // P).astype(np.uint32) if paged else None
+    kk = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    vv = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    keep = [dev(qn) if qk_norm else None, dev(kn) if qk_norm else None, dev(rope), dev(pages) if paged else None]
+    pnorm = [ptr(k) if k is not None else None for k in keep]
+    print(f"qkv epilogue {QH}/{KVH}x{HD} rot {rot} M={M} n_act={n_act} paged={paged} S={S}", flush=True)
+
+    def ctrl():
+        c = np.zeros(64, np.uint32)
+        c[0], c[1] = pos, n_act
+        return dev(c)
+
+    # the plain GEMV, then attn_prep
+    part = empty((S, M, N), np.float32)
+    mi.call("mi_gemv_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(part), M, K, N, S, stream())
+    c1, aq1, k1, v1 = ctrl(), empty((M, QH, HD), np.float32), dev(kk), dev(vv)
+    aq1.zero_()
+    mi.call("mi_attn_prep", ptr(c1), ptr(part), S, M, C.byref(sh), pnorm[0], pnorm[1], pnorm[2], ptr(aq1), None,
+            ptr(k1), ptr(v1), HD, Lm * HD, pnorm[3], P if paged else 0, Lm, stream())
+    # the fused launch, twice (the hand-off words are empty again after the first)
+    dpart = handoff(S * M * N)
+    for rep in range(2):
+        c2, aq2, k2, v2 = ctrl(), empty((M, QH, HD), np.float32), dev(kk), dev(vv)
+        aq2.zero_()
+        ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(c2), shape=C.cast(C.pointer(sh), C.c_void_p),
+                             q_norm=pnorm[0], k_norm=pnorm[1], rope=pnorm[2], attn_q=ptr(aq2), kv_k=ptr(k2),
+                             kv_v=ptr(v2), row_stride=HD, head_stride=Lm * HD, pages=pnorm[3],
+                             page=P if paged else 0, kv_len=Lm)
+        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        sync()
+        assert all_empty(dpart)
+        assert np.array_equal(host(aq2, np.uint32), host(aq1, np.uint32)), rep
+        assert np.array_equal(host(k2, np.uint16), host(k1, np.uint16)), rep
+        assert np.array_equal(host(v2, np.uint16), host(v1, np.uint16)), rep
+        assert np.array_equal(host(c2, np.uint32), host(c1, np.uint32)), rep
+
+
+def test_qkv_epilogue_past_the_cache():
+    """A position at or past kv_len writes nothing and flags the step (attn_prep's rule)."""
+    sh = O.attn_shape(40, 8, 128)
+    K, N, S, Lm = 1024, sh.qkv_n, 4, 256
+    qw, sc = rand_w(K, N, 7)
+    x = O.f32_to_f16_bits(np.random.default_rng(7).standard_normal((1, K)).astype(np.float32))
+    rope = dev(O.rope_table(1e6, 128, Lm + 8))
+    c = np.zeros(64, np.uint32)
+    c[0], c[1] = Lm, 1
+    dc = dev(c)
+    kk = np.full((8, Lm, 128), 7, np.uint16)
+    k2, v2 = dev(kk), dev(kk)
+    aq = dev(np.zeros((1, 40, 128), np.float32))
+    dpart = handoff(S * N)
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(dc), shape=C.cast(C.pointer(sh), C.c_void_p), rope=ptr(rope),
+                         attn_q=ptr(aq), kv_k=ptr(k2), kv_v=ptr(v2), row_stride=128, head_stride=Lm * 128,
+                         kv_len=Lm)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), 1, K, N, S, C.byref(ep), stream())
+    sync()
+    assert all_empty(dpart)
+    assert host(dc, np.uint32)[18] == 0xDEAD0002
+    assert np.array_equal(host(k2, np.uint16), kk) and np.array_equal(host(v2, np.uint16), kk)
+    assert not host(aq, np.uint32).any()
+
+
 def test_embed_norm_bitwise():
     V, H, M = 512, 5120, 2
     rng = np.random.default_rng(4)
