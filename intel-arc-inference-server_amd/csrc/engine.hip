@@ -158,7 +158,7 @@ struct mi_engine {
       dn_block = size_t(H / 16) * (m.moe_inter / 64) * 136;
     }
     for (Layer& L : layer) {
-      MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_PARTIALS));
+      MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_QKV));  // the S of the fused launch, at every M
       MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
       if (moe) {
         MI_TRY(alloc(&L.router, size_t(router_n) * H));
@@ -289,9 +289,10 @@ struct mi_engine {
   }
 
   // One step over M rows, enqueued on `stream` (recorded into a graph by capture()).
-  // Seven launches per layer: qkv GEMV; attn_prep (or attn_prep_kv8); attn_decode;
-  // attn_reduce; o GEMV with the residual fold + post-attention norm fused; gate||up GEMV with
-  // silu*up fused; down GEMV with the residual fold + next norm fused.
+  // Six launches per layer (fp16 cache, M <= 4): the qkv GEMV with attn_prep fused;
+  // attn_decode; attn_reduce; the o GEMV with the residual fold + post-attention norm fused;
+  // gate||up GEMV with silu*up fused; down GEMV with the residual fold + next norm fused.
+  // (The int8 cache or M > 4: the qkv partials and attn_prep apart.)
   int enqueue_step(uint32_t M) {
     const uint32_t HD = d.head_dim, KVH = d.kv_heads;
     const size_t layer_kv = size_t(KVH) * d.max_len * HD;

@@ -616,8 +616,15 @@ extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
 extern "C" uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue) {
   // The consumer folds the tile's slices after one poll round trip whatever S is, and the
   // producers do not wait, so the fused launches keep the plain choice (measured on MI355X
-  // over the 27B shapes: o 20, gate_up 10 and down 34 beat the largest S <= 8).
-  (void)epilogue;
+  // over the 27B shapes: o 20, gate_up 10 and down 34 beat the largest S <= 8). QKV's head
+  // consumers fold a whole head over every slice: there the smallest S | K/64 with at most 8
+  // k-groups per slice (27B qkv: 10, measured ahead of 5, 8, 16 and 20).
+  if (epilogue == MI_EPI_QKV) {
+    const uint32_t G = K / 64;
+    for (uint32_t S = 1; S <= G; ++S)
+      if (G % S == 0 && G / S <= 8) return S;
+    return G ? G : 1;
+  }
   return mi_gemv_pick_s(K, N);
 }
 

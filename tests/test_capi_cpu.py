@@ -41,6 +41,8 @@ def test_split_k_choices_for_the_27b_shapes():
         assert L.mi_gemv_pick_s_ex(K, N, mi.EPI_PARTIALS) == want
         for epi in (mi.EPI_RESID, mi.EPI_SILU, mi.EPI_LOGITS, mi.EPI_F16OUT):
             assert L.mi_gemv_pick_s_ex(K, N, epi) == want
+    assert L.mi_gemv_pick_s_ex(5120, 7168, mi.EPI_QKV) == 10  # the 27B qkv, fused with attn_prep
+    assert L.mi_gemv_pick_s_ex(2048, 4608, mi.EPI_QKV) == 4
     for K in (64, 128, 512, 1024, 3072, 8192, 17408):
         for N in (64, 512, 4096):
             for epi in range(4):
