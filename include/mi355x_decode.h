@@ -299,6 +299,25 @@ int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blo
                 uint16_t* resid, uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden,
                 uint32_t inter, void* stream);
 
+/* ---- the chunked prefill's kernels (src/kernels/prefill: pf_gemm_q4.cl, pf_flash_attn.cl,
+ * pf_embed.cl) ---- */
+/* out [T][N] fp32 = x [T][K] f16 . W (int4 GPTQ g64 layout 0) on the matrix cores, with
+ * w = f16((q - 8) * scale) (the reference's prefill rounds the same product to bf16,
+ * pf_dequant_slab.cl). 64 | K, 128 | N. */
+int mi_gemm_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, float* out,
+                  uint32_t T, uint32_t K, uint32_t N, void* stream);
+/* Causal attention of T rows at positions pos0 .. pos0 + T - 1 (q fp32 [T][q_heads][head_dim],
+ * as mi_attn_prep writes it) over the fp16 cache rows [0, pos0 + t] (row layout and page table as
+ * mi_attn_decode); attn_out [T][q_heads * head_dim] f16. head_dim 128 or 256. */
+int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v,
+                    size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page,
+                    uint32_t T, uint32_t pos0, const mi_attn_shape* shape, uint16_t* attn_out,
+                    void* stream);
+/* resid [T][hidden] = embed rows of ids [T] (pf_embed_gather); an id >= vocab leaves its row
+ * and sets *flag = 0xDEAD0001 (flag may be NULL). */
+int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T,
+                  uint32_t hidden, uint32_t vocab, uint32_t* flag, void* stream);
+
 /* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
  * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the
  * GQA decoders this build runs: every layer is attention + a SwiGLU MLP (int4 g64 layout 0)
@@ -357,6 +376,14 @@ int mi_engine_step_eager(mi_engine* e, uint32_t M);
 int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens);
 /* Engine::ingest (engine.cc:715-724): one step per prompt id. */
 int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
+/* Engine::prefill (src/runtime/engine.h:97-115, the walk of src/runtime/prefill/step.h): the
+ * ids in chunks of at most `chunk` positions (0: 2048, the cap) from the current position, on
+ * the matrix cores (mi_gemm_w4a16, mi_attn_prefill). On return pos has advanced by n, the KV
+ * cache holds those positions and cur_token is the argmax of the last position's logits, as
+ * mi_engine_ingest of the same ids leaves them (up to the two paths' roundings). Refused: no
+ * ids, chunk above the cap, an id outside the vocabulary, past the cache, and (today) MoE
+ * models and the int8 cache. Allocates its scratch on the first call (and for a larger chunk). */
+int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
  * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. */

@@ -76,6 +76,10 @@ SIGNATURES = {
     "mi_engine_step_eager": (i32, [vp, u32]),
     "mi_engine_generate": (i32, [vp, u32, vp]),
     "mi_engine_ingest": (i32, [vp, vp, u32]),
+    "mi_engine_prefill": (i32, [vp, vp, u32, u32]),
+    "mi_gemm_w4a16": (i32, [vp, vp, vp, vp, u32, u32, u32, vp]),
+    "mi_attn_prefill": (i32, [vp, vp, vp, sz, sz, vp, u32, u32, u32, vp, vp, vp]),
+    "mi_embed_rows": (i32, [vp, vp, vp, u32, u32, u32, vp, vp]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
@@ -300,6 +304,12 @@ class Engine:
         import numpy as np
         a = np.ascontiguousarray(ids, np.uint32)
         check(lib().mi_engine_ingest(self._h, a.ctypes.data, a.size), "engine_ingest")
+
+    def prefill(self, ids, chunk=0):
+        """Engine::prefill: the ids in chunks of at most `chunk` positions (0: the cap)."""
+        import numpy as np
+        a = np.ascontiguousarray(ids, np.uint32)
+        check(lib().mi_engine_prefill(self._h, a.ctypes.data, a.size, chunk), "engine_prefill")
 
     def ctrl(self):
         import numpy as np

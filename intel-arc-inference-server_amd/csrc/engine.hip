@@ -21,6 +21,7 @@
 // and every weight tensor is reachable through mi_engine_tensor for checks or loading.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -69,6 +70,8 @@ __global__ void ctrl_set_rows_kernel(uint32_t* ctrl, uint32_t pos, uint32_t n_ac
 }
 
 }  // namespace
+
+constexpr uint32_t kPrefillCap = 2048;  // positions per prefill chunk at most (the reference's default cap)
 
 struct mi_engine {
   mi_model_desc d{};
@@ -403,6 +406,107 @@ struct mi_engine {
   int read_ctrl(uint32_t* out) {
     return mi_memcpy_d2h(out, ctrl, MI_CTRL_WORDS * 4, stream);
   }
+
+  // ---- chunked prefill (Engine::prefill, src/runtime/engine.h:97-115; the walk of
+  // src/runtime/prefill/step.h step_chunk). Scratch is allocated on the first call for the
+  // largest chunk asked so far, as the reference allocates its prefill scratch on first use. ----
+  uint32_t pf_cap = 0;
+  uint32_t* pf_ids = nullptr;    // [max_len] the prompt's ids
+  uint32_t* pf_ctrl = nullptr;   // the chunk's control block: pos = its first position, n_act = T
+  float* pf_out = nullptr;       // [cap][widest linear] fp32 linear outputs
+  float* pf_q = nullptr;         // [cap][q_heads][head_dim]
+  uint16_t* pf_resid = nullptr;  // [cap][hidden]
+  uint16_t* pf_x = nullptr;      // [cap][max(hidden, q_heads * head_dim)]
+  uint16_t* pf_h = nullptr;      // [cap][inter]
+  uint16_t* pf_attn = nullptr;   // [cap][q_heads * head_dim]
+
+  int prefill_alloc(uint32_t cap) {
+    if (cap <= pf_cap) return 0;
+    const size_t H = d.hidden, QHD = size_t(d.q_heads) * d.head_dim;
+    const size_t qkv_n = size_t(d.q_heads + 2 * d.kv_heads) * d.head_dim;
+    const size_t widest = std::max({qkv_n, 2 * size_t(d.inter), H});
+    if (!pf_ids) {
+      MI_TRY(alloc(&pf_ids, d.max_len));
+      MI_TRY(alloc(&pf_ctrl, MI_CTRL_WORDS));
+      MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(pf_ctrl, 0, MI_CTRL_WORDS * 4, stream)), "prefill ctrl clear"));
+    }
+    MI_TRY(alloc(&pf_out, size_t(cap) * widest));
+    MI_TRY(alloc(&pf_q, size_t(cap) * QHD));
+    MI_TRY(alloc(&pf_resid, size_t(cap) * H));
+    MI_TRY(alloc(&pf_x, size_t(cap) * std::max(H, QHD)));
+    MI_TRY(alloc(&pf_h, size_t(cap) * d.inter));
+    MI_TRY(alloc(&pf_attn, size_t(cap) * QHD));
+    pf_cap = cap;
+    return 0;
+  }
+
+  // One chunk of T positions from pos: every layer over the chunk's rows; leaves the last
+  // layer's normed rows (the final norm's output) in pf_x.
+  int prefill_chunk(const uint32_t* ids_dev_chunk, uint32_t pos, uint32_t T) {
+    const uint32_t H = d.hidden, HD = d.head_dim, QHD = d.q_heads * d.head_dim;
+    const size_t layer_kv = size_t(d.kv_heads) * d.max_len * HD;
+    ctrl_set_rows_kernel<<<1, 64, 0, stream>>>(pf_ctrl, pos, T, nullptr, 0);
+    MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "prefill ctrl"));
+    MI_TRY(mi_embed_rows(ids_dev_chunk, embed, pf_resid, T, H, d.vocab, pf_ctrl + MI_CTRL_DEBUG, stream));
+    MI_TRY(mi_res_norm(nullptr, pf_resid, layer[0].in_norm, pf_x, T, H, 0, d.rms_eps, stream));
+    for (uint32_t li = 0; li < d.layers; ++li) {
+      const Layer& L = layer[li];
+      uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
+      uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+      MI_TRY(mi_gemm_w4a16(L.qkv.q, L.qkv.s, pf_x, pf_out, T, L.qkv.K, L.qkv.N, stream));
+      MI_TRY(mi_attn_prep(pf_ctrl, pf_out, 1, T, &ash, L.q_norm, L.k_norm, rope, pf_q, nullptr, lk, lv, HD,
+                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+      MI_TRY(mi_attn_prefill(pf_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, T, pos, &ash, pf_attn, stream));
+      MI_TRY(mi_gemm_w4a16(L.o.q, L.o.s, pf_attn, pf_out, T, QHD, H, stream));
+      MI_TRY(mi_res_norm(pf_out, pf_resid, L.post_norm, pf_x, T, H, 1, d.rms_eps, stream));
+      MI_TRY(mi_gemm_w4a16(L.gate_up.q, L.gate_up.s, pf_x, pf_out, T, H, L.gate_up.N, stream));
+      MI_TRY(mi_silu_mul(pf_out, pf_h, T, d.inter, 1, stream));
+      MI_TRY(mi_gemm_w4a16(L.down.q, L.down.s, pf_h, pf_out, T, d.inter, H, stream));
+      const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
+      MI_TRY(mi_res_norm(pf_out, pf_resid, next_w, pf_x, T, H, 1, d.rms_eps, stream));
+    }
+    return 0;
+  }
+
+  int prefill(const uint32_t* ids, uint32_t n, uint32_t chunk) {
+    if (d.kv_int8 || d.experts)
+      return mi_fail(MI_ERR_STATE, "engine_prefill: dense models on the fp16 cache only (use ingest)");
+    if (!ids || n == 0) return mi_fail(MI_ERR_ARG, "engine_prefill: no ids");
+    if (chunk == 0) chunk = std::min(kPrefillCap, d.max_len);
+    if (chunk > kPrefillCap) return mi_fail(MI_ERR_ARG, "engine_prefill: chunk above the cap (2048)");
+    for (uint32_t i = 0; i < n; ++i)
+      if (ids[i] >= d.vocab) return mi_fail(MI_ERR_ARG, "engine_prefill: an id outside the vocabulary");
+    uint32_t c[MI_CTRL_WORDS];
+    MI_TRY(read_ctrl(c));
+    const uint32_t pos0 = c[MI_CTRL_POS];
+    if (size_t(pos0) + n > d.max_len) return mi_fail(MI_ERR_ARG, "engine_prefill: past the KV cache");
+    MI_TRY(prefill_alloc(std::min(chunk, n)));
+    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(pf_ctrl, 0, MI_CTRL_WORDS * 4, stream)), "prefill ctrl clear"));
+    MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(pf_ids, ids, size_t(n) * 4, hipMemcpyHostToDevice, stream)),
+                  "prefill ids upload"));
+    MI_TRY(mi_stream_sync(stream));  // the host array may go once this returns
+    uint32_t T = 0;
+    for (uint32_t c0 = 0; c0 < n; c0 += chunk) {
+      T = std::min(chunk, n - c0);
+      MI_TRY(prefill_chunk(pf_ids + c0, pos0 + c0, T));
+    }
+    // the last position's head and argmax, on the decode control block: the step at pos0 + n - 1
+    // leaves cur_token = its argmax and pos = pos0 + n, as ingest's last replay would
+    mi_gemv_epilogue el{};
+    el.kind = MI_EPI_LOGITS;
+    el.logits = logits;
+    el.argmax_part = argmax_part;
+    el.vocab_used = d.vocab_used;
+    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, pf_x + size_t(T - 1) * d.hidden, part_ex, 1, lm_head.K, lm_head.N,
+                            lm_head.S, &el, stream));
+    MI_TRY(set_rows(pos0 + n - 1, 1, nullptr, 0));
+    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
+    MI_TRY(mi_stream_sync(stream));
+    uint32_t pc[MI_CTRL_WORDS];
+    MI_TRY(mi_memcpy_d2h(pc, pf_ctrl, sizeof pc, stream));
+    if (pc[MI_CTRL_DEBUG]) return mi_fail(MI_ERR_STATE, "engine_prefill: the device flagged the chunk");
+    return 0;
+  }
 };
 
 extern "C" {
@@ -551,6 +655,11 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
     MI_TRY(mi_engine_replay(e, 1));
   }
   return mi_stream_sync(e->stream);
+}
+
+int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_prefill: null");
+  return e->prefill(ids, n, chunk);
 }
 
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out) {

@@ -1,0 +1,393 @@
+// prefill.hip - the chunked prefill's kernels on gfx950: the int4 linear for many rows on the
+// matrix cores, the causal attention of a chunk over the KV cache, and the chunk's embedding
+// gather.
+//
+// Replaces the reference's prefill walk (src/runtime/prefill/step.h step_chunk, Engine::prefill
+// src/runtime/engine.h:97-115): per chunk of T positions, the embedding gather and first norm,
+// then per layer q||k||v, attn_prep, the chunk's causal attention, o + residual + norm,
+// gate||up + SiLU, down + residual + norm; the last position's head and argmax leave the control
+// block as decode's ingest of the same ids would (cur_token = the argmax, pos advanced by T).
+//
+// gemm_w4a16_kernel: out[T][N] fp32 = x[T][K] (f16) . W[K][N] (int4 GPTQ g64, layout 0). The
+// contraction is a dense GEMM here (2 T K N flops over K N / 2 weight bytes): MFMA-bound from a
+// few dozen rows, so it is tiled for the matrix cores rather than streamed like the decode GEMV.
+//   * work-group tile 128 rows x 128 columns, 4 waves in 2 x 2, each wave 64 x 64 = 4 x 4
+//     v_mfma_f32_16x16x32_f16 tiles (64 fp32 accumulators per lane);
+//   * one 64-deep k-group per iteration (one scale per column), double-buffered in LDS: the
+//     next group's activations and weight words are loaded into registers while the current
+//     group is multiplied, then written to the other buffer;
+//   * weights are dequantised once per work-group and group: w = f16((q - 8) * scale), q - 8
+//     exact in f16 (the magic-number unpack of the decode GEMV), one f16 rounding of the product
+//     (the reference's prefill rounds the same product to bf16, pf_dequant_slab.cl); the
+//     activations are permuted to the unpack's pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) inside
+//     each 8-k chunk, so the products pair up;
+//   * fp32 accumulation across the whole K in MFMA order.
+//
+// attn_prefill_kernel: causal GQA attention of T query rows at positions pos0 .. pos0+T-1 over
+// the fp16 cache rows [0, pos0 + t] (the chunk's own rows written by attn_prep before it). A
+// work-group takes one kv head and 64 / GQA rows; its 4 waves each own 16 (row, q head) columns
+// of the MFMA and walk the same keys, 64 per iteration staged once in LDS for all of them.
+// Per 16-key group the decode kernel's per-wave flash step (csrc/attn.hip): S^T = K Q^T with q
+// as f16 high + low parts, the online softmax per column in fp32, O^T += V^T P^T with P as f16
+// high + low parts, so the result is fp32-accurate attention; keys past a row's position are
+// -inf. Every wave covers every key its rows need, so no merge across waves is needed.
+#include <algorithm>
+
+#include "mi_capi_internal.h"
+#include "mi_common.h"
+
+namespace mi {
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// the int4 linear for many rows
+// ---------------------------------------------------------------------------------------------
+constexpr uint32_t GBM = 128, GBN = 128, GBK = 64;
+constexpr uint32_t GPAD = 8;             // f16 of padding per LDS row (a 144-byte stride)
+constexpr uint32_t GROW = GBK + GPAD;    // LDS row length in f16
+
+// 8 natural-order activations (x0..x7 in four u32) into the unpack's pair order.
+__device__ __forceinline__ u4_t perm_pairs(u4_t v) {
+  return u4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+              __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
+// f16((q_i - 8) * s) of one word's 8 nibbles, pair order (q0,q4)(q1,q5)(q2,q6)(q3,q7)
+__device__ __forceinline__ u4_t dequant_scaled(uint32_t w, h2_t s2) {
+  const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
+  const h2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
+  const h2_t s16 = {(half_t)0.0625f, (half_t)0.0625f};
+  const h2_t b72 = {(half_t)-72.0f, (half_t)-72.0f};
+  const uint32_t t = w >> 8;
+  const h2_t p0 = as_h2(and_or(w, m_lo, magic)) - b1032;                               // q - 8, exact
+  const h2_t p1 = __builtin_elementwise_fma(as_h2(and_or(w, m_hi, magic)), s16, b72);  // exact
+  const h2_t p2 = as_h2(and_or(t, m_lo, magic)) - b1032;
+  const h2_t p3 = __builtin_elementwise_fma(as_h2(and_or(t, m_hi, magic)), s16, b72);
+  return u4_t{h2_bits(p0 * s2), h2_bits(p1 * s2), h2_bits(p2 * s2), h2_bits(p3 * s2)};
+}
+
+__global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restrict__ qweight,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ x,
+                                                         float* __restrict__ out, uint32_t T, uint32_t K,
+                                                         uint32_t N) {
+  __shared__ __align__(16) uint16_t As[2][GBM][GROW];
+  __shared__ __align__(16) uint16_t Bs[2][GBN][GROW];  // column-major: Bs[n][k]
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1u;
+  const uint32_t n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  const uint32_t G = K / GBK;
+
+  // staging: activations, thread t takes rows (t >> 3) + 32 i (i < 4), 8-k chunk t & 7;
+  // weights, thread t takes word row t >> 5 (k 8 r .. 8 r + 7) of columns 4 (t & 31) .. + 3
+  const uint32_t a_row = t >> 3, a_chunk = t & 7u;
+  const uint32_t b_r = t >> 5, b_c = 4u * (t & 31u);
+  u4_t a_st[4];
+  u4_t b_w;
+  u2_t b_s;
+  auto load_group = [&](uint32_t g) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t row = m0 + a_row + 32u * i;
+      a_st[i] = row < T ? *reinterpret_cast<const u4_t*>(x + (size_t)row * K + g * GBK + 8u * a_chunk)
+                        : u4_t{0u, 0u, 0u, 0u};
+    }
+    b_w = load_stream16(qweight + (size_t)(g * 8u + b_r) * N + n0 + b_c);
+    b_s = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + n0 + b_c);
+  };
+  auto store_group = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i)
+      *reinterpret_cast<u4_t*>(&As[buf][a_row + 32u * i][8u * a_chunk]) = perm_pairs(a_st[i]);
+    const uint32_t ws[4] = {b_w.x, b_w.y, b_w.z, b_w.w};
+    const uint32_t ss[4] = {b_s.x & 0xFFFFu, b_s.x >> 16, b_s.y & 0xFFFFu, b_s.y >> 16};
+#pragma unroll
+    for (uint32_t c = 0; c < 4; ++c) {
+      const h2_t s2 = as_h2(ss[c] | (ss[c] << 16));
+      *reinterpret_cast<u4_t*>(&Bs[buf][b_c + c][8u * b_r]) = dequant_scaled(ws[c], s2);
+    }
+  };
+
+  f4_t acc[4][4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  load_group(0);
+  store_group(0);
+  lds_barrier();
+  const uint32_t fr = lane & 15u, fk = 8u * (lane >> 4);  // fragment row/column and k offset
+  for (uint32_t g = 0; g < G; ++g) {
+    const uint32_t buf = g & 1u;
+    if (g + 1 < G) load_group(g + 1);
+#pragma unroll
+    for (uint32_t ks = 0; ks < 2; ++ks) {
+      h8_t af[4], bf[4];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][64u * wm + 16u * i + fr][32u * ks + fk]);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+        bf[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][64u * wn + 16u * j + fr][32u * ks + fk]);
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (g + 1 < G) store_group(buf ^ 1u);  // the other buffer was last read before the previous barrier
+    lds_barrier();
+  }
+  // lane holds rows 4 (lane >> 4) + r of column lane & 15 of each 16 x 16 tile
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      const uint32_t row = m0 + 64u * wm + 16u * i + 4u * (lane >> 4) + r;
+      if (row < T) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) out[(size_t)row * N + n0 + 64u * wn + 16u * j + fr] = acc[i][j][r];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// the chunk's causal attention
+// ---------------------------------------------------------------------------------------------
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
+struct PrefillAttnArgs {
+  const float* attn_q;  // [T][q_heads][HD] fp32
+  const uint16_t* kv_k;
+  const uint16_t* kv_v;
+  const uint32_t* pages;
+  uint16_t* attn_out;   // [T][q_heads * HD] f16
+  size_t row_stride, head_stride;
+  uint32_t page, T, pos0, q_heads;
+  float scale;
+};
+
+template <int HD, int GQA>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
+  constexpr uint32_t KK = HD / 32, NT = HD / 16;
+  constexpr uint32_t RB = 64 / GQA;          // rows per work-group
+  constexpr uint32_t KB = 64;                // keys per iteration
+  constexpr uint32_t KROW = HD + 8;          // padded K row in LDS (f16)
+  constexpr uint32_t ROWB = HD * 2, CW = 32; // V row bytes, bytes of one 16-dim column
+  __shared__ __align__(16) uint16_t sK[KB * KROW];
+  __shared__ __align__(16) unsigned char sV[KB * ROWB];
+  const uint32_t j = blockIdx.x, t0 = blockIdx.y * RB;
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t qi = lane & 15u, qq = lane >> 4;
+  // this lane's column: pair p = 16 wave + qi -> row t0 + p / GQA, q head j GQA + p % GQA
+  const uint32_t p = 16u * wave + qi, prow = p / GQA, ph = j * GQA + p % GQA;
+  const bool col_live = prow < RB && t0 + prow < a.T;
+  const uint32_t rows_here = min(RB, a.T - t0);
+  const uint32_t kend = a.pos0 + t0 + rows_here;  // keys [0, kend) cover every row of the block
+  const uint32_t lim = col_live ? a.pos0 + t0 + prow : kend - 1u;  // last key this column sees
+
+  // q as the B operand (f16 high and low parts): column qi, k = 32 kk + 8 qq + e
+  h8_t qh[KK], ql[KK];
+#pragma unroll
+  for (uint32_t kk = 0; kk < KK; ++kk) {
+    float v[8];
+    if (col_live) {
+      const float* qp = a.attn_q + ((size_t)(t0 + prow) * a.q_heads + ph) * HD + 32u * kk + 8u * qq;
+      const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
+      const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
+      v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+      v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const half_t h = (half_t)v[e];
+      qh[kk][e] = h;
+      ql[kk][e] = (half_t)(v[e] - (float)h);
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f4_t acc[NT];
+#pragma unroll
+  for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  // V rows staged with the decode kernel's swizzle per 16-row group: the four row groups one
+  // A-operand read touches land on distinct banks
+  auto sv_off = [](uint32_t r, uint32_t c) -> uint32_t {
+    return (r >> 4) * 16u * ROWB + (r & 15u) * ROWB + ((c ^ ((r >> 2) & 3u)) * CW);
+  };
+  const size_t hoff = (size_t)j * a.head_stride;
+  // staging: thread t loads key row t >> 2, quarter t & 3 of its K and V rows
+  constexpr uint32_t QB = ROWB / 4u;  // bytes per quarter row
+  const uint32_t srow = t >> 2, squart = t & 3u;
+  for (uint32_t kb = 0; kb < kend; kb += KB) {
+    {
+      const uint32_t key = kb + srow;
+      const bool live = key < kend;
+      const size_t crow = live ? (a.pages ? (size_t)a.pages[key / a.page] * a.page + key % a.page : (size_t)key) : 0;
+      const unsigned char* kp = reinterpret_cast<const unsigned char*>(a.kv_k + crow * a.row_stride + hoff) + squart * QB;
+      const unsigned char* vp = reinterpret_cast<const unsigned char*>(a.kv_v + crow * a.row_stride + hoff) + squart * QB;
+#pragma unroll
+      for (uint32_t i = 0; i < QB / 16u; ++i) {
+        const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+        const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+        const uint32_t byte = squart * QB + 16u * i;
+        *reinterpret_cast<u4_t*>(reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte) = kv;
+        *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = vv;
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (uint32_t grp = 0; grp < KB / 16u; ++grp) {
+      const uint32_t g0 = kb + 16u * grp;
+      if (g0 >= kend) break;  // uniform
+      // scores S^T[key g0 + 4 qq + r][column qi]
+      f4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk) {
+        const h8_t kh = *reinterpret_cast<const h8_t*>(sK + (16u * grp + qi) * KROW + 32u * kk + 8u * qq);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[kk], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[kk], d, 0, 0, 0);
+      }
+      float sc[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) {
+        const uint32_t key = g0 + 4u * qq + r;
+        sc[r] = key <= lim ? d[r] * a.scale : -INFINITY;
+        mx = fmaxf(mx, sc[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);  // finite: key 0 <= lim for every column
+      const float alpha = expf(m_run - m_new);
+      float w[4];
+#pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) w[r] = expf(sc[r] - m_new);
+      l_run = __builtin_fmaf(l_run, alpha, (w[0] + w[1]) + (w[2] + w[3]));
+      m_run = m_new;
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+      }
+      h4_t bh, bl;
+#pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) {
+        const half_t h = (half_t)w[r];
+        bh[r] = h;
+        bl[r] = (half_t)(w[r] - (float)h);
+      }
+#pragma unroll
+      for (uint32_t tt = 0; tt < NT; ++tt) {
+        h4_t av;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; ++jj)
+          av[jj] = *reinterpret_cast<const half_t*>(sV + sv_off(16u * grp + 4u * qq + jj, tt) + 2u * qi);
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, acc[tt], 0, 0, 0);
+      }
+    }
+    lds_barrier();  // every wave is done with this iteration's keys before they are replaced
+  }
+  float l = l_run + __shfl_xor(l_run, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  if (col_live) {
+    uint16_t* op = a.attn_out + (size_t)(t0 + prow) * a.q_heads * HD + (size_t)ph * HD;
+#pragma unroll
+    for (uint32_t tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) op[16u * tt + 4u * qq + r] = f2h(acc[tt][r] / l);
+  }
+}
+
+template <int HD, int GQA>
+void launch_prefill_gqa(const PrefillAttnArgs& a, uint32_t kv_heads, hipStream_t st) {
+  constexpr uint32_t RB = 64 / GQA;
+  attn_prefill_kernel<HD, GQA><<<dim3(kv_heads, (a.T + RB - 1) / RB), 256, 0, st>>>(a);
+}
+
+template <int HD>
+int launch_prefill_attn(const PrefillAttnArgs& a, uint32_t gqa, uint32_t kv_heads, hipStream_t st) {
+  switch (gqa) {
+    case 1: launch_prefill_gqa<HD, 1>(a, kv_heads, st); return 0;
+    case 2: launch_prefill_gqa<HD, 2>(a, kv_heads, st); return 0;
+    case 4: launch_prefill_gqa<HD, 4>(a, kv_heads, st); return 0;
+    case 5: launch_prefill_gqa<HD, 5>(a, kv_heads, st); return 0;
+    case 6: launch_prefill_gqa<HD, 6>(a, kv_heads, st); return 0;
+    case 8: launch_prefill_gqa<HD, 8>(a, kv_heads, st); return 0;
+    default: return -1;
+  }
+}
+
+// grid (T), 256 lanes: resid[t] = embed[ids[t]]; an id outside the table leaves the row and
+// sets the flag word (the caller's host check rejects such ids before launching)
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint32_t* __restrict__ ids,
+                                                         const uint16_t* __restrict__ embed,
+                                                         uint16_t* __restrict__ resid, uint32_t hidden,
+                                                         uint32_t vocab, uint32_t* flag) {
+  const uint32_t row = ids[blockIdx.x];
+  if (row >= vocab) {
+    if (threadIdx.x == 0 && flag) *flag = 0xDEAD0001u;
+    return;
+  }
+  const u4_t* s4 = reinterpret_cast<const u4_t*>(embed + (size_t)row * hidden);
+  u4_t* d4 = reinterpret_cast<u4_t*>(resid + (size_t)blockIdx.x * hidden);
+  for (uint32_t k = threadIdx.x; k < hidden / 8u; k += 256u) d4[k] = s4[k];
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+int mi_gemm_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, float* out, uint32_t T,
+                  uint32_t K, uint32_t N, void* stream) {
+  if (!qweight || !scales || !x || !out || T == 0) return mi_fail(MI_ERR_ARG, "gemm_w4a16: bad arguments");
+  if (K == 0 || K % GBK || N == 0 || N % GBN)
+    return mi_fail(MI_ERR_SHAPE, "gemm_w4a16: K must be a multiple of 64 and N of 128");
+  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(scales) % 8)
+    return mi_fail(MI_ERR_ARG, "gemm_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
+  if ((T + GBM - 1) / GBM > 65535) return mi_fail(MI_ERR_SHAPE, "gemm_w4a16: too many rows");
+  gemm_w4a16_kernel<<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(qweight, scales, x, out,
+                                                                                         T, K, N);
+  return mi_hip((int)hipGetLastError(), "gemm_w4a16");
+}
+
+int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v, size_t row_stride,
+                    size_t head_stride, const uint32_t* pages, uint32_t page, uint32_t T, uint32_t pos0,
+                    const mi_attn_shape* shape, uint16_t* attn_out, void* stream) {
+  if (!attn_q || !kv_k || !kv_v || !attn_out || !shape || T == 0)
+    return mi_fail(MI_ERR_ARG, "attn_prefill: bad arguments");
+  const uint32_t HD = shape->head_dim;
+  if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prefill: head_dim must be 128 or 256");
+  const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
+  if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads ||
+      !(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 5 || gqa == 6 || gqa == 8))
+    return mi_fail(MI_ERR_SHAPE, "attn_prefill: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
+  if (pages && page == 0) return mi_fail(MI_ERR_ARG, "attn_prefill: page size 0");
+  if ((row_stride % 8) || (head_stride % 8))
+    return mi_fail(MI_ERR_ARG, "attn_prefill: KV strides must keep 8-element alignment");
+  PrefillAttnArgs a{attn_q, kv_k, kv_v, pages, attn_out, row_stride, head_stride, page, T, pos0,
+                    shape->q_heads, shape->scale};
+  hipStream_t st = (hipStream_t)stream;
+  const int r = HD == 128 ? launch_prefill_attn<128>(a, gqa, shape->kv_heads, st)
+                          : launch_prefill_attn<256>(a, gqa, shape->kv_heads, st);
+  if (r) return mi_fail(MI_ERR_SHAPE, "attn_prefill: unsupported GQA");
+  return mi_hip((int)hipGetLastError(), "attn_prefill");
+}
+
+int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T, uint32_t hidden,
+                  uint32_t vocab, uint32_t* flag, void* stream) {
+  if (!ids || !embed || !resid || T == 0 || hidden == 0 || hidden % 8)
+    return mi_fail(MI_ERR_ARG, "embed_rows: bad arguments (hidden a multiple of 8)");
+  embed_rows_kernel<<<T, 256, 0, (hipStream_t)stream>>>(ids, embed, resid, hidden, vocab, flag);
+  return mi_hip((int)hipGetLastError(), "embed_rows");
+}
+
+}  // extern "C"

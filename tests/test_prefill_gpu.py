@@ -1,0 +1,183 @@
+"""The chunked prefill on the GPU: the int4 linear for many rows on the matrix cores, the chunk's
+causal attention, and Engine::prefill against decode's ingest of the same ids on one engine
+(tests/prefill/prefill_consistency_test.cc's comparison: prefill against decode-ingest, same
+engine, same prompt).
+
+Bars: the GEMM within 2^-16 sum |x w| of the fp64 product of the same f16-rounded weights
+(w = f16((q - 8) scale)), exact where every operation is exact; the attention within rel 2e-3 of
+fp64 causal softmax attention, cosine >= 0.99999, paged bitwise the contiguous cache; the engine's
+prefill leaves the control block as ingest does (pos, cur_token unless the last logits' top two are
+closer than the tolerance), the KV rows and the last logits within the two paths' rounding
+difference (prefill rounds each dequantised weight to f16; decode's GEMV multiplies the exact
+integers and scales once per group)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mipkg import dev, empty, host, mi, ptr, stream, sync
+from test_engine_gpu import small_desc
+
+pytestmark = pytest.mark.gpu
+F16 = O.ORC_F16
+
+
+def weights(K, N, seed, exact=False):
+    rng = np.random.default_rng(seed)
+    qw = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
+    if exact:
+        sc = np.full((K // 64, N), O.f32_to_f16_bits(np.float32(1 / 16)), np.uint16)
+    else:
+        sc = O.f32_to_f16_bits(rng.uniform(0.002, 0.02, size=(K // 64, N)).astype(np.float32))
+    return qw, sc
+
+
+def dequant16(qw, sc):
+    """w[k][n] = f16((q - 8) * s): the product of two f16 values is exact in fp32, so one
+    rounding to f16 is the correctly rounded f16 product"""
+    K = qw.shape[0] * 8
+    k = np.arange(K)
+    q = (qw[k // 8, :] >> (4 * (k % 8))[:, None]) & 0xF
+    s = O.f16_bits_to_f32(sc)[k // 64, :]
+    return ((q.astype(np.float32) - 8) * s).astype(np.float16).astype(np.float64)
+
+
+@pytest.mark.parametrize("T,K,N", [(1, 256, 128), (37, 1024, 384), (130, 2048, 256), (256, 5120, 512)])
+def test_gemm_vs_fp64(T, K, N):
+    qw, sc = weights(K, N, T + K)
+    x = O.f32_to_f16_bits(np.random.default_rng(T).standard_normal((T, K)).astype(np.float32))
+    print(f"gemm T={T} K={K} N={N}", flush=True)
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    out = empty((T, N), np.float32)
+    mi.call("mi_gemm_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(out), T, K, N, stream())
+    sync()
+    got = host(out, np.float32).astype(np.float64)
+    w = dequant16(qw, sc)
+    xf = O.f16_bits_to_f32(x).astype(np.float64)
+    want = xf @ w
+    bound = 2.0 ** -16 * (np.abs(xf) @ np.abs(w)) + 1e-30
+    assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) / bound)
+
+
+def test_gemm_exact_arithmetic():
+    """Small-integer activations and scale 1/16: every product and partial sum is exact in fp32,
+    so the GEMM equals the fp64 product bit for bit (any misplaced nibble, row or column shows)."""
+    T, K, N = 70, 512, 256
+    qw, sc = weights(K, N, 3, exact=True)
+    x = O.f32_to_f16_bits(np.random.default_rng(4).integers(-3, 4, size=(T, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    out = empty((T, N), np.float32)
+    mi.call("mi_gemm_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(out), T, K, N, stream())
+    sync()
+    want = O.f16_bits_to_f32(x).astype(np.float64) @ dequant16(qw, sc)
+    assert np.array_equal(host(out, np.float32).astype(np.float64), want)
+
+
+def test_gemm_refuses_bad_shapes():
+    with pytest.raises(mi.MiError):
+        mi.call("mi_gemm_w4a16", 16, 16, 16, 16, 4, 100, 128, None)
+    with pytest.raises(mi.MiError):
+        mi.call("mi_gemm_w4a16", 16, 16, 16, 16, 4, 128, 100, None)
+
+
+def prefill_attention(sh, q, k, v, T, pos0, pages=None, page=0):
+    HD, QH = sh.head_dim, sh.q_heads
+    Lm = k.shape[1]
+    dq, dk, dv, dpg = dev(q), dev(k), dev(v), dev(pages)
+    out = empty((T, QH * HD), np.uint16)
+    mi.call("mi_attn_prefill", ptr(dq), ptr(dk), ptr(dv), HD, Lm * HD, ptr(dpg), page, T, pos0, C.byref(sh),
+            ptr(out), stream())
+    sync()
+    return host(out, np.uint16)
+
+
+@pytest.mark.parametrize("QH,KVH,HD,T,pos0", [(40, 8, 128, 37, 100), (40, 8, 128, 130, 0), (16, 2, 256, 20, 64),
+                                              (8, 8, 128, 65, 3)])
+def test_attn_prefill_vs_fp64(QH, KVH, HD, T, pos0):
+    sh = O.attn_shape(QH, KVH, HD)
+    Lm = 256
+    rng = np.random.default_rng(QH + T)
+    k = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    v = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    q = rng.standard_normal((T, QH, HD)).astype(np.float32)
+    print(f"attn_prefill {QH}/{KVH}x{HD} T={T} pos0={pos0}", flush=True)
+    got = prefill_attention(sh, q, k, v, T, pos0)
+    G = QH // KVH
+    want = np.zeros((T, QH, HD))
+    for t in range(T):
+        for h in range(QH):
+            O.lib().orc_attend64(C.byref(sh), O._p(np.ascontiguousarray(q[t, h])), h // G, pos0 + t + 1, 0, F16,
+                                 O._p(k), O._p(v), None, None, HD, Lm * HD, 1, Lm, None, 0, O._p(want[t, h]))
+    g = O.f16_bits_to_f32(got).astype(np.float64).reshape(T, QH, HD)
+    err = np.abs(g - want)
+    assert np.all(err <= 2e-3 * np.abs(want) + 2e-3 * np.abs(want).max(axis=-1, keepdims=True)), err.max()
+    cos = (g * want).sum(-1) / np.sqrt((g * g).sum(-1) * (want * want).sum(-1))
+    assert cos.min() >= 0.99999
+
+
+def test_attn_prefill_paged_bitwise():
+    sh = O.attn_shape(40, 8, 128)
+    Lm, P, T, pos0 = 512, 64, 50, 300
+    rng = np.random.default_rng(5)
+    k = O.f32_to_f16_bits(rng.standard_normal((8, Lm, 128)).astype(np.float32))
+    v = O.f32_to_f16_bits(rng.standard_normal((8, Lm, 128)).astype(np.float32))
+    q = rng.standard_normal((T, 40, 128)).astype(np.float32)
+    a = prefill_attention(sh, q, k, v, T, pos0)
+    pages = rng.permutation(Lm // P).astype(np.uint32)
+    phys = np.concatenate([np.arange(pg * P, pg * P + P) for pg in pages])
+    kp, vp = np.empty_like(k), np.empty_like(v)
+    kp[:, phys], vp[:, phys] = k, v
+    b = prefill_attention(sh, q, kp, vp, T, pos0, pages, P)
+    assert np.array_equal(a, b)
+
+
+def kv_rows(eng, p0, n):
+    d = eng.desc
+    k = eng.to_host(mi.T_KV_K, 0, np.uint16).reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)
+    v = eng.to_host(mi.T_KV_V, 0, np.uint16).reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)
+    f = lambda a: O.f16_bits_to_f32(a[:, :, p0:p0 + n]).astype(np.float64)
+    return f(k), f(v)
+
+
+@pytest.mark.parametrize("n,chunk,p0", [(40, 0, 0), (40, 16, 0), (33, 8, 100)])
+def test_prefill_matches_ingest(n, chunk, p0):
+    eng = mi.Engine(small_desc(max_len=512), seed=11)
+    eng.capture(1)
+    ids = np.random.default_rng(n + chunk).integers(0, eng.desc.vocab_used, n).astype(np.uint32)
+    print(f"prefill vs ingest n={n} chunk={chunk} p0={p0}", flush=True)
+    eng.reset(p0, 0)
+    eng.ingest(ids)
+    c_ing = eng.ctrl()
+    lg_ing = eng.logits(1)[0].astype(np.float64)
+    k_ing, v_ing = kv_rows(eng, p0, n)
+    eng.reset(p0, 0)
+    eng.prefill(ids, chunk)
+    c_pf = eng.ctrl()
+    lg_pf = eng.logits(1)[0].astype(np.float64)
+    k_pf, v_pf = kv_rows(eng, p0, n)
+    assert c_pf[mi.CTRL_POS] == c_ing[mi.CTRL_POS] == p0 + n
+    assert c_pf[mi.CTRL_NACT] == 1
+    # the two paths differ by the f16 rounding of the dequantised weights (2^-11 relative each)
+    for a, b in ((k_pf, k_ing), (v_pf, v_ing)):
+        assert np.all(np.abs(a - b) <= 0.02 * np.abs(b) + 0.02 * np.abs(b).max()), np.abs(a - b).max()
+    scale = np.abs(lg_ing).max()
+    assert np.all(np.abs(lg_pf - lg_ing) <= 0.01 * scale), np.abs(lg_pf - lg_ing).max() / scale
+    top2 = np.sort(lg_ing)[-2:]
+    if top2[1] - top2[0] > 0.02 * scale:
+        assert c_pf[mi.CTRL_CUR] == c_ing[mi.CTRL_CUR] == int(np.argmax(lg_ing))
+    # decode continues from the prefilled cache as from the ingested one
+    eng.close()
+
+
+def test_prefill_refusals():
+    eng = mi.Engine(small_desc(max_len=256), seed=2)
+    eng.reset(250, 0)
+    with pytest.raises(mi.MiError):
+        eng.prefill(np.arange(10, dtype=np.uint32))  # past the cache
+    eng.reset(0, 0)
+    with pytest.raises(mi.MiError):
+        eng.prefill(np.array([eng.desc.vocab], np.uint32))  # outside the vocabulary
+    with pytest.raises(mi.MiError):
+        eng.prefill(np.arange(4, dtype=np.uint32), 4096)  # chunk above the cap
+    eng.close()
