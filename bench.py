@@ -297,6 +297,45 @@ def measure_cfg5(st):
     return rows
 
 
+def measure_prefill(eng, T=2048):
+    """The chunked prefill (the reference's Engine::prefill, north_star's small-M/prefill GEMM on
+    the matrix cores): one T-token prompt from position 0 in one chunk on the 27B engine, and
+    the int4 GEMM alone at T rows on layer 0's four linears (MFMA rate against the 2.5 PFLOP/s
+    dense fp16 peak; 2 T K N flops per call)."""
+    L, d, st = mi.lib(), eng.desc, eng.stream
+    ids = np.random.default_rng(7).integers(0, d.vocab_used, T).astype(np.uint32)
+    eng.reset(0, 0)
+    eng.prefill(ids, T)  # first call: scratch allocation
+    eng.reset(0, 0)
+    ev = Events(st)
+    ev.start()
+    eng.prefill(ids, T)
+    ms = ev.stop_ms()
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == T and c[mi.CTRL_DEBUG] == 0, c[:20]
+    out = {"workload": f"27B-shape prefill of a {T}-token prompt in one chunk (synthetic ids, random-init weights)",
+           "ms": round(ms, 2), "tokens_per_s": round(T / ms * 1e3, 1)}
+    H, QH, KVH, HD, I = d.hidden, d.q_heads, d.kv_heads, d.head_dim, d.inter
+    D = Dev()
+    x = D.alloc(T * max(H, I, QH * HD) * 2)
+    mi.check(L.mi_fill_f16(x, T * max(H, I, QH * HD), 5, 1, 0.0, 1.0, st))
+    o = D.alloc(T * 2 * I * 4)
+    gemms = []
+    for name, (kq, ks), K, N in (("qkv", (mi.T_QKV_Q, mi.T_QKV_S), H, (QH + 2 * KVH) * HD),
+                                 ("o", (mi.T_O_Q, mi.T_O_S), QH * HD, H),
+                                 ("gate_up", (mi.T_GU_Q, mi.T_GU_S), H, 2 * I),
+                                 ("down", (mi.T_DOWN_Q, mi.T_DOWN_S), I, H)):
+        qp, sp = eng.tensor(kq, 0)[0], eng.tensor(ks, 0)[0]
+        fn = lambda i: mi.check(L.mi_gemm_w4a16(qp, sp, x, o, T, K, N, st))
+        t = time_calls(st, fn, 10, warm=2)
+        tf = 2.0 * T * K * N / t / 1e6
+        gemms.append({"linear": name, "T": T, "K": K, "N": N, "us": round(t, 1), "tflops": round(tf, 1),
+                      "mfma_frac_fp16": round(tf / 2500.0, 4)})
+    D.free()
+    out["gemm_w4a16"] = gemms
+    return out
+
+
 def measure_cfg4(args, kv_int8=0):
     """a 40-layer MoE decoder (hidden 2048, 256 experts top 8 + shared,
     expert inter 512, attention 16 q / 2 kv of 256, vocab 151936 assumed) at context 4096:
@@ -420,7 +459,7 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
-    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5"], default=None,
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5", "prefill"], default=None,
                     help="run only that secondary measurement and print its JSON (the command the "
                          "attention and single-GEMV kernel profiles use)")
     args = ap.parse_args()
@@ -428,6 +467,11 @@ def main():
         print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
               "use --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.only == "prefill":
+        eng = mi.Engine(mi.desc_27b(max_len=2112), seed=args.seed)
+        print(json.dumps({"prefill": measure_prefill(eng)}), flush=True)
+        eng.close()
+        return
     if args.only:
         fn = {"cfg1": lambda: measure_cfg1(None),
               "cfg3": lambda: [measure_cfg3(None, L) for L in (32768, 131072)],
@@ -501,6 +545,10 @@ def main():
     roof["stream_read_gbs"] = round(stream_gbs, 1)
     roof["frac_of_stream"] = round(roof["achieved"] / stream_gbs, 4)
     log(f"bench: gemv roofline {roof}")
+    prefill = None
+    if not args.eager and not args.no_other:
+        prefill = measure_prefill(eng)
+        log(f"bench: prefill {prefill}")
     eng.close()
 
     other = None
@@ -512,6 +560,7 @@ def main():
         log(f"bench: cfg3 {other['cfg3_attention_int8_paged']}")
         other["cfg5_small_m_gemv"] = measure_cfg5(None)
         log(f"bench: cfg5 {other['cfg5_small_m_gemv']}")
+        other["prefill_27b"] = prefill
         other["cfg4_moe_step"] = measure_cfg4(args)
         other["cfg4_moe_step_int8_kv"] = measure_cfg4(args, kv_int8=1)
         log(f"bench: cfg4 {other['cfg4_moe_step']}")
