@@ -13,14 +13,16 @@
 // few dozen rows, so it is tiled for the matrix cores rather than streamed like the decode GEMV.
 //   * work-group tile 128 rows x 128 columns, 4 waves in 2 x 2, each wave 64 x 64 = 4 x 4
 //     v_mfma_f32_16x16x32_f16 tiles (64 fp32 accumulators per lane);
-//   * one 64-deep k-group per iteration (one scale per column), double-buffered in LDS: the
-//     next group's activations and weight words are loaded into registers while the current
-//     group is multiplied, then written to the other buffer;
-//   * weights are dequantised once per work-group and group: w = f16((q - 8) * scale), q - 8
-//     exact in f16 (the magic-number unpack of the decode GEMV), one f16 rounding of the product
-//     (the reference's prefill rounds the same product to bf16, pf_dequant_slab.cl); the
-//     activations are permuted to the unpack's pair order (k0,k4)(k1,k5)(k2,k6)(k3,k7) inside
-//     each 8-k chunk, so the products pair up;
+//   * one 64-deep k-group per iteration (one scale per column). The activations go through LDS,
+//     double-buffered (the next group's rows are loaded into registers while the current group
+//     is multiplied, then written to the other buffer). The weights skip LDS: a B fragment of
+//     v_mfma_f32_16x16x32_f16 is 8 consecutive k of one column, which is exactly one int4 word,
+//     so each lane loads its own words a group ahead and dequantises them into the fragment
+//     (LDS then carries the activations only, which halves its traffic per MFMA);
+//   * w = f16((q - 8) * scale): q - 8 exact in f16 (the magic-number unpack of the decode GEMV),
+//     one f16 rounding of the product (the reference's prefill rounds the same product to bf16,
+//     pf_dequant_slab.cl); the activations are permuted to the unpack's pair order
+//     (k0,k4)(k1,k5)(k2,k6)(k3,k7) inside each 8-k chunk, so the products pair up;
 //   * fp32 accumulation across the whole K in MFMA order.
 //
 // attn_prefill_kernel: causal GQA attention of T query rows at positions pos0 .. pos0+T-1 over
@@ -72,40 +74,41 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
                                                          float* __restrict__ out, uint32_t T, uint32_t K,
                                                          uint32_t N) {
   __shared__ __align__(16) uint16_t As[2][GBM][GROW];
-  __shared__ __align__(16) uint16_t Bs[2][GBN][GROW];  // column-major: Bs[n][k]
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1u;
   const uint32_t n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
   const uint32_t G = K / GBK;
+  const uint32_t fr = lane & 15u, fq = lane >> 4;  // fragment row/column, k chunk (8 k)
 
-  // staging: activations, thread t takes rows (t >> 3) + 32 i (i < 4), 8-k chunk t & 7;
-  // weights, thread t takes word row t >> 5 (k 8 r .. 8 r + 7) of columns 4 (t & 31) .. + 3
+  // activations, staged through LDS: thread t takes rows (t >> 3) + 32 i (i < 4), 8-k chunk t & 7
   const uint32_t a_row = t >> 3, a_chunk = t & 7u;
-  const uint32_t b_r = t >> 5, b_c = 4u * (t & 31u);
   u4_t a_st[4];
-  u4_t b_w;
-  u2_t b_s;
-  auto load_group = [&](uint32_t g) {
+  auto load_a = [&](uint32_t g) {
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
       const uint32_t row = m0 + a_row + 32u * i;
       a_st[i] = row < T ? *reinterpret_cast<const u4_t*>(x + (size_t)row * K + g * GBK + 8u * a_chunk)
                         : u4_t{0u, 0u, 0u, 0u};
     }
-    b_w = load_stream16(qweight + (size_t)(g * 8u + b_r) * N + n0 + b_c);
-    b_s = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + n0 + b_c);
   };
-  auto store_group = [&](uint32_t buf) {
+  auto store_a = [&](uint32_t buf) {
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i)
       *reinterpret_cast<u4_t*>(&As[buf][a_row + 32u * i][8u * a_chunk]) = perm_pairs(a_st[i]);
-    const uint32_t ws[4] = {b_w.x, b_w.y, b_w.z, b_w.w};
-    const uint32_t ss[4] = {b_s.x & 0xFFFFu, b_s.x >> 16, b_s.y & 0xFFFFu, b_s.y >> 16};
+  };
+  // weights, straight into registers: the B fragment of n-tile j and k half ks is one word per
+  // lane (8 k of column 16 j + fr, word row 4 ks + fq of the group), dequantised just before use
+  const uint32_t ncol = n0 + 64u * wn + fr;
+  uint32_t b_w[2][4];
+  uint16_t b_s[4];
+  auto load_b = [&](uint32_t g) {
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) {
-      const h2_t s2 = as_h2(ss[c] | (ss[c] << 16));
-      *reinterpret_cast<u4_t*>(&Bs[buf][b_c + c][8u * b_r]) = dequant_scaled(ws[c], s2);
-    }
+    for (uint32_t ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+        b_w[ks][j] = __builtin_nontemporal_load(qweight + (size_t)(8u * g + 4u * ks + fq) * N + ncol + 16u * j);
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) b_s[j] = scales[(size_t)g * N + ncol + 16u * j];
   };
 
   f4_t acc[4][4];
@@ -114,29 +117,37 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  load_group(0);
-  store_group(0);
+  load_a(0);
+  load_b(0);
+  store_a(0);
   lds_barrier();
-  const uint32_t fr = lane & 15u, fk = 8u * (lane >> 4);  // fragment row/column and k offset
   for (uint32_t g = 0; g < G; ++g) {
     const uint32_t buf = g & 1u;
-    if (g + 1 < G) load_group(g + 1);
+    // this group's weights become fragments; the next group's loads go out
+    h8_t bf[2][4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const h2_t s2 = as_h2((uint32_t)b_s[j] | ((uint32_t)b_s[j] << 16));
+#pragma unroll
+      for (uint32_t ks = 0; ks < 2; ++ks) bf[ks][j] = __builtin_bit_cast(h8_t, dequant_scaled(b_w[ks][j], s2));
+    }
+    if (g + 1 < G) {
+      load_a(g + 1);
+      load_b(g + 1);
+    }
 #pragma unroll
     for (uint32_t ks = 0; ks < 2; ++ks) {
-      h8_t af[4], bf[4];
+      h8_t af[4];
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][64u * wm + 16u * i + fr][32u * ks + fk]);
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j)
-        bf[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][64u * wn + 16u * j + fr][32u * ks + fk]);
+        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][64u * wm + 16u * i + fr][32u * ks + 8u * fq]);
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i)
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[ks][j], acc[i][j], 0, 0, 0);
     }
-    if (g + 1 < G) store_group(buf ^ 1u);  // the other buffer was last read before the previous barrier
+    if (g + 1 < G) store_a(buf ^ 1u);  // the other buffer was last read before the previous barrier
     lds_barrier();
   }
   // lane holds rows 4 (lane >> 4) + r of column lane & 15 of each 16 x 16 tile
@@ -144,10 +155,10 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
   for (uint32_t i = 0; i < 4; ++i)
 #pragma unroll
     for (uint32_t r = 0; r < 4; ++r) {
-      const uint32_t row = m0 + 64u * wm + 16u * i + 4u * (lane >> 4) + r;
+      const uint32_t row = m0 + 64u * wm + 16u * i + 4u * fq + r;
       if (row < T) {
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) out[(size_t)row * N + n0 + 64u * wn + 16u * j + fr] = acc[i][j][r];
+        for (uint32_t j = 0; j < 4; ++j) out[(size_t)row * N + ncol + 16u * j] = acc[i][j][r];
       }
     }
 }
