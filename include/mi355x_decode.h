@@ -380,9 +380,10 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
  * ids in chunks of at most `chunk` positions (0: 2048, the cap) from the current position, on
  * the matrix cores (mi_gemm_w4a16, mi_attn_prefill). On return pos has advanced by n, the KV
  * cache holds those positions and cur_token is the argmax of the last position's logits, as
- * mi_engine_ingest of the same ids leaves them (up to the two paths' roundings). Refused: no
- * ids, chunk above the cap, an id outside the vocabulary, past the cache, and (today) MoE
- * models and the int8 cache. Allocates its scratch on the first call (and for a larger chunk). */
+ * mi_engine_ingest of the same ids leaves them (up to the two paths' roundings). MoE layers run
+ * their expert kernels over the chunk's rows in slices. Refused: no ids, chunk above the cap,
+ * an id outside the vocabulary, past the cache, and (today) the int8 cache. Allocates its
+ * scratch on the first call (and for a larger chunk). */
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];

@@ -434,7 +434,7 @@ struct mi_engine {
     MI_TRY(alloc(&pf_q, size_t(cap) * QHD));
     MI_TRY(alloc(&pf_resid, size_t(cap) * H));
     MI_TRY(alloc(&pf_x, size_t(cap) * std::max(H, QHD)));
-    MI_TRY(alloc(&pf_h, size_t(cap) * d.inter));
+    MI_TRY(alloc(&pf_h, size_t(cap) * std::max(d.inter, 1u)));
     MI_TRY(alloc(&pf_attn, size_t(cap) * QHD));
     pf_cap = cap;
     return 0;
@@ -459,18 +459,33 @@ struct mi_engine {
       MI_TRY(mi_attn_prefill(pf_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, T, pos, &ash, pf_attn, stream));
       MI_TRY(mi_gemm_w4a16(L.o.q, L.o.s, pf_attn, pf_out, T, QHD, H, stream));
       MI_TRY(mi_res_norm(pf_out, pf_resid, L.post_norm, pf_x, T, H, 1, d.rms_eps, stream));
+      const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
+      if (d.experts) {
+        // the MoE block (moe.cl:1-13) over the chunk's rows in slices of the decode kernels' row
+        // capacity: router || shared gate, route, gate||up, down folding into the residual
+        const uint32_t slice = std::min(16u, d.max_rows);
+        for (uint32_t r0 = 0; r0 < T; r0 += slice) {
+          const uint32_t m = std::min(slice, T - r0);
+          const uint16_t* xs = pf_x + size_t(r0) * H;
+          MI_TRY(mi_gemv_f16w(L.router, xs, moe_logits, m, H, router_n, router_ksplit(), stream));
+          MI_TRY(mi_moe_route(moe_logits, moe_route, m, d.experts, d.top_k, router_n, stream));
+          MI_TRY(mi_moe_gate_up(moe_route, xs, L.moe_gu, moe_h, m, d.experts, d.top_k, H, d.moe_inter, stream));
+          MI_TRY(mi_moe_down(moe_route, moe_h, L.moe_dn, pf_resid + size_t(r0) * H, m, d.experts, d.top_k, H,
+                             d.moe_inter, stream));
+        }
+        MI_TRY(mi_res_norm(nullptr, pf_resid, next_w, pf_x, T, H, 0, d.rms_eps, stream));
+        continue;
+      }
       MI_TRY(mi_gemm_w4a16(L.gate_up.q, L.gate_up.s, pf_x, pf_out, T, H, L.gate_up.N, stream));
       MI_TRY(mi_silu_mul(pf_out, pf_h, T, d.inter, 1, stream));
       MI_TRY(mi_gemm_w4a16(L.down.q, L.down.s, pf_h, pf_out, T, d.inter, H, stream));
-      const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
       MI_TRY(mi_res_norm(pf_out, pf_resid, next_w, pf_x, T, H, 1, d.rms_eps, stream));
     }
     return 0;
   }
 
   int prefill(const uint32_t* ids, uint32_t n, uint32_t chunk) {
-    if (d.kv_int8 || d.experts)
-      return mi_fail(MI_ERR_STATE, "engine_prefill: dense models on the fp16 cache only (use ingest)");
+    if (d.kv_int8) return mi_fail(MI_ERR_STATE, "engine_prefill: the fp16 cache only (use ingest)");
     if (!ids || n == 0) return mi_fail(MI_ERR_ARG, "engine_prefill: no ids");
     if (chunk == 0) chunk = std::min(kPrefillCap, d.max_len);
     if (chunk > kPrefillCap) return mi_fail(MI_ERR_ARG, "engine_prefill: chunk above the cap (2048)");

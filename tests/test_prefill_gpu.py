@@ -181,3 +181,30 @@ def test_prefill_refusals():
     with pytest.raises(mi.MiError):
         eng.prefill(np.arange(4, dtype=np.uint32), 4096)  # chunk above the cap
     eng.close()
+
+
+def test_moe_prefill_matches_ingest():
+    """A mixture-of-experts model: the expert kernels run over the chunk's rows in slices. Layer
+    0's K/V rows come before any routing and hold the dense bar; later layers sit behind top-k
+    routing, where a near-tied expert choice may flip between the two roundings, so the last
+    logits are held to a cosine bar there."""
+    from test_engine_gpu import moe_small_desc
+    eng = mi.Engine(moe_small_desc(max_len=512), seed=12)
+    eng.capture(1)
+    n, p0 = 37, 20
+    ids = np.random.default_rng(3).integers(0, eng.desc.vocab_used, n).astype(np.uint32)
+    print(f"moe prefill vs ingest n={n} p0={p0}", flush=True)
+    eng.reset(p0, 0)
+    eng.ingest(ids)
+    c_ing, lg_ing = eng.ctrl(), eng.logits(1)[0].astype(np.float64)
+    k_ing, v_ing = kv_rows(eng, p0, n)
+    eng.reset(p0, 0)
+    eng.prefill(ids, 16)
+    c_pf, lg_pf = eng.ctrl(), eng.logits(1)[0].astype(np.float64)
+    k_pf, v_pf = kv_rows(eng, p0, n)
+    assert c_pf[mi.CTRL_POS] == c_ing[mi.CTRL_POS] == p0 + n
+    for a, b in ((k_pf[0], k_ing[0]), (v_pf[0], v_ing[0])):
+        assert np.all(np.abs(a - b) <= 0.02 * np.abs(b) + 0.02 * np.abs(b).max()), np.abs(a - b).max()
+    cos = (lg_pf * lg_ing).sum() / np.sqrt((lg_pf * lg_pf).sum() * (lg_ing * lg_ing).sum())
+    assert cos >= 0.99, cos
+    eng.close()
