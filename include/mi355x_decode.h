@@ -313,6 +313,15 @@ int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* k
                     size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page,
                     uint32_t T, uint32_t pos0, const mi_attn_shape* shape, uint16_t* attn_out,
                     void* stream);
+/* mi_attn_prefill over the int8 rotated cache (attn_prep_kv8's rows and fp16 scales, the
+ * reader of attn_decode_v2_kv8 + attn_reduce_v2_kv8, kv8.cl:535/814; head_dim 256): q as
+ * mi_attn_prep_kv8 writes it (rotated), the output fp32 in the rotated basis into out_rot
+ * [T][q_heads][256], then un-rotated into attn_out f16. */
+int mi_attn_prefill_kv8(const float* attn_q, const int8_t* kv_k, const int8_t* kv_v,
+                        const uint16_t* k_scale, const uint16_t* v_scale, size_t row_stride,
+                        size_t head_stride, size_t sc_row_stride, size_t sc_head_stride,
+                        const uint32_t* pages, uint32_t page, uint32_t T, uint32_t pos0,
+                        const mi_attn_shape* shape, float* out_rot, uint16_t* attn_out, void* stream);
 /* resid [T][hidden] = embed rows of ids [T] (pf_embed_gather); an id >= vocab leaves its row
  * and sets *flag = 0xDEAD0001 (flag may be NULL). */
 int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T,
@@ -381,9 +390,9 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
  * the matrix cores (mi_gemm_w4a16, mi_attn_prefill). On return pos has advanced by n, the KV
  * cache holds those positions and cur_token is the argmax of the last position's logits, as
  * mi_engine_ingest of the same ids leaves them (up to the two paths' roundings). MoE layers run
- * their expert kernels over the chunk's rows in slices. Refused: no ids, chunk above the cap,
- * an id outside the vocabulary, past the cache, and (today) the int8 cache. Allocates its
- * scratch on the first call (and for a larger chunk). */
+ * their expert kernels over the chunk's rows in slices; the int8 cache takes attn_prep_kv8's
+ * rows and mi_attn_prefill_kv8. Refused: no ids, chunk above the cap, an id outside the
+ * vocabulary, past the cache. Allocates its scratch on the first call (and for a larger chunk). */
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];

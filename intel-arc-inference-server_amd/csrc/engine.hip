@@ -451,12 +451,23 @@ struct mi_engine {
     MI_TRY(mi_res_norm(nullptr, pf_resid, layer[0].in_norm, pf_x, T, H, 0, d.rms_eps, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
-      uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
       MI_TRY(mi_gemm_w4a16(L.qkv.q, L.qkv.s, pf_x, pf_out, T, L.qkv.K, L.qkv.N, stream));
-      MI_TRY(mi_attn_prep(pf_ctrl, pf_out, 1, T, &ash, L.q_norm, L.k_norm, rope, pf_q, nullptr, lk, lv, HD,
-                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
-      MI_TRY(mi_attn_prefill(pf_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, T, pos, &ash, pf_attn, stream));
+      if (d.kv_int8) {  // attn_prep_kv8's rows, the int8 reader, the un-rotation (pf_out is free here)
+        int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
+        int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
+        uint16_t* lks = kv_ks + size_t(li) * d.kv_heads * d.max_len;
+        uint16_t* lvs = kv_vs + size_t(li) * d.kv_heads * d.max_len;
+        MI_TRY(mi_attn_prep_kv8(pf_ctrl, pf_out, 1, T, &ash, L.q_norm, L.k_norm, rope, pf_q, nullptr, lk, lv, lks,
+                                lvs, HD, size_t(d.max_len) * HD, 1, d.max_len, nullptr, 0, d.max_len, stream));
+        MI_TRY(mi_attn_prefill_kv8(pf_q, lk, lv, lks, lvs, HD, size_t(d.max_len) * HD, 1, d.max_len, nullptr, 0, T,
+                                   pos, &ash, pf_out, pf_attn, stream));
+      } else {
+        uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
+        uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+        MI_TRY(mi_attn_prep(pf_ctrl, pf_out, 1, T, &ash, L.q_norm, L.k_norm, rope, pf_q, nullptr, lk, lv, HD,
+                            size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+        MI_TRY(mi_attn_prefill(pf_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, T, pos, &ash, pf_attn, stream));
+      }
       MI_TRY(mi_gemm_w4a16(L.o.q, L.o.s, pf_attn, pf_out, T, QHD, H, stream));
       MI_TRY(mi_res_norm(pf_out, pf_resid, L.post_norm, pf_x, T, H, 1, d.rms_eps, stream));
       const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
@@ -485,7 +496,6 @@ struct mi_engine {
   }
 
   int prefill(const uint32_t* ids, uint32_t n, uint32_t chunk) {
-    if (d.kv_int8) return mi_fail(MI_ERR_STATE, "engine_prefill: the fp16 cache only (use ingest)");
     if (!ids || n == 0) return mi_fail(MI_ERR_ARG, "engine_prefill: no ids");
     if (chunk == 0) chunk = std::min(kPrefillCap, d.max_len);
     if (chunk > kPrefillCap) return mi_fail(MI_ERR_ARG, "engine_prefill: chunk above the cap (2048)");

@@ -170,16 +170,39 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 
 struct PrefillAttnArgs {
   const float* attn_q;  // [T][q_heads][HD] fp32
-  const uint16_t* kv_k;
-  const uint16_t* kv_v;
+  const void* kv_k;     // f16, or int8 (KV8)
+  const void* kv_v;
   const uint32_t* pages;
   uint16_t* attn_out;   // [T][q_heads * HD] f16
   size_t row_stride, head_stride;
   uint32_t page, T, pos0, q_heads;
   float scale;
+  // KV8: fp16 row scales at row * sc_row_stride + head * sc_head_stride, and the output in
+  // the cache's rotated basis, fp32 [T][q_heads][HD], for the un-rotation pass
+  const uint16_t* k_scale;
+  const uint16_t* v_scale;
+  size_t sc_row_stride, sc_head_stride;
+  float* out_rot;
 };
 
-template <int HD, int GQA>
+// 8 int8 values (two u32) widened exactly to f16: each biased byte u = q8 + 128 under an f16
+// exponent byte 0x64 is 1024 + u; subtracting 1152 leaves q8 (f16 integers up to 2048 are exact)
+__device__ __forceinline__ u4_t widen_i8x8(uint32_t x0, uint32_t x1) {
+  x0 ^= 0x80808080u;
+  x1 ^= 0x80808080u;
+  const uint32_t hi = 0x64646464u;
+  const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+  return u4_t{h2_bits(as_h2(__builtin_amdgcn_perm(hi, x0, 0x04010400u)) - bias),
+              h2_bits(as_h2(__builtin_amdgcn_perm(hi, x0, 0x04030402u)) - bias),
+              h2_bits(as_h2(__builtin_amdgcn_perm(hi, x1, 0x04010400u)) - bias),
+              h2_bits(as_h2(__builtin_amdgcn_perm(hi, x1, 0x04030402u)) - bias)};
+}
+
+// KV8: the K and V rows are int8 with one fp16 scale per (position, kv head), the attn_prep_kv8
+// form (kv8.cl): the rows are widened exactly to f16 in LDS, a score is scaled by its key's K
+// scale and a weight by its key's V scale before P V (the decode reader's order), and the
+// output stays in the rotated basis (un-rotated by unrotate_rows_kernel).
+template <int HD, int GQA, int KV8>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   constexpr uint32_t KK = HD / 32, NT = HD / 16;
   constexpr uint32_t RB = 64 / GQA;          // rows per work-group
@@ -188,6 +211,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   constexpr uint32_t ROWB = HD * 2, CW = 32; // V row bytes, bytes of one 16-dim column
   __shared__ __align__(16) uint16_t sK[KB * KROW];
   __shared__ __align__(16) unsigned char sV[KB * ROWB];
+  __shared__ float sKs[KV8 ? KB : 1], sVs[KV8 ? KB : 1];
   const uint32_t j = blockIdx.x, t0 = blockIdx.y * RB;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t qi = lane & 15u, qq = lane >> 4;
@@ -231,23 +255,46 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     return (r >> 4) * 16u * ROWB + (r & 15u) * ROWB + ((c ^ ((r >> 2) & 3u)) * CW);
   };
   const size_t hoff = (size_t)j * a.head_stride;
-  // staging: thread t loads key row t >> 2, quarter t & 3 of its K and V rows
-  constexpr uint32_t QB = ROWB / 4u;  // bytes per quarter row
+  // staging: thread t loads key row t >> 2, quarter t & 3 of its K and V rows (f16 bytes in LDS)
+  constexpr uint32_t QB = ROWB / 4u;  // f16 bytes per quarter row
   const uint32_t srow = t >> 2, squart = t & 3u;
   for (uint32_t kb = 0; kb < kend; kb += KB) {
     {
       const uint32_t key = kb + srow;
       const bool live = key < kend;
       const size_t crow = live ? (a.pages ? (size_t)a.pages[key / a.page] * a.page + key % a.page : (size_t)key) : 0;
-      const unsigned char* kp = reinterpret_cast<const unsigned char*>(a.kv_k + crow * a.row_stride + hoff) + squart * QB;
-      const unsigned char* vp = reinterpret_cast<const unsigned char*>(a.kv_v + crow * a.row_stride + hoff) + squart * QB;
+      if constexpr (KV8 == 0) {
+        const unsigned char* kp =
+            static_cast<const unsigned char*>(a.kv_k) + (crow * a.row_stride + hoff) * 2u + squart * QB;
+        const unsigned char* vp =
+            static_cast<const unsigned char*>(a.kv_v) + (crow * a.row_stride + hoff) * 2u + squart * QB;
 #pragma unroll
-      for (uint32_t i = 0; i < QB / 16u; ++i) {
-        const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-        const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-        const uint32_t byte = squart * QB + 16u * i;
-        *reinterpret_cast<u4_t*>(reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte) = kv;
-        *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = vv;
+        for (uint32_t i = 0; i < QB / 16u; ++i) {
+          const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const uint32_t byte = squart * QB + 16u * i;
+          *reinterpret_cast<u4_t*>(reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte) = kv;
+          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = vv;
+        }
+      } else {
+        const unsigned char* kp = static_cast<const unsigned char*>(a.kv_k) + crow * a.row_stride + hoff + squart * (QB / 2u);
+        const unsigned char* vp = static_cast<const unsigned char*>(a.kv_v) + crow * a.row_stride + hoff + squart * (QB / 2u);
+#pragma unroll
+        for (uint32_t i = 0; i < QB / 32u; ++i) {  // 16 int8 -> 32 bytes of f16
+          const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const uint32_t byte = squart * QB + 32u * i;
+          unsigned char* kd = reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte;
+          *reinterpret_cast<u4_t*>(kd) = widen_i8x8(kv.x, kv.y);
+          *reinterpret_cast<u4_t*>(kd + 16) = widen_i8x8(kv.z, kv.w);
+          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = widen_i8x8(vv.x, vv.y);
+          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW + 16) = widen_i8x8(vv.z, vv.w);
+        }
+        if (squart == 0) {
+          const size_t so = crow * a.sc_row_stride + (size_t)j * a.sc_head_stride;
+          sKs[srow] = live ? h2f(a.k_scale[so]) : 0.f;
+          sVs[srow] = live ? h2f(a.v_scale[so]) : 0.f;
+        }
       }
     }
     lds_barrier();
@@ -268,7 +315,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
 #pragma unroll
       for (uint32_t r = 0; r < 4; ++r) {
         const uint32_t key = g0 + 4u * qq + r;
-        sc[r] = key <= lim ? d[r] * a.scale : -INFINITY;
+        float rs = a.scale;
+        if constexpr (KV8 == 1) rs = a.scale * sKs[16u * grp + 4u * qq + r];
+        sc[r] = key <= lim ? d[r] * rs : -INFINITY;
         mx = fmaxf(mx, sc[r]);
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -287,9 +336,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
       h4_t bh, bl;
 #pragma unroll
       for (uint32_t r = 0; r < 4; ++r) {
-        const half_t h = (half_t)w[r];
+        float wv = w[r];
+        if constexpr (KV8 == 1) wv *= sVs[16u * grp + 4u * qq + r];
+        const half_t h = (half_t)wv;
         bh[r] = h;
-        bl[r] = (half_t)(w[r] - (float)h);
+        bl[r] = (half_t)(wv - (float)h);
       }
 #pragma unroll
       for (uint32_t tt = 0; tt < NT; ++tt) {
@@ -306,29 +357,49 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   float l = l_run + __shfl_xor(l_run, 16, 64);
   l = l + __shfl_xor(l, 32, 64);
   if (col_live) {
-    uint16_t* op = a.attn_out + (size_t)(t0 + prow) * a.q_heads * HD + (size_t)ph * HD;
+    if constexpr (KV8 == 1) {
+      float* op = a.out_rot + ((size_t)(t0 + prow) * a.q_heads + ph) * HD;
 #pragma unroll
-    for (uint32_t tt = 0; tt < NT; ++tt)
+      for (uint32_t tt = 0; tt < NT; ++tt)
 #pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) op[16u * tt + 4u * qq + r] = f2h(acc[tt][r] / l);
+        for (uint32_t r = 0; r < 4; ++r) op[16u * tt + 4u * qq + r] = acc[tt][r] / l;
+    } else {
+      uint16_t* op = a.attn_out + (size_t)(t0 + prow) * a.q_heads * HD + (size_t)ph * HD;
+#pragma unroll
+      for (uint32_t tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) op[16u * tt + 4u * qq + r] = f2h(acc[tt][r] / l);
+    }
   }
 }
 
-template <int HD, int GQA>
-void launch_prefill_gqa(const PrefillAttnArgs& a, uint32_t kv_heads, hipStream_t st) {
-  constexpr uint32_t RB = 64 / GQA;
-  attn_prefill_kernel<HD, GQA><<<dim3(kv_heads, (a.T + RB - 1) / RB), 256, 0, st>>>(a);
+// grid (q_heads, T), 256 lanes: attn_reduce_v2_kv8's un-rotation (kv8.cl:814-860) of one
+// (row, head) output, head_dim 256: unrotate(y) = FWHT(s * y) / 16, then f16
+__global__ __launch_bounds__(256) void unrotate_rows_kernel(const float* __restrict__ in, uint16_t* __restrict__ out,
+                                                            uint32_t q_heads) {
+  __shared__ float xch[256];
+  const uint32_t h = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+  const size_t off = ((size_t)row * q_heads + h) * 256u;
+  float v1[1] = {kv8_flip(in[off + d], kv8_sign_neg(d))};
+  fwht256<1>(v1, d, xch);
+  out[off + d] = f2h(v1[0] * 0.0625f);
 }
 
-template <int HD>
+template <int HD, int GQA, int KV8>
+void launch_prefill_gqa(const PrefillAttnArgs& a, uint32_t kv_heads, hipStream_t st) {
+  constexpr uint32_t RB = 64 / GQA;
+  attn_prefill_kernel<HD, GQA, KV8><<<dim3(kv_heads, (a.T + RB - 1) / RB), 256, 0, st>>>(a);
+}
+
+template <int HD, int KV8>
 int launch_prefill_attn(const PrefillAttnArgs& a, uint32_t gqa, uint32_t kv_heads, hipStream_t st) {
   switch (gqa) {
-    case 1: launch_prefill_gqa<HD, 1>(a, kv_heads, st); return 0;
-    case 2: launch_prefill_gqa<HD, 2>(a, kv_heads, st); return 0;
-    case 4: launch_prefill_gqa<HD, 4>(a, kv_heads, st); return 0;
-    case 5: launch_prefill_gqa<HD, 5>(a, kv_heads, st); return 0;
-    case 6: launch_prefill_gqa<HD, 6>(a, kv_heads, st); return 0;
-    case 8: launch_prefill_gqa<HD, 8>(a, kv_heads, st); return 0;
+    case 1: launch_prefill_gqa<HD, 1, KV8>(a, kv_heads, st); return 0;
+    case 2: launch_prefill_gqa<HD, 2, KV8>(a, kv_heads, st); return 0;
+    case 4: launch_prefill_gqa<HD, 4, KV8>(a, kv_heads, st); return 0;
+    case 5: launch_prefill_gqa<HD, 5, KV8>(a, kv_heads, st); return 0;
+    case 6: launch_prefill_gqa<HD, 6, KV8>(a, kv_heads, st); return 0;
+    case 8: launch_prefill_gqa<HD, 8, KV8>(a, kv_heads, st); return 0;
     default: return -1;
   }
 }
@@ -385,12 +456,37 @@ int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* k
   if ((row_stride % 8) || (head_stride % 8))
     return mi_fail(MI_ERR_ARG, "attn_prefill: KV strides must keep 8-element alignment");
   PrefillAttnArgs a{attn_q, kv_k, kv_v, pages, attn_out, row_stride, head_stride, page, T, pos0,
-                    shape->q_heads, shape->scale};
+                    shape->q_heads, shape->scale, nullptr, nullptr, 0, 0, nullptr};
   hipStream_t st = (hipStream_t)stream;
-  const int r = HD == 128 ? launch_prefill_attn<128>(a, gqa, shape->kv_heads, st)
-                          : launch_prefill_attn<256>(a, gqa, shape->kv_heads, st);
+  const int r = HD == 128 ? launch_prefill_attn<128, 0>(a, gqa, shape->kv_heads, st)
+                          : launch_prefill_attn<256, 0>(a, gqa, shape->kv_heads, st);
   if (r) return mi_fail(MI_ERR_SHAPE, "attn_prefill: unsupported GQA");
   return mi_hip((int)hipGetLastError(), "attn_prefill");
+}
+
+int mi_attn_prefill_kv8(const float* attn_q, const int8_t* kv_k, const int8_t* kv_v, const uint16_t* k_scale,
+                        const uint16_t* v_scale, size_t row_stride, size_t head_stride, size_t sc_row_stride,
+                        size_t sc_head_stride, const uint32_t* pages, uint32_t page, uint32_t T, uint32_t pos0,
+                        const mi_attn_shape* shape, float* out_rot, uint16_t* attn_out, void* stream) {
+  if (!attn_q || !kv_k || !kv_v || !k_scale || !v_scale || !out_rot || !attn_out || !shape || T == 0)
+    return mi_fail(MI_ERR_ARG, "attn_prefill_kv8: bad arguments");
+  if (shape->head_dim != 256) return mi_fail(MI_ERR_SHAPE, "attn_prefill_kv8: the rotation is defined for head_dim 256");
+  const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
+  if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads ||
+      !(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 5 || gqa == 6 || gqa == 8))
+    return mi_fail(MI_ERR_SHAPE, "attn_prefill_kv8: q_heads / kv_heads must be 1, 2, 4, 5, 6 or 8");
+  if (pages && page == 0) return mi_fail(MI_ERR_ARG, "attn_prefill_kv8: page size 0");
+  if ((row_stride % 16) || (head_stride % 16))
+    return mi_fail(MI_ERR_ARG, "attn_prefill_kv8: int8 KV strides must keep 16-byte alignment");
+  PrefillAttnArgs a{attn_q, kv_k, kv_v, pages, attn_out, row_stride, head_stride, page, T, pos0,
+                    shape->q_heads, shape->scale, k_scale, v_scale, sc_row_stride, sc_head_stride, out_rot};
+  hipStream_t st = (hipStream_t)stream;
+  if (launch_prefill_attn<256, 1>(a, gqa, shape->kv_heads, st))
+    return mi_fail(MI_ERR_SHAPE, "attn_prefill_kv8: unsupported GQA");
+  int e = (int)hipGetLastError();
+  if (e) return mi_hip(e, "attn_prefill_kv8");
+  unrotate_rows_kernel<<<dim3(shape->q_heads, T), 256, 0, st>>>(out_rot, attn_out, shape->q_heads);
+  return mi_hip((int)hipGetLastError(), "attn_prefill_kv8 unrotate");
 }
 
 int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T, uint32_t hidden,

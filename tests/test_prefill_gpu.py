@@ -208,3 +208,69 @@ def test_moe_prefill_matches_ingest():
     cos = (lg_pf * lg_ing).sum() / np.sqrt((lg_pf * lg_pf).sum() * (lg_ing * lg_ing).sum())
     assert cos >= 0.99, cos
     eng.close()
+
+
+def test_attn_prefill_kv8_rows_match_the_decode_reader():
+    """mi_attn_prefill_kv8 over the int8 rotated cache: row t equals the decode reader's
+    (attn_decode int8 + attn_reduce_kv8, itself held to fp64 attention with an fp64
+    un-rotation in test_kv8_gpu) at position pos0 + t, within rel 2e-3 / cosine 0.99999."""
+    QH, KVH, HD, Lm, T, pos0 = 16, 2, 256, 256, 20, 64
+    sh = O.attn_shape(QH, KVH, HD)
+    rng = np.random.default_rng(31)
+    k8 = rng.integers(-127, 128, size=(KVH, Lm, HD)).astype(np.int8)
+    v8 = rng.integers(-127, 128, size=(KVH, Lm, HD)).astype(np.int8)
+    ks = O.f32_to_f16_bits(rng.uniform(0.005, 0.05, (KVH, Lm)).astype(np.float32))
+    vs = O.f32_to_f16_bits(rng.uniform(0.005, 0.05, (KVH, Lm)).astype(np.float32))
+    q = rng.standard_normal((T, QH, HD)).astype(np.float32)
+    dk, dv, dks, dvs, dq = dev(k8), dev(v8), dev(ks), dev(vs), dev(q)
+    rot = empty((T, QH, HD), np.float32)
+    out = empty((T, QH * HD), np.uint16)
+    print("attn_prefill_kv8", flush=True)
+    mi.call("mi_attn_prefill_kv8", ptr(dq), ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm, None, 0, T,
+            pos0, C.byref(sh), ptr(rot), ptr(out), stream())
+    sync()
+    got = O.f16_bits_to_f32(host(out, np.uint16)).astype(np.float64).reshape(T, QH, HD)
+    tgt = 16
+    for t in (0, 7, T - 1):
+        c = np.zeros(64, np.uint32)
+        c[0], c[1] = pos0 + t, 1
+        ctrl = dev(c)
+        qt = dev(np.ascontiguousarray(q[t:t + 1]))
+        part = empty((QH, tgt, 1, HD + 2), np.float32)
+        want16 = empty((1, QH * HD), np.uint16)
+        mi.call("mi_attn_decode", ptr(ctrl), ptr(qt), 1, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm,
+                None, 0, Lm, ptr(part), 1, tgt, C.byref(sh), stream())
+        mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(part), None, ptr(want16), 1, tgt, Lm, C.byref(sh), stream())
+        sync()
+        want = O.f16_bits_to_f32(host(want16, np.uint16)).astype(np.float64).reshape(QH, HD)
+        g = got[t]
+        err = np.abs(g - want)
+        assert np.all(err <= 2e-3 * np.abs(want) + 2e-3 * np.abs(want).max(axis=-1, keepdims=True)), (t, err.max())
+        cos = (g * want).sum(-1) / np.sqrt((g * g).sum(-1) * (want * want).sum(-1))
+        assert cos.min() >= 0.99999, t
+
+
+def test_int8_cache_prefill_matches_ingest():
+    eng = mi.Engine(small_desc(max_len=256, head_dim=256, q_heads=8, kv_heads=2, kv_int8=1), seed=13)
+    eng.capture(1)
+    d = eng.desc
+    n, p0 = 30, 10
+    ids = np.random.default_rng(9).integers(0, d.vocab_used, n).astype(np.uint32)
+    print(f"int8-cache prefill vs ingest n={n} p0={p0}", flush=True)
+
+    def rows():
+        k = eng.to_host(mi.T_KV_K, 0, np.int8).reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)
+        ks = O.f16_bits_to_f32(eng.to_host(mi.T_KV_KS, 0, np.uint16).reshape(d.layers, d.kv_heads, d.max_len))
+        return k[:, :, p0:p0 + n].astype(np.float64) * ks[:, :, p0:p0 + n, None]
+
+    eng.reset(p0, 0)
+    eng.ingest(ids)
+    c_ing, lg_ing, k_ing = eng.ctrl(), eng.logits(1)[0].astype(np.float64), rows()
+    eng.reset(p0, 0)
+    eng.prefill(ids, 16)
+    c_pf, lg_pf, k_pf = eng.ctrl(), eng.logits(1)[0].astype(np.float64), rows()
+    assert c_pf[mi.CTRL_POS] == c_ing[mi.CTRL_POS] == p0 + n
+    assert np.all(np.abs(k_pf - k_ing) <= 0.03 * np.abs(k_ing).max()), np.abs(k_pf - k_ing).max()
+    scale = np.abs(lg_ing).max()
+    assert np.all(np.abs(lg_pf - lg_ing) <= 0.01 * scale), np.abs(lg_pf - lg_ing).max() / scale
+    eng.close()
