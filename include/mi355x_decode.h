@@ -306,6 +306,11 @@ int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blo
  * pf_dequant_slab.cl). 64 | K, 128 | N. */
 int mi_gemm_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, float* out,
                   uint32_t T, uint32_t K, uint32_t N, void* stream);
+/* The same for the gate||up linear (N = 2 * inter, interleave16 columns) with prep_silu_mul
+ * (prep.cl:384) in the epilogue: h [T][N/2] f16 = rne(rne(silu(rne(g))) * rne(u)), bitwise
+ * mi_gemm_w4a16 followed by mi_silu_mul. */
+int mi_gemm_w4a16_silu(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, uint16_t* h,
+                       uint32_t T, uint32_t K, uint32_t N, void* stream);
 /* Causal attention of T rows at positions pos0 .. pos0 + T - 1 (q fp32 [T][q_heads][head_dim],
  * as mi_attn_prep writes it) over the fp16 cache rows [0, pos0 + t] (row layout and page table as
  * mi_attn_decode); attn_out [T][q_heads * head_dim] f16. head_dim 128 or 256. */

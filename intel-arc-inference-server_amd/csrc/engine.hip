@@ -487,8 +487,7 @@ struct mi_engine {
         MI_TRY(mi_res_norm(nullptr, pf_resid, next_w, pf_x, T, H, 0, d.rms_eps, stream));
         continue;
       }
-      MI_TRY(mi_gemm_w4a16(L.gate_up.q, L.gate_up.s, pf_x, pf_out, T, H, L.gate_up.N, stream));
-      MI_TRY(mi_silu_mul(pf_out, pf_h, T, d.inter, 1, stream));
+      MI_TRY(mi_gemm_w4a16_silu(L.gate_up.q, L.gate_up.s, pf_x, pf_h, T, H, L.gate_up.N, stream));
       MI_TRY(mi_gemm_w4a16(L.down.q, L.down.s, pf_h, pf_out, T, d.inter, H, stream));
       MI_TRY(mi_res_norm(pf_out, pf_resid, next_w, pf_x, T, H, 1, d.rms_eps, stream));
     }

@@ -68,11 +68,16 @@ __device__ __forceinline__ u4_t dequant_scaled(uint32_t w, h2_t s2) {
   return u4_t{h2_bits(p0 * s2), h2_bits(p1 * s2), h2_bits(p2 * s2), h2_bits(p3 * s2)};
 }
 
+// SILU: the columns are gate||up in the interleave16 order (gate block, up block, ...); a wave's
+// 64 columns hold two such pairs, so each lane has the gate and up value of the same output in
+// its tiles j and j + 1, and writes h [T][N/2] f16 = rne(rne(silu(rne(g))) * rne(u)) (the
+// arithmetic of prep_silu_mul, prep.cl:384) instead of the fp32 output.
+template <bool SILU>
 __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restrict__ qweight,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ x,
-                                                         float* __restrict__ out, uint32_t T, uint32_t K,
-                                                         uint32_t N) {
+                                                         float* __restrict__ out, uint16_t* __restrict__ h_out,
+                                                         uint32_t T, uint32_t K, uint32_t N) {
   __shared__ __align__(16) uint16_t As[2][GBM][GROW];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1u;
@@ -157,8 +162,17 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
     for (uint32_t r = 0; r < 4; ++r) {
       const uint32_t row = m0 + 64u * wm + 16u * i + 4u * fq + r;
       if (row < T) {
+        if constexpr (SILU) {
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) out[(size_t)row * N + ncol + 16u * j] = acc[i][j][r];
+          for (uint32_t jp = 0; jp < 2; ++jp) {
+            const uint16_t g_b = f2h(acc[i][2 * jp][r]), u_b = f2h(acc[i][2 * jp + 1][r]);
+            const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
+            h_out[(size_t)row * (N / 2) + (n0 + 64u * wn) / 2 + 16u * jp + fr] = f2h(h2f(s_b) * h2f(u_b));
+          }
+        } else {
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j) out[(size_t)row * N + ncol + 16u * j] = acc[i][j][r];
+        }
       }
     }
 }
@@ -436,9 +450,23 @@ int mi_gemm_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_
       reinterpret_cast<uintptr_t>(scales) % 8)
     return mi_fail(MI_ERR_ARG, "gemm_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
   if ((T + GBM - 1) / GBM > 65535) return mi_fail(MI_ERR_SHAPE, "gemm_w4a16: too many rows");
-  gemm_w4a16_kernel<<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(qweight, scales, x, out,
-                                                                                         T, K, N);
+  gemm_w4a16_kernel<false><<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(
+      qweight, scales, x, out, nullptr, T, K, N);
   return mi_hip((int)hipGetLastError(), "gemm_w4a16");
+}
+
+int mi_gemm_w4a16_silu(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, uint16_t* h, uint32_t T,
+                       uint32_t K, uint32_t N, void* stream) {
+  if (!qweight || !scales || !x || !h || T == 0) return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: bad arguments");
+  if (K == 0 || K % GBK || N == 0 || N % GBN)
+    return mi_fail(MI_ERR_SHAPE, "gemm_w4a16_silu: K must be a multiple of 64 and N of 128");
+  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(scales) % 8)
+    return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: qweight/x need 16-byte, scales 8-byte alignment");
+  if ((T + GBM - 1) / GBM > 65535) return mi_fail(MI_ERR_SHAPE, "gemm_w4a16_silu: too many rows");
+  gemm_w4a16_kernel<true><<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(
+      qweight, scales, x, nullptr, h, T, K, N);
+  return mi_hip((int)hipGetLastError(), "gemm_w4a16_silu");
 }
 
 int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v, size_t row_stride,

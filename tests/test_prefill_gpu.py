@@ -74,6 +74,23 @@ def test_gemm_exact_arithmetic():
     assert np.array_equal(host(out, np.float32).astype(np.float64), want)
 
 
+def test_gemm_silu_is_gemm_then_silu_mul():
+    """mi_gemm_w4a16_silu: SwiGLU in the GEMM's epilogue, bitwise mi_gemm_w4a16 followed by
+    mi_silu_mul (the interleave16 gate||up columns)."""
+    T, K, I = 77, 1024, 640
+    qw, sc = weights(K, 2 * I, 8)
+    x = O.f32_to_f16_bits(np.random.default_rng(8).standard_normal((T, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    out = empty((T, 2 * I), np.float32)
+    want = empty((T, I), np.uint16)
+    got = empty((T, I), np.uint16)
+    mi.call("mi_gemm_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(out), T, K, 2 * I, stream())
+    mi.call("mi_silu_mul", ptr(out), ptr(want), T, I, 1, stream())
+    mi.call("mi_gemm_w4a16_silu", ptr(dq), ptr(ds), ptr(dx), ptr(got), T, K, 2 * I, stream())
+    sync()
+    assert np.array_equal(host(got, np.uint16), host(want, np.uint16))
+
+
 def test_gemm_refuses_bad_shapes():
     with pytest.raises(mi.MiError):
         mi.call("mi_gemm_w4a16", 16, 16, 16, 16, 4, 100, 128, None)
