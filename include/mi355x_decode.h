@@ -327,6 +327,13 @@ int mi_attn_prefill_kv8(const float* attn_q, const int8_t* kv_k, const int8_t* k
                         size_t head_stride, size_t sc_row_stride, size_t sc_head_stride,
                         const uint32_t* pages, uint32_t page, uint32_t T, uint32_t pos0,
                         const mi_attn_shape* shape, float* out_rot, uint16_t* attn_out, void* stream);
+/* mi_attn_prep for a chunk's T rows (positions pos0 .. pos0 + T - 1) from a one-slice fold
+ * qkv [T][qkv_n] fp32, one wave per (head, row): bitwise mi_attn_prep with S = 1 and n_act = T
+ * (plain q||k||v, not gated, head_dim 128 or 256). The caller keeps pos0 + T within the cache. */
+int mi_attn_prep_rows(const float* qkv, uint32_t T, uint32_t pos0, const mi_attn_shape* shape,
+                      const float* q_norm, const float* k_norm, const float* rope, float* attn_q,
+                      uint16_t* kv_k, uint16_t* kv_v, size_t row_stride, size_t head_stride,
+                      const uint32_t* pages, uint32_t page, void* stream);
 /* resid [T][hidden] = embed rows of ids [T] (pf_embed_gather); an id >= vocab leaves its row
  * and sets *flag = 0xDEAD0001 (flag may be NULL). */
 int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T,

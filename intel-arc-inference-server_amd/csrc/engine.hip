@@ -464,8 +464,8 @@ struct mi_engine {
       } else {
         uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
         uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
-        MI_TRY(mi_attn_prep(pf_ctrl, pf_out, 1, T, &ash, L.q_norm, L.k_norm, rope, pf_q, nullptr, lk, lv, HD,
-                            size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+        MI_TRY(mi_attn_prep_rows(pf_out, T, pos, &ash, L.q_norm, L.k_norm, rope, pf_q, lk, lv, HD,
+                                 size_t(d.max_len) * HD, nullptr, 0, stream));
         MI_TRY(mi_attn_prefill(pf_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, T, pos, &ash, pf_attn, stream));
       }
       MI_TRY(mi_gemm_w4a16(L.o.q, L.o.s, pf_attn, pf_out, T, QHD, H, stream));

@@ -418,6 +418,97 @@ int launch_prefill_attn(const PrefillAttnArgs& a, uint32_t gqa, uint32_t kv_head
   }
 }
 
+// attn_prep for the chunk's rows (prep.cl attn_prep, attn.cl:361-372) with one wave per (head,
+// row): grid (q_heads + 2 kv_heads, ceil(T / 4)), 256 lanes; wave w of work-group (hh, y) takes
+// row 4 y + w of head hh (q heads, then k, then v), lane l elements l + 64 k. The chain is
+// attn_prep's operation for operation on a one-slice fold (qkv [T][qkv_n] fp32): q/k rounded to
+// f16, the RMSNorm with the 256-lane tree's order (a lane's own elements, then the 64-lane
+// shuffle tree), RoPE's rotate_half pairs, q -> attn_q fp32, k and v -> the f16 cache row of
+// position pos0 + t. No work-group barrier: the waves are independent.
+template <int HD>
+__global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict__ qkv, uint32_t T, uint32_t pos0,
+                                                        uint32_t q_heads, uint32_t kv_heads, uint32_t rot_dim,
+                                                        uint32_t qkv_n, const float* __restrict__ q_norm,
+                                                        const float* __restrict__ k_norm, const float* __restrict__ rope,
+                                                        float* __restrict__ attn_q, uint16_t* __restrict__ kv_k,
+                                                        uint16_t* __restrict__ kv_v, size_t row_stride, size_t head_stride,
+                                                        const uint32_t* __restrict__ pages, uint32_t page, float eps) {
+  constexpr uint32_t EPL = HD / 64u;
+  __shared__ float s_row[4][HD];
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t hh = blockIdx.x, t = blockIdx.y * 4u + wave;
+  if (t >= T) return;  // uniform per wave
+  const bool is_q = hh < q_heads, is_k = !is_q && hh < q_heads + kv_heads;
+  const uint32_t h = is_q ? hh : (is_k ? hh - q_heads : hh - q_heads - kv_heads);
+  const float* src = qkv + (size_t)t * qkv_n + (size_t)hh * HD;  // q || k || v, HD columns per head
+  const uint32_t p = pos0 + t;
+  const size_t crow = pages ? (size_t)pages[p / page] * page + p % page : (size_t)p;
+  float raw[EPL];
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) raw[k] = src[lane + 64u * k];
+  if (!is_q && !is_k) {
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) kv_v[crow * row_stride + h * head_stride + lane + 64u * k] = f2h(raw[k]);
+    return;
+  }
+  const float* nw = is_q ? q_norm : k_norm;
+  const uint32_t half = rot_dim / 2u;
+  const float* cs = rope + (size_t)p * 2u * half;
+  float wn[EPL], rc[EPL], rsn[EPL], xf[EPL], nv[EPL];
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) {
+    const uint32_t e = lane + 64u * k;
+    wn[k] = nw ? nw[e] : 0.f;
+    rc[k] = 1.f;
+    rsn[k] = 0.f;
+    if (e < rot_dim) {
+      const uint32_t ii = e < half ? e : e - half;
+      rc[k] = cs[ii];
+      rsn[k] = cs[half + ii];
+    }
+    xf[k] = h2f(f2h(raw[k]));
+  }
+  if (nw) {
+    float sq[EPL];
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) sq[k] = xf[k] * xf[k];
+    float acc;
+    if constexpr (EPL == 4) acc = (sq[0] + sq[2]) + (sq[1] + sq[3]);
+    else acc = sq[0] + sq[1];
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) acc += __shfl_down(acc, st, 64);
+    const float tot = __shfl(acc, 0, 64);
+    const float rstd = 1.0f / sqrtf(tot / (float)HD + eps);
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) nv[k] = h2f(f2h(xf[k] * rstd * wn[k]));
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < EPL; ++k) nv[k] = xf[k];
+  }
+  float* nrm = s_row[wave];
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) nrm[lane + 64u * k] = nv[k];
+  wave_lds_sync();
+#pragma unroll
+  for (uint32_t k = 0; k < EPL; ++k) {
+    const uint32_t e = lane + 64u * k;
+    float out;
+    if (e < half) {
+      const float tt = nrm[e + half] * rsn[k];
+      out = __builtin_fmaf(nv[k], rc[k], -tt);
+    } else if (e < rot_dim) {
+      const float tt = nrm[e - half] * rsn[k];
+      out = __builtin_fmaf(nv[k], rc[k], tt);
+    } else {
+      out = nv[k];
+    }
+    if (is_q)
+      attn_q[((size_t)t * q_heads + h) * HD + e] = out;
+    else
+      kv_k[crow * row_stride + h * head_stride + e] = f2h(out);
+  }
+}
+
 // grid (T), 256 lanes: resid[t] = embed[ids[t]]; an id outside the table leaves the row and
 // sets the flag word (the caller's host check rejects such ids before launching)
 __global__ __launch_bounds__(256) void embed_rows_kernel(const uint32_t* __restrict__ ids,
@@ -515,6 +606,31 @@ int mi_attn_prefill_kv8(const float* attn_q, const int8_t* kv_k, const int8_t* k
   if (e) return mi_hip(e, "attn_prefill_kv8");
   unrotate_rows_kernel<<<dim3(shape->q_heads, T), 256, 0, st>>>(out_rot, attn_out, shape->q_heads);
   return mi_hip((int)hipGetLastError(), "attn_prefill_kv8 unrotate");
+}
+
+int mi_attn_prep_rows(const float* qkv, uint32_t T, uint32_t pos0, const mi_attn_shape* shape, const float* q_norm,
+                      const float* k_norm, const float* rope, float* attn_q, uint16_t* kv_k, uint16_t* kv_v,
+                      size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page, void* stream) {
+  if (!qkv || !shape || !rope || !attn_q || !kv_k || !kv_v || T == 0)
+    return mi_fail(MI_ERR_ARG, "attn_prep_rows: bad arguments");
+  const uint32_t HD = shape->head_dim;
+  if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prep_rows: head_dim must be 128 or 256");
+  if (shape->gated || shape->kv_heads == 0 || shape->k_off != shape->q_heads * HD ||
+      shape->v_off != (shape->q_heads + shape->kv_heads) * HD || shape->qkv_n != shape->v_off + shape->kv_heads * HD)
+    return mi_fail(MI_ERR_SHAPE, "attn_prep_rows: a plain q||k||v layout (not gated)");
+  if (shape->rot_dim > HD || shape->rot_dim % 2) return mi_fail(MI_ERR_SHAPE, "attn_prep_rows: bad rot_dim");
+  if (pages && page == 0) return mi_fail(MI_ERR_ARG, "attn_prep_rows: page size 0");
+  const dim3 grid(shape->q_heads + 2 * shape->kv_heads, (T + 3) / 4);
+  hipStream_t st = (hipStream_t)stream;
+  if (HD == 128)
+    prep_rows_kernel<128><<<grid, 256, 0, st>>>(qkv, T, pos0, shape->q_heads, shape->kv_heads, shape->rot_dim,
+                                                shape->qkv_n, q_norm, k_norm, rope, attn_q, kv_k, kv_v, row_stride,
+                                                head_stride, pages, page, shape->eps);
+  else
+    prep_rows_kernel<256><<<grid, 256, 0, st>>>(qkv, T, pos0, shape->q_heads, shape->kv_heads, shape->rot_dim,
+                                                shape->qkv_n, q_norm, k_norm, rope, attn_q, kv_k, kv_v, row_stride,
+                                                head_stride, pages, page, shape->eps);
+  return mi_hip((int)hipGetLastError(), "attn_prep_rows");
 }
 
 int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T, uint32_t hidden,

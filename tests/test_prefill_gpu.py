@@ -91,6 +91,37 @@ def test_gemm_silu_is_gemm_then_silu_mul():
     assert np.array_equal(host(got, np.uint16), host(want, np.uint16))
 
 
+@pytest.mark.parametrize("QH,KVH,HD,rot,qk,paged", [(40, 8, 128, 128, True, False), (16, 2, 256, 64, False, True)])
+def test_attn_prep_rows_is_attn_prep(QH, KVH, HD, rot, qk, paged):
+    """mi_attn_prep_rows (one wave per head and row): bitwise mi_attn_prep on the same one-slice
+    fold, for T rows at pos0 (attn_q and the written cache rows; the other rows untouched)."""
+    sh = O.attn_shape(QH, KVH, HD, rot_dim=rot)
+    T, pos0, Lm, P = 37, 100, 256, 64
+    rng = np.random.default_rng(QH + HD)
+    qkv = rng.standard_normal((T, sh.qkv_n)).astype(np.float32)
+    qn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk else None
+    kn = (1 + 0.05 * rng.standard_normal(HD)).astype(np.float32) if qk else None
+    rope = O.rope_table(1e6, rot, Lm)
+    pages = rng.permutation(Lm // P).astype(np.uint32) if paged else None
+    kk = O.f32_to_f16_bits(rng.standard_normal((KVH, Lm, HD)).astype(np.float32))
+    keep = [dev(qkv), dev(qn), dev(kn), dev(rope), dev(pages)]
+    pp = [ptr(k) if k is not None else None for k in keep]
+    c = np.zeros(64, np.uint32)
+    c[0], c[1] = pos0, T
+    ctrl = dev(c)
+    q1, k1, v1 = empty((T, QH, HD), np.float32), dev(kk), dev(kk)
+    q2, k2, v2 = empty((T, QH, HD), np.float32), dev(kk), dev(kk)
+    print(f"attn_prep_rows {QH}/{KVH}x{HD}", flush=True)
+    mi.call("mi_attn_prep", ptr(ctrl), pp[0], 1, T, C.byref(sh), pp[1], pp[2], pp[3], ptr(q1), None, ptr(k1),
+            ptr(v1), HD, Lm * HD, pp[4], P if paged else 0, Lm, stream())
+    mi.call("mi_attn_prep_rows", pp[0], T, pos0, C.byref(sh), pp[1], pp[2], pp[3], ptr(q2), ptr(k2), ptr(v2), HD,
+            Lm * HD, pp[4], P if paged else 0, stream())
+    sync()
+    assert np.array_equal(host(q2, np.uint32), host(q1, np.uint32))
+    assert np.array_equal(host(k2, np.uint16), host(k1, np.uint16))
+    assert np.array_equal(host(v2, np.uint16), host(v1, np.uint16))
+
+
 def test_gemm_refuses_bad_shapes():
     with pytest.raises(mi.MiError):
         mi.call("mi_gemm_w4a16", 16, 16, 16, 16, 4, 100, 128, None)
