@@ -82,3 +82,21 @@ def test_engine_rejects_int8_kv_off_head_dim_256():
     d = mi.dense_desc(2, 512, 8, 2, 128, 1024, 4096, 512, kv_int8=1)
     assert not L.mi_engine_create(C.byref(d), 1, None)
     assert b"unsupported model shape" in L.mi_last_error()
+
+
+def test_prefill_and_handoff_argument_errors_without_a_gpu():
+    """The prefill kernels' and the hand-off initialiser's argument checks run before any launch."""
+    import oracle as O
+    L = mi.lib()
+    assert L.mi_gemv_handoff_init(None, 16, None) == -1
+    assert L.mi_gemm_w4a16(16, 16, 16, 16, 4, 96, 128, None) == -2       # K not a multiple of 64
+    assert L.mi_gemm_w4a16(16, 16, 16, 16, 4, 128, 96, None) == -2       # N not a multiple of 128
+    assert L.mi_gemm_w4a16_silu(None, 16, 16, 16, 4, 128, 128, None) == -1
+    sh = O.attn_shape(8, 2, 64)
+    assert L.mi_attn_prefill(16, 16, 16, 64, 64, None, 0, 4, 0, C.byref(sh), 16, None) == -2  # head_dim 64
+    sh = O.attn_shape(8, 2, 128, gated=True)
+    assert L.mi_attn_prep_rows(16, 4, 0, C.byref(sh), None, None, 16, 16, 16, 16, 128, 128, None, 0, None) == -2
+    sh = O.attn_shape(16, 2, 128)
+    assert L.mi_attn_prefill_kv8(16, 16, 16, 16, 16, 128, 128, 1, 128, None, 0, 4, 0, C.byref(sh), 16, 16,
+                                 None) == -2  # the rotation needs head_dim 256
+    assert L.mi_engine_prefill(None, None, 0, 0) == -1
