@@ -11,8 +11,10 @@
 // gemm_w4a16_kernel: out[T][N] fp32 = x[T][K] (f16) . W[K][N] (int4 GPTQ g64, layout 0). The
 // contraction is a dense GEMM here (2 T K N flops over K N / 2 weight bytes): MFMA-bound from a
 // few dozen rows, so it is tiled for the matrix cores rather than streamed like the decode GEMV.
-//   * work-group tile 128 rows x 128 columns, 4 waves in 2 x 2, each wave 64 x 64 = 4 x 4
-//     v_mfma_f32_16x16x32_f16 tiles (64 fp32 accumulators per lane);
+//   * 4 waves per work-group, each 16 RI rows x 64 columns = RI x 4 v_mfma_f32_16x16x32_f16
+//     tiles; WM waves along the rows: tiles of 128 x 256 (RI 8, one row of waves: the B words
+//     are loaded and dequantised once per work-group and serve 128 rows), 64 x 256 and 128 x 128
+//     (see launch_gemm for the choice);
 //   * one 64-deep k-group per iteration (one scale per column). The activations go through LDS,
 //     double-buffered (the next group's rows are loaded into registers while the current group
 //     is multiplied, then written to the other buffer). The weights skip LDS: a B fragment of
@@ -34,6 +36,7 @@
 // high + low parts, so the result is fp32-accurate attention; keys past a row's position are
 // -inf. Every wave covers every key its rows need, so no merge across waves is needed.
 #include <algorithm>
+#include <string>
 
 #include "mi_capi_internal.h"
 #include "mi_common.h"
@@ -44,7 +47,7 @@ namespace {
 // ---------------------------------------------------------------------------------------------
 // the int4 linear for many rows
 // ---------------------------------------------------------------------------------------------
-constexpr uint32_t GBM = 128, GBN = 128, GBK = 64;
+constexpr uint32_t GBK = 64;
 constexpr uint32_t GPAD = 8;             // f16 of padding per LDS row (a 144-byte stride)
 constexpr uint32_t GROW = GBK + GPAD;    // LDS row length in f16
 
@@ -72,25 +75,27 @@ __device__ __forceinline__ u4_t dequant_scaled(uint32_t w, h2_t s2) {
 // 64 columns hold two such pairs, so each lane has the gate and up value of the same output in
 // its tiles j and j + 1, and writes h [T][N/2] f16 = rne(rne(silu(rne(g))) * rne(u)) (the
 // arithmetic of prep_silu_mul, prep.cl:384) instead of the fp32 output.
-template <bool SILU>
-__global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restrict__ qweight,
+template <bool SILU, uint32_t WM, uint32_t RI, uint32_t LB>
+__global__ __launch_bounds__(256, LB) void gemm_w4a16_kernel(const uint32_t* __restrict__ qweight,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ x,
                                                          float* __restrict__ out, uint16_t* __restrict__ h_out,
                                                          uint32_t T, uint32_t K, uint32_t N) {
-  __shared__ __align__(16) uint16_t As[2][GBM][GROW];
+  // WM waves along the rows, 4 / WM along the columns, each wave 16 RI rows x 64 columns
+  constexpr uint32_t BM = 16u * RI * WM, BN = 256u / WM, WN = 4u / WM, AI = BM / 32u;
+  __shared__ __align__(16) uint16_t As[2][BM][GROW];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
-  const uint32_t n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  const uint32_t wm = wave / WN, wn = wave % WN;
+  const uint32_t n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const uint32_t G = K / GBK;
   const uint32_t fr = lane & 15u, fq = lane >> 4;  // fragment row/column, k chunk (8 k)
 
-  // activations, staged through LDS: thread t takes rows (t >> 3) + 32 i (i < 4), 8-k chunk t & 7
+  // activations, staged through LDS: thread t takes rows (t >> 3) + 32 i (i < BM / 32), 8-k chunk t & 7
   const uint32_t a_row = t >> 3, a_chunk = t & 7u;
-  u4_t a_st[4];
+  u4_t a_st[AI];
   auto load_a = [&](uint32_t g) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < AI; ++i) {
       const uint32_t row = m0 + a_row + 32u * i;
       a_st[i] = row < T ? *reinterpret_cast<const u4_t*>(x + (size_t)row * K + g * GBK + 8u * a_chunk)
                         : u4_t{0u, 0u, 0u, 0u};
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
   };
   auto store_a = [&](uint32_t buf) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i)
+    for (uint32_t i = 0; i < AI; ++i)
       *reinterpret_cast<u4_t*>(&As[buf][a_row + 32u * i][8u * a_chunk]) = perm_pairs(a_st[i]);
   };
   // weights, straight into registers: the B fragment of n-tile j and k half ks is one word per
@@ -116,9 +121,9 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
     for (uint32_t j = 0; j < 4; ++j) b_s[j] = scales[(size_t)g * N + ncol + 16u * j];
   };
 
-  f4_t acc[4][4];
+  f4_t acc[RI][4];
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i)
+  for (uint32_t i = 0; i < RI; ++i)
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -142,12 +147,12 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
     }
 #pragma unroll
     for (uint32_t ks = 0; ks < 2; ++ks) {
-      h8_t af[4];
+      h8_t af[RI];
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][64u * wm + 16u * i + fr][32u * ks + 8u * fq]);
+      for (uint32_t i = 0; i < RI; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][16u * RI * wm + 16u * i + fr][32u * ks + 8u * fq]);
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i)
+      for (uint32_t i = 0; i < RI; ++i)
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[ks][j], acc[i][j], 0, 0, 0);
@@ -157,10 +162,10 @@ __global__ __launch_bounds__(256) void gemm_w4a16_kernel(const uint32_t* __restr
   }
   // lane holds rows 4 (lane >> 4) + r of column lane & 15 of each 16 x 16 tile
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i)
+  for (uint32_t i = 0; i < RI; ++i)
 #pragma unroll
     for (uint32_t r = 0; r < 4; ++r) {
-      const uint32_t row = m0 + 64u * wm + 16u * i + 4u * fq + r;
+      const uint32_t row = m0 + 16u * RI * wm + 16u * i + 4u * fq + r;
       if (row < T) {
         if constexpr (SILU) {
 #pragma unroll
@@ -530,34 +535,50 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint32_t* __restr
 
 using namespace mi;
 
+// The work-group tile of the GEMM. Every tile sums a column over the k-groups in the same MFMA
+// order, so the choice changes the speed only, never a bit of the result:
+//   * 128 x 256 (4 waves of 128 x 64, two waves per SIMD): half the dequantisation per MFMA and
+//     the fewest loads per flop; taken when its grid fills the chip's two slots per CU to at
+//     least 7/8 (the qkv and gate||up linears of a long chunk);
+//   * 64 x 256 (4 waves of 64 x 64, three per SIMD): twice the work-groups of the former, for
+//     the narrower linears (o and down) whose 128 x 256 grid would leave CUs idle;
+//   * 128 x 128 (2 x 2 waves of 64 x 64) when N is not a multiple of 256.
+template <bool SILU>
+static int launch_gemm(const char* name, const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
+                       float* out, uint16_t* h, uint32_t T, uint32_t K, uint32_t N, void* stream) {
+  if (!qweight || !scales || !x || (!out && !h) || T == 0) return mi_fail(MI_ERR_ARG, (std::string(name) + ": bad arguments").c_str());
+  if (K == 0 || K % GBK || N == 0 || N % 128u)
+    return mi_fail(MI_ERR_SHAPE, (std::string(name) + ": K must be a multiple of 64 and N of 128").c_str());
+  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(scales) % 8)
+    return mi_fail(MI_ERR_ARG, (std::string(name) + ": qweight/x need 16-byte, scales 8-byte alignment").c_str());
+  if ((T + 63u) / 64u > 65535u) return mi_fail(MI_ERR_SHAPE, (std::string(name) + ": too many rows").c_str());
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return mi_hip((int)hipGetLastError(), name);
+  const uint32_t rb = (T + 127u) / 128u;
+  hipStream_t st = (hipStream_t)stream;
+  if (N % 256u == 0 && (uint64_t)(N / 256u) * rb * 8u >= 7ull * 2u * (uint64_t)cus)
+    gemm_w4a16_kernel<SILU, 1, 8, 2><<<dim3(N / 256u, rb), 256, 0, st>>>(qweight, scales, x, out, h, T, K, N);
+  else if (N % 256u == 0)
+    gemm_w4a16_kernel<SILU, 1, 4, 1><<<dim3(N / 256u, (T + 63u) / 64u), 256, 0, st>>>(qweight, scales, x, out, h,
+                                                                                        T, K, N);
+  else
+    gemm_w4a16_kernel<SILU, 2, 4, 1><<<dim3(N / 128u, rb), 256, 0, st>>>(qweight, scales, x, out, h, T, K, N);
+  return mi_hip((int)hipGetLastError(), name);
+}
+
 extern "C" {
 
 int mi_gemm_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, float* out, uint32_t T,
                   uint32_t K, uint32_t N, void* stream) {
-  if (!qweight || !scales || !x || !out || T == 0) return mi_fail(MI_ERR_ARG, "gemm_w4a16: bad arguments");
-  if (K == 0 || K % GBK || N == 0 || N % GBN)
-    return mi_fail(MI_ERR_SHAPE, "gemm_w4a16: K must be a multiple of 64 and N of 128");
-  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(scales) % 8)
-    return mi_fail(MI_ERR_ARG, "gemm_w4a16: qweight/x need 16-byte, scales 8-byte alignment");
-  if ((T + GBM - 1) / GBM > 65535) return mi_fail(MI_ERR_SHAPE, "gemm_w4a16: too many rows");
-  gemm_w4a16_kernel<false><<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(
-      qweight, scales, x, out, nullptr, T, K, N);
-  return mi_hip((int)hipGetLastError(), "gemm_w4a16");
+  return launch_gemm<false>("gemm_w4a16", qweight, scales, x, out, nullptr, T, K, N, stream);
 }
 
 int mi_gemm_w4a16_silu(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x, uint16_t* h, uint32_t T,
                        uint32_t K, uint32_t N, void* stream) {
-  if (!qweight || !scales || !x || !h || T == 0) return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: bad arguments");
-  if (K == 0 || K % GBK || N == 0 || N % GBN)
-    return mi_fail(MI_ERR_SHAPE, "gemm_w4a16_silu: K must be a multiple of 64 and N of 128");
-  if (reinterpret_cast<uintptr_t>(qweight) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(scales) % 8)
-    return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: qweight/x need 16-byte, scales 8-byte alignment");
-  if ((T + GBM - 1) / GBM > 65535) return mi_fail(MI_ERR_SHAPE, "gemm_w4a16_silu: too many rows");
-  gemm_w4a16_kernel<true><<<dim3(N / GBN, (T + GBM - 1) / GBM), 256, 0, (hipStream_t)stream>>>(
-      qweight, scales, x, nullptr, h, T, K, N);
-  return mi_hip((int)hipGetLastError(), "gemm_w4a16_silu");
+  if (!h) return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: bad arguments");
+  return launch_gemm<true>("gemm_w4a16_silu", qweight, scales, x, nullptr, h, T, K, N, stream);
 }
 
 int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v, size_t row_stride,
