@@ -92,14 +92,21 @@ __global__ __launch_bounds__(256, LB) void gemm_w4a16_kernel(const uint32_t* __r
 
   // activations, staged through LDS: thread t takes rows (t >> 3) + 32 i (i < BM / 32), 8-k chunk t & 7
   const uint32_t a_row = t >> 3, a_chunk = t & 7u;
+  // buffer loads: 32-bit offsets keep the addresses out of 64-bit registers; the row sits in the
+  // per-thread offset, so a row at or past T lies outside the resource's T K elements and reads 0
+  const __amdgpu_buffer_rsrc_t x_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), 0, T * K * 2u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t w_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(qweight), 0, (K / 8u) * N * 4u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t s_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(scales), 0, (K / GBK) * N * 2u, 0x00020000);
+  const uint32_t a_voff = ((m0 + a_row) * K + 8u * a_chunk) * 2u;
   u4_t a_st[AI];
   auto load_a = [&](uint32_t g) {
 #pragma unroll
-    for (uint32_t i = 0; i < AI; ++i) {
-      const uint32_t row = m0 + a_row + 32u * i;
-      a_st[i] = row < T ? *reinterpret_cast<const u4_t*>(x + (size_t)row * K + g * GBK + 8u * a_chunk)
-                        : u4_t{0u, 0u, 0u, 0u};
-    }
+    for (uint32_t i = 0; i < AI; ++i)
+      a_st[i] = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rs, a_voff + 32u * i * K * 2u, g * GBK * 2u, 0));
   };
   auto store_a = [&](uint32_t buf) {
 #pragma unroll
@@ -109,6 +116,7 @@ __global__ __launch_bounds__(256, LB) void gemm_w4a16_kernel(const uint32_t* __r
   // weights, straight into registers: the B fragment of n-tile j and k half ks is one word per
   // lane (8 k of column 16 j + fr, word row 4 ks + fq of the group), dequantised just before use
   const uint32_t ncol = n0 + 64u * wn + fr;
+  const uint32_t w_voff = (fq * N + ncol) * 4u, s_voff = ncol * 2u;
   uint32_t b_w[2][4];
   uint16_t b_s[4];
   auto load_b = [&](uint32_t g) {
@@ -116,9 +124,10 @@ __global__ __launch_bounds__(256, LB) void gemm_w4a16_kernel(const uint32_t* __r
     for (uint32_t ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j)
-        b_w[ks][j] = __builtin_nontemporal_load(qweight + (size_t)(8u * g + 4u * ks + fq) * N + ncol + 16u * j);
+        b_w[ks][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rs, w_voff, ((8u * g + 4u * ks) * N + 16u * j) * 4u, 2);
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) b_s[j] = scales[(size_t)g * N + ncol + 16u * j];
+    for (uint32_t j = 0; j < 4; ++j)
+      b_s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, s_voff, (g * N + 16u * j) * 2u, 0);
   };
 
   f4_t acc[RI][4];
@@ -553,6 +562,10 @@ static int launch_gemm(const char* name, const uint32_t* qweight, const uint16_t
       reinterpret_cast<uintptr_t>(scales) % 8)
     return mi_fail(MI_ERR_ARG, (std::string(name) + ": qweight/x need 16-byte, scales 8-byte alignment").c_str());
   if ((T + 63u) / 64u > 65535u) return mi_fail(MI_ERR_SHAPE, (std::string(name) + ": too many rows").c_str());
+  // the kernels' buffer loads take 32-bit byte offsets: x (with the last tile's rows past T) and
+  // the packed weights stay below 2 GiB
+  if (((uint64_t)T + 128u) * K * 2u >= (1ull << 31) || (uint64_t)K * N / 2u >= (1ull << 31))
+    return mi_fail(MI_ERR_SHAPE, (std::string(name) + ": x or qweight beyond 2 GiB").c_str());
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return mi_hip((int)hipGetLastError(), name);
