@@ -13,8 +13,8 @@
 // few dozen rows, so it is tiled for the matrix cores rather than streamed like the decode GEMV.
 //   * 4 waves per work-group, each 16 RI rows x 64 columns = RI x 4 v_mfma_f32_16x16x32_f16
 //     tiles; WM waves along the rows: tiles of 128 x 256 (RI 8, one row of waves: the B words
-//     are loaded and dequantised once per work-group and serve 128 rows), 64 x 256 and 128 x 128
-//     (see launch_gemm for the choice);
+//     are loaded and dequantised once per work-group and serve 128 rows), 96 x 256, 64 x 256 and
+//     128 x 128 (see launch_gemm for the choice);
 //   * one 64-deep k-group per iteration (one scale per column). The activations go through LDS,
 //     double-buffered (the next group's rows are loaded into registers while the current group
 //     is multiplied, then written to the other buffer). The weights skip LDS: a B fragment of
@@ -545,13 +545,12 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint32_t* __restr
 using namespace mi;
 
 // The work-group tile of the GEMM. Every tile sums a column over the k-groups in the same MFMA
-// order, so the choice changes the speed only, never a bit of the result:
-//   * 128 x 256 (4 waves of 128 x 64, two waves per SIMD): half the dequantisation per MFMA and
-//     the fewest loads per flop; taken when its grid fills the chip's two slots per CU to at
-//     least 7/8 (the qkv and gate||up linears of a long chunk);
-//   * 64 x 256 (4 waves of 64 x 64, three per SIMD): twice the work-groups of the former, for
-//     the narrower linears (o and down) whose 128 x 256 grid would leave CUs idle;
-//   * 128 x 128 (2 x 2 waves of 64 x 64) when N is not a multiple of 256.
+// order, so the choice changes the speed only, never a bit of the result. For N a multiple of
+// 256 the tile is a row of 4 waves of R x 64 (R = 128, 96 or 64): the larger R, the less
+// dequantisation and fewer loads per MFMA (measured relative rates 1 : 0.93 : 0.85), the
+// coarser the grid. The choice minimises the rows the busiest CU works through over that rate,
+// ceil(work-groups / CUs) R / rate: 128 rows for the qkv and gate||up linears of a long chunk,
+// 96 for o and down, 64 for short chunks. Otherwise 128 x 128 (2 x 2 waves of 64 x 64).
 template <bool SILU>
 static int launch_gemm(const char* name, const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                        float* out, uint16_t* h, uint32_t T, uint32_t K, uint32_t N, void* stream) {
@@ -569,15 +568,27 @@ static int launch_gemm(const char* name, const uint32_t* qweight, const uint16_t
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return mi_hip((int)hipGetLastError(), name);
-  const uint32_t rb = (T + 127u) / 128u;
   hipStream_t st = (hipStream_t)stream;
-  if (N % 256u == 0 && (uint64_t)(N / 256u) * rb * 8u >= 7ull * 2u * (uint64_t)cus)
-    gemm_w4a16_kernel<SILU, 1, 8, 2><<<dim3(N / 256u, rb), 256, 0, st>>>(qweight, scales, x, out, h, T, K, N);
-  else if (N % 256u == 0)
-    gemm_w4a16_kernel<SILU, 1, 4, 1><<<dim3(N / 256u, (T + 63u) / 64u), 256, 0, st>>>(qweight, scales, x, out, h,
-                                                                                        T, K, N);
-  else
-    gemm_w4a16_kernel<SILU, 2, 4, 1><<<dim3(N / 128u, rb), 256, 0, st>>>(qweight, scales, x, out, h, T, K, N);
+  if (N % 256u == 0) {
+    const uint64_t C = (uint64_t)(cus > 0 ? cus : 1);
+    auto cost = [&](uint32_t R, uint64_t rate) {  // rows on the busiest CU x 100 / rate (percent)
+      const uint64_t wg = (uint64_t)(N / 256u) * ((T + R - 1u) / R);
+      return (wg + C - 1u) / C * R * 10000u / rate;
+    };
+    const uint64_t c128 = cost(128u, 100u), c96 = cost(96u, 93u), c64 = cost(64u, 85u);
+    if (c128 <= c96 && c128 <= c64)
+      gemm_w4a16_kernel<SILU, 1, 8, 2><<<dim3(N / 256u, (T + 127u) / 128u), 256, 0, st>>>(qweight, scales, x, out,
+                                                                                          h, T, K, N);
+    else if (c96 <= c64)
+      gemm_w4a16_kernel<SILU, 1, 6, 2><<<dim3(N / 256u, (T + 95u) / 96u), 256, 0, st>>>(qweight, scales, x, out, h,
+                                                                                         T, K, N);
+    else
+      gemm_w4a16_kernel<SILU, 1, 4, 1><<<dim3(N / 256u, (T + 63u) / 64u), 256, 0, st>>>(qweight, scales, x, out, h,
+                                                                                         T, K, N);
+  } else {
+    gemm_w4a16_kernel<SILU, 2, 4, 1><<<dim3(N / 128u, (T + 127u) / 128u), 256, 0, st>>>(qweight, scales, x, out, h,
+                                                                                         T, K, N);
+  }
   return mi_hip((int)hipGetLastError(), name);
 }
 

@@ -43,10 +43,11 @@ def dequant16(qw, sc):
     return ((q.astype(np.float32) - 8) * s).astype(np.float16).astype(np.float64)
 
 
-# the shapes take all three work-group tiles (N % 256 != 0: 128 x 128; a small grid: 64 x 256;
-# at least 448 tiles of 128 x 256 on a 256-CU part: 128 x 256), with ragged T and odd group counts
+# the shapes take all four work-group tiles on a 256-CU part (N % 256 != 0: 128 x 128; small
+# grids: 64 x 256; T = 2000, N = 5120: 96 x 256; T = 1000, N = 14336: 128 x 256), with ragged T
+# and odd group counts
 @pytest.mark.parametrize("T,K,N", [(1, 256, 128), (3, 64, 256), (9, 320, 384), (37, 1024, 384), (130, 2048, 256),
-                                   (256, 5120, 512), (1000, 192, 14336)])
+                                   (256, 5120, 512), (1000, 192, 14336), (2000, 64, 5120)])
 def test_gemm_vs_fp64(T, K, N):
     qw, sc = weights(K, N, T + K)
     x = O.f32_to_f16_bits(np.random.default_rng(T).standard_normal((T, K)).astype(np.float32))
@@ -63,7 +64,7 @@ def test_gemm_vs_fp64(T, K, N):
     assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) / bound)
 
 
-@pytest.mark.parametrize("T,K,N", [(70, 512, 256), (70, 512, 384), (1000, 128, 14336)])
+@pytest.mark.parametrize("T,K,N", [(70, 512, 256), (70, 512, 384), (1000, 128, 14336), (2000, 64, 5120)])
 def test_gemm_exact_arithmetic(T, K, N):
     """Small-integer activations and scale 1/16: every product and partial sum is exact in fp32,
     so the GEMM equals the fp64 product bit for bit (any misplaced nibble, row or column shows)."""
@@ -77,7 +78,7 @@ def test_gemm_exact_arithmetic(T, K, N):
     assert np.array_equal(host(out, np.float32).astype(np.float64), want)
 
 
-@pytest.mark.parametrize("T,K,I", [(77, 1024, 640), (70, 512, 576), (1000, 128, 7168)])
+@pytest.mark.parametrize("T,K,I", [(77, 1024, 640), (70, 512, 576), (1000, 128, 7168), (2000, 64, 2560)])
 def test_gemm_silu_is_gemm_then_silu_mul(T, K, I):
     """mi_gemm_w4a16_silu: SwiGLU in the GEMM's epilogue, bitwise mi_gemm_w4a16 followed by
     mi_silu_mul (the interleave16 gate||up columns), on each work-group tile."""
