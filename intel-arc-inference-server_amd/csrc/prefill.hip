@@ -30,7 +30,8 @@
 // attn_prefill_kernel: causal GQA attention of T query rows at positions pos0 .. pos0+T-1 over
 // the fp16 cache rows [0, pos0 + t] (the chunk's own rows written by attn_prep before it). A
 // work-group takes one kv head and 64 / GQA rows; its 4 waves each own 16 (row, q head) columns
-// of the MFMA and walk the same keys, 64 per iteration staged once in LDS for all of them.
+// of the MFMA and walk the same keys, 64 per iteration staged once in LDS for all of them (K as
+// rows, V transposed so that the P.V operand of 4 keys of one dimension is one 8-byte read).
 // Per 16-key group the decode kernel's per-wave flash step (csrc/attn.hip): S^T = K Q^T with q
 // as f16 high + low parts, the online softmax per column in fp32, O^T += V^T P^T with P as f16
 // high + low parts, so the result is fp32-accurate attention; keys past a row's position are
@@ -236,9 +237,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   constexpr uint32_t RB = 64 / GQA;          // rows per work-group
   constexpr uint32_t KB = 64;                // keys per iteration
   constexpr uint32_t KROW = HD + 8;          // padded K row in LDS (f16)
-  constexpr uint32_t ROWB = HD * 2, CW = 32; // V row bytes, bytes of one 16-dim column
+  constexpr uint32_t ROWB = HD * 2;          // K row bytes
+  constexpr uint32_t VTP = KB + 4;           // V^T row (one dimension over the 64 keys), padded
+  constexpr uint32_t DPT = HD / 8;           // dimensions per staging thread of a key pair
   __shared__ __align__(16) uint16_t sK[KB * KROW];
-  __shared__ __align__(16) unsigned char sV[KB * ROWB];
+  __shared__ __align__(16) uint16_t sVt[HD * VTP];
   __shared__ float sKs[KV8 ? KB : 1], sVs[KV8 ? KB : 1];
   const uint32_t j = blockIdx.x, t0 = blockIdx.y * RB;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
@@ -277,46 +280,74 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   f4_t acc[NT];
 #pragma unroll
   for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] = f4_t{0.f, 0.f, 0.f, 0.f};
-  // V rows staged with the decode kernel's swizzle per 16-row group: the four row groups one
-  // A-operand read touches land on distinct banks
-  auto sv_off = [](uint32_t r, uint32_t c) -> uint32_t {
-    return (r >> 4) * 16u * ROWB + (r & 15u) * ROWB + ((c ^ ((r >> 2) & 3u)) * CW);
-  };
   const size_t hoff = (size_t)j * a.head_stride;
-  // staging: thread t loads key row t >> 2, quarter t & 3 of its K and V rows (f16 bytes in LDS)
+  // staging: thread t loads key row t >> 2, quarter t & 3 of its K row (f16 bytes in LDS), and
+  // dimensions DPT (t & 7) .. + DPT - 1 of the key pair 2 (t >> 3), 2 (t >> 3) + 1 of V, which it
+  // writes transposed (V^T[dimension][key], a u32 per dimension holding both keys) so that the
+  // A operand of the P.V product (4 consecutive keys of one dimension) is one 8-byte read
   constexpr uint32_t QB = ROWB / 4u;  // f16 bytes per quarter row
   const uint32_t srow = t >> 2, squart = t & 3u;
+  const uint32_t vpair = t >> 3, vd0 = DPT * (t & 7u);
+  auto cache_row = [&](uint32_t key) -> size_t {
+    return a.pages ? (size_t)a.pages[key / a.page] * a.page + key % a.page : (size_t)key;
+  };
   for (uint32_t kb = 0; kb < kend; kb += KB) {
     {
       const uint32_t key = kb + srow;
       const bool live = key < kend;
-      const size_t crow = live ? (a.pages ? (size_t)a.pages[key / a.page] * a.page + key % a.page : (size_t)key) : 0;
+      const size_t crow = live ? cache_row(key) : 0;
+      const uint32_t vk0 = kb + 2u * vpair;
+      const bool vlive0 = vk0 < kend, vlive1 = vk0 + 1u < kend;
+      const size_t vrow0 = vlive0 ? cache_row(vk0) : 0, vrow1 = vlive1 ? cache_row(vk0 + 1u) : 0;
+      uint16_t vt0[DPT], vt1[DPT];  // dimensions vd0 .. of the pair's two keys (f16 bits)
       if constexpr (KV8 == 0) {
         const unsigned char* kp =
             static_cast<const unsigned char*>(a.kv_k) + (crow * a.row_stride + hoff) * 2u + squart * QB;
-        const unsigned char* vp =
-            static_cast<const unsigned char*>(a.kv_v) + (crow * a.row_stride + hoff) * 2u + squart * QB;
 #pragma unroll
         for (uint32_t i = 0; i < QB / 16u; ++i) {
           const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-          const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-          const uint32_t byte = squart * QB + 16u * i;
-          *reinterpret_cast<u4_t*>(reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte) = kv;
-          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = vv;
+          *reinterpret_cast<u4_t*>(reinterpret_cast<unsigned char*>(sK + srow * KROW) + squart * QB + 16u * i) = kv;
+        }
+        const uint16_t* v0 = static_cast<const uint16_t*>(a.kv_v) + vrow0 * a.row_stride + hoff + vd0;
+        const uint16_t* v1 = static_cast<const uint16_t*>(a.kv_v) + vrow1 * a.row_stride + hoff + vd0;
+#pragma unroll
+        for (uint32_t i = 0; i < DPT / 8u; ++i) {
+          const u4_t x0 = vlive0 ? *reinterpret_cast<const u4_t*>(v0 + 8u * i) : u4_t{0u, 0u, 0u, 0u};
+          const u4_t x1 = vlive1 ? *reinterpret_cast<const u4_t*>(v1 + 8u * i) : u4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (uint32_t e = 0; e < 4; ++e) {
+            vt0[8u * i + 2u * e] = (uint16_t)(x0[e] & 0xFFFFu);
+            vt0[8u * i + 2u * e + 1u] = (uint16_t)(x0[e] >> 16);
+            vt1[8u * i + 2u * e] = (uint16_t)(x1[e] & 0xFFFFu);
+            vt1[8u * i + 2u * e + 1u] = (uint16_t)(x1[e] >> 16);
+          }
         }
       } else {
         const unsigned char* kp = static_cast<const unsigned char*>(a.kv_k) + crow * a.row_stride + hoff + squart * (QB / 2u);
-        const unsigned char* vp = static_cast<const unsigned char*>(a.kv_v) + crow * a.row_stride + hoff + squart * (QB / 2u);
 #pragma unroll
         for (uint32_t i = 0; i < QB / 32u; ++i) {  // 16 int8 -> 32 bytes of f16
           const u4_t kv = live ? *reinterpret_cast<const u4_t*>(kp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-          const u4_t vv = live ? *reinterpret_cast<const u4_t*>(vp + 16u * i) : u4_t{0u, 0u, 0u, 0u};
-          const uint32_t byte = squart * QB + 32u * i;
-          unsigned char* kd = reinterpret_cast<unsigned char*>(sK + srow * KROW) + byte;
+          unsigned char* kd = reinterpret_cast<unsigned char*>(sK + srow * KROW) + squart * QB + 32u * i;
           *reinterpret_cast<u4_t*>(kd) = widen_i8x8(kv.x, kv.y);
           *reinterpret_cast<u4_t*>(kd + 16) = widen_i8x8(kv.z, kv.w);
-          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW) = widen_i8x8(vv.x, vv.y);
-          *reinterpret_cast<u4_t*>(sV + sv_off(srow, byte / CW) + byte % CW + 16) = widen_i8x8(vv.z, vv.w);
+        }
+        const unsigned char* v0 = static_cast<const unsigned char*>(a.kv_v) + vrow0 * a.row_stride + hoff + vd0;
+        const unsigned char* v1 = static_cast<const unsigned char*>(a.kv_v) + vrow1 * a.row_stride + hoff + vd0;
+#pragma unroll
+        for (uint32_t i = 0; i < DPT / 16u; ++i) {  // 16 int8 per load
+          const u4_t x0 = vlive0 ? *reinterpret_cast<const u4_t*>(v0 + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const u4_t x1 = vlive1 ? *reinterpret_cast<const u4_t*>(v1 + 16u * i) : u4_t{0u, 0u, 0u, 0u};
+          const u4_t w0[2] = {widen_i8x8(x0.x, x0.y), widen_i8x8(x0.z, x0.w)};
+          const u4_t w1[2] = {widen_i8x8(x1.x, x1.y), widen_i8x8(x1.z, x1.w)};
+#pragma unroll
+          for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e) {
+              vt0[16u * i + 8u * h + 2u * e] = (uint16_t)(w0[h][e] & 0xFFFFu);
+              vt0[16u * i + 8u * h + 2u * e + 1u] = (uint16_t)(w0[h][e] >> 16);
+              vt1[16u * i + 8u * h + 2u * e] = (uint16_t)(w1[h][e] & 0xFFFFu);
+              vt1[16u * i + 8u * h + 2u * e + 1u] = (uint16_t)(w1[h][e] >> 16);
+            }
         }
         if (squart == 0) {
           const size_t so = crow * a.sc_row_stride + (size_t)j * a.sc_head_stride;
@@ -324,6 +355,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
           sVs[srow] = live ? h2f(a.v_scale[so]) : 0.f;
         }
       }
+#pragma unroll
+      for (uint32_t d = 0; d < DPT; ++d)
+        *reinterpret_cast<uint32_t*>(sVt + (vd0 + d) * VTP + 2u * vpair) = (uint32_t)vt0[d] | ((uint32_t)vt1[d] << 16);
     }
     lds_barrier();
 #pragma unroll
@@ -372,10 +406,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
       }
 #pragma unroll
       for (uint32_t tt = 0; tt < NT; ++tt) {
-        h4_t av;
-#pragma unroll
-        for (uint32_t jj = 0; jj < 4; ++jj)
-          av[jj] = *reinterpret_cast<const half_t*>(sV + sv_off(16u * grp + 4u * qq + jj, tt) + 2u * qi);
+        const h4_t av = *reinterpret_cast<const h4_t*>(sVt + (16u * tt + qi) * VTP + 16u * grp + 4u * qq);
         acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, acc[tt], 0, 0, 0);
         acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, acc[tt], 0, 0, 0);
       }
