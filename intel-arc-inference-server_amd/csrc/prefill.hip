@@ -243,7 +243,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   __shared__ __align__(16) uint16_t sK[KB * KROW];
   __shared__ __align__(16) uint16_t sVt[HD * VTP];
   __shared__ float sKs[KV8 ? KB : 1], sVs[KV8 ? KB : 1];
-  const uint32_t j = blockIdx.x, t0 = blockIdx.y * RB;
+  // the last row blocks see the most keys: they are dispatched first, so the short blocks fill
+  // the tail of the grid
+  const uint32_t j = blockIdx.x, t0 = (gridDim.y - 1u - blockIdx.y) * RB;
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t qi = lane & 15u, qq = lane >> 4;
   // this lane's column: pair p = 16 wave + qi -> row t0 + p / GQA, q head j GQA + p % GQA
