@@ -81,6 +81,7 @@ SIGNATURES = {
     "mi_gemm_w4a16_silu": (i32, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "mi_attn_prefill": (i32, [vp, vp, vp, sz, sz, vp, u32, u32, u32, vp, vp, vp]),
     "mi_embed_rows": (i32, [vp, vp, vp, u32, u32, u32, vp, vp]),
+    "mi_moe_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp]),
     "mi_attn_prep_rows": (i32, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, vp]),
     "mi_attn_prefill_kv8": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, u32, vp, vp, vp, vp]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),

@@ -193,6 +193,214 @@ __global__ __launch_bounds__(256, LB) void gemm_w4a16_kernel(const uint32_t* __r
 }
 
 // ---------------------------------------------------------------------------------------------
+// the chunk's MoE block, grouped by expert
+// ---------------------------------------------------------------------------------------------
+// The decode kernels take one row at a time through every expert it routes to, which for a
+// chunk reads each expert's weights once per routed row. Here the chunk's (row, slot) pairs are
+// grouped by expert first (moe_group_kernel), so each expert's weights stream once per 64 of
+// its pairs through the MFMA tile of gemm_w4a16_kernel (moe_gemm_kernel: layout-1 weights,
+// gathered activation rows, scattered outputs), and the slot-ordered combine with the residual
+// (moe.cl:383-470's epilogue, moe_ref.h:144-152) runs per row afterwards.
+constexpr uint32_t kMoeRouteWords = 32, kMoeW = 8, kMoeSG = 16;  // the route row (moe.cl:49-56)
+constexpr uint32_t kMoeTile = 136;                                 // layout 1: 128 words + 16 f16 scales
+constexpr uint32_t kMoeRows = 64;                                  // pairs per row tile
+constexpr uint32_t kMoeMaxPairs = 2048u * 9u;                      // T <= 2048, top_k <= 8
+
+// the expert of slot s of a route row: the shared expert (index E) for s = top_k, and for an
+// id outside [0, E) (moe.hip's slot_expert)
+__device__ __forceinline__ uint32_t moe_slot_expert(const uint32_t* row, uint32_t s, uint32_t E, uint32_t top_k) {
+  if (s >= top_k) return E;
+  const uint32_t id = row[s];
+  return id < E ? id : E;
+}
+
+// One work-group. pairs p = t (top_k + 1) + s of T rows; expert e's pairs in ascending p go to
+// list[off_e ..], and its row tiles to tiles[] as {e, first list index, pair count}; the
+// tile count to tiles_n[0].
+__global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restrict__ route, uint32_t T,
+                                                        uint32_t E, uint32_t top_k, uint32_t* __restrict__ list,
+                                                        u4_t* __restrict__ tiles, uint32_t* __restrict__ tiles_n) {
+  __shared__ uint16_t s_ex[kMoeMaxPairs];
+  __shared__ uint32_t s_cnt[257], s_off[257], s_toff[257];
+  const uint32_t t = threadIdx.x, slots = top_k + 1, P = T * slots;
+  for (uint32_t p = t; p < P; p += 256u)
+    s_ex[p] = (uint16_t)moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
+  __syncthreads();
+  for (uint32_t e = t; e <= E; e += 256u) {
+    uint32_t c = 0;
+    for (uint32_t p = 0; p < P; ++p) c += s_ex[p] == e ? 1u : 0u;
+    s_cnt[e] = c;
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t o = 0, to = 0;
+    for (uint32_t e = 0; e <= E; ++e) {
+      s_off[e] = o;
+      s_toff[e] = to;
+      o += s_cnt[e];
+      to += (s_cnt[e] + kMoeRows - 1u) / kMoeRows;
+    }
+    tiles_n[0] = to;
+  }
+  __syncthreads();
+  for (uint32_t e = t; e <= E; e += 256u) {
+    uint32_t i = s_off[e];
+    for (uint32_t p = 0; p < P; ++p)
+      if (s_ex[p] == e) list[i++] = p;
+    const uint32_t n = s_cnt[e];
+    for (uint32_t k = 0; k * kMoeRows < n; ++k)
+      tiles[s_toff[e] + k] = u4_t{e, s_off[e] + k * kMoeRows, min(kMoeRows, n - k * kMoeRows), 0u};
+  }
+}
+
+// out rows = pairs of one expert (a row tile) x that expert's layout-1 block (K x N, columns in
+// 16-column tiles of 64-k groups: word j of the group's tile holds k 8 j .. 8 j + 7 of column c
+// at j 16 + c, its f16 scale at half-word 256 + c). A row of a pair p is row p / slots of x
+// (GATE_UP) or row p of h (down). GATE_UP: N = 2 inter in interleave16 order, SwiGLU in the
+// epilogue into h[p][inter] (the dense GEMM's epilogue); down: d[p][N] fp32. Tile: 64 pairs x
+// 256 columns, 4 waves of 64 x 64, the dense GEMM's k loop.
+template <bool GATE_UP>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(const u4_t* __restrict__ tiles,
+                                                       const uint32_t* __restrict__ tiles_n,
+                                                       const uint32_t* __restrict__ list,
+                                                       const uint32_t* __restrict__ blocks, size_t block_u32,
+                                                       const uint16_t* __restrict__ a, uint32_t a_rows,
+                                                       uint16_t* __restrict__ h_out, float* __restrict__ d_out,
+                                                       uint32_t slots, uint32_t K, uint32_t N) {
+  __shared__ __align__(16) uint16_t As[2][kMoeRows][GROW];
+  if (blockIdx.y >= tiles_n[0]) return;  // uniform: the grid is sized for the most tiles
+  const u4_t tile = tiles[blockIdx.y];
+  const uint32_t e = tile.x, first = tile.y, cnt = tile.z;
+  const uint32_t t = threadIdx.x, lane = t & 63u, wn = t >> 6;
+  const uint32_t n0 = blockIdx.x * 256u, G = K / GBK;
+  const uint32_t fr = lane & 15u, fq = lane >> 4;
+
+  // activations: thread t stages pairs (t >> 3) + 32 i (i < 2), 8-k chunk t & 7; a pair past
+  // the tile's count gets an offset outside the resource and reads zeros
+  const uint32_t a_row = t >> 3, a_chunk = t & 7u;
+  const __amdgpu_buffer_rsrc_t x_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a), 0, a_rows * K * 2u, 0x00020000);
+  uint32_t a_voff[2];
+#pragma unroll
+  for (uint32_t i = 0; i < 2; ++i) {
+    const uint32_t r = a_row + 32u * i;
+    const uint32_t p = r < cnt ? list[first + r] : 0u;
+    const uint32_t src = GATE_UP ? p / slots : p;
+    a_voff[i] = r < cnt ? (src * K + 8u * a_chunk) * 2u : 0x80000000u;
+  }
+  u4_t a_st[2];
+  auto load_a = [&](uint32_t g) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i)
+      a_st[i] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rs, a_voff[i], g * GBK * 2u, 0));
+  };
+  auto store_a = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i)
+      *reinterpret_cast<u4_t*>(&As[buf][a_row + 32u * i][8u * a_chunk]) = perm_pairs(a_st[i]);
+  };
+  // weights: column n = n0 + 64 wn + 16 j + fr sits in 16-column tile n / 16 at column fr
+  const uint32_t* wb = blocks + (size_t)e * block_u32;
+  const __amdgpu_buffer_rsrc_t w_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(wb), 0, (uint32_t)(block_u32 * 4u), 0x00020000);
+  const uint32_t cb0 = (n0 + 64u * wn) / 16u;
+  uint32_t b_w[2][4];
+  uint32_t b_s[4];
+  auto load_b = [&](uint32_t g) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t tb = ((cb0 + j) * G + g) * kMoeTile;  // u32 index of the tile
+#pragma unroll
+      for (uint32_t ks = 0; ks < 2; ++ks)
+        b_w[ks][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rs, ((4u * ks + fq) * 16u + fr) * 4u, tb * 4u, 2);
+      b_s[j] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, (256u + fr) * 2u, tb * 4u, 0);
+    }
+  };
+
+  f4_t acc[4][4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  load_a(0);
+  load_b(0);
+  store_a(0);
+  lds_barrier();
+  for (uint32_t g = 0; g < G; ++g) {
+    const uint32_t buf = g & 1u;
+    h8_t bf[2][4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const h2_t s2 = as_h2(b_s[j] | (b_s[j] << 16));
+#pragma unroll
+      for (uint32_t ks = 0; ks < 2; ++ks) bf[ks][j] = __builtin_bit_cast(h8_t, dequant_scaled(b_w[ks][j], s2));
+    }
+    if (g + 1 < G) {
+      load_a(g + 1);
+      load_b(g + 1);
+    }
+#pragma unroll
+    for (uint32_t ks = 0; ks < 2; ++ks) {
+      h8_t af[4];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const h8_t*>(&As[buf][16u * i + fr][32u * ks + 8u * fq]);
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[ks][j], acc[i][j], 0, 0, 0);
+    }
+    if (g + 1 < G) store_a(buf ^ 1u);
+    lds_barrier();
+  }
+  // lane holds pairs 4 (lane >> 4) + r of column lane & 15 of each 16 x 16 tile
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      const uint32_t q = 16u * i + 4u * fq + r;
+      if (q < cnt) {
+        const uint32_t p = list[first + q];
+        if constexpr (GATE_UP) {
+#pragma unroll
+          for (uint32_t jp = 0; jp < 2; ++jp) {
+            const uint16_t g_b = f2h(acc[i][2 * jp][r]), u_b = f2h(acc[i][2 * jp + 1][r]);
+            const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
+            h_out[(size_t)p * (N / 2) + (n0 + 64u * wn) / 2 + 16u * jp + fr] = f2h(h2f(s_b) * h2f(u_b));
+          }
+        } else {
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j) d_out[(size_t)p * N + n0 + 64u * wn + 16u * j + fr] = acc[i][j][r];
+        }
+      }
+    }
+}
+
+// resid[t][n] += the slot-ordered combine of row t's pair outputs (moe_down_kernel's epilogue,
+// moe_ref.h:144-152): sum_k rne(rne(d_k) w_k) in slot order, + rne(rne(d_shared) s)
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint32_t* __restrict__ route,
+                                                          const float* __restrict__ d, uint16_t* __restrict__ resid,
+                                                          uint32_t top_k, uint32_t hidden) {
+  const uint32_t t = blockIdx.y, n = blockIdx.x * 256u + threadIdx.x;
+  if (n >= hidden) return;
+  const uint32_t* row = route + (size_t)t * kMoeRouteWords;
+  const uint32_t slots = top_k + 1;
+  const float* dp = d + (size_t)t * slots * hidden + n;
+  float sum = 0.f;
+  for (uint32_t k = 0; k < top_k; ++k) {
+    const float wk = __builtin_bit_cast(float, row[kMoeW + k]);
+    sum += h2f(f2h(h2f(f2h(dp[(size_t)k * hidden])) * wk));
+  }
+  const uint16_t r_b = f2h(sum);
+  const float sg = __builtin_bit_cast(float, row[kMoeSG]);
+  const uint16_t sh_b = f2h(h2f(f2h(dp[(size_t)top_k * hidden])) * sg);
+  const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
+  uint16_t* rp = resid + (size_t)t * hidden + n;
+  *rp = f2h(h2f(*rp) + h2f(o_b));
+}
+
+// ---------------------------------------------------------------------------------------------
 // the chunk's causal attention
 // ---------------------------------------------------------------------------------------------
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
@@ -636,6 +844,38 @@ int mi_gemm_w4a16_silu(const uint32_t* qweight, const uint16_t* scales, const ui
                        uint32_t K, uint32_t N, void* stream) {
   if (!h) return mi_fail(MI_ERR_ARG, "gemm_w4a16_silu: bad arguments");
   return launch_gemm<true>("gemm_w4a16_silu", qweight, scales, x, nullptr, h, T, K, N, stream);
+}
+
+int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks, const uint32_t* dn_blocks,
+                   uint16_t* resid, uint32_t T, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                   uint32_t* list, uint32_t* tiles, uint32_t* tiles_n, uint16_t* h, float* d, void* stream) {
+  if (!route || !x || !gu_blocks || !dn_blocks || !resid || !list || !tiles || !tiles_n || !h || !d)
+    return mi_fail(MI_ERR_ARG, "moe_prefill: null pointer");
+  if (T == 0 || T > 2048u) return mi_fail(MI_ERR_SHAPE, "moe_prefill: T must be 1..2048");
+  if (experts < 16 || experts > 256 || (experts & (experts - 1)))
+    return mi_fail(MI_ERR_SHAPE, "moe_prefill: experts must be a power of two in [16, 256]");
+  if (top_k < 1 || top_k > 8) return mi_fail(MI_ERR_SHAPE, "moe_prefill: top_k must be 1..8");
+  if (hidden == 0 || hidden % 512 || hidden > 4096)
+    return mi_fail(MI_ERR_SHAPE, "moe_prefill: hidden must be a multiple of 512 up to 4096");
+  if (inter == 0 || inter % 128 || inter > 1024)
+    return mi_fail(MI_ERR_SHAPE, "moe_prefill: inter must be a multiple of 128 up to 1024");
+  if (reinterpret_cast<uintptr_t>(tiles) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(gu_blocks) % 4)
+    return mi_fail(MI_ERR_ARG, "moe_prefill: tiles, x and h need 16-byte alignment");
+  const uint32_t slots = top_k + 1, P = T * slots;
+  const uint32_t max_tiles = (P + kMoeRows - 1u) / kMoeRows + experts + 1u;
+  const size_t gu_block = (size_t)(2u * inter / 16u) * (hidden / GBK) * kMoeTile;
+  const size_t dn_block = (size_t)(hidden / 16u) * (inter / GBK) * kMoeTile;
+  hipStream_t st = (hipStream_t)stream;
+  u4_t* tl = reinterpret_cast<u4_t*>(tiles);
+  moe_group_kernel<<<1, 256, 0, st>>>(route, T, experts, top_k, list, tl, tiles_n);
+  moe_gemm_kernel<true><<<dim3(2u * inter / 256u, max_tiles), 256, 0, st>>>(tl, tiles_n, list, gu_blocks, gu_block,
+                                                                            x, T, h, nullptr, slots, hidden,
+                                                                            2u * inter);
+  moe_gemm_kernel<false><<<dim3(hidden / 256u, max_tiles), 256, 0, st>>>(tl, tiles_n, list, dn_blocks, dn_block, h,
+                                                                          P, nullptr, d, slots, inter, hidden);
+  moe_combine_kernel<<<dim3(hidden / 256u, T), 256, 0, st>>>(route, d, resid, top_k, hidden);
+  return mi_hip((int)hipGetLastError(), "moe_prefill");
 }
 
 int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v, size_t row_stride,
