@@ -279,11 +279,13 @@ int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history
 #define MI_MOE_ROUTE_WORDS 32
 /* gemv_bf16 (gemv_bf16.cl:103-200) with fp16 weights: out [M][N] fp32 = x [M][K] . w, w in
  * the tile layout [N/16][K/8][8][16] (common/repack.h:118); per column `ksplit` K slices
- * (power of two <= 16) each summed in ascending k, merged by the pairwise tree. */
+ * (power of two <= 16) each summed in ascending k, merged by the pairwise tree. M up to 65535
+ * (one work-group per row and 16 columns). */
 int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* out, uint32_t M, uint32_t K,
                  uint32_t N, uint32_t ksplit, void* stream);
 /* moe_route (moe.cl:192-262): logits [M][router_n] (experts router rows, then the shared
- * gate's row) -> route [M][MI_MOE_ROUTE_WORDS]. experts: power of two in [16, 256]. */
+ * gate's row) -> route [M][MI_MOE_ROUTE_WORDS]. experts: power of two in [16, 256]; M up to
+ * 65535 (rows are independent). */
 int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts,
                  uint32_t top_k, uint32_t router_n, void* stream);
 /* moe_gate_up (moe.cl:335-381): h [M][top_k + 1][inter] fp16 = rne(silu(g)) * u of each slot's

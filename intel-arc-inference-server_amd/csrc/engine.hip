@@ -420,6 +420,7 @@ struct mi_engine {
   uint16_t* pf_h = nullptr;      // [cap][inter]
   uint16_t* pf_attn = nullptr;   // [cap][q_heads * head_dim]
   // MoE chunks: route rows, the grouped pairs' list and row tiles, and the pair outputs
+  float* pf_logits = nullptr;    // [cap][router_n]
   uint32_t* pf_route = nullptr;  // [cap][MI_MOE_ROUTE_WORDS]
   uint32_t* pf_list = nullptr;   // [cap (top_k + 1)]
   uint32_t* pf_tiles = nullptr;  // [(cap (top_k + 1) + 63) / 64 + experts + 1][4]
@@ -445,6 +446,7 @@ struct mi_engine {
     MI_TRY(alloc(&pf_attn, size_t(cap) * QHD));
     if (d.experts) {
       const size_t pairs = size_t(cap) * (d.top_k + 1);
+      MI_TRY(alloc(&pf_logits, size_t(cap) * router_n));
       MI_TRY(alloc(&pf_route, size_t(cap) * MI_MOE_ROUTE_WORDS));
       MI_TRY(alloc(&pf_list, pairs));
       MI_TRY(alloc(&pf_tiles, ((pairs + 63) / 64 + d.experts + 1) * 4));
@@ -488,16 +490,10 @@ struct mi_engine {
       MI_TRY(mi_res_norm(pf_out, pf_resid, L.post_norm, pf_x, T, H, 1, d.rms_eps, stream));
       const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
       if (d.experts) {
-        // the MoE block (moe.cl:1-13): router || shared gate and route over the chunk's rows in
-        // slices of the decode kernels' row capacity, then the expert FFN grouped by expert
-        const uint32_t slice = std::min(16u, d.max_rows);
-        for (uint32_t r0 = 0; r0 < T; r0 += slice) {
-          const uint32_t m = std::min(slice, T - r0);
-          const uint16_t* xs = pf_x + size_t(r0) * H;
-          MI_TRY(mi_gemv_f16w(L.router, xs, moe_logits, m, H, router_n, router_ksplit(), stream));
-          MI_TRY(mi_moe_route(moe_logits, pf_route + size_t(r0) * MI_MOE_ROUTE_WORDS, m, d.experts, d.top_k,
-                              router_n, stream));
-        }
+        // the MoE block (moe.cl:1-13): router || shared gate and the route of every row of the
+        // chunk in one launch each, then the expert FFN grouped by expert
+        MI_TRY(mi_gemv_f16w(L.router, pf_x, pf_logits, T, H, router_n, router_ksplit(), stream));
+        MI_TRY(mi_moe_route(pf_logits, pf_route, T, d.experts, d.top_k, router_n, stream));
         MI_TRY(mi_moe_prefill(pf_route, pf_x, L.moe_gu, L.moe_dn, pf_resid, T, d.experts, d.top_k, H, d.moe_inter,
                               pf_list, pf_tiles, pf_tiles_n, pf_mh, pf_md, stream));
         MI_TRY(mi_res_norm(nullptr, pf_resid, next_w, pf_x, T, H, 0, d.rms_eps, stream));

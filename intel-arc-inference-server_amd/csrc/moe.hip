@@ -283,8 +283,9 @@ using namespace mi;
 extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* out, uint32_t M, uint32_t K,
                             uint32_t N, uint32_t ksplit, void* stream) {
   if (!w_tiled || !x || !out) return mi_fail(MI_ERR_ARG, "gemv_f16w: null pointer");
-  if (M == 0 || M > 16 || K == 0 || N == 0 || N % 16 || K % 64)
-    return mi_fail(MI_ERR_SHAPE, "gemv_f16w: M 1..16, K a multiple of 64, N a multiple of 16");
+  // one work-group per (16 columns, row), rows independent: any M up to the grid's 65535 rows
+  if (M == 0 || M > 65535u || K == 0 || N == 0 || N % 16 || K % 64)
+    return mi_fail(MI_ERR_SHAPE, "gemv_f16w: M 1..65535, K a multiple of 64, N a multiple of 16");
   if (ksplit == 0 || ksplit > 16 || (ksplit & (ksplit - 1)) || (K / 8) % ksplit)
     return mi_fail(MI_ERR_SHAPE, "gemv_f16w: ksplit must be a power of two <= 16 dividing K/8");
   if (reinterpret_cast<uintptr_t>(x) % 16) return mi_fail(MI_ERR_ARG, "gemv_f16w: x needs 16-byte alignment");
@@ -296,7 +297,9 @@ extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* o
 extern "C" int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts, uint32_t top_k,
                             uint32_t router_n, void* stream) {
   if (!logits || !route) return mi_fail(MI_ERR_ARG, "moe_route: null pointer");
-  if (int e = check_moe(M, experts, top_k, 512, 128)) return e;
+  // one work-group per row, rows independent: any M (a prefill chunk routes all its rows at once)
+  if (M == 0 || M > 65535u) return mi_fail(MI_ERR_SHAPE, "moe_route: M must be 1..65535");
+  if (int e = check_moe(1, experts, top_k, 512, 128)) return e;
   if (router_n < experts + 1) return mi_fail(MI_ERR_SHAPE, "moe_route: router_n must hold experts + 1 rows");
   moe_route_kernel<<<M, experts, 0, static_cast<hipStream_t>(stream)>>>(logits, route, experts, top_k, router_n);
   return mi_hip(static_cast<int>(hipGetLastError()), "moe_route launch");

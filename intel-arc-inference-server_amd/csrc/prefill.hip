@@ -214,22 +214,23 @@ __device__ __forceinline__ uint32_t moe_slot_expert(const uint32_t* row, uint32_
   return id < E ? id : E;
 }
 
-// One work-group. pairs p = t (top_k + 1) + s of T rows; expert e's pairs in ascending p go to
-// list[off_e ..], and its row tiles to tiles[] as {e, first list index, pair count}; the
-// tile count to tiles_n[0].
+// One work-group, a counting sort of the pairs p = t (top_k + 1) + s of T rows by expert: expert
+// e's pairs go to list[off_e ..], its row tiles to tiles[] as {e, first list index, pair count},
+// the tile count to tiles_n[0]. The order of the pairs within an expert comes from LDS atomics
+// and may differ between calls; it changes no result (an output row of the GEMM depends on its
+// own activation row only).
 __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restrict__ route, uint32_t T,
                                                         uint32_t E, uint32_t top_k, uint32_t* __restrict__ list,
                                                         u4_t* __restrict__ tiles, uint32_t* __restrict__ tiles_n) {
   __shared__ uint16_t s_ex[kMoeMaxPairs];
-  __shared__ uint32_t s_cnt[257], s_off[257], s_toff[257];
+  __shared__ uint32_t s_cnt[257], s_off[257], s_toff[257], s_cur[257];
   const uint32_t t = threadIdx.x, slots = top_k + 1, P = T * slots;
-  for (uint32_t p = t; p < P; p += 256u)
-    s_ex[p] = (uint16_t)moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
+  for (uint32_t e = t; e <= E; e += 256u) s_cnt[e] = s_cur[e] = 0;
   __syncthreads();
-  for (uint32_t e = t; e <= E; e += 256u) {
-    uint32_t c = 0;
-    for (uint32_t p = 0; p < P; ++p) c += s_ex[p] == e ? 1u : 0u;
-    s_cnt[e] = c;
+  for (uint32_t p = t; p < P; p += 256u) {
+    const uint32_t e = moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
+    s_ex[p] = (uint16_t)e;
+    atomicAdd(&s_cnt[e], 1u);
   }
   __syncthreads();
   if (t == 0) {
@@ -243,10 +244,11 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
     tiles_n[0] = to;
   }
   __syncthreads();
+  for (uint32_t p = t; p < P; p += 256u) {
+    const uint32_t e = s_ex[p];
+    list[s_off[e] + atomicAdd(&s_cur[e], 1u)] = p;
+  }
   for (uint32_t e = t; e <= E; e += 256u) {
-    uint32_t i = s_off[e];
-    for (uint32_t p = 0; p < P; ++p)
-      if (s_ex[p] == e) list[i++] = p;
     const uint32_t n = s_cnt[e];
     for (uint32_t k = 0; k * kMoeRows < n; ++k)
       tiles[s_toff[e] + k] = u4_t{e, s_off[e] + k * kMoeRows, min(kMoeRows, n - k * kMoeRows), 0u};
