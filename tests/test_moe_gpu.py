@@ -195,3 +195,73 @@ def test_malformed_route_row_reads_the_shared_block():
     # every slot computed the shared expert's block
     for slot in range(mo.top_k):
         assert np.array_equal(hh[0, slot], hh[0, mo.top_k])
+
+
+@pytest.mark.parametrize("T,bad", [(1, False), (37, True), (300, False)])
+def test_moe_prefill_matches_decode_kernels(T, bad):
+    """mi_moe_prefill (the chunk's expert FFN grouped by expert on the MFMA tile) against the
+    decode kernels (mi_moe_gate_up + mi_moe_down) on the same route rows: within 2 % of the
+    largest output (the prefill rounds each dequantised weight to fp16, the decode kernels
+    multiply exact integers and scale per group). The router GEMV and the route over all T rows
+    in one launch are bitwise the 16-row launches. bad: some route ids outside [0, E), which
+    both paths send to the shared expert."""
+    mo = Moe(11)
+    E, K, H, I = mo.E, mo.top_k, mo.hidden, mo.inter
+    rng = np.random.default_rng(T)
+    x = O.f32_to_f16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    dx = dev(x)
+    logits = empty((T, mo.router_n), np.float32)
+    route = empty((T, ROUTE_WORDS), np.uint32)
+    print(f"moe_prefill T={T}", flush=True)
+    mi.call("mi_gemv_f16w", ptr(mo.d_router), ptr(dx), ptr(logits), T, H, mo.router_n, 16, stream())
+    mi.call("mi_moe_route", ptr(logits), ptr(route), T, E, K, mo.router_n, stream())
+    sync()
+    lg_all, rt_all = host(logits, np.float32).reshape(T, -1), host(route, np.uint32).reshape(T, -1)
+    for r0 in range(0, T, 16):
+        m = min(16, T - r0)
+        ls, rs = empty((m, mo.router_n), np.float32), empty((m, ROUTE_WORDS), np.uint32)
+        xs = dev(x[r0:r0 + m])
+        mi.call("mi_gemv_f16w", ptr(mo.d_router), ptr(xs), ptr(ls), m, H, mo.router_n, 16, stream())
+        mi.call("mi_moe_route", ptr(ls), ptr(rs), m, E, K, mo.router_n, stream())
+        sync()
+        assert np.array_equal(host(ls, np.float32).reshape(m, -1), lg_all[r0:r0 + m])
+        assert np.array_equal(host(rs, np.uint32).reshape(m, -1), rt_all[r0:r0 + m])
+    if bad:
+        rt_all[::5, 2] = E + 5
+        rt_all[3, 0] = 0xFFFFFFFF
+    droute = dev(np.ascontiguousarray(rt_all))
+    # the decode kernels, 16 rows at a time
+    want = np.zeros((T, H), np.uint16)
+    for r0 in range(0, T, 16):
+        m = min(16, T - r0)
+        h = empty((m, K + 1, I), np.uint16)
+        res = dev(np.zeros((m, H), np.uint16))
+        rs = dev(np.ascontiguousarray(rt_all[r0:r0 + m]))
+        xs = dev(x[r0:r0 + m])
+        mi.call("mi_moe_gate_up", ptr(rs), ptr(xs), ptr(mo.d_gu), ptr(h), m, E, K, H, I, stream())
+        mi.call("mi_moe_down", ptr(rs), ptr(h), ptr(mo.d_dn), ptr(res), m, E, K, H, I, stream())
+        sync()
+        want[r0:r0 + m] = host(res, np.uint16).reshape(m, H)
+    # the grouped path
+    P = T * (K + 1)
+    lst, tiles, tiles_n = empty(P, np.uint32), empty(((P + 63) // 64 + E + 1) * 4, np.uint32), empty(1, np.uint32)
+    hh, dd = empty((P, I), np.uint16), empty((P, H), np.float32)
+    resid = dev(np.zeros((T, H), np.uint16))
+    mi.call("mi_moe_prefill", ptr(droute), ptr(dx), ptr(mo.d_gu), ptr(mo.d_dn), ptr(resid), T, E, K, H, I, ptr(lst),
+            ptr(tiles), ptr(tiles_n), ptr(hh), ptr(dd), stream())
+    sync()
+    got = O.f16_bits_to_f32(host(resid, np.uint16).reshape(T, H)).astype(np.float64)
+    ref = O.f16_bits_to_f32(want).astype(np.float64)
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - ref)) <= 0.02 * np.max(np.abs(ref)), np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    # every pair listed once, grouped by expert
+    n_tiles = int(host(tiles_n, np.uint32)[0])
+    assert sorted(host(lst, np.uint32).tolist()) == list(range(P))
+    assert 1 <= n_tiles <= (P + 63) // 64 + E + 1
+
+
+def test_moe_prefill_refuses_bad_shapes():
+    with pytest.raises(mi.MiError):
+        mi.call("mi_moe_prefill", 16, 16, 16, 16, 16, 2049, 256, 8, 2048, 512, 16, 16, 16, 16, 16, None)
+    with pytest.raises(mi.MiError):
+        mi.call("mi_moe_prefill", 16, 16, 16, 16, 16, 4, 100, 8, 2048, 512, 16, 16, 16, 16, 16, None)
