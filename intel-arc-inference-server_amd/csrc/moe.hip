@@ -31,44 +31,65 @@ __device__ __forceinline__ float rf(float v) { return h2f(f2h(v)); }
 // ---- router || shared-gate GEMV (gemv_bf16.cl:103-200), fp16 weights --------------------
 // grid (N/16, M), 16 * ksplit lanes: lane l of slice q sums column n_tile*16 + l over k8 in
 // [q*per, (q+1)*per), 8 products per k8 in k order; slices merge by the pairwise tree.
+// R rows per work-group (R > 1 for a prefill chunk's rows): the weights a lane loads serve all
+// R rows, each row's sum running in the same order as with R = 1.
+template <uint32_t R>
 __global__ __launch_bounds__(256) void gemv_f16w_kernel(const uint16_t* __restrict__ w,
                                                         const uint16_t* __restrict__ x,
-                                                        float* __restrict__ out, uint32_t K,
+                                                        float* __restrict__ out, uint32_t M, uint32_t K,
                                                         uint32_t N, uint32_t ksplit) {
-  __shared__ float red[16][16];
+  __shared__ float red[R][16][16];
   const uint32_t lane = threadIdx.x & 15u, q = threadIdx.x >> 4;
-  const uint32_t nt = blockIdx.x, m = blockIdx.y;
+  const uint32_t nt = blockIdx.x, m0 = blockIdx.y * R;
+  const uint32_t rows = min(R, M - m0);
   const uint32_t K8 = K / 8, per = K8 / ksplit;
   const uint16_t* tile = w + (size_t)nt * K8 * 128 + (size_t)q * per * 128 + lane;
-  const uint16_t* xr = x + (size_t)m * K + (size_t)q * per * 8;
-  float acc = 0.f;
+  const uint16_t* xr = x + (size_t)m0 * K + (size_t)q * per * 8;
+  float acc[R];
+#pragma unroll
+  for (uint32_t r = 0; r < R; ++r) acc[r] = 0.f;
   uint32_t k8 = 0;
   for (; k8 + 4 <= per; k8 += 4) {
     uint16_t wv[4][8];
-    u4_t xv[4];
 #pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) {
+    for (uint32_t u = 0; u < 4; ++u)
 #pragma unroll
       for (uint32_t j = 0; j < 8; ++j) wv[u][j] = tile[(size_t)(k8 + u) * 128 + j * 16];
-      xv[u] = *reinterpret_cast<const u4_t*>(xr + (k8 + u) * 8);
-    }
 #pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) {
-      const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+    for (uint32_t r = 0; r < R; ++r) {
+      if (r < rows) {
+        u4_t xv[4];
 #pragma unroll
-      for (uint32_t j = 0; j < 8; ++j)
-        acc += h2f(wv[u][j]) * h2f((uint16_t)(xw[j / 2] >> (16 * (j % 2))));
+        for (uint32_t u = 0; u < 4; ++u) xv[u] = *reinterpret_cast<const u4_t*>(xr + (size_t)r * K + (k8 + u) * 8);
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+          const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+          for (uint32_t j = 0; j < 8; ++j)
+            acc[r] += h2f(wv[u][j]) * h2f((uint16_t)(xw[j / 2] >> (16 * (j % 2))));
+        }
+      }
     }
   }
   for (; k8 < per; ++k8)
-    for (uint32_t j = 0; j < 8; ++j) acc += h2f(tile[(size_t)k8 * 128 + j * 16]) * h2f(xr[k8 * 8 + j]);
-  red[q][lane] = acc;
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r)
+      if (r < rows)
+        for (uint32_t j = 0; j < 8; ++j)
+          acc[r] += h2f(tile[(size_t)k8 * 128 + j * 16]) * h2f(xr[(size_t)r * K + k8 * 8 + j]);
+#pragma unroll
+  for (uint32_t r = 0; r < R; ++r) red[r][q][lane] = acc[r];
   __syncthreads();
   for (uint32_t stride = ksplit / 2; stride > 0; stride >>= 1) {
-    if (q < stride) red[q][lane] += red[q + stride][lane];
+    if (q < stride)
+#pragma unroll
+      for (uint32_t r = 0; r < R; ++r) red[r][q][lane] += red[r][q + stride][lane];
     __syncthreads();
   }
-  if (q == 0) out[(size_t)m * N + nt * 16 + lane] = red[0][lane];
+  if (q == 0)
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r)
+      if (r < rows) out[(size_t)(m0 + r) * N + nt * 16 + lane] = red[r][0][lane];
 }
 
 // ---- routing (moe.cl:192-262; twin moe_ref.h:62-96) ----------------------------------------
@@ -289,8 +310,11 @@ extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* o
   if (ksplit == 0 || ksplit > 16 || (ksplit & (ksplit - 1)) || (K / 8) % ksplit)
     return mi_fail(MI_ERR_SHAPE, "gemv_f16w: ksplit must be a power of two <= 16 dividing K/8");
   if (reinterpret_cast<uintptr_t>(x) % 16) return mi_fail(MI_ERR_ARG, "gemv_f16w: x needs 16-byte alignment");
-  gemv_f16w_kernel<<<dim3(N / 16, M), 16 * ksplit, 0, static_cast<hipStream_t>(stream)>>>(w_tiled, x, out, K, N,
-                                                                                          ksplit);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (M >= 64)
+    gemv_f16w_kernel<8><<<dim3(N / 16, (M + 7) / 8), 16 * ksplit, 0, st>>>(w_tiled, x, out, M, K, N, ksplit);
+  else
+    gemv_f16w_kernel<1><<<dim3(N / 16, M), 16 * ksplit, 0, st>>>(w_tiled, x, out, M, K, N, ksplit);
   return mi_hip(static_cast<int>(hipGetLastError()), "gemv_f16w launch");
 }
 
