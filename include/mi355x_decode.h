@@ -340,8 +340,8 @@ int mi_attn_prep_rows(const float* qkv, uint32_t T, uint32_t pos0, const mi_attn
  * and sets *flag = 0xDEAD0001 (flag may be NULL). */
 int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, uint32_t T,
                   uint32_t hidden, uint32_t vocab, uint32_t* flag, void* stream);
-/* The chunk's MoE expert FFN grouped by expert (replaces the per-row expert walk that the
- * reference's prefill runs through moe.cl:1-13 for each row): route [T][32] (mi_moe_route rows),
+/* The chunk's MoE expert FFN (the expert part of the reference's MoE block, moe.cl:1-13, for
+ * T rows at once), grouped by expert: route [T][32] (mi_moe_route rows),
  * x [T][hidden] f16, the layer's layout-1 gate||up and down blocks (experts + 1 of each, the
  * shared expert last); resid [T][hidden] f16 += the slot-ordered combine (moe_ref.h:144-152).
  * Workspace: list [T (top_k + 1)] u32, tiles [(T (top_k + 1) + 63) / 64 + experts + 1] x 4 u32
