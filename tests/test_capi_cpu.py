@@ -60,6 +60,18 @@ def test_moe_argument_errors_without_a_gpu():
     assert L.mi_moe_down(8, 8, 8, 8, 1, 256, 8, 2048, 2048, None) == -2    # inter > 1024
     assert L.mi_gemv_f16w(8, 16, 8, 1, 2048, 272, 3, None) == -2           # ksplit not 2^n
     assert b"ksplit" in L.mi_last_error()
+    assert L.mi_moe_route(8, 8, 65536, 256, 8, 272, None) == -2    # more rows than the grid takes
+    assert L.mi_gemv_f16w(16, 16, 8, 65536, 2048, 272, 16, None) == -2
+    # the grouped expert FFN of a prefill chunk: T 1..2048, the decode kernels' shape limits
+    a = [16] * 5
+    w = [16, 16, 16, 16, 16, None]
+    assert L.mi_moe_prefill(None, *a[1:], 4, 256, 8, 2048, 512, *w) == -1
+    assert L.mi_moe_prefill(*a, 2049, 256, 8, 2048, 512, *w) == -2
+    assert L.mi_moe_prefill(*a, 4, 100, 8, 2048, 512, *w) == -2
+    assert L.mi_moe_prefill(*a, 4, 256, 9, 2048, 512, *w) == -2
+    assert L.mi_moe_prefill(*a, 4, 256, 8, 2000, 512, *w) == -2
+    assert L.mi_moe_prefill(*a, 4, 256, 8, 2048, 2048, *w) == -2
+    assert b"moe_prefill" in L.mi_last_error()
 
 
 def test_kv8_argument_errors_without_a_gpu():
