@@ -473,7 +473,7 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
-    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5", "prefill"], default=None,
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5", "prefill", "moe_prefill"], default=None,
                     help="run only that secondary measurement and print its JSON (the command the "
                          "attention and single-GEMV kernel profiles use)")
     args = ap.parse_args()
@@ -485,6 +485,16 @@ def main():
         eng = mi.Engine(mi.desc_27b(max_len=2112), seed=args.seed)
         print(json.dumps({"prefill": measure_prefill(eng)}), flush=True)
         eng.close()
+        return
+    if args.only == "moe_prefill":
+        # the configs[3] MoE model's chunked prefill of a 2048-token prompt, three timed calls
+        eng = mi.Engine(mi.desc_moe_cfg4(max_len=2112), seed=args.seed + 1)
+        ms = [time_prefill(eng, 2048) for _ in range(3)]
+        eng.close()
+        print(json.dumps({"moe_prefill": {"workload": "configs[3] MoE model, prefill of a 2048-token prompt in one "
+                                          "chunk (synthetic ids, random-init weights)",
+                                          "ms": [round(m, 2) for m in ms],
+                                          "tokens_per_s": round(2048 / min(ms) * 1e3, 1)}}), flush=True)
         return
     if args.only:
         fn = {"cfg1": lambda: measure_cfg1(None),
