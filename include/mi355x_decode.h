@@ -345,13 +345,13 @@ int mi_embed_rows(const uint32_t* ids, const uint16_t* embed, uint16_t* resid, u
  * x [T][hidden] f16, the layer's layout-1 gate||up and down blocks (experts + 1 of each, the
  * shared expert last); resid [T][hidden] f16 += the slot-ordered combine (moe_ref.h:144-152).
  * Workspace: list [T (top_k + 1)] u32, tiles [(T (top_k + 1) + 63) / 64 + experts + 1] x 4 u32
- * (16-byte aligned), tiles_n [1], h [T (top_k + 1)][inter] f16, d [T (top_k + 1)][hidden] fp32.
+ * (16-byte aligned), tiles_n [1], h [T (top_k + 1)][inter] f16, d [T (top_k + 1)][hidden] f16.
  * Each expert's pairs run through the int4 MFMA tile in 64-row tiles, so the per-pair values
  * round like mi_gemm_w4a16 (one f16 rounding per weight), not like the decode kernels. T <= 2048. */
 int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks,
                    const uint32_t* dn_blocks, uint16_t* resid, uint32_t T, uint32_t experts,
                    uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t* list, uint32_t* tiles,
-                   uint32_t* tiles_n, uint16_t* h, float* d, void* stream);
+                   uint32_t* tiles_n, uint16_t* h, uint16_t* d, void* stream);
 
 /* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
  * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the

@@ -426,7 +426,7 @@ struct mi_engine {
   uint32_t* pf_tiles = nullptr;  // [(cap (top_k + 1) + 63) / 64 + experts + 1][4]
   uint32_t* pf_tiles_n = nullptr;
   uint16_t* pf_mh = nullptr;     // [cap (top_k + 1)][moe_inter]
-  float* pf_md = nullptr;        // [cap (top_k + 1)][hidden]
+  uint16_t* pf_md = nullptr;     // [cap (top_k + 1)][hidden] f16
 
   int prefill_alloc(uint32_t cap) {
     if (cap <= pf_cap) return 0;

@@ -259,7 +259,8 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
 // 16-column tiles of 64-k groups: word j of the group's tile holds k 8 j .. 8 j + 7 of column c
 // at j 16 + c, its f16 scale at half-word 256 + c). A row of a pair p is row p / slots of x
 // (GATE_UP) or row p of h (down). GATE_UP: N = 2 inter in interleave16 order, SwiGLU in the
-// epilogue into h[p][inter] (the dense GEMM's epilogue); down: d[p][N] fp32. Tile: 64 pairs x
+// epilogue into h[p][inter] (the dense GEMM's epilogue); down: d[p][N] rounded to f16 (the
+// combine's first rounding of a slot's value, so nothing is lost). Tile: 64 pairs x
 // 256 columns, 4 waves of 64 x 64, the dense GEMM's k loop.
 template <bool GATE_UP>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(const u4_t* __restrict__ tiles,
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const u4_t* __restrict__ 
                                                        const uint32_t* __restrict__ list,
                                                        const uint32_t* __restrict__ blocks, size_t block_u32,
                                                        const uint16_t* __restrict__ a, uint32_t a_rows,
-                                                       uint16_t* __restrict__ h_out, float* __restrict__ d_out,
+                                                       uint16_t* __restrict__ h_out, uint16_t* __restrict__ d_out,
                                                        uint32_t slots, uint32_t K, uint32_t N) {
   __shared__ __align__(16) uint16_t As[2][kMoeRows][GROW];
   if (blockIdx.y >= tiles_n[0]) return;  // uniform: the grid is sized for the most tiles
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const u4_t* __restrict__ 
           }
         } else {
 #pragma unroll
-          for (uint32_t j = 0; j < 4; ++j) d_out[(size_t)p * N + n0 + 64u * wn + 16u * j + fr] = acc[i][j][r];
+          for (uint32_t j = 0; j < 4; ++j) d_out[(size_t)p * N + n0 + 64u * wn + 16u * j + fr] = f2h(acc[i][j][r]);
         }
       }
     }
@@ -382,21 +383,21 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const u4_t* __restrict__ 
 // resid[t][n] += the slot-ordered combine of row t's pair outputs (moe_down_kernel's epilogue,
 // moe_ref.h:144-152): sum_k rne(rne(d_k) w_k) in slot order, + rne(rne(d_shared) s)
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint32_t* __restrict__ route,
-                                                          const float* __restrict__ d, uint16_t* __restrict__ resid,
+                                                          const uint16_t* __restrict__ d, uint16_t* __restrict__ resid,
                                                           uint32_t top_k, uint32_t hidden) {
   const uint32_t t = blockIdx.y, n = blockIdx.x * 256u + threadIdx.x;
   if (n >= hidden) return;
   const uint32_t* row = route + (size_t)t * kMoeRouteWords;
   const uint32_t slots = top_k + 1;
-  const float* dp = d + (size_t)t * slots * hidden + n;
+  const uint16_t* dp = d + (size_t)t * slots * hidden + n;
   float sum = 0.f;
   for (uint32_t k = 0; k < top_k; ++k) {
     const float wk = __builtin_bit_cast(float, row[kMoeW + k]);
-    sum += h2f(f2h(h2f(f2h(dp[(size_t)k * hidden])) * wk));
+    sum += h2f(f2h(h2f(dp[(size_t)k * hidden]) * wk));
   }
   const uint16_t r_b = f2h(sum);
   const float sg = __builtin_bit_cast(float, row[kMoeSG]);
-  const uint16_t sh_b = f2h(h2f(f2h(dp[(size_t)top_k * hidden])) * sg);
+  const uint16_t sh_b = f2h(h2f(dp[(size_t)top_k * hidden]) * sg);
   const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
   uint16_t* rp = resid + (size_t)t * hidden + n;
   *rp = f2h(h2f(*rp) + h2f(o_b));
@@ -850,7 +851,7 @@ int mi_gemm_w4a16_silu(const uint32_t* qweight, const uint16_t* scales, const ui
 
 int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks, const uint32_t* dn_blocks,
                    uint16_t* resid, uint32_t T, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
-                   uint32_t* list, uint32_t* tiles, uint32_t* tiles_n, uint16_t* h, float* d, void* stream) {
+                   uint32_t* list, uint32_t* tiles, uint32_t* tiles_n, uint16_t* h, uint16_t* d, void* stream) {
   if (!route || !x || !gu_blocks || !dn_blocks || !resid || !list || !tiles || !tiles_n || !h || !d)
     return mi_fail(MI_ERR_ARG, "moe_prefill: null pointer");
   if (T == 0 || T > 2048u) return mi_fail(MI_ERR_SHAPE, "moe_prefill: T must be 1..2048");

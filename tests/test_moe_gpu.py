@@ -245,7 +245,7 @@ def test_moe_prefill_matches_decode_kernels(T, bad):
     # the grouped path
     P = T * (K + 1)
     lst, tiles, tiles_n = empty(P, np.uint32), empty(((P + 63) // 64 + E + 1) * 4, np.uint32), empty(1, np.uint32)
-    hh, dd = empty((P, I), np.uint16), empty((P, H), np.float32)
+    hh, dd = empty((P, I), np.uint16), empty((P, H), np.uint16)
     resid = dev(np.zeros((T, H), np.uint16))
     mi.call("mi_moe_prefill", ptr(droute), ptr(dx), ptr(mo.d_gu), ptr(mo.d_dn), ptr(resid), T, E, K, H, I, ptr(lst),
             ptr(tiles), ptr(tiles_n), ptr(hh), ptr(dd), stream())
