@@ -398,63 +398,107 @@ def measure_cfg4(args, kv_int8=0):
     return out
 
 
-def cpu_oracle_step(eng, tok, pos):
-    """One full decode step of the same model through the CPU oracle (the reference's
-    scalar twins restated; OpenMP over columns in the GEMV twins). Returns (seconds,
-    logits, argmax, threads)."""
-    import oracle as O
-    d = eng.desc
-    H, I, HD, QH, KVH = d.hidden, d.inter, d.head_dim, d.q_heads, d.kv_heads
-    S = [eng.linear_s(w) for w in range(5)]
-    dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
-    keep = []
+class CpuOracle:
+    """The same model wired into the CPU oracle (the reference's scalar twins restated;
+    OpenMP over columns in the GEMV twins, each column's order unchanged, so any thread count
+    gives the same bits). Host copies of every weight are taken once."""
 
-    def h(kind, layer, dt):
-        a = eng.to_host(kind, layer, dt)
-        keep.append(a)
-        return a.ctypes.data
+    def __init__(self, eng):
+        import oracle as O
+        self.O = O
+        d = self.d = eng.desc
+        H, I, HD, QH, KVH = d.hidden, d.inter, d.head_dim, d.q_heads, d.kv_heads
+        S = [eng.linear_s(w) for w in range(5)]
+        dims = [(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]
+        keep = self.keep = []
 
-    moe = d.experts > 0
-    layers = (O.Layer * d.layers)()
-    for li in range(d.layers):
-        lins = [O.Linear(h(2 * w, li, np.uint32), h(2 * w + 1, li, np.uint16), K, N, S[w])
-                if not (moe and w >= 2) else O.Linear(None, None, K, N, 1)
-                for w, (K, N) in enumerate(dims)]
-        Ly = layers[li]
-        Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+        def h(kind, layer, dt):
+            a = eng.to_host(kind, layer, dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        moe = d.experts > 0
+        layers = (O.Layer * d.layers)()
+        keep.append(layers)
+        for li in range(d.layers):
+            lins = [O.Linear(h(2 * w, li, np.uint32), h(2 * w + 1, li, np.uint16), K, N, S[w])
+                    if not (moe and w >= 2) else O.Linear(None, None, K, N, 1)
+                    for w, (K, N) in enumerate(dims)]
+            Ly = layers[li]
+            Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+            if moe:
+                Ly.router = h(mi.T_ROUTER, li, np.uint16)
+                Ly.moe_gu = h(mi.T_MOE_GU, li, np.uint32)
+                Ly.moe_dn = h(mi.T_MOE_DN, li, np.uint32)
+            Ly.in_norm = h(mi.T_IN_NORM, li, np.float32)
+            Ly.post_norm = h(mi.T_POST_NORM, li, np.float32)
+            if d.qk_norm:
+                Ly.q_norm = h(mi.T_Q_NORM, li, np.float32)
+                Ly.k_norm = h(mi.T_K_NORM, li, np.float32)
+        kv_t = np.int8 if d.kv_int8 else np.uint16
+        self.kv_k = eng.to_host(mi.T_KV_K, 0, kv_t).copy()
+        self.kv_v = eng.to_host(mi.T_KV_V, 0, kv_t).copy()
+        if d.kv_int8:
+            self.kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
+            self.kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
+        sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
+        self.model = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
+                                  C.cast(layers, C.c_void_p), h(mi.T_EMBED, 0, np.uint16),
+                                  h(mi.T_FINAL_NORM, 0, np.float32),
+                                  O.Linear(h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab,
+                                           S[4]),
+                                  h(mi.T_ROPE, 0, np.float32), d.attn_tgt, H // 64)
         if moe:
-            Ly.router = h(mi.T_ROUTER, li, np.uint16)
-            Ly.moe_gu = h(mi.T_MOE_GU, li, np.uint32)
-            Ly.moe_dn = h(mi.T_MOE_DN, li, np.uint32)
-        Ly.in_norm = h(mi.T_IN_NORM, li, np.float32)
-        Ly.post_norm = h(mi.T_POST_NORM, li, np.float32)
-        if d.qk_norm:
-            Ly.q_norm = h(mi.T_Q_NORM, li, np.float32)
-            Ly.k_norm = h(mi.T_K_NORM, li, np.float32)
-    kv_t = np.int8 if d.kv_int8 else np.uint16
-    kv_k = eng.to_host(mi.T_KV_K, 0, kv_t).copy()
-    kv_v = eng.to_host(mi.T_KV_V, 0, kv_t).copy()
-    sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
-    model = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
-                         C.cast(layers, C.c_void_p), h(mi.T_EMBED, 0, np.uint16),
-                         h(mi.T_FINAL_NORM, 0, np.float32),
-                         O.Linear(h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab, S[4]),
-                         h(mi.T_ROPE, 0, np.float32), d.attn_tgt, H // 64)
-    if moe:
-        model.experts, model.top_k, model.moe_inter = d.experts, d.top_k, d.moe_inter
-        model.router_n, model.router_ksplit = (d.experts + 1 + 15) // 16 * 16, 16
-    logits = np.zeros(d.vocab, np.float32)
-    t0 = time.perf_counter()
-    if d.kv_int8:
-        kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
-        kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
-        am = O.lib().orc_dense_step_kv8(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(kv_ks),
-                                        O._p(kv_vs), O._p(logits), d.layers)
-    else:
-        am = O.lib().orc_dense_step(O.ORC_F16, C.byref(model), tok, pos, O._p(kv_k), O._p(kv_v), O._p(logits),
-                                    d.layers)
-    dt = time.perf_counter() - t0
-    return dt, logits, int(am), int(O.lib().orc_threads())
+            m = self.model
+            m.experts, m.top_k, m.moe_inter = d.experts, d.top_k, d.moe_inter
+            m.router_n, m.router_ksplit = (d.experts + 1 + 15) // 16 * 16, 16
+
+    def step(self, tok, pos, layers=None, threads=None):
+        """One decode step over the first `layers` layers (all by default) and the head.
+        Returns (seconds, logits, argmax, threads used). The KV copies are the step's inputs
+        (a step writes row `pos` into them, the same values on every call)."""
+        O, d = self.O, self.d
+        nl = d.layers if layers is None else layers
+        full = O.lib().orc_threads()
+        if threads:
+            O.lib().orc_set_threads(threads)
+        used = O.lib().orc_threads()
+        logits = np.zeros(d.vocab, np.float32)
+        t0 = time.perf_counter()
+        if d.kv_int8:
+            am = O.lib().orc_dense_step_kv8(O.ORC_F16, C.byref(self.model), tok, pos, O._p(self.kv_k),
+                                            O._p(self.kv_v), O._p(self.kv_ks), O._p(self.kv_vs), O._p(logits), nl)
+        else:
+            am = O.lib().orc_dense_step(O.ORC_F16, C.byref(self.model), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
+                                        O._p(logits), nl)
+        dt = time.perf_counter() - t0
+        if threads:
+            O.lib().orc_set_threads(full)
+        return dt, logits, int(am), int(used)
+
+
+def cpu_oracle_step(eng, tok, pos):
+    """One full decode step of the same model through the CPU oracle on every host thread.
+    Returns (seconds, logits, argmax, threads)."""
+    return CpuOracle(eng).step(tok, pos)
+
+
+def cpu_model():
+    """The host CPU's model string and the threads this process may run on."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count()
+    return name, avail, os.cpu_count()
 
 
 def main():
@@ -521,7 +565,14 @@ def main():
     if not args.no_cpu and not args.eager:
         log("bench: CPU oracle step (one full 64-layer step on the host) ...")
         eng.reset(args.context, tok0)
-        dt, cpu_logits, cpu_am, threads = cpu_oracle_step(eng, tok0, args.context)
+        orc = CpuOracle(eng)
+        dt, cpu_logits, cpu_am, threads = orc.step(tok0, args.context)
+        # 1 core, on a bounded sample: 1 and 3 layers + the head; per layer = the difference / 2
+        t1 = orc.step(tok0, args.context, layers=1, threads=1)[0]
+        t3 = orc.step(tok0, args.context, layers=3, threads=1)[0]
+        per_layer = max(t3 - t1, 0.0) / 2
+        one_core_step = (t1 - per_layer) + desc.layers * per_layer
+        del orc
         eng.reset(args.context, tok0)
         gpu_tok = int(eng.generate(1)[0])
         g = eng.logits(1)[0].astype(np.float64)
@@ -533,10 +584,16 @@ def main():
             "within_rel_2e-3": bool(np.all(err <= 2e-3 * np.abs(w) + 2e-3 * np.abs(w).max())),
             "argmax_gpu": gpu_tok, "argmax_oracle": cpu_am,
         }
+        cpu_name, cpu_avail, cpu_all = cpu_model()
         cpu = {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
                "sample": f"one full decode step of the same 64-layer model at context {args.context} "
                          f"(oracle/oracle.cpp orc_dense_step, twin GEMV order, {threads} OpenMP threads), "
-                         f"{dt:.2f} s"}
+                         f"{dt:.2f} s",
+               "cpu_model": cpu_name, "threads_available": cpu_avail, "nproc": cpu_all,
+               "one_core": {"value": round(1.0 / one_core_step, 5), "unit": "tokens/s", "cores": 1,
+                            "sample": f"1 thread: the step over 1 layer + head ({t1:.2f} s) and 3 layers + head "
+                                      f"({t3:.2f} s); per layer {per_layer:.2f} s, so the 64-layer step is "
+                                      f"{one_core_step:.1f} s"}}
         log(f"bench: cpu step {dt:.2f} s on {threads} threads; parity {parity}")
 
     eng.reset(args.context, tok0)

@@ -29,6 +29,10 @@
 extern "C" {
 #endif
 
+/* The device status word's value after a fused launch's hand-off wait timed out
+ * (mi_gemv_epilogue.status; the engine's control block word MI_CTRL_DEBUG). */
+#define MI_STATUS_HANDOFF_TIMEOUT 0xDEAD0003u
+
 enum {
   MI_OK = 0,
   MI_ERR_ARG = -1,   /* null / misaligned pointer or inconsistent argument */
@@ -135,6 +139,19 @@ typedef struct mi_gemv_epilogue {
   const uint32_t* pages;
   uint32_t page;
   uint32_t kv_len;
+  /* Every fused kind. A consumer's wait for a hand-off word is bounded: after poll_limit polls
+   * of a word that stays empty (0 = the default, 2^21, about a second) it gives up, takes the
+   * empty NaN as the value and sets *status = MI_STATUS_HANDOFF_TIMEOUT (status may be NULL).
+   * The output of such a launch is not to be used, and the hand-off words may then hold
+   * values published late: run mi_gemv_handoff_init on them before the next fused launch.
+   * (The waits complete because every XCD dispatches its share of the grid in order and the
+   * consumers are the grid's last row: all producers are resident or finished before a
+   * consumer waits; RESID's consumers also need all N/64 of them resident at once.)
+   * inject: fault injection for tests of that path, 0 in normal use; bit 0 = the producer
+   * work-groups publish nothing, so every consumer's wait times out. */
+  uint32_t* status;
+  uint32_t poll_limit;
+  uint32_t inject;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,

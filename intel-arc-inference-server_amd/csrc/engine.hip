@@ -98,6 +98,7 @@ struct mi_engine {
   float* part = nullptr;     // the plain launches' split-K partials (qkv)
   float* part_ex = nullptr;  // the fused launches' hand-off words (empty between launches)
   float* sumsq = nullptr;    // RESID's hand-off words for the tiles' sums of squares
+  size_t part_ex_n = 0, sumsq_n = 0;
   float* attn_q = nullptr;
   float* attn_part = nullptr;
   float* logits = nullptr;
@@ -126,6 +127,18 @@ struct mi_engine {
     allocs.push_back(v);
     *p = static_cast<T*>(v);
     return 0;
+  }
+
+  // frees one allocation of alloc() (the stream must have drained) and clears the pointer
+  void release(void** p) {
+    if (!*p) return;
+    for (auto it = allocs.begin(); it != allocs.end(); ++it)
+      if (*it == *p) {
+        hipFree(*it);
+        allocs.erase(it);
+        break;
+      }
+    *p = nullptr;
   }
 
   // epi: the epilogue the step runs this linear with (its split-K width depends on it)
@@ -207,8 +220,9 @@ struct mi_engine {
     MI_TRY(alloc(&attn_out, size_t(R) * QH * HD));
     MI_TRY(alloc(&part, part_max));
     MI_TRY(alloc(&part_ex, part_ex_max));
+    part_ex_n = part_ex_max;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_max, stream));
-    const size_t sumsq_n = size_t(H / 64) * R * (H / 64);
+    sumsq_n = size_t(H / 64) * R * (H / 64);
     MI_TRY(alloc(&sumsq, sumsq_n));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
     MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
@@ -288,6 +302,7 @@ struct mi_engine {
     e.next_norm_w = next_w;
     e.x_next = x;
     e.eps = d.rms_eps;
+    e.status = ctrl + MI_CTRL_DEBUG;
     return e;
   }
 
@@ -318,6 +333,7 @@ struct mi_engine {
         eq.row_stride = HD;
         eq.head_stride = size_t(d.max_len) * HD;
         eq.kv_len = d.max_len;
+        eq.status = ctrl + MI_CTRL_DEBUG;
         MI_TRY(mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream));
       } else {
         MI_TRY(gemv(L.qkv, x, M));
@@ -362,6 +378,7 @@ struct mi_engine {
       mi_gemv_epilogue eg{};
       eg.kind = MI_EPI_SILU;
       eg.h = hbuf;
+      eg.status = ctrl + MI_CTRL_DEBUG;
       MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                               stream));
       const mi_gemv_epilogue ed = resid_epi(next_w);
@@ -372,6 +389,7 @@ struct mi_engine {
     el.logits = logits;
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
+    el.status = ctrl + MI_CTRL_DEBUG;
     MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
     MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
     return 0;
@@ -407,6 +425,23 @@ struct mi_engine {
     return mi_memcpy_d2h(out, ctrl, MI_CTRL_WORDS * 4, stream);
   }
 
+  // After the stream has drained: a fused launch whose hand-off wait timed out leaves
+  // MI_STATUS_HANDOFF_TIMEOUT in the debug word, and its hand-off words may hold values that
+  // were published late. Those are emptied again here so the next step starts clean, and the
+  // caller gets an error (the tokens of that call are not to be used). The word is cleared.
+  int check_handoff() {
+    uint32_t c[MI_CTRL_WORDS];
+    MI_TRY(read_ctrl(c));
+    if (c[MI_CTRL_DEBUG] != MI_STATUS_HANDOFF_TIMEOUT) return 0;
+    MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
+    MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
+    ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
+    MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
+    MI_TRY(mi_stream_sync(stream));
+    return mi_fail(MI_ERR_STATE, "a fused GEMV's hand-off wait timed out; the step's output is invalid "
+                                 "(hand-off words re-initialised)");
+  }
+
   // ---- chunked prefill (Engine::prefill, src/runtime/engine.h:97-115; the walk of
   // src/runtime/prefill/step.h step_chunk). Scratch is allocated on the first call for the
   // largest chunk asked so far, as the reference allocates its prefill scratch on first use. ----
@@ -437,6 +472,14 @@ struct mi_engine {
       MI_TRY(alloc(&pf_ids, d.max_len));
       MI_TRY(alloc(&pf_ctrl, MI_CTRL_WORDS));
       MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(pf_ctrl, 0, MI_CTRL_WORDS * 4, stream)), "prefill ctrl clear"));
+    }
+    if (pf_cap) {
+      // a larger chunk than before: the previous set goes (after the stream has drained)
+      MI_TRY(mi_stream_sync(stream));
+      for (void** p : {(void**)&pf_out, (void**)&pf_q, (void**)&pf_resid, (void**)&pf_x, (void**)&pf_h,
+                       (void**)&pf_attn, (void**)&pf_logits, (void**)&pf_route, (void**)&pf_list,
+                       (void**)&pf_tiles, (void**)&pf_tiles_n, (void**)&pf_mh, (void**)&pf_md})
+        release(p);
     }
     MI_TRY(alloc(&pf_out, size_t(cap) * widest));
     MI_TRY(alloc(&pf_q, size_t(cap) * QHD));
@@ -533,6 +576,7 @@ struct mi_engine {
     el.logits = logits;
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
+    el.status = ctrl + MI_CTRL_DEBUG;
     MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, pf_x + size_t(T - 1) * d.hidden, part_ex, 1, lm_head.K, lm_head.N,
                             lm_head.S, &el, stream));
     MI_TRY(set_rows(pos0 + n - 1, 1, nullptr, 0));
@@ -677,7 +721,8 @@ int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens) {
   const uint32_t first = c[MI_CTRL_STEPS];
   for (uint32_t i = 0; i < n; ++i) MI_TRY(mi_engine_replay(e, 1));
   if (tokens) MI_TRY(mi_memcpy_d2h(tokens, e->history + first, size_t(n) * 4, e->stream));
-  return mi_stream_sync(e->stream);
+  MI_TRY(mi_stream_sync(e->stream));
+  return e->check_handoff();
 }
 
 int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
@@ -690,7 +735,8 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
     MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
     MI_TRY(mi_engine_replay(e, 1));
   }
-  return mi_stream_sync(e->stream);
+  MI_TRY(mi_stream_sync(e->stream));
+  return e->check_handoff();
 }
 
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk) {
@@ -717,6 +763,7 @@ int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t*
   MI_TRY(mi_engine_replay(e, k + 1));
   uint32_t c2[MI_CTRL_WORDS];
   MI_TRY(e->read_ctrl(c2));
+  MI_TRY(e->check_handoff());
   if (argmax_rows) std::memcpy(argmax_rows, c2 + MI_CTRL_OUT, (k + 1) * 4);
   // leave pos at the verify position until commit (Engine::commit decides the advance)
   return e->set_rows(c[MI_CTRL_POS], 1, nullptr, 0);

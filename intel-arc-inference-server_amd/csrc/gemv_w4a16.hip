@@ -115,6 +115,10 @@ struct GemvEpi {
   size_t row_stride, head_stride;
   uint32_t page, kv_len, q_heads, kv_heads, head_dim, rot_dim;
   float qk_eps;
+  // a device word set to kStatusTimeout when a hand-off wait gives up (NULL: none)
+  uint32_t* status;
+  uint32_t poll_limit;  // polls of one word before giving up
+  uint32_t inject;      // fault injection for tests: bit 0 = producers publish nothing
 };
 
 enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3, EPI_F16OUT = 4, EPI_QKV = 5 };
@@ -130,6 +134,7 @@ template <int MR>
 constexpr int fold_buf() { return 2048; }
 constexpr int kFoldBuf_QKV = 2048;
 constexpr uint32_t kPollLimit = 1u << 21; // polls of one word before giving up (~seconds)
+constexpr uint32_t kStatusTimeout = 0xDEAD0003u;  // the status word's value after a wait gave up
 
 __device__ __forceinline__ float empty_f() { return __builtin_bit_cast(float, kEmpty); }
 __device__ __forceinline__ bool is_empty(float v) { return __builtin_bit_cast(uint32_t, v) == kEmpty; }
@@ -143,9 +148,12 @@ __device__ __forceinline__ float publishable(float v) {
 // voff + u * ustride from base: buffer accesses with a per-thread 32-bit offset and a uniform
 // one per u keep the addresses out of 64-bit registers. sc1 makes them the device-coherent
 // accesses of ld_agent / st_agent. The whole work-group calls this; dst is LDS.
+// A wait that reaches `limit` polls gives up: the words still empty are taken as they are
+// (the empty NaN) and `status` (when not NULL) is set to kStatusTimeout, so the host learns
+// that this launch's output is not to be used.
 template <int BUF>
 __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base, uint32_t voff,
-                                          uint32_t ustride) {
+                                          uint32_t ustride, uint32_t* status, uint32_t limit) {
   constexpr int PER = BUF / 256;
   constexpr int kSc1 = 16;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7FFFFFFF, 0x00020000);
@@ -159,7 +167,7 @@ __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base,
   for (int u = 0; u < PER; ++u)
     if (t + 256u * u < cnt && v[u] == kEmpty) pending |= 1u << u;
   // re-poll every still-empty word together, so a wait costs one round trip per poll, not per word
-  for (uint32_t n = 0; pending && n < kPollLimit; ++n) {
+  for (uint32_t n = 0; pending && n < limit; ++n) {
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int u = 0; u < PER; ++u)
@@ -168,6 +176,7 @@ __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base,
     for (int u = 0; u < PER; ++u)
       if ((pending & (1u << u)) && v[u] != kEmpty) pending &= ~(1u << u);
   }
+  if (pending && status) st_agent(status, kStatusTimeout);
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const uint32_t e = t + 256u * u;
@@ -234,7 +243,8 @@ __device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, 
   for (uint32_t s0 = 0; s0 < S; s0 += per_round) {
     const uint32_t ns = min(per_round, S - s0);
     poll_into<kFoldBuf_QKV>(s_fold, ns * total, const_cast<float*>(partials) + (size_t)s0 * M * N,
-                            ((t / HD) * N + nh0 + t % HD) * 4u, (256u / HD) * N * 4u);
+                            ((t / HD) * N + nh0 + t % HD) * 4u, (256u / HD) * N * 4u, epi.status,
+                            epi.poll_limit);
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < EL; ++u) {
@@ -414,7 +424,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       partials[((size_t)s * M + row) * N + n0 + col] = v;
     else if (consumer)
       red[0][row][col] = v;  // the consumer's own slice stays in LDS
-    else
+    else if (!(epi.inject & 1u))
       st_agent(partials + ((size_t)s * M + row) * N + n0 + col, publishable(v));
   }
   if constexpr (EPI == EPI_QKV) return;
@@ -449,7 +459,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       const uint32_t ns = min(per_round, S - 1 - s0);
       // element e: row-slice e / 64 of slices s0.., column e % 64 (e / 64 = t / 64 + 4 u)
       poll_into<kFoldBuf>(s_fold, ns * total, partials + (size_t)s0 * M * N,
-                          ((t / kCols) * N + n0 + t % kCols) * 4u, 4u * N * 4u);
+                          ((t / kCols) * N + n0 + t % kCols) * 4u, 4u * N * 4u, epi.status, epi.poll_limit);
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < EL; ++u) {
@@ -491,7 +501,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     const uint32_t rows_per_round = kFoldBuf / ntiles;
     for (uint32_t r0 = 0; r0 < M; r0 += rows_per_round) {
       const uint32_t nr = min(rows_per_round, M - r0);
-      poll_into<kFoldBuf>(s_fold, nr * ntiles, epi.sumsq + ((size_t)tile * M + r0) * ntiles, t * 4u, 1024u);
+      poll_into<kFoldBuf>(s_fold, nr * ntiles, epi.sumsq + ((size_t)tile * M + r0) * ntiles, t * 4u, 1024u,
+                          epi.status, epi.poll_limit);
       __syncthreads();
       if (t < nr) {
         const float* ss = s_fold + t * ntiles;
@@ -646,6 +657,9 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   hipStream_t st = static_cast<hipStream_t>(stream);
   GemvEpi e{ep->resid, ep->sumsq, ep->rstd, ep->next_norm_w, ep->x_next, ep->h,
             ep->logits, reinterpret_cast<u2_t*>(ep->argmax_part), ep->vocab_used, ep->eps, ep->out16};
+  e.status = ep->status;
+  e.poll_limit = ep->poll_limit ? ep->poll_limit : kPollLimit;
+  e.inject = ep->inject;
   int r;
   switch (ep->kind) {
     case MI_EPI_PARTIALS:

@@ -863,8 +863,9 @@ int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_
   if (inter == 0 || inter % 128 || inter > 1024)
     return mi_fail(MI_ERR_SHAPE, "moe_prefill: inter must be a multiple of 128 up to 1024");
   if (reinterpret_cast<uintptr_t>(tiles) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(gu_blocks) % 4)
-    return mi_fail(MI_ERR_ARG, "moe_prefill: tiles, x and h need 16-byte alignment");
+      reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(gu_blocks) % 4 ||
+      reinterpret_cast<uintptr_t>(dn_blocks) % 4)
+    return mi_fail(MI_ERR_ARG, "moe_prefill: tiles, x and h need 16-byte, gu_blocks and dn_blocks 4-byte alignment");
   const uint32_t slots = top_k + 1, P = T * slots;
   const uint32_t max_tiles = (P + kMoeRows - 1u) / kMoeRows + experts + 1u;
   const size_t gu_block = (size_t)(2u * inter / 16u) * (hidden / GBK) * kMoeTile;

@@ -78,6 +78,7 @@ def lib():
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
             "orc_threads": (i32, []),
+            "orc_set_threads": (None, [i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

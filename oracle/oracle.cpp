@@ -165,6 +165,15 @@ int orc_threads(void) {
 #endif
 }
 
+// Threads the OpenMP column loops use from now on (n >= 1); the result does not depend on it.
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+  if (n >= 1) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
 // ---- conversions -----------------------------------------------------------------------
 // src/common/bf16.h:8-16
 float orc_bf16_to_f32(uint16_t h) { return bitsf(uint32_t(h) << 16); }

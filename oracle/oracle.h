@@ -26,6 +26,7 @@ enum { ORC_BF16 = 0, ORC_F16 = 1 };
 /* threads the OpenMP-parallel functions use (the GEMV twins split columns; each column's
  * order is unchanged, so results do not depend on the thread count) */
 int orc_threads(void);
+void orc_set_threads(int n);
 
 /* ---- scalar conversions (src/common/bf16.h:8-43, src/common/kv8.h:56-78) ---- */
 uint16_t orc_f32_to_bf16(float f);

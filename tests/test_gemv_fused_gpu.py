@@ -283,3 +283,62 @@ def test_embed_norm_bitwise():
     L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, H, G, 1e-6)
     assert np.array_equal(host(dr, np.uint16), r_ref)
     assert np.array_equal(host(dx, np.uint16), x_ref)
+
+
+@pytest.mark.parametrize("kind", ["resid", "silu"])
+def test_handoff_timeout_sets_the_status_word(kind):
+    """A consumer whose hand-off words never fill gives up after poll_limit polls, sets the
+    status word and exits (fault injection from the host: the producers publish nothing, and
+    the poll limit is tiny, so every kernel still ends normally). The words are left empty, and
+    the next normal launch on the same words gives the normal result."""
+    M, K, S = 1, 1024, 4
+    N = 1024
+    qw, sc = rand_w(K, N, 77)
+    rng = np.random.default_rng(5)
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    dq, ds, dx = dev(qw), dev(sc), dev(x)
+    part = partials_of(dq, ds, dx, M, K, N, S)
+    dpart = handoff(S * M * N)
+    status = dev(np.zeros(1, np.uint32))
+    G = N // 64
+    if kind == "resid":
+        resid = O.f32_to_f16_bits(rng.standard_normal((M, N)).astype(np.float32))
+        w = np.ones(N, np.float32)
+        dr, dw = dev(resid), dev(w)
+        dss = handoff(G * M * G)
+        drs = empty((M,), np.float32)
+        dout = empty((M, N), np.uint16)
+        ep = mi.GemvEpilogue(kind=mi.EPI_RESID, resid=ptr(dr), sumsq=ptr(dss), rstd=ptr(drs), next_norm_w=ptr(dw),
+                             x_next=ptr(dout), eps=1e-6)
+    else:
+        dout = empty((M, N // 2), np.uint16)
+        ep = mi.GemvEpilogue(kind=mi.EPI_SILU, h=ptr(dout))
+    ep.status, ep.poll_limit, ep.inject = ptr(status), 64, 1
+    print(f"handoff timeout {kind}: injected launch", flush=True)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    sync()
+    assert int(host(status, np.uint32)[0]) == mi.STATUS_HANDOFF_TIMEOUT
+    assert all_empty(dpart)
+    if kind == "resid":
+        assert all_empty(dss)
+    # a normal launch afterwards: status untouched, result as the oracle's
+    status.zero_()
+    ep.poll_limit, ep.inject = 0, 0
+    if kind == "resid":
+        dr.copy_(dev(resid))
+    print(f"handoff timeout {kind}: normal launch", flush=True)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    sync()
+    assert int(host(status, np.uint32)[0]) == 0
+    if kind == "resid":
+        r_ref = resid.copy()
+        s_ref = np.zeros((G, M), np.float32)
+        x_ref = np.zeros((M, N), np.uint16)
+        L().orc_res_fold(F16, O._p(part), O._p(r_ref), O._p(s_ref), M, N, S, G)
+        L().orc_norm_finish(F16, O._p(s_ref), O._p(r_ref), O._p(w), O._p(x_ref), M, N, G, 1e-6)
+        assert np.array_equal(host(dout, np.uint16), x_ref)
+    else:
+        want = O.silu_mul(F16, part, M, N // 2, S)
+        a = O.f16_bits_to_f32(host(dout, np.uint16)).astype(np.float64)
+        b = O.f16_bits_to_f32(want).astype(np.float64)
+        assert np.all(np.abs(a - b) <= 2 * np.maximum(np.abs(b), 2.0 ** -14) * 2.0 ** -10)
