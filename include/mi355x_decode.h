@@ -285,6 +285,15 @@ int mi_norm_rows(const uint16_t* resid, const float* norm_w, uint16_t* x_out, fl
                  uint32_t M, uint32_t hidden, float eps, void* stream);
 int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history,
               uint32_t history_len, uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
+/* mi_argmax without the `part` argument, allocating nothing: the chunk winners go to a
+ * file-scope device array of this library (8192 entries of 8 bytes, 64 KiB per GPU, held until
+ * the process ends), so ceil(vocab / 1024) * M must be <= 8192 (MI_ERR_SHAPE otherwise). No
+ * counterpart in the reference: for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race. The first call on a device looks the array's address up (hipGetSymbolAddress). */
+int mi_argmax_static(uint32_t* ctrl, const float* logits, uint32_t* history, uint32_t history_len,
+                     uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream);
 
 
 /* ---- mixture of experts (src/kernels/moe.cl, src/kernels/gemv_bf16.cl) ----

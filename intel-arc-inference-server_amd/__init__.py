@@ -59,6 +59,7 @@ SIGNATURES = {
     "mi_embed_gather": (i32, [vp, vp, vp, u32, u32, u32, vp]),
     "mi_argmax_groups": (u32, [u32]),
     "mi_argmax": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
+    "mi_argmax_static": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_argmax_finish": (i32, [vp, vp, u32, vp, u32, vp]),
     "mi_embed_norm": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, f32, vp]),
     "mi_gemv_w4a16_ex": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),

@@ -14,6 +14,8 @@
 // Wave64 note: strides >= 64 cross waves and go through LDS; strides < 64 are
 // __shfl_down within the wave, which adds exactly the same pairs.
 #include "mi_capi_internal.h"
+#include <mutex>
+
 #include "mi_common.h"
 
 namespace mi {
@@ -599,3 +601,45 @@ int mi_argmax(uint32_t* ctrl, const float* logits, void* part, uint32_t* history
 }
 
 }  // extern "C"
+
+// ---- mi_argmax_static: mi_argmax's two stages with the chunk winners in a file-scope device
+// array instead of a caller buffer, for callers that cannot allocate. ----
+namespace {
+constexpr uint32_t kArgmaxScratchMax = 8192;  // (value, index) pairs: groups * M at most (64 KiB)
+// Each GPU holds its own copy at its own address; the host learns it with hipGetSymbolAddress.
+static __device__ __align__(256) u2_t scratch[kArgmaxScratchMax];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+extern "C" int mi_argmax_static(uint32_t* ctrl, const float* logits, uint32_t* history, uint32_t history_len,
+                                uint32_t M, uint32_t vocab, uint32_t vocab_used, void* stream) {
+  if (!ctrl || !logits || M == 0 || M > 8 || vocab == 0 || vocab_used > vocab)
+    return mi_fail(MI_ERR_ARG, "argmax_static: bad arguments");
+  const uint32_t groups = mi_argmax_groups(vocab);
+  if ((size_t)groups * M > kArgmaxScratchMax)
+    return mi_fail(MI_ERR_SHAPE, "argmax_static: ceil(vocab / 1024) * M exceeds the 8192-entry device scratch");
+  int dev = 0;
+  if (int e = (int)hipGetDevice(&dev)) return mi_hip(e, "argmax_static: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return mi_fail(MI_ERR_STATE, "argmax_static: device index out of range");
+  void* part = nullptr;
+  {
+    // once per device, with that device current: the address of this device's copy
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      if (int e = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return mi_hip(e, "argmax_static: hipGetSymbolAddress");
+      g_scratch_ptr[dev] = p;
+    }
+    part = g_scratch_ptr[dev];
+  }
+  // stage 1 writes every (row, chunk) winner that stage 2 reads, so nothing needs clearing
+  argmax_stage1_kernel<<<dim3(groups, M), kWG, 0, (hipStream_t)stream>>>(ctrl, logits, (u2_t*)part, vocab,
+                                                                         vocab_used, groups);
+  int e = (int)hipGetLastError();
+  if (e) return mi_hip(e, "argmax_static stage1");
+  argmax_stage2_kernel<<<1, kWG, 0, (hipStream_t)stream>>>(ctrl, (const u2_t*)part, history, history_len,
+                                                            groups);
+  return mi_hip((int)hipGetLastError(), "argmax_static stage2");
+}

@@ -112,3 +112,12 @@ def test_prefill_and_handoff_argument_errors_without_a_gpu():
     assert L.mi_attn_prefill_kv8(16, 16, 16, 16, 16, 128, 128, 1, 128, None, 0, 4, 0, C.byref(sh), 16, 16,
                                  None) == -2  # the rotation needs head_dim 256
     assert L.mi_engine_prefill(None, None, 0, 0) == -1
+
+
+def test_argmax_static_rejects_sizes_beyond_its_scratch():
+    """mi_argmax_static's device array holds 8192 chunk winners: ceil(vocab / 1024) * M above
+    that is refused before anything touches a GPU."""
+    L = mi.lib()
+    assert L.mi_argmax_static(8, 8, None, 0, 8, 1025 * 1024, 1024, None) == -2
+    assert b"8192" in L.mi_last_error()
+    assert L.mi_argmax_static(None, 8, None, 0, 1, 1024, 1024, None) == -1
