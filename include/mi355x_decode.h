@@ -410,7 +410,13 @@ enum {
   MI_T_ROUTER, MI_T_MOE_GU, MI_T_MOE_DN, /* MoE layers: router tiles, expert blocks */
   MI_T_EMBED = 32, MI_T_FINAL_NORM, MI_T_LM_Q, MI_T_LM_S, MI_T_ROPE, MI_T_KV_K, MI_T_KV_V,
   MI_T_LOGITS, MI_T_CTRL, MI_T_HISTORY,
-  MI_T_KV_KS, MI_T_KV_VS /* the int8 cache's fp16 row scales (kv_int8) */
+  MI_T_KV_KS, MI_T_KV_VS, /* the int8 cache's fp16 row scales (kv_int8) */
+  /* activations of the last step of the graph path (diagnostics): the residual [rows][hidden],
+   * the normed input x, q fp32 [rows][q_heads][head_dim], the attention output, SwiGLU's output */
+  MI_T_RESID, MI_T_X, MI_T_ATTN_Q, MI_T_ATTN_OUT, MI_T_HBUF,
+  /* the persistent step's work-item table and hand-off words (diagnostics; empty before
+   * mi_engine_persistent) */
+  MI_T_STEP_STAGES, MI_T_STEP_ARENA
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's
@@ -447,6 +453,13 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
  * vocabulary, past the cache. Allocates its scratch on the first call (and for a larger chunk). */
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
+/* The single-row step as ONE persistent launch instead of the captured graph of launches
+ * (Engine::replay, src/runtime/engine.cc:702-713, with capture.cc's list run as work-items of
+ * one kernel): on = 1 makes replay(1), generate and ingest use it, on = 0 the graph again.
+ * The first call builds its hand-off words (allocation happens here, not per step). The
+ * results are bitwise the graph's. Dense layers with an f16 cache only (MI_ERR_SHAPE
+ * otherwise). *wgs (may be NULL) receives the work-groups per launch. */
+int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
  * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. */
 int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);

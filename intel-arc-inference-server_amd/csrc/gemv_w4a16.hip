@@ -60,36 +60,13 @@
 
 #include "mi_common.h"
 #include "mi_capi_internal.h"
+#include "gemv_core.h"
 
 namespace mi {
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kCols = 64;
-
-// 8 dequantised int4 weights of one word, in the pair order (q0,q4)(q1,q5)(q2,q6)(q3,q7).
-__device__ __forceinline__ h8_t dequant_word(uint32_t w, uint32_t m_lo, uint32_t m_hi,
-                                             uint32_t magic) {
-  const h2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
-  const h2_t s16 = {(half_t)0.0625f, (half_t)0.0625f};
-  const h2_t b72 = {(half_t)-72.0f, (half_t)-72.0f};
-  const uint32_t t = w >> 8;
-  const h2_t p0 = as_h2(and_or(w, m_lo, magic)) - b1032;                          // 1024+q   -> q-8
-  const h2_t p1 = __builtin_elementwise_fma(as_h2(and_or(w, m_hi, magic)), s16, b72);  // 1024+16q -> q-8
-  const h2_t p2 = as_h2(and_or(t, m_lo, magic)) - b1032;
-  const h2_t p3 = __builtin_elementwise_fma(as_h2(and_or(t, m_hi, magic)), s16, b72);
-  return h8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-}
-
-// 8 natural-order activations (x0..x7 in four u32) into the same pair order.
-__device__ __forceinline__ h8_t perm_x(u4_t v) {
-  const uint32_t a0 = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);  // (x0, x4)
-  const uint32_t a1 = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);  // (x1, x5)
-  const uint32_t a2 = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);  // (x2, x6)
-  const uint32_t a3 = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);  // (x3, x7)
-  const h2_t b0 = as_h2(a0), b1 = as_h2(a1), b2 = as_h2(a2), b3 = as_h2(a3);
-  return h8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
-}
 
 struct GemvEpi {
   uint16_t* resid;        // RESID: [M][N]
@@ -128,20 +105,10 @@ __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t
   return (av > bv) || (av == bv && ai < bi);
 }
 
-constexpr uint32_t kEmpty = 0xFFFFFFFFu;  // a hand-off word with no value yet
-// floats of LDS a consumer polls into per round (16 KB at 16 rows: two slices a round at 2048)
 template <int MR>
 constexpr int fold_buf() { return 2048; }
 constexpr int kFoldBuf_QKV = 2048;
 constexpr uint32_t kPollLimit = 1u << 21; // polls of one word before giving up (~seconds)
-constexpr uint32_t kStatusTimeout = 0xDEAD0003u;  // the status word's value after a wait gave up
-
-__device__ __forceinline__ float empty_f() { return __builtin_bit_cast(float, kEmpty); }
-__device__ __forceinline__ bool is_empty(float v) { return __builtin_bit_cast(uint32_t, v) == kEmpty; }
-// a computed value never goes out with the empty pattern (it stays a NaN)
-__device__ __forceinline__ float publishable(float v) {
-  return is_empty(v) ? __builtin_bit_cast(float, 0x7FC00000u) : v;
-}
 
 // dst[e] = the hand-off word of element e < cnt (cnt <= BUF) once it is not empty; then the
 // word is emptied again. Element e = t + 256 u (t = threadIdx.x) sits at byte offset
