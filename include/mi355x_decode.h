@@ -414,9 +414,10 @@ enum {
   /* activations of the last step of the graph path (diagnostics): the residual [rows][hidden],
    * the normed input x, q fp32 [rows][q_heads][head_dim], the attention output, SwiGLU's output */
   MI_T_RESID, MI_T_X, MI_T_ATTN_Q, MI_T_ATTN_OUT, MI_T_HBUF,
-  /* the persistent step's work-item table and hand-off words (diagnostics; empty before
+  /* the persistent step's work-item table, hand-off words and (with MI_STEP_TRACE set in the
+   * environment when the step is built) per-item start/end times (diagnostics; empty before
    * mi_engine_persistent) */
-  MI_T_STEP_STAGES, MI_T_STEP_ARENA
+  MI_T_STEP_STAGES, MI_T_STEP_ARENA, MI_T_STEP_TRACE
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's

@@ -231,7 +231,7 @@ def desc_27b(max_len=4096 + 512):
  T_Q_NORM, T_K_NORM, T_ROUTER, T_MOE_GU, T_MOE_DN) = range(15)
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_STEP_STAGES,
- T_STEP_ARENA) = range(32, 51)
+ T_STEP_ARENA, T_STEP_TRACE) = range(32, 52)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 

@@ -114,7 +114,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   constexpr uint32_t EB = KV8 ? 1u : 2u, ROWB = HD * EB;  // bytes per row
   constexpr uint32_t VLD = ROWB / 64u;                     // 16-byte V loads per lane (4 lanes per row)
   constexpr uint32_t CW = 16u * EB;                        // bytes of one 16-dim column
-  constexpr bool PF = (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;
+  constexpr bool PF = !PS && (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;  // (the persistent step keeps its registers)
   constexpr uint32_t SV = 16u * ROWB;                      // one wave's staged V group
   constexpr uint32_t RED = 4u * GQA * HD * 4u;             // the end merge's accumulators
   __shared__ __align__(16) unsigned char s_buf[(4u * SV > RED ? 4u * SV : RED)];
@@ -126,7 +126,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   __shared__ __align__(16) uint16_t s_newk[FPN], s_newv[FPN];  // FP: new K/V rows, f16
   __shared__ float s_nrm[FPW];                       // FP: one wave's normed row (RoPE pairs)
 
-  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6;
   const uint32_t qi = lane & 15u, qq = lane >> 4;
   const uint32_t n_act = a.ctrl[CTRL_NACT];
   if (m >= n_act) return;
@@ -321,7 +321,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
     }
     if (a.kv_len && pos + m >= a.kv_len && j == 0 && blk == 0 && t == 0)
       a.ctrl_w[CTRL_DEBUG] = 0xDEAD0002u;  // attn_prep's flag: the row's position is past the cache
-    __syncthreads();
+    lds_barrier();
   }
   if constexpr (PS) {
     // the step's new position, when this block holds it: its K and V rows come from the
@@ -337,7 +337,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
       }
       pn0 = pos;
     }
-    __syncthreads();
+    lds_barrier();
   }
   // q as the MFMA B operand, staged once by wave 0: column qi = head (zero past GQA),
   // k = 32 kk + 8 qq + e; the waves read it from LDS per group rather than holding it
@@ -374,7 +374,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
       s_q[1][kk][lane] = lo;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // this wave's running state for head qi; acc[tt][r] = O^T[16 tt + 4 qq + r][qi]
   float m_run = -INFINITY, l_run = 0.f;

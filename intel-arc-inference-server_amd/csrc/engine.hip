@@ -708,6 +708,7 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_HBUF: *ptr = e->hbuf; b = size_t(m.max_rows) * m.inter * 2; break;
     case MI_T_STEP_STAGES: mi::step_plan_debug(e->step, 0, ptr, &b); break;
     case MI_T_STEP_ARENA: mi::step_plan_debug(e->step, 1, ptr, &b); break;
+    case MI_T_STEP_TRACE: mi::step_plan_debug(e->step, 2, ptr, &b); break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;

@@ -30,6 +30,20 @@ __device__ __forceinline__ h8_t perm_x(u4_t v) {
   return h8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
 }
 
+// Keeps an MFMA source operand's registers intact until every MFMA of the batch that reads it
+// has been issued. Without it the register allocator may give the batch's last MFMA the shared
+// A operand's registers as its destination while the earlier MFMAs of the batch may still be
+// reading them; under register pressure (the persistent step's kernel) that corrupted the
+// middle products of a batch on gfx950.
+__device__ __forceinline__ void keep_mfma_operand(const h8_t& v) { asm volatile("" ::"v"(v)); }
+// The same for a batch of four MFMAs with one A operand: A, every B and every full result stay
+// in their own registers until the batch has been issued, so no destination overlaps a source
+// or another result of the batch.
+__device__ __forceinline__ void keep_mfma_batch(const h8_t& a, const h8_t (&b)[4], const f4_t (&d)[4]) {
+  asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+  asm volatile("" ::"v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]));
+}
+
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;  // a hand-off word with no value yet
 
 __device__ __forceinline__ float empty_f() { return __builtin_bit_cast(float, kEmpty); }

@@ -345,9 +345,12 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
         for (int h = 0; h < 2; ++h) {
           const h8_t a = perm_x(xv[u][h]);
           const uint32_t ws[4] = {wv[u][h].x, wv[u][h].y, wv[u][h].z, wv[u][h].w};
+          h8_t bw[4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-            d[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, dequant_word(ws[c], m_lo, m_hi, magic), d[c], 0, 0, 0);
+          for (int c = 0; c < 4; ++c) bw[c] = dequant_word(ws[c], m_lo, m_hi, magic);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) d[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw[c], d[c], 0, 0, 0);
+          keep_mfma_batch(a, bw, d);
         }
         const float sc[4] = {h2f((uint16_t)(sv[u].x & 0xFFFFu)), h2f((uint16_t)(sv[u].x >> 16)),
                              h2f((uint16_t)(sv[u].y & 0xFFFFu)), h2f((uint16_t)(sv[u].y >> 16))};

@@ -34,6 +34,14 @@ enum : uint32_t {
   CTRL_WORDS = 64
 };
 
+// threadIdx.x as a value the compiler cannot hoist: inside a loop over work-items of different
+// kinds (the persistent step), lane-derived addresses are then recomputed per item instead of
+// being hoisted out of the loop, where every kind's would stay live (and in registers) at once.
+__device__ __forceinline__ uint32_t opaque_tid() {
+  uint32_t v = threadIdx.x;
+  asm volatile("" : "+v"(v));
+  return v;
+}
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(half_t, h); }
 // fp32 -> f16 RNE of an fp32 value that has been rounded to fp32 first. The empty asm
 // pins `f` in a VGPR, so the backend cannot fold the producing multiply or add into a

@@ -111,6 +111,8 @@ struct StepArgs {
   const float* rope;
   uint32_t hidden, vocab, q_heads, kv_heads, rot_dim, max_len, tgt;
   float eps, scale;
+  uint32_t* trace;  // diagnostics (NULL normally): per item its start, end and (slices) the time
+                    // its GEMV was done (s_memrealtime)
 };
 
 struct SliceW {
@@ -123,7 +125,7 @@ struct SliceW {
 __device__ __forceinline__ void slice_load(SliceW& W, const Stage& st, uint32_t i) {
   const uint32_t tiles = st.tiles, N = st.N, gps = st.gps;
   const uint32_t s = i / tiles, tile = i - s * tiles;
-  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, c4 = lane & 15u, q = lane >> 4;
+  const uint32_t lane = opaque_tid() & 63u, wave = opaque_tid() >> 6, c4 = lane & 15u, q = lane >> 4;
   const uint32_t ncol = tile * 64u + 4u * c4;
 #pragma unroll
   for (uint32_t u = 0; u < 2; ++u) {
@@ -133,6 +135,9 @@ __device__ __forceinline__ void slice_load(SliceW& W, const Stage& st, uint32_t 
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) W.w[u][h] = load_stream16(st.qw + (size_t)(g * 8u + 4u * h + q) * N + ncol);
       W.s[u] = *reinterpret_cast<const u2_t*>(st.sc + (size_t)g * N + ncol);
+    } else {  // every register defined: nothing of an older value stays live
+      W.w[u][0] = W.w[u][1] = u4_t{0u, 0u, 0u, 0u};
+      W.s[u] = u2_t{0u, 0u};
     }
   }
 }
@@ -148,7 +153,7 @@ __device__ __forceinline__ void poll_lds(Waiter& wt, const void* base, uint32_t 
   constexpr int kSc1 = 16;
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = opaque_tid();
   uint32_t v[PER];
   uint32_t pending = 0;
 #pragma unroll
@@ -174,12 +179,21 @@ __device__ __forceinline__ void poll_lds(Waiter& wt, const void* base, uint32_t 
     }
 }
 
+// poll_lds over any n: rounds of 2048 elements (8 per thread), element e = 2048 r + t + 256 u
+// at byte offset voff + (8 r + u) * ustride
+__device__ __forceinline__ void poll_lds_n(Waiter& wt, const void* base, uint32_t n, uint32_t voff, uint32_t ustride,
+                                           uint32_t* dst, bool take) {
+  for (uint32_t r0 = 0; r0 < n; r0 += 2048u)
+    poll_lds<8>(wt, static_cast<const unsigned char*>(base) + (size_t)(r0 / 256u) * ustride, n - r0, voff, ustride,
+                dst + r0, take);
+}
+
 // empties this item's share of the stage's many-reader words
 __device__ __forceinline__ void janitor(const Stage& st, uint32_t i) {
   if (!st.jan_words) return;
   const uint32_t per = (st.jan_words + st.count - 1u) / st.count;
   const uint32_t b = i * per, e = min(b + per, st.jan_words);
-  for (uint32_t k = b + threadIdx.x; k < e; k += 256u) st_agent(st.jan + k, kEmpty);
+  for (uint32_t k = b + opaque_tid(); k < e; k += 256u) st_agent(st.jan + k, kEmpty);
 }
 
 struct Lds {
@@ -193,8 +207,8 @@ struct Lds {
 
 // ---- slice items: the GEMV (gemv_w4a16_kernel<1, 2, EPI> at M = 1) and its consumers ----
 __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const SliceW& W, const uint16_t* xrow,
-                                           Lds& L, Waiter& wt) {
-  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, c4 = lane & 15u, q = lane >> 4;
+                                           Lds& L, Waiter& wt, uint32_t& t_mid) {
+  const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6, c4 = lane & 15u, q = lane >> 4;
   const uint32_t tiles = st.tiles, N = st.N, S = st.S, gps = st.gps;
   const uint32_t s = i / tiles, tile = i - s * tiles, n0 = tile * 64u;
   const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
@@ -212,9 +226,12 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
                                 : u4_t{0u, 0u, 0u, 0u};
         const h8_t av = perm_x(xv);
         const uint32_t ws[4] = {W.w[u][h].x, W.w[u][h].y, W.w[u][h].z, W.w[u][h].w};
+        h8_t bw[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          d[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, dequant_word(ws[c], m_lo, m_hi, magic), d[c], 0, 0, 0);
+        for (int c = 0; c < 4; ++c) bw[c] = dequant_word(ws[c], m_lo, m_hi, magic);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) d[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bw[c], d[c], 0, 0, 0);
+        keep_mfma_batch(av, bw, d);
       }
       const float sc[4] = {h2f((uint16_t)(W.s[u].x & 0xFFFFu)), h2f((uint16_t)(W.s[u].x >> 16)),
                            h2f((uint16_t)(W.s[u].y & 0xFFFFu)), h2f((uint16_t)(W.s[u].y >> 16))};
@@ -226,8 +243,9 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
 #pragma unroll
     for (int c = 0; c < 4; ++c) L.red[wave][4u * c4 + c] = acc[c];
   }
-  __syncthreads();
+  lds_barrier();
   const bool consumer = st.epi != SE_NONE && s + 1u == S;  // uniform
+  t_mid = (uint32_t)__builtin_amdgcn_s_memrealtime();
   float v = 0.f;
   if (t < 64u) {
     v = L.red[0][t];
@@ -236,7 +254,7 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
     if (!consumer) st_agent(st.part + (size_t)s * N + n0 + t, publishable(v));
   }
   if (!consumer) {
-    __syncthreads();  // L.red is reused by the next item
+    lds_barrier();  // L.red is reused by the next item
     return;
   }
   // ---- the tile's consumer: fold the other S-1 slices in ascending s, its own last ----
@@ -244,15 +262,15 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
   uint32_t* words = L.words;
   const uint32_t np = (S - 1u) * 64u;
   const float* part = st.part;
-  poll_lds<16>(wt, part, np, ((t >> 6) * N + n0 + (t & 63u)) * 4u, 4u * N * 4u, words, true);
+  poll_lds_n(wt, part, np, ((t >> 6) * N + n0 + (t & 63u)) * 4u, 4u * N * 4u, words, true);
   if (st.epi == SE_RESID) poll_lds<1>(wt, st.resid_in + tile * 32u, 32u, t * 4u, 0u, L.rw, true);
-  __syncthreads();
+  lds_barrier();
   if (t < 64u) {
     float a = 0.f;
     for (uint32_t j = 0; j + 1u < S; ++j) a += __builtin_bit_cast(float, words[j * 64u + t]);
     L.rowv[t] = a + v;
   }
-  __syncthreads();
+  lds_barrier();
   if (st.epi == SE_RESID) {
     // wave 0, a column per lane: the residual, the tile's sum of squares to every consumer's copy
     if (wave == 0) {
@@ -271,13 +289,13 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
     }
     // every tile's sum (this consumer's copy), added in ascending tile order
     poll_lds<1>(wt, st.sumsq + (size_t)tile * tiles, tiles, t * 4u, 0u, words, true);
-    __syncthreads();
+    lds_barrier();
     if (t == 0) {
       float tot = 0.f;
       for (uint32_t g = 0; g < tiles; ++g) tot += __builtin_bit_cast(float, words[g]);
       L.misc[0] = 1.0f / sqrtf(tot / (float)N + L.misc[1]);
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       const uint16_t xb = f2h(L.red[1][lane] * L.misc[0] * st.norm_w[n0 + lane]);
       const uint16_t xb_up = (uint16_t)__shfl((int)xb, (int)(lane + 1u), 64);
@@ -318,7 +336,7 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---- head items: attn_prep's chain on one head (qkv_consumer in gemv_w4a16.hip, M = 1) ----
@@ -326,7 +344,7 @@ template <int HD>
 __device__ __forceinline__ void head_item(const StepArgs& a, const Stage& st, uint32_t hh, uint32_t pos, Lds& L,
                                           Waiter& wt) {
   constexpr uint32_t EPL = HD / 64u;
-  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6;
   const uint32_t QH = a.q_heads, KVH = a.kv_heads, N = st.qkv_n, S = st.S_qkv;
   const bool is_q = hh < QH, is_k = !is_q && hh < QH + KVH;
   const uint32_t h = is_q ? hh : (is_k ? hh - QH : hh - QH - KVH);
@@ -351,14 +369,14 @@ __device__ __forceinline__ void head_item(const StepArgs& a, const Stage& st, ui
   }
   // the fold over all S slices in ascending s from +0
   const float* part = st.part_qkv;
-  poll_lds<16>(wt, part, S * HD, ((t / HD) * N + nh0 + t % HD) * 4u, (256u / HD) * N * 4u, L.words, true);
-  __syncthreads();
+  poll_lds_n(wt, part, S * HD, ((t / HD) * N + nh0 + t % HD) * 4u, (256u / HD) * N * 4u, L.words, true);
+  lds_barrier();
   if (t < HD) {
     float acc = 0.f;
     for (uint32_t j = 0; j < S; ++j) acc += __builtin_bit_cast(float, L.words[j * HD + t]);
     L.fold[t] = acc;
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     const size_t crow = (size_t)pos * HD + (size_t)h * a.max_len * HD;  // row pos of kv head h
     if (!is_q && !is_k) {
@@ -419,14 +437,14 @@ __device__ __forceinline__ void head_item(const StepArgs& a, const Stage& st, ui
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---- merge items: attn_reduce_kernel<false, 64> at M = 1, ungated ----
 template <int HD>
 __device__ __forceinline__ void reduce_item(const StepArgs& a, const Stage& st, uint32_t h, uint32_t pos, Lds& L,
                                             Waiter& wt) {
-  const uint32_t t = threadIdx.x, d = t;
+  const uint32_t t = opaque_tid(), d = t;
   const uint32_t L1 = pos + 1u;
   uint32_t nb = (L1 - 1u) / v2_ppw(L1, a.tgt) + 1u;
   if (nb > a.tgt) nb = a.tgt;
@@ -434,7 +452,7 @@ __device__ __forceinline__ void reduce_item(const StepArgs& a, const Stage& st, 
   float* base = st.attn_part + (size_t)h * a.tgt * PART;  // block b at + b * PART
   // every block's (max, sum)
   poll_lds<1>(wt, base, 2u * nb, ((t >> 1) * (uint32_t)PART + (t & 1u)) * 4u, 0u, L.words, true);
-  __syncthreads();
+  lds_barrier();
   float* fac = L.fold;
   if (t < 64u) {
     float mx = -INFINITY;
@@ -449,7 +467,7 @@ __device__ __forceinline__ void reduce_item(const StepArgs& a, const Stage& st, 
     sm = wave_sum(sm);
     if (t == 0) L.misc[2] = sm;
   }
-  __syncthreads();
+  lds_barrier();
   // the blocks' accumulators, 16 blocks per round, added in ascending block order
   float acc = 0.f;
   if (d < HD) {
@@ -490,12 +508,12 @@ __device__ __forceinline__ void reduce_item(const StepArgs& a, const Stage& st, 
     if (!(d & 1u)) st_agent(st.attn_out + ((size_t)h * HD + d) / 2u, publishable_pair(r, up));
   }
   janitor(st, h);
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---- the first item: embed_gather + the first RMSNorm (embed_norm_kernel<true>, M = 1) ----
 __device__ __forceinline__ void embed_item(const StepArgs& a, Lds& L) {
-  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, H = a.hidden;
+  const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6, H = a.hidden;
   const uint32_t row = a.ctrl[CTRL_CUR];
   const bool bad = row >= a.vocab;  // embed_gather's rule: flag it (the step then embeds zeros)
   if (bad && t == 0) a.ctrl[CTRL_DEBUG] = 0xDEAD0001u;
@@ -521,13 +539,13 @@ __device__ __forceinline__ void embed_item(const StepArgs& a, Lds& L) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (t == 0) {
     float tot = 0.f;
     for (uint32_t c = 0; c < nch; ++c) tot += chunk[c];
     L.misc[3] = 1.0f / sqrtf(tot / (float)H + a.eps);
   }
-  __syncthreads();
+  lds_barrier();
   const float r = L.misc[3];
   for (uint32_t p = t; p < H / 2u; p += 256u) {
     const uint32_t k = 2u * p;
@@ -536,19 +554,19 @@ __device__ __forceinline__ void embed_item(const StepArgs& a, Lds& L) {
     const uint16_t x0 = f2h(h2f(e0) * r * a.norm0[k]), x1 = f2h(h2f(e1) * r * a.norm0[k + 1u]);
     st_agent(a.x0 + p, publishable_pair(x0, x1));
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---- the last item: argmax_stage2 over the head's tile winners, the control block ----
 __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, Lds& L, Waiter& wt) {
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = opaque_tid();
   const uint32_t groups = st.count ? st.tiles : 0u;  // the head GEMV's tiles
   float bv = -INFINITY;
   uint32_t bi = 0x7FFFFFFFu;
   for (uint32_t g0 = 0; g0 < groups; g0 += 2048u) {
     const uint32_t ng = min(2048u, groups - g0);
-    poll_lds<16>(wt, st.am + 2u * g0, 2u * ng, t * 4u, 1024u, L.words, true);
-    __syncthreads();
+    poll_lds_n(wt, st.am + 2u * g0, 2u * ng, t * 4u, 1024u, L.words, true);
+    lds_barrier();
     for (uint32_t g = t; g < ng; g += 256u) {
       const float v = __builtin_bit_cast(float, L.words[2u * g]);
       const uint32_t ix = L.words[2u * g + 1u];
@@ -557,14 +575,14 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
         bi = ix;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   // the comparator is exact, so any reduction order gives argmax_stage2's winner
   float* sv = L.fold;
   uint32_t* si = L.words;
   sv[t] = bv;
   si[t] = bi;
-  __syncthreads();
+  lds_barrier();
   for (uint32_t sst = 128; sst > 0; sst >>= 1) {
     if (t < sst) {
       const float ov = sv[t + sst];
@@ -574,7 +592,7 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
         si[t] = oi;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (t == 0) {
     const uint32_t tok = si[0];
@@ -586,14 +604,14 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
     a.ctrl[CTRL_POS] += 1u;
   }
   janitor(st, 0);
-  __syncthreads();
+  lds_barrier();
 }
 
 template <int HD, int GQA>
-__global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
+__global__ __launch_bounds__(256, 2) void step_kernel(StepArgs a, const Stage* __restrict__ stages) {
   __shared__ __align__(16) uint16_t s_xc[kXcHalves];
   __shared__ Lds L;
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = opaque_tid();
   Waiter wt{__builtin_amdgcn_s_memrealtime() + kTimeoutTicks, a.ctrl + CTRL_DEBUG, false};
   const uint32_t pos = a.ctrl[CTRL_POS];
   if (pos >= a.max_len || a.ctrl[CTRL_NACT] != 1u) {  // nothing to do (the host checks both first)
@@ -607,34 +625,43 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
   uint32_t si = 0;
   const uint32_t P = gridDim.x;
   for (uint32_t j = blockIdx.x; j < a.total; j += P) {
-    while (j >= a.stages[si].first + a.stages[si].count) ++si;
-    const Stage& st = a.stages[si];
+    while (j >= stages[si].first + stages[si].count) ++si;
+    const Stage& st = stages[si];
     const uint32_t i = j - st.first;
     const uint32_t kind = st.kind;
+    const uint32_t t_begin = a.trace ? (uint32_t)__builtin_amdgcn_s_memrealtime() : 0u;
+    // Weights of this work-group's next item (when it is a slice) go out before this item's
+    // waits; an attention item issues them after its own work, so they are not live across it.
+    auto prefetch_next = [&]() {
+      have_next = false;
+      if (j + P < a.total) {
+        uint32_t sn = si;
+        while (j + P >= stages[sn].first + stages[sn].count) ++sn;
+        if (stages[sn].kind == SK_SLICE) {
+          slice_load(wn, stages[sn], j + P - stages[sn].first);
+          have_next = true;
+        }
+      }
+      if (!have_next) wn = SliceW{};
+    };
+    uint32_t t_mid = 0;
     if (kind == SK_SLICE) {
       if (have_next) wc = wn;
       else slice_load(wc, st, i);
-    }
-    // the next item's weights go out now, whatever this item waits for
-    have_next = false;
-    if (j + P < a.total) {
-      uint32_t sn = si;
-      while (j + P >= a.stages[sn].first + a.stages[sn].count) ++sn;
-      if (a.stages[sn].kind == SK_SLICE) {
-        slice_load(wn, a.stages[sn], j + P - a.stages[sn].first);
-        have_next = true;
-      }
+      prefetch_next();
+    } else if (kind != SK_ATTN) {
+      prefetch_next();
     }
     if (kind == SK_SLICE) {
       const uint32_t span = st.gps * 64u;  // halves of K per slice
       if (xc_stage != si) {
         // this stage's first item here: its inputs into LDS, the whole vector or the K ranges
         // of this work-group's items of the stage (slot k = item i + k P)
-        __syncthreads();
+        lds_barrier();
         uint32_t* xw = reinterpret_cast<uint32_t*>(s_xc);
         const uint32_t* xs = st.x;
         if (st.xc_whole) {
-          poll_lds<16>(wt, xs, st.K / 2u, t * 4u, 1024u, xw, false);
+          poll_lds_n(wt, xs, st.K / 2u, t * 4u, 1024u, xw, false);
         } else {
           const uint32_t slots = (st.count - i + P - 1u) / P;
           const uint32_t tiles = st.tiles, half = span / 2u;
@@ -643,13 +670,13 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
             poll_lds<1>(wt, xs + sk * half, half, t * 4u, 0u, xw + k * half, false);
           }
         }
-        __syncthreads();
+        lds_barrier();
         xc_stage = si;
         xc_i0 = i;
       }
       const uint32_t s = i / st.tiles;
       const uint16_t* xrow = st.xc_whole ? s_xc + s * span : s_xc + ((i - xc_i0) / P) * span;
-      slice_item(st, i, wc, xrow, L, wt);
+      slice_item(st, i, wc, xrow, L, wt, t_mid);
     } else if (kind == SK_HEAD) {
       head_item<HD>(a, st, i, pos, L, wt);
     } else if (kind == SK_ATTN) {
@@ -669,7 +696,8 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
       ad.scale = a.scale;
       ad.ps_new = st.newkv;
       attn_block<HD, 0, GQA, false, true>(ad, i / a.tgt, i % a.tgt, 0, &wt);
-      __syncthreads();
+      lds_barrier();
+      prefetch_next();
     } else if (kind == SK_REDUCE) {
       reduce_item<HD>(a, st, i, pos, L, wt);
     } else if (kind == SK_EMBED) {
@@ -677,12 +705,17 @@ __global__ __launch_bounds__(256) void step_kernel(StepArgs a) {
     } else {
       finish_item(a, st, L, wt);
     }
+    if (a.trace && t == 0) {
+      a.trace[3u * j] = t_begin;
+      a.trace[3u * j + 1u] = (uint32_t)__builtin_amdgcn_s_memrealtime();
+      a.trace[3u * j + 2u] = t_mid;
+    }
   }
 }
 
 template <int HD, int GQA>
 int launch_step(const StepArgs& a, uint32_t wgs, hipStream_t st) {
-  step_kernel<HD, GQA><<<wgs, 256, 0, st>>>(a);
+  step_kernel<HD, GQA><<<wgs, 256, 0, st>>>(a, a.stages);
   return (int)hipGetLastError();
 }
 
@@ -715,6 +748,7 @@ struct StepPlan {
   Stage* d_stages = nullptr;
   uint32_t* arena = nullptr;
   size_t arena_words = 0;
+  uint32_t* trace = nullptr;
   StepArgs args{};
   uint32_t wgs = 0;
   LaunchFn launch = nullptr;
@@ -722,6 +756,7 @@ struct StepPlan {
   ~StepPlan() {
     if (d_stages) hipFree(d_stages);
     if (arena) hipFree(arena);
+    if (trace) hipFree(trace);
   }
 };
 
@@ -931,6 +966,10 @@ int step_plan_create(const StepModel& m, hipStream_t st, StepPlan** out) {
   StepArgs& a = p->args;
   a.stages = p->d_stages;
   a.total = first;
+  if (std::getenv("MI_STEP_TRACE")) {  // diagnostics: item start/end times, [items][2] u32
+    if (hipMalloc(&p->trace, (size_t)first * 12) != hipSuccess) return mi_fail(MI_ERR_OOM, "step: trace");
+    a.trace = p->trace;
+  }
   if (const char* env = std::getenv("MI_STEP_STOP")) {  // diagnostics: only the first n stages run
     const long n = std::strtol(env, nullptr, 10);
     if (n > 0 && (size_t)n < S.size()) a.total = S[n].first;
@@ -977,9 +1016,12 @@ void step_plan_debug(const StepPlan* p, uint32_t what, void** ptr, size_t* bytes
   if (what == 0) {
     *ptr = p->d_stages;
     *bytes = p->stages.size() * sizeof(Stage);
-  } else {
+  } else if (what == 1) {
     *ptr = p->arena;
     *bytes = p->arena_words * 4;
+  } else {
+    *ptr = p->trace;
+    *bytes = p->trace ? (size_t)p->args.total * 12 : 0;
   }
 }
 
