@@ -157,12 +157,14 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
 #pragma unroll
       for (uint32_t kk = 0; kk < KK; ++kk) {
         const size_t off = row * a.row_stride + hoff + 32 * kk + 8 * qq;
-        if constexpr (KV8 == 0) g.k[kk].w = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(a.kv_k) + off);
-        else g.k[kk].w = *reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(a.kv_k) + off);
+        if constexpr (KV8 == 0)
+          g.k[kk].w = *as_global(reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(a.kv_k) + off));
+        else
+          g.k[kk].w = *as_global(reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(a.kv_k) + off));
       }
       if constexpr (KV8 == 1) {
-        g.ks = a.k_scale[row * a.sc_row_stride + shoff];
-        g.vs = a.v_scale[row * a.sc_row_stride + shoff];
+        g.ks = *as_global(a.k_scale + row * a.sc_row_stride + shoff);
+        g.vs = *as_global(a.v_scale + row * a.sc_row_stride + shoff);
       }
     } else {
 #pragma unroll
@@ -174,7 +176,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
       const unsigned char* vb = static_cast<const unsigned char*>(a.kv_v) +
                                 (((size_t)rb + vrow) * a.row_stride + hoff) * EB + vpart * (ROWB / 4u);
 #pragma unroll
-      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = *reinterpret_cast<const u4_t*>(vb + 16u * i);
+      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = *as_global(reinterpret_cast<const u4_t*>(vb + 16u * i));
     } else {
 #pragma unroll
       for (uint32_t i = 0; i < VLD; ++i) g.v[i] = u4_t{0u, 0u, 0u, 0u};
@@ -529,7 +531,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
         st_agent(out + 1, publishable(st_hs[g]));
       }
     } else {
-      out[2 + dd] = v;
+      *as_global(out + 2 + dd) = v;
       if (dd == 0) {
         out[0] = st_hm[g];
         out[1] = st_hs[g];

@@ -65,10 +65,21 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t m
   return r;
 }
 
+// A pointer into global memory, typed so: the compiler then emits global_* instructions, which
+// count only in the vector memory counter. Through a generic pointer it emits flat_*, which count
+// in the LDS/scalar counter as well, so every later LDS wait or barrier would also wait for them
+// (for a weight prefetch or a hand-off store still in flight).
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global(T* p) {
+  return (gptr<T>)p;
+}
+
 // Streaming 16-byte load that does not allocate in the caches (weights are read once per
 // token; keeping them out of L2/MALL leaves room for activations and partials).
 __device__ __forceinline__ u4_t load_stream16(const uint32_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
+  return __builtin_nontemporal_load(as_global(reinterpret_cast<const u4_t*>(p)));
 }
 
 // Device-coherent (agent scope) accesses for data that work-groups of one launch hand to
@@ -76,11 +87,11 @@ __device__ __forceinline__ u4_t load_stream16(const uint32_t* p) {
 // coherent across the XCDs' L2s without any cache writeback or invalidate.
 template <typename T>
 __device__ __forceinline__ void st_agent(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(as_global(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
 __device__ __forceinline__ T ld_agent(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Whole-wave reductions on the vector ALUs: a butterfly inside each 16-lane row through DPP
 // lane swaps (quad_perm xor 1, xor 2, half-mirror, mirror), then the four row results via

@@ -61,10 +61,15 @@ enum : uint32_t { SE_NONE = 0, SE_RESID = 1, SE_SILU = 2, SE_LOGITS = 3 };
 
 constexpr uint32_t kXcHalves = 8192;  // the LDS activation cache of a work-group (16 KiB)
 constexpr uint32_t kMaxGps = 8;       // k-groups per slice (two per wave)
+constexpr uint32_t kQuad = 4;         // producer slice items per unit
 constexpr uint64_t kTimeoutTicks = 20000000ull;  // 200 ms of s_memrealtime (100 MHz)
 
 struct Stage {
   uint32_t kind, first, count, epi;
+  // units: what one work-group takes at a time. A slice stage's producer items go in groups of
+  // up to kQuad adjacent tiles of one slice (their weights all in flight at once), its consumer
+  // items one by one; every other stage's items one by one.
+  uint32_t ufirst, units, prod_units, prod_items, ups;  // ups: producer units per slice
   // SK_SLICE: the linear and its split
   const uint32_t* qw;
   const uint16_t* sc;
@@ -100,7 +105,7 @@ struct Stage {
 
 struct StepArgs {
   const Stage* stages;
-  uint32_t total;
+  uint32_t total;  // units
   uint32_t* ctrl;
   uint32_t* history;
   uint32_t history_len;
@@ -111,8 +116,7 @@ struct StepArgs {
   const float* rope;
   uint32_t hidden, vocab, q_heads, kv_heads, rot_dim, max_len, tgt;
   float eps, scale;
-  uint32_t* trace;  // diagnostics (NULL normally): per item its start, end and (slices) the time
-                    // its GEMV was done (s_memrealtime)
+  uint32_t* trace;  // diagnostics (NULL normally): per unit its start and end (s_memrealtime)
 };
 
 struct SliceW {
@@ -134,12 +138,20 @@ __device__ __forceinline__ void slice_load(SliceW& W, const Stage& st, uint32_t 
       const uint32_t g = s * gps + gl;
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) W.w[u][h] = load_stream16(st.qw + (size_t)(g * 8u + 4u * h + q) * N + ncol);
-      W.s[u] = *reinterpret_cast<const u2_t*>(st.sc + (size_t)g * N + ncol);
-    } else {  // every register defined: nothing of an older value stays live
-      W.w[u][0] = W.w[u][1] = u4_t{0u, 0u, 0u, 0u};
-      W.s[u] = u2_t{0u, 0u};
+      W.s[u] = *as_global(reinterpret_cast<const u2_t*>(st.sc + (size_t)g * N + ncol));
     }
   }
+}
+
+struct SliceWQ {
+  SliceW w[kQuad];
+};
+// the weights of a unit's n <= kQuad slice items i0 .. i0 + n - 1, all loads out together in
+// item order
+__device__ __forceinline__ void slice_loadq(SliceWQ& W, const Stage& st, uint32_t i0, uint32_t n) {
+#pragma unroll
+  for (uint32_t k = 0; k < kQuad; ++k)
+    if (k < n) slice_load(W.w[k], st, i0 + k);
 }
 
 // Thread t polls the hand-off words of elements e = t + 256 u < n (u < PER) into dst[e] (LDS):
@@ -198,6 +210,7 @@ __device__ __forceinline__ void janitor(const Stage& st, uint32_t i) {
 
 struct Lds {
   float red[4][64];
+  float redq[kQuad][4][64];  // a producer unit's items
   float fold[2048];
   uint32_t words[4096];  // polled words (consumers, heads, merges, the argmax)
   uint32_t rw[32];       // a RESID consumer's residual tile (f16 pairs)
@@ -206,11 +219,12 @@ struct Lds {
 };
 
 // ---- slice items: the GEMV (gemv_w4a16_kernel<1, 2, EPI> at M = 1) and its consumers ----
-__device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const SliceW& W, const uint16_t* xrow,
-                                           Lds& L, Waiter& wt, uint32_t& t_mid) {
+// One slice of one tile into red[wave][col]: wave w's k-groups w and w + 4 of the slice, each an
+// MFMA batch scaled per column, summed in group order (the launch kernel's per-wave partial).
+__device__ __forceinline__ void slice_gemv(const Stage& st, const SliceW& W, const uint16_t* xrow,
+                                           float (*red)[64]) {
   const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6, c4 = lane & 15u, q = lane >> 4;
-  const uint32_t tiles = st.tiles, N = st.N, S = st.S, gps = st.gps;
-  const uint32_t s = i / tiles, tile = i - s * tiles, n0 = tile * 64u;
+  const uint32_t gps = st.gps;
   const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -241,11 +255,40 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
   }
   if (q == 0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) L.red[wave][4u * c4 + c] = acc[c];
+    for (int c = 0; c < 4; ++c) red[wave][4u * c4 + c] = acc[c];
   }
+}
+
+// A producer unit: items i0 .. i0 + n - 1, adjacent tiles of one slice; each tile's four wave
+// partials summed in wave order (wave k sums item i0 + k) and published as its slice's partial.
+__device__ __forceinline__ void slice_quad(const Stage& st, uint32_t i0, uint32_t n, const SliceWQ& W,
+                                           const uint16_t* xrow, Lds& L) {
+  const uint32_t t = opaque_tid();
+#pragma unroll
+  for (uint32_t k = 0; k < kQuad; ++k)
+    if (k < n) slice_gemv(st, W.w[k], xrow, L.redq[k]);
+  lds_barrier();
+  const uint32_t k = t >> 6, col = t & 63u;
+  if (k < n) {
+    const uint32_t i = i0 + k, s = i / st.tiles, n0 = (i - s * st.tiles) * 64u;
+    float v = L.redq[k][0][col];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += L.redq[k][w][col];
+    st_agent(st.part + (size_t)s * st.N + n0 + col, publishable(v));
+  }
+  lds_barrier();  // L.redq is reused by the next unit
+}
+
+// A single slice item; the consumer slice (S-1) of a fused stage also folds the tile and applies
+// the epilogue.
+__device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const SliceW& W, const uint16_t* xrow,
+                                           Lds& L, Waiter& wt) {
+  const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6;
+  const uint32_t tiles = st.tiles, N = st.N, S = st.S;
+  const uint32_t s = i / tiles, tile = i - s * tiles, n0 = tile * 64u;
+  slice_gemv(st, W, xrow, L.red);
   lds_barrier();
   const bool consumer = st.epi != SE_NONE && s + 1u == S;  // uniform
-  t_mid = (uint32_t)__builtin_amdgcn_s_memrealtime();
   float v = 0.f;
   if (t < 64u) {
     v = L.red[0][t];
@@ -297,7 +340,7 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
     }
     lds_barrier();
     if (wave == 0) {
-      const uint16_t xb = f2h(L.red[1][lane] * L.misc[0] * st.norm_w[n0 + lane]);
+      const uint16_t xb = f2h(L.red[1][lane] * L.misc[0] * *as_global(st.norm_w + n0 + lane));
       const uint16_t xb_up = (uint16_t)__shfl((int)xb, (int)(lane + 1u), 64);
       if (!(lane & 1u)) st_agent(st.x_next + tile * 32u + lane / 2u, publishable_pair(xb, xb_up));
     }
@@ -318,7 +361,7 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
     if (wave == 0) {
       const uint32_t n = n0 + lane;
       const float lv = L.rowv[lane];
-      st.logits[n] = lv;
+      *as_global(st.logits + n) = lv;
       float bv = n < st.vocab_used ? lv : -INFINITY;
       uint32_t bi = n;
 #pragma unroll
@@ -384,7 +427,7 @@ __device__ __forceinline__ void head_item(const StepArgs& a, const Stage& st, ui
 #pragma unroll
       for (uint32_t k = 0; k < EPL; ++k) {
         vb[k] = f2h(L.fold[lane + 64u * k]);
-        st.kv_v[crow + lane + 64u * k] = vb[k];
+        *as_global(st.kv_v + crow + lane + 64u * k) = vb[k];
         const uint16_t up = (uint16_t)__shfl((int)vb[k], (int)(lane + 1u), 64);
         if (!(lane & 1u)) st_agent(st.newkv + (size_t)h * HD + HD / 2u + (lane + 64u * k) / 2u, publishable_pair(vb[k], up));
       }
@@ -430,7 +473,7 @@ __device__ __forceinline__ void head_item(const StepArgs& a, const Stage& st, ui
           st_agent(st.attn_q + (size_t)h * HD + e, publishable(out));
         } else {
           const uint16_t kb = f2h(out);
-          st.kv_k[crow + e] = kb;
+          *as_global(st.kv_k + crow + e) = kb;
           const uint16_t up = (uint16_t)__shfl((int)kb, (int)(lane + 1u), 64);
           if (!(lane & 1u)) st_agent(st.newkv + (size_t)h * HD + e / 2u, publishable_pair(kb, up));
         }
@@ -619,64 +662,61 @@ __global__ __launch_bounds__(256, 2) void step_kernel(StepArgs a, const Stage* _
     return;
   }
   if (t == 0) L.misc[1] = a.eps;
-  uint32_t xc_stage = 0xFFFFFFFFu, xc_i0 = 0;
-  SliceW wc, wn;
-  bool have_next = false;
+  uint32_t xc_stage = 0xFFFFFFFFu, xc_u0 = 0;
   uint32_t si = 0;
   const uint32_t P = gridDim.x;
-  for (uint32_t j = blockIdx.x; j < a.total; j += P) {
-    while (j >= stages[si].first + stages[si].count) ++si;
+  // unit ul of stage `sg` -> its first item and item count
+  auto unit_items = [](const Stage& sg, uint32_t ul, uint32_t& n) -> uint32_t {
+    n = 1u;
+    if (sg.kind != SK_SLICE) return ul;
+    if (ul < sg.prod_units) {
+      const uint32_t s = ul / sg.ups, t0 = (ul - s * sg.ups) * kQuad;
+      n = min(kQuad, sg.tiles - t0);
+      return s * sg.tiles + t0;
+    }
+    return sg.prod_items + (ul - sg.prod_units);
+  };
+  for (uint32_t U = blockIdx.x; U < a.total; U += P) {
+    while (U >= stages[si].ufirst + stages[si].units) ++si;
     const Stage& st = stages[si];
-    const uint32_t i = j - st.first;
+    const uint32_t ul = U - st.ufirst;
+    uint32_t n = 1;
+    const uint32_t i = unit_items(st, ul, n);
     const uint32_t kind = st.kind;
     const uint32_t t_begin = a.trace ? (uint32_t)__builtin_amdgcn_s_memrealtime() : 0u;
-    // Weights of this work-group's next item (when it is a slice) go out before this item's
-    // waits; an attention item issues them after its own work, so they are not live across it.
-    auto prefetch_next = [&]() {
-      have_next = false;
-      if (j + P < a.total) {
-        uint32_t sn = si;
-        while (j + P >= stages[sn].first + stages[sn].count) ++sn;
-        if (stages[sn].kind == SK_SLICE) {
-          slice_load(wn, stages[sn], j + P - stages[sn].first);
-          have_next = true;
-        }
-      }
-      if (!have_next) wn = SliceW{};
-    };
-    uint32_t t_mid = 0;
     if (kind == SK_SLICE) {
-      if (have_next) wc = wn;
-      else slice_load(wc, st, i);
-      prefetch_next();
-    } else if (kind != SK_ATTN) {
-      prefetch_next();
-    }
-    if (kind == SK_SLICE) {
+      // the unit's weights go out first, then (at this work-group's first unit of the stage) its
+      // inputs are polled into LDS while they are on the way
+      SliceWQ W;
+      slice_loadq(W, st, i, n);
       const uint32_t span = st.gps * 64u;  // halves of K per slice
       if (xc_stage != si) {
-        // this stage's first item here: its inputs into LDS, the whole vector or the K ranges
-        // of this work-group's items of the stage (slot k = item i + k P)
+        // the whole input vector, or the K ranges of this work-group's units of the stage (slot
+        // k = unit ul + k P; a unit's items share their slice)
         lds_barrier();
         uint32_t* xw = reinterpret_cast<uint32_t*>(s_xc);
         const uint32_t* xs = st.x;
         if (st.xc_whole) {
           poll_lds_n(wt, xs, st.K / 2u, t * 4u, 1024u, xw, false);
         } else {
-          const uint32_t slots = (st.count - i + P - 1u) / P;
+          const uint32_t slots = (st.units - ul + P - 1u) / P;
           const uint32_t tiles = st.tiles, half = span / 2u;
           for (uint32_t k = 0; k < slots; ++k) {
-            const uint32_t sk = (i + k * P) / tiles;
+            uint32_t nk = 1;
+            const uint32_t sk = unit_items(st, ul + k * P, nk) / tiles;
             poll_lds<1>(wt, xs + sk * half, half, t * 4u, 0u, xw + k * half, false);
           }
         }
         lds_barrier();
         xc_stage = si;
-        xc_i0 = i;
+        xc_u0 = ul;
       }
       const uint32_t s = i / st.tiles;
-      const uint16_t* xrow = st.xc_whole ? s_xc + s * span : s_xc + ((i - xc_i0) / P) * span;
-      slice_item(st, i, wc, xrow, L, wt, t_mid);
+      const uint16_t* xrow = st.xc_whole ? s_xc + s * span : s_xc + ((ul - xc_u0) / P) * span;
+      if (ul >= st.prod_units)
+        slice_item(st, i, W.w[0], xrow, L, wt);
+      else
+        slice_quad(st, i, n, W, xrow, L);
     } else if (kind == SK_HEAD) {
       head_item<HD>(a, st, i, pos, L, wt);
     } else if (kind == SK_ATTN) {
@@ -697,7 +737,6 @@ __global__ __launch_bounds__(256, 2) void step_kernel(StepArgs a, const Stage* _
       ad.ps_new = st.newkv;
       attn_block<HD, 0, GQA, false, true>(ad, i / a.tgt, i % a.tgt, 0, &wt);
       lds_barrier();
-      prefetch_next();
     } else if (kind == SK_REDUCE) {
       reduce_item<HD>(a, st, i, pos, L, wt);
     } else if (kind == SK_EMBED) {
@@ -706,9 +745,8 @@ __global__ __launch_bounds__(256, 2) void step_kernel(StepArgs a, const Stage* _
       finish_item(a, st, L, wt);
     }
     if (a.trace && t == 0) {
-      a.trace[3u * j] = t_begin;
-      a.trace[3u * j + 1u] = (uint32_t)__builtin_amdgcn_s_memrealtime();
-      a.trace[3u * j + 2u] = t_mid;
+      a.trace[2u * U] = t_begin;
+      a.trace[2u * U + 1u] = (uint32_t)__builtin_amdgcn_s_memrealtime();
     }
   }
 }
@@ -857,9 +895,21 @@ int step_plan_create(const StepModel& m, hipStream_t st, StepPlan** out) {
   // ---- the work-item list ----
   std::vector<Stage>& S = p->stages;
   uint32_t first = 0;
+  uint32_t ufirst = 0;
   auto add = [&](Stage s) {
     s.first = first;
     first += s.count;
+    s.units = s.count;
+    if (s.kind == SK_SLICE) {
+      // producer items in units of up to kQuad adjacent tiles of one slice (items are
+      // slice-major), the consumer slice's items one by one
+      s.prod_items = s.epi != SE_NONE ? s.tiles * (s.S - 1) : s.count;
+      s.ups = (s.tiles + kQuad - 1) / kQuad;
+      s.prod_units = (s.prod_items / s.tiles) * s.ups;
+      s.units = s.prod_units + (s.count - s.prod_items);
+    }
+    s.ufirst = ufirst;
+    ufirst += s.units;
     S.push_back(s);
     return &S.back();
   };
@@ -877,8 +927,10 @@ int step_plan_create(const StepModel& m, hipStream_t st, StepPlan** out) {
     s.count = s.tiles * l.S;
     s.x = x;
     s.part = part;
-    // the work-group's K ranges when they take less LDS than the whole vector
-    const size_t ranges = (size_t)((s.count + wgs - 1) / wgs) * s.gps * 64;
+    // the work-group's K ranges (one per unit) when they take less LDS than the whole vector
+    const uint32_t ups = (s.tiles + kQuad - 1) / kQuad;
+    const uint32_t units = epi != SE_NONE ? (l.S - 1) * ups + s.tiles : l.S * ups;
+    const size_t ranges = (size_t)((units + wgs - 1) / wgs) * s.gps * 64;
     s.xc_whole = (ranges > kXcHalves || ranges >= K) ? 1u : 0u;
     return s;
   };
@@ -965,14 +1017,14 @@ int step_plan_create(const StepModel& m, hipStream_t st, StepPlan** out) {
 
   StepArgs& a = p->args;
   a.stages = p->d_stages;
-  a.total = first;
+  a.total = ufirst;
   if (std::getenv("MI_STEP_TRACE")) {  // diagnostics: item start/end times, [items][2] u32
-    if (hipMalloc(&p->trace, (size_t)first * 12) != hipSuccess) return mi_fail(MI_ERR_OOM, "step: trace");
+    if (hipMalloc(&p->trace, (size_t)ufirst * 8) != hipSuccess) return mi_fail(MI_ERR_OOM, "step: trace");
     a.trace = p->trace;
   }
   if (const char* env = std::getenv("MI_STEP_STOP")) {  // diagnostics: only the first n stages run
     const long n = std::strtol(env, nullptr, 10);
-    if (n > 0 && (size_t)n < S.size()) a.total = S[n].first;
+    if (n > 0 && (size_t)n < S.size()) a.total = S[n].ufirst;
   }
   a.ctrl = m.ctrl;
   a.history = m.history;
@@ -1021,7 +1073,7 @@ void step_plan_debug(const StepPlan* p, uint32_t what, void** ptr, size_t* bytes
     *bytes = p->arena_words * 4;
   } else {
     *ptr = p->trace;
-    *bytes = p->trace ? (size_t)p->args.total * 12 : 0;
+    *bytes = p->trace ? (size_t)p->args.total * 8 : 0;
   }
 }
 
