@@ -125,8 +125,8 @@ typedef struct mi_gemv_epilogue {
   /* QKV (N = shape->qkv_n, M <= 4, not gated, head_dim 128 or 256): mi_attn_prep on the
    * folded q||k||v row in the same launch - q/k RMSNorm, RoPE, q -> attn_q fp32
    * [M][q_heads][head_dim], K/V f16 at the cache row of position pos + m (the arguments of
-   * mi_attn_prep, whose output this is bit for bit). The launch takes S slices plus one
-   * consumer work-group per head; partials[0 .. S*M*N) are its hand-off words. */
+   * mi_attn_prep, whose output this is bit for bit). Without `arrive` the launch takes S
+   * slices plus one consumer work-group per head; partials[0 .. S*M*N) are its hand-off words. */
   uint32_t* ctrl;
   const struct mi_attn_shape* shape;
   const float* q_norm;
@@ -144,14 +144,21 @@ typedef struct mi_gemv_epilogue {
    * empty NaN as the value and sets *status = MI_STATUS_HANDOFF_TIMEOUT (status may be NULL).
    * The output of such a launch is not to be used, and the hand-off words may then hold
    * values published late: run mi_gemv_handoff_init on them before the next fused launch.
-   * (The waits complete because every XCD dispatches its share of the grid in order and the
-   * consumers are the grid's last row: all producers are resident or finished before a
-   * consumer waits; RESID's consumers also need all N/64 of them resident at once.)
    * inject: fault injection for tests of that path, 0 in normal use; bit 0 = the producer
-   * work-groups publish nothing, so every consumer's wait times out. */
+   * work-groups publish nothing, so every consumer's wait times out.
+   * arrive: NULL, or a device array of uint32 arrival counts, zero before the first launch
+   * (hipMemset, or mi_memcpy_h2d of zeros): one count per tile (QKV: per head) every 32
+   * words (128 bytes), so 32 * N/64 words, which every launch leaves at zero; launches that
+   * may run at the same time need separate arrays. With it the slice that completes a tile
+   * (a head) is that tile's consumer, so no wait depends on the dispatch order (each
+   * producer then waits for one atomic's round trip before it exits). Without it slice S-1
+   * (QKV: one extra row of work-groups) is, and the waits complete because every XCD
+   * dispatches its share of the grid in order and those consumers are the grid's last row.
+   * RESID's consumers also need all N/64 of them resident at once, either way. */
   uint32_t* status;
   uint32_t poll_limit;
   uint32_t inject;
+  uint32_t* arrive;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,

@@ -108,7 +108,8 @@ class GemvEpilogue(C.Structure):
                 ("argmax_part", vp), ("vocab_used", u32), ("out16", vp),
                 ("ctrl", vp), ("shape", vp), ("q_norm", vp), ("k_norm", vp), ("rope", vp), ("attn_q", vp),
                 ("kv_k", vp), ("kv_v", vp), ("row_stride", sz), ("head_stride", sz), ("pages", vp),
-                ("page", u32), ("kv_len", u32), ("status", vp), ("poll_limit", u32), ("inject", u32)]
+                ("page", u32), ("kv_len", u32), ("status", vp), ("poll_limit", u32), ("inject", u32),
+                ("arrive", vp)]
 
 
 STATUS_HANDOFF_TIMEOUT = 0xDEAD0003

@@ -100,6 +100,12 @@ struct mi_engine {
   float* part_ex = nullptr;  // the fused launches' hand-off words (empty between launches)
   float* sumsq = nullptr;    // RESID's hand-off words for the tiles' sums of squares
   size_t part_ex_n = 0, sumsq_n = 0;
+  uint32_t* arrive = nullptr;  // the fused launches' arrival counts (zero between launches)
+  size_t arrive_n = 0;
+  // last-arriver consumers (mi_gemv_epilogue.arrive): measured slower on MI355X than the
+  // fixed last-row consumers (27B step 4.79 vs 4.34 ms: every producer then waits for an
+  // atomic's round trip before it exits), so the engine keeps the fixed ones
+  bool use_arrive = false;
   float* attn_q = nullptr;
   float* attn_part = nullptr;
   float* logits = nullptr;
@@ -196,11 +202,11 @@ struct mi_engine {
       }
       if (L.qkv.q) part_max = std::max(part_max, size_t(L.qkv.S) * R * L.qkv.N);
       for (const Linear* l : {&L.o, &L.gate_up, &L.down})
-        if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S - 1) * R * l->N);
+        if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S) * R * l->N);
       part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(R, 4u) * L.qkv.N);  // QKV: all S slices
     }
     MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
-    part_ex_max = std::max(part_ex_max, size_t(lm_head.S - 1) * R * m.vocab);
+    part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * R * m.vocab);
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
     MI_TRY(alloc(&final_norm, H));
     MI_TRY(alloc(&rope, size_t(m.max_len) * m.rot_dim));
@@ -229,6 +235,9 @@ struct mi_engine {
     sumsq_n = size_t(H / 64) * R * (H / 64);
     MI_TRY(alloc(&sumsq, sumsq_n));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
+    arrive_n = 32 * std::max<size_t>({m.vocab / 64, 2 * m.inter / 64, qkv_n / 64, H / 64});
+    MI_TRY(alloc(&arrive, arrive_n));
+    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
     MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
     MI_TRY(alloc(&attn_part, size_t(QH) * m.attn_tgt * R * (HD + 2)));
     MI_TRY(alloc(&logits, size_t(R) * m.vocab));
@@ -307,6 +316,7 @@ struct mi_engine {
     e.x_next = x;
     e.eps = d.rms_eps;
     e.status = ctrl + MI_CTRL_DEBUG;
+    e.arrive = use_arrive ? arrive : nullptr;
     return e;
   }
 
@@ -338,6 +348,7 @@ struct mi_engine {
         eq.head_stride = size_t(d.max_len) * HD;
         eq.kv_len = d.max_len;
         eq.status = ctrl + MI_CTRL_DEBUG;
+        eq.arrive = use_arrive ? arrive : nullptr;
         MI_TRY(mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream));
       } else {
         MI_TRY(gemv(L.qkv, x, M));
@@ -383,6 +394,7 @@ struct mi_engine {
       eg.kind = MI_EPI_SILU;
       eg.h = hbuf;
       eg.status = ctrl + MI_CTRL_DEBUG;
+      eg.arrive = use_arrive ? arrive : nullptr;
       MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                               stream));
       const mi_gemv_epilogue ed = resid_epi(next_w);
@@ -394,6 +406,7 @@ struct mi_engine {
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
     el.status = ctrl + MI_CTRL_DEBUG;
+    el.arrive = use_arrive ? arrive : nullptr;
     MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
     MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
     return 0;
@@ -467,6 +480,7 @@ struct mi_engine {
     if (c[MI_CTRL_DEBUG] != MI_STATUS_HANDOFF_TIMEOUT) return 0;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
+    MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
     if (step) MI_TRY(mi::step_plan_reset(step, stream));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
     MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
@@ -610,6 +624,7 @@ struct mi_engine {
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
     el.status = ctrl + MI_CTRL_DEBUG;
+    el.arrive = use_arrive ? arrive : nullptr;
     MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, pf_x + size_t(T - 1) * d.hidden, part_ex, 1, lm_head.K, lm_head.N,
                             lm_head.S, &el, stream));
     MI_TRY(set_rows(pos0 + n - 1, 1, nullptr, 0));

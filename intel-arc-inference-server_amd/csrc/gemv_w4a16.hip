@@ -29,10 +29,9 @@
 // rows - every output element is its own MFMA dot and the same fixed merges - so S and
 // the wave split are functions of the shape only (mi_gemv_pick_s).
 //
-// Fused epilogues (mi_gemv_w4a16_ex). Slice S-1 of each 64-column tile is its consumer:
-// the other slices write their partials and exit, and the consumer, dispatched after all of
-// them, folds the tile's S partials in ascending s (the consumer's fold of gemv.cl:1-10; its
-// own slice is the last term and never leaves LDS) and applies the step's next operation:
+// Fused epilogues (mi_gemv_w4a16_ex). One work-group per 64-column tile is its consumer: it
+// folds the tile's S partials in ascending s (the consumer's fold of gemv.cl:1-10) and applies
+// the step's next operation:
 //   RESID   resid = rne(resid + rne(sum_s part)) and the tile's sum of squares (the
 //           reference's res_fold at 64-element chunks, prep_ref.h:120-156); every consumer
 //           then sums all tiles' sums in ascending tile order, forms rstd = 1/sqrt(sum / N +
@@ -43,18 +42,24 @@
 //   LOGITS  fp32 logits and the tile's (max, lowest index) for argmax_stage2
 //           (argmax.cl:63-65's comparator; the vocab_used mask);
 //   F16OUT  the fold rounded to fp16.
-// Hand-off without counters or fences: the hand-off words (partials; RESID's per-consumer
-// copies of the tile sums) hold the empty pattern 0xFFFFFFFF between launches - a NaN that
-// fp32 arithmetic on fp16 data never produces (a computed value with those bits is stored as
-// the canonical NaN). Producers store with device-coherent (sc1) single-word stores and
-// exit without waiting; a consumer polls each word with device-coherent loads until it is
-// not empty, then writes the empty pattern back, so every launch leaves the words as it
-// found them. A polled word is either empty or final, so no ordering between words is
-// needed. Deadlock freedom: each XCD dispatches its share of the grid in linear order and
-// the consumers are the grid's last row, so every producer is resident or done before a
-// consumer on its XCD waits; RESID's consumers also wait on each other, which needs all N/64
-// of them resident at once (N <= 16384: at most 256 work-groups). A bounded poll ends a
-// wait that never completes with the empty NaN in the result instead of a hang.
+// Hand-off words: the partials (and RESID's per-consumer copies of the tile sums) hold the
+// empty pattern 0xFFFFFFFF between launches - a NaN that fp32 arithmetic on fp16 data never
+// produces (a computed value with those bits is stored as the canonical NaN). Producers store
+// with device-coherent (sc1) single-word stores; a consumer polls each word with
+// device-coherent loads until it is not empty, then writes the empty pattern back, so every
+// launch leaves the words as it found them. A polled word is either empty or final, so no
+// ordering between words is needed.
+// Who consumes. With an arrival array (epi.arrive, zero between launches) every slice
+// publishes its partial and then counts itself in with one atomic add on its tile's word
+// (QKV: its head's word); the work-group that arrives last is the consumer and sets the word
+// back to zero. No work-group waits for another one that may not have started, whatever the
+// dispatch order: the consumer's polls only cover words already stored (or about to land).
+// Without it, slice S-1 of each tile is the consumer and keeps its own slice in LDS: each XCD
+// dispatches its share of the grid in linear order and the consumers are the grid's last row,
+// so every producer is resident or done before a consumer on its XCD waits. Either way
+// RESID's consumers also wait on each other, which needs all N/64 of them resident at once
+// (N <= 16384: at most 256 work-groups). A bounded poll ends a wait that never completes
+// with the empty NaN in the result instead of a hang.
 // No float atomics: replays stay bitwise identical.
 #include <algorithm>
 
@@ -96,7 +101,26 @@ struct GemvEpi {
   uint32_t* status;
   uint32_t poll_limit;  // polls of one word before giving up
   uint32_t inject;      // fault injection for tests: bit 0 = producers publish nothing
+  uint32_t* arrive;     // per-tile (QKV: per-head) arrival counts, zero between launches; NULL:
+                        // the fixed consumers (slice S-1; QKV's extra row)
 };
+
+// arrival words sit 128 bytes apart: no two tiles' counts share a cache line
+constexpr uint32_t kArriveStride = 32;
+
+// One atomic add on an arrival word by thread 0 after the work-group's partial stores; true
+// (uniform) in the work-group that completes the count `need`, which sets the word back to 0.
+__device__ __forceinline__ bool arrive_last(uint32_t* word, uint32_t need, uint32_t* s_flag) {
+  lds_barrier();  // every thread's partial stores are issued (not waited for)
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1u == need;
+    if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last;
+  }
+  lds_barrier();
+  return *s_flag != 0u;
+}
 
 enum { EPI_PARTIALS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_LOGITS = 3, EPI_F16OUT = 4, EPI_QKV = 5 };
 
@@ -301,9 +325,10 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   const uint32_t n0 = blockIdx.x * kCols;
   const uint32_t ncol = n0 + 4u * c4;
   const uint32_t s = blockIdx.y;
+  const bool dyn = EPI != EPI_PARTIALS && epi.arrive != nullptr;  // last-arriver consumers
   const uint32_t g_begin = s * gps + wave;
-  // QKV's consumer row (s = S) has no slice of its own
-  const uint32_t g_end = (EPI == EPI_QKV && s + 1 == gridDim.y) ? 0u : (s + 1) * gps;
+  // QKV's fixed consumer row (s = S) has no slice of its own
+  const uint32_t g_end = (EPI == EPI_QKV && !dyn && s + 1 == gridDim.y) ? 0u : (s + 1) * gps;
   const bool xrow = c4 < M;  // this lane feeds activation row c4 of the A operand
 
   const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, magic = 0x64006400u;
@@ -372,9 +397,10 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     }
   }
   __syncthreads();
+  __shared__ uint32_t s_last;
+  __shared__ float s_qfold[EPI == EPI_QKV ? kFoldBuf_QKV : 1];
   if constexpr (EPI == EPI_QKV) {
-    if (s + 1 == gridDim.y) {  // the consumer row (uniform)
-      __shared__ float s_qfold[kFoldBuf_QKV];
+    if (!dyn && s + 1 == gridDim.y) {  // the fixed consumer row (uniform)
       if (epi.head_dim == 128)
         qkv_consumer<128>(partials, M, N, gridDim.y - 1, blockIdx.x, epi, s_qfold);
       else
@@ -384,7 +410,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   }
   const uint32_t total = M * kCols;
   const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
-  const bool consumer = EPI != EPI_PARTIALS && EPI != EPI_QKV && s + 1 == S;
+  const bool consumer = EPI != EPI_PARTIALS && EPI != EPI_QKV && !dyn && s + 1 == S;
   for (uint32_t i = threadIdx.x; i < total; i += 256u) {
     const uint32_t row = i / kCols, col = i % kCols;
     float v = red[0][row][col];
@@ -397,8 +423,24 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     else if (!(epi.inject & 1u))
       st_agent(partials + ((size_t)s * M + row) * N + n0 + col, publishable(v));
   }
-  if constexpr (EPI == EPI_QKV) return;
-  if (!consumer) return;
+  if constexpr (EPI == EPI_QKV) {
+    if (dyn) {  // the head's last arriving tile-slice runs the head's consumer
+      const uint32_t tph = epi.head_dim / kCols, hh = tile / tph;
+      if (arrive_last(epi.arrive + hh * kArriveStride, S * tph, &s_last)) {
+        if (epi.head_dim == 128)
+          qkv_consumer<128>(partials, M, N, S, hh * tph + tph - 1u, epi, s_qfold);
+        else
+          qkv_consumer<256>(partials, M, N, S, hh * tph + tph - 1u, epi, s_qfold);
+      }
+    }
+    return;
+  }
+  if (dyn) {
+    if (!arrive_last(epi.arrive + tile * kArriveStride, S, &s_last)) return;
+  } else if (!consumer) {
+    return;
+  }
+  const uint32_t npoll = dyn ? S : S - 1u;  // slices to poll (the fixed consumer holds S-1)
 
   // ---- the tile's consumer folds the S partials and applies the epilogue ----
   // RESID: the residual and the next norm's weights for rows wave, wave + 4, ... (at most 4
@@ -417,16 +459,16 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   __shared__ float s_fold[kFoldBuf];
   const uint32_t t = threadIdx.x;
   {
-    // sum_s partials[s][row][n] from 0.f in ascending s; slices 0 .. S-2 are polled in rounds
-    // of `per_round` slices, slice S-1 is this work-group's own (red[0])
+    // sum_s partials[s][row][n] from 0.f in ascending s, polled in rounds of `per_round`
+    // slices (the fixed consumer's own slice S-1 is the last term, from red[0])
     // (thread t folds elements t + 256 u of the tile's M x 64)
     constexpr int EL = MR * kCols / 256 > 0 ? MR * kCols / 256 : 1;
     const uint32_t per_round = kFoldBuf / total;
     float a[EL];
 #pragma unroll
     for (int u = 0; u < EL; ++u) a[u] = 0.f;
-    for (uint32_t s0 = 0; s0 + 1 < S; s0 += per_round) {
-      const uint32_t ns = min(per_round, S - 1 - s0);
+    for (uint32_t s0 = 0; s0 < npoll; s0 += per_round) {
+      const uint32_t ns = min(per_round, npoll - s0);
       // element e: row-slice e / 64 of slices s0.., column e % 64 (e / 64 = t / 64 + 4 u)
       poll_into<kFoldBuf>(s_fold, ns * total, partials + (size_t)s0 * M * N,
                           ((t / kCols) * N + n0 + t % kCols) * 4u, 4u * N * 4u, epi.status, epi.poll_limit);
@@ -442,7 +484,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
 #pragma unroll
     for (int u = 0; u < EL; ++u) {
       const uint32_t i = t + 256u * u;
-      if (i < total) red[0][i / kCols][i % kCols] = a[u] + red[0][i / kCols][i % kCols];
+      if (i < total) red[0][i / kCols][i % kCols] = dyn ? a[u] : a[u] + red[0][i / kCols][i % kCols];
     }
     __syncthreads();
   }
@@ -544,7 +586,8 @@ template <int MR, int EPI>
 int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part, uint32_t M,
                 uint32_t K, uint32_t N, uint32_t S, const GemvEpi& epi, hipStream_t st) {
   const uint32_t G = K / 64, gps = G / S;
-  dim3 grid(N / kCols, EPI == EPI_QKV ? S + 1 : S);  // QKV: one more row, the heads' consumers
+  // QKV with fixed consumers: one more row, the heads' consumers
+  dim3 grid(N / kCols, EPI == EPI_QKV && !epi.arrive ? S + 1 : S);
   if (gps >= 16)
     gemv_w4a16_kernel<MR, 4, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, epi);
   else
@@ -630,6 +673,7 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   e.status = ep->status;
   e.poll_limit = ep->poll_limit ? ep->poll_limit : kPollLimit;
   e.inject = ep->inject;
+  e.arrive = ep->arrive;
   int r;
   switch (ep->kind) {
     case MI_EPI_PARTIALS:

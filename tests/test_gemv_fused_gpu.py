@@ -2,7 +2,10 @@
 embed + first norm, against the separate-kernel chain they replace, bit for bit on the
 same partials: prep_res_fold at 64-element chunks + prep_norm_finish, prep_silu_mul,
 the lm_head fold + argmax (tests/kernels/prep_test.cc, argmax_test.cc's bars). Every
-launch must leave its hand-off words empty again, so a replay gives the same bits."""
+launch must leave its hand-off words empty again, so a replay gives the same bits.
+Each test runs twice: with the fixed consumers (slice S-1, QKV's extra row) and with an
+arrival array (the last slice to arrive consumes), which must give the same bits and leave
+the array at zero."""
 import ctypes as C
 
 import numpy as np
@@ -36,6 +39,28 @@ def handoff(n):
 def all_empty(d, n=None):
     h = host(d, np.uint32).ravel()
     return bool(np.all(h[:n] == EMPTY))
+
+
+MODE = {"consumers": "fixed"}
+
+
+@pytest.fixture(autouse=True, params=["fixed", "arrive"])
+def consumers(request):
+    MODE["consumers"] = request.param
+    yield request.param
+    MODE["consumers"] = "fixed"
+
+
+def launch_ex(dq, ds, dx, dpart, M, K, N, S, ep):
+    """mi_gemv_w4a16_ex with this test's consumer mode; the arrival words must end at zero"""
+    arr = None
+    if MODE["consumers"] == "arrive":
+        arr = dev(np.zeros(32 * (N // 64 + 1), np.uint32))
+        ep.arrive = ptr(arr)
+    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    if arr is not None:
+        sync()
+        assert not host(arr, np.uint32).any(), "arrival words not back at zero"
 
 
 def partials_of(dq, ds, dx, M, K, N, S):
@@ -80,7 +105,7 @@ def test_resid_epilogue_bitwise(M, S, K, N):
     for rep in range(2):  # a replay must find the hand-off words empty again
         if rep:
             dr.copy_(dev(resid))
-        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
         sync()
         assert all_empty(dpart) and all_empty(dss)
         assert np.array_equal(host(dr, np.uint16), r_ref)
@@ -99,7 +124,7 @@ def test_silu_epilogue(M, S):
     dh = empty((M, I), np.uint16)
     dpart = handoff(S * M * N)
     ep = mi.GemvEpilogue(mi.EPI_SILU, None, None, None, None, None, 0.0, ptr(dh), None, None, 0)
-    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
     sync()
     assert all_empty(dpart)
     got = host(dh, np.uint16)
@@ -122,7 +147,7 @@ def test_logits_epilogue_and_argmax(M):
     dap = empty((M * (V // 64) * 2,), np.uint32)
     dpart = handoff(S * M * V)
     ep = mi.GemvEpilogue(mi.EPI_LOGITS, None, None, None, None, None, 0.0, None, ptr(dl), ptr(dap), used)
-    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, V, S, C.byref(ep), stream())
+    launch_ex(dq, ds, dx, dpart, M, K, V, S, ep)
     c = np.zeros(64, np.uint32)
     c[1] = M
     ctrl = dev(c)
@@ -154,7 +179,7 @@ def test_f16out_epilogue_is_gemv_then_fold(M, S):
     dpart = handoff(S * M * N)
     ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, out16=ptr(out))
     for _ in range(2):  # the hand-off words are empty again: a second launch gives the same bits
-        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
         sync()
         assert all_empty(dpart)
         assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want))
@@ -177,7 +202,7 @@ def test_launches_share_handoff_words():
             want = want + part[s_]
         out = empty((1, n), np.uint16)
         ep = mi.GemvEpilogue(kind=mi.EPI_F16OUT, out16=ptr(out))
-        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), 1, k, n, S, C.byref(ep), stream())
+        launch_ex(dq, ds, dx, dpart, 1, k, n, S, ep)
         sync()
         assert all_empty(dpart), i
         assert np.array_equal(host(out, np.uint16), O.f32_to_f16_bits(want)), i
@@ -227,7 +252,7 @@ def test_qkv_epilogue_is_gemv_then_attn_prep(QH, KVH, HD, rot, M, n_act, paged, 
                              q_norm=pnorm[0], k_norm=pnorm[1], rope=pnorm[2], attn_q=ptr(aq2), kv_k=ptr(k2),
                              kv_v=ptr(v2), row_stride=HD, head_stride=Lm * HD, pages=pnorm[3],
                              page=P if paged else 0, kv_len=Lm)
-        mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+        launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
         sync()
         assert all_empty(dpart)
         assert np.array_equal(host(aq2, np.uint32), host(aq1, np.uint32)), rep
@@ -254,7 +279,7 @@ def test_qkv_epilogue_past_the_cache():
     ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(dc), shape=C.cast(C.pointer(sh), C.c_void_p), rope=ptr(rope),
                          attn_q=ptr(aq), kv_k=ptr(k2), kv_v=ptr(v2), row_stride=128, head_stride=Lm * 128,
                          kv_len=Lm)
-    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), 1, K, N, S, C.byref(ep), stream())
+    launch_ex(dq, ds, dx, dpart, 1, K, N, S, ep)
     sync()
     assert all_empty(dpart)
     assert host(dc, np.uint32)[18] == 0xDEAD0002
@@ -315,7 +340,7 @@ def test_handoff_timeout_sets_the_status_word(kind):
         ep = mi.GemvEpilogue(kind=mi.EPI_SILU, h=ptr(dout))
     ep.status, ep.poll_limit, ep.inject = ptr(status), 64, 1
     print(f"handoff timeout {kind}: injected launch", flush=True)
-    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
     sync()
     assert int(host(status, np.uint32)[0]) == mi.STATUS_HANDOFF_TIMEOUT
     assert all_empty(dpart)
@@ -327,7 +352,7 @@ def test_handoff_timeout_sets_the_status_word(kind):
     if kind == "resid":
         dr.copy_(dev(resid))
     print(f"handoff timeout {kind}: normal launch", flush=True)
-    mi.call("mi_gemv_w4a16_ex", ptr(dq), ptr(ds), ptr(dx), ptr(dpart), M, K, N, S, C.byref(ep), stream())
+    launch_ex(dq, ds, dx, dpart, M, K, N, S, ep)
     sync()
     assert int(host(status, np.uint32)[0]) == 0
     if kind == "resid":
