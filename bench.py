@@ -517,7 +517,7 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
-    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg5", "prefill", "moe_prefill"], default=None,
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill"], default=None,
                     help="run only that secondary measurement and print its JSON (the command the "
                          "attention and single-GEMV kernel profiles use)")
     args = ap.parse_args()
@@ -529,6 +529,21 @@ def main():
         eng = mi.Engine(mi.desc_27b(max_len=2112), seed=args.seed)
         print(json.dumps({"prefill": measure_prefill(eng)}), flush=True)
         eng.close()
+        return
+    if args.only == "cfg4" and args.eager:
+        # the configs[3] MoE decode step enqueued kernel by kernel (the MoE kernel profiles'
+        # command): `--steps` steps at context `--context`
+        eng = mi.Engine(mi.desc_moe_cfg4(max_len=((args.context + 64 + 1 + 63) // 64) * 64), seed=args.seed + 1)
+        eng.reset(args.context, 1000)
+        for _ in range(max(args.steps, 1)):
+            eng.step_eager(1)
+        mi.check(mi.lib().mi_device_sync())
+        assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+        eng.close()
+        print(json.dumps({"cfg4_eager_steps": args.steps}), flush=True)
+        return
+    if args.only == "cfg4":
+        print(json.dumps({"cfg4_moe_step": measure_cfg4(args)}), flush=True)
         return
     if args.only == "moe_prefill":
         # the configs[3] MoE model's chunked prefill of a 2048-token prompt, three timed calls
