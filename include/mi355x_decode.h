@@ -386,25 +386,6 @@ int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_
                    uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t* list, uint32_t* tiles,
                    uint32_t* tiles_n, uint16_t* h, uint16_t* d, void* stream);
 
-/* The whole MoE block of ONE decode row in one launch: mi_gemv_f16w (ksplit) -> mi_moe_route ->
- * mi_moe_gate_up -> mi_moe_down -> mi_norm_rows, with the same values bit for bit (resid updated
- * in place, x_next = the next RMSNorm of it, rstd[0], and route_out, when not NULL, the route
- * row). The stages hand their values to each other through `work`, a device array of
- * mi_moe_block_work_words(...) words prepared once by mi_moe_block_work_init (every launch
- * leaves it as it found it; launches that may run at the same time need separate arrays). A
- * wait that gives up after about 200 ms sets *status = MI_STATUS_HANDOFF_TIMEOUT (status may be
- * NULL): the output is then not to be used and `work` must be prepared again. No reference
- * counterpart as one entry: it fuses the decode list of moe.cl:1-13 (the reference's five
- * kernels of the block, src/runtime/capture.cc's MoE layer) into one launch. */
-size_t mi_moe_block_work_words(uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
-                               uint32_t router_n, uint32_t ksplit);
-int mi_moe_block_work_init(uint32_t* work, size_t words, void* stream);
-int mi_moe_block(const uint16_t* router_w, const uint16_t* x, const uint32_t* gu_blocks,
-                 const uint32_t* dn_blocks, uint16_t* resid, const float* next_norm_w, uint16_t* x_next,
-                 float* rstd, float eps, uint32_t experts, uint32_t top_k, uint32_t hidden,
-                 uint32_t inter, uint32_t router_n, uint32_t ksplit, uint32_t* route_out,
-                 uint32_t* work, uint32_t* status, void* stream);
-
 /* ---- the decode loop (src/runtime/engine.h:52-331, capture.cc, control.h) ----
  * Model shape as data (model::ModelDesc, src/model/model_desc.h:67-229), restricted to the
  * GQA decoders this build runs: every layer is attention + a SwiGLU MLP (int4 g64 layout 0)

@@ -95,9 +95,6 @@ SIGNATURES = {
     "mi_moe_route": (i32, [vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_gate_up": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "mi_moe_down": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
-    "mi_moe_block_work_words": (sz, [u32, u32, u32, u32, u32, u32]),
-    "mi_moe_block_work_init": (i32, [vp, sz, vp]),
-    "mi_moe_block": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, f32, u32, u32, u32, u32, u32, u32, vp, vp, vp, vp]),
 }
 
 

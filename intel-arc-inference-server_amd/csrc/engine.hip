@@ -114,8 +114,6 @@ struct mi_engine {
   float* moe_logits = nullptr;   // [max_rows][router_n]
   uint32_t* moe_route = nullptr; // [max_rows][MI_MOE_ROUTE_WORDS]
   uint16_t* moe_h = nullptr;     // [max_rows][top_k + 1][moe_inter]
-  uint32_t* moe_work = nullptr;  // mi_moe_block's hand-off words (one decode row)
-  size_t moe_work_n = 0;
   uint32_t router_n = 0;
   size_t gu_block = 0, dn_block = 0;  // u32 per expert block
   mi_attn_shape ash{};
@@ -249,11 +247,6 @@ struct mi_engine {
       MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
       MI_TRY(alloc(&moe_route, size_t(R) * MI_MOE_ROUTE_WORDS));
       MI_TRY(alloc(&moe_h, size_t(R) * (m.top_k + 1) * m.moe_inter));
-      moe_work_n = mi_moe_block_work_words(m.experts, m.top_k, H, m.moe_inter, router_n, router_ksplit_of(H));
-      if (moe_work_n) {  // 0: a shape the one-launch block does not serve (the five launches run)
-        MI_TRY(alloc(&moe_work, moe_work_n));
-        MI_TRY(mi_moe_block_work_init(moe_work, moe_work_n, stream));
-      }
     }
 
     // synthetic weights (BASELINE config 2's distributions)
@@ -390,14 +383,7 @@ struct mi_engine {
       const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
       if (d.experts) {
         // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
-        // into the residual, then the next norm with nothing left to fold; one launch for a
-        // single row (mi_moe_block: the same values), else the five launches
-        if (M == 1 && moe_work) {
-          MI_TRY(mi_moe_block(L.router, x, L.moe_gu, L.moe_dn, resid, next_w, x, rstd, d.rms_eps, d.experts, d.top_k,
-                              d.hidden, d.moe_inter, router_n, router_ksplit(), moe_route, moe_work,
-                              ctrl + MI_CTRL_DEBUG, stream));
-          continue;
-        }
+        // into the residual, then the next norm with nothing left to fold
         MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
         MI_TRY(mi_moe_route(moe_logits, moe_route, M, d.experts, d.top_k, router_n, stream));
         MI_TRY(mi_moe_gate_up(moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
@@ -496,7 +482,6 @@ struct mi_engine {
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
-    if (moe_work) MI_TRY(mi_moe_block_work_init(moe_work, moe_work_n, stream));
     if (step) MI_TRY(mi::step_plan_reset(step, stream));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
     MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));

@@ -15,11 +15,8 @@
 // separate lanes (each is independent) and one lane per (column, slice) then adds them in
 // order from LDS: the same operations in the same order, spread over 256 lanes so the
 // expert weights stream at HBM rate instead of one lane per column walking K.
-#include <algorithm>
-
 #include "mi_common.h"
 #include "mi_capi_internal.h"
-#include "gemv_core.h"
 
 namespace mi {
 namespace {
@@ -113,7 +110,7 @@ __device__ __forceinline__ float wave_tree(float x, uint32_t n, F op) {
 // barrier). The whole work-group calls it; blockDim.x >= max(E, 64).
 __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint32_t top_k) {
   __shared__ float s_red[256], s_top_p[9], s_bc;
-  __shared__ uint64_t s_key[256];
+  __shared__ uint32_t s_pb[256];
   __shared__ uint32_t s_top_id[9];
   const uint32_t e = threadIdx.x, lane = e & 63u;
   const bool live = e < E;
@@ -147,19 +144,37 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
   }
   __syncthreads();
   const float p = ex / s_bc;
-  // rank = #{j : p_j > p_e or (p_j == p_e and j < e)}: with p >= 0 the key (p's bits, ~j)
-  // orders exactly so, one 64-bit compare per j, every lane's count in parallel; slots
-  // 0..top_k take ranks 0..top_k
-  const uint64_t key = live ? ((uint64_t)__builtin_bit_cast(uint32_t, p) << 32) | (uint32_t)~e : 0u;
-  s_key[e] = key;
+  // rank = #{j : p_j > p_e or (p_j == p_e and j < e)} = #{j < e : p_j >= p_e} + #{j > e :
+  // p_j > p_e}; p >= 0, so p's bits compare as unsigned integers. The j below the wave's
+  // experts all take >=, those above all take >, the wave's own 64 the per-lane choice.
+  const uint32_t pb = __builtin_bit_cast(uint32_t, p);
+  s_pb[e] = pb;
   __syncthreads();
+  const uint32_t wb = e & ~63u, we = min(wb + 64u, E);
   uint32_t rank = 0;
-  for (uint32_t j0 = 0; j0 < E; j0 += 16u) {
-    uint64_t kv[16];
+  for (uint32_t j0 = 0; j0 < wb; j0 += 16u) {
+    uint32_t kv[16];
 #pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_key[j0 + u];
+    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
 #pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) rank += kv[u] > key ? 1u : 0u;
+    for (uint32_t u = 0; u < 16; ++u) rank += kv[u] >= pb ? 1u : 0u;
+  }
+  for (uint32_t j0 = wb; j0 < we; j0 += 16u) {
+    uint32_t kv[16];
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) {
+      const uint32_t j = j0 + u;
+      rank += (j < e ? kv[u] >= pb : (j > e && kv[u] > pb)) ? 1u : 0u;
+    }
+  }
+  for (uint32_t j0 = wb + 64u; j0 < E; j0 += 16u) {
+    uint32_t kv[16];
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
+#pragma unroll
+    for (uint32_t u = 0; u < 16; ++u) rank += kv[u] > pb ? 1u : 0u;
   }
   const uint32_t slots = top_k + 1;
   if (live && rank < slots) {
@@ -167,19 +182,22 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
     s_top_p[rank] = p;
   }
   __syncthreads();
-  uint32_t* row = s_row;
-  if (e == 0) {
-    float s8 = 0.f;
-    for (uint32_t k = 0; k < top_k; ++k) s8 += s_top_p[k];
-    for (uint32_t k = 0; k < 8; ++k) {
-      const bool on = k < top_k;
-      row[R_IDS + k] = on ? s_top_id[k] : 0u;
-      row[R_W + k] = on ? __builtin_bit_cast(uint32_t, rf(s_top_p[k] / s8)) : 0u;
-      row[R_P + k] = on ? __builtin_bit_cast(uint32_t, s_top_p[k]) : 0u;
-    }
-    row[R_P9] = __builtin_bit_cast(uint32_t, s_top_p[top_k]);
-    row[R_SG] = __builtin_bit_cast(uint32_t, rf(sigmoid_f32(rf(lg[E]))));
-    for (uint32_t k = R_P9 + 1; k < kRouteWords; ++k) row[k] = 0u;
+  // the row, one word per lane: w_k = rne(p_k / s8) with s8 the top_k p added in rank order
+  float s8 = 0.f;
+#pragma unroll
+  for (uint32_t k = 0; k < 8; ++k)
+    if (k < top_k) s8 += s_top_p[k];
+  if (e < 8u) {
+    const bool on = e < top_k;
+    s_row[R_IDS + e] = on ? s_top_id[e] : 0u;
+    s_row[R_W + e] = on ? __builtin_bit_cast(uint32_t, rf(s_top_p[e] / s8)) : 0u;
+    s_row[R_P + e] = on ? __builtin_bit_cast(uint32_t, s_top_p[e]) : 0u;
+  } else if (e == 8u) {
+    s_row[R_P9] = __builtin_bit_cast(uint32_t, s_top_p[top_k]);
+  } else if (e == 9u) {
+    s_row[R_SG] = __builtin_bit_cast(uint32_t, rf(sigmoid_f32(rf(lg[E]))));
+  } else if (e > R_P9 && e < kRouteWords) {
+    s_row[e] = 0u;
   }
   __syncthreads();
 }
@@ -429,425 +447,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
   }
 }
 
-// ---- the whole block of one decode row in one launch (mi_moe_block) ----------------------
-// Three ranges of work-groups, connected by hand-off words (empty pattern 0xFFFFFFFF between
-// launches, device-coherent loads and stores):
-//   router   (router_n/16) * rq work-groups: work-group (nt, qq) computes the router GEMV's
-//            k-slices qq * ksplit/rq .. of column tile nt exactly as gemv_f16w_kernel does and
-//            publishes them; the one that arrives last (an atomic count) merges the slices by
-//            the pairwise tree, routes (route_compute) and publishes the 32-word route row;
-//   gate_up  slots * inter/8 work-groups: moe_gate_up_kernel's half tiles, the expert id
-//            polled from the route row, h published as f16 pairs; the one that arrives last
-//            raises the "h complete" flag;
-//   down     hidden/8 work-groups: moe_down_kernel's half tiles over the polled route row and,
-//            once one lane has seen the flag, h (a single validating pass instead of every
-//            work-group re-polling all of h), the residual written in place and published;
-//            the one that arrives last runs
-//            the next RMSNorm over the whole row (embed_norm_kernel's order) and empties the
-//            many-reader words (route row, h) for the next launch.
-// Every wait is on a lower range (or, for a last arriver, on work-groups that have already
-// published), so it completes when each XCD dispatches its share of the grid in order; a wait
-// is bounded (kBlockTimeout) and sets *status to kStatusTimeout when it gives up.
-constexpr uint64_t kBlockTimeout = 20000000;  // s_memrealtime ticks (100 MHz): 200 ms
-
-struct MoeBlockArgs {
-  const uint16_t* router;  // tiled fp16 (mi_gemv_f16w's layout)
-  const uint16_t* x;       // the block's normed input [hidden]
-  const uint32_t* gu;
-  const uint32_t* dn;
-  uint16_t* resid;         // [hidden], updated in place
-  const float* next_w;     // the next RMSNorm's weights [hidden]
-  uint16_t* x_next;        // [hidden]
-  float* rstd;             // [1]
-  uint32_t* route_out;     // a plain copy of the route row, or NULL
-  uint32_t* work;          // counts and hand-off words (moe_block_layout)
-  uint32_t* status;
-  float eps;
-  uint32_t E, top_k, hidden, inter, router_n, ksplit, rq, n_router, n_gu;
-};
-
-// workspace words: 128 control words, zero between launches (128 bytes apart: [0] the router
-// range's arrival count, [32] gate_up's, [64] down's, [96] the "h complete" flag), then the
-// hand-off words: router slices [ksplit][router_n], route row [32], h pairs, residual pairs
-struct MoeBlockLayout {
-  uint32_t part, route, hw, rw, total;
-};
-__host__ __device__ inline MoeBlockLayout moe_block_layout(uint32_t top_k, uint32_t hidden, uint32_t inter,
-                                                           uint32_t router_n, uint32_t ksplit) {
-  MoeBlockLayout l;
-  l.part = 128;
-  l.route = l.part + ((ksplit * router_n + 31u) & ~31u);
-  l.hw = l.route + 32u;
-  l.rw = l.hw + (((top_k + 1) * inter / 2 + 31u) & ~31u);
-  l.total = l.rw + ((hidden / 2 + 31u) & ~31u);
-  return l;
-}
-
-// dynamic LDS of the block kernel (bytes): the largest role's need
-__host__ __device__ inline uint32_t moe_block_lds(uint32_t top_k, uint32_t hidden, uint32_t inter,
-                                                  uint32_t router_n, uint32_t ksplit, uint32_t rq) {
-  const uint32_t K8 = hidden / 8, G = hidden / 64, Gd = inter / 64, slots = top_k + 1;
-  const uint32_t router = K8 / rq * 256u + K8 / rq * 8u * 4u;
-  const uint32_t route = ksplit * router_n * 4u + router_n * 4u;
-  const uint32_t gate_up = 2u * G * kHalfU32 * 4u + hidden * 4u;
-  const uint32_t down = slots * Gd * kHalfU32 * 4u + slots * inter * 4u;
-  const uint32_t last = hidden * 4u;
-  uint32_t m = router > route ? router : route;
-  m = m > gate_up ? m : gate_up;
-  m = m > down ? m : down;
-  return m > last ? m : last;
-}
-
-// thread t polls words t + 256 u < n of src into v[u]; `take`: empties them afterwards.
-// Device-coherent (sc1) buffer loads and stores with 32-bit offsets: no 64-bit address per word.
-template <int PER>
-__device__ __forceinline__ void poll_regs(Waiter& wt, uint32_t* src, uint32_t n, uint32_t (&v)[PER], bool take) {
-  constexpr int kSc1 = 16;
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(src, 0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t t = threadIdx.x, voff = t * 4u;
-  uint32_t pending = 0;
-#pragma unroll
-  for (int u = 0; u < PER; ++u) {
-    if (t + 256u * u < n) {
-      v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 1024u * u, kSc1);
-      if (v[u] == kEmpty) pending |= 1u << u;
-    }
-  }
-  while (pending && !wt.give_up()) {
-    __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      if (pending & (1u << u)) {
-        v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 1024u * u, kSc1);
-        if (v[u] != kEmpty) pending &= ~(1u << u);
-      }
-    }
-  }
-  if (take) {
-#pragma unroll
-    for (int u = 0; u < PER; ++u)
-      if (t + 256u * u < n) __builtin_amdgcn_raw_buffer_store_b32(kEmpty, rs, voff, 1024u * u, kSc1);
-  }
-}
-
-// one atomic add by thread 0 after the work-group's hand-off stores; true in the work-group
-// that completes `need` (uniform), which sets the count back to zero
-__device__ __forceinline__ bool block_arrive(uint32_t* cnt, uint32_t need, uint32_t* s_flag) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old + 1u == need;
-    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
-  }
-  __syncthreads();
-  return *s_flag != 0u;
-}
-
-__device__ __forceinline__ void moe_block_router(const MoeBlockArgs& a, const MoeBlockLayout& L, uint32_t r,
-                                                 float* smem, Waiter& wt) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t K8 = a.hidden / 8, per = K8 / a.ksplit, sp = a.ksplit / a.rq;
-  const uint32_t nt = r / a.rq, qq = r % a.rq, k0 = qq * sp * per, nk8 = sp * per;
-  uint16_t* s_w = reinterpret_cast<uint16_t*>(smem);   // [nk8][8][16] halves
-  float* s_xr = smem + nk8 * 64u;                       // [nk8 * 8]
-  {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.router + ((size_t)nt * K8 + k0) * 128u);
-    const uint32_t n4 = nk8 * 16u;  // 16-byte pieces (<= 2048)
-    constexpr uint32_t kB = 8;
-    u4_t v[kB];
-#pragma unroll
-    for (uint32_t u = 0; u < kB; ++u)
-      if (t + 256u * u < n4) v[u] = load_stream16(src + 4u * (t + 256u * u));
-    u4_t xv[1];
-    get_f16<1>(xv, a.x + k0 * 8u, nk8 * 8u);  // nk8 * 8 <= 2048: one piece per thread
-    put_f16<1>(s_xr, xv, nk8 * 8u);
-#pragma unroll
-    for (uint32_t u = 0; u < kB; ++u)
-      if (t + 256u * u < n4) reinterpret_cast<u4_t*>(s_w)[t + 256u * u] = v[u];
-  }
-  __syncthreads();
-  if (t < 16u * sp) {
-    // gemv_f16w_kernel<1>'s lane: column nt*16 + lane, k8 of its slice in order, 8 products each
-    const uint32_t ql = t / 16u, lane = t % 16u;
-    float acc = 0.f;
-    for (uint32_t k8 = ql * per; k8 < (ql + 1u) * per; ++k8)
-#pragma unroll
-      for (uint32_t j = 0; j < 8; ++j) acc += h2f(s_w[k8 * 128u + j * 16u + lane]) * s_xr[k8 * 8u + j];
-    st_agent(a.work + L.part + (qq * sp + ql) * a.router_n + nt * 16u + lane, __builtin_bit_cast(uint32_t, publishable(acc)));
-  }
-  __shared__ uint32_t s_flag;
-  if (!block_arrive(a.work, a.n_router, &s_flag)) return;
-  // the last router work-group: the slices, the tree, the route
-  float* s_lg = smem + a.ksplit * a.router_n;
-  {
-    constexpr int PER = 17;  // ksplit * router_n <= 16 * 272
-    uint32_t v[PER];
-    poll_regs<PER>(wt, a.work + L.part, a.ksplit * a.router_n, v, true);
-#pragma unroll
-    for (int u = 0; u < PER; ++u)
-      if (t + 256u * u < a.ksplit * a.router_n) smem[t + 256u * u] = __builtin_bit_cast(float, v[u]);
-  }
-  __syncthreads();
-  for (uint32_t n = t; n < a.router_n; n += 256u) {
-    float v[16];
-#pragma unroll
-    for (uint32_t q = 0; q < 16; ++q) v[q] = q < a.ksplit ? smem[q * a.router_n + n] : 0.f;
-    // gemv_f16w_kernel's merge: red[q] += red[q + stride], stride = ksplit/2 .. 1 (the
-    // strides >= ksplit skipped; constant indices keep v in registers)
-#pragma unroll
-    for (uint32_t stride = 8; stride > 0; stride >>= 1)
-      if (stride < a.ksplit)
-#pragma unroll
-        for (uint32_t q = 0; q < stride; ++q) v[q] += v[q + stride];
-    s_lg[n] = v[0];
-  }
-  __syncthreads();
-  __shared__ uint32_t s_row[kRouteWords];
-  route_compute(s_lg, s_row, a.E, a.top_k);
-  if (t < kRouteWords) {
-    st_agent(a.work + L.route + t, s_row[t]);
-    if (a.route_out) a.route_out[t] = s_row[t];
-  }
-}
-
-__device__ __forceinline__ void moe_block_gate_up(const MoeBlockArgs& a, const MoeBlockLayout& L, uint32_t gi,
-                                                  float* smem, Waiter& wt) {
-  const uint32_t t = threadIdx.x, hidden = a.hidden, inter = a.inter;
-  const uint32_t nhb = inter / 8, slot = gi / nhb, hb = gi % nhb, ib = hb / 2, ch = hb % 2;
-  const uint32_t G = hidden / 64, E = a.E;
-  uint32_t* s_w = reinterpret_cast<uint32_t*>(smem);  // [2][G][kHalfU32]
-  float* s_x = smem + 2u * G * kHalfU32;              // [hidden]
-  __shared__ float s_t[2][8][kMaxGroups];
-  __shared__ float s_r[2][8][kUpKs];
-  __shared__ uint16_t s_h[8];
-  constexpr int XP = kMaxHidden / 8 / 256;
-  u4_t xv[XP];
-  get_f16<XP>(xv, a.x, hidden);  // the input does not depend on the route
-  __shared__ uint32_t s_id;
-  uint32_t e = E;  // the shared expert's slot needs no route
-  if (slot < a.top_k) {
-    if (t == 0) s_id = wt.poll_word(a.work + L.route + R_IDS + slot);  // one lane polls
-    __syncthreads();
-    e = s_id < E ? s_id : E;
-  }
-  {
-    const size_t block = (size_t)(2 * inter / 16) * G * kTileU32;
-    const uint32_t* base = a.gu + (size_t)e * block + (size_t)(2 * ib) * G * kTileU32;
-    const uint32_t n4 = 2u * G * kHalfU4;
-    constexpr uint32_t kBatch = 9;
-    u4_t v[kBatch];
-#pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
-      const uint32_t i = t + 256u * u;
-      if (i < n4) {
-        const uint32_t tg = i / kHalfU4, k = i - tg * kHalfU4;
-        v[u] = half_piece(base + (size_t)tg * kTileU32, ch, k);
-      }
-    }
-    put_f16<XP>(s_x, xv, hidden);
-#pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
-      const uint32_t i = t + 256u * u;
-      if (i < n4) reinterpret_cast<u4_t*>(s_w)[i] = v[u];
-    }
-  }
-  __syncthreads();
-  const uint32_t c = t & 7u, gsub = (t >> 3) & 15u, tl = t >> 7;
-  const uint32_t* tiles = s_w + (size_t)tl * G * kHalfU32;
-  for (uint32_t g = gsub; g < G; g += 16u) s_t[tl][c][g] = half_term(tiles + (size_t)g * kHalfU32, c, s_x + g * 64);
-  __syncthreads();
-  if (t < 2u * 8u * kUpKs) {
-    const uint32_t tl2 = t / (8u * kUpKs), c2 = (t / kUpKs) % 8u, q = t % kUpKs;
-    const uint32_t per = G / kUpKs;
-    float acc = 0.f;
-    for (uint32_t g = q * per; g < (q + 1) * per; ++g) acc += s_t[tl2][c2][g];
-    s_r[tl2][c2][q] = acc;
-  }
-  __syncthreads();
-  if (t < 8u) {
-    float r[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float a0 = s_r[u][t][0] + s_r[u][t][2];
-      const float a1 = s_r[u][t][1] + s_r[u][t][3];
-      r[u] = a0 + a1;
-    }
-    const uint16_t g_b = f2h(r[0]), u_b = f2h(r[1]);
-    const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
-    s_h[t] = f2h(h2f(s_b) * h2f(u_b));
-  }
-  __syncthreads();
-  if (t < 4u)
-    st_agent(a.work + L.hw + (slot * inter + ib * 16u + ch * 8u) / 2u + t, publishable_pair(s_h[2 * t], s_h[2 * t + 1]));
-  __shared__ uint32_t s_flag;
-  if (block_arrive(a.work + 32, a.n_gu, &s_flag) && t == 0) st_agent(a.work + 96, 1u);
-}
-
-__device__ __forceinline__ void moe_block_down(const MoeBlockArgs& a, const MoeBlockLayout& L, uint32_t di,
-                                               float* smem, Waiter& wt) {
-  const uint32_t t = threadIdx.x, hidden = a.hidden, inter = a.inter;
-  const uint32_t nb = di / 2, ch = di % 2, G = inter / 64, slots = a.top_k + 1, E = a.E;
-  uint32_t* s_w = reinterpret_cast<uint32_t*>(smem);  // [slots][G][kHalfU32]
-  float* s_h = smem + slots * G * kHalfU32;           // [slots * inter]
-  __shared__ float s_t[9][8][16];
-  __shared__ float s_d[9][8];
-  __shared__ uint32_t s_row[kRouteWords];
-  __shared__ uint16_t s_rn[8];
-  if (t < kRouteWords) s_row[t] = wt.poll_word(a.work + L.route + t);
-  __syncthreads();
-  uint32_t ids[9];
-#pragma unroll
-  for (uint32_t k = 0; k < 9; ++k) {
-    const uint32_t id = s_row[R_IDS + (k < 8 ? k : 0)];
-    ids[k] = k < a.top_k ? (id < E ? id : E) : E;
-  }
-  const size_t block = (size_t)(hidden / 16) * G * kTileU32;
-  const uint32_t n4 = slots * G * kHalfU4;
-  constexpr uint32_t kBatch = 10;
-  u4_t v[kBatch];
-#pragma unroll
-  for (uint32_t u = 0; u < kBatch; ++u) {
-    const uint32_t i = t + 256u * u;
-    if (i < n4) {
-      const uint32_t sg = i / kHalfU4, k = i - sg * kHalfU4, sl = sg / G, g = sg - sl * G;
-      uint32_t eid = ids[0];
-#pragma unroll
-      for (uint32_t q = 1; q < 9; ++q) eid = sl == q ? ids[q] : eid;
-      v[u] = half_piece(a.dn + (size_t)eid * block + ((size_t)nb * G + g) * kTileU32, ch, k);
-    }
-  }
-  // the weights land in LDS while h is still being made (this work-group waits for it below)
-#pragma unroll
-  for (uint32_t u = 0; u < kBatch; ++u) {
-    const uint32_t i = t + 256u * u;
-    if (i < n4) reinterpret_cast<u4_t*>(s_w)[i] = v[u];
-  }
-  {
-    // one lane waits for the flag (every h word has been stored), then one pass reads h
-    __shared__ uint32_t s_ready;
-    if (t == 0) {
-      uint32_t f = ld_agent(a.work + 96);
-      while (f == 0u && !wt.give_up()) {
-        __builtin_amdgcn_s_sleep(4);
-        f = ld_agent(a.work + 96);
-      }
-      s_ready = f;
-    }
-    __syncthreads();
-    constexpr int PER = kMaxSlotsInter / 2 / 256;  // h pair words per thread
-    uint32_t hv[PER];
-    const uint32_t nw = slots * inter / 2u;
-    poll_regs<PER>(wt, a.work + L.hw, nw, hv, false);
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const uint32_t i = t + 256u * u;
-      if (i < nw) {
-        s_h[2u * i] = h2f((uint16_t)(hv[u] & 0xFFFFu));
-        s_h[2u * i + 1u] = h2f((uint16_t)(hv[u] >> 16));
-      }
-    }
-  }
-  __syncthreads();
-  const uint32_t tasks = slots * 8u * G;
-#pragma unroll 1
-  for (uint32_t i = t; i < tasks; i += 256u) {
-    const uint32_t slot = i / (8u * G), rem = i % (8u * G), g = rem / 8u, c = rem % 8u;
-    s_t[slot][c][g] = half_term(s_w + ((size_t)slot * G + g) * kHalfU32, c, s_h + slot * inter + g * 64);
-  }
-  __syncthreads();
-  if (t < slots * 8u) {
-    const uint32_t slot = t / 8u, c = t % 8u, per = G / kDnKs;
-    float r[kDnKs];
-#pragma unroll
-    for (uint32_t q = 0; q < kDnKs; ++q) {
-      float acc = 0.f;
-      for (uint32_t g = q * per; g < (q + 1) * per; ++g) acc += s_t[slot][c][g];
-      r[q] = acc;
-    }
-    s_d[slot][c] = r[0] + r[1];
-  }
-  __syncthreads();
-  if (t < 8u) {
-    float sum = 0.f;
-    for (uint32_t k = 0; k < a.top_k; ++k) {
-      const float wk = __builtin_bit_cast(float, s_row[R_W + k]);
-      sum += h2f(f2h(h2f(f2h(s_d[k][t])) * wk));
-    }
-    const uint16_t r_b = f2h(sum);
-    const float sg = __builtin_bit_cast(float, s_row[R_SG]);
-    const uint16_t sh_b = f2h(h2f(f2h(s_d[a.top_k][t])) * sg);
-    const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
-    uint16_t* rp = a.resid + nb * 16 + ch * 8 + t;
-    const uint16_t nv = f2h(h2f(*rp) + h2f(o_b));
-    *rp = nv;
-    s_rn[t] = nv;
-  }
-  __syncthreads();
-  if (t < 4u)
-    st_agent(a.work + L.rw + (nb * 16u + ch * 8u) / 2u + t, publishable_pair(s_rn[2 * t], s_rn[2 * t + 1]));
-  __shared__ uint32_t s_flag;
-  if (!block_arrive(a.work + 64, hidden / 8u, &s_flag)) return;
-  // the last down work-group: the next RMSNorm over the whole residual row (embed_norm's order:
-  // 64-element chunk sums by the wave tree, chunks added in ascending order)
-  float* s_v = smem;
-  {
-    constexpr int PER = kMaxHidden / 2 / 256;
-    uint32_t rv[PER];
-    poll_regs<PER>(wt, a.work + L.rw, hidden / 2u, rv, true);
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const uint32_t i = t + 256u * u;
-      if (i < hidden / 2u) {
-        s_v[2u * i] = h2f((uint16_t)(rv[u] & 0xFFFFu));
-        s_v[2u * i + 1u] = h2f((uint16_t)(rv[u] >> 16));
-      }
-    }
-  }
-  __shared__ float s_chunk[kMaxHidden / 64];
-  __shared__ float s_rstd;
-  __syncthreads();
-  const uint32_t lane = t & 63u, wave = t >> 6, nch = hidden / 64u;
-  for (uint32_t c = wave; c < nch; c += 4u) {
-    const float v = s_v[c * 64u + lane];
-    float q = __builtin_fmaf(v, v, 0.f);
-#pragma unroll
-    for (int st = 32; st > 0; st >>= 1) q += __shfl_down(q, st, 64);
-    if (lane == 0) s_chunk[c] = q;
-  }
-  __syncthreads();
-  if (t == 0) {
-    float tot = 0.f;
-    for (uint32_t c = 0; c < nch; ++c) tot += s_chunk[c];
-    s_rstd = 1.0f / sqrtf(tot / (float)hidden + a.eps);
-    a.rstd[0] = s_rstd;
-  }
-  __syncthreads();
-  const float rs = s_rstd;
-  for (uint32_t k = t; k < hidden; k += 256u) a.x_next[k] = f2h(s_v[k] * rs * a.next_w[k]);
-  // every reader of the route row and of h has finished: empty them for the next launch
-  for (uint32_t k = t; k < kRouteWords; k += 256u) st_agent(a.work + L.route + k, kEmpty);
-  for (uint32_t k = t; k < slots * inter / 2u; k += 256u) st_agent(a.work + L.hw + k, kEmpty);
-  if (t == 0) st_agent(a.work + 96, 0u);
-}
-
-__global__ __launch_bounds__(256) void moe_block_kernel(MoeBlockArgs a) {
-  extern __shared__ float smem[];
-  const MoeBlockLayout L = moe_block_layout(a.top_k, a.hidden, a.inter, a.router_n, a.ksplit);
-  Waiter wt{__builtin_amdgcn_s_memrealtime() + kBlockTimeout, a.status, false};
-  const uint32_t b = blockIdx.x;
-  if (b < a.n_router)
-    moe_block_router(a, L, b, smem, wt);
-  else if (b < a.n_router + a.n_gu)
-    moe_block_gate_up(a, L, b - a.n_router, smem, wt);
-  else
-    moe_block_down(a, L, b - a.n_router - a.n_gu, smem, wt);
-}
-
-__global__ void moe_block_init_kernel(uint32_t* __restrict__ w, uint32_t n) {
-  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) w[i] = i < 128u ? 0u : kEmpty;
-}
-
 int check_moe(uint32_t M, uint32_t E, uint32_t top_k, uint32_t hidden, uint32_t inter) {
   if (M == 0 || M > 16) return mi_fail(MI_ERR_SHAPE, "moe: M must be 1..16");
   if (E < 16 || E > 256 || (E & (E - 1))) return mi_fail(MI_ERR_SHAPE, "moe: experts must be a power of two in [16, 256]");
@@ -918,52 +517,3 @@ extern "C" int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint3
   return mi_hip(static_cast<int>(hipGetLastError()), "moe_down launch");
 }
 
-namespace {
-int check_block(uint32_t E, uint32_t top_k, uint32_t hidden, uint32_t inter, uint32_t router_n, uint32_t ksplit) {
-  if (int e = check_moe(1, E, top_k, hidden, inter)) return e;
-  if (router_n % 16 || router_n < E + 1 || router_n > 272)
-    return mi_fail(MI_ERR_SHAPE, "moe_block: router_n must be a multiple of 16 in [experts + 1, 272]");
-  if (ksplit == 0 || ksplit > 16 || (ksplit & (ksplit - 1)) || (hidden / 8) % ksplit)
-    return mi_fail(MI_ERR_SHAPE, "moe_block: ksplit must be a power of two <= 16 dividing hidden/8");
-  if (hidden / 8 / (ksplit < 4 ? ksplit : 4) > 128)  // a router work-group stages <= 32 KB
-    return mi_fail(MI_ERR_SHAPE, "moe_block: hidden / 8 / min(ksplit, 4) must be <= 128");
-  return 0;
-}
-}  // namespace
-
-extern "C" size_t mi_moe_block_work_words(uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
-                                          uint32_t router_n, uint32_t ksplit) {
-  if (check_block(experts, top_k, hidden, inter, router_n, ksplit)) return 0;
-  return moe_block_layout(top_k, hidden, inter, router_n, ksplit).total;
-}
-
-extern "C" int mi_moe_block_work_init(uint32_t* work, size_t words, void* stream) {
-  if (!work || words < 128 || words > 0xFFFFFFFFu) return mi_fail(MI_ERR_ARG, "moe_block_work_init: bad arguments");
-  const uint32_t blocks = (uint32_t)std::min<size_t>((words + 255) / 256, 1024);
-  moe_block_init_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(work, (uint32_t)words);
-  return mi_hip(static_cast<int>(hipGetLastError()), "moe_block_work_init launch");
-}
-
-extern "C" int mi_moe_block(const uint16_t* router_w, const uint16_t* x, const uint32_t* gu_blocks,
-                            const uint32_t* dn_blocks, uint16_t* resid, const float* next_norm_w, uint16_t* x_next,
-                            float* rstd, float eps, uint32_t experts, uint32_t top_k, uint32_t hidden,
-                            uint32_t inter, uint32_t router_n, uint32_t ksplit, uint32_t* route_out,
-                            uint32_t* work, uint32_t* status, void* stream) {
-  if (!router_w || !x || !gu_blocks || !dn_blocks || !resid || !next_norm_w || !x_next || !rstd || !work)
-    return mi_fail(MI_ERR_ARG, "moe_block: null pointer");
-  if (int e = check_block(experts, top_k, hidden, inter, router_n, ksplit)) return e;
-  if (reinterpret_cast<uintptr_t>(router_w) % 16 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(gu_blocks) % 16 || reinterpret_cast<uintptr_t>(dn_blocks) % 16)
-    return mi_fail(MI_ERR_ARG, "moe_block: router_w, x, gu_blocks and dn_blocks need 16-byte alignment");
-  MoeBlockArgs a{};
-  a.router = router_w; a.x = x; a.gu = gu_blocks; a.dn = dn_blocks; a.resid = resid; a.next_w = next_norm_w;
-  a.x_next = x_next; a.rstd = rstd; a.route_out = route_out; a.work = work; a.status = status; a.eps = eps;
-  a.E = experts; a.top_k = top_k; a.hidden = hidden; a.inter = inter; a.router_n = router_n; a.ksplit = ksplit;
-  a.rq = ksplit < 4 ? ksplit : 4;
-  a.n_router = router_n / 16 * a.rq;
-  a.n_gu = (top_k + 1) * (inter / 8);
-  const uint32_t grid = a.n_router + a.n_gu + hidden / 8;
-  const uint32_t lds = moe_block_lds(top_k, hidden, inter, router_n, ksplit, a.rq);
-  moe_block_kernel<<<grid, 256, lds, static_cast<hipStream_t>(stream)>>>(a);
-  return mi_hip(static_cast<int>(hipGetLastError()), "moe_block launch");
-}

@@ -122,10 +122,3 @@ def test_argmax_static_rejects_sizes_beyond_its_scratch():
     assert b"8192" in L.mi_last_error()
     assert L.mi_argmax_static(None, 8, None, 0, 1, 1024, 1024, None) == -1
 
-
-def test_moe_block_refuses_bad_shapes():
-    L = mi.lib()
-    assert L.mi_moe_block_work_words(256, 8, 2048, 512, 272, 16) > 0
-    assert L.mi_moe_block_work_words(256, 8, 2048, 512, 256, 16) == 0   # router_n < experts + 1
-    assert L.mi_moe_block_work_words(256, 8, 2048, 512, 272, 3) == 0    # ksplit not a power of two
-    assert L.mi_moe_block_work_words(256, 8, 2048, 512, 272, 1) == 0    # router work-group > 32 KB

@@ -266,64 +266,3 @@ def test_moe_prefill_refuses_bad_shapes():
     with pytest.raises(mi.MiError):
         mi.call("mi_moe_prefill", 16, 16, 16, 16, 16, 4, 100, 8, 2048, 512, 16, 16, 16, 16, 16, None)
 
-
-@pytest.fixture(scope="module")
-def moe16():
-    return Moe(7, E=16, top_k=2, hidden=512, inter=128, router_n=32)
-
-
-@pytest.mark.parametrize("which", ["cfg4", "small"])
-def test_moe_block_is_the_five_launches(moe256, moe16, which):
-    """mi_moe_block (one launch) against router GEMV -> route -> gate_up -> down -> norm_rows on
-    the same row, bit for bit: residual, next x, rstd and the route row; three launches in a row
-    on different rows (the hand-off words must be left as they were found)."""
-    mo = moe256 if which == "cfg4" else moe16
-    ks = 16
-    while (mo.hidden // 8) % ks:
-        ks //= 2
-    words = mi.lib().mi_moe_block_work_words(mo.E, mo.top_k, mo.hidden, mo.inter, mo.router_n, ks)
-    assert words > 0
-    work = empty((words,), np.uint32)
-    mi.call("mi_moe_block_work_init", ptr(work), words, stream())
-    sync()
-    init = host(work, np.uint32).copy()
-    assert not init[:128].any() and np.all(init[128:] == 0xFFFFFFFF)
-    rng = np.random.default_rng(11)
-    nw = rng.uniform(0.5, 1.5, mo.hidden).astype(np.float32)
-    dnw = dev(nw)
-    status = dev(np.zeros(1, np.uint32))
-    for rep in range(3):
-        print(f"moe_block {which} rep {rep}", flush=True)
-        x = O.f32_to_f16_bits(rng.normal(0, 1, (1, mo.hidden)).astype(np.float32))
-        resid = O.f32_to_f16_bits(rng.normal(0, 1, (1, mo.hidden)).astype(np.float32))
-        # the five launches
-        dx = dev(x)
-        logits = empty((1, mo.router_n), np.float32)
-        route = empty((1, ROUTE_WORDS), np.uint32)
-        h = empty((1, mo.top_k + 1, mo.inter), np.uint16)
-        dres = dev(resid)
-        xa = empty((1, mo.hidden), np.uint16)
-        ra = empty((1,), np.float32)
-        mi.call("mi_gemv_f16w", ptr(mo.d_router), ptr(dx), ptr(logits), 1, mo.hidden, mo.router_n, ks, stream())
-        mi.call("mi_moe_route", ptr(logits), ptr(route), 1, mo.E, mo.top_k, mo.router_n, stream())
-        mi.call("mi_moe_gate_up", ptr(route), ptr(dx), ptr(mo.d_gu), ptr(h), 1, mo.E, mo.top_k, mo.hidden,
-                mo.inter, stream())
-        mi.call("mi_moe_down", ptr(route), ptr(h), ptr(mo.d_dn), ptr(dres), 1, mo.E, mo.top_k, mo.hidden, mo.inter,
-                stream())
-        mi.call("mi_norm_rows", ptr(dres), ptr(dnw), ptr(xa), ptr(ra), 1, mo.hidden, C.c_float(1e-6), stream())
-        # the one launch
-        dres_b = dev(resid)
-        xb = empty((1, mo.hidden), np.uint16)
-        rb = empty((1,), np.float32)
-        route_b = empty((ROUTE_WORDS,), np.uint32)
-        mi.call("mi_moe_block", ptr(mo.d_router), ptr(dx), ptr(mo.d_gu), ptr(mo.d_dn), ptr(dres_b), ptr(dnw),
-                ptr(xb), ptr(rb), C.c_float(1e-6), mo.E, mo.top_k, mo.hidden, mo.inter, mo.router_n, ks,
-                ptr(route_b), ptr(work), ptr(status), stream())
-        sync()
-        assert host(status, np.uint32)[0] == 0
-        np.testing.assert_array_equal(host(route_b, np.uint32), host(route, np.uint32)[0])
-        np.testing.assert_array_equal(host(dres_b, np.uint16), host(dres, np.uint16))
-        np.testing.assert_array_equal(host(xb, np.uint16), host(xa, np.uint16))
-        np.testing.assert_array_equal(host(rb, np.uint32), host(ra, np.uint32))
-        np.testing.assert_array_equal(host(work, np.uint32), init)
-
