@@ -13,7 +13,9 @@ HBM before it starts.
 
 Also printed in the same JSON line:
   roofline     the int4 GEMV (the step's dominant kernel): algorithmic bytes of every GEMV
-               launch of one step / their measured time, HIP events on the engine's stream;
+               launch of one step / their time, each linear's fused launch as the step issues
+               it timed with HIP events on the engine's stream (beside it the same GEMVs as
+               plain launches);
   cpu_baseline this repository's CPU oracle (the reference's scalar twins restated) running
                one full decode step of the same model on the host's cores;
   parity       GPU vs oracle logits of that same step (rel 2e-3 bar) and their argmax.
@@ -57,11 +59,69 @@ class Events:
         return float(ms.value)
 
 
+LINEARS = ["qkv", "o", "gate_up", "down", "lm_head"]
+EPILOGUES = ["QKV (attn_prep fused)", "RESID (residual + next norm)", "SILU (silu * up)",
+             "RESID (residual + next norm)", "LOGITS (+ argmax parts)"]
+
+
+def linear_dims(d):
+    qkv_n = (d.q_heads + 2 * d.kv_heads) * d.head_dim
+    return [(d.hidden, qkv_n), (d.q_heads * d.head_dim, d.hidden), (d.hidden, 2 * d.inter),
+            (d.inter, d.hidden), (d.hidden, d.vocab)]
+
+
+def alg_bytes(K, N):
+    """a GEMV launch's algorithmic bytes: int4 weights + fp16 scales + fp16 x in + fp32 y out"""
+    return K * N // 2 + (K // 64) * N * 2 + 2 * K + 4 * N
+
+
+def step_gemv_roofline(eng, reps=3):
+    """The int4 GEMV launches the step runs: for each linear, `reps` rounds of its fused
+    launch exactly as the step issues it (mi_engine_bench_linear: every layer's weights in
+    turn, the engine's split-K width and epilogue), HIP events on the engine's stream. The
+    step's GEMV time is sum over linears of (launches per step x time per launch); achieved =
+    the step's GEMV algorithmic bytes / that time. Rewrites the engine's state (the caller
+    resets it)."""
+    L = mi.lib()
+    d = eng.desc
+    dims = linear_dims(d)
+    per = []
+    t_step = 0.0
+    alg_step = 0
+    for which, (K, N) in enumerate(dims):
+        ms = C.c_float()
+        mi.check(L.mi_engine_bench_linear(eng._h, which, reps, C.byref(ms)), "engine_bench_linear")
+        n = 1 if which == 4 else d.layers
+        a = alg_bytes(K, N)
+        t_step += ms.value * n
+        alg_step += a * n
+        per.append({"linear": LINEARS[which], "epilogue": EPILOGUES[which], "K": K, "N": N,
+                    "S": eng.linear_s(which), "launches_per_step": n,
+                    "avg_launch_us": round(ms.value * 1e3, 3),
+                    "gbs": round(a / (ms.value * 1e-3) / 1e9, 1),
+                    "frac": round(a / (ms.value * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    launches = sum(x["launches_per_step"] for x in per)
+    achieved = alg_step / (t_step * 1e-3) / 1e9
+    return {
+        "kernel": "gemv_w4a16_kernel, the step's fused launches (int4 g64 GEMV, M=1)",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "launches_per_step": launches,
+        "alg_bytes_per_step": alg_step,
+        "gemv_ms_per_step": round(t_step, 4),
+        "avg_launch_us": round(t_step / launches * 1e3, 3),
+        "per_linear": per,
+    }, alg_step
+
+
 def gemv_roofline(eng, reps=3):
-    """Every int4 GEMV launch of one step (4 per layer + lm_head), each on the engine's own
-    weights and split-K width, back to back on the engine's stream; HIP events around
-    `reps` such sweeps. Algorithmic bytes per launch = int4 weights + fp16 scales + fp16 x
-    in + fp32 y out (K N / 2 + (K / 64) N 2 + 2 K + 4 N)."""
+    """The plain sweep: every int4 GEMV of one step as a plain partials launch (no epilogue),
+    each on the engine's own weights and split-K width, back to back on the engine's stream;
+    HIP events around `reps` such sweeps (algorithmic bytes as alg_bytes)."""
     L = mi.lib()
     d = eng.desc
     st = eng.stream
@@ -117,11 +177,12 @@ def gemv_roofline(eng, reps=3):
     }, alg
 
 
-def profiled_traffic(eng):
-    """HBM bytes per GEMV launch of the sweep from the committed PMC summary (FETCH_SIZE and
-    WRITE_SIZE runs of `bench.py --eager --steps 0`, each scaled by a kernel of known size),
-    provided it was measured at the split-K widths this engine uses; else None."""
-    path = os.path.join(ROOT, "profiles", "gemv_w4a16_27b_traffic.json")
+def profiled_traffic(eng, name="gemv_w4a16_27b_traffic.json"):
+    """HBM bytes per GEMV launch from a committed PMC summary under profiles/ (FETCH_SIZE and
+    WRITE_SIZE runs of the launches, each scaled by a kernel of known size), provided it was
+    measured at the split-K widths this engine uses; else None. gemv_w4a16_27b_traffic.json:
+    the plain sweep; gemv_w4a16_27b_step_traffic.json: the step's fused launches."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -517,7 +578,8 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
-    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill"], default=None,
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill", "roofline"],
+                    default=None,
                     help="run only that secondary measurement and print its JSON (the command the "
                          "attention and single-GEMV kernel profiles use)")
     args = ap.parse_args()
@@ -529,6 +591,16 @@ def main():
         eng = mi.Engine(mi.desc_27b(max_len=2112), seed=args.seed)
         print(json.dumps({"prefill": measure_prefill(eng)}), flush=True)
         eng.close()
+        return
+    if args.only == "roofline":
+        # the GEMV roofline's launches alone (the command the GEMV kernel profiles use): the
+        # step's fused launches per linear, then the plain sweep
+        eng = mi.Engine(mi.desc_27b(max_len=((args.context + 64 + 1 + 63) // 64) * 64), seed=args.seed)
+        eng.reset(args.context, 1000)
+        roof, _ = step_gemv_roofline(eng)
+        plain, _ = gemv_roofline(eng)
+        eng.close()
+        print(json.dumps({"roofline": roof, "plain_sweep": plain}), flush=True)
         return
     if args.only == "cfg4" and args.eager:
         # the configs[3] MoE decode step enqueued kernel by kernel (the MoE kernel profiles'
@@ -633,11 +705,15 @@ def main():
         tok_s = 1000.0 / ms_per_step
         log(f"bench: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms wall -> {tok_s:.1f} tok/s")
 
-    roof, alg_gemv = gemv_roofline(eng)
+    roof, alg_gemv = step_gemv_roofline(eng)
+    plain, _ = gemv_roofline(eng)
+    roof["plain_sweep"] = {k: plain[k] for k in ("achieved", "frac", "gemv_ms_per_step", "avg_launch_us")}
+    roof["plain_sweep"]["note"] = "the same GEMVs as plain partials launches (no fused epilogue)"
     stream_gbs = stream_read_rate(st)
     kv_bytes = 2 * desc.layers * desc.kv_heads * (args.context + 1) * desc.head_dim * 2
     step_alg = alg_gemv + kv_bytes
-    roof["traffic"] = profiled_traffic(eng)
+    roof["traffic"] = profiled_traffic(eng, "gemv_w4a16_27b_step_traffic.json")
+    roof["plain_sweep"]["traffic"] = profiled_traffic(eng)
     roof["stream_read_gbs"] = round(stream_gbs, 1)
     roof["frac_of_stream"] = round(roof["achieved"] / stream_gbs, 4)
     log(f"bench: gemv roofline {roof}")

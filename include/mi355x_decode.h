@@ -468,6 +468,13 @@ int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
  * results are bitwise the graph's. Dense layers with an f16 cache only (MI_ERR_SHAPE
  * otherwise). *wgs (may be NULL) receives the work-groups per launch. */
 int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs);
+/* Measurement (no reference counterpart: the role of the reference's per-kernel timing in
+ * tools/bench): `reps` rounds of one linear's single-row step launch, exactly as the step
+ * issues it (which = 0 qkv with attn_prep, 1 o + residual + norm, 2 gate||up + silu*up,
+ * 3 down + residual + norm: each layer's in turn; 4 the lm_head + argmax parts), back to back
+ * on the engine's stream; *ms_per_launch = the HIP-event time per launch. The launches rewrite
+ * the step's state: reset the engine (mi_engine_reset) before generating again. */
+int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
  * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. */
 int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);

@@ -303,10 +303,6 @@ struct mi_engine {
   }
   uint32_t router_ksplit() const { return router_ksplit_of(d.hidden); }
 
-  int gemv(const Linear& l, const uint16_t* in, uint32_t M) {
-    return mi_gemv_w4a16(l.q, l.s, in, part, M, l.K, l.N, l.S, stream);
-  }
-
   mi_gemv_epilogue resid_epi(const float* next_w) const {
     mi_gemv_epilogue e{};
     e.kind = MI_EPI_RESID;
@@ -332,28 +328,8 @@ struct mi_engine {
     MI_TRY(mi_embed_norm(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      const bool qkv_fused = !d.kv_int8 && (HD == 128 || HD == 256) && M <= 4;
-      if (qkv_fused) {
-        // attn_prep inside the qkv launch (one consumer work-group per head)
-        mi_gemv_epilogue eq{};
-        eq.kind = MI_EPI_QKV;
-        eq.ctrl = ctrl;
-        eq.shape = &ash;
-        eq.q_norm = L.q_norm;
-        eq.k_norm = L.k_norm;
-        eq.rope = rope;
-        eq.attn_q = attn_q;
-        eq.kv_k = static_cast<uint16_t*>(kv_k) + li * layer_kv;
-        eq.kv_v = static_cast<uint16_t*>(kv_v) + li * layer_kv;
-        eq.row_stride = HD;
-        eq.head_stride = size_t(d.max_len) * HD;
-        eq.kv_len = d.max_len;
-        eq.status = ctrl + MI_CTRL_DEBUG;
-        eq.arrive = use_arrive ? arrive : nullptr;
-        MI_TRY(mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream));
-      } else {
-        MI_TRY(gemv(L.qkv, x, M));
-      }
+      const bool qkv_fused = qkv_is_fused(M);
+      MI_TRY(launch_qkv(li, M));
       if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
         int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
         int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
@@ -378,9 +354,8 @@ struct mi_engine {
                               nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
         MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
       }
-      const mi_gemv_epilogue eo = resid_epi(L.post_norm);
-      MI_TRY(mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream));
-      const float* next_w = li + 1 < d.layers ? layer[li + 1].in_norm : final_norm;
+      MI_TRY(launch_o(li, M));
+      const float* next_w = next_norm(li);
       if (d.experts) {
         // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
         // into the residual, then the next norm with nothing left to fold
@@ -391,16 +366,69 @@ struct mi_engine {
         MI_TRY(mi_norm_rows(resid, next_w, x, rstd, M, d.hidden, d.rms_eps, stream));
         continue;
       }
-      mi_gemv_epilogue eg{};
-      eg.kind = MI_EPI_SILU;
-      eg.h = hbuf;
-      eg.status = ctrl + MI_CTRL_DEBUG;
-      eg.arrive = use_arrive ? arrive : nullptr;
-      MI_TRY(mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
-                              stream));
-      const mi_gemv_epilogue ed = resid_epi(next_w);
-      MI_TRY(mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream));
+      MI_TRY(launch_gate_up(li, M));
+      MI_TRY(launch_down(li, M));
     }
+    MI_TRY(launch_lm_head(M));
+    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
+    return 0;
+  }
+
+  // ---- the step's int4 GEMV launches, one per linear, as enqueue_step issues them ----
+  bool qkv_is_fused(uint32_t M) const {
+    return !d.kv_int8 && (d.head_dim == 128 || d.head_dim == 256) && M <= 4;
+  }
+  const float* next_norm(uint32_t li) const { return li + 1 < d.layers ? layer[li + 1].in_norm : final_norm; }
+
+  // the qkv GEMV; with the f16 cache and M <= 4, attn_prep inside it (one consumer work-group
+  // per head), else plain partials for mi_attn_prep / mi_attn_prep_kv8
+  int launch_qkv(uint32_t li, uint32_t M) {
+    const Layer& L = layer[li];
+    if (!qkv_is_fused(M)) return mi_gemv_w4a16(L.qkv.q, L.qkv.s, x, part, M, L.qkv.K, L.qkv.N, L.qkv.S, stream);
+    const uint32_t HD = d.head_dim;
+    const size_t layer_kv = size_t(d.kv_heads) * d.max_len * HD;
+    mi_gemv_epilogue eq{};
+    eq.kind = MI_EPI_QKV;
+    eq.ctrl = ctrl;
+    eq.shape = &ash;
+    eq.q_norm = L.q_norm;
+    eq.k_norm = L.k_norm;
+    eq.rope = rope;
+    eq.attn_q = attn_q;
+    eq.kv_k = static_cast<uint16_t*>(kv_k) + li * layer_kv;
+    eq.kv_v = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+    eq.row_stride = HD;
+    eq.head_stride = size_t(d.max_len) * HD;
+    eq.kv_len = d.max_len;
+    eq.status = ctrl + MI_CTRL_DEBUG;
+    eq.arrive = use_arrive ? arrive : nullptr;
+    return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream);
+  }
+  // o with the residual fold and the post-attention norm
+  int launch_o(uint32_t li, uint32_t M) {
+    const Layer& L = layer[li];
+    const mi_gemv_epilogue eo = resid_epi(L.post_norm);
+    return mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream);
+  }
+  // gate||up with silu * up
+  int launch_gate_up(uint32_t li, uint32_t M) {
+    const Layer& L = layer[li];
+    mi_gemv_epilogue eg{};
+    eg.kind = MI_EPI_SILU;
+    eg.h = hbuf;
+    eg.status = ctrl + MI_CTRL_DEBUG;
+    eg.arrive = use_arrive ? arrive : nullptr;
+    return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
+                            stream);
+  }
+  // down with the residual fold and the next layer's (or the final) norm
+  int launch_down(uint32_t li, uint32_t M) {
+    const Layer& L = layer[li];
+    const mi_gemv_epilogue ed = resid_epi(next_norm(li));
+    return mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream);
+  }
+  // the lm_head with the logits and the per-tile argmax
+  int launch_lm_head(uint32_t M) {
     mi_gemv_epilogue el{};
     el.kind = MI_EPI_LOGITS;
     el.logits = logits;
@@ -408,9 +436,42 @@ struct mi_engine {
     el.vocab_used = d.vocab_used;
     el.status = ctrl + MI_CTRL_DEBUG;
     el.arrive = use_arrive ? arrive : nullptr;
-    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream));
-    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
-    return 0;
+    return mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream);
+  }
+
+  // `reps` rounds of one linear's step launch (0 qkv, 1 o, 2 gate_up, 3 down: every layer's in
+  // turn; 4 the lm_head) back to back on the stream, HIP events around; *ms = the average per
+  // launch. The launches rewrite the step's buffers (residual, KV row at pos, logits): the
+  // caller resets the engine afterwards.
+  int bench_linear(uint32_t which, uint32_t reps, float* ms) {
+    if (which > 4 || reps == 0 || !ms) return mi_fail(MI_ERR_ARG, "engine_bench_linear: which 0..4, reps > 0");
+    if (d.experts && (which == 2 || which == 3))
+      return mi_fail(MI_ERR_SHAPE, "engine_bench_linear: an MoE model has no dense gate_up / down");
+    auto one = [&](uint32_t li) -> int {
+      switch (which) {
+        case 0: return launch_qkv(li, 1);
+        case 1: return launch_o(li, 1);
+        case 2: return launch_gate_up(li, 1);
+        case 3: return launch_down(li, 1);
+        default: return launch_lm_head(1);
+      }
+    };
+    const uint32_t per_round = which == 4 ? 1u : d.layers;
+    for (uint32_t li = 0; li < per_round; ++li) MI_TRY(one(li));  // warm-up round
+    hipEvent_t a, b;
+    MI_TRY(mi_hip(static_cast<int>(hipEventCreate(&a)), "event"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventCreate(&b)), "event"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventRecord(a, stream)), "event record"));
+    for (uint32_t r = 0; r < reps; ++r)
+      for (uint32_t li = 0; li < per_round; ++li) MI_TRY(one(li));
+    MI_TRY(mi_hip(static_cast<int>(hipEventRecord(b, stream)), "event record"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventSynchronize(b)), "event sync"));
+    float t = 0.f;
+    MI_TRY(mi_hip(static_cast<int>(hipEventElapsedTime(&t, a, b)), "event elapsed"));
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    *ms = t / float(reps * per_round);
+    return check_handoff();
   }
 
   int capture(uint32_t M) {
@@ -807,6 +868,11 @@ int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs) {
   MI_TRY(e->enable_step(on != 0));
   if (wgs) *wgs = e->use_step ? mi::step_plan_wgs(e->step) : 0u;
   return 0;
+}
+
+int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_bench_linear: null");
+  return e->bench_linear(which, reps, ms_per_launch);
 }
 
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out) {
