@@ -241,6 +241,19 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
                    size_t sc_head_stride, const uint32_t* pages, uint32_t page, uint32_t kv_len,
                    float* attn_part, uint32_t M, uint32_t tgt, const mi_attn_shape* shape,
                    void* stream);
+/* The verify step's attention for many rows (attn_verify_dpas, attn_verify_dpas.cl:383; bound by
+ * verify_attn.h:93-96's rule, mi_attn_verify_binds): M <= 64 rows of a model with 8 q heads per
+ * kv head (16 / 2 at head_dim 256 in the reference), f16 cache. The same arguments, partials
+ * and blocking as mi_attn_decode (reduce with mi_attn_reduce), each KV block read once for 8
+ * rows. A row's partials depend only on its own key count, not on M or the other rows (the
+ * reference's property R); they are not bitwise mi_attn_decode's (another accumulation order). */
+int mi_attn_verify(const uint32_t* ctrl, const float* attn_q, const uint16_t* kv_k, const uint16_t* kv_v,
+                   size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page, uint32_t kv_len,
+                   float* attn_part, uint32_t M, uint32_t tgt, const mi_attn_shape* shape, void* stream);
+/* verify_attn.h:93-100 (verify_attn_wide_heads / verify_attn_kind at those heads): 1 when a verify
+ * list of M rows binds mi_attn_verify (16 q / 2 kv heads, f16 cache (kv_kind 0), M = 16, 32 or
+ * 64), 0 when it keeps mi_attn_decode. */
+int mi_attn_verify_binds(uint32_t M, uint32_t kv_kind, uint32_t q_heads, uint32_t kv_heads);
 /* attn_prep (attn.cl:361-372) and attn_decode_v2 (attn_v2.cl:172-188) in one launch, f16 cache
  * only: the decode's work-groups compute q of their heads and the new K/V rows of their block
  * from the qkv partials themselves (the same chain as mi_attn_prep, bitwise), write each new

@@ -52,6 +52,8 @@ SIGNATURES = {
     "mi_attn_prep_kv8": (i32, [vp, vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32,
                                u32, vp]),
     "mi_attn_ppw": (u32, [u32, u32]),
+    "mi_attn_verify": (i32, [vp, vp, vp, vp, sz, sz, vp, u32, u32, vp, u32, u32, vp, vp]),
+    "mi_attn_verify_binds": (i32, [u32, u32, u32, u32]),
     "mi_attn_decode": (i32, [vp, vp, u32, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, vp, u32, u32, vp, vp]),
     "mi_attn_reduce": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, vp]),
     "mi_attn_prep_decode": (i32, [vp, vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, u32, vp, u32, vp]),

@@ -122,3 +122,13 @@ def test_argmax_static_rejects_sizes_beyond_its_scratch():
     assert b"8192" in L.mi_last_error()
     assert L.mi_argmax_static(None, 8, None, 0, 1, 1024, 1024, None) == -1
 
+
+
+def test_verify_attention_bind_rule():
+    """verify_attn.h:93-100 at 16 q / 2 kv heads: the many-row kernel at 16, 32, 64 rows of an
+    f16 cache only"""
+    L = mi.lib()
+    assert [L.mi_attn_verify_binds(M, 0, 16, 2) for M in (1, 2, 4, 8, 15, 16, 32, 64, 65)] == \
+        [0, 0, 0, 0, 0, 1, 1, 1, 0]
+    assert L.mi_attn_verify_binds(16, 1, 16, 2) == 0     # int8 cache: the decode kernel
+    assert L.mi_attn_verify_binds(16, 0, 40, 8) == 0     # other heads
