@@ -350,8 +350,14 @@ struct mi_engine {
         if (!qkv_fused)
           MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
                               HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
-        MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
-                              nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+        // verify_attn.h's rule: the many-row kernel for the lists it binds (16, 32, 64 rows at
+        // 16 / 2 heads), else the decode kernel (every list this engine builds: M <= 8)
+        if (mi_attn_verify_binds(M, 0, d.q_heads, d.kv_heads))
+          MI_TRY(mi_attn_verify(ctrl, attn_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, attn_part,
+                                M, d.attn_tgt, &ash, stream));
+        else
+          MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
+                                nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
         MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
       }
       MI_TRY(launch_o(li, M));

@@ -75,6 +75,7 @@ def lib():
                                      vp, sz, sz, u32, u32, vp, vp]),
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
             "orc_dense_step_kv8": (u32, [i32, vp, u32, u32, vp, vp, vp, vp, vp, u32]),
+            "orc_prefill_chunk": (u32, [i32, vp, vp, u32, u32, vp, vp, vp]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
             "orc_threads": (i32, []),

@@ -1065,4 +1065,79 @@ uint32_t orc_dense_step_kv8(int act, const orc_dense_model* md, uint32_t tok, ui
   return dense_step(act, md, tok, pos, kv_k, kv_v, k_scale, v_scale, logits, n_layers_run);
 }
 
+
+// ---- the chunked prefill (src/runtime/prefill/step.h step_chunk; this build's
+// Engine::prefill_chunk walk) ---------------------------------------------------------------
+// The prefill's own roundings: every int4 weight dequantised ONCE to act, w = rne((q - 8) * s)
+// (pf_dequant_slab.cl's slab), and each output the fp32 sum over k ascending of w * x (the
+// products are exact in fp32); the residual, norms, SiLU and attention prep are the decode twins
+// at one slice (S = 1) over the chunk's T rows; the causal attention of row t over keys
+// [0, pos + t] in fp64, rounded once (the prefill kernel's fp32-accurate flash attention).
+static void prefill_gemm(const Act& A, const orc_linear& l, const uint16_t* x, uint32_t T, float* out) {
+  const uint32_t K = l.K, N = l.N;
+  std::vector<float> w(size_t(K) * N);
+  for (uint32_t k = 0; k < K; ++k)
+    for (uint32_t n = 0; n < N; ++n) {
+      const int q = int((l.qweight[size_t(k / 8) * N + n] >> (4 * (k % 8))) & 0xFu) - 8;
+      w[size_t(k) * N + n] = A.rf(float(q) * orc_f16_to_f32(l.scales[size_t(k / 64) * N + n]));
+    }
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < int64_t(T); ++t) {
+    std::vector<float> xf(K);
+    for (uint32_t k = 0; k < K; ++k) xf[k] = A.w(x[size_t(t) * K + k]);
+    float* o = out + size_t(t) * N;
+    for (uint32_t n = 0; n < N; ++n) o[n] = 0.f;
+    for (uint32_t k = 0; k < K; ++k) {
+      const float xv = xf[k];
+      const float* wr = w.data() + size_t(k) * N;
+      for (uint32_t n = 0; n < N; ++n) o[n] += wr[n] * xv;
+    }
+  }
+}
+
+uint32_t orc_prefill_chunk(int act, const orc_dense_model* md, const uint32_t* ids, uint32_t T, uint32_t pos,
+                           uint16_t* kv_k, uint16_t* kv_v, float* logits) {
+  if (md->experts || T == 0 || size_t(pos) + T > md->max_len) return 0xFFFFFFFFu;
+  const Act A{act};
+  const uint32_t H = md->hidden, HD = md->attn.head_dim, QH = md->attn.q_heads, KVH = md->attn.kv_heads;
+  const uint32_t L = md->max_len, G = QH / KVH, QHD = QH * HD;
+  std::vector<uint16_t> resid(size_t(T) * H), x(size_t(T) * H), attn(size_t(T) * QHD), h(size_t(T) * md->inter);
+  std::vector<float> out, attn_q(size_t(T) * QHD);
+  if (orc_embed_gather(ids, T, md->embed, md->vocab, H, resid.data())) return 0xFFFFFFFFu;
+  orc_res_norm(act, nullptr, resid.data(), md->layer[0].in_norm, x.data(), T, H, 0, md->rms_eps);
+  for (uint32_t li = 0; li < md->layers; ++li) {
+    const orc_layer& ly = md->layer[li];
+    const size_t lo = size_t(li) * KVH * L * HD;
+    uint16_t* lk = kv_k + lo;
+    uint16_t* lv = kv_v + lo;
+    out.assign(size_t(T) * ly.qkv.N, 0.f);
+    prefill_gemm(A, ly.qkv, x.data(), T, out.data());
+    orc_attn_prep(act, &md->attn, pos, T, T, out.data(), 1, ly.q_norm, ly.k_norm, md->rope, attn_q.data(), nullptr,
+                  lk, lv, HD, size_t(L) * HD, nullptr, 0);
+#pragma omp parallel for schedule(static)
+    for (int64_t th = 0; th < int64_t(T) * QH; ++th) {
+      const uint32_t t = uint32_t(th / QH), hh = uint32_t(th % QH);
+      std::vector<double> o(HD);
+      orc_attend64(&md->attn, attn_q.data() + (size_t(t) * QH + hh) * HD, hh / G, pos + t + 1, 0, act, lk, lv,
+                   nullptr, nullptr, HD, size_t(L) * HD, 0, 0, nullptr, 0, o.data());
+      for (uint32_t dd = 0; dd < HD; ++dd) attn[size_t(t) * QHD + size_t(hh) * HD + dd] = A.rne(float(o[dd]));
+    }
+    out.assign(size_t(T) * H, 0.f);
+    prefill_gemm(A, ly.o, attn.data(), T, out.data());
+    orc_res_norm(act, out.data(), resid.data(), ly.post_norm, x.data(), T, H, 1, md->rms_eps);
+    out.assign(size_t(T) * ly.gate_up.N, 0.f);
+    prefill_gemm(A, ly.gate_up, x.data(), T, out.data());
+    orc_silu_mul(act, out.data(), h.data(), T, md->inter, 1);
+    out.assign(size_t(T) * H, 0.f);
+    prefill_gemm(A, ly.down, h.data(), T, out.data());
+    const float* next_w = li + 1 < md->layers ? md->layer[li + 1].in_norm : md->final_norm;
+    orc_res_norm(act, out.data(), resid.data(), next_w, x.data(), T, H, 1, md->rms_eps);
+  }
+  // the last row's head on the decode GEMV (the engine runs the step's lm_head launch)
+  std::vector<float> xf(H);
+  for (uint32_t k = 0; k < H; ++k) xf[k] = A.w(x[size_t(T - 1) * H + k]);
+  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
+  return orc_argmax(logits, md->vocab, md->vocab_used);
+}
+
 }  // extern "C"

@@ -212,6 +212,13 @@ uint32_t orc_dense_step_kv8(int act, const orc_dense_model* m, uint32_t tok, uin
                             int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
                             float* logits, uint32_t n_layers_run);
 
+/* The chunked prefill of T ids at positions pos .. pos + T - 1 (dense layers, f16 cache; the
+ * walk of src/runtime/prefill/step.h with the prefill's roundings: weights rounded once to act,
+ * fp32 sums, causal attention in fp64 rounded once). Writes the chunk's K/V rows, the logits of
+ * the last row (the decode head) and returns their argmax (0xFFFFFFFF: unsupported). */
+uint32_t orc_prefill_chunk(int act, const orc_dense_model* m, const uint32_t* ids, uint32_t T, uint32_t pos,
+                           uint16_t* kv_k, uint16_t* kv_v, float* logits);
+
 #ifdef __cplusplus
 }
 #endif

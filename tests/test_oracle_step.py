@@ -173,6 +173,70 @@ def test_bar_rejects_plausible_wiring_mistakes(mistake):
     assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
 
 
+def prefill_fp64(m, ids, pos, mistake=None):
+    """T consecutive fp64 steps (each attending to the fp64 K/V rows of the previous ones)"""
+    cache = (O.f16_bits_to_f32(m.kv_k).astype(np.float64), O.f16_bits_to_f32(m.kv_v).astype(np.float64))
+    for t, tok in enumerate(ids):
+        lg, kc, vc = m.fp64_step(int(tok), pos + t, mistake=mistake, cache=cache)
+        cache = (kc, vc)
+    return lg, cache[0], cache[1]
+
+
+def oracle_prefill(m, ids, pos):
+    kk, vv = m.kv_k.copy(), m.kv_v.copy()
+    logits = np.zeros(m.d["V"], np.float32)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    am = O.lib().orc_prefill_chunk(F16, C.byref(m.m), O._p(ids), len(ids), pos, O._p(kk), O._p(vv), O._p(logits))
+    return int(am), logits, kk, vv
+
+
+@pytest.mark.parametrize("seed,T,pos,qk_norm", [(4, 12, 0, True), (5, 23, 30, True), (6, 9, 50, False)])
+def test_prefill_chunk_vs_independent_fp64_forward(seed, T, pos, qk_norm):
+    """orc_prefill_chunk (the prefill walk with its own roundings: weights rounded once, fp32
+    sums, fp64 attention rounded once) against T consecutive fp64 steps of the same model: the
+    last row's logits and every K/V row the chunk writes, at the step's bar, and nothing else
+    of the cache touched."""
+    m = TinyModel(seed, qk_norm=qk_norm)
+    ids = np.random.default_rng(seed).integers(0, m.d["V"], T)
+    am, got, kk, vv = oracle_prefill(m, ids, pos)
+    want, kc, vc = prefill_fp64(m, ids, pos)
+    scale = np.abs(want).max()
+    err = np.abs(got.astype(np.float64) - want)
+    assert err.max() <= 5e-3 * scale, (err.max(), scale)
+    assert np.corrcoef(got, want)[0, 1] > 0.9999
+    top = np.sort(want)[::-1]
+    assert am == int(np.argmax(want)) or top[0] - want[am] <= 1e-2 * scale
+    rows = slice(pos, pos + T)
+    for li in range(m.d["layers"]):
+        gk = O.f16_bits_to_f32(kk[li, :, rows]).astype(np.float64)
+        assert np.abs(gk - kc[li, :, rows]).max() <= 2e-2 * np.abs(kc[li, :, rows]).max()
+        gv = O.f16_bits_to_f32(vv[li, :, rows]).astype(np.float64)
+        assert np.abs(gv - vc[li, :, rows]).max() <= 2e-2 * np.abs(vc[li, :, rows]).max()
+    mask = np.ones(m.d["L"], bool)
+    mask[rows] = False
+    assert np.array_equal(kk[:, :, mask], m.kv_k[:, :, mask])
+    assert np.array_equal(vv[:, :, mask], m.kv_v[:, :, mask])
+
+
+@pytest.mark.parametrize("mistake", ["rope_sign", "gqa_map", "gate_up_swap", "no_attn_resid"])
+def test_prefill_bar_rejects_plausible_wiring_mistakes(mistake):
+    m = TinyModel(5)
+    ids = np.random.default_rng(5).integers(0, m.d["V"], 10)
+    _, got, _, _ = oracle_prefill(m, ids, 20)
+    want = prefill_fp64(m, ids, 20, mistake=mistake)[0]
+    assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
+
+
+def test_prefill_chunk_refuses_what_it_does_not_model():
+    m = TinyModel(4)
+    logits = np.zeros(m.d["V"], np.float32)
+    ids = np.zeros(4, np.uint32)
+    kk, vv = m.kv_k.copy(), m.kv_v.copy()
+    # past the cache
+    assert O.lib().orc_prefill_chunk(F16, C.byref(m.m), O._p(ids), 4, m.d["L"] - 2, O._p(kk), O._p(vv),
+                                     O._p(logits)) == 0xFFFFFFFF
+
+
 def layout1_dequant(blocks, K, N):
     """fp64 [K][N] of one int4 g64 layout-1 block, from the format's definition: tile
     (n/16, k/64) of 136 words; word (k%64)/8 * 16 + n%16 holds k's nibble k%8 (low first);

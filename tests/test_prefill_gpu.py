@@ -17,7 +17,7 @@ import pytest
 
 import oracle as O
 from mipkg import dev, empty, host, mi, ptr, stream, sync
-from test_engine_gpu import small_desc
+from test_engine_gpu import OracleModel, close, small_desc
 
 pytestmark = pytest.mark.gpu
 F16 = O.ORC_F16
@@ -219,6 +219,41 @@ def test_prefill_matches_ingest(n, chunk, p0):
     if top2[1] - top2[0] > 0.02 * scale:
         assert c_pf[mi.CTRL_CUR] == c_ing[mi.CTRL_CUR] == int(np.argmax(lg_ing))
     # decode continues from the prefilled cache as from the ingested one
+    eng.close()
+
+
+@pytest.mark.parametrize("n,chunk,p0,qk_norm", [(40, 0, 0, 1), (40, 16, 0, 1), (33, 8, 100, 0)])
+def test_prefill_vs_oracle_prefill(n, chunk, p0, qk_norm):
+    """The engine's chunked prefill against the oracle's prefill walk (orc_prefill_chunk, chunk by
+    chunk on the same cache): the last position's logits and every K/V row written, at the
+    north star's rel 2e-3, and the control block as ingest leaves it."""
+    eng = mi.Engine(small_desc(max_len=512, qk_norm=qk_norm), seed=13)
+    orc = OracleModel(eng)
+    ids = np.random.default_rng(n + chunk + 1).integers(0, eng.desc.vocab_used, n).astype(np.uint32)
+    print(f"prefill vs oracle n={n} chunk={chunk} p0={p0} qk_norm={qk_norm}", flush=True)
+    eng.reset(p0, 0)
+    eng.prefill(ids, chunk)
+    c = eng.ctrl()
+    lg = eng.logits(1)[0].astype(np.float64)
+    k_pf, v_pf = kv_rows(eng, p0, n)
+    step = chunk or n
+    want = np.zeros(eng.desc.vocab, np.float32)
+    for c0 in range(0, n, step):
+        part = np.ascontiguousarray(ids[c0:c0 + step])
+        am = O.lib().orc_prefill_chunk(O.ORC_F16, C.byref(orc.m), O._p(part), len(part), p0 + c0, O._p(orc.kv_k),
+                                       O._p(orc.kv_v), O._p(want))
+    d = eng.desc
+    kw = orc.kv_k.reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)[:, :, p0:p0 + n]
+    vw = orc.kv_v.reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)[:, :, p0:p0 + n]
+    for a, b in ((k_pf, kw), (v_pf, vw)):
+        b = O.f16_bits_to_f32(b).astype(np.float64)
+        assert np.all(np.abs(a - b) <= 2e-3 * np.abs(b) + 2e-3 * np.abs(b).max()), np.abs(a - b).max()
+    w = want.astype(np.float64)
+    assert close(lg, w), np.abs(lg - w).max() / np.abs(w).max()
+    assert c[mi.CTRL_POS] == p0 + n and c[mi.CTRL_NACT] == 1
+    top2 = np.sort(w)[-2:]
+    if top2[1] - top2[0] > 4e-3 * np.abs(w).max():
+        assert c[mi.CTRL_CUR] == am
     eng.close()
 
 
