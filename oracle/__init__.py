@@ -76,6 +76,7 @@ def lib():
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
             "orc_dense_step_kv8": (u32, [i32, vp, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_prefill_chunk": (u32, [i32, vp, vp, u32, u32, vp, vp, vp]),
+            "orc_moe_prefill": (None, [i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
             "orc_threads": (i32, []),
@@ -125,6 +126,7 @@ def ref():
             "ref_moe_silu_up": (u16, [f32, f32]),
             "ref_moe_combine": (u16, [vp, vp, u32, u32, u16]),
             "ref_moe_block": (None, [vp, u32, u32, u32, u32, u32, vp, vp, vp, u32, u32, vp]),
+            "ref_pf_moe_block": (None, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
             "ref_repack_bf16_tiled": (None, [vp, u32, u32, vp]),
         }
         for name, (res, args) in sig.items():

@@ -1097,7 +1097,7 @@ static void prefill_gemm(const Act& A, const orc_linear& l, const uint16_t* x, u
 
 uint32_t orc_prefill_chunk(int act, const orc_dense_model* md, const uint32_t* ids, uint32_t T, uint32_t pos,
                            uint16_t* kv_k, uint16_t* kv_v, float* logits) {
-  if (md->experts || T == 0 || size_t(pos) + T > md->max_len) return 0xFFFFFFFFu;
+  if (T == 0 || size_t(pos) + T > md->max_len) return 0xFFFFFFFFu;
   const Act A{act};
   const uint32_t H = md->hidden, HD = md->attn.head_dim, QH = md->attn.q_heads, KVH = md->attn.kv_heads;
   const uint32_t L = md->max_len, G = QH / KVH, QHD = QH * HD;
@@ -1125,12 +1125,36 @@ uint32_t orc_prefill_chunk(int act, const orc_dense_model* md, const uint32_t* i
     out.assign(size_t(T) * H, 0.f);
     prefill_gemm(A, ly.o, attn.data(), T, out.data());
     orc_res_norm(act, out.data(), resid.data(), ly.post_norm, x.data(), T, H, 1, md->rms_eps);
+    const float* next_w = li + 1 < md->layers ? md->layer[li + 1].in_norm : md->final_norm;
+    if (md->experts) {
+      // the MoE block over the chunk: the router GEMV and the route of every row (the decode
+      // twins, row by row), the experts as pf_moe_ref's values, then the next norm (moe_down
+      // folds its output into the residual itself)
+      std::vector<float> lg(size_t(T) * md->router_n);
+      orc_gemv_f16w(act, ly.router, x.data(), T, H, md->router_n, md->router_ksplit, lg.data());
+      std::vector<uint32_t> route(size_t(T) * 32, 0u);
+      for (uint32_t t = 0; t < T; ++t) {
+        orc_moe_route r;
+        orc_moe_route_fn(act, lg.data() + size_t(t) * md->router_n, md->experts, md->top_k, &r);
+        uint32_t* rw = route.data() + size_t(t) * 32;
+        for (uint32_t j = 0; j < md->top_k; ++j) {
+          rw[j] = r.ids[j];
+          std::memcpy(rw + 8 + j, &r.w[j], 4);
+          std::memcpy(rw + 17 + j, &r.p[j], 4);
+        }
+        std::memcpy(rw + 16, &r.sg, 4);
+        std::memcpy(rw + 25, &r.p9, 4);
+      }
+      orc_moe_prefill(act, md->experts, md->top_k, H, md->moe_inter, route.data(), x.data(), ly.moe_gu, ly.moe_dn,
+                      resid.data(), T);
+      orc_res_norm(act, nullptr, resid.data(), next_w, x.data(), T, H, 0, md->rms_eps);
+      continue;
+    }
     out.assign(size_t(T) * ly.gate_up.N, 0.f);
     prefill_gemm(A, ly.gate_up, x.data(), T, out.data());
     orc_silu_mul(act, out.data(), h.data(), T, md->inter, 1);
     out.assign(size_t(T) * H, 0.f);
     prefill_gemm(A, ly.down, h.data(), T, out.data());
-    const float* next_w = li + 1 < md->layers ? md->layer[li + 1].in_norm : md->final_norm;
     orc_res_norm(act, out.data(), resid.data(), next_w, x.data(), T, H, 1, md->rms_eps);
   }
   // the last row's head on the decode GEMV (the engine runs the step's lm_head launch)
@@ -1138,6 +1162,101 @@ uint32_t orc_prefill_chunk(int act, const orc_dense_model* md, const uint32_t* i
   for (uint32_t k = 0; k < H; ++k) xf[k] = A.w(x[size_t(T - 1) * H + k]);
   orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);
+}
+
+
+// ---- the chunk's MoE block (tests/kernels/pf_moe_ref.h: pf_moe_sort / dequant / grouped GEMM /
+// combine) -----------------------------------------------------------------------------------
+// The values pf_moe_ref's chain gives every (token, slot) pair, token by token (the sort only
+// places the rows; no value depends on it): the expert's layout-1 blocks dequantised once,
+// w = rne((q - 8) * scale) (dequant_block); gate||up = fp32 sums of x w in ascending k
+// (gemm_rows); h = silu_up per intermediate column (silu_row); y = rne(fp32 sums of h w_down)
+// (the down outputs, rounded); then combine_token: sum_j rne(y_j w_j) in slot order from +0,
+// r = rne(sum), sh = rne(y_shared sg), o = rne(r + sh), resid = rne(resid + o). A slot's id
+// past the last expert is clamped to it (pf_moe_sort's byte staging).
+static std::vector<float> dequant_layout1(const Act& A, const uint32_t* blk, uint32_t K, uint32_t N) {
+  std::vector<float> out(size_t(K) * N);
+  const uint32_t G = K / 64;
+  for (uint32_t n = 0; n < N; ++n)
+    for (uint32_t g = 0; g < G; ++g) {
+      const uint32_t* tile = blk + (size_t(n / 16) * G + g) * 136;
+      uint16_t sh;
+      std::memcpy(&sh, reinterpret_cast<const uint16_t*>(tile + 128) + n % 16, 2);
+      const float scale = orc_f16_to_f32(sh);
+      for (uint32_t j = 0; j < 8; ++j) {
+        const uint32_t word = tile[j * 16 + n % 16];
+        for (uint32_t i = 0; i < 8; ++i) {
+          const int q = int((word >> (4 * i)) & 0xFu) - 8;
+          out[size_t(g * 64 + j * 8 + i) * N + n] = A.rf(float(q) * scale);
+        }
+      }
+    }
+  return out;
+}
+
+void orc_moe_prefill(int act, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                     const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks, const uint32_t* dn_blocks,
+                     uint16_t* resid, uint32_t T) {
+  const Act A{act};
+  const uint32_t E = experts, slots = top_k + 1, N2 = 2 * inter;
+  const size_t gub = size_t(N2 / 16) * (hidden / 64) * 136, dnb = size_t(hidden / 16) * (inter / 64) * 136;
+  auto expert = [&](uint32_t t, uint32_t j) -> uint32_t {
+    if (j == top_k) return E;
+    return std::min(route[size_t(t) * 32 + j], E - 1);
+  };
+  // expert by expert (each block dequantised once, then every pair routed to it)
+  std::vector<std::vector<uint32_t>> pairs(E + 1);
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t j = 0; j < slots; ++j) pairs[expert(t, j)].push_back(t * slots + j);
+  std::vector<float> y(size_t(T) * slots * hidden);  // the rounded down outputs
+  for (uint32_t e = 0; e <= E; ++e) {
+    if (pairs[e].empty()) continue;
+    const std::vector<float> gw = dequant_layout1(A, gu_blocks + e * gub, hidden, N2);
+    const std::vector<float> dw = dequant_layout1(A, dn_blocks + e * dnb, inter, hidden);
+    const std::vector<uint32_t>& pe = pairs[e];
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t pi = 0; pi < int64_t(pe.size()); ++pi) {
+      const uint32_t p = pe[size_t(pi)], t = p / slots;
+      std::vector<float> gu(N2, 0.f), hf(inter);
+      for (uint32_t k = 0; k < hidden; ++k) {
+        const float av = A.w(x[size_t(t) * hidden + k]);
+        const float* wr = gw.data() + size_t(k) * N2;
+        for (uint32_t n = 0; n < N2; ++n) gu[n] += av * wr[n];
+      }
+      for (uint32_t i = 0; i < inter; ++i) {
+        const uint32_t gc = (i / 16) * 32 + i % 16;
+        const uint16_t g_b = A.rne(gu[gc]), u_b = A.rne(gu[gc + 16]);
+        const uint16_t s_b = A.rne(silu_f32(A.w(g_b)));
+        hf[i] = A.w(A.rne(A.w(s_b) * A.w(u_b)));
+      }
+      float* yo = y.data() + size_t(p) * hidden;
+      for (uint32_t n = 0; n < hidden; ++n) yo[n] = 0.f;
+      for (uint32_t k = 0; k < inter; ++k) {
+        const float* wr = dw.data() + size_t(k) * hidden;
+        for (uint32_t n = 0; n < hidden; ++n) yo[n] += hf[k] * wr[n];
+      }
+      for (uint32_t n = 0; n < hidden; ++n) yo[n] = A.rf(yo[n]);
+    }
+  }
+  for (uint32_t t = 0; t < T; ++t) {
+    const uint32_t* row = route + size_t(t) * 32;
+    const float* yt = y.data() + size_t(t) * slots * hidden;
+    float sg;
+    std::memcpy(&sg, row + 16, 4);
+    for (uint32_t n = 0; n < hidden; ++n) {
+      float sum = 0.f;
+      for (uint32_t j = 0; j < top_k; ++j) {
+        float w;
+        std::memcpy(&w, row + 8 + j, 4);
+        sum += A.rf(yt[size_t(j) * hidden + n] * w);
+      }
+      const uint16_t r_b = A.rne(sum);
+      const uint16_t sh_b = A.rne(yt[size_t(top_k) * hidden + n] * sg);
+      const uint16_t o_b = A.rne(A.w(r_b) + A.w(sh_b));
+      uint16_t* rp = resid + size_t(t) * hidden + n;
+      *rp = A.rne(A.w(*rp) + A.w(o_b));
+    }
+  }
 }
 
 }  // extern "C"

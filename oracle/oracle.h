@@ -212,9 +212,16 @@ uint32_t orc_dense_step_kv8(int act, const orc_dense_model* m, uint32_t tok, uin
                             int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
                             float* logits, uint32_t n_layers_run);
 
-/* The chunked prefill of T ids at positions pos .. pos + T - 1 (dense layers, f16 cache; the
- * walk of src/runtime/prefill/step.h with the prefill's roundings: weights rounded once to act,
- * fp32 sums, causal attention in fp64 rounded once). Writes the chunk's K/V rows, the logits of
+/* The chunk's MoE block for T rows (tests/kernels/pf_moe_ref.h's values: expert weights rounded
+ * once to act, fp32 sums, the down outputs rounded, combine_token's slot-ordered combine with
+ * the residual): route [T][32] (the route rows), x [T][hidden] act, experts + 1 layout-1 gate||up
+ * and down blocks (the shared expert last); resid [T][hidden] act updated in place. */
+void orc_moe_prefill(int act, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                     const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks, const uint32_t* dn_blocks,
+                     uint16_t* resid, uint32_t T);
+/* The chunked prefill of T ids at positions pos .. pos + T - 1 (f16 cache; the walk of
+ * src/runtime/prefill/step.h with the prefill's roundings: weights rounded once to act, fp32
+ * sums, causal attention in fp64 rounded once; an MoE layer's experts as orc_moe_prefill). Writes the chunk's K/V rows, the logits of
  * the last row (the decode head) and returns their argmax (0xFFFFFFFF: unsupported). */
 uint32_t orc_prefill_chunk(int act, const orc_dense_model* m, const uint32_t* ids, uint32_t T, uint32_t pos,
                            uint16_t* kv_k, uint16_t* kv_v, float* logits);

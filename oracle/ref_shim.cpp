@@ -4,7 +4,7 @@
 // Built by oracle/build_oracle.py into oracle/_ref/libref.so; only tests load it.
 //
 // Included reference headers: src/common/{bf16,int4,repack,kv8}.h,
-// tests/kernels/{gemv_ref,gemm_sm_ref,prep_ref,attn_ref,kv8_ref,moe_ref}.h.
+// tests/kernels/{gemv_ref,gemm_sm_ref,prep_ref,attn_ref,kv8_ref,moe_ref,pf_moe_ref}.h.
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -17,6 +17,7 @@
 #include "kernels/gemm_sm_ref.h"
 #include "kernels/kv8_ref.h"
 #include "kernels/moe_ref.h"
+#include "kernels/pf_moe_ref.h"
 #include "kernels/prep_ref.h"
 
 extern "C" {
@@ -191,6 +192,35 @@ void ref_moe_block(const float* logits, uint32_t experts, uint32_t top_k, uint32
 // common/repack.h:118 (the bf16 tile layout gemv_bf16.cl reads; element type agnostic)
 void ref_repack_bf16_tiled(const uint16_t* w_rowmajor, uint32_t K, uint32_t N, uint16_t* out) {
   common::repack_bf16_tiled(w_rowmajor, K, N, out);
+}
+
+// The chunk's MoE block by pf_moe_ref's own pieces (bf16): sort, dequant_block, gemm_rows,
+// silu_row over every row of every live tile (grouped), the down outputs rounded, then
+// combine_token per token and column.
+void ref_pf_moe_block(const uint32_t* route, uint32_t C, const uint16_t* x, const uint32_t* gu, const uint32_t* dn,
+                      uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter, uint16_t* resid_inout) {
+  const moe_ref::Shape s{experts, top_k, hidden, inter, 0};
+  const pf_moe_ref::Sorted st = pf_moe_ref::sort(route, C, s);
+  std::vector<std::vector<uint16_t>> gw(experts + 1), dw(experts + 1);
+  const uint32_t rows = st.rows_used();
+  std::vector<uint16_t> y(size_t(rows) * hidden, 0);
+  pf_moe_ref::grouped(st, 0, experts + 1, [&](uint32_t b, uint32_t r) {
+    const uint32_t tok = st.row_tok[r];
+    if (tok == pf_moe_ref::kNone) return;
+    if (gw[b].empty()) {
+      gw[b] = pf_moe_ref::dequant_block(gu + b * s.gate_up_words(), hidden, 2 * inter);
+      dw[b] = pf_moe_ref::dequant_block(dn + b * s.down_words(), inter, hidden);
+    }
+    const std::vector<float> g = pf_moe_ref::gemm_rows(x + size_t(tok) * hidden, gw[b].data(), hidden, 2 * inter);
+    const std::vector<uint16_t> h = pf_moe_ref::silu_row(g, inter);
+    const std::vector<float> d = pf_moe_ref::gemm_rows(h.data(), dw[b].data(), inter, hidden);
+    for (uint32_t n = 0; n < hidden; ++n) y[size_t(r) * hidden + n] = moe_ref::rne(d[n]);
+  });
+  for (uint32_t t = 0; t < C; ++t)
+    for (uint32_t n = 0; n < hidden; ++n)
+      resid_inout[size_t(t) * hidden + n] = pf_moe_ref::combine_token(st, route + size_t(t) * moe_ref::kWords, y.data(),
+                                                                     hidden, s, t, n,
+                                                                     resid_inout[size_t(t) * hidden + n]);
 }
 
 }  // extern "C"

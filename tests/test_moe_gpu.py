@@ -200,9 +200,10 @@ def test_malformed_route_row_reads_the_shared_block():
 @pytest.mark.parametrize("T,bad", [(1, False), (37, True), (300, False)])
 def test_moe_prefill_matches_decode_kernels(T, bad):
     """mi_moe_prefill (the chunk's expert FFN grouped by expert on the MFMA tile) against the
-    decode kernels (mi_moe_gate_up + mi_moe_down) on the same route rows: within 2 % of the
-    largest output (the prefill rounds each dequantised weight to fp16, the decode kernels
-    multiply exact integers and scale per group). The router GEMV and the route over all T rows
+    oracle of the prefill block (orc_moe_prefill, pf_moe_ref.h's values) at rel 2e-3, and
+    against the decode kernels (mi_moe_gate_up + mi_moe_down) on the same route rows within 2 %
+    of the largest output (the prefill rounds each dequantised weight to fp16, the decode
+    kernels multiply exact integers and scale per group). The router GEMV and the route over all T rows
     in one launch are bitwise the 16-row launches. bad: some route ids outside [0, E), which
     both paths send to the shared expert."""
     mo = Moe(11)
@@ -254,6 +255,16 @@ def test_moe_prefill_matches_decode_kernels(T, bad):
     ref = O.f16_bits_to_f32(want).astype(np.float64)
     assert np.all(np.isfinite(got))
     assert np.max(np.abs(got - ref)) <= 0.02 * np.max(np.abs(ref)), np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    # the oracle of the prefill block (tests/kernels/pf_moe_ref.h's values, pinned bit for bit to
+    # the reference's twin): rel 2e-3 on every row whose ids are all valid (the reference clamps
+    # a bad id to the last expert where this build reads the shared expert)
+    orc = np.zeros((T, H), np.uint16)
+    O.lib().orc_moe_prefill(O.ORC_F16, E, K, H, I, O._p(np.ascontiguousarray(rt_all)), O._p(x), O._p(mo.gu),
+                            O._p(mo.dn), O._p(orc), T)
+    ok = np.all(rt_all[:, :K] < E, axis=1)
+    w = O.f16_bits_to_f32(orc).astype(np.float64)[ok]
+    g = got[ok]
+    assert np.all(np.abs(g - w) <= 2e-3 * np.abs(w) + 2e-3 * np.abs(w).max()), np.abs(g - w).max() / np.abs(w).max()
     # every pair listed once, grouped by expert
     n_tiles = int(host(tiles_n, np.uint32)[0])
     assert sorted(host(lst, np.uint32).tolist()) == list(range(P))

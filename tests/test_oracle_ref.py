@@ -341,3 +341,50 @@ def test_f16w_tile_layout_matches_reference_repack():
     O.lib().orc_f16w_tile(O._p(w), K, N, O._p(a))
     R.ref_repack_bf16_tiled(O._p(w), K, N, O._p(b))
     assert np.array_equal(a, b)
+
+
+def _moe_blocks(E, Hd, I, seed):
+    """E + 1 experts' layout-1 gate||up (interleave16) and down blocks from the reference's
+    random int4 weights"""
+    gu_t, dn_t = [], []
+    for b in range(E + 1):
+        gq, gs = _rand(Hd, I, seed + 3 * b)
+        uq, us = _rand(Hd, I, seed + 1 + 3 * b)
+        oq = np.zeros((Hd // 8, 2 * I), np.uint32); os_ = np.zeros((Hd // 64, 2 * I), np.uint16)
+        L().orc_interleave16_l0(P(gq), P(gs), P(uq), P(us), Hd, I, P(oq), P(os_))
+        t = np.zeros((2 * I // 16) * (Hd // 64) * 136, np.uint32)
+        L().orc_repack_layout1(P(oq), P(os_), Hd, 2 * I, P(t))
+        gu_t.append(t)
+        dq, ds = _rand(I, Hd, seed + 2 + 3 * b)
+        t2 = np.zeros((Hd // 16) * (I // 64) * 136, np.uint32)
+        L().orc_repack_layout1(P(dq), P(ds), I, Hd, P(t2))
+        dn_t.append(t2)
+    return np.ascontiguousarray(np.concatenate(gu_t)), np.ascontiguousarray(np.concatenate(dn_t))
+
+
+@pytest.mark.parametrize("E,K,T", [(16, 4, 37), (32, 8, 21)])
+def test_moe_prefill_bitwise_pf_moe_ref(E, K, T):
+    """orc_moe_prefill (token by token) against pf_moe_ref's sort + dequant_block + gemm_rows +
+    silu_row + grouped walk + combine_token (bf16): every residual bit, with routes that send
+    several tokens to the same experts."""
+    Hd, I = 512, 128
+    gu, dn = _moe_blocks(E, Hd, I, 300 + E)
+    rng = np.random.default_rng(E + T)
+    route = np.zeros((T, 32), np.uint32)
+    for t in range(T):
+        lg = np.zeros(E + 16, np.float32)
+        lg[:E + 1] = rng.uniform(-3, 3, E + 1)
+        if t % 4 == 0:
+            lg[:E] = lg[:E] * 0.05  # near-uniform: many tokens share experts
+        r = O.MoeRoute()
+        L().orc_moe_route_fn(BF, P(lg), E, K, C.byref(r))
+        route[t, :K] = list(r.ids[:K])
+        route[t, 8:8 + K] = np.array(r.w[:K], np.float32).view(np.uint32)
+        route[t, 16] = np.float32(r.sg).view(np.uint32)
+    x = O.f32_to_bf16_bits(rng.uniform(-0.5, 0.5, (T, Hd)).astype(np.float32))
+    resid = O.f32_to_bf16_bits(rng.uniform(-3, 3, (T, Hd)).astype(np.float32))
+    a, b = resid.copy(), resid.copy()
+    L().orc_moe_prefill(BF, E, K, Hd, I, P(route), P(x), P(gu), P(dn), P(a), T)
+    R.ref_pf_moe_block(P(route), T, P(x), P(gu), P(dn), E, K, Hd, I, P(b))
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, resid)

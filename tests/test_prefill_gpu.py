@@ -297,6 +297,36 @@ def test_moe_prefill_matches_ingest():
     eng.close()
 
 
+def test_moe_prefill_vs_oracle_prefill():
+    """The MoE model's chunked prefill against the oracle's prefill walk (orc_prefill_chunk with
+    the experts as orc_moe_prefill, pinned to pf_moe_ref.h): every K/V row and the last logits
+    at rel 2e-3."""
+    from test_engine_gpu import moe_small_desc
+    eng = mi.Engine(moe_small_desc(max_len=512), seed=12)
+    orc = OracleModel(eng)
+    n, p0, chunk = 37, 20, 16
+    ids = np.random.default_rng(3).integers(0, eng.desc.vocab_used, n).astype(np.uint32)
+    print(f"moe prefill vs oracle n={n} p0={p0}", flush=True)
+    eng.reset(p0, 0)
+    eng.prefill(ids, chunk)
+    lg = eng.logits(1)[0].astype(np.float64)
+    k_pf, v_pf = kv_rows(eng, p0, n)
+    want = np.zeros(eng.desc.vocab, np.float32)
+    for c0 in range(0, n, chunk):
+        part = np.ascontiguousarray(ids[c0:c0 + chunk])
+        O.lib().orc_prefill_chunk(O.ORC_F16, C.byref(orc.m), O._p(part), len(part), p0 + c0, O._p(orc.kv_k),
+                                  O._p(orc.kv_v), O._p(want))
+    d = eng.desc
+    kw = orc.kv_k.reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)[:, :, p0:p0 + n]
+    vw = orc.kv_v.reshape(d.layers, d.kv_heads, d.max_len, d.head_dim)[:, :, p0:p0 + n]
+    for a, b in ((k_pf, kw), (v_pf, vw)):
+        b = O.f16_bits_to_f32(b).astype(np.float64)
+        assert np.all(np.abs(a - b) <= 2e-3 * np.abs(b) + 2e-3 * np.abs(b).max()), np.abs(a - b).max()
+    w = want.astype(np.float64)
+    assert close(lg, w), np.abs(lg - w).max() / np.abs(w).max()
+    eng.close()
+
+
 def test_attn_prefill_kv8_rows_match_the_decode_reader():
     """mi_attn_prefill_kv8 over the int8 rotated cache: row t equals the decode reader's
     (attn_decode int8 + attn_reduce_kv8, itself held to fp64 attention with an fp64
