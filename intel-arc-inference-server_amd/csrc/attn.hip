@@ -51,35 +51,49 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   __shared__ float fac[1024];
   __shared__ float s_sm;
   const uint32_t h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+  const size_t PART = HD + 2;
+  const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
+  const size_t bstride = (size_t)M * PART;
+  // The first PRE blocks' values and wave 0's (mx, sm) of blocks d and d + 64 do not depend on
+  // the row's block count nb, so they are loaded before the control words arrive, bounded by
+  // tgt (a slot past nb is read but never added); runs of 16 behind a uniform bound keep a
+  // small tgt's merge to few loads.
+  float v[PRE];
+#pragma unroll
+  for (uint32_t c = 0; c < PRE; c += 16)
+    if (c < tgt) {
+#pragma unroll
+      for (uint32_t u = c; u < c + 16; ++u) v[u] = base[min(u, tgt - 1) * bstride + 2 + d];
+    }
+  float pm[2] = {0.f, 0.f}, ps[2] = {0.f, 0.f};
+  if (d < 64) {
+#pragma unroll
+    for (uint32_t k = 0; k < 2; ++k)
+      if (d + 64u * k < tgt) {
+        pm[k] = base[(d + 64u * k) * bstride];
+        ps[k] = base[(d + 64u * k) * bstride + 1];
+      }
+  }
+  const float gv = gated && attn_gate ? attn_gate[((size_t)m * q_heads + h) * HD + d] : 0.f;
   if (m >= ctrl[CTRL_NACT]) return;  // uniform
   const uint32_t pos = ctrl[CTRL_POS];
   uint32_t L = pos + m + 1;
   if (kv_len && L > kv_len) L = kv_len;
   uint32_t nb = (L - 1) / v2_ppw(L, tgt) + 1;
   if (nb > tgt) nb = tgt;
-  const size_t PART = HD + 2;
-  const float* base = attn_part + ((size_t)h * tgt * M + m) * PART;  // block b at + b * M * PART
-  const size_t bstride = (size_t)M * PART;
-  // (a load past nb re-reads block nb - 1 and is not added)
   constexpr uint32_t BAT = 64;
-  // loads go out in runs of 16 behind a uniform bound, so a short merge issues few of them
-  float v[PRE];
-#pragma unroll
-  for (uint32_t c = 0; c < PRE; c += 16)
-    if (c < nb) {
-#pragma unroll
-      for (uint32_t u = c; u < c + 16; ++u) v[u] = base[min(u, nb - 1) * bstride + 2 + d];
-    }
   // wave 0: the common max and the per-block factors
   if (d < 64) {
+    auto mx_of = [&](uint32_t b) { return b < 128u ? pm[b >> 6] : base[b * bstride]; };
+    auto sm_of = [&](uint32_t b) { return b < 128u ? ps[b >> 6] : base[b * bstride + 1]; };
     float mx = -INFINITY;
-    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, base[b * bstride]);
+    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, mx_of(b));
     mx = wave_max(mx);
     float sm = 0.f;
     for (uint32_t b = d; b < nb; b += 64) {
-      const float f = expf(base[b * bstride] - mx);
+      const float f = expf(mx_of(b) - mx);
       fac[b] = f;
-      sm = __builtin_fmaf(base[b * bstride + 1], f, sm);
+      sm = __builtin_fmaf(sm_of(b), f, sm);
     }
     sm = wave_sum(sm);
     if (d == 0) s_sm = sm;
@@ -109,7 +123,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   }
   uint16_t r;
   if (gated && attn_gate)
-    r = f2h(h2f(f2h(o)) * sigmoid_f32(attn_gate[((size_t)m * q_heads + h) * HD + d]));
+    r = f2h(h2f(f2h(o)) * sigmoid_f32(gv));
   else
     r = f2h(o);
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;

@@ -128,6 +128,20 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
 
   const uint32_t t = opaque_tid(), lane = t & 63u, wave = t >> 6;
   const uint32_t qi = lane & 15u, qq = lane >> 4;
+  // q (plain form): wave 0's loads of the B operand go out before anything else, so waiting
+  // for them later does not wait for the K/V loads issued after them (loads retire in order)
+  constexpr bool QE = !FP && !PS;
+  f4_t qv[QE ? 2u * KK : 1u];
+  if constexpr (QE) {
+    if (wave == 0 && qi < GQA) {
+      const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 8 * qq;
+#pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk) {
+        qv[2 * kk] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk));
+        qv[2 * kk + 1] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk + 4));
+      }
+    }
+  }
   const uint32_t n_act = a.ctrl[CTRL_NACT];
   if (m >= n_act) return;
   const uint32_t pos = a.ctrl[CTRL_POS];
@@ -186,12 +200,16 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
 
   // this wave's first group goes out before anything else: its row straight from the page
   // table, the later groups' rows staged in LDS below
+  // (PF: its second group too, so both are in flight while q is staged)
   Group cur, nxt;
   uint32_t gi = wave;
-  if (gi < ng) {
-    const uint32_t p0 = p_begin + 16u * gi;
-    const uint32_t rb = a.pages ? a.pages[p0 / a.page] * a.page + p0 % a.page : p0;
-    load_group(gi, __builtin_amdgcn_readfirstlane(rb), cur);
+  auto direct_row = [&](uint32_t g) -> uint32_t {
+    const uint32_t p0 = p_begin + 16u * g;
+    return __builtin_amdgcn_readfirstlane(a.pages ? a.pages[p0 / a.page] * a.page + p0 % a.page : p0);
+  };
+  if (gi < ng) load_group(gi, direct_row(gi), cur);
+  if constexpr (PF) {
+    if (gi + 4u < ng) load_group(gi + 4u, direct_row(gi + 4u), nxt);
   }
   // A paged cache: a page holds whole 16-position groups, so a group's rows are consecutive.
   // Each group's first cache row is looked up once, into LDS (the only divisions by the page
@@ -355,9 +373,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
           // q from the head work-items' hand-off words (many readers: emptied later in the step)
           wt->poll8(a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq, v);
         } else {
-          const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq;
-          const f4_t q0 = *reinterpret_cast<const f4_t*>(qp);
-          const f4_t q1 = *reinterpret_cast<const f4_t*>(qp + 4);
+          const f4_t q0 = qv[2 * kk], q1 = qv[2 * kk + 1];
           v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
           v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
         }
@@ -393,7 +409,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   };
   for (; gi < ng; gi += 4u) {
     if constexpr (PF) {
-      if (gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);
+      if (gi != wave && gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);  // (the first: above)
     }
     const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
     if constexpr (FP || PS) {
