@@ -76,6 +76,7 @@ def lib():
             "orc_dense_step": (u32, [i32, vp, u32, u32, vp, vp, vp, u32]),
             "orc_dense_step_kv8": (u32, [i32, vp, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_prefill_chunk": (u32, [i32, vp, vp, u32, u32, vp, vp, vp]),
+            "orc_mtp_head_step": (u32, [i32, vp, vp, u32, vp, u32, vp, vp, i32, vp, vp]),
             "orc_moe_prefill": (None, [i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
@@ -169,6 +170,12 @@ class Layer(C.Structure):
                 ("in_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
                 ("k_norm", C.c_void_p), ("router", C.c_void_p), ("moe_gu", C.c_void_p),
                 ("moe_dn", C.c_void_p)]
+
+
+class MtpHead(C.Structure):
+    """orc_mtp_head: the MTP head's fc, its decoder layer and its three norms."""
+    _fields_ = [("fc", Linear), ("layer", Layer), ("pre_e", C.c_void_p), ("pre_h", C.c_void_p),
+                ("final_norm", C.c_void_p)]
 
 
 class DenseModel(C.Structure):

@@ -1066,6 +1066,71 @@ uint32_t orc_dense_step_kv8(int act, const orc_dense_model* md, uint32_t tok, ui
 }
 
 
+// ---- the MTP head (src/runtime/capture.cc:1772-1939) ----------------------------------------
+uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_head* hd, uint32_t tok,
+                           const uint16_t* h, uint32_t p, uint16_t* kv_k, uint16_t* kv_v, int full,
+                           uint16_t* h_out, float* logits) {
+  const Act A{act};
+  const uint32_t H = md->hidden, HD = md->attn.head_dim, QH = md->attn.q_heads, L = md->max_len;
+  const uint32_t G = H / 64;
+  if (p >= L || hd->fc.K != 2 * H || hd->fc.N != H) return 0xFFFFFFFFu;
+  std::vector<uint16_t> resid(H), hrow(h, h + H), x2(size_t(2) * H), x(H), attn_out(size_t(QH) * HD);
+  std::vector<uint16_t> hbuf(md->inter);
+  std::vector<float> sumsq(G), part, attn_q(size_t(QH) * HD), attn_part;
+  std::vector<float> xf(std::max<size_t>({size_t(2) * H, size_t(QH) * HD, size_t(md->inter)}));
+  const orc_layer& ly = hd->layer;
+  auto linear = [&](const orc_linear& l, const uint16_t* in) {
+    for (uint32_t i = 0; i < l.K; ++i) xf[i] = A.w(in[i]);
+    part.assign(size_t(l.S) * l.N, 0.f);
+    orc_gemv_twin_partials(0, l.qweight, l.scales, l.K, l.N, xf.data(), 1, l.S, part.data());
+  };
+  auto norm = [&](const float* partials, uint32_t s_prev, const float* w) {  // as orc_dense_step's
+    if (md->norm_g == 0) {
+      orc_res_norm(act, partials, resid.data(), w, x.data(), 1, H, s_prev, md->rms_eps);
+    } else {
+      std::vector<float> sq(md->norm_g);
+      orc_res_fold(act, partials, resid.data(), sq.data(), 1, H, s_prev, md->norm_g);
+      orc_norm_finish(act, sq.data(), resid.data(), w, x.data(), 1, H, md->norm_g, md->rms_eps);
+    }
+  };
+  // head_front: enorm(embed(tok)) into x2[0, H), hnorm(h) into x2[H, 2H) (prep_norm_finish with
+  // X_STRIDE = 2 hidden), both after prep_res_fold with nothing to fold
+  if (orc_embed_gather(&tok, 1, md->embed, md->vocab, H, resid.data())) return 0xFFFFFFFFu;
+  orc_res_fold(act, nullptr, resid.data(), sumsq.data(), 1, H, 0, G);
+  orc_norm_finish(act, sumsq.data(), resid.data(), hd->pre_e, x2.data(), 1, H, G, md->rms_eps);
+  orc_res_fold(act, nullptr, hrow.data(), sumsq.data(), 1, H, 0, G);
+  orc_norm_finish(act, sumsq.data(), hrow.data(), hd->pre_h, x2.data() + H, 1, H, G, md->rms_eps);
+  linear(hd->fc, x2.data());
+  // ZERO_RESID (prep.cl:308-309): the residual stream starts at fc's output, rne(sum_s partials)
+  for (uint32_t k = 0; k < H; ++k) {
+    float acc = 0.f;
+    for (uint32_t s = 0; s < hd->fc.S; ++s) acc += part[size_t(s) * H + k];
+    resid[k] = A.rne(acc);
+  }
+  orc_res_fold(act, nullptr, resid.data(), sumsq.data(), 1, H, 0, G);
+  orc_norm_finish(act, sumsq.data(), resid.data(), ly.in_norm, x.data(), 1, H, G, md->rms_eps);
+  linear(ly.qkv, x.data());
+  orc_attn_prep(act, &md->attn, p, 1, 1, part.data(), ly.qkv.S, ly.q_norm, ly.k_norm, md->rope, attn_q.data(),
+                nullptr, kv_k, kv_v, HD, size_t(L) * HD, nullptr, 0);
+  if (!full) return 0;
+  // draft(): the attention pair over the head's keys 0..p, o and the post-attention norm, the MLP,
+  // the head's final norm, the shared lm_head
+  attn_part.assign(size_t(QH) * md->tgt * (HD + 2), 0.f);
+  orc_attn_decode_v2(act, &md->attn, p, 1, 1, md->tgt, attn_q.data(), 0, kv_k, kv_v, nullptr, nullptr, HD,
+                     size_t(L) * HD, 0, 0, nullptr, 0, attn_part.data());
+  orc_attn_reduce_v2(act, &md->attn, p, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
+  linear(ly.o, attn_out.data());
+  norm(part.data(), ly.o.S, ly.post_norm);
+  linear(ly.gate_up, x.data());
+  orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
+  linear(ly.down, hbuf.data());
+  norm(part.data(), ly.down.S, hd->final_norm);
+  if (h_out) std::copy(x.begin(), x.end(), h_out);
+  for (uint32_t i = 0; i < H; ++i) xf[i] = A.w(x[i]);
+  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
+  return orc_argmax(logits, md->vocab, md->vocab_used);
+}
+
 // ---- the chunked prefill (src/runtime/prefill/step.h step_chunk; this build's
 // Engine::prefill_chunk walk) ---------------------------------------------------------------
 // The prefill's own roundings: every int4 weight dequantised ONCE to act, w = rne((q - 8) * s)

@@ -212,6 +212,31 @@ uint32_t orc_dense_step_kv8(int act, const orc_dense_model* m, uint32_t tok, uin
                             int8_t* kv_k, int8_t* kv_v, uint16_t* k_scale, uint16_t* v_scale,
                             float* logits, uint32_t n_layers_run);
 
+/* The MTP head (the model's next-token predictor, src/runtime/capture.cc:1772-1939): a dense
+ * decoder layer behind a projection of [enorm(embed(tok)) | hnorm(h)]. fc: [2 hidden] -> hidden;
+ * layer: its q||k||v, o, gate||up, down and norms (in_norm the head's input norm, post_norm its
+ * post-attention norm); final_norm the head's own output norm (mtp.norm). */
+typedef struct orc_mtp_head {
+  orc_linear fc;
+  orc_layer layer;
+  const float* pre_e; /* the embedding's norm */
+  const float* pre_h; /* the hidden's norm */
+  const float* final_norm;
+} orc_mtp_head;
+/* One head row at head position p for token `tok` and hidden h (act [hidden]: the main model's
+ * post-final-norm hidden of position p, or the head's own output of the previous draft):
+ * head_front (capture.cc:1772-1826: both pre-fc norms into one [2 hidden] row, fc, its output
+ * as the residual (prep.cl ZERO_RESID), the input norm, q||k||v, attn_prep into the head's
+ * one KV layer kv_k / kv_v [kv_heads][max_len][hd] at p). full = 0 stops there (the KV fill,
+ * head_kv_fill :1840) and returns 0. full = 1 runs draft() (:1849-1939): attention over keys
+ * 0..p, o, the post-attention norm, the MLP, the head's final norm into h_out (act [hidden]),
+ * the shared lm_head into logits fp32 [vocab], and returns their argmax. The model's norm_g
+ * sets the norms' order as for orc_dense_step (the head's pre-fc and input norms always take
+ * prep_res_fold + prep_norm_finish over hidden / 64 chunks). */
+uint32_t orc_mtp_head_step(int act, const orc_dense_model* m, const orc_mtp_head* head, uint32_t tok,
+                           const uint16_t* h, uint32_t p, uint16_t* kv_k, uint16_t* kv_v, int full,
+                           uint16_t* h_out, float* logits);
+
 /* The chunk's MoE block for T rows (tests/kernels/pf_moe_ref.h's values: expert weights rounded
  * once to act, fp32 sums, the down outputs rounded, combine_token's slot-ordered combine with
  * the residual): route [T][32] (the route rows), x [T][hidden] act, experts + 1 layout-1 gate||up

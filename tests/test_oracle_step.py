@@ -446,3 +446,164 @@ def test_kv8_bar_rejects_a_missing_unrotation():
     _, got, _ = m.oracle_step_kv8(155, 41)
     want = m.fp64_step_kv8(155, 41, mistake="kv8_rotated_basis")[0]
     assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
+
+
+class TinyMtp(TinyModel):
+    """TinyModel plus an MTP head (capture.cc:1772-1939): fc [2H] -> H, one dense decoder
+    layer with its own one-layer KV cache, the embedding / hidden / final norms; the head
+    shares the model's embedding and lm_head."""
+
+    def __init__(self, seed, **kw):
+        super().__init__(seed, **kw)
+        d = self.d
+        H, QH, KVH, HD, I, L = d["H"], d["QH"], d["KVH"], d["HD"], d["I"], d["L"]
+        rng = np.random.default_rng(seed + 500)
+
+        def lin(K, N, S=2):
+            q = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
+            sc = f16(rng.uniform(0.004, 0.03, (K // 64, N)))
+            self.keep += [q, sc]
+            return O.Linear(q.ctypes.data, sc.ctypes.data, K, N, S), O.int4_dequant(q, sc, K, N).astype(np.float64)
+
+        def gamma(n):
+            a = (1.0 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+            self.keep.append(a)
+            return a
+
+        self.hw = {}
+        fc, self.hw["fc"] = lin(2 * H, H)
+        Ly = O.Layer()
+        lins = []
+        for i, (K, N) in enumerate([(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]):
+            l, w = lin(K, N)
+            lins.append(l)
+            self.hw[i] = w
+        Ly.qkv, Ly.o, Ly.gate_up, Ly.down = lins
+        self.hn = {k: gamma(n) for k, n in (("in_norm", H), ("post_norm", H), ("q_norm", HD), ("k_norm", HD),
+                                           ("pre_e", H), ("pre_h", H), ("final", H))}
+        Ly.in_norm, Ly.post_norm = self.hn["in_norm"].ctypes.data, self.hn["post_norm"].ctypes.data
+        if d["qk_norm"]:
+            Ly.q_norm, Ly.k_norm = self.hn["q_norm"].ctypes.data, self.hn["k_norm"].ctypes.data
+        self.head = O.MtpHead(fc, Ly, self.hn["pre_e"].ctypes.data, self.hn["pre_h"].ctypes.data,
+                              self.hn["final"].ctypes.data)
+        self.hkv_k = f16(rng.standard_normal((KVH, L, HD)))
+        self.hkv_v = f16(rng.standard_normal((KVH, L, HD)))
+
+    def oracle_head(self, tok, h16, p, kk, vv, full=1):
+        logits = np.zeros(self.d["V"], np.float32)
+        hout = np.zeros(self.d["H"], np.uint16)
+        am = O.lib().orc_mtp_head_step(F16, C.byref(self.m), C.byref(self.head), tok, O._p(h16), p, O._p(kk),
+                                       O._p(vv), full, O._p(hout), O._p(logits))
+        return int(am), logits, hout
+
+    def fp64_head(self, tok, h, p, kc, vc, mistake=None):
+        """fp64 forward of the head at position p; h fp64 [H]; kc / vc fp64 [KVH][L][HD]
+        (updated at p). Returns (logits, h_out)."""
+        d = self.d
+        H, QH, KVH, HD, rot, I = d["H"], d["QH"], d["KVH"], d["HD"], d["rot"], d["I"]
+        eps = 1e-6
+
+        def rms(v, w):
+            return v / np.sqrt(np.mean(v * v) + eps) * w
+
+        half = rot // 2
+        rp = p + 1 if mistake == "head_pos" else p
+        cos = self.rope[rp, 0].astype(np.float64)
+        sin = self.rope[rp, 1].astype(np.float64)
+
+        def rope(v):
+            out = v.copy()
+            a, b = v[:half], v[half:rot]
+            out[:half] = a * cos - b * sin
+            out[half:rot] = b * cos + a * sin
+            return out
+
+        e = O.f16_bits_to_f32(self.embed[tok]).astype(np.float64)
+        halves = [rms(e, self.hn["pre_e"]), rms(h, self.hn["pre_h"])]
+        if mistake == "cat_swap":
+            halves = halves[::-1]
+        resid = np.concatenate(halves) @ self.hw["fc"]
+        if mistake == "stale_resid":
+            resid = resid + e
+        x = rms(resid, self.hn["in_norm"])
+        qkv = x @ self.hw[0]
+        q = qkv[:QH * HD].reshape(QH, HD)
+        k = qkv[QH * HD:(QH + KVH) * HD].reshape(KVH, HD)
+        v = qkv[(QH + KVH) * HD:].reshape(KVH, HD)
+        if d["qk_norm"]:
+            q = np.stack([rms(r, self.hn["q_norm"]) for r in q])
+            k = np.stack([rms(r, self.hn["k_norm"]) for r in k])
+        q = np.stack([rope(r) for r in q])
+        k = np.stack([rope(r) for r in k])
+        kc[:, p], vc[:, p] = k, v
+        G = QH // KVH
+        att = np.empty((QH, HD))
+        for hh in range(QH):
+            sc = kc[hh // G, :p + 1] @ q[hh] / np.sqrt(HD)
+            w = np.exp(sc - sc.max())
+            att[hh] = (w / w.sum()) @ vc[hh // G, :p + 1]
+        resid = resid + att.reshape(-1) @ self.hw[1]
+        x = rms(resid, self.hn["post_norm"])
+        gu = x @ self.hw[2]
+        j = np.arange(I)
+        g, u = gu[(j // 16) * 32 + j % 16], gu[(j // 16) * 32 + j % 16 + 16]
+        resid = resid + (g / (1.0 + np.exp(-g)) * u) @ self.hw[3]
+        x = rms(resid, self.hn["final"]) if mistake != "no_final_norm" else resid
+        return x @ self.lm, x
+
+
+def _head_case(m, tok, p, seed):
+    h = O.f16_bits_to_f32(f16(np.random.default_rng(seed).standard_normal(m.d["H"]))).astype(np.float64)
+    return h, f16(h)
+
+
+@pytest.mark.parametrize("seed,p,qk_norm", [(1, 0, True), (2, 29, True), (3, 63, False)])
+def test_mtp_head_vs_independent_fp64_forward(seed, p, qk_norm):
+    """orc_mtp_head_step against an fp64 forward of the head written here: the draft's logits,
+    its output hidden and the K/V row it writes at the head position, and two chained drafts
+    (the second fed the first's id and output hidden), at the dense step's bar; the fill form
+    (full = 0) writes the same K/V row and nothing else."""
+    m = TinyMtp(seed, qk_norm=qk_norm)
+    tok = (seed * 131) % m.d["V"]
+    h, h16 = _head_case(m, tok, p, seed)
+    kk, vv = m.hkv_k.copy(), m.hkv_v.copy()
+    kc = O.f16_bits_to_f32(m.hkv_k).astype(np.float64)
+    vc = O.f16_bits_to_f32(m.hkv_v).astype(np.float64)
+    toks, hs = tok, h16
+    for step in range(2 if p + 1 < m.d["L"] else 1):
+        am, got, hout = m.oracle_head(toks, hs, p + step, kk, vv)
+        want, hwant = m.fp64_head(toks, O.f16_bits_to_f32(hs).astype(np.float64), p + step, kc, vc)
+        scale = np.abs(want).max()
+        assert np.abs(got - want).max() <= 5e-3 * scale, (step, np.abs(got - want).max(), scale)
+        assert np.corrcoef(got, want)[0, 1] > 0.9999
+        top = np.sort(want)[::-1]
+        assert am == int(np.argmax(want)) or top[0] - want[am] <= 1e-2 * scale
+        gh = O.f16_bits_to_f32(hout).astype(np.float64)
+        assert np.abs(gh - hwant).max() <= 2e-2 * np.abs(hwant).max()
+        for a, b in ((kk, kc), (vv, vc)):
+            g = O.f16_bits_to_f32(a[:, p + step]).astype(np.float64)
+            assert np.abs(g - b[:, p + step]).max() <= 2e-2 * np.abs(b[:, p + step]).max()
+        # the second draft: the id the first drafted and the head's own output hidden
+        toks, hs = am, hout
+        kc[:, p + step] = O.f16_bits_to_f32(kk[:, p + step])  # the cache as the oracle holds it
+        vc[:, p + step] = O.f16_bits_to_f32(vv[:, p + step])
+    kf, vf = m.hkv_k.copy(), m.hkv_v.copy()
+    assert m.oracle_head(tok, h16, p, kf, vf, full=0)[0] == 0
+    assert np.array_equal(kf[:, p], kk[:, p]) and np.array_equal(vf[:, p], vv[:, p])
+    mask = np.ones(m.d["L"], bool)
+    mask[p] = False
+    assert np.array_equal(kf[:, mask], m.hkv_k[:, mask]) and np.array_equal(vf[:, mask], m.hkv_v[:, mask])
+
+
+@pytest.mark.parametrize("mistake", ["cat_swap", "stale_resid", "head_pos", "no_final_norm"])
+def test_mtp_bar_rejects_plausible_wiring_mistakes(mistake):
+    """The head's comparison is not vacuous: the fp64 forward with one plausible mistake (the
+    concat halves swapped, the fc output added to a stale residual, the head's RoPE one
+    position off, the final norm dropped) misses the bar."""
+    m = TinyMtp(2)
+    h, h16 = _head_case(m, 77, 29, 2)
+    _, got, _ = m.oracle_head(77, h16, 29, m.hkv_k.copy(), m.hkv_v.copy())
+    kc = O.f16_bits_to_f32(m.hkv_k).astype(np.float64)
+    vc = O.f16_bits_to_f32(m.hkv_v).astype(np.float64)
+    want = m.fp64_head(77, h, 29, kc, vc, mistake=mistake)[0]
+    assert np.abs(got - want).max() > 5e-3 * np.abs(want).max()
