@@ -188,6 +188,14 @@ int mi_res_fold(const float* partials, uint16_t* resid, float* sumsq, uint32_t M
 /* prep_norm_finish (prep.cl:350): x = rne(r * (1/sqrt(sum_g sumsq / K + eps)) * w) */
 int mi_norm_finish(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
                    uint32_t M, uint32_t K, uint32_t G, float eps, void* stream);
+/* mi_res_fold with prep.cl's ZERO_RESID (zero_resid = 1: resid = rne(sum_s partials), the
+ * residual taken as zero - the MTP head's fc fold, capture.cc:1790) */
+int mi_res_fold_ex(const float* partials, uint16_t* resid, float* sumsq, uint32_t M, uint32_t K,
+                   uint32_t S_PREV, uint32_t G, uint32_t zero_resid, void* stream);
+/* mi_norm_finish with prep.cl's X_STRIDE: row m of x at x_out + m * x_stride (the MTP head's
+ * two pre-fc norms into the halves of one [M][2K] row, capture.cc:1784-1788) */
+int mi_norm_finish_ex(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                      size_t x_stride, uint32_t M, uint32_t K, uint32_t G, float eps, void* stream);
 /* prep_res_norm (tests/kernels/prep_ref.h:59-92): both halves in one launch per row */
 int mi_res_norm(const float* partials, uint16_t* resid, const float* norm_w, uint16_t* x_out,
                 uint32_t M, uint32_t K, uint32_t S_PREV, float eps, void* stream);
@@ -419,6 +427,13 @@ typedef struct mi_model_desc {
    * head_dim 256): int8 rows [layers][kv_heads][max_len][head_dim] and fp16 scales
    * [layers][kv_heads][max_len]; the step runs attn_prep_kv8 and the rotated reader pair. */
   uint32_t kv_int8;
+  /* 1: the model's MTP head (loader::MtpHead; the draft lists of capture.cc:1772-1939): fc
+   * [2 hidden] -> hidden behind the embedding's and the hidden's norms, one dense decoder layer
+   * at the model's shapes (mtp_intermediate = inter) with its own one-layer KV cache, the
+   * head's final norm, the shared embedding and lm_head. Dense layers and the f16 cache only.
+   * Every step then also fills the head's K/V (capture.cc:362-370) and mi_engine_draft runs the
+   * draft lists. */
+  uint32_t mtp;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;
@@ -437,7 +452,13 @@ enum {
   /* the persistent step's work-item table, hand-off words and (with MI_STEP_TRACE set in the
    * environment when the step is built) per-item start/end times (diagnostics; empty before
    * mi_engine_persistent) */
-  MI_T_STEP_STAGES, MI_T_STEP_ARENA, MI_T_STEP_TRACE
+  MI_T_STEP_STAGES, MI_T_STEP_ARENA, MI_T_STEP_TRACE,
+  /* the MTP head (mtp): its layer's tensors are the per-layer kinds at layer = layers; these
+   * are its fc, its three norms, its KV layer [kv_heads][max_len][head_dim] f16, the hidden rows
+   * hh [max_rows + 1][hidden] (row 0: the post-final-norm hidden of position pos - 1), the
+   * draft chain's hidden [hidden], its control block and the last draft's logits [vocab] */
+  MI_T_MTP_FC_Q, MI_T_MTP_FC_S, MI_T_MTP_PRE_E, MI_T_MTP_PRE_H, MI_T_MTP_FINAL, MI_T_MTP_KV_K,
+  MI_T_MTP_KV_V, MI_T_MTP_HH, MI_T_MTP_DH, MI_T_MTP_CTRL, MI_T_MTP_LOGITS
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's
@@ -450,7 +471,8 @@ void mi_engine_destroy(mi_engine* e);
 void* mi_engine_stream(mi_engine* e);
 /* Device pointer and size of a weight or buffer (for loading real weights or checks). */
 int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes);
-/* Split-K width of linear `which` (0 qkv, 1 o, 2 gate||up, 3 down, 4 lm_head). */
+/* Split-K width of linear `which` (0 qkv, 1 o, 2 gate||up, 3 down, 4 lm_head, 5 the MTP head's fc:
+ * 0 without the head; the head's own layer takes the widths of 0..3). */
 int mi_engine_linear_s(mi_engine* e, uint32_t which, uint32_t* S);
 /* runtime::build / build_verify (capture.cc:2135-2144): record the M-row step as a graph. */
 int mi_engine_capture(mi_engine* e, uint32_t M);
@@ -489,10 +511,19 @@ int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs);
  * the step's state: reset the engine (mi_engine_reset) before generating again. */
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
- * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. */
+ * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. With the MTP head
+ * the rows' post-final-norm hidden goes to hh rows 1..k+1 and the head's K/V are filled over
+ * hh rows 0..k at positions pos - 1 .. pos + k - 1 (capture.cc:362-370); k > 0 needs pos >= 1. */
 int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);
-/* Engine::commit (engine.cc:927-960): pos = verify_pos + j + 1, cur_token[0] = next. */
+/* Engine::commit (engine.cc:927-960): pos = verify_pos + j + 1, cur_token[0] = next; with the
+ * MTP head, hh row j + 1 (the accepted row's hidden) becomes row 0. */
 int mi_engine_commit(mi_engine* e, uint32_t verify_pos, uint32_t j, uint32_t next);
+/* Engine::draft (engine.h:259-290, capture.cc:1849-1939; mtp models): k (1..3) greedy drafts
+ * from the MTP head at head positions pos - 1 .. pos + k - 2, the first from (hh row 0,
+ * cur_token), each next one from the previous draft's id and the head's own output hidden.
+ * drafts[i] = d_{i+1}; the main model's state is untouched (verify(k) with these ids next).
+ * Needs pos >= 1 and pos + k + 1 <= max_len. */
+int mi_engine_draft(mi_engine* e, uint32_t k, uint32_t* drafts);
 /* ---- checkpoints (src/loader/loader.cc, quant.cc, repack.h, moe.cc; docs/13-loader.md) ----
  * A directory with config.json and *.safetensors of a GPTQ / AutoRound int4 g64 symmetric
  * checkpoint (quantization_config: bits 4, group_size 64, sym true, desc_act false or absent)

@@ -92,6 +92,9 @@ SIGNATURES = {
     "mi_engine_read_ctrl": (i32, [vp, vp]),
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
+    "mi_engine_draft": (i32, [vp, u32, vp]),
+    "mi_res_fold_ex": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "mi_norm_finish_ex": (i32, [vp, vp, vp, vp, sz, u32, u32, u32, f32, vp]),
     "mi_accept_greedy": (u32, [vp, vp, u32, vp]),
     "mi_norm_rows": (i32, [vp, vp, vp, vp, u32, u32, f32, vp]),
     "mi_gemv_f16w": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
@@ -178,17 +181,19 @@ class ModelDesc(C.Structure):
                 ("head_dim", u32), ("rot_dim", u32), ("inter", u32), ("vocab", u32),
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
                 ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
-                ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32)]
+                ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32),
+                ("mtp", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
                rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
-               rope_theta=1e6, rms_eps=1e-6, kv_int8=0):
+               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0):
     d = ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
                   head_dim if rot_dim is None else rot_dim, inter, vocab,
                   vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
                   attn_tgt, rope_theta, rms_eps)
     d.kv_int8 = kv_int8
+    d.mtp = mtp
     return d
 
 
@@ -235,7 +240,8 @@ def desc_27b(max_len=4096 + 512):
  T_Q_NORM, T_K_NORM, T_ROUTER, T_MOE_GU, T_MOE_DN) = range(15)
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_STEP_STAGES,
- T_STEP_ARENA, T_STEP_TRACE) = range(32, 52)
+ T_STEP_ARENA, T_STEP_TRACE, T_MTP_FC_Q, T_MTP_FC_S, T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K,
+ T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS) = range(32, 63)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 
@@ -348,6 +354,13 @@ class Engine:
 
     def commit(self, verify_pos, j, nxt):
         check(lib().mi_engine_commit(self._h, verify_pos, j, nxt), "engine_commit")
+
+    def draft(self, k):
+        """Engine::draft: k greedy drafts from the MTP head (mtp models)."""
+        import numpy as np
+        out = np.zeros(k, np.uint32)
+        check(lib().mi_engine_draft(self._h, k, out.ctypes.data), "engine_draft")
+        return out
 
     def logits(self, rows=1):
         import numpy as np

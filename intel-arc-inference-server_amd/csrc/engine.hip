@@ -70,9 +70,44 @@ __global__ void ctrl_set_rows_kernel(uint32_t* ctrl, uint32_t pos, uint32_t n_ac
   if (t < n_ids) ctrl[MI_CTRL_CUR + t] = ids[t];
 }
 
+// The MTP head's control block for the K/V fill over a step's M rows (capture.cc:362-370):
+// row r pairs hh row r (the hidden of position pos - 1 + r) with the row's id at head position
+// pos - 1 + r. At pos 0 there is no h_{-1}: no row is filled (n_active 0).
+__global__ void mtp_fill_ctrl_kernel(const uint32_t* ctrl, uint32_t* hctl, uint32_t M) {
+  const uint32_t t = threadIdx.x, pos = ctrl[MI_CTRL_POS];
+  if (t == 0) {
+    hctl[MI_CTRL_POS] = pos ? pos - 1u : 0u;
+    hctl[MI_CTRL_NACT] = pos ? ctrl[MI_CTRL_NACT] : 0u;
+  }
+  if (t < M) hctl[MI_CTRL_CUR + t] = ctrl[MI_CTRL_CUR + t];
+}
+// Engine::draft's start: head position pos - 1, the pending id, the chain's hidden = hh row 0.
+__global__ void mtp_draft_begin_kernel(const uint32_t* ctrl, uint32_t* hctl, const uint16_t* hh0, uint16_t* dh,
+                                       uint32_t H) {
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {
+    hctl[MI_CTRL_POS] = ctrl[MI_CTRL_POS] - 1u;
+    hctl[MI_CTRL_NACT] = 1u;
+    hctl[MI_CTRL_CUR] = ctrl[MI_CTRL_CUR];
+    hctl[MI_CTRL_STEPS] = 0u;
+  }
+  for (uint32_t i = t; i < H; i += blockDim.x) dh[i] = hh0[i];
+}
+
 }  // namespace
 
 constexpr uint32_t kPrefillCap = 2048;  // positions per prefill chunk at most (the reference's default cap)
+constexpr uint32_t kMaxDraft = 3;       // draft lists per iteration (MtpBuffers::kMaxK, engine.h:280)
+
+// The MTP head's weights (loader::MtpHead): fc behind the two pre-fc norms, one dense decoder
+// layer, the head's final norm.
+struct MtpHead {
+  Linear fc;
+  Layer L;
+  float* pre_e = nullptr;
+  float* pre_h = nullptr;
+  float* final_n = nullptr;
+};
 
 struct mi_engine {
   mi_model_desc d{};
@@ -118,6 +153,18 @@ struct mi_engine {
   size_t gu_block = 0, dn_block = 0;  // u32 per expert block
   mi_attn_shape ash{};
   hipGraphExec_t graphs[17] = {};
+  // the MTP head (d.mtp): weights, its one-layer KV cache, the hidden rows, the draft chain
+  MtpHead mh;
+  uint16_t* hkv_k = nullptr;  // [kv_heads][max_len][head_dim] f16
+  uint16_t* hkv_v = nullptr;
+  uint16_t* hh = nullptr;     // [max_rows + 1][hidden]: row 0 = h_{pos-1}, rows 1.. the step's rows
+  uint16_t* dh = nullptr;     // [hidden] the draft chain's hidden
+  uint16_t* hx2 = nullptr;    // [max_rows][2 hidden] fc's input
+  float* hsumsq = nullptr;    // [hidden / 64][max_rows] the head's norm chunk sums
+  uint32_t* hctl = nullptr;   // the head's control block
+  uint32_t* hhist = nullptr;  // [max_len] the drafted ids (the head's argmax history)
+  float* hlogits = nullptr;   // [vocab] the last draft's logits
+  hipGraphExec_t draft_graph = nullptr;
   mi::StepPlan* step = nullptr;  // the persistent one-launch step (M = 1), when enabled
   bool use_step = false;
 
@@ -125,6 +172,7 @@ struct mi_engine {
     if (step) mi::step_plan_destroy(step);
     for (auto& g : graphs)
       if (g) hipGraphExecDestroy(g);
+    if (draft_graph) hipGraphExecDestroy(draft_graph);
     for (void* p : allocs) hipFree(p);
     if (own_stream && stream) hipStreamDestroy(stream);
   }
@@ -205,6 +253,31 @@ struct mi_engine {
         if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S) * R * l->N);
       part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(R, 4u) * L.qkv.N);  // QKV: all S slices
     }
+    if (m.mtp) {  // the head: fc (plain partials) and a dense layer at the model's shapes
+      MI_TRY(alloc_linear(mh.fc, 2 * H, H, 0));
+      Layer& L = mh.L;
+      MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_QKV));
+      MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
+      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
+      MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
+      for (float** nw : {&L.in_norm, &L.post_norm, &mh.pre_e, &mh.pre_h, &mh.final_n}) MI_TRY(alloc(nw, H));
+      if (m.qk_norm) {
+        MI_TRY(alloc(&L.q_norm, HD));
+        MI_TRY(alloc(&L.k_norm, HD));
+      }
+      part_max = std::max({part_max, size_t(mh.fc.S) * R * H, size_t(L.qkv.S) * R * L.qkv.N});
+      MI_TRY(alloc(&hkv_k, size_t(KVH) * m.max_len * HD));
+      MI_TRY(alloc(&hkv_v, size_t(KVH) * m.max_len * HD));
+      MI_TRY(alloc(&hh, size_t(R + 1) * H));
+      MI_TRY(alloc(&dh, H));
+      MI_TRY(alloc(&hx2, size_t(R) * 2 * H));
+      MI_TRY(alloc(&hsumsq, size_t(H / 64) * R));
+      MI_TRY(alloc(&hctl, MI_CTRL_WORDS));
+      MI_TRY(alloc(&hhist, m.max_len));
+      MI_TRY(alloc(&hlogits, m.vocab));
+      MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(hctl, 0, MI_CTRL_WORDS * 4, stream)), "hctl clear"));
+      MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(hh, 0, size_t(R + 1) * H * 2, stream)), "hh clear"));
+    }
     MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
     part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * R * m.vocab);
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
@@ -264,6 +337,17 @@ struct mi_engine {
         MI_TRY(mi_fill_f32(L.q_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
         MI_TRY(mi_fill_f32(L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
       }
+    }
+    if (m.mtp) {
+      for (Linear* l : {&mh.fc, &mh.L.qkv, &mh.L.o, &mh.L.gate_up, &mh.L.down}) MI_TRY(init_linear(*l, seed));
+      for (float* nw : {mh.L.in_norm, mh.L.post_norm, mh.pre_e, mh.pre_h, mh.final_n})
+        MI_TRY(mi_fill_f32(nw, H, seed++, 1, 1.0f, 0.02f, 1, stream));
+      if (m.qk_norm) {
+        MI_TRY(mi_fill_f32(mh.L.q_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+        MI_TRY(mi_fill_f32(mh.L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+      }
+      MI_TRY(mi_fill_f16(hkv_k, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
+      MI_TRY(mi_fill_f16(hkv_v, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
     }
     MI_TRY(init_linear(lm_head, seed));
     MI_TRY(mi_fill_f16(embed, size_t(m.vocab) * H, seed++, 1, 0.0f, 1.0f, stream));
@@ -325,10 +409,13 @@ struct mi_engine {
   int enqueue_step(uint32_t M) {
     const uint32_t HD = d.head_dim, KVH = d.kv_heads;
     const size_t layer_kv = size_t(KVH) * d.max_len * HD;
+    if (d.mtp) {  // the head's control block for this step's K/V fill, before argmax moves ctrl
+      mtp_fill_ctrl_kernel<<<1, 64, 0, stream>>>(ctrl, hctl, M);
+      MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "mtp_fill_ctrl"));
+    }
     MI_TRY(mi_embed_norm(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      const bool qkv_fused = qkv_is_fused(M);
       MI_TRY(launch_qkv(li, M));
       if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
         int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
@@ -347,20 +434,9 @@ struct mi_engine {
         // 4096, 33 blocks per kv head, that costs more than the separate launch saves.)
         uint16_t* lk = static_cast<uint16_t*>(kv_k) + li * layer_kv;
         uint16_t* lv = static_cast<uint16_t*>(kv_v) + li * layer_kv;
-        if (!qkv_fused)
-          MI_TRY(mi_attn_prep(ctrl, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv,
-                              HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
-        // verify_attn.h's rule: the many-row kernel for the lists it binds (16, 32, 64 rows at
-        // 16 / 2 heads), else the decode kernel (every list this engine builds: M <= 8)
-        if (mi_attn_verify_binds(M, 0, d.q_heads, d.kv_heads))
-          MI_TRY(mi_attn_verify(ctrl, attn_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, attn_part,
-                                M, d.attn_tgt, &ash, stream));
-        else
-          MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0,
-                                nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
-        MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+        MI_TRY(attn_pair(L, ctrl, lk, lv, M, !qkv_is_fused(M)));
       }
-      MI_TRY(launch_o(li, M));
+      MI_TRY(launch_o(L, M));
       const float* next_w = next_norm(li);
       if (d.experts) {
         // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
@@ -372,12 +448,55 @@ struct mi_engine {
         MI_TRY(mi_norm_rows(resid, next_w, x, rstd, M, d.hidden, d.rms_eps, stream));
         continue;
       }
-      MI_TRY(launch_gate_up(li, M));
-      MI_TRY(launch_down(li, M));
+      MI_TRY(launch_gate_up(L, M));
+      MI_TRY(launch_down(L, M, next_w));
     }
-    MI_TRY(launch_lm_head(M));
+    MI_TRY(launch_lm_head(M, logits));
     MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
+    if (d.mtp) {
+      // capture.cc:362-370: the rows' post-final-norm hidden (what lm_head read) into hh rows
+      // 1..M, then the head's K/V over hh rows 0..M-1; a single-row step commits its row at
+      // once (hh row 1 becomes row 0), as generate's verify(0) + commit(0) does
+      const size_t row = size_t(d.hidden) * 2;
+      MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(hh + d.hidden, x, row * M, hipMemcpyDeviceToDevice, stream)),
+                    "hh rows"));
+      MI_TRY(head_front(hh, M));
+      if (M == 1)
+        MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(hh, hh + d.hidden, row, hipMemcpyDeviceToDevice, stream)),
+                      "hh commit"));
+    }
     return 0;
+  }
+
+  // ---- the MTP head (capture.cc:1772-1939) ----
+  // head_front over M rows on the head's control block: enorm(embed(id)) and hnorm(hid row)
+  // into the two halves of fc's input row (prep_norm_finish with X_STRIDE), fc, its output as
+  // the head's residual (prep_res_fold ZERO_RESID) and the input norm, then q||k||v with
+  // attn_prep into the head's KV layer at the head positions hctl.pos + r.
+  int head_front(uint16_t* hid, uint32_t M) {
+    const uint32_t H = d.hidden, G = H / 64;
+    MI_TRY(mi_embed_gather(hctl, embed, resid, M, H, d.vocab, stream));
+    MI_TRY(mi_res_fold(nullptr, resid, hsumsq, M, H, 0, G, stream));
+    MI_TRY(mi_norm_finish_ex(hsumsq, resid, mh.pre_e, hx2, size_t(2) * H, M, H, G, d.rms_eps, stream));
+    MI_TRY(mi_res_fold(nullptr, hid, hsumsq, M, H, 0, G, stream));
+    MI_TRY(mi_norm_finish_ex(hsumsq, hid, mh.pre_h, hx2 + H, size_t(2) * H, M, H, G, d.rms_eps, stream));
+    MI_TRY(mi_gemv_w4a16(mh.fc.q, mh.fc.s, hx2, part, M, mh.fc.K, mh.fc.N, mh.fc.S, stream));
+    MI_TRY(mi_res_fold_ex(part, resid, hsumsq, M, H, mh.fc.S, G, 1, stream));
+    MI_TRY(mi_norm_finish(hsumsq, resid, mh.L.in_norm, x, M, H, G, d.rms_eps, stream));
+    return launch_qkv_on(mh.L, hctl, hkv_k, hkv_v, M, true);
+  }
+  // draft() (capture.cc:1849-1939): the whole head at one row on hctl, from (hctl's id, dh);
+  // its final-normed hidden back into dh, its logits into hlogits, the argmax into hctl
+  int enqueue_draft() {
+    MI_TRY(head_front(dh, 1));
+    MI_TRY(attn_pair(mh.L, hctl, hkv_k, hkv_v, 1, false));
+    MI_TRY(launch_o(mh.L, 1));
+    MI_TRY(launch_gate_up(mh.L, 1));
+    MI_TRY(launch_down(mh.L, 1, mh.final_n));
+    MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(dh, x, size_t(d.hidden) * 2, hipMemcpyDeviceToDevice, stream)),
+                  "dh"));
+    MI_TRY(launch_lm_head(1, hlogits));
+    return mi_argmax_finish(hctl, argmax_part, d.vocab / 64, hhist, d.max_len, stream);
   }
 
   // ---- the step's int4 GEMV launches, one per linear, as enqueue_step issues them ----
@@ -386,23 +505,35 @@ struct mi_engine {
   }
   const float* next_norm(uint32_t li) const { return li + 1 < d.layers ? layer[li + 1].in_norm : final_norm; }
 
-  // the qkv GEMV; with the f16 cache and M <= 4, attn_prep inside it (one consumer work-group
-  // per head), else plain partials for mi_attn_prep / mi_attn_prep_kv8
+  // the qkv GEMV of layer li; with the f16 cache and M <= 4, attn_prep inside it (one consumer
+  // work-group per head), else plain partials for mi_attn_prep / mi_attn_prep_kv8
   int launch_qkv(uint32_t li, uint32_t M) {
-    const Layer& L = layer[li];
-    if (!qkv_is_fused(M)) return mi_gemv_w4a16(L.qkv.q, L.qkv.s, x, part, M, L.qkv.K, L.qkv.N, L.qkv.S, stream);
+    const size_t layer_kv = size_t(d.kv_heads) * d.max_len * d.head_dim;
+    if (d.kv_int8) return mi_gemv_w4a16(layer[li].qkv.q, layer[li].qkv.s, x, part, M, layer[li].qkv.K,
+                                        layer[li].qkv.N, layer[li].qkv.S, stream);
+    return launch_qkv_on(layer[li], ctrl, static_cast<uint16_t*>(kv_k) + li * layer_kv,
+                         static_cast<uint16_t*>(kv_v) + li * layer_kv, M, false);
+  }
+  // layer L's qkv on control block c, K/V rows into the f16 layer lk / lv; prep: run attn_prep
+  // here too when it is not fused (M > 4)
+  int launch_qkv_on(const Layer& L, uint32_t* c, uint16_t* lk, uint16_t* lv, uint32_t M, bool prep) {
     const uint32_t HD = d.head_dim;
-    const size_t layer_kv = size_t(d.kv_heads) * d.max_len * HD;
+    if (!qkv_is_fused(M)) {
+      MI_TRY(mi_gemv_w4a16(L.qkv.q, L.qkv.s, x, part, M, L.qkv.K, L.qkv.N, L.qkv.S, stream));
+      return prep ? mi_attn_prep(c, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv, HD,
+                                 size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream)
+                  : 0;
+    }
     mi_gemv_epilogue eq{};
     eq.kind = MI_EPI_QKV;
-    eq.ctrl = ctrl;
+    eq.ctrl = c;
     eq.shape = &ash;
     eq.q_norm = L.q_norm;
     eq.k_norm = L.k_norm;
     eq.rope = rope;
     eq.attn_q = attn_q;
-    eq.kv_k = static_cast<uint16_t*>(kv_k) + li * layer_kv;
-    eq.kv_v = static_cast<uint16_t*>(kv_v) + li * layer_kv;
+    eq.kv_k = lk;
+    eq.kv_v = lv;
     eq.row_stride = HD;
     eq.head_stride = size_t(d.max_len) * HD;
     eq.kv_len = d.max_len;
@@ -410,15 +541,30 @@ struct mi_engine {
     eq.arrive = use_arrive ? arrive : nullptr;
     return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream);
   }
+  // the f16 cache's attention pair on control block c over the layer lk / lv: attn_prep first
+  // when `prep` (the qkv launch did not fuse it); verify_attn.h's rule picks the many-row kernel for
+  // the lists it binds (16, 32, 64 rows at 16 / 2 heads), else the decode kernel (every list
+  // this engine builds: M <= 8); then the merge
+  int attn_pair(const Layer& L, uint32_t* c, uint16_t* lk, uint16_t* lv, uint32_t M, bool prep) {
+    const uint32_t HD = d.head_dim;
+    if (prep)
+      MI_TRY(mi_attn_prep(c, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv, HD,
+                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream));
+    if (mi_attn_verify_binds(M, 0, d.q_heads, d.kv_heads))
+      MI_TRY(mi_attn_verify(c, attn_q, lk, lv, HD, size_t(d.max_len) * HD, nullptr, 0, d.max_len, attn_part, M,
+                            d.attn_tgt, &ash, stream));
+    else
+      MI_TRY(mi_attn_decode(c, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0, nullptr, 0,
+                            d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+    return mi_attn_reduce(c, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream);
+  }
   // o with the residual fold and the post-attention norm
-  int launch_o(uint32_t li, uint32_t M) {
-    const Layer& L = layer[li];
+  int launch_o(const Layer& L, uint32_t M) {
     const mi_gemv_epilogue eo = resid_epi(L.post_norm);
     return mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream);
   }
   // gate||up with silu * up
-  int launch_gate_up(uint32_t li, uint32_t M) {
-    const Layer& L = layer[li];
+  int launch_gate_up(const Layer& L, uint32_t M) {
     mi_gemv_epilogue eg{};
     eg.kind = MI_EPI_SILU;
     eg.h = hbuf;
@@ -427,17 +573,16 @@ struct mi_engine {
     return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                             stream);
   }
-  // down with the residual fold and the next layer's (or the final) norm
-  int launch_down(uint32_t li, uint32_t M) {
-    const Layer& L = layer[li];
-    const mi_gemv_epilogue ed = resid_epi(next_norm(li));
+  // down with the residual fold and the next norm (the next layer's, the final one, the head's)
+  int launch_down(const Layer& L, uint32_t M, const float* next_w) {
+    const mi_gemv_epilogue ed = resid_epi(next_w);
     return mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream);
   }
   // the lm_head with the logits and the per-tile argmax
-  int launch_lm_head(uint32_t M) {
+  int launch_lm_head(uint32_t M, float* out) {
     mi_gemv_epilogue el{};
     el.kind = MI_EPI_LOGITS;
-    el.logits = logits;
+    el.logits = out;
     el.argmax_part = argmax_part;
     el.vocab_used = d.vocab_used;
     el.status = ctrl + MI_CTRL_DEBUG;
@@ -456,10 +601,10 @@ struct mi_engine {
     auto one = [&](uint32_t li) -> int {
       switch (which) {
         case 0: return launch_qkv(li, 1);
-        case 1: return launch_o(li, 1);
-        case 2: return launch_gate_up(li, 1);
-        case 3: return launch_down(li, 1);
-        default: return launch_lm_head(1);
+        case 1: return launch_o(layer[li], 1);
+        case 2: return launch_gate_up(layer[li], 1);
+        case 3: return launch_down(layer[li], 1, next_norm(li));
+        default: return launch_lm_head(1, logits);
       }
     };
     const uint32_t per_round = which == 4 ? 1u : d.layers;
@@ -497,6 +642,67 @@ struct mi_engine {
     return mi_hip(e3, "hipGraphInstantiate");
   }
 
+  int capture_draft() {
+    if (draft_graph) return 0;
+    hipGraph_t g = nullptr;
+    MI_TRY(mi_hip(static_cast<int>(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal)),
+                  "hipStreamBeginCapture"));
+    const int e = enqueue_draft();
+    const int e2 = static_cast<int>(hipStreamEndCapture(stream, &g));
+    if (e != 0) {
+      if (g) hipGraphDestroy(g);
+      return e;
+    }
+    MI_TRY(mi_hip(e2, "hipStreamEndCapture"));
+    const int e3 = static_cast<int>(hipGraphInstantiate(&draft_graph, g, nullptr, nullptr, 0));
+    hipGraphDestroy(g);
+    return mi_hip(e3, "hipGraphInstantiate");
+  }
+
+  // Engine::draft (engine.h:259-290): k draft lists, each one replay of the draft graph
+  int draft(uint32_t k, uint32_t* out) {
+    if (!d.mtp) return mi_fail(MI_ERR_STATE, "engine_draft: the model has no MTP head");
+    if (k == 0 || k > kMaxDraft || !out) return mi_fail(MI_ERR_ARG, "engine_draft: k must be 1..3");
+    uint32_t c[MI_CTRL_WORDS];
+    MI_TRY(read_ctrl(c));
+    if (c[MI_CTRL_POS] == 0 || c[MI_CTRL_POS] + k + 1 > d.max_len)
+      return mi_fail(MI_ERR_ARG, "engine_draft: needs 1 <= pos and pos + k + 1 <= max_len");
+    MI_TRY(capture_draft());
+    mtp_draft_begin_kernel<<<1, 256, 0, stream>>>(ctrl, hctl, hh, dh, d.hidden);
+    MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "mtp_draft_begin"));
+    for (uint32_t i = 0; i < k; ++i)
+      MI_TRY(mi_hip(static_cast<int>(hipGraphLaunch(draft_graph, stream)), "draft hipGraphLaunch"));
+    MI_TRY(mi_memcpy_d2h(out, hhist, size_t(k) * 4, stream));
+    MI_TRY(mi_stream_sync(stream));
+    return check_handoff();
+  }
+
+  // step_mtp_kv (src/runtime/prefill/step.h:181-196) for a prefill chunk of T positions from
+  // pos whose final-normed rows are in pf_x: the head's K/V at positions pos - 1 + r from
+  // (h_{pos-1+r}, ids[r]) - hh row 0 for r = 0, pf_x row r - 1 after (at pos 0 from r = 1) -
+  // in groups of max_rows rows through head_front, the decode step's own launches; then hh row
+  // 0 = the chunk's last row.
+  int prefill_head_fill(const uint32_t* ids_chunk, uint32_t pos, uint32_t T) {
+    const size_t row = size_t(d.hidden) * 2;
+    for (uint32_t r = pos == 0 ? 1u : 0u; r < T;) {
+      const uint32_t n = std::min(d.max_rows, T - r);
+      if (r == 0) {
+        if (n > 1)
+          MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(hh + d.hidden, pf_x, row * (n - 1), hipMemcpyDeviceToDevice,
+                                                        stream)), "hh rows"));
+      } else {
+        MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(hh, pf_x + size_t(r - 1) * d.hidden, row * n,
+                                                      hipMemcpyDeviceToDevice, stream)), "hh rows"));
+      }
+      ctrl_set_rows_kernel<<<1, 64, 0, stream>>>(hctl, pos + r - 1, n, ids_chunk + r, n);
+      MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "head ctrl"));
+      MI_TRY(head_front(hh, n));
+      r += n;
+    }
+    return mi_hip(static_cast<int>(hipMemcpyAsync(hh, pf_x + size_t(T - 1) * d.hidden, row, hipMemcpyDeviceToDevice,
+                                                  stream)), "hh row 0");
+  }
+
   // The persistent step (step.h) for single-row steps: the same step as the M = 1 graph in one
   // launch. Dense layers with an f16 cache only (MI_ERR_SHAPE otherwise).
   int enable_step(bool on) {
@@ -505,7 +711,8 @@ struct mi_engine {
       return 0;
     }
     if (!step) {
-      if (d.experts || d.kv_int8) return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache only");
+      if (d.experts || d.kv_int8 || d.mtp)
+        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache only, no MTP head");
       std::vector<mi::StepLayerW> lw(d.layers);
       auto sl = [](const Linear& l) { return mi::StepLinear{l.q, l.s, l.K, l.N, l.S}; };
       for (uint32_t li = 0; li < d.layers; ++li) {
@@ -683,6 +890,7 @@ struct mi_engine {
     for (uint32_t c0 = 0; c0 < n; c0 += chunk) {
       T = std::min(chunk, n - c0);
       MI_TRY(prefill_chunk(pf_ids + c0, pos0 + c0, T));
+      if (d.mtp) MI_TRY(prefill_head_fill(pf_ids + c0, pos0 + c0, T));
     }
     // the last position's head and argmax, on the decode control block: the step at pos0 + n - 1
     // leaves cur_token = its argmax and pos = pos0 + n, as ingest's last replay would
@@ -717,6 +925,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
+      m.mtp > 1 || (m.mtp && (m.experts || m.kv_int8)) ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {
@@ -749,8 +958,12 @@ void* mi_engine_stream(mi_engine* e) { return e ? e->stream : nullptr; }
 int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes) {
   if (!e || !ptr) return mi_fail(MI_ERR_ARG, "engine_tensor: null");
   const mi_model_desc& m = e->d;
-  if (kind < MI_T_EMBED && layer >= m.layers) return mi_fail(MI_ERR_ARG, "engine_tensor: layer out of range");
-  const Layer* L = kind < MI_T_EMBED ? &e->layer[layer] : nullptr;
+  // per-layer kinds at layer == layers: the MTP head's layer
+  if (kind < MI_T_EMBED && layer >= m.layers + (m.mtp ? 1u : 0u))
+    return mi_fail(MI_ERR_ARG, "engine_tensor: layer out of range");
+  if (kind >= MI_T_MTP_FC_Q && !m.mtp) return mi_fail(MI_ERR_ARG, "engine_tensor: the model has no MTP head");
+  const Layer* L = kind < MI_T_EMBED ? (layer == m.layers ? &e->mh.L : &e->layer[layer]) : nullptr;
+  const size_t hkvb = size_t(m.kv_heads) * m.max_len * m.head_dim * 2;
   auto lin_q = [](const Linear& l, void** p, size_t* b) { *p = l.q; if (b) *b = size_t(l.K / 8) * l.N * 4; };
   auto lin_s = [](const Linear& l, void** p, size_t* b) { *p = l.s; if (b) *b = size_t(l.K / 64) * l.N * 2; };
   size_t b = 0;
@@ -792,6 +1005,17 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_STEP_STAGES: mi::step_plan_debug(e->step, 0, ptr, &b); break;
     case MI_T_STEP_ARENA: mi::step_plan_debug(e->step, 1, ptr, &b); break;
     case MI_T_STEP_TRACE: mi::step_plan_debug(e->step, 2, ptr, &b); break;
+    case MI_T_MTP_FC_Q: lin_q(e->mh.fc, ptr, &b); break;
+    case MI_T_MTP_FC_S: lin_s(e->mh.fc, ptr, &b); break;
+    case MI_T_MTP_PRE_E: *ptr = e->mh.pre_e; b = size_t(m.hidden) * 4; break;
+    case MI_T_MTP_PRE_H: *ptr = e->mh.pre_h; b = size_t(m.hidden) * 4; break;
+    case MI_T_MTP_FINAL: *ptr = e->mh.final_n; b = size_t(m.hidden) * 4; break;
+    case MI_T_MTP_KV_K: *ptr = e->hkv_k; b = hkvb; break;
+    case MI_T_MTP_KV_V: *ptr = e->hkv_v; b = hkvb; break;
+    case MI_T_MTP_HH: *ptr = e->hh; b = size_t(m.max_rows + 1) * m.hidden * 2; break;
+    case MI_T_MTP_DH: *ptr = e->dh; b = size_t(m.hidden) * 2; break;
+    case MI_T_MTP_CTRL: *ptr = e->hctl; b = MI_CTRL_WORDS * 4; break;
+    case MI_T_MTP_LOGITS: *ptr = e->hlogits; b = size_t(m.vocab) * 4; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;
@@ -807,7 +1031,8 @@ int mi_engine_linear_s(mi_engine* e, uint32_t which, uint32_t* S) {
     case 2: *S = L.gate_up.q ? L.gate_up.S : 0; break;  // 0: a MoE model has no dense MLP
     case 3: *S = L.down.q ? L.down.S : 0; break;
     case 4: *S = e->lm_head.S; break;
-    default: return mi_fail(MI_ERR_ARG, "engine_linear_s: which 0..4");
+    case 5: *S = e->mh.fc.q ? e->mh.fc.S : 0; break;  // the MTP head's fc (0: no head)
+    default: return mi_fail(MI_ERR_ARG, "engine_linear_s: which 0..5");
   }
   return 0;
 }
@@ -893,6 +1118,8 @@ int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t*
   uint32_t c[MI_CTRL_WORDS];
   MI_TRY(e->read_ctrl(c));
   if (c[MI_CTRL_POS] + k + 1 > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_verify: past the KV cache");
+  if (e->d.mtp && k && c[MI_CTRL_POS] == 0)
+    return mi_fail(MI_ERR_ARG, "engine_verify: with the MTP head, drafts need pos >= 1 (engine.h:277)");
   std::vector<uint32_t> ids(k + 1);
   ids[0] = c[MI_CTRL_CUR];
   for (uint32_t i = 0; i < k; ++i) ids[i + 1] = drafts[i];
@@ -909,7 +1136,18 @@ int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t*
 // Engine::commit (engine.cc:927-960): j accepted drafts, next token = argmax row j.
 int mi_engine_commit(mi_engine* e, uint32_t verify_pos, uint32_t j, uint32_t next) {
   if (!e) return mi_fail(MI_ERR_ARG, "engine_commit: null");
+  if (e->d.mtp) {  // the accepted row's hidden becomes h_{pos-1}
+    if (j + 1 > e->d.max_rows) return mi_fail(MI_ERR_ARG, "engine_commit: j beyond the verify rows");
+    const size_t row = size_t(e->d.hidden) * 2;
+    MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(e->hh, e->hh + size_t(j + 1) * e->d.hidden, row,
+                                                  hipMemcpyDeviceToDevice, e->stream)), "hh commit"));
+  }
   return e->set_rows(verify_pos + j + 1, 1, &next, 1);
+}
+
+int mi_engine_draft(mi_engine* e, uint32_t k, uint32_t* drafts) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_draft: null");
+  return e->draft(k, drafts);
 }
 
 }  // extern "C"

@@ -68,21 +68,23 @@ __device__ __forceinline__ float tree_hd(float v, float* lds, uint32_t HD) {
   return r;
 }
 
-// r_b = rne(resid + rne(sum_s partials)), or resid when S_PREV == 0
+// r_b = rne(resid + rne(sum_s partials)), or resid when S_PREV == 0; ZERO (prep.cl's
+// ZERO_RESID, the MTP head's fc fold): r_b = rne(sum_s partials), the residual taken as zero
 __device__ __forceinline__ uint16_t fold_resid(const float* __restrict__ partials, uint16_t rb,
                                                uint32_t S_PREV, uint32_t M, uint32_t m, uint32_t K,
-                                               uint32_t k) {
+                                               uint32_t k, bool zero = false) {
   if (S_PREV == 0) return rb;
   float acc = 0.f;
   for (uint32_t s = 0; s < S_PREV; ++s) acc += partials[((size_t)s * M + m) * K + k];
-  return f2h(h2f(rb) + h2f(f2h(acc)));
+  return zero ? f2h(acc) : f2h(h2f(rb) + h2f(f2h(acc)));
 }
 
 // grid (G, M), 256 lanes: chunk g of K/G elements, lane i takes k = g chunk + i, + 256 ...
 __global__ __launch_bounds__(256) void res_fold_kernel(const float* __restrict__ partials,
                                                        uint16_t* __restrict__ resid,
                                                        float* __restrict__ sumsq, uint32_t M,
-                                                       uint32_t K, uint32_t S_PREV, uint32_t G) {
+                                                       uint32_t K, uint32_t S_PREV, uint32_t G,
+                                                       uint32_t zero) {
   __shared__ float lds[kWG];
   const uint32_t g = blockIdx.x, m = blockIdx.y, i = threadIdx.x;
   const uint32_t chunk = (K + G - 1) / G;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void res_fold_kernel(const float* __restrict__
   uint16_t* rp = resid + (size_t)m * K;
   float acc2 = 0.f;
   for (uint32_t k = k0 + i; k < k1; k += kWG) {
-    const uint16_t rb = fold_resid(partials, rp[k], S_PREV, M, m, K, k);
+    const uint16_t rb = fold_resid(partials, rp[k], S_PREV, M, m, K, k, zero != 0);
     rp[k] = rb;
     const float v = h2f(rb);
     acc2 = __builtin_fmaf(v, v, acc2);
@@ -99,18 +101,19 @@ __global__ __launch_bounds__(256) void res_fold_kernel(const float* __restrict__
   if (i == 0) sumsq[(size_t)g * M + m] = tot;
 }
 
-// grid (ceil(K / 256), M): x = rne(r * rstd * w), rstd from the G chunk sums in g order.
+// grid (ceil(K / 256), M): x = rne(r * rstd * w), rstd from the G chunk sums in g order; row m
+// of x at m * x_stride (prep.cl's X_STRIDE: the MTP head's two norms into one [M][2K] row).
 __global__ __launch_bounds__(256) void norm_finish_kernel(const float* __restrict__ sumsq,
                                                           const uint16_t* __restrict__ resid,
                                                           const float* __restrict__ norm_w,
                                                           uint16_t* __restrict__ x_out, uint32_t M,
-                                                          uint32_t K, uint32_t G, float eps) {
+                                                          uint32_t K, uint32_t G, float eps, size_t x_stride) {
   const uint32_t m = blockIdx.y, k = blockIdx.x * kWG + threadIdx.x;
   float total = 0.f;
   for (uint32_t g = 0; g < G; ++g) total += sumsq[(size_t)g * M + m];
   const float mean = total / (float)K;
   const float rstd = 1.0f / sqrtf(mean + eps);
-  if (k < K) x_out[(size_t)m * K + k] = f2h(h2f(resid[(size_t)m * K + k]) * rstd * norm_w[k]);
+  if (k < K) x_out[(size_t)m * x_stride + k] = f2h(h2f(resid[(size_t)m * K + k]) * rstd * norm_w[k]);
 }
 
 // grid (M), 256 lanes: the single-launch residual fold + RMSNorm (prep_ref res_norm).
@@ -479,16 +482,32 @@ int mi_res_fold(const float* partials, uint16_t* resid, float* sumsq, uint32_t M
                 uint32_t S_PREV, uint32_t G, void* stream) {
   if (!resid || !sumsq || (S_PREV && !partials) || G == 0 || M == 0 || K == 0)
     return mi_fail(MI_ERR_ARG, "res_fold: bad arguments");
-  res_fold_kernel<<<dim3(G, M), kWG, 0, (hipStream_t)stream>>>(partials, resid, sumsq, M, K, S_PREV, G);
+  res_fold_kernel<<<dim3(G, M), kWG, 0, (hipStream_t)stream>>>(partials, resid, sumsq, M, K, S_PREV, G, 0u);
   return mi_hip((int)hipGetLastError(), "res_fold");
+}
+int mi_res_fold_ex(const float* partials, uint16_t* resid, float* sumsq, uint32_t M, uint32_t K, uint32_t S_PREV,
+                   uint32_t G, uint32_t zero_resid, void* stream) {
+  if (!resid || !sumsq || (S_PREV && !partials) || G == 0 || M == 0 || K == 0 || zero_resid > 1)
+    return mi_fail(MI_ERR_ARG, "res_fold_ex: bad arguments");
+  res_fold_kernel<<<dim3(G, M), kWG, 0, (hipStream_t)stream>>>(partials, resid, sumsq, M, K, S_PREV, G,
+                                                               zero_resid);
+  return mi_hip((int)hipGetLastError(), "res_fold_ex");
 }
 int mi_norm_finish(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
                    uint32_t M, uint32_t K, uint32_t G, float eps, void* stream) {
   if (!sumsq || !resid || !norm_w || !x_out || G == 0 || M == 0 || K == 0)
     return mi_fail(MI_ERR_ARG, "norm_finish: bad arguments");
   norm_finish_kernel<<<dim3((K + kWG - 1) / kWG, M), kWG, 0, (hipStream_t)stream>>>(sumsq, resid, norm_w,
-                                                                                      x_out, M, K, G, eps);
+                                                                                      x_out, M, K, G, eps, K);
   return mi_hip((int)hipGetLastError(), "norm_finish");
+}
+int mi_norm_finish_ex(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                      size_t x_stride, uint32_t M, uint32_t K, uint32_t G, float eps, void* stream) {
+  if (!sumsq || !resid || !norm_w || !x_out || G == 0 || M == 0 || K == 0 || x_stride < K)
+    return mi_fail(MI_ERR_ARG, "norm_finish_ex: bad arguments (x_stride >= K)");
+  norm_finish_kernel<<<dim3((K + kWG - 1) / kWG, M), kWG, 0, (hipStream_t)stream>>>(sumsq, resid, norm_w,
+                                                                                      x_out, M, K, G, eps, x_stride);
+  return mi_hip((int)hipGetLastError(), "norm_finish_ex");
 }
 int mi_res_norm(const float* partials, uint16_t* resid, const float* norm_w, uint16_t* x_out, uint32_t M,
                 uint32_t K, uint32_t S_PREV, float eps, void* stream) {

@@ -132,3 +132,16 @@ def test_verify_attention_bind_rule():
         [0, 0, 0, 0, 0, 1, 1, 1, 0]
     assert L.mi_attn_verify_binds(16, 1, 16, 2) == 0     # int8 cache: the decode kernel
     assert L.mi_attn_verify_binds(16, 0, 40, 8) == 0     # other heads
+
+
+def test_mtp_head_shape_rules_without_a_gpu():
+    """The MTP head is a dense layer over the f16 cache: engine_create refuses it with an MoE
+    model or the int8 cache before touching the device."""
+    import ctypes as C
+    L = mi.lib()
+    d = mi.dense_desc(2, 512, 8, 2, 256, 1024, 4096, 512, kv_int8=1, mtp=1)
+    assert not L.mi_engine_create(C.byref(d), 1, None)
+    assert b"unsupported model shape" in L.mi_last_error()
+    m = mi.moe_desc(2, 512, 8, 2, 128, 16, 4, 128, 4096, 512)
+    m.mtp = 1
+    assert not L.mi_engine_create(C.byref(m), 1, None)
