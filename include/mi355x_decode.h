@@ -188,6 +188,20 @@ int mi_res_fold(const float* partials, uint16_t* resid, float* sumsq, uint32_t M
 /* prep_norm_finish (prep.cl:350): x = rne(r * (1/sqrt(sum_g sumsq / K + eps)) * w) */
 int mi_norm_finish(const float* sumsq, const uint16_t* resid, const float* norm_w, uint16_t* x_out,
                    uint32_t M, uint32_t K, uint32_t G, float eps, void* stream);
+/* The int8 lm_head (spec 9: W8A16; src/loader/lm_head_int8.h, src/kernels/gemv_i8w.cl:55-58).
+ * The weight is int8 in this library's matrix-core layout: element (k, n) of the [K][N] head at
+ * byte mi_i8w_index(K, k, n) ([N/16][K/64][64 lanes][16 bytes]); scales fp32 [N], one per
+ * output column. */
+size_t mi_i8w_index(uint32_t K, uint32_t k, uint32_t n);
+/* lm_head_int8.cc:22-37 on the host: each row n of w fp32 [N][K] (a 16-bit head widened)
+ * quantised symmetrically, s = max|w| / 127 (fp32), q = rne(w / s) clamped to [-127, 127], a
+ * zero row s = 0, q = 0; into q_tiled (K N bytes, the layout above) and scales[N]. K a
+ * multiple of 64, N of 16. */
+int mi_lm_head_int8_quantise(const float* w, uint32_t K, uint32_t N, int8_t* q_tiled, float* scales);
+/* gemv_i8w: out fp32 [M][N] = (sum_k q[k][n] x[m][k]) * scales[n]; x f16 [M][K]; M <= 8, K a
+ * multiple of 64, N of 64. */
+int mi_gemv_i8w(const int8_t* w, const float* scales, const uint16_t* x, float* out, uint32_t M,
+                uint32_t K, uint32_t N, void* stream);
 /* mi_res_fold with prep.cl's ZERO_RESID (zero_resid = 1: resid = rne(sum_s partials), the
  * residual taken as zero - the MTP head's fc fold, capture.cc:1790) */
 int mi_res_fold_ex(const float* partials, uint16_t* resid, float* sumsq, uint32_t M, uint32_t K,

@@ -93,6 +93,9 @@ SIGNATURES = {
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
     "mi_engine_draft": (i32, [vp, u32, vp]),
+    "mi_i8w_index": (sz, [u32, u32, u32]),
+    "mi_lm_head_int8_quantise": (i32, [vp, u32, u32, vp, vp]),
+    "mi_gemv_i8w": (i32, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "mi_res_fold_ex": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "mi_norm_finish_ex": (i32, [vp, vp, vp, vp, sz, u32, u32, u32, f32, vp]),
     "mi_accept_greedy": (u32, [vp, vp, u32, vp]),

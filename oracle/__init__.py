@@ -77,6 +77,8 @@ def lib():
             "orc_dense_step_kv8": (u32, [i32, vp, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_prefill_chunk": (u32, [i32, vp, vp, u32, u32, vp, vp, vp]),
             "orc_mtp_head_step": (u32, [i32, vp, vp, u32, vp, u32, vp, vp, i32, vp, vp]),
+            "orc_quantise_row_int8": (f32, [vp, u32, vp]),
+            "orc_gemv_i8w": (None, [i32, vp, vp, vp, u32, u32, u32, vp]),
             "orc_moe_prefill": (None, [i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
             "orc_f16w_tile": (None, [vp, u32, u32, vp]),
@@ -129,6 +131,8 @@ def ref():
             "ref_moe_block": (None, [vp, u32, u32, u32, u32, u32, vp, vp, vp, u32, u32, vp]),
             "ref_pf_moe_block": (None, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
             "ref_repack_bf16_tiled": (None, [vp, u32, u32, vp]),
+            "ref_quantise_int8_tiled": (None, [vp, u32, u32, vp, vp]),
+            "ref_int8_tiled_index": (C.c_size_t, [u32, u32, u32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(R, name)
@@ -185,7 +189,8 @@ class DenseModel(C.Structure):
                 ("embed", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", Linear),
                 ("rope", C.c_void_p), ("tgt", C.c_uint32), ("norm_g", C.c_uint32),
                 ("experts", C.c_uint32), ("top_k", C.c_uint32), ("moe_inter", C.c_uint32),
-                ("router_n", C.c_uint32), ("router_ksplit", C.c_uint32)]
+                ("router_n", C.c_uint32), ("router_ksplit", C.c_uint32),
+                ("lm_i8", C.c_void_p), ("lm_i8_scales", C.c_void_p)]
 
 
 # ---- numpy helpers ----------------------------------------------------------------------

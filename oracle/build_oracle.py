@@ -36,7 +36,8 @@ def build_ref():
     out = os.path.join(outdir, "libref.so")
     _run(["g++", "-std=c++20", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-w",
           "-I" + os.path.join(REF, "src"), "-I" + os.path.join(REF, "tests"),
-          os.path.join(HERE, "ref_shim.cpp"), "-o", out])
+          os.path.join(HERE, "ref_shim.cpp"), os.path.join(REF, "src", "loader", "lm_head_int8.cc"),
+          "-pthread", "-o", out])
     return out
 
 

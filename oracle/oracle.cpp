@@ -967,6 +967,53 @@ void orc_f16w_tile(const uint16_t* w_rm, uint32_t K, uint32_t N, uint16_t* wt) {
 // ---- dense decode step (src/runtime/capture.cc:997, 1247-1263, 1370-1423, 1461-1480) --------
 // k_scale != NULL: the int8 rotated cache (kv8.cl's writer and readers, head_dim 256), int8 rows
 // [layers][kv_heads][max_len][hd] and fp16 scales [layers][kv_heads][max_len]
+// ---- the int8 lm_head ------------------------------------------------------------------------
+// lm_head_int8.cc:22-37: the row's largest magnitude over 127, then w / s rounded to nearest even
+// (nearbyint in the default mode) and clamped
+float orc_quantise_row_int8(const float* w, uint32_t K, int8_t* q) {
+  float amax = 0.f;
+  for (uint32_t k = 0; k < K; ++k) amax = std::fmax(amax, std::fabs(w[k]));
+  const float s = amax / 127.0f;
+  for (uint32_t k = 0; k < K; ++k) {
+    if (s == 0.f) {
+      q[k] = 0;
+      continue;
+    }
+    const float r = std::nearbyint(w[k] / s);
+    q[k] = int8_t(std::min(127.f, std::max(-127.f, r)));
+  }
+  return s;
+}
+// gemv_i8w.cl:67-105: one fp32 chain per column over k ascending, then the column's scale
+void orc_gemv_i8w(int act, const int8_t* q, const float* s, const uint16_t* x, uint32_t M, uint32_t K, uint32_t N,
+                  float* out) {
+  const Act A{act};
+  for (uint32_t m = 0; m < M; ++m) {
+    std::vector<float> xf(K);
+    for (uint32_t k = 0; k < K; ++k) xf[k] = A.w(x[size_t(m) * K + k]);
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < int64_t(N); ++n) {
+      const int8_t* r = q + size_t(n) * K;
+      float a = 0.f;
+      for (uint32_t k = 0; k < K; ++k) a += float(r[k]) * xf[k];
+      out[size_t(m) * N + n] = a * s[n];
+    }
+  }
+}
+
+// the model's head: the int4 lm_head (the twin's split-K order) or the int8 one
+static void head_logits(int act, const orc_dense_model* md, const uint16_t* x, float* logits) {
+  const Act A{act};
+  const uint32_t H = md->hidden;
+  if (md->lm_i8) {
+    orc_gemv_i8w(act, md->lm_i8, md->lm_i8_scales, x, 1, H, md->vocab, logits);
+    return;
+  }
+  std::vector<float> xf(H);
+  for (uint32_t i = 0; i < H; ++i) xf[i] = A.w(x[i]);
+  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
+}
+
 static uint32_t dense_step(int act, const orc_dense_model* md, uint32_t tok, uint32_t pos, void* kv_k,
                            void* kv_v, uint16_t* k_scale, uint16_t* v_scale, float* logits,
                            uint32_t n_layers_run) {
@@ -1048,9 +1095,7 @@ static uint32_t dense_step(int act, const orc_dense_model* md, uint32_t tok, uin
   }
   if (nl < md->layers) return 0;
   norm(prev.data(), s_prev, md->final_norm);
-  widen(x.data(), H);
-  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1,
-                md->lm_head.S, logits);
+  head_logits(act, md, x.data(), logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);
 }
 
@@ -1126,8 +1171,7 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
   linear(ly.down, hbuf.data());
   norm(part.data(), ly.down.S, hd->final_norm);
   if (h_out) std::copy(x.begin(), x.end(), h_out);
-  for (uint32_t i = 0; i < H; ++i) xf[i] = A.w(x[i]);
-  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
+  head_logits(act, md, x.data(), logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);
 }
 
@@ -1223,9 +1267,7 @@ uint32_t orc_prefill_chunk(int act, const orc_dense_model* md, const uint32_t* i
     orc_res_norm(act, out.data(), resid.data(), next_w, x.data(), T, H, 1, md->rms_eps);
   }
   // the last row's head on the decode GEMV (the engine runs the step's lm_head launch)
-  std::vector<float> xf(H);
-  for (uint32_t k = 0; k < H; ++k) xf[k] = A.w(x[size_t(T - 1) * H + k]);
-  orc_gemv_twin(0, md->lm_head.qweight, md->lm_head.scales, H, md->vocab, xf.data(), 1, md->lm_head.S, logits);
+  head_logits(act, md, x.data() + size_t(T - 1) * H, logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);
 }
 

@@ -170,6 +170,15 @@ void orc_gemv_f16w(int act, const uint16_t* w, const uint16_t* x, uint32_t M, ui
 /* row-major [N][K] fp16 -> the tile layout above */
 void orc_f16w_tile(const uint16_t* w_rowmajor, uint32_t K, uint32_t N, uint16_t* w_tiled);
 
+/* ---- the int8 lm_head (src/loader/lm_head_int8.cc:22-37, src/kernels/gemv_i8w.cl:55-106) ---- */
+/* One row of K fp32 values: s = max|w| / 127 (fp32), q = rne(w / s) clamped to [-127, 127];
+ * a zero row gives s = 0 and q = 0. Returns s. */
+float orc_quantise_row_int8(const float* w, uint32_t K, int8_t* q);
+/* out[m][n] = (sum over k ascending of q[n][k] * x[m][k], fp32) * s[n]; q int8 [N][K]
+ * row-major, x act [M][K] */
+void orc_gemv_i8w(int act, const int8_t* q, const float* s, const uint16_t* x, uint32_t M, uint32_t K,
+                  uint32_t N, float* out);
+
 /* ---- a whole dense decode step (src/runtime/capture.cc:1247-1480 layer walk) ---- */
 typedef struct orc_linear {
   const uint32_t* qweight; /* [K/8][N] */
@@ -201,6 +210,10 @@ typedef struct orc_dense_model {
   uint32_t norm_g;   /* 0: single-launch res_norm tree; G > 0: res_fold over G chunks + norm_finish */
   /* experts > 0: every layer's MLP is the MoE block (moe.cl), router K split router_ksplit */
   uint32_t experts, top_k, moe_inter, router_n, router_ksplit;
+  /* the int8 lm_head (spec 9): when lm_i8 is set the head is orc_gemv_i8w over lm_i8 int8
+   * [vocab][hidden] row-major and lm_i8_scales fp32 [vocab], in place of lm_head */
+  const int8_t* lm_i8;
+  const float* lm_i8_scales;
 } orc_dense_model;
 /* One step for token `tok` at position pos. kv_k/kv_v: [layers][kv_heads][max_len][hd] act
  * (this build's layout), updated in place. Writes logits fp32 [vocab] and returns argmax. */

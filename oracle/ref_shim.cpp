@@ -19,6 +19,7 @@
 #include "kernels/moe_ref.h"
 #include "kernels/pf_moe_ref.h"
 #include "kernels/prep_ref.h"
+#include "loader/lm_head_int8.h"
 
 extern "C" {
 
@@ -222,5 +223,12 @@ void ref_pf_moe_block(const uint32_t* route, uint32_t C, const uint16_t* x, cons
                                                                      hidden, s, t, n,
                                                                      resid_inout[size_t(t) * hidden + n]);
 }
+
+// The int8 lm_head's load-time quantisation (src/loader/lm_head_int8.cc, compiled with this
+// shim): bf16 [N][K] rows into gemv_i8w's tiled layout and the fp32 row scales, one thread.
+void ref_quantise_int8_tiled(const uint16_t* w, uint32_t K, uint32_t N, int8_t* q_tiled, float* scales) {
+  loader::quantise_int8_tiled(w, K, N, q_tiled, scales, 1);
+}
+size_t ref_int8_tiled_index(uint32_t K, uint32_t k, uint32_t n) { return loader::int8_tiled_index(K, k, n); }
 
 }  // extern "C"

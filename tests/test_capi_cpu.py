@@ -145,3 +145,28 @@ def test_mtp_head_shape_rules_without_a_gpu():
     m = mi.moe_desc(2, 512, 8, 2, 128, 16, 4, 128, 4096, 512)
     m.mtp = 1
     assert not L.mi_engine_create(C.byref(m), 1, None)
+
+
+def test_int8_head_quantiser_is_the_oracles():
+    """mi_lm_head_int8_quantise (the product's load-time quantiser, host code) bitwise the
+    oracle's row quantiser at every element of its layout, which is a bijection onto K N
+    bytes."""
+    import numpy as np
+    import oracle as O
+    L = mi.lib()
+    K, N = 256, 48
+    rng = np.random.default_rng(2)
+    w = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    w[4] = 0
+    w[9, 3] = -2.0
+    qt = np.zeros(K * N, np.int8)
+    st = np.zeros(N, np.float32)
+    assert L.mi_lm_head_int8_quantise(w.ctypes.data, K, N, qt.ctypes.data, st.ctypes.data) == 0
+    idx = np.array([[L.mi_i8w_index(K, k, n) for k in range(K)] for n in range(N)])
+    assert np.array_equal(np.sort(idx.ravel()), np.arange(K * N))
+    for n in range(N):
+        q = np.zeros(K, np.int8)
+        s = O.lib().orc_quantise_row_int8(O._p(np.ascontiguousarray(w[n])), K, O._p(q))
+        assert np.float32(s).view(np.uint32) == st[n].view(np.uint32)
+        assert np.array_equal(qt[idx[n]], q)
+    assert L.mi_lm_head_int8_quantise(w.ctypes.data, 100, N, qt.ctypes.data, st.ctypes.data) == -1

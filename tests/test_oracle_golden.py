@@ -535,3 +535,46 @@ def test_gemv_f16w_vs_fp64(ksplit):
     want = xf @ wf.T
     bound = (K / ksplit + np.log2(ksplit) + 1) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)
     assert np.all(np.abs(out - want) <= bound)
+
+
+def test_int8_head_quantiser_known_answers():
+    """lm_head_int8_test's hand-made rows: max 127 gives s = 1 exactly, so w / s is w and the
+    ties are exact (2.5 -> 2, 3.5 -> 4, -2.5 -> -2, 0.5 -> 0, 1.5 -> 2, -0.5 -> 0, round to
+    nearest even); a zero row gives s = 0 and q = 0; values past the row's scale clamp at
+    +-127; the round trip |w - q s| <= s / 2 (1 + 2^-22)."""
+    w = np.zeros(64, np.float32)
+    w[:8] = [127.0, 2.5, 3.5, -2.5, -127.0, 0.5, 1.5, -0.5]
+    q = np.zeros(64, np.int8)
+    assert O.lib().orc_quantise_row_int8(O._p(w), 64, O._p(q)) == 1.0
+    assert list(q[:8]) == [127, 2, 4, -2, -127, 0, 2, 0] and not np.any(q[8:])
+    z = np.zeros(64, np.float32)
+    qz = np.ones(64, np.int8)
+    assert O.lib().orc_quantise_row_int8(O._p(z), 64, O._p(qz)) == 0.0 and not np.any(qz)
+    rng = np.random.default_rng(3)
+    r = (0.02 * rng.standard_normal(5120)).astype(np.float32)
+    qr = np.zeros(5120, np.int8)
+    s = O.lib().orc_quantise_row_int8(O._p(r), 5120, O._p(qr))
+    assert s == np.float32(np.abs(r).max()) / np.float32(127.0)
+    assert np.abs(qr.astype(np.int32)).max() == 127
+    err = np.abs(r.astype(np.float64) - qr.astype(np.float64) * s)
+    assert err.max() <= s * 0.5 * (1 + 2.0 ** -22)
+
+
+def test_int8_gemv_vs_fp64():
+    """orc_gemv_i8w (one fp32 chain over k, then the scale) within the fp32 summation bound of
+    the fp64 sum: |got - want| <= K 2^-24 sum|q x| s + a rounding of the result."""
+    rng = np.random.default_rng(8)
+    M, K, N = 3, 1024, 96
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(2e-4, 2e-3, N).astype(np.float32)
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    out = np.zeros((M, N), np.float32)
+    O.lib().orc_gemv_i8w(O.ORC_F16, O._p(q), O._p(s), O._p(x), M, K, N, O._p(out))
+    xf = O.f16_bits_to_f32(x).astype(np.float64)
+    prod = xf @ q.T.astype(np.float64)
+    want = prod * s.astype(np.float64)
+    bound = (K * 2.0 ** -24 * (np.abs(xf) @ np.abs(q.T.astype(np.float64))) + 2.0 ** -24 * np.abs(prod)) * s + \
+        2.0 ** -24 * np.abs(want)
+    assert np.all(np.abs(out - want) <= bound)
+    # the scales applied one column off miss it
+    assert not np.all(np.abs(out - prod * np.roll(s, 1).astype(np.float64)) <= bound)

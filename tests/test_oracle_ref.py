@@ -388,3 +388,32 @@ def test_moe_prefill_bitwise_pf_moe_ref(E, K, T):
     R.ref_pf_moe_block(P(route), T, P(x), P(gu), P(dn), E, K, Hd, I, P(b))
     assert np.array_equal(a, b)
     assert not np.array_equal(a, resid)
+
+
+def _int8_rows(N, K, seed):
+    """bf16 rows N(0, 0.02) with lm_head_int8_test's special rows: one all zero, one with a
+    large positive outlier, one whose largest magnitude is negative."""
+    rng = np.random.default_rng(seed)
+    w = O.f32_to_bf16_bits((0.02 * rng.standard_normal((N, K))).astype(np.float32))
+    w[5] = 0
+    w[3, 17] = O.f32_to_bf16_bits(np.float32(0.9))
+    w[7, K - 1] = O.f32_to_bf16_bits(np.float32(-1.5))
+    return w
+
+
+@pytest.mark.parametrize("N,K,seed", [(64, 256, 1234), (48, 5120, 7)])
+def test_int8_head_quantiser_bitwise_lm_head_int8(N, K, seed):
+    """orc_quantise_row_int8 against the reference's quantise_int8_tiled (lm_head_int8.cc,
+    compiled into _ref): every scale's bits and every q at int8_tiled_index."""
+    w = _int8_rows(N, K, seed)
+    qt = np.zeros(N * K, np.int8)
+    st = np.zeros(N, np.float32)
+    R.ref_quantise_int8_tiled(P(w), K, N, P(qt), P(st))
+    wf = O.bf16_bits_to_f32(w).astype(np.float32)
+    for n in range(N):
+        q = np.zeros(K, np.int8)
+        s = L().orc_quantise_row_int8(P(np.ascontiguousarray(wf[n])), K, P(q))
+        assert np.float32(s).view(np.uint32) == st[n].view(np.uint32), n
+        idx = np.array([R.ref_int8_tiled_index(K, k, n) for k in range(K)])
+        assert np.array_equal(qt[idx], q), n
+    assert st[5] == 0 and not np.any(qt[[R.ref_int8_tiled_index(K, k, 5) for k in range(K)]])
