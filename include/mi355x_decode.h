@@ -448,6 +448,11 @@ typedef struct mi_model_desc {
    * Every step then also fills the head's K/V (capture.cc:362-370) and mi_engine_draft runs the
    * draft lists. */
   uint32_t mtp;
+  /* 1: the int8 lm_head (spec 9, loader::LmHeadForm::Int8): int8 [vocab][hidden] in
+   * mi_i8w_index's layout with one fp32 scale per row, read by mi_gemv_i8w, then both argmax
+   * stages; a loaded checkpoint's 16-bit head is quantised at load (lm_head_int8.cc). 0: the
+   * int4 g64 head. */
+  uint32_t lm_head_int8;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;
@@ -472,7 +477,9 @@ enum {
    * hh [max_rows + 1][hidden] (row 0: the post-final-norm hidden of position pos - 1), the
    * draft chain's hidden [hidden], its control block and the last draft's logits [vocab] */
   MI_T_MTP_FC_Q, MI_T_MTP_FC_S, MI_T_MTP_PRE_E, MI_T_MTP_PRE_H, MI_T_MTP_FINAL, MI_T_MTP_KV_K,
-  MI_T_MTP_KV_V, MI_T_MTP_HH, MI_T_MTP_DH, MI_T_MTP_CTRL, MI_T_MTP_LOGITS
+  MI_T_MTP_KV_V, MI_T_MTP_HH, MI_T_MTP_DH, MI_T_MTP_CTRL, MI_T_MTP_LOGITS,
+  /* the int8 lm_head (lm_head_int8): its tiled int8 weight and fp32 row scales */
+  MI_T_LM_I8, MI_T_LM_I8_S
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's

@@ -185,18 +185,19 @@ class ModelDesc(C.Structure):
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
                 ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
                 ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32),
-                ("mtp", u32)]
+                ("mtp", u32), ("lm_head_int8", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
                rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
-               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0):
+               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0, lm_head_int8=0):
     d = ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
                   head_dim if rot_dim is None else rot_dim, inter, vocab,
                   vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
                   attn_tgt, rope_theta, rms_eps)
     d.kv_int8 = kv_int8
     d.mtp = mtp
+    d.lm_head_int8 = lm_head_int8
     return d
 
 
@@ -244,7 +245,7 @@ def desc_27b(max_len=4096 + 512):
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_STEP_STAGES,
  T_STEP_ARENA, T_STEP_TRACE, T_MTP_FC_Q, T_MTP_FC_S, T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K,
- T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS) = range(32, 63)
+ T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS, T_LM_I8, T_LM_I8_S) = range(32, 65)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 

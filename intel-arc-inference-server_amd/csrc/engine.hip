@@ -117,7 +117,9 @@ struct mi_engine {
   std::vector<Layer> layer;
   uint16_t* embed = nullptr;
   float* final_norm = nullptr;
-  Linear lm_head;
+  Linear lm_head;           // the int4 head (lm_head_int8 = 0)
+  int8_t* lm_i8 = nullptr;  // the int8 head (lm_head_int8): [vocab][hidden] in mi_i8w_index's layout
+  float* lm_i8s = nullptr;  // its fp32 row scales [vocab]
   float* rope = nullptr;
   void* kv_k = nullptr;  // [layers][kv_heads][max_len][head_dim] f16, or int8 (kv_int8)
   void* kv_v = nullptr;
@@ -278,8 +280,13 @@ struct mi_engine {
       MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(hctl, 0, MI_CTRL_WORDS * 4, stream)), "hctl clear"));
       MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(hh, 0, size_t(R + 1) * H * 2, stream)), "hh clear"));
     }
-    MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
-    part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * R * m.vocab);
+    if (m.lm_head_int8) {
+      MI_TRY(alloc(&lm_i8, size_t(m.vocab) * H));
+      MI_TRY(alloc(&lm_i8s, m.vocab));
+    } else {
+      MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
+      part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * R * m.vocab);
+    }
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
     MI_TRY(alloc(&final_norm, H));
     MI_TRY(alloc(&rope, size_t(m.max_len) * m.rot_dim));
@@ -349,7 +356,12 @@ struct mi_engine {
       MI_TRY(mi_fill_f16(hkv_k, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
       MI_TRY(mi_fill_f16(hkv_v, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
     }
-    MI_TRY(init_linear(lm_head, seed));
+    if (m.lm_head_int8) {  // uniform int8 with row scales U(2e-4, 1.2e-3): the int4 head's spread
+      MI_TRY(mi_fill_i8(lm_i8, size_t(m.vocab) * H, seed++, -127, 127, stream));
+      MI_TRY(mi_fill_f32(lm_i8s, m.vocab, seed++, 0, 2e-4f, 1.2e-3f, 0, stream));
+    } else {
+      MI_TRY(init_linear(lm_head, seed));
+    }
     MI_TRY(mi_fill_f16(embed, size_t(m.vocab) * H, seed++, 1, 0.0f, 1.0f, stream));
     MI_TRY(mi_fill_f32(final_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
     if (m.kv_int8) {  // BASELINE config 3's int8 cache: uniform [-127, 127], scales U(0.005, 0.05)
@@ -451,8 +463,7 @@ struct mi_engine {
       MI_TRY(launch_gate_up(L, M));
       MI_TRY(launch_down(L, M, next_w));
     }
-    MI_TRY(launch_lm_head(M, logits));
-    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
+    MI_TRY(head(ctrl, M, x, logits, history));
     if (d.mtp) {
       // capture.cc:362-370: the rows' post-final-norm hidden (what lm_head read) into hh rows
       // 1..M, then the head's K/V over hh rows 0..M-1; a single-row step commits its row at
@@ -495,8 +506,20 @@ struct mi_engine {
     MI_TRY(launch_down(mh.L, 1, mh.final_n));
     MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(dh, x, size_t(d.hidden) * 2, hipMemcpyDeviceToDevice, stream)),
                   "dh"));
-    MI_TRY(launch_lm_head(1, hlogits));
-    return mi_argmax_finish(hctl, argmax_part, d.vocab / 64, hhist, d.max_len, stream);
+    return head(hctl, 1, x, hlogits, hhist);
+  }
+
+  // head() (capture.cc:1461-1480 / 1913-1939): the lm_head over rows xin into out and the argmax
+  // into control block c (out_token, cur_token, history, pos += n_active): the int4 head's
+  // LOGITS launch (logits + tile winners) and argmax_stage2, or the int8 head's gemv_i8w and
+  // both argmax stages
+  int head(uint32_t* c, uint32_t M, const uint16_t* xin, float* out, uint32_t* hist) {
+    if (d.lm_head_int8) {
+      MI_TRY(mi_gemv_i8w(lm_i8, lm_i8s, xin, out, M, d.hidden, d.vocab, stream));
+      return mi_argmax(c, out, argmax_part, hist, d.max_len, M, d.vocab, d.vocab_used, stream);
+    }
+    MI_TRY(launch_lm_head(M, xin, out));
+    return mi_argmax_finish(c, argmax_part, d.vocab / 64, hist, d.max_len, stream);
   }
 
   // ---- the step's int4 GEMV launches, one per linear, as enqueue_step issues them ----
@@ -578,8 +601,8 @@ struct mi_engine {
     const mi_gemv_epilogue ed = resid_epi(next_w);
     return mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream);
   }
-  // the lm_head with the logits and the per-tile argmax
-  int launch_lm_head(uint32_t M, float* out) {
+  // the int4 lm_head with the logits and the per-tile argmax
+  int launch_lm_head(uint32_t M, const uint16_t* xin, float* out) {
     mi_gemv_epilogue el{};
     el.kind = MI_EPI_LOGITS;
     el.logits = out;
@@ -587,7 +610,7 @@ struct mi_engine {
     el.vocab_used = d.vocab_used;
     el.status = ctrl + MI_CTRL_DEBUG;
     el.arrive = use_arrive ? arrive : nullptr;
-    return mi_gemv_w4a16_ex(lm_head.q, lm_head.s, x, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream);
+    return mi_gemv_w4a16_ex(lm_head.q, lm_head.s, xin, part_ex, M, lm_head.K, lm_head.N, lm_head.S, &el, stream);
   }
 
   // `reps` rounds of one linear's step launch (0 qkv, 1 o, 2 gate_up, 3 down: every layer's in
@@ -604,7 +627,9 @@ struct mi_engine {
         case 1: return launch_o(layer[li], 1);
         case 2: return launch_gate_up(layer[li], 1);
         case 3: return launch_down(layer[li], 1, next_norm(li));
-        default: return launch_lm_head(1, logits);
+        default:
+          return d.lm_head_int8 ? mi_gemv_i8w(lm_i8, lm_i8s, x, logits, 1, d.hidden, d.vocab, stream)
+                                : launch_lm_head(1, x, logits);
       }
     };
     const uint32_t per_round = which == 4 ? 1u : d.layers;
@@ -711,8 +736,8 @@ struct mi_engine {
       return 0;
     }
     if (!step) {
-      if (d.experts || d.kv_int8 || d.mtp)
-        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache only, no MTP head");
+      if (d.experts || d.kv_int8 || d.mtp || d.lm_head_int8)
+        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache and the int4 head only, no MTP head");
       std::vector<mi::StepLayerW> lw(d.layers);
       auto sl = [](const Linear& l) { return mi::StepLinear{l.q, l.s, l.K, l.N, l.S}; };
       for (uint32_t li = 0; li < d.layers; ++li) {
@@ -894,17 +919,8 @@ struct mi_engine {
     }
     // the last position's head and argmax, on the decode control block: the step at pos0 + n - 1
     // leaves cur_token = its argmax and pos = pos0 + n, as ingest's last replay would
-    mi_gemv_epilogue el{};
-    el.kind = MI_EPI_LOGITS;
-    el.logits = logits;
-    el.argmax_part = argmax_part;
-    el.vocab_used = d.vocab_used;
-    el.status = ctrl + MI_CTRL_DEBUG;
-    el.arrive = use_arrive ? arrive : nullptr;
-    MI_TRY(mi_gemv_w4a16_ex(lm_head.q, lm_head.s, pf_x + size_t(T - 1) * d.hidden, part_ex, 1, lm_head.K, lm_head.N,
-                            lm_head.S, &el, stream));
     MI_TRY(set_rows(pos0 + n - 1, 1, nullptr, 0));
-    MI_TRY(mi_argmax_finish(ctrl, argmax_part, d.vocab / 64, history, d.max_len, stream));
+    MI_TRY(head(ctrl, 1, pf_x + size_t(T - 1) * d.hidden, logits, history));
     MI_TRY(mi_stream_sync(stream));
     uint32_t pc[MI_CTRL_WORDS];
     MI_TRY(mi_memcpy_d2h(pc, pf_ctrl, sizeof pc, stream));
@@ -925,7 +941,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
-      m.mtp > 1 || (m.mtp && (m.experts || m.kv_int8)) ||
+      m.mtp > 1 || (m.mtp && (m.experts || m.kv_int8)) || m.lm_head_int8 > 1 ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {
@@ -961,7 +977,8 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
   // per-layer kinds at layer == layers: the MTP head's layer
   if (kind < MI_T_EMBED && layer >= m.layers + (m.mtp ? 1u : 0u))
     return mi_fail(MI_ERR_ARG, "engine_tensor: layer out of range");
-  if (kind >= MI_T_MTP_FC_Q && !m.mtp) return mi_fail(MI_ERR_ARG, "engine_tensor: the model has no MTP head");
+  if (kind >= MI_T_MTP_FC_Q && kind <= MI_T_MTP_LOGITS && !m.mtp)
+    return mi_fail(MI_ERR_ARG, "engine_tensor: the model has no MTP head");
   const Layer* L = kind < MI_T_EMBED ? (layer == m.layers ? &e->mh.L : &e->layer[layer]) : nullptr;
   const size_t hkvb = size_t(m.kv_heads) * m.max_len * m.head_dim * 2;
   auto lin_q = [](const Linear& l, void** p, size_t* b) { *p = l.q; if (b) *b = size_t(l.K / 8) * l.N * 4; };
@@ -1016,6 +1033,8 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_MTP_DH: *ptr = e->dh; b = size_t(m.hidden) * 2; break;
     case MI_T_MTP_CTRL: *ptr = e->hctl; b = MI_CTRL_WORDS * 4; break;
     case MI_T_MTP_LOGITS: *ptr = e->hlogits; b = size_t(m.vocab) * 4; break;
+    case MI_T_LM_I8: *ptr = e->lm_i8; b = e->lm_i8 ? size_t(m.vocab) * m.hidden : 0; break;
+    case MI_T_LM_I8_S: *ptr = e->lm_i8s; b = e->lm_i8s ? size_t(m.vocab) * 4 : 0; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;

@@ -623,6 +623,14 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   mi_model_desc want{};
   if (int rc = mi_checkpoint_desc(dir, 1, 1, &want)) return rc;
   void* st = mi_engine_stream(e);
+  // the engine's lm_head form (its descriptor's lm_head_int8): whether it holds an int8 head
+  bool head_i8 = false;
+  {
+    void* p8 = nullptr;
+    size_t b8 = 0;
+    if (int rc = mi_engine_tensor(e, MI_T_LM_I8, 0, &p8, &b8)) return rc;
+    head_i8 = b8 != 0;
+  }
   const std::string pre = lm_prefix(ck);
   const uint32_t H = want.hidden, QH = want.q_heads, KVH = want.kv_heads, HD = want.head_dim;
   const uint32_t I = want.inter, Vp = want.vocab;
@@ -663,8 +671,24 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   if (int rc = upload(MI_T_EMBED, 0, f16.data(), f16.size() * 2, "embed_tokens")) return rc;
   if (!get_float(ck, pre + "norm.weight", H, f32)) return fail_ck(ck);
   if (int rc = upload(MI_T_FINAL_NORM, 0, f32.data(), f32.size() * 4, "norm")) return rc;
-  // lm_head: int4 as shipped, or a 16-bit head (or the tied embeddings) quantised here
-  {
+  // lm_head: int4 as shipped, or a 16-bit head (or the tied embeddings) quantised here to int4
+  // g64 - or, for an engine built with the int8 head, to int8 rows (lm_head_int8.cc: a packed
+  // head is refused there as here)
+  if (head_i8) {
+    if (ck.find("lm_head.qweight"))
+      return mi_fail(MI_ERR_ARG, "engine_load: the int8 lm_head is made from a 16-bit head, this one is packed");
+    const std::string src = ck.find("lm_head.weight") ? "lm_head.weight" : pre + "embed_tokens.weight";
+    if (src != "lm_head.weight" && !cfg_bool(ck.config, "tie_word_embeddings", false))
+      return mi_fail(MI_ERR_ARG, "engine_load: no lm_head and tie_word_embeddings is not set");
+    if (!get_float(ck, src, size_t(V) * H, f32)) return fail_ck(ck);
+    f32.resize(size_t(Vp) * H, 0.f);  // padded vocabulary rows: scale 0, q 0 (masked by vocab_used)
+    std::vector<int8_t> q8(size_t(Vp) * H);
+    std::vector<float> s8(Vp);
+    if (int rc = mi_lm_head_int8_quantise(f32.data(), H, Vp, q8.data(), s8.data())) return rc;
+    rep.quantised_head = 1;
+    if (int rc = upload(MI_T_LM_I8, 0, q8.data(), q8.size(), "lm_head (int8)")) return rc;
+    if (int rc = upload(MI_T_LM_I8_S, 0, s8.data(), s8.size() * 4, "lm_head scales (int8)")) return rc;
+  } else {
     Linear4 lm;
     std::vector<uint32_t> lq;
     std::vector<uint16_t> ls;
@@ -779,7 +803,8 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
                   "loaded %zu int4 linears; dropped %zu qzeros + %zu g_idx (invariants asserted); %zu subnormal "
                   "scales kept; lm_head %s",
                   rep.linears, rep.qzeros, rep.g_idx, rep.subnormal_scales,
-                  rep.quantised_head ? "quantised to int4 g64 at load" : "int4 as shipped");
+                  rep.quantised_head ? (head_i8 ? "quantised to int8 rows at load" : "quantised to int4 g64 at load")
+                                     : "int4 as shipped");
   }
   return 0;
 }

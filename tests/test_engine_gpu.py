@@ -78,6 +78,11 @@ class OracleModel:
                               C.cast(layers, C.c_void_p), embed.ctypes.data, fnorm.ctypes.data,
                               O.Linear(lmq.ctypes.data, lms.ctypes.data, H, d.vocab, S[4]),
                               self.rope.ctypes.data, d.attn_tgt, H // 64)
+        if d.lm_head_int8:  # the int8 head, row-major for the oracle
+            from test_gemv_i8w_gpu import untile
+            q8 = self._h(untile(eng.to_host(mi.T_LM_I8, 0, np.int8), H, d.vocab))
+            s8 = self._h(eng.to_host(mi.T_LM_I8_S, 0, np.float32))
+            self.m.lm_i8, self.m.lm_i8_scales = q8.ctypes.data, s8.ctypes.data
         if moe:
             self.m.experts, self.m.top_k, self.m.moe_inter = d.experts, d.top_k, d.moe_inter
             self.m.router_n = (d.experts + 1 + 15) // 16 * 16
@@ -112,10 +117,11 @@ def argmax_ok(gpu_tok, want_logits):
     return (top[0] - want_logits[gpu_tok]) <= 2e-3 * np.abs(want_logits).max() * 2
 
 
-@pytest.mark.parametrize("qk_norm", [1, 0])
-def test_decode_steps_vs_oracle_teacher_forced(qk_norm):
-    eng = mi.Engine(small_desc(qk_norm=qk_norm), seed=42)
-    print(f"engine qk_norm={qk_norm} S={[eng.linear_s(w) for w in range(5)]}", flush=True)
+@pytest.mark.parametrize("qk_norm,lm8", [(1, 0), (0, 0), (1, 1)])
+def test_decode_steps_vs_oracle_teacher_forced(qk_norm, lm8):
+    """lm8: the int8 lm_head (gemv_i8w and both argmax stages) in place of the int4 one."""
+    eng = mi.Engine(small_desc(qk_norm=qk_norm, lm_head_int8=lm8), seed=42)
+    print(f"engine qk_norm={qk_norm} lm8={lm8} S={[eng.linear_s(w) for w in range(5)]}", flush=True)
     orc = OracleModel(eng)
     eng.capture(1)
     pos, tok = 300, 7

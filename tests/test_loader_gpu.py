@@ -101,6 +101,49 @@ def test_bf16_head_quantised_at_load(tmp_path, tie):
     eng.close()
 
 
+@pytest.mark.parametrize("tie", [False, True])
+def test_int8_head_made_at_load(tmp_path, tie):
+    """An engine built with the int8 lm_head: the checkpoint's 16-bit head (or the tied
+    embeddings) quantised at load is bitwise the oracle's row quantiser (itself pinned against
+    the reference's lm_head_int8.cc), and a decode step of the loaded model matches the oracle's
+    step with the int8 head. A packed (int4) head is refused."""
+    from test_gemv_i8w_gpu import untile
+    syn = Synth(str(tmp_path / "i8"), layers=1, V=2048, head="bf16", tie=tie)
+    path = syn.write(split=2)
+    desc = mi.checkpoint_desc(path, max_len=512, max_rows=4)
+    desc.lm_head_int8 = 1
+    eng = mi.Engine(desc, seed=5)
+    print(f"engine_load {path} (int8 head): {eng.load(path)}", flush=True)
+    H, V = eng.desc.hidden, 2048
+    q = untile(eng.to_host(mi.T_LM_I8, 0, np.int8), H, V)
+    s = eng.to_host(mi.T_LM_I8_S, 0, np.float32)
+    w = np.ascontiguousarray(syn.lm_w.astype(np.float32))  # [V][H]
+    for n in range(0, V, 7):
+        qr = np.zeros(H, np.int8)
+        sr = O.lib().orc_quantise_row_int8(O._p(np.ascontiguousarray(w[n])), H, O._p(qr))
+        assert np.float32(sr).view(np.uint32) == s[n].view(np.uint32) and np.array_equal(q[n], qr), n
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 60, 9
+    eng.reset(pos, tok)
+    for step in range(2):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        assert close(got, want), step
+        assert argmax_ok(got_tok, want)
+        tok, pos = got_tok, pos + 1
+    eng.close()
+    packed = Synth(str(tmp_path / "p8"), layers=1, V=2048)
+    ppath = packed.write(split=1)
+    d2 = mi.checkpoint_desc(ppath, max_len=512, max_rows=4)
+    d2.lm_head_int8 = 1
+    e2 = mi.Engine(d2, seed=5)
+    with pytest.raises(mi.MiError, match="packed"):
+        e2.load(ppath)
+    e2.close()
+
+
 def test_moe_tensors(tmp_path):
     syn = Synth(str(tmp_path / "m"), layers=1, H=512, experts=16, top_k=4, moe_inter=128, V=2048)
     eng = load(syn)
