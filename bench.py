@@ -293,6 +293,75 @@ def measure_cfg1(st):
             "alg_bytes": alg}
 
 
+def measure_lm_head_int8(st):
+    """The int8 lm_head (spec 9, gemv_i8w) at the 27B head's shape: K = 5120, N = 151936, M = 1,
+    int8 uniform [-127, 127] with fp32 row scales; calls alternate between two copies
+    (1.56 GB, past the 256 MB MALL). Algorithmic bytes = K N + 4 N (weights and scales) + 2 K
+    (x) + 4 N (fp32 logits)."""
+    L, D = mi.lib(), Dev()
+    K, N, copies = 5120, 151936, 2
+    ws, ss = [], []
+    for c in range(copies):
+        w = D.alloc(K * N)
+        s = D.alloc(N * 4)
+        mi.check(L.mi_fill_i8(w, K * N, 70 + c, -127, 127, st))
+        mi.check(L.mi_fill_f32(s, N, 80 + c, 0, 2e-4, 1.2e-3, 0, st))
+        ws.append(w)
+        ss.append(s)
+    x = D.alloc(K * 2)
+    mi.check(L.mi_fill_f16(x, K, 90, 1, 0.0, 1.0, st))
+    out = D.alloc(N * 4)
+    call = lambda i: mi.check(L.mi_gemv_i8w(ws[i % copies], ss[i % copies], x, out, 1, K, N, st))
+    t = time_calls(st, call, 40)
+    D.free()
+    alg = K * N + 4 * N + 2 * K + 4 * N
+    return {"workload": "int8 lm_head GEMV (gemv_i8w) at the 27B head: K=5120, N=151936, M=1",
+            "us_per_call": round(t, 2), "gbs": round(alg / t / 1e3, 1),
+            "frac_of_peak": round(alg / t / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
+
+
+def measure_mtp(args):
+    """The MTP draft lists at the 27B shape (the head: one more dense layer at the model's
+    shapes, sharing the embedding and lm_head; random-init): the plain step with the head's K/V
+    fill, one draft list (the head at one row: front, attention over its own cache, MLP, head)
+    and the verify step at k = 3 (four rows, the fill over them), at context `--context`. The
+    weights are random, so the acceptance rate says nothing about a trained head; the time per
+    list is what the speculative loop pays."""
+    ctx = args.context
+    desc = mi.desc_27b(max_len=((ctx + 64 + 1 + 63) // 64) * 64)
+    desc.mtp = 1
+    eng = mi.Engine(desc, seed=args.seed)  # the main model's weights are the bench engine's
+    eng.capture(1)
+    eng.capture(4)
+    st = eng.stream
+    eng.reset(ctx, 1000)
+    eng.generate(2)
+    pos = int(eng.ctrl()[mi.CTRL_POS])
+    plain = time_calls(st, lambda i: eng.replay(1), 20)
+    eng.reset(pos, 1000)
+    eng.draft(1)  # captures the draft graph
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        eng.draft(3)
+    t_draft3 = (time.perf_counter() - t0) / reps * 1e3
+    drafts = eng.draft(3)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        eng.verify(drafts)
+    t_verify = (time.perf_counter() - t0) / reps * 1e3
+    c = eng.ctrl()
+    assert c[mi.CTRL_DEBUG] == 0, (hex(c[mi.CTRL_DEBUG]), list(drafts), [hex(v) for v in c[:20]],
+                                   [hex(v) for v in eng.to_host(mi.T_MTP_CTRL, 0, np.uint32)[:20]])
+    eng.close()
+    return {"workload": f"27B shape with an MTP head (random-init), context {ctx}",
+            "plain_step_with_fill_ms": round(plain / 1e3, 4),
+            "draft_3_ms": round(t_draft3, 3), "draft_list_ms": round(t_draft3 / 3, 3),
+            "verify_k3_ms": round(t_verify, 3),
+            "note": "draft and verify times are host wall clock around each call (one "
+                    "synchronisation per call); the plain step is HIP-event timed"}
+
+
 def measure_cfg3(st, ctx):
     """one layer's decode attention at context `ctx`, 40 q / 8 kv heads
     of 128, int8 K/V uniform [-127, 127] with fp16 scales U(0.005, 0.05) per (pos, kv head),
@@ -586,7 +655,8 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
-    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill", "roofline"],
+    ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill", "roofline",
+                                       "lm8", "mtp"],
                     default=None,
                     help="run only that secondary measurement and print its JSON (the command the "
                          "attention and single-GEMV kernel profiles use)")
@@ -624,6 +694,12 @@ def main():
         return
     if args.only == "cfg4":
         print(json.dumps({"cfg4_moe_step": measure_cfg4(args)}), flush=True)
+        return
+    if args.only == "lm8":
+        print(json.dumps({"lm_head_int8": measure_lm_head_int8(None)}), flush=True)
+        return
+    if args.only == "mtp":
+        print(json.dumps({"mtp": measure_mtp(args)}), flush=True)
         return
     if args.only == "moe_prefill":
         # the configs[3] MoE model's chunked prefill of a 2048-token prompt, three timed calls
@@ -744,6 +820,10 @@ def main():
         other["cfg4_moe_step"] = measure_cfg4(args)
         other["cfg4_moe_step_int8_kv"] = measure_cfg4(args, kv_int8=1)
         log(f"bench: cfg4 {other['cfg4_moe_step']}")
+        other["lm_head_int8"] = measure_lm_head_int8(None)
+        log(f"bench: int8 lm_head {other['lm_head_int8']}")
+        other["mtp"] = measure_mtp(args)
+        log(f"bench: mtp {other['mtp']}")
 
     out = {
         "metric": "batch-1 decode tokens/s (27B-shape W4A16); int4 GEMV HBM GB/s vs peak",

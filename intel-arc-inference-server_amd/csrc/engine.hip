@@ -345,17 +345,6 @@ struct mi_engine {
         MI_TRY(mi_fill_f32(L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
       }
     }
-    if (m.mtp) {
-      for (Linear* l : {&mh.fc, &mh.L.qkv, &mh.L.o, &mh.L.gate_up, &mh.L.down}) MI_TRY(init_linear(*l, seed));
-      for (float* nw : {mh.L.in_norm, mh.L.post_norm, mh.pre_e, mh.pre_h, mh.final_n})
-        MI_TRY(mi_fill_f32(nw, H, seed++, 1, 1.0f, 0.02f, 1, stream));
-      if (m.qk_norm) {
-        MI_TRY(mi_fill_f32(mh.L.q_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
-        MI_TRY(mi_fill_f32(mh.L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
-      }
-      MI_TRY(mi_fill_f16(hkv_k, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
-      MI_TRY(mi_fill_f16(hkv_v, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
-    }
     if (m.lm_head_int8) {  // uniform int8 with row scales U(2e-4, 1.2e-3): the int4 head's spread
       MI_TRY(mi_fill_i8(lm_i8, size_t(m.vocab) * H, seed++, -127, 127, stream));
       MI_TRY(mi_fill_f32(lm_i8s, m.vocab, seed++, 0, 2e-4f, 1.2e-3f, 0, stream));
@@ -372,6 +361,24 @@ struct mi_engine {
     } else {
       MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_k), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
       MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_v), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+    }
+    // the head last, so a model's own weights are the same with and without it
+    if (m.mtp) {
+      // the head's linears at a quarter of the layers' scales, U(0.0005, 0.005): its residual
+      // stream starts at fc's output (K = 2 hidden over inputs with a common mode), and at the
+      // layers' scales the random head's MLP output overflows fp16 at the 27B shape
+      for (Linear* l : {&mh.fc, &mh.L.qkv, &mh.L.o, &mh.L.gate_up, &mh.L.down}) {
+        MI_TRY(mi_fill_u32(l->q, size_t(l->K / 8) * l->N, seed++, stream));
+        MI_TRY(mi_fill_f16(l->s, size_t(l->K / 64) * l->N, seed++, 0, 0.0005f, 0.005f, stream));
+      }
+      for (float* nw : {mh.L.in_norm, mh.L.post_norm, mh.pre_e, mh.pre_h, mh.final_n})
+        MI_TRY(mi_fill_f32(nw, H, seed++, 1, 1.0f, 0.02f, 1, stream));
+      if (m.qk_norm) {
+        MI_TRY(mi_fill_f32(mh.L.q_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+        MI_TRY(mi_fill_f32(mh.L.k_norm, HD, seed++, 1, 1.0f, 0.02f, 1, stream));
+      }
+      MI_TRY(mi_fill_f16(hkv_k, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
+      MI_TRY(mi_fill_f16(hkv_v, size_t(KVH) * m.max_len * HD, seed++, 1, 0.0f, 1.0f, stream));
     }
     // RoPE table in double, stored fp32 (src/loader/loader.cc:702-716)
     {
