@@ -365,11 +365,12 @@ def measure_mtp(args):
 def measure_cfg3(st, ctx):
     """one layer's decode attention at context `ctx`, 40 q / 8 kv heads
     of 128, int8 K/V uniform [-127, 127] with fp16 scales U(0.005, 0.05) per (pos, kv head),
-    64-token pages in a shuffled table; attn_decode + attn_reduce per call. The calls cycle
+    64-token pages in a shuffled table; attn_decode + attn_reduce per call at 64 blocks per kv
+    head (the engine's blocking; 512 / 2048 positions per block). The calls cycle
     through enough cache copies (at least 4, at least 640 MB in all) that none is still in
     the 256 MB MALL when it is read again."""
     L, D = mi.lib(), Dev()
-    QH, KVH, HD, P, tgt = 40, 8, 128, 64, 128
+    QH, KVH, HD, P, tgt = 40, 8, 128, 64, 64  # tgt 64: the fastest blocking at 32k and 128k (a 24..128 sweep)
     rng = np.random.default_rng(ctx)
     copy_bytes = 2 * KVH * ctx * HD + 2 * KVH * ctx * 2
     copies = max(4, -(-640 * 2**20 // copy_bytes))
