@@ -334,6 +334,9 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
                                                          float* __restrict__ rstd_out, uint32_t hidden,
                                                          uint32_t vocab, float eps) {
   __shared__ float chunk[1024];
+  // rows up to kHeld * 64 wide stay in registers between the two passes (with their norm weights,
+  // loaded alongside), so a row takes one memory round trip; wider rows are read again
+  constexpr uint32_t kPass = 8, kIters = 3, kHeld = kPass * kIters * 4;
   const uint32_t m = blockIdx.x, t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint16_t* src = resid + (size_t)m * hidden;
   if constexpr (GATHER) {
@@ -346,16 +349,33 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
   }
   uint16_t* dst = resid + (size_t)m * hidden;
   const uint32_t nch = hidden / 64;
-  // wave w takes chunks w, w + 4, ...; the loads of up to 8 chunks go out together
-  for (uint32_t c0 = wave; c0 < nch; c0 += 32) {
-    uint16_t v16[8];
+  const bool held = nch <= kHeld;
+  // wave w takes chunks w, w + 4, ...; the loads of up to kPass chunks go out together
+  uint16_t hv[kIters][kPass];
+  float hw[kIters][kPass];
+  if (held) {
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {
+    for (uint32_t it = 0; it < kIters; ++it)
+#pragma unroll
+      for (uint32_t u = 0; u < kPass; ++u) {
+        const uint32_t c = wave + 4u * (kPass * it + u);
+        hv[it][u] = c < nch ? src[c * 64 + lane] : (uint16_t)0;
+        hw[it][u] = c < nch ? norm_w[c * 64 + lane] : 0.f;
+      }
+  }
+  for (uint32_t c0 = wave, it = 0; c0 < nch; c0 += 4u * kPass, ++it) {
+    uint16_t v16[kPass];
+#pragma unroll
+    for (uint32_t u = 0; u < kPass; ++u) {
       const uint32_t c = c0 + 4 * u;
-      v16[u] = c < nch ? src[c * 64 + lane] : (uint16_t)0;
+      if (held) {
+        v16[u] = it == 0 ? hv[0][u] : (it == 1 ? hv[1][u] : hv[2][u]);
+      } else {
+        v16[u] = c < nch ? src[c * 64 + lane] : (uint16_t)0;
+      }
     }
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {
+    for (uint32_t u = 0; u < kPass; ++u) {
       const uint32_t c = c0 + 4 * u;
       if (c < nch) {
         if constexpr (GATHER) dst[c * 64 + lane] = v16[u];
@@ -377,6 +397,16 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
   __syncthreads();
   const float r = s_rstd;
   if (t == 0 && rstd_out) rstd_out[m] = r;  // after the barrier, which would otherwise wait for it
+  if (held) {
+#pragma unroll
+    for (uint32_t it = 0; it < kIters; ++it)
+#pragma unroll
+      for (uint32_t u = 0; u < kPass; ++u) {
+        const uint32_t c = wave + 4u * (kPass * it + u);
+        if (c < nch) x_out[(size_t)m * hidden + c * 64 + lane] = f2h(h2f(hv[it][u]) * r * hw[it][u]);
+      }
+    return;
+  }
   for (uint32_t k0 = t; k0 < hidden; k0 += 8 * kWG) {
     uint16_t v16[8];
 #pragma unroll
