@@ -22,6 +22,7 @@
 #include "mi_capi_internal.h"
 #include "mi_common.h"
 #include "attn_core.h"
+#include "attn_merge.h"
 
 namespace mi {
 namespace {
@@ -76,26 +77,13 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   }
   const float gv = gated && attn_gate ? attn_gate[((size_t)m * q_heads + h) * HD + d] : 0.f;
   if (m >= ctrl[CTRL_NACT]) return;  // uniform
-  const uint32_t pos = ctrl[CTRL_POS];
-  uint32_t L = pos + m + 1;
-  if (kv_len && L > kv_len) L = kv_len;
-  uint32_t nb = (L - 1) / v2_ppw(L, tgt) + 1;
-  if (nb > tgt) nb = tgt;
+  const uint32_t nb = merge_blocks(ctrl[CTRL_POS], m, kv_len, tgt);
   constexpr uint32_t BAT = 64;
   // wave 0: the common max and the per-block factors
   if (d < 64) {
     auto mx_of = [&](uint32_t b) { return b < 128u ? pm[b >> 6] : base[b * bstride]; };
     auto sm_of = [&](uint32_t b) { return b < 128u ? ps[b >> 6] : base[b * bstride + 1]; };
-    float mx = -INFINITY;
-    for (uint32_t b = d; b < nb; b += 64) mx = fmaxf(mx, mx_of(b));
-    mx = wave_max(mx);
-    float sm = 0.f;
-    for (uint32_t b = d; b < nb; b += 64) {
-      const float f = expf(mx_of(b) - mx);
-      fac[b] = f;
-      sm = __builtin_fmaf(sm_of(b), f, sm);
-    }
-    sm = wave_sum(sm);
+    const float sm = merge_factors(d, nb, mx_of, sm_of, fac);
     if (d == 0) s_sm = sm;
   }
   __syncthreads();
@@ -114,18 +102,20 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
     for (uint32_t u = 0; u < BAT; ++u)
       if (b + u < nb) acc = __builtin_fmaf(v[u], fac[b + u], acc);
   }
-  float o = acc / s_sm;
+  uint16_t r;
   if constexpr (ROT) {
+    float o = acc / s_sm;
     __shared__ float xch[256];
     float v1[1] = {kv8_flip(o, kv8_sign_neg(d))};
     fwht256<1>(v1, d, xch);  // HD = 256: every thread of the work-group is here
     o = v1[0] * 0.0625f;
+    if (gated && attn_gate)
+      r = f2h(h2f(f2h(o)) * sigmoid_f32(gv));
+    else
+      r = f2h(o);
+  } else {
+    r = merge_out(acc, s_sm, gated && attn_gate, gv);
   }
-  uint16_t r;
-  if (gated && attn_gate)
-    r = f2h(h2f(f2h(o)) * sigmoid_f32(gv));
-  else
-    r = f2h(o);
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
