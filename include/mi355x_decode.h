@@ -362,6 +362,13 @@ int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t expe
 int mi_moe_gate_up(const uint32_t* route, const uint16_t* x, const uint32_t* gu_blocks,
                    uint16_t* h, uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden,
                    uint32_t inter, void* stream);
+/* moe_route (moe.cl:192-262) and moe_gate_up (moe.cl:335-381) in one launch: every
+ * work-group of a row forms the row's route from logits [M][router_n] (bitwise mi_moe_route's
+ * row) before addressing its expert, and stores it to route [M][MI_MOE_ROUTE_WORDS] for
+ * mi_moe_down; h as mi_moe_gate_up. The reference runs the two as separate kernels. */
+int mi_moe_gate_up_routed(const float* logits, uint32_t router_n, uint32_t* route, const uint16_t* x,
+                          const uint32_t* gu_blocks, uint16_t* h, uint32_t M, uint32_t experts,
+                          uint32_t top_k, uint32_t hidden, uint32_t inter, void* stream);
 /* moe_down (moe.cl:383-470): resid [M][hidden] += the slot-ordered combine of each slot's
  * down projection (layout-1 blocks of (hidden / 16) * (inter / 64) * 136 u32 per expert, K
  * split in 2 slices) weighted by w_k, plus the shared expert's times its gate. */

@@ -103,6 +103,7 @@ SIGNATURES = {
     "mi_gemv_f16w": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_route": (i32, [vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_gate_up": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+    "mi_moe_gate_up_routed": (i32, [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "mi_moe_down": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
 }
 

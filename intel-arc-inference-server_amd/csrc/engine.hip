@@ -458,11 +458,12 @@ struct mi_engine {
       MI_TRY(launch_o(L, M));
       const float* next_w = next_norm(li);
       if (d.experts) {
-        // the MoE block (moe.cl:1-13): router || shared gate, route, gate||up, down folding
-        // into the residual, then the next norm with nothing left to fold
+        // the MoE block (moe.cl:1-13): router || shared gate, route + gate||up (one launch:
+        // each work-group routes its row itself), down folding into the residual, then the
+        // next norm with nothing left to fold
         MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
-        MI_TRY(mi_moe_route(moe_logits, moe_route, M, d.experts, d.top_k, router_n, stream));
-        MI_TRY(mi_moe_gate_up(moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
+        MI_TRY(mi_moe_gate_up_routed(moe_logits, router_n, moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k,
+                                     d.hidden, d.moe_inter, stream));
         MI_TRY(mi_moe_down(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
         MI_TRY(mi_norm_rows(resid, next_w, x, rstd, M, d.hidden, d.rms_eps, stream));
         continue;

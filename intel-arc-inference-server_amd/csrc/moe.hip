@@ -28,6 +28,14 @@ constexpr uint32_t kMaxHidden = 4096, kMaxSlotsInter = 9 * 1024, kMaxGroups = kM
 
 __device__ __forceinline__ float rf(float v) { return h2f(f2h(v)); }
 
+#ifdef MI_MOE_STAMPS
+__device__ uint64_t g_moe_stamps[2][1024][12];
+#define MOE_STAMP(k, i) \
+  if (threadIdx.x == 0 && blockIdx.y == 0) g_moe_stamps[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime();
+#else
+#define MOE_STAMP(k, i)
+#endif
+
 // ---- router || shared-gate GEMV (gemv_bf16.cl:103-200), fp16 weights --------------------
 // grid (N/16, M), 16 * ksplit lanes: lane l of slice q sums column n_tile*16 + l over k8 in
 // [q*per, (q+1)*per), 8 products per k8 in k order; slices merge by the pairwise tree.
@@ -109,77 +117,74 @@ __device__ __forceinline__ float wave_tree(float x, uint32_t n, F op) {
 // and the shared gate's), into s_row (32 words of LDS; complete after the function's closing
 // barrier). The whole work-group calls it; blockDim.x >= max(E, 64).
 __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint32_t top_k) {
-  __shared__ float s_red[256], s_top_p[9], s_bc;
-  __shared__ uint32_t s_pb[256];
+  __shared__ float s_red[256], s_top_p[9];
+  __shared__ uint64_t s_key[256], s_cand[4 * 9];
   __shared__ uint32_t s_top_id[9];
   const uint32_t e = threadIdx.x, lane = e & 63u;
   const bool live = e < E;
   const float l = live ? rf(lg[e]) : -INFINITY;
+  const float l_gate = e == 9u ? lg[E] : 0.f;  // the shared gate's logit (lane 9 writes s)
   const uint32_t n0 = E < 64u ? E : 64u;  // elements left when the cross-wave levels are done
-  // max (exact whatever the order): the levels st >= 64 in LDS, the rest in wave 0
   s_red[e] = l;
+  if (e < 4u * 9u) s_cand[e] = 0ull;
   __syncthreads();
-  for (uint32_t st = E / 2; st >= 64u; st >>= 1) {
-    if (e < st) s_red[e] = fmaxf(s_red[e], s_red[e + st]);
-    __syncthreads();
-  }
+  MOE_STAMP(0, 5);
+  // Wave 0 alone: lane l holds v[u] = element l + 64 u and applies the cross-wave levels of
+  // the trees in their order (st = E/2 .. 64: s[e] = op(s[e], s[e + st])), then the levels
+  // st < 64 across its lanes. The max is exact whatever the order; the sum is the pairwise
+  // tree. p and the rank keys of all E elements go to LDS for the other waves.
   if (e < 64u) {
-    const float r = wave_tree(lane < n0 ? s_red[lane] : -INFINITY, n0, [](float a, float b) { return fmaxf(a, b); });
-    if (e == 0) s_bc = r;
-  }
-  __syncthreads();
-  const float mx = s_bc;
-  const float ex = live ? expf(l - mx) : 0.f;
-  // the pairwise sum, level st: s[e] = s[e] + s[e + st] for e < st (the same tree in LDS and
-  // then in wave 0's lanes)
-  s_red[e] = ex;
-  __syncthreads();
-  for (uint32_t st = E / 2; st >= 64u; st >>= 1) {
-    if (e < st) s_red[e] += s_red[e + st];
-    __syncthreads();
-  }
-  if (e < 64u) {
-    const float r = wave_tree(lane < n0 ? s_red[lane] : 0.f, n0, [](float a, float b) { return a + b; });
-    if (e == 0) s_bc = r;
-  }
-  __syncthreads();
-  const float p = ex / s_bc;
-  // rank = #{j : p_j > p_e or (p_j == p_e and j < e)} = #{j < e : p_j >= p_e} + #{j > e :
-  // p_j > p_e}; p >= 0, so p's bits compare as unsigned integers. The j below the wave's
-  // experts all take >=, those above all take >, the wave's own 64 the per-lane choice.
-  const uint32_t pb = __builtin_bit_cast(uint32_t, p);
-  s_pb[e] = pb;
-  __syncthreads();
-  const uint32_t wb = e & ~63u, we = min(wb + 64u, E);
-  uint32_t rank = 0;
-  for (uint32_t j0 = 0; j0 < wb; j0 += 16u) {
-    uint32_t kv[16];
+    float v[4];
 #pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
+    for (uint32_t u = 0; u < 4; ++u) v[u] = lane + 64u * u < E ? s_red[lane + 64u * u] : -INFINITY;
+    auto levels = [E](float v0, float v1, float v2, float v3, auto op) {
+      return E == 256u ? op(op(v0, v2), op(v1, v3)) : (E == 128u ? op(v0, v1) : v0);
+    };
+    const auto fmax_op = [](float a, float b) { return fmaxf(a, b); };
+    const auto add_op = [](float a, float b) { return a + b; };
+    const float mloc = levels(v[0], v[1], v[2], v[3], fmax_op);
+    const float mx = __shfl(wave_tree(lane < n0 ? mloc : -INFINITY, n0, fmax_op), 0, 64);
+    float ex[4];
 #pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) rank += kv[u] >= pb ? 1u : 0u;
-  }
-  for (uint32_t j0 = wb; j0 < we; j0 += 16u) {
-    uint32_t kv[16];
+    for (uint32_t u = 0; u < 4; ++u) ex[u] = lane + 64u * u < E ? expf(v[u] - mx) : 0.f;
+    const float sloc = levels(ex[0], ex[1], ex[2], ex[3], add_op);
+    const float sum = __shfl(wave_tree(lane < n0 ? sloc : 0.f, n0, add_op), 0, 64);
 #pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
-#pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) {
-      const uint32_t j = j0 + u;
-      rank += (j < e ? kv[u] >= pb : (j > e && kv[u] > pb)) ? 1u : 0u;
+    for (uint32_t u = 0; u < 4; ++u) {
+      const uint32_t j = lane + 64u * u;
+      const uint32_t pb = __builtin_bit_cast(uint32_t, ex[u] / sum);
+      s_key[j] = j < E ? ((uint64_t)pb << 32) | (uint32_t)~j : 0ull;
     }
   }
-  for (uint32_t j0 = wb + 64u; j0 < E; j0 += 16u) {
-    uint32_t kv[16];
-#pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) kv[u] = s_pb[j0 + u];
-#pragma unroll
-    for (uint32_t u = 0; u < 16; ++u) rank += kv[u] > pb ? 1u : 0u;
-  }
+  __syncthreads();
+  MOE_STAMP(0, 6);
+  MOE_STAMP(0, 7);
   const uint32_t slots = top_k + 1;
-  if (live && rank < slots) {
-    s_top_id[rank] = e;
-    s_top_p[rank] = p;
+  const uint64_t key = s_key[e];
+  const float p = __builtin_bit_cast(float, (uint32_t)(key >> 32));
+  const uint32_t nw = (blockDim.x + 63u) / 64u, wb = e & ~63u;
+  uint32_t r1 = 0;
+#pragma unroll 4
+  for (uint32_t j0 = 0; j0 < 64u; j0 += 8u) {
+    uint64_t kv[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) kv[u] = s_key[wb + j0 + u];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) r1 += kv[u] > key ? 1u : 0u;
+  }
+  const bool cand = live && r1 < slots;
+  if (cand) s_cand[(e >> 6) * 9u + r1] = key;
+  __syncthreads();
+  MOE_STAMP(0, 8);
+  if (cand) {
+    uint32_t rank = 0;
+    for (uint32_t w = 0; w < nw; ++w)
+#pragma unroll
+      for (uint32_t k = 0; k < 9u; ++k) rank += s_cand[w * 9u + k] > key ? 1u : 0u;
+    if (rank < slots) {
+      s_top_id[rank] = e;
+      s_top_p[rank] = p;
+    }
   }
   __syncthreads();
   // the row, one word per lane: w_k = rne(p_k / s8) with s8 the top_k p added in rank order
@@ -195,7 +200,7 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
   } else if (e == 8u) {
     s_row[R_P9] = __builtin_bit_cast(uint32_t, s_top_p[top_k]);
   } else if (e == 9u) {
-    s_row[R_SG] = __builtin_bit_cast(uint32_t, rf(sigmoid_f32(rf(lg[E]))));
+    s_row[R_SG] = __builtin_bit_cast(uint32_t, rf(sigmoid_f32(rf(l_gate))));
   } else if (e > R_P9 && e < kRouteWords) {
     s_row[e] = 0u;
   }
@@ -253,8 +258,12 @@ __device__ __forceinline__ u4_t half_piece(const uint32_t* tile, uint32_t ch, ui
   return load_stream16(tile + off);
 }
 
-// dst[k] = h2f(src[k]) for k < n (n a multiple of 8, src 16-byte aligned), from u4_t pieces
-// already loaded: v[u] holds piece threadIdx.x + 256 u
+// LDS floats per 64-element group of a staged activation row: 4 of padding, so the groups
+// that the lanes of one wave read together start in different banks
+constexpr uint32_t kXs = 68;
+
+// dst[g * kXs + k % 64] = h2f(src[k]) for k < n, g = k / 64 (n a multiple of 8, src 16-byte
+// aligned), from u4_t pieces already loaded: v[u] holds piece threadIdx.x + 256 u
 template <int PER>
 __device__ __forceinline__ void put_f16(float* dst, const u4_t (&v)[PER], uint32_t n) {
   const uint32_t n8 = n / 8u;
@@ -263,8 +272,9 @@ __device__ __forceinline__ void put_f16(float* dst, const u4_t (&v)[PER], uint32
     const uint32_t i = threadIdx.x + 256u * u;
     if (i < n8) {
       const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      float* d = dst + (i / 8u) * kXs + (i % 8u) * 8u;
 #pragma unroll
-      for (uint32_t j = 0; j < 8; ++j) dst[8u * i + j] = h2f((uint16_t)(w[j / 2] >> (16 * (j % 2))));
+      for (uint32_t j = 0; j < 8; ++j) d[j] = h2f((uint16_t)(w[j / 2] >> (16 * (j % 2))));
     }
   }
 }
@@ -278,18 +288,22 @@ __device__ __forceinline__ void get_f16(u4_t (&v)[PER], const uint16_t* src, uin
   }
 }
 
-// group_term on a staged half tile (column c < 8 of it)
+// group_term on a staged half tile (column c < 8 of it); xs: the group's 64 activations
+// (16-byte aligned), read four at a time
 __device__ __forceinline__ float half_term(const uint32_t* ht, uint32_t c, const float* __restrict__ xs) {
   uint32_t wd[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) wd[j] = ht[j * 8 + c];
   const uint16_t sc = reinterpret_cast<const uint16_t*>(ht + 64)[c];
+  const f4_t* x4 = reinterpret_cast<const f4_t*>(xs);
   float g = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    const f4_t lo = x4[2 * j], hi = x4[2 * j + 1];
+    const float xv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     float a = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a += (float)((int)((wd[j] >> (4 * i)) & 0xFu) - 8) * xs[j * 8 + i];
+    for (int i = 0; i < 8; ++i) a += (float)((int)((wd[j] >> (4 * i)) & 0xFu) - 8) * xv[i];
     g += a;
   }
   return g * h2f(sc);
@@ -299,23 +313,40 @@ __device__ __forceinline__ float half_term(const uint32_t* ht, uint32_t c, const
 // grid (slots * inter/8, M): work-group (slot, ib, ch) makes h[m][slot][16 ib + 8 ch .. + 7]
 // from half ch of the expert's gate tile 2 ib and up tile 2 ib + 1 (interleave16 columns).
 // Dynamic LDS: 2 G staged half tiles.
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(const uint32_t* __restrict__ route,
+// ROUTED: the work-group forms its row's route row itself from the router logits (every
+// work-group of the row runs route_compute on the same logits, so they agree bitwise with
+// each other and with moe_route_kernel) and work-group 0 of the row stores it for the down
+// launch; `route` is then the output. This takes the routing launch off the block's chain.
+template <bool ROUTED>
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__ route,
+                                                          const float* __restrict__ logits,
+                                                          uint32_t router_n,
                                                           const uint16_t* __restrict__ x,
                                                           const uint32_t* __restrict__ gu,
                                                           uint16_t* __restrict__ h, uint32_t E,
                                                           uint32_t top_k, uint32_t hidden,
                                                           uint32_t inter) {
   extern __shared__ uint32_t s_w[];  // [2][G][kHalfU32]
-  __shared__ float s_x[kMaxHidden];
+  __shared__ __align__(16) float s_x[kMaxHidden / 64 * kXs];
   __shared__ float s_t[2][8][kMaxGroups];
   __shared__ float s_r[2][8][kUpKs];
+  __shared__ uint32_t s_row[ROUTED ? kRouteWords : 1];
   const uint32_t t = threadIdx.x, m = blockIdx.y;
   const uint32_t nhb = inter / 8, slot = blockIdx.x / nhb, hb = blockIdx.x % nhb, ib = hb / 2, ch = hb % 2;
   const uint32_t G = hidden / 64, slots = top_k + 1;
-  const uint32_t e = slot_expert(route + (size_t)m * kRouteWords, slot, E, top_k);
+  MOE_STAMP(0, 0);
   constexpr int XP = kMaxHidden / 8 / 256;  // x pieces per thread
   u4_t xv[XP];
   get_f16<XP>(xv, x + (size_t)m * hidden, hidden);
+  uint32_t e;
+  if constexpr (ROUTED) {
+    route_compute(logits + (size_t)m * router_n, s_row, E, top_k);
+    e = slot_expert(s_row, slot, E, top_k);
+    if (blockIdx.x == 0 && t < kRouteWords) route[(size_t)m * kRouteWords + t] = s_row[t];
+  } else {
+    e = slot_expert(route + (size_t)m * kRouteWords, slot, E, top_k);
+  }
+  MOE_STAMP(0, 1);
   {
     const size_t block = (size_t)(2 * inter / 16) * G * kTileU32;
     const uint32_t* base = gu + (size_t)e * block + (size_t)(2 * ib) * G * kTileU32;
@@ -340,10 +371,12 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const uint32_t* __rest
   __syncthreads();
   // (tile, column, group) terms: thread t takes column t % 8 of groups (t / 8) % 16 + 16 k
   // of tile t / 128
+  MOE_STAMP(0, 2);
   const uint32_t c = t & 7u, gsub = (t >> 3) & 15u, tl = t >> 7;
   const uint32_t* tiles = s_w + (size_t)tl * G * kHalfU32;
-  for (uint32_t g = gsub; g < G; g += 16u) s_t[tl][c][g] = half_term(tiles + (size_t)g * kHalfU32, c, s_x + g * 64);
+  for (uint32_t g = gsub; g < G; g += 16u) s_t[tl][c][g] = half_term(tiles + (size_t)g * kHalfU32, c, s_x + g * kXs);
   __syncthreads();
+  MOE_STAMP(0, 3);
   if (t < 2u * 8u * kUpKs) {  // (tile, column, slice): the slice's groups in order
     const uint32_t tl2 = t / (8u * kUpKs), c2 = (t / kUpKs) % 8u, q = t % kUpKs;
     const uint32_t per = G / kUpKs;
@@ -365,6 +398,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(const uint32_t* __rest
     const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
     h[((size_t)m * slots + slot) * inter + ib * 16 + ch * 8 + t] = f2h(h2f(s_b) * h2f(u_b));
   }
+  MOE_STAMP(0, 4);
 }
 
 // ---- down + combine + residual (moe.cl:383-470; twin moe_ref.h:140-177) ---------------------
@@ -377,15 +411,24 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
                                                        uint32_t top_k, uint32_t hidden,
                                                        uint32_t inter) {
   extern __shared__ uint32_t s_w[];  // [slots][G][kHalfU32]
-  __shared__ float s_h[kMaxSlotsInter];
+  __shared__ __align__(16) float s_h[kMaxSlotsInter / 64 * kXs];
   __shared__ float s_t[9][8][16];  // [slot][column][group], inter <= 1024
   __shared__ float s_d[9][8];
   const uint32_t t = threadIdx.x, m = blockIdx.y, nb = blockIdx.x / 2, ch = blockIdx.x % 2;
   const uint32_t G = inter / 64, slots = top_k + 1;
+  MOE_STAMP(1, 0);
   const uint32_t* row = route + (size_t)m * kRouteWords;
   uint32_t ids[9];
 #pragma unroll
   for (uint32_t k = 0; k < 9; ++k) ids[k] = k < slots ? slot_expert(row, k, E, top_k) : E;
+  // the combine's operands go out now rather than after the arithmetic: the slot weights and
+  // the shared gate (uniform), and this lane's residual element (lanes 0..7)
+  float wk[8];
+#pragma unroll
+  for (uint32_t k = 0; k < 8; ++k) wk[k] = k < top_k ? __builtin_bit_cast(float, row[R_W + k]) : 0.f;
+  const float sg = __builtin_bit_cast(float, row[R_SG]);
+  uint16_t* rp = resid + (size_t)m * hidden + nb * 16 + ch * 8 + (t & 7u);
+  const uint16_t r_old = t < 8u ? *rp : (uint16_t)0;
   constexpr int HP = kMaxSlotsInter / 8 / 256 + 1;  // h pieces per thread (<= 1152 pieces)
   u4_t hv[HP];
   get_f16<HP>(hv, h + (size_t)m * slots * inter, slots * inter);
@@ -413,12 +456,14 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
     }
   }
   __syncthreads();
+  MOE_STAMP(1, 2);
   const uint32_t tasks = slots * 8u * G;
   for (uint32_t i = t; i < tasks; i += 256u) {
     const uint32_t slot = i / (8u * G), rem = i % (8u * G), g = rem / 8u, c = rem % 8u;
-    s_t[slot][c][g] = half_term(s_w + ((size_t)slot * G + g) * kHalfU32, c, s_h + slot * inter + g * 64);
+    s_t[slot][c][g] = half_term(s_w + ((size_t)slot * G + g) * kHalfU32, c, s_h + (slot * G + g) * kXs);
   }
   __syncthreads();
+  MOE_STAMP(1, 3);
   if (t < slots * 8u) {
     const uint32_t slot = t / 8u, c = t % 8u, per = G / kDnKs;
     float r[kDnKs];
@@ -434,17 +479,15 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
   if (t < 8u) {
     // moe_ref.h:144-152: sum_k rne(rne(d_k) * w_k) in slot order; + rne(rne(d_shared) * s)
     float sum = 0.f;
-    for (uint32_t k = 0; k < top_k; ++k) {
-      const float wk = __builtin_bit_cast(float, row[R_W + k]);
-      sum += h2f(f2h(h2f(f2h(s_d[k][t])) * wk));
-    }
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k)
+      if (k < top_k) sum += h2f(f2h(h2f(f2h(s_d[k][t])) * wk[k]));
     const uint16_t r_b = f2h(sum);
-    const float sg = __builtin_bit_cast(float, row[R_SG]);
     const uint16_t sh_b = f2h(h2f(f2h(s_d[top_k][t])) * sg);
     const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
-    uint16_t* rp = resid + (size_t)m * hidden + nb * 16 + ch * 8 + t;
-    *rp = f2h(h2f(*rp) + h2f(o_b));
+    *rp = f2h(h2f(r_old) + h2f(o_b));
   }
+  MOE_STAMP(1, 4);
 }
 
 int check_moe(uint32_t M, uint32_t E, uint32_t top_k, uint32_t hidden, uint32_t inter) {
@@ -480,6 +523,13 @@ extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* o
   return mi_hip(static_cast<int>(hipGetLastError()), "gemv_f16w launch");
 }
 
+#ifdef MI_MOE_STAMPS
+extern "C" int mi_moe_stamps(uint64_t* out) {
+  return mi_hip((int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_moe_stamps), sizeof(uint64_t) * 2 * 1024 * 12),
+                "moe stamps");
+}
+#endif
+
 extern "C" int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts, uint32_t top_k,
                             uint32_t router_n, void* stream) {
   if (!logits || !route) return mi_fail(MI_ERR_ARG, "moe_route: null pointer");
@@ -499,9 +549,23 @@ extern "C" int mi_moe_gate_up(const uint32_t* route, const uint16_t* x, const ui
   if (reinterpret_cast<uintptr_t>(gu_blocks) % 16 || reinterpret_cast<uintptr_t>(x) % 16)
     return mi_fail(MI_ERR_ARG, "moe_gate_up: gu_blocks and x need 16-byte alignment");
   const size_t lds = size_t(2) * (hidden / 64) * kHalfU32 * 4;
-  moe_gate_up_kernel<<<dim3((top_k + 1) * (inter / 8), M), 256, lds, static_cast<hipStream_t>(stream)>>>(
-      route, x, gu_blocks, h, experts, top_k, hidden, inter);
+  moe_gate_up_kernel<false><<<dim3((top_k + 1) * (inter / 8), M), 256, lds, static_cast<hipStream_t>(stream)>>>(
+      const_cast<uint32_t*>(route), nullptr, 0, x, gu_blocks, h, experts, top_k, hidden, inter);
   return mi_hip(static_cast<int>(hipGetLastError()), "moe_gate_up launch");
+}
+
+extern "C" int mi_moe_gate_up_routed(const float* logits, uint32_t router_n, uint32_t* route, const uint16_t* x,
+                                     const uint32_t* gu_blocks, uint16_t* h, uint32_t M, uint32_t experts,
+                                     uint32_t top_k, uint32_t hidden, uint32_t inter, void* stream) {
+  if (!logits || !route || !x || !gu_blocks || !h) return mi_fail(MI_ERR_ARG, "moe_gate_up_routed: null pointer");
+  if (int e = check_moe(M, experts, top_k, hidden, inter)) return e;
+  if (router_n < experts + 1) return mi_fail(MI_ERR_SHAPE, "moe_gate_up_routed: router_n must hold experts + 1 rows");
+  if (reinterpret_cast<uintptr_t>(gu_blocks) % 16 || reinterpret_cast<uintptr_t>(x) % 16)
+    return mi_fail(MI_ERR_ARG, "moe_gate_up_routed: gu_blocks and x need 16-byte alignment");
+  const size_t lds = size_t(2) * (hidden / 64) * kHalfU32 * 4;
+  moe_gate_up_kernel<true><<<dim3((top_k + 1) * (inter / 8), M), 256, lds, static_cast<hipStream_t>(stream)>>>(
+      route, logits, router_n, x, gu_blocks, h, experts, top_k, hidden, inter);
+  return mi_hip(static_cast<int>(hipGetLastError()), "moe_gate_up_routed launch");
 }
 
 extern "C" int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks, uint16_t* resid,

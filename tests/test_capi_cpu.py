@@ -57,6 +57,9 @@ def test_moe_argument_errors_without_a_gpu():
     assert L.mi_moe_route(8, 8, 1, 256, 9, 272, None) == -2      # top_k > 8
     assert L.mi_moe_route(8, 8, 1, 256, 8, 256, None) == -2      # router_n < experts + 1
     assert L.mi_moe_gate_up(8, 8, 8, 8, 1, 256, 8, 2000, 512, None) == -2  # hidden % 512
+    assert L.mi_moe_gate_up_routed(None, 272, 8, 8, 8, 8, 1, 256, 8, 2048, 512, None) == -1
+    assert L.mi_moe_gate_up_routed(8, 256, 8, 8, 8, 8, 1, 256, 8, 2048, 512, None) == -2  # router_n < E + 1
+    assert L.mi_moe_gate_up_routed(8, 272, 8, 8, 8, 8, 1, 256, 8, 2000, 512, None) == -2  # hidden % 512
     assert L.mi_moe_down(8, 8, 8, 8, 1, 256, 8, 2048, 2048, None) == -2    # inter > 1024
     assert L.mi_gemv_f16w(8, 16, 8, 1, 2048, 272, 3, None) == -2           # ksplit not 2^n
     assert b"ksplit" in L.mi_last_error()

@@ -178,6 +178,29 @@ def test_gate_up_and_down_vs_oracle(moe256, M):
         assert f16_ulps(res_gpu[m], res_or).max() <= 2
 
 
+@pytest.mark.parametrize("E,hidden,inter,M", [(256, 2048, 512, 1), (256, 2048, 512, 3), (16, 512, 128, 2)])
+def test_routed_gate_up_is_route_then_gate_up(E, hidden, inter, M):
+    """mi_moe_gate_up_routed (routing inside the gate||up launch) writes the route rows and h
+    bitwise mi_moe_route + mi_moe_gate_up, including planted exact ties in the logits."""
+    mo = Moe(3, E=E, hidden=hidden, inter=inter, router_n=E + 16)
+    print(f"routed gate_up E={E} hidden={hidden} inter={inter} M={M}", flush=True)
+    rng = np.random.default_rng(E + M)
+    lg = rng.standard_normal((M, mo.router_n)).astype(np.float32)
+    lg[0, [1, 5, 9, 13]] = 2.75  # a tie straddling the top-k boundary
+    x = O.f32_to_f16_bits(rng.standard_normal((M, hidden)).astype(np.float32))
+    dl, dx = dev(lg), dev(x)
+    r1, r2 = empty((M, ROUTE_WORDS), np.uint32), empty((M, ROUTE_WORDS), np.uint32)
+    h1 = empty((M, mo.top_k + 1, inter), np.uint16)
+    h2 = empty((M, mo.top_k + 1, inter), np.uint16)
+    mi.call("mi_moe_route", ptr(dl), ptr(r1), M, E, mo.top_k, mo.router_n, stream())
+    mi.call("mi_moe_gate_up", ptr(r1), ptr(dx), ptr(mo.d_gu), ptr(h1), M, E, mo.top_k, hidden, inter, stream())
+    mi.call("mi_moe_gate_up_routed", ptr(dl), mo.router_n, ptr(r2), ptr(dx), ptr(mo.d_gu), ptr(h2), M, E,
+            mo.top_k, hidden, inter, stream())
+    sync()
+    assert np.array_equal(host(r1, np.uint32), host(r2, np.uint32))
+    assert np.array_equal(host(h1, np.uint16), host(h2, np.uint16))
+
+
 def test_malformed_route_row_reads_the_shared_block():
     mo = Moe(2, E=16, hidden=512, inter=128, router_n=32)
     M = 1
