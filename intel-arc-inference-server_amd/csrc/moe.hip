@@ -28,13 +28,6 @@ constexpr uint32_t kMaxHidden = 4096, kMaxSlotsInter = 9 * 1024, kMaxGroups = kM
 
 __device__ __forceinline__ float rf(float v) { return h2f(f2h(v)); }
 
-#ifdef MI_MOE_STAMPS
-__device__ uint64_t g_moe_stamps[2][1024][12];
-#define MOE_STAMP(k, i) \
-  if (threadIdx.x == 0 && blockIdx.y == 0) g_moe_stamps[k][blockIdx.x][i] = __builtin_amdgcn_s_memrealtime();
-#else
-#define MOE_STAMP(k, i)
-#endif
 
 // ---- router || shared-gate GEMV (gemv_bf16.cl:103-200), fp16 weights --------------------
 // grid (N/16, M), 16 * ksplit lanes: lane l of slice q sums column n_tile*16 + l over k8 in
@@ -128,7 +121,6 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
   s_red[e] = l;
   if (e < 4u * 9u) s_cand[e] = 0ull;
   __syncthreads();
-  MOE_STAMP(0, 5);
   // Wave 0 alone: lane l holds v[u] = element l + 64 u and applies the cross-wave levels of
   // the trees in their order (st = E/2 .. 64: s[e] = op(s[e], s[e + st])), then the levels
   // st < 64 across its lanes. The max is exact whatever the order; the sum is the pairwise
@@ -157,8 +149,6 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
     }
   }
   __syncthreads();
-  MOE_STAMP(0, 6);
-  MOE_STAMP(0, 7);
   const uint32_t slots = top_k + 1;
   const uint64_t key = s_key[e];
   const float p = __builtin_bit_cast(float, (uint32_t)(key >> 32));
@@ -175,7 +165,6 @@ __device__ void route_compute(const float* lg, uint32_t* s_row, uint32_t E, uint
   const bool cand = live && r1 < slots;
   if (cand) s_cand[(e >> 6) * 9u + r1] = key;
   __syncthreads();
-  MOE_STAMP(0, 8);
   if (cand) {
     uint32_t rank = 0;
     for (uint32_t w = 0; w < nw; ++w)
@@ -334,7 +323,6 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__
   const uint32_t t = threadIdx.x, m = blockIdx.y;
   const uint32_t nhb = inter / 8, slot = blockIdx.x / nhb, hb = blockIdx.x % nhb, ib = hb / 2, ch = hb % 2;
   const uint32_t G = hidden / 64, slots = top_k + 1;
-  MOE_STAMP(0, 0);
   constexpr int XP = kMaxHidden / 8 / 256;  // x pieces per thread
   u4_t xv[XP];
   get_f16<XP>(xv, x + (size_t)m * hidden, hidden);
@@ -346,7 +334,6 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__
   } else {
     e = slot_expert(route + (size_t)m * kRouteWords, slot, E, top_k);
   }
-  MOE_STAMP(0, 1);
   {
     const size_t block = (size_t)(2 * inter / 16) * G * kTileU32;
     const uint32_t* base = gu + (size_t)e * block + (size_t)(2 * ib) * G * kTileU32;
@@ -371,12 +358,10 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__
   __syncthreads();
   // (tile, column, group) terms: thread t takes column t % 8 of groups (t / 8) % 16 + 16 k
   // of tile t / 128
-  MOE_STAMP(0, 2);
   const uint32_t c = t & 7u, gsub = (t >> 3) & 15u, tl = t >> 7;
   const uint32_t* tiles = s_w + (size_t)tl * G * kHalfU32;
   for (uint32_t g = gsub; g < G; g += 16u) s_t[tl][c][g] = half_term(tiles + (size_t)g * kHalfU32, c, s_x + g * kXs);
   __syncthreads();
-  MOE_STAMP(0, 3);
   if (t < 2u * 8u * kUpKs) {  // (tile, column, slice): the slice's groups in order
     const uint32_t tl2 = t / (8u * kUpKs), c2 = (t / kUpKs) % 8u, q = t % kUpKs;
     const uint32_t per = G / kUpKs;
@@ -398,7 +383,6 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__
     const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
     h[((size_t)m * slots + slot) * inter + ib * 16 + ch * 8 + t] = f2h(h2f(s_b) * h2f(u_b));
   }
-  MOE_STAMP(0, 4);
 }
 
 // ---- down + combine + residual (moe.cl:383-470; twin moe_ref.h:140-177) ---------------------
@@ -416,7 +400,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
   __shared__ float s_d[9][8];
   const uint32_t t = threadIdx.x, m = blockIdx.y, nb = blockIdx.x / 2, ch = blockIdx.x % 2;
   const uint32_t G = inter / 64, slots = top_k + 1;
-  MOE_STAMP(1, 0);
   const uint32_t* row = route + (size_t)m * kRouteWords;
   uint32_t ids[9];
 #pragma unroll
@@ -456,14 +439,12 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
     }
   }
   __syncthreads();
-  MOE_STAMP(1, 2);
   const uint32_t tasks = slots * 8u * G;
   for (uint32_t i = t; i < tasks; i += 256u) {
     const uint32_t slot = i / (8u * G), rem = i % (8u * G), g = rem / 8u, c = rem % 8u;
     s_t[slot][c][g] = half_term(s_w + ((size_t)slot * G + g) * kHalfU32, c, s_h + (slot * G + g) * kXs);
   }
   __syncthreads();
-  MOE_STAMP(1, 3);
   if (t < slots * 8u) {
     const uint32_t slot = t / 8u, c = t % 8u, per = G / kDnKs;
     float r[kDnKs];
@@ -487,7 +468,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
     const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
     *rp = f2h(h2f(r_old) + h2f(o_b));
   }
-  MOE_STAMP(1, 4);
 }
 
 int check_moe(uint32_t M, uint32_t E, uint32_t top_k, uint32_t hidden, uint32_t inter) {
@@ -522,13 +502,6 @@ extern "C" int mi_gemv_f16w(const uint16_t* w_tiled, const uint16_t* x, float* o
     gemv_f16w_kernel<1><<<dim3(N / 16, M), 16 * ksplit, 0, st>>>(w_tiled, x, out, M, K, N, ksplit);
   return mi_hip(static_cast<int>(hipGetLastError()), "gemv_f16w launch");
 }
-
-#ifdef MI_MOE_STAMPS
-extern "C" int mi_moe_stamps(uint64_t* out) {
-  return mi_hip((int)hipMemcpyFromSymbol(out, HIP_SYMBOL(g_moe_stamps), sizeof(uint64_t) * 2 * 1024 * 12),
-                "moe stamps");
-}
-#endif
 
 extern "C" int mi_moe_route(const float* logits, uint32_t* route, uint32_t M, uint32_t experts, uint32_t top_k,
                             uint32_t router_n, void* stream) {
