@@ -151,6 +151,7 @@ struct mi_engine {
   float* moe_logits = nullptr;   // [max_rows][router_n]
   uint32_t* moe_route = nullptr; // [max_rows][MI_MOE_ROUTE_WORDS]
   uint16_t* moe_h = nullptr;     // [max_rows][top_k + 1][moe_inter]
+  uint32_t* dn_words = nullptr;  // [max_rows][hidden / 2] moe_down_norm's hand-off words
   uint32_t router_n = 0;
   size_t gu_block = 0, dn_block = 0;  // u32 per expert block
   mi_attn_shape ash{};
@@ -173,10 +174,10 @@ struct mi_engine {
   ~mi_engine() {
     if (step) mi::step_plan_destroy(step);
     for (auto& g : graphs)
-      if (g) hipGraphExecDestroy(g);
-    if (draft_graph) hipGraphExecDestroy(draft_graph);
-    for (void* p : allocs) hipFree(p);
-    if (own_stream && stream) hipStreamDestroy(stream);
+      if (g) (void)hipGraphExecDestroy(g);
+    if (draft_graph) (void)hipGraphExecDestroy(draft_graph);
+    for (void* p : allocs) (void)hipFree(p);
+    if (own_stream && stream) (void)hipStreamDestroy(stream);
   }
 
   template <typename T>
@@ -194,7 +195,7 @@ struct mi_engine {
     if (!*p) return;
     for (auto it = allocs.begin(); it != allocs.end(); ++it)
       if (*it == *p) {
-        hipFree(*it);
+        (void)hipFree(*it);
         allocs.erase(it);
         break;
       }
@@ -327,6 +328,8 @@ struct mi_engine {
       MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
       MI_TRY(alloc(&moe_route, size_t(R) * MI_MOE_ROUTE_WORDS));
       MI_TRY(alloc(&moe_h, size_t(R) * (m.top_k + 1) * m.moe_inter));
+      MI_TRY(alloc(&dn_words, size_t(R) * (H / 2)));
+      MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(R) * (H / 2), stream));
     }
 
     // synthetic weights (BASELINE config 2's distributions)
@@ -464,8 +467,9 @@ struct mi_engine {
         MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
         MI_TRY(mi_moe_gate_up_routed(moe_logits, router_n, moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k,
                                      d.hidden, d.moe_inter, stream));
-        MI_TRY(mi_moe_down(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter, stream));
-        MI_TRY(mi_norm_rows(resid, next_w, x, rstd, M, d.hidden, d.rms_eps, stream));
+        // down + combine into the residual, and the next norm in the same launch
+        MI_TRY(mi_moe_down_norm(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter,
+                                next_w, x, rstd, d.rms_eps, dn_words, ctrl + MI_CTRL_DEBUG, stream));
         continue;
       }
       MI_TRY(launch_gate_up(L, M));
@@ -652,8 +656,8 @@ struct mi_engine {
     MI_TRY(mi_hip(static_cast<int>(hipEventSynchronize(b)), "event sync"));
     float t = 0.f;
     MI_TRY(mi_hip(static_cast<int>(hipEventElapsedTime(&t, a, b)), "event elapsed"));
-    hipEventDestroy(a);
-    hipEventDestroy(b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
     *ms = t / float(reps * per_round);
     return check_handoff();
   }
@@ -666,12 +670,12 @@ struct mi_engine {
     const int e = enqueue_step(M);
     const int e2 = static_cast<int>(hipStreamEndCapture(stream, &g));
     if (e != 0) {
-      if (g) hipGraphDestroy(g);
+      if (g) (void)hipGraphDestroy(g);
       return e;
     }
     MI_TRY(mi_hip(e2, "hipStreamEndCapture"));
     const int e3 = static_cast<int>(hipGraphInstantiate(&graphs[M], g, nullptr, nullptr, 0));
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     return mi_hip(e3, "hipGraphInstantiate");
   }
 
@@ -683,12 +687,12 @@ struct mi_engine {
     const int e = enqueue_draft();
     const int e2 = static_cast<int>(hipStreamEndCapture(stream, &g));
     if (e != 0) {
-      if (g) hipGraphDestroy(g);
+      if (g) (void)hipGraphDestroy(g);
       return e;
     }
     MI_TRY(mi_hip(e2, "hipStreamEndCapture"));
     const int e3 = static_cast<int>(hipGraphInstantiate(&draft_graph, g, nullptr, nullptr, 0));
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     return mi_hip(e3, "hipGraphInstantiate");
   }
 
@@ -945,7 +949,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
     return nullptr;
   }
   const mi_model_desc& m = *desc;
-  if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || m.head_dim != 128 && m.head_dim != 256 || m.kv_heads == 0 ||
+  if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || (m.head_dim != 128 && m.head_dim != 256) || m.kv_heads == 0 ||
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||

@@ -17,6 +17,7 @@
 // expert weights stream at HBM rate instead of one lane per column walking K.
 #include "mi_common.h"
 #include "mi_capi_internal.h"
+#include "gemv_core.h"
 
 namespace mi {
 namespace {
@@ -213,25 +214,6 @@ __device__ __forceinline__ uint32_t slot_expert(const uint32_t* row, uint32_t sl
   return id < E ? id : E;
 }
 
-// one k-group's dot for column c of a layout-1 tile (moe_ref.h:98-116's tile_dot body):
-// sum over words j of (sum over nibbles i of (q - 8) * x) in ascending order, then * scale
-__device__ __forceinline__ float group_term(const uint32_t* __restrict__ tile, uint32_t c,
-                                            const float* __restrict__ xs) {
-  uint32_t wd[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) wd[j] = tile[j * 16 + c];
-  const uint16_t sc = reinterpret_cast<const uint16_t*>(tile + 128)[c];
-  float g = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float a = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) a += (float)((int)((wd[j] >> (4 * i)) & 0xFu) - 8) * xs[j * 8 + i];
-    g += a;
-  }
-  return g * h2f(sc);
-}
-
 // The expert kernels work on half tiles: 8 of a layout-1 tile's 16 columns, so the grids
 // hold twice the work-groups. A work-group reads its route row with scalar loads, sends out
 // its activation loads (which do not depend on the route), then every weight load of its
@@ -277,8 +259,9 @@ __device__ __forceinline__ void get_f16(u4_t (&v)[PER], const uint16_t* src, uin
   }
 }
 
-// group_term on a staged half tile (column c < 8 of it); xs: the group's 64 activations
-// (16-byte aligned), read four at a time
+// One k-group's dot for column c < 8 of a staged half tile (moe_ref.h:98-116's tile_dot body):
+// sum over words j of (sum over nibbles i of (q - 8) * x) in ascending order, then * scale;
+// xs: the group's 64 activations (16-byte aligned), read four at a time
 __device__ __forceinline__ float half_term(const uint32_t* ht, uint32_t c, const float* __restrict__ xs) {
   uint32_t wd[8];
 #pragma unroll
@@ -388,16 +371,110 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(uint32_t* __restrict__
 // ---- down + combine + residual (moe.cl:383-470; twin moe_ref.h:140-177) ---------------------
 // grid (hidden/8, M): work-group (nb, ch) makes resid[m][16 nb + 8 ch .. + 7] from half ch of
 // every slot's down tile nb, combined in slot order. Dynamic LDS: slots * G staged half tiles.
+// The next RMSNorm in the same launch (DownNorm::x non-NULL): the grid has one more row of
+// work-groups, after every producer; work-group m of it is row m's norm. Each producer also
+// publishes its 8 new residual values as 4 hand-off words (f16 pairs, empty pattern between
+// launches); the norm work-group polls the row's hidden/2 words, empties them again and
+// runs mi_norm_rows' arithmetic on them (64-element chunk trees, chunks in ascending order).
+struct DownNorm {
+  uint32_t* words;      // [M][hidden / 2]
+  const float* w;       // the norm's fp32 weights [hidden]
+  uint16_t* x;          // [M][hidden]
+  float* rstd;          // [M] or NULL
+  float eps;
+  uint32_t* status;     // set to kStatusTimeout when a wait gives up (NULL: none)
+  uint32_t poll_limit;
+};
+constexpr uint32_t kDnPollLimit = 1u << 21;
+
+__device__ void down_norm_consumer(const DownNorm& dnm, uint32_t m, uint32_t hidden, uint32_t* s_words,
+                                   float* s_chunk) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, nch = hidden / 64u, nw = hidden / 2u;
+  // the norm weights of this thread's elements first: chunks wave + 4 u, element lane
+  constexpr uint32_t kCh = kMaxHidden / 64 / 4;  // chunks per wave
+  float wv[kCh];
+#pragma unroll
+  for (uint32_t u = 0; u < kCh; ++u) {
+    const uint32_t c = wave + 4u * u;
+    wv[u] = c < nch ? dnm.w[c * 64u + lane] : 0.f;
+  }
+  uint32_t* words = dnm.words + (size_t)m * nw;
+  constexpr uint32_t kPer = kMaxHidden / 2 / 256;
+  uint32_t v[kPer];
+  uint32_t pending = 0;
+#pragma unroll
+  for (uint32_t u = 0; u < kPer; ++u) {
+    const uint32_t i = t + 256u * u;
+    if (i < nw) {
+      v[u] = ld_agent(words + i);
+      if (v[u] == kEmpty) pending |= 1u << u;
+    }
+  }
+  for (uint32_t n = 0; pending && n < dnm.poll_limit; ++n) {
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u)
+      if (pending & (1u << u)) {
+        v[u] = ld_agent(words + t + 256u * u);
+        if (v[u] != kEmpty) pending &= ~(1u << u);
+      }
+  }
+  if (pending && dnm.status) st_agent(dnm.status, kStatusTimeout);
+#pragma unroll
+  for (uint32_t u = 0; u < kPer; ++u) {
+    const uint32_t i = t + 256u * u;
+    if (i < nw) {
+      s_words[i] = v[u];
+      st_agent(words + i, kEmpty);
+    }
+  }
+  __syncthreads();
+  const uint16_t* sres = reinterpret_cast<const uint16_t*>(s_words);
+  float rv[kCh];
+#pragma unroll
+  for (uint32_t u = 0; u < kCh; ++u) {
+    const uint32_t c = wave + 4u * u;
+    rv[u] = 0.f;
+    if (c < nch) {
+      rv[u] = h2f(sres[c * 64u + lane]);
+      float a = __builtin_fmaf(rv[u], rv[u], 0.f);
+#pragma unroll
+      for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
+      if (lane == 0) s_chunk[c] = a;
+    }
+  }
+  __syncthreads();
+  __shared__ float s_rstd;
+  if (t == 0) {
+    float tot = 0.f;
+    for (uint32_t c = 0; c < nch; ++c) tot += s_chunk[c];
+    s_rstd = 1.0f / sqrtf(tot / (float)hidden + dnm.eps);
+  }
+  __syncthreads();
+  const float r = s_rstd;
+  if (t == 0 && dnm.rstd) dnm.rstd[m] = r;
+#pragma unroll
+  for (uint32_t u = 0; u < kCh; ++u) {
+    const uint32_t c = wave + 4u * u;
+    if (c < nch) dnm.x[(size_t)m * hidden + c * 64u + lane] = f2h(rv[u] * r * wv[u]);
+  }
+}
+
 __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restrict__ route,
                                                        const uint16_t* __restrict__ h,
                                                        const uint32_t* __restrict__ dn,
                                                        uint16_t* __restrict__ resid, uint32_t E,
                                                        uint32_t top_k, uint32_t hidden,
-                                                       uint32_t inter) {
+                                                       uint32_t inter, uint32_t M, DownNorm dnm) {
   extern __shared__ uint32_t s_w[];  // [slots][G][kHalfU32]
   __shared__ __align__(16) float s_h[kMaxSlotsInter / 64 * kXs];
   __shared__ float s_t[9][8][16];  // [slot][column][group], inter <= 1024
   __shared__ float s_d[9][8];
+  if (dnm.x && blockIdx.y == M) {  // the norm row (uniform)
+    if (blockIdx.x < M)
+      down_norm_consumer(dnm, blockIdx.x, hidden, reinterpret_cast<uint32_t*>(s_h), &s_t[0][0][0]);
+    return;
+  }
   const uint32_t t = threadIdx.x, m = blockIdx.y, nb = blockIdx.x / 2, ch = blockIdx.x % 2;
   const uint32_t G = inter / 64, slots = top_k + 1;
   const uint32_t* row = route + (size_t)m * kRouteWords;
@@ -466,7 +543,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
     const uint16_t r_b = f2h(sum);
     const uint16_t sh_b = f2h(h2f(f2h(s_d[top_k][t])) * sg);
     const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
-    *rp = f2h(h2f(r_old) + h2f(o_b));
+    const uint16_t nv = f2h(h2f(r_old) + h2f(o_b));
+    *rp = nv;
+    if (dnm.x) {  // the pair (t, t + 1) as one hand-off word for the norm work-group
+      const uint16_t hi = (uint16_t)__shfl_down((int)nv, 1, 64);
+      if ((t & 1u) == 0)
+        st_agent(dnm.words + (size_t)m * (hidden / 2) + (nb * 16u + ch * 8u + t) / 2u, publishable_pair(nv, hi));
+    }
   }
 }
 
@@ -549,8 +632,25 @@ extern "C" int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint3
   if (reinterpret_cast<uintptr_t>(dn_blocks) % 16 || reinterpret_cast<uintptr_t>(h) % 16)
     return mi_fail(MI_ERR_ARG, "moe_down: dn_blocks and h need 16-byte alignment");
   const size_t lds = size_t(top_k + 1) * (inter / 64) * kHalfU32 * 4;
-  moe_down_kernel<<<dim3(hidden / 8, M), 256, lds, static_cast<hipStream_t>(stream)>>>(route, h, dn_blocks, resid,
-                                                                                      experts, top_k, hidden, inter);
+  moe_down_kernel<<<dim3(hidden / 8, M), 256, lds, static_cast<hipStream_t>(stream)>>>(
+      route, h, dn_blocks, resid, experts, top_k, hidden, inter, M, DownNorm{});
   return mi_hip(static_cast<int>(hipGetLastError()), "moe_down launch");
+}
+
+extern "C" int mi_moe_down_norm(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks, uint16_t* resid,
+                                uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
+                                const float* norm_w, uint16_t* x_out, float* rstd, float eps, uint32_t* handoff,
+                                uint32_t* status, void* stream) {
+  if (!route || !h || !dn_blocks || !resid || !norm_w || !x_out || !handoff)
+    return mi_fail(MI_ERR_ARG, "moe_down_norm: null pointer");
+  if (int e = check_moe(M, experts, top_k, hidden, inter)) return e;
+  if (M > 8) return mi_fail(MI_ERR_SHAPE, "moe_down_norm: M must be <= 8");
+  if (reinterpret_cast<uintptr_t>(dn_blocks) % 16 || reinterpret_cast<uintptr_t>(h) % 16)
+    return mi_fail(MI_ERR_ARG, "moe_down_norm: dn_blocks and h need 16-byte alignment");
+  const size_t lds = size_t(top_k + 1) * (inter / 64) * kHalfU32 * 4;
+  const DownNorm dnm{handoff, norm_w, x_out, rstd, eps, status, kDnPollLimit};
+  moe_down_kernel<<<dim3(hidden / 8, M + 1), 256, lds, static_cast<hipStream_t>(stream)>>>(
+      route, h, dn_blocks, resid, experts, top_k, hidden, inter, M, dnm);
+  return mi_hip(static_cast<int>(hipGetLastError()), "moe_down_norm launch");
 }
 

@@ -792,9 +792,9 @@ struct StepPlan {
   LaunchFn launch = nullptr;
 
   ~StepPlan() {
-    if (d_stages) hipFree(d_stages);
-    if (arena) hipFree(arena);
-    if (trace) hipFree(trace);
+    if (d_stages) (void)hipFree(d_stages);
+    if (arena) (void)hipFree(arena);
+    if (trace) (void)hipFree(trace);
   }
 };
 

@@ -201,6 +201,45 @@ def test_routed_gate_up_is_route_then_gate_up(E, hidden, inter, M):
     assert np.array_equal(host(h1, np.uint16), host(h2, np.uint16))
 
 
+@pytest.mark.parametrize("E,hidden,inter,M", [(256, 2048, 512, 1), (256, 2048, 512, 3), (16, 4096, 128, 8),
+                                              (16, 512, 128, 2)])
+def test_down_norm_is_down_then_norm_rows(E, hidden, inter, M):
+    """mi_moe_down_norm writes the residual of mi_moe_down and the x / rstd of mi_norm_rows on
+    it, bit for bit, and leaves its hand-off words empty (two launches in a row, the second
+    with fewer rows)."""
+    mo = Moe(7, E=E, hidden=hidden, inter=inter, router_n=E + 16)
+    print(f"down_norm E={E} hidden={hidden} inter={inter} M={M}", flush=True)
+    rng = np.random.default_rng(70 + M)
+    handoff = empty((M, hidden // 2), np.uint32)
+    mi.call("mi_gemv_handoff_init", ptr(handoff), M * hidden // 2, stream())
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    dw = dev(w)
+    for rows in (M, max(1, M - 1)):
+        lg = rng.standard_normal((rows, mo.router_n)).astype(np.float32)
+        x = O.f32_to_f16_bits(rng.standard_normal((rows, hidden)).astype(np.float32))
+        resid = O.f32_to_f16_bits(rng.standard_normal((rows, hidden)).astype(np.float32))
+        dl, dx = dev(lg), dev(x)
+        route = empty((rows, ROUTE_WORDS), np.uint32)
+        h = empty((rows, mo.top_k + 1, inter), np.uint16)
+        mi.call("mi_moe_route", ptr(dl), ptr(route), rows, E, mo.top_k, mo.router_n, stream())
+        mi.call("mi_moe_gate_up", ptr(route), ptr(dx), ptr(mo.d_gu), ptr(h), rows, E, mo.top_k, hidden, inter,
+                stream())
+        r1, r2 = dev(resid), dev(resid)
+        x1, x2 = empty((rows, hidden), np.uint16), empty((rows, hidden), np.uint16)
+        s1, s2 = empty((rows,), np.float32), empty((rows,), np.float32)
+        status = dev(np.zeros(1, np.uint32))
+        mi.call("mi_moe_down", ptr(route), ptr(h), ptr(mo.d_dn), ptr(r1), rows, E, mo.top_k, hidden, inter, stream())
+        mi.call("mi_norm_rows", ptr(r1), ptr(dw), ptr(x1), ptr(s1), rows, hidden, np.float32(1e-6), stream())
+        mi.call("mi_moe_down_norm", ptr(route), ptr(h), ptr(mo.d_dn), ptr(r2), rows, E, mo.top_k, hidden, inter,
+                ptr(dw), ptr(x2), ptr(s2), np.float32(1e-6), ptr(handoff), ptr(status), stream())
+        sync()
+        assert host(status, np.uint32)[0] == 0
+        assert np.all(host(handoff, np.uint32) == 0xFFFFFFFF), "hand-off words not left empty"
+        assert np.array_equal(host(r1, np.uint16), host(r2, np.uint16))
+        assert np.array_equal(host(x1, np.uint16), host(x2, np.uint16))
+        assert np.array_equal(host(s1, np.uint32), host(s2, np.uint32))
+
+
 def test_malformed_route_row_reads_the_shared_block():
     mo = Moe(2, E=16, hidden=512, inter=128, router_n=32)
     M = 1
