@@ -983,6 +983,8 @@ void mi_engine_destroy(mi_engine* e) { delete e; }
 
 void* mi_engine_stream(mi_engine* e) { return e ? e->stream : nullptr; }
 
+bool mi_engine_has_mtp(const mi_engine* e) { return e && e->d.mtp; }
+
 int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes) {
   if (!e || !ptr) return mi_fail(MI_ERR_ARG, "engine_tensor: null");
   const mi_model_desc& m = e->d;

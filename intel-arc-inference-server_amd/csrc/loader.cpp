@@ -360,6 +360,7 @@ bool check_quant(const Json& c, std::string& err, bool& desc_act_declared) {
 
 struct Report {
   size_t linears = 0, qzeros = 0, g_idx = 0, subnormal_scales = 0, quantised_head = 0;
+  size_t mtp_tensors = 0, mtp_quantised = 0;  // the MTP head's tensors; its linears quantised at load
 };
 
 // one int4 linear: qweight I32 [K/8][N], scales F16 [K/64][N]; the data checks of
@@ -784,8 +785,88 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
     }
     if (int rc = flush()) return rc;
   }
+  // The MTP head, for an engine created with one (desc.mtp; the reference loads it only when
+  // asked, loader.cc:521-670): the 15 tensors of a dense head under `mtp.`. A linear shipped
+  // in 16 bits (the published checkpoints ship the head in bf16) is quantised here to int4 g64
+  // by rtn.h's round-to-nearest rule - the reference does that for its MoE head's experts;
+  // the head only drafts, so its quantisation moves acceptance, never output; a packed int4
+  // linear is taken as shipped. Layouts as the main layers': q||k||v by columns, gate/up
+  // interleaved in 16-column blocks; fc reads cat(pre_fc_norm_embedding(e),
+  // pre_fc_norm_hidden(h)), K = 2 hidden.
+  if (mi_engine_has_mtp(e)) {
+    const uint32_t HL = want.layers;  // the per-layer kinds at layer = layers are the head's
+    auto mtp_linear = [&](const std::string& base, uint32_t K, uint32_t N, std::vector<uint32_t>& q,
+                          std::vector<uint16_t>& sc) -> bool {
+      ++rep.mtp_tensors;
+      if (ck.find(base + ".qweight")) {
+        Linear4 l;
+        if (!get_linear(ck, base, K, N, l, rep)) return false;
+        q.assign(l.q, l.q + size_t(K / 8) * N);
+        sc.assign(l.s, l.s + size_t(K / 64) * N);
+        return true;
+      }
+      if (!ck.find(base + ".weight"))
+        return ck.fail("engine_load: the engine has an MTP head and the checkpoint has no " + base + " (.weight or .qweight)");
+      if (!get_float(ck, base + ".weight", size_t(N) * K, f32)) return false;
+      quantise_rtn(f32, N, K, q, sc);
+      ++rep.mtp_quantised;
+      return true;
+    };
+    auto mtp_norm = [&](const std::string& name, uint32_t n, uint32_t kind, uint32_t layer) -> int {
+      ++rep.mtp_tensors;
+      if (!ck.find(name)) {
+        ck.fail("engine_load: the engine has an MTP head and the checkpoint has no " + name);
+        return fail_ck(ck);
+      }
+      if (!get_float(ck, name, n, f32)) return fail_ck(ck);
+      return upload(kind, layer, f32.data(), f32.size() * 4, name.c_str());
+    };
+    std::vector<uint32_t> q1, q2, q3;
+    std::vector<uint16_t> s1, s2, s3;
+    if (!mtp_linear("mtp.fc", 2 * H, H, q1, s1)) return fail_ck(ck);
+    if (int rc = upload(MI_T_MTP_FC_Q, 0, q1.data(), q1.size() * 4, "mtp.fc qweight")) return rc;
+    if (int rc = upload(MI_T_MTP_FC_S, 0, s1.data(), s1.size() * 2, "mtp.fc scales")) return rc;
+    if (int rc = mtp_norm("mtp.pre_fc_norm_embedding.weight", H, MI_T_MTP_PRE_E, 0)) return rc;
+    if (int rc = mtp_norm("mtp.pre_fc_norm_hidden.weight", H, MI_T_MTP_PRE_H, 0)) return rc;
+    if (int rc = mtp_norm("mtp.norm.weight", H, MI_T_MTP_FINAL, 0)) return rc;
+    if (int rc = flush()) return rc;
+    const std::string lp = "mtp.layers.0.";
+    {
+      std::vector<uint32_t> qq, kq, vq;
+      std::vector<uint16_t> qs, ks, vs;
+      if (!mtp_linear(lp + "self_attn.q_proj", H, QH * HD, qq, qs) ||
+          !mtp_linear(lp + "self_attn.k_proj", H, KVH * HD, kq, ks) ||
+          !mtp_linear(lp + "self_attn.v_proj", H, KVH * HD, vq, vs))
+        return fail_ck(ck);
+      concat_cols<uint32_t>({{qq.data(), QH * HD}, {kq.data(), KVH * HD}, {vq.data(), KVH * HD}}, H / 8, qcat);
+      concat_cols<uint16_t>({{qs.data(), QH * HD}, {ks.data(), KVH * HD}, {vs.data(), KVH * HD}}, H / 64, scat);
+      if (int rc = upload(MI_T_QKV_Q, HL, qcat.data(), qcat.size() * 4, "mtp q||k||v qweight")) return rc;
+      if (int rc = upload(MI_T_QKV_S, HL, scat.data(), scat.size() * 2, "mtp q||k||v scales")) return rc;
+    }
+    if (!mtp_linear(lp + "self_attn.o_proj", QH * HD, H, q1, s1)) return fail_ck(ck);
+    if (int rc = upload(MI_T_O_Q, HL, q1.data(), q1.size() * 4, "mtp o_proj qweight")) return rc;
+    if (int rc = upload(MI_T_O_S, HL, s1.data(), s1.size() * 2, "mtp o_proj scales")) return rc;
+    if (int rc = mtp_norm(lp + "input_layernorm.weight", H, MI_T_IN_NORM, HL)) return rc;
+    if (int rc = mtp_norm(lp + "post_attention_layernorm.weight", H, MI_T_POST_NORM, HL)) return rc;
+    if (want.qk_norm) {
+      if (int rc = mtp_norm(lp + "self_attn.q_norm.weight", HD, MI_T_Q_NORM, HL)) return rc;
+      if (int rc = mtp_norm(lp + "self_attn.k_norm.weight", HD, MI_T_K_NORM, HL)) return rc;
+    }
+    if (int rc = flush()) return rc;
+    if (!mtp_linear(lp + "mlp.gate_proj", H, I, q1, s1) || !mtp_linear(lp + "mlp.up_proj", H, I, q2, s2) ||
+        !mtp_linear(lp + "mlp.down_proj", I, H, q3, s3))
+      return fail_ck(ck);
+    interleave16(q1.data(), q2.data(), H / 8, I, qcat);
+    interleave16(s1.data(), s2.data(), H / 64, I, scat);
+    if (int rc = upload(MI_T_GU_Q, HL, qcat.data(), qcat.size() * 4, "mtp gate||up qweight")) return rc;
+    if (int rc = upload(MI_T_GU_S, HL, scat.data(), scat.size() * 2, "mtp gate||up scales")) return rc;
+    if (int rc = upload(MI_T_DOWN_Q, HL, q3.data(), q3.size() * 4, "mtp down_proj qweight")) return rc;
+    if (int rc = upload(MI_T_DOWN_S, HL, s3.data(), s3.size() * 2, "mtp down_proj scales")) return rc;
+    if (int rc = flush()) return rc;
+  }
   // every tensor of the language model must have been bound (qzeros / g_idx are checked and
-  // dropped; other namespaces - vision towers, MTP heads - are not this engine's)
+  // dropped; other namespaces - vision towers, an MTP head the engine does not hold - are not
+  // this engine's)
   size_t unused = 0;
   std::string first;
   for (const auto& kv : ck.t) {
@@ -801,10 +882,11 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   if (report && report_len) {
     std::snprintf(report, report_len,
                   "loaded %zu int4 linears; dropped %zu qzeros + %zu g_idx (invariants asserted); %zu subnormal "
-                  "scales kept; lm_head %s",
+                  "scales kept; lm_head %s; MTP head: %zu tensors, %zu linears quantised to int4 g64 at load",
                   rep.linears, rep.qzeros, rep.g_idx, rep.subnormal_scales,
                   rep.quantised_head ? (head_i8 ? "quantised to int8 rows at load" : "quantised to int4 g64 at load")
-                                     : "int4 as shipped");
+                                     : "int4 as shipped",
+                  rep.mtp_tensors, rep.mtp_quantised);
   }
   return 0;
 }

@@ -8,3 +8,5 @@
 int mi_fail(int code, const char* msg);
 // Returns `e` (a hipError_t value); records `where` and the HIP error string when non-zero.
 int mi_hip(int e, const char* where);
+// Whether the engine was created with an MTP head (its descriptor's mtp); for the loader.
+extern "C" bool mi_engine_has_mtp(const mi_engine* e);

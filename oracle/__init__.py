@@ -78,6 +78,7 @@ def lib():
             "orc_prefill_chunk": (u32, [i32, vp, vp, u32, u32, vp, vp, vp]),
             "orc_mtp_head_step": (u32, [i32, vp, vp, u32, vp, u32, vp, vp, i32, vp, vp]),
             "orc_quantise_row_int8": (f32, [vp, u32, vp]),
+            "orc_rtn_int4_g64": (None, [vp, u32, u32, vp, vp]),
             "orc_gemv_i8w": (None, [i32, vp, vp, vp, u32, u32, u32, vp]),
             "orc_moe_prefill": (None, [i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, u32]),
             "orc_gemv_f16w": (None, [i32, vp, vp, u32, u32, u32, u32, vp]),
@@ -132,6 +133,7 @@ def ref():
             "ref_pf_moe_block": (None, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
             "ref_repack_bf16_tiled": (None, [vp, u32, u32, vp]),
             "ref_quantise_int8_tiled": (None, [vp, u32, u32, vp, vp]),
+            "ref_rtn_int4_g64": (None, [vp, u32, u32, vp, vp]),
             "ref_int8_tiled_index": (C.c_size_t, [u32, u32, u32]),
         }
         for name, (res, args) in sig.items():

@@ -984,6 +984,32 @@ float orc_quantise_row_int8(const float* w, uint32_t K, int8_t* q) {
   }
   return s;
 }
+// ---- round-to-nearest int4 g64 of a bf16 linear (src/loader/rtn.h:35-60) ------------------------
+// per output column n and group of 64 k: amax = max |w| (bf16 values in fp32), s16 =
+// f16_rne(2 amax / 15), q = clamp(rint(w / f32(s16)) + 8, 0, 15); a zero group: s16 = 0, q = 8.
+// GPTQ packing: qweight [K/8][N] (k = 8r + j in nibble j of word (r, n)), scales [K/64][N].
+void orc_rtn_int4_g64(const uint16_t* w_bf16, uint32_t K, uint32_t N, uint32_t* qweight, uint16_t* scales) {
+  for (uint32_t n = 0; n < N; ++n) {
+    const uint16_t* row = w_bf16 + size_t(n) * K;
+    for (uint32_t g = 0; g < K / 64; ++g) {
+      float amax = 0.f;
+      for (uint32_t k = g * 64; k < g * 64 + 64; ++k) amax = std::fmax(amax, std::fabs(orc_bf16_to_f32(row[k])));
+      const uint16_t s16 = orc_f32_to_f16(2.0f * amax / 15.0f);
+      scales[size_t(g) * N + n] = s16;
+      const float s = orc_f16_to_f32(s16);
+      for (uint32_t r = g * 8; r < g * 8 + 8; ++r) {
+        uint32_t word = 0;
+        for (uint32_t j = 0; j < 8; ++j) {
+          float q = s > 0.f ? std::rint(orc_bf16_to_f32(row[r * 8 + j]) / s) + 8.0f : 8.0f;
+          q = std::fmin(std::fmax(q, 0.0f), 15.0f);
+          word |= uint32_t(q) << (4 * j);
+        }
+        qweight[size_t(r) * N + n] = word;
+      }
+    }
+  }
+}
+
 // gemv_i8w.cl:67-105: one fp32 chain per column over k ascending, then the column's scale
 void orc_gemv_i8w(int act, const int8_t* q, const float* s, const uint16_t* x, uint32_t M, uint32_t K, uint32_t N,
                   float* out) {

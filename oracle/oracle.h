@@ -174,6 +174,9 @@ void orc_f16w_tile(const uint16_t* w_rowmajor, uint32_t K, uint32_t N, uint16_t*
 /* One row of K fp32 values: s = max|w| / 127 (fp32), q = rne(w / s) clamped to [-127, 127];
  * a zero row gives s = 0 and q = 0. Returns s. */
 float orc_quantise_row_int8(const float* w, uint32_t K, int8_t* q);
+/* Round-to-nearest int4 g64 of a bf16 row-major [N][K] linear into the GPTQ packing (qweight
+ * [K/8][N], f16 scales [K/64][N], zero point 8): src/loader/rtn.h:35-60. */
+void orc_rtn_int4_g64(const uint16_t* w_bf16, uint32_t K, uint32_t N, uint32_t* qweight, uint16_t* scales);
 /* out[m][n] = (sum over k ascending of q[n][k] * x[m][k], fp32) * s[n]; q int8 [N][K]
  * row-major, x act [M][K] */
 void orc_gemv_i8w(int act, const int8_t* q, const float* s, const uint16_t* x, uint32_t M, uint32_t K,

@@ -20,6 +20,7 @@
 #include "kernels/pf_moe_ref.h"
 #include "kernels/prep_ref.h"
 #include "loader/lm_head_int8.h"
+#include "loader/rtn.h"
 
 extern "C" {
 
@@ -230,5 +231,10 @@ void ref_quantise_int8_tiled(const uint16_t* w, uint32_t K, uint32_t N, int8_t* 
   loader::quantise_int8_tiled(w, K, N, q_tiled, scales, 1);
 }
 size_t ref_int8_tiled_index(uint32_t K, uint32_t k, uint32_t n) { return loader::int8_tiled_index(K, k, n); }
+
+// src/loader/rtn.h: the round-to-nearest int4 g64 quantiser of a bf16 linear (header only)
+void ref_rtn_int4_g64(const uint16_t* w, uint32_t K, uint32_t N, uint32_t* qweight, uint16_t* scales) {
+  loader::rtn_int4_g64(w, K, N, qweight, scales);
+}
 
 }  // extern "C"

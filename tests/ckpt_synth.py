@@ -44,7 +44,7 @@ class Synth:
 
     def __init__(self, path, seed=0, layers=2, H=512, QH=8, KVH=2, HD=128, I=1024, V=4000, qk_norm=True,
                  experts=0, top_k=4, moe_inter=128, head="int4", norm_dtype="BF16", tie=False,
-                 qzeros=True, g_idx=True, prefix="model."):
+                 qzeros=True, g_idx=True, prefix="model.", mtp=False):
         rng = np.random.default_rng(seed)
         os.makedirs(path, exist_ok=True)
         self.path = path
@@ -110,6 +110,28 @@ class Synth:
                 L["up"] = lin(lp + "mlp.up_proj", H, I)
                 L["down"] = lin(lp + "mlp.down_proj", I, H)
             self.layers.append(L)
+        if mtp:  # a dense MTP head in bf16 (the published checkpoints' form): 15 mtp.* tensors
+            def wbf(name, N, K, sd=0.05):
+                b = bf16(sd * rng.standard_normal((N, K)))
+                self.t[name] = ("BF16", b)
+                return b
+            self.mtp = {"fc": wbf("mtp.fc.weight", H, 2 * H),
+                        "pre_e": vec("mtp.pre_fc_norm_embedding.weight", H),
+                        "pre_h": vec("mtp.pre_fc_norm_hidden.weight", H),
+                        "final": vec("mtp.norm.weight", H)}
+            mp = "mtp.layers.0."
+            self.mtp.update({"q": wbf(mp + "self_attn.q_proj.weight", QH * HD, H),
+                             "k": wbf(mp + "self_attn.k_proj.weight", KVH * HD, H),
+                             "v": wbf(mp + "self_attn.v_proj.weight", KVH * HD, H),
+                             "o": wbf(mp + "self_attn.o_proj.weight", H, QH * HD),
+                             "in_norm": vec(mp + "input_layernorm.weight", H),
+                             "post_norm": vec(mp + "post_attention_layernorm.weight", H),
+                             "gate": wbf(mp + "mlp.gate_proj.weight", I, H),
+                             "up": wbf(mp + "mlp.up_proj.weight", I, H),
+                             "down": wbf(mp + "mlp.down_proj.weight", H, I)})
+            if qk_norm:
+                self.mtp["q_norm"] = vec(mp + "self_attn.q_norm.weight", HD)
+                self.mtp["k_norm"] = vec(mp + "self_attn.k_norm.weight", HD)
         self.head = head
         if head == "int4":
             self.lm = lin("lm_head", H, V)

@@ -182,3 +182,72 @@ def test_mismatched_engine_is_refused(tmp_path):
         eng.load(path)
     assert "does not match config.json" in str(e.value)
     eng.close()
+
+
+def test_mtp_head_loaded_and_drafts(tmp_path):
+    """An engine built with the MTP head loads the checkpoint's bf16 mtp.* tensors: every linear
+    quantised at load bitwise as the oracle's restatement of rtn.h (itself pinned against the
+    reference's rtn_int4_g64), in the main layers' layouts; the norms as shipped. The loaded
+    head's three draft lists follow the oracle's head on the same weights."""
+    from test_mtp_gpu import OracleHead, head_kv
+    syn = Synth(str(tmp_path / "mtp"), layers=2, V=2048, mtp=True)
+    path = syn.write(split=2)
+    desc = mi.checkpoint_desc(path, max_len=512, max_rows=4)
+    desc.mtp = 1
+    eng = mi.Engine(desc, seed=5)
+    rep = eng.load(path)
+    print(f"engine_load {path} (MTP head): {rep}", flush=True)
+    assert "MTP head: 15 tensors, 8 linears quantised" in rep
+    d = eng.desc
+    H, I, QH, KVH, HD, li = d.hidden, d.inter, d.q_heads, d.kv_heads, d.head_dim, d.layers
+
+    def rtn(b, K, N):
+        q = np.zeros((K // 8, N), np.uint32)
+        s = np.zeros((K // 64, N), np.uint16)
+        O.lib().orc_rtn_int4_g64(O._p(np.ascontiguousarray(b)), K, N, O._p(q), O._p(s))
+        return q, s
+
+    m = syn.mtp
+    fq, fs = rtn(m["fc"], 2 * H, H)
+    assert np.array_equal(eng.to_host(mi.T_MTP_FC_Q, 0, np.uint32), fq.ravel())
+    assert np.array_equal(eng.to_host(mi.T_MTP_FC_S, 0, np.uint16), fs.ravel())
+    q, k, v = rtn(m["q"], H, QH * HD), rtn(m["k"], H, KVH * HD), rtn(m["v"], H, KVH * HD)
+    assert np.array_equal(eng.to_host(mi.T_QKV_Q, li, np.uint32), np.concatenate([q[0], k[0], v[0]], 1).ravel())
+    assert np.array_equal(eng.to_host(mi.T_QKV_S, li, np.uint16), np.concatenate([q[1], k[1], v[1]], 1).ravel())
+    o = rtn(m["o"], QH * HD, H)
+    assert np.array_equal(eng.to_host(mi.T_O_Q, li, np.uint32), o[0].ravel())
+    g, u, dn = rtn(m["gate"], H, I), rtn(m["up"], H, I), rtn(m["down"], I, H)
+    assert np.array_equal(eng.to_host(mi.T_GU_Q, li, np.uint32), expect_interleave(g[0], u[0]).ravel())
+    assert np.array_equal(eng.to_host(mi.T_GU_S, li, np.uint16), expect_interleave(g[1], u[1]).ravel())
+    assert np.array_equal(eng.to_host(mi.T_DOWN_Q, li, np.uint32), dn[0].ravel())
+    assert np.array_equal(eng.to_host(mi.T_DOWN_S, li, np.uint16), dn[1].ravel())
+    for kind, layer, key in ((mi.T_MTP_PRE_E, 0, "pre_e"), (mi.T_MTP_PRE_H, 0, "pre_h"), (mi.T_MTP_FINAL, 0, "final"),
+                             (mi.T_IN_NORM, li, "in_norm"), (mi.T_POST_NORM, li, "post_norm"),
+                             (mi.T_Q_NORM, li, "q_norm"), (mi.T_K_NORM, li, "k_norm")):
+        assert np.array_equal(eng.to_host(kind, layer, np.float32), m[key].astype(np.float32)), key
+    # the loaded head drafts as the oracle's head on the same weights
+    orc = OracleModel(eng)
+    oh = OracleHead(eng, orc)
+    eng.capture(1)
+    eng.reset(100, 7)
+    eng.generate(3)
+    c = eng.ctrl()
+    pos, cur = int(c[mi.CTRL_POS]), int(c[mi.CTRL_CUR])
+    hh0 = eng.to_host(mi.T_MTP_HH, 0, np.uint16)[:H].copy()
+    kk, vv = head_kv(eng)
+    drafts = eng.draft(3)
+    tok, h = cur, hh0
+    for i in range(3):
+        am, logits, hout = oh.run(tok, h, pos - 1 + i, kk, vv)
+        assert argmax_ok(int(drafts[i]), logits), (i, drafts[i], am)
+        tok, h = int(drafts[i]), hout
+    eng.close()
+    # an engine with the head refuses a checkpoint without one
+    plain = Synth(str(tmp_path / "nomtp"), layers=1, V=2048)
+    ppath = plain.write(split=1)
+    d2 = mi.checkpoint_desc(ppath, max_len=512, max_rows=4)
+    d2.mtp = 1
+    e2 = mi.Engine(d2, seed=5)
+    with pytest.raises(mi.MiError, match="no mtp.fc"):
+        e2.load(ppath)
+    e2.close()

@@ -578,3 +578,30 @@ def test_int8_gemv_vs_fp64():
     assert np.all(np.abs(out - want) <= bound)
     # the scales applied one column off miss it
     assert not np.all(np.abs(out - prod * np.roll(s, 1).astype(np.float64)) <= bound)
+
+
+def test_rtn_int4_known_answers():
+    """orc_rtn_int4_g64 (src/loader/rtn.h) on hand-made groups: amax 7.5 gives the scale 1.0
+    exactly, so w / s = w and the ties go to the even integer (0.5 -> 0, 1.5 -> 2, 2.5 -> 2,
+    -0.5 -> 0, -1.5 -> -2); +-7.5 clamp to nibbles 15 and 0; amax 1.0 gives the scale
+    f16(2/15) = 0x3044; an all-zero group has scale 0 and every nibble 8."""
+    K, N = 128, 1
+    w = np.zeros(K, np.float32)
+    vals = [0.5, 1.5, 2.5, -0.5, -1.5, 7.5, -7.5, 3.0]
+    want_q = [8, 10, 10, 8, 6, 15, 0, 11]
+    w[:8] = vals
+    w[64] = 1.0  # group 1: amax 1.0
+    wb = O.f32_to_bf16_bits(w).reshape(N, K)
+    q = np.zeros((K // 8, N), np.uint32)
+    s = np.zeros((K // 64, N), np.uint16)
+    O.lib().orc_rtn_int4_g64(O._p(wb), K, N, O._p(q), O._p(s))
+    assert s[0, 0] == 0x3C00 and s[1, 0] == 0x3044
+    nib = [(int(q[0, 0]) >> (4 * j)) & 0xF for j in range(8)]
+    assert nib == want_q
+    assert np.all(q[1:8, 0] == 0x88888888)  # the rest of group 0 is zero: nibble 8
+    # group 1: 1.0 / f32(0x3044) = 7.5018... -> 8 + 8 = 16 -> clamped to 15; zeros -> 8
+    assert (int(q[8, 0]) & 0xF) == 15 and (int(q[8, 0]) >> 4) == 0x8888888
+    zero = np.zeros((1, 64), np.uint16)
+    qz = np.zeros((8, 1), np.uint32); sz = np.ones((1, 1), np.uint16)
+    O.lib().orc_rtn_int4_g64(O._p(zero), 64, 1, O._p(qz), O._p(sz))
+    assert sz[0, 0] == 0 and np.all(qz == 0x88888888)

@@ -417,3 +417,30 @@ def test_int8_head_quantiser_bitwise_lm_head_int8(N, K, seed):
         idx = np.array([R.ref_int8_tiled_index(K, k, n) for k in range(K)])
         assert np.array_equal(qt[idx], q), n
     assert st[5] == 0 and not np.any(qt[[R.ref_int8_tiled_index(K, k, 5) for k in range(K)]])
+
+
+def _rtn_rows(N, K, seed):
+    """bf16 [N][K] with the quantiser's corner cases: an all-zero group, a group whose largest
+    magnitude makes w / s land on .5 ties, subnormal-scale groups, negative extremes"""
+    rng = np.random.default_rng(seed)
+    w = O.f32_to_bf16_bits((0.05 * rng.standard_normal((N, K))).astype(np.float32))
+    w[3, 64:128] = 0
+    # amax 7.5 -> s = 1.0 exactly: the row is k/2 steps, every odd k a tie (round to even)
+    w[4, :64] = O.f32_to_bf16_bits(np.arange(-64, 64, 2, dtype=np.float32)[:64] * 0.125 - 0.0)
+    w[4, 0] = O.f32_to_bf16_bits(np.float32([7.5]))[0]
+    w[5, 128:192] = O.f32_to_bf16_bits(rng.uniform(-1e-6, 1e-6, 64).astype(np.float32))  # s16 subnormal
+    w[6, 192:256] = O.f32_to_bf16_bits(-np.abs(rng.standard_normal(64)).astype(np.float32))
+    return np.ascontiguousarray(w)
+
+
+@pytest.mark.parametrize("N,K,seed", [(32, 256, 3), (16, 1024, 11)])
+def test_rtn_int4_quantiser_bitwise_rtn_h(N, K, seed):
+    """orc_rtn_int4_g64 against the reference's rtn_int4_g64 (src/loader/rtn.h, compiled into
+    _ref): every qweight word and every scale, bit for bit, corner cases included."""
+    w = _rtn_rows(N, K, seed)
+    q1 = np.zeros((K // 8, N), np.uint32); s1 = np.zeros((K // 64, N), np.uint16)
+    q2 = np.zeros_like(q1); s2 = np.zeros_like(s1)
+    L().orc_rtn_int4_g64(P(w), K, N, P(q1), P(s1))
+    R.ref_rtn_int4_g64(P(w), K, N, P(q2), P(s2))
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+    assert s1[1, 3] == 0 and np.all(q1[8:16, 3] == 0x88888888)  # the zero group: s 0, q 8
