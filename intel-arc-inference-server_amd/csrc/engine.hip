@@ -953,7 +953,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
-      m.mtp > 1 || (m.mtp && (m.experts || m.kv_int8)) || m.lm_head_int8 > 1 ||
+      m.mtp > 1 || (m.mtp && m.experts) || m.lm_head_int8 > 1 ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {

@@ -87,8 +87,10 @@ def make(seed=42, **kw):
     return eng, orc, OracleHead(eng, orc)
 
 
-def test_drafts_vs_oracle_head_chain():
-    eng, orc, oh = make()
+@pytest.mark.parametrize("kv8", [0, 1])
+def test_drafts_vs_oracle_head_chain(kv8):
+    # kv8: the main model over the int8 rotated cache (head_dim 256); the head keeps its own f16 cache
+    eng, orc, oh = make(**(dict(head_dim=256, kv_int8=1) if kv8 else {}))
     H = eng.desc.hidden
     eng.capture(1)
     eng.reset(300, 7)
@@ -200,15 +202,18 @@ def test_prefill_fills_the_head_like_ingest():
         assert np.abs(x - y).max() <= 2e-2 * np.abs(y).max(), np.abs(x - y).max()
 
 
-def test_speculative_loop_emits_the_greedy_tokens():
+@pytest.mark.parametrize("kv8", [0, 1])
+def test_speculative_loop_emits_the_greedy_tokens(kv8):
     """draft(3) -> verify -> accept_greedy -> commit, repeated, against plain generate on a twin
-    engine: the same token stream, bit for bit (verify rows are bitwise the plain steps)."""
+    engine: the same token stream, bit for bit (verify rows are bitwise the plain steps); also
+    with the main model over the int8 cache."""
     n = 14
-    plain = mi.Engine(small_desc(mtp=1), seed=31)
+    kw = dict(head_dim=256, kv_int8=1) if kv8 else {}
+    plain = mi.Engine(small_desc(mtp=1, **kw), seed=31)
     plain.capture(1)
     plain.reset(100, 5)
     want = list(plain.generate(n))
-    eng = mi.Engine(small_desc(mtp=1), seed=31)
+    eng = mi.Engine(small_desc(mtp=1, **kw), seed=31)
     eng.capture(1)
     eng.reset(100, 5)
     got, accepted = [], 0
