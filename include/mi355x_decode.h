@@ -461,9 +461,9 @@ typedef struct mi_model_desc {
   uint32_t kv_int8;
   /* 1: the model's MTP head (loader::MtpHead; the draft lists of capture.cc:1772-1939): fc
    * [2 hidden] -> hidden behind the embedding's and the hidden's norms, one dense decoder layer
-   * at the model's shapes (mtp_intermediate = inter) with its own one-layer f16 KV cache, the
-   * head's final norm, the shared embedding and lm_head. Dense models only (the main cache f16
-   * or int8).
+   * at the model's shapes (mtp_intermediate = inter; an MoE model's head: one MoE layer of the
+   * model's shape, spec 15e) with its own one-layer f16 KV cache, the head's final norm, the
+   * shared embedding and lm_head (the main cache f16 or int8).
    * Every step then also fills the head's K/V (capture.cc:362-370) and mi_engine_draft runs the
    * draft lists. */
   uint32_t mtp;

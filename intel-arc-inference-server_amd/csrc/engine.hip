@@ -261,8 +261,14 @@ struct mi_engine {
       Layer& L = mh.L;
       MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_QKV));
       MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
-      MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
-      MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
+      if (moe) {  // an MoE model's head (spec 15e): one MoE layer of the model's shape
+        MI_TRY(alloc(&L.router, size_t(router_n) * H));
+        MI_TRY(alloc(&L.moe_gu, (m.experts + 1) * gu_block));
+        MI_TRY(alloc(&L.moe_dn, (m.experts + 1) * dn_block));
+      } else {
+        MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
+        MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
+      }
       for (float** nw : {&L.in_norm, &L.post_norm, &mh.pre_e, &mh.pre_h, &mh.final_n}) MI_TRY(alloc(nw, H));
       if (m.qk_norm) {
         MI_TRY(alloc(&L.q_norm, HD));
@@ -371,8 +377,14 @@ struct mi_engine {
       // stream starts at fc's output (K = 2 hidden over inputs with a common mode), and at the
       // layers' scales the random head's MLP output overflows fp16 at the 27B shape
       for (Linear* l : {&mh.fc, &mh.L.qkv, &mh.L.o, &mh.L.gate_up, &mh.L.down}) {
+        if (!l->q) continue;  // an MoE head has no dense gate||up / down
         MI_TRY(mi_fill_u32(l->q, size_t(l->K / 8) * l->N, seed++, stream));
         MI_TRY(mi_fill_f16(l->s, size_t(l->K / 64) * l->N, seed++, 0, 0.0005f, 0.005f, stream));
+      }
+      if (m.experts) {  // the MoE head's router as the layers', its experts at the head's scales
+        MI_TRY(mi_fill_f16(mh.L.router, size_t(router_n) * H, seed++, 1, 0.0f, 0.02f, stream));
+        MI_TRY(mi_fill_layout1(mh.L.moe_gu, (m.experts + 1) * gu_block / 136, seed++, 0.0005f, 0.005f, stream));
+        MI_TRY(mi_fill_layout1(mh.L.moe_dn, (m.experts + 1) * dn_block / 136, seed++, 0.0005f, 0.005f, stream));
       }
       for (float* nw : {mh.L.in_norm, mh.L.post_norm, mh.pre_e, mh.pre_h, mh.final_n})
         MI_TRY(mi_fill_f32(nw, H, seed++, 1, 1.0f, 0.02f, 1, stream));
@@ -464,12 +476,7 @@ struct mi_engine {
         // the MoE block (moe.cl:1-13): router || shared gate, route + gate||up (one launch:
         // each work-group routes its row itself), down folding into the residual, then the
         // next norm with nothing left to fold
-        MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
-        MI_TRY(mi_moe_gate_up_routed(moe_logits, router_n, moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k,
-                                     d.hidden, d.moe_inter, stream));
-        // down + combine into the residual, and the next norm in the same launch
-        MI_TRY(mi_moe_down_norm(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter,
-                                next_w, x, rstd, d.rms_eps, dn_words, ctrl + MI_CTRL_DEBUG, stream));
+        MI_TRY(moe_block(L, M, next_w));
         continue;
       }
       MI_TRY(launch_gate_up(L, M));
@@ -508,14 +515,28 @@ struct mi_engine {
     MI_TRY(mi_norm_finish(hsumsq, resid, mh.L.in_norm, x, M, H, G, d.rms_eps, stream));
     return launch_qkv_on(mh.L, hctl, hkv_k, hkv_v, M, true);
   }
+  // an MoE layer's FFN on x (rows M): router || shared gate, route + gate||up, down + combine
+  // into the residual with the next norm (weights next_w) into x
+  int moe_block(const Layer& L, uint32_t M, const float* next_w) {
+    MI_TRY(mi_gemv_f16w(L.router, x, moe_logits, M, d.hidden, router_n, router_ksplit(), stream));
+    MI_TRY(mi_moe_gate_up_routed(moe_logits, router_n, moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k,
+                                 d.hidden, d.moe_inter, stream));
+    return mi_moe_down_norm(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter, next_w,
+                            x, rstd, d.rms_eps, dn_words, ctrl + MI_CTRL_DEBUG, stream);
+  }
+
   // draft() (capture.cc:1849-1939): the whole head at one row on hctl, from (hctl's id, dh);
   // its final-normed hidden back into dh, its logits into hlogits, the argmax into hctl
   int enqueue_draft() {
     MI_TRY(head_front(dh, 1));
     MI_TRY(attn_pair(mh.L, hctl, hkv_k, hkv_v, 1, false));
     MI_TRY(launch_o(mh.L, 1));
-    MI_TRY(launch_gate_up(mh.L, 1));
-    MI_TRY(launch_down(mh.L, 1, mh.final_n));
+    if (d.experts) {  // an MoE model's head: its MoE layer (capture.cc:1913's moe_block)
+      MI_TRY(moe_block(mh.L, 1, mh.final_n));
+    } else {
+      MI_TRY(launch_gate_up(mh.L, 1));
+      MI_TRY(launch_down(mh.L, 1, mh.final_n));
+    }
     MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(dh, x, size_t(d.hidden) * 2, hipMemcpyDeviceToDevice, stream)),
                   "dh"));
     return head(hctl, 1, x, hlogits, hhist);
@@ -953,7 +974,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
-      m.mtp > 1 || (m.mtp && m.experts) || m.lm_head_int8 > 1 ||
+      m.mtp > 1 || m.lm_head_int8 > 1 ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {

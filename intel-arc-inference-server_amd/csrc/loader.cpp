@@ -719,6 +719,54 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   if (int rc = flush()) return rc;
   const bool moe = want.experts > 0;
   const uint32_t E = want.experts, MI = want.moe_inter;
+  // one int4 linear as shipped, or (rtn: the MTP head's 16-bit linears) quantised here by rtn.h's
+  // rule from its 16-bit weight
+  auto linear_or_rtn = [&](const std::string& base, uint32_t K, uint32_t N, bool rtn, std::vector<uint32_t>& q,
+                           std::vector<uint16_t>& sc) -> bool {
+    if (!rtn || ck.find(base + ".qweight")) {
+      Linear4 l;
+      if (!get_linear(ck, base, K, N, l, rep)) return false;
+      q.assign(l.q, l.q + size_t(K / 8) * N);
+      sc.assign(l.s, l.s + size_t(K / 64) * N);
+      return true;
+    }
+    if (!ck.find(base + ".weight"))
+      return ck.fail("engine_load: the engine has an MTP head and the checkpoint has no " + base + " (.weight or .qweight)");
+    if (!get_float(ck, base + ".weight", size_t(N) * K, f32)) return false;
+    quantise_rtn(f32, N, K, q, sc);
+    ++rep.mtp_quantised;
+    return true;
+  };
+  // an MoE layer's FFN under prefix lp into layer index li: router || shared gate as f16 tiles
+  // (rows 0..E-1 the router, row E the shared expert's gate, zero rows up to a multiple of 16,
+  // moe.cc), the experts and the shared expert (last) as layout-1 blocks
+  auto load_moe_ffn = [&](const std::string& lp, uint32_t li, bool rtn) -> int {
+    const uint32_t RN = (E + 1 + 15) / 16 * 16;
+    std::vector<float> rt;
+    if (!get_float(ck, lp + "mlp.gate.weight", size_t(E) * H, rt)) return fail_ck(ck);
+    if (!get_float(ck, lp + "mlp.shared_expert_gate.weight", H, f32)) return fail_ck(ck);
+    rt.insert(rt.end(), f32.begin(), f32.end());
+    rt.resize(size_t(RN) * H, 0.f);
+    if (!to_f16(ck, lp + "mlp.gate", rt, f16)) return fail_ck(ck);
+    std::vector<uint16_t> tiles(f16.size());
+    f16w_tile(f16.data(), H, RN, tiles.data());
+    if (int rc = upload(MI_T_ROUTER, li, tiles.data(), tiles.size() * 2, "router")) return rc;
+    const size_t gub = size_t(2 * MI / 16) * (H / 64) * 136, dnb = size_t(H / 16) * (MI / 64) * 136;
+    std::vector<uint32_t> gu((E + 1) * gub), dn((E + 1) * dnb), gq, uq, dq;
+    std::vector<uint16_t> gs, us, ds;
+    for (uint32_t ex = 0; ex <= E; ++ex) {
+      const std::string ep = ex < E ? lp + "mlp.experts." + std::to_string(ex) + "." : lp + "mlp.shared_expert.";
+      if (!linear_or_rtn(ep + "gate_proj", H, MI, rtn, gq, gs) || !linear_or_rtn(ep + "up_proj", H, MI, rtn, uq, us) ||
+          !linear_or_rtn(ep + "down_proj", MI, H, rtn, dq, ds))
+        return fail_ck(ck);
+      interleave16(gq.data(), uq.data(), H / 8, MI, qcat);
+      interleave16(gs.data(), us.data(), H / 64, MI, scat);
+      layout1(qcat.data(), scat.data(), H, 2 * MI, gu.data() + ex * gub);
+      layout1(dq.data(), ds.data(), MI, H, dn.data() + ex * dnb);
+    }
+    if (int rc = upload(MI_T_MOE_GU, li, gu.data(), gu.size() * 4, "expert gate||up blocks")) return rc;
+    return upload(MI_T_MOE_DN, li, dn.data(), dn.size() * 4, "expert down blocks");
+  };
   for (uint32_t li = 0; li < want.layers; ++li) {
     const std::string lp = pre + "layers." + std::to_string(li) + ".";
     Linear4 q, k, v, o;
@@ -755,33 +803,7 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
       if (int rc = upload(MI_T_DOWN_Q, li, dn.q, size_t(I / 8) * H * 4, "down_proj.qweight")) return rc;
       if (int rc = upload(MI_T_DOWN_S, li, dn.s, size_t(I / 64) * H * 2, "down_proj.scales")) return rc;
     } else {
-      // router || shared gate: rows 0..E-1 the router, row E the shared expert's gate, then
-      // zero rows up to a multiple of 16 (moe.cc), as f16 tiles
-      const uint32_t RN = (E + 1 + 15) / 16 * 16;
-      std::vector<float> rt;
-      if (!get_float(ck, lp + "mlp.gate.weight", size_t(E) * H, rt)) return fail_ck(ck);
-      if (!get_float(ck, lp + "mlp.shared_expert_gate.weight", H, f32)) return fail_ck(ck);
-      rt.insert(rt.end(), f32.begin(), f32.end());
-      rt.resize(size_t(RN) * H, 0.f);
-      if (!to_f16(ck, lp + "mlp.gate", rt, f16)) return fail_ck(ck);
-      std::vector<uint16_t> tiles(f16.size());
-      f16w_tile(f16.data(), H, RN, tiles.data());
-      if (int rc = upload(MI_T_ROUTER, li, tiles.data(), tiles.size() * 2, "router")) return rc;
-      const size_t gub = size_t(2 * MI / 16) * (H / 64) * 136, dnb = size_t(H / 16) * (MI / 64) * 136;
-      std::vector<uint32_t> gu((E + 1) * gub), dn((E + 1) * dnb);
-      for (uint32_t ex = 0; ex <= E; ++ex) {
-        const std::string ep = ex < E ? lp + "mlp.experts." + std::to_string(ex) + "." : lp + "mlp.shared_expert.";
-        Linear4 g, u, d2;
-        if (!get_linear(ck, ep + "gate_proj", H, MI, g, rep) || !get_linear(ck, ep + "up_proj", H, MI, u, rep) ||
-            !get_linear(ck, ep + "down_proj", MI, H, d2, rep))
-          return fail_ck(ck);
-        interleave16(g.q, u.q, H / 8, MI, qcat);
-        interleave16(g.s, u.s, H / 64, MI, scat);
-        layout1(qcat.data(), scat.data(), H, 2 * MI, gu.data() + ex * gub);
-        layout1(d2.q, d2.s, MI, H, dn.data() + ex * dnb);
-      }
-      if (int rc = upload(MI_T_MOE_GU, li, gu.data(), gu.size() * 4, "expert gate||up blocks")) return rc;
-      if (int rc = upload(MI_T_MOE_DN, li, dn.data(), dn.size() * 4, "expert down blocks")) return rc;
+      if (int rc = load_moe_ffn(lp, li, false)) return rc;
     }
     if (int rc = flush()) return rc;
   }
@@ -798,19 +820,7 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
     auto mtp_linear = [&](const std::string& base, uint32_t K, uint32_t N, std::vector<uint32_t>& q,
                           std::vector<uint16_t>& sc) -> bool {
       ++rep.mtp_tensors;
-      if (ck.find(base + ".qweight")) {
-        Linear4 l;
-        if (!get_linear(ck, base, K, N, l, rep)) return false;
-        q.assign(l.q, l.q + size_t(K / 8) * N);
-        sc.assign(l.s, l.s + size_t(K / 64) * N);
-        return true;
-      }
-      if (!ck.find(base + ".weight"))
-        return ck.fail("engine_load: the engine has an MTP head and the checkpoint has no " + base + " (.weight or .qweight)");
-      if (!get_float(ck, base + ".weight", size_t(N) * K, f32)) return false;
-      quantise_rtn(f32, N, K, q, sc);
-      ++rep.mtp_quantised;
-      return true;
+      return linear_or_rtn(base, K, N, true, q, sc);
     };
     auto mtp_norm = [&](const std::string& name, uint32_t n, uint32_t kind, uint32_t layer) -> int {
       ++rep.mtp_tensors;
@@ -853,15 +863,20 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
       if (int rc = mtp_norm(lp + "self_attn.k_norm.weight", HD, MI_T_K_NORM, HL)) return rc;
     }
     if (int rc = flush()) return rc;
-    if (!mtp_linear(lp + "mlp.gate_proj", H, I, q1, s1) || !mtp_linear(lp + "mlp.up_proj", H, I, q2, s2) ||
-        !mtp_linear(lp + "mlp.down_proj", I, H, q3, s3))
-      return fail_ck(ck);
-    interleave16(q1.data(), q2.data(), H / 8, I, qcat);
-    interleave16(s1.data(), s2.data(), H / 64, I, scat);
-    if (int rc = upload(MI_T_GU_Q, HL, qcat.data(), qcat.size() * 4, "mtp gate||up qweight")) return rc;
-    if (int rc = upload(MI_T_GU_S, HL, scat.data(), scat.size() * 2, "mtp gate||up scales")) return rc;
-    if (int rc = upload(MI_T_DOWN_Q, HL, q3.data(), q3.size() * 4, "mtp down_proj qweight")) return rc;
-    if (int rc = upload(MI_T_DOWN_S, HL, s3.data(), s3.size() * 2, "mtp down_proj scales")) return rc;
+    if (moe) {  // an MoE model's head (spec 15e): one MoE layer in the main layers' device form
+      if (int rc = load_moe_ffn(lp, HL, true)) return rc;
+      rep.mtp_tensors += 2 + 3 * (size_t(E) + 1);  // router, shared gate, the experts' linears
+    } else {
+      if (!mtp_linear(lp + "mlp.gate_proj", H, I, q1, s1) || !mtp_linear(lp + "mlp.up_proj", H, I, q2, s2) ||
+          !mtp_linear(lp + "mlp.down_proj", I, H, q3, s3))
+        return fail_ck(ck);
+      interleave16(q1.data(), q2.data(), H / 8, I, qcat);
+      interleave16(s1.data(), s2.data(), H / 64, I, scat);
+      if (int rc = upload(MI_T_GU_Q, HL, qcat.data(), qcat.size() * 4, "mtp gate||up qweight")) return rc;
+      if (int rc = upload(MI_T_GU_S, HL, scat.data(), scat.size() * 2, "mtp gate||up scales")) return rc;
+      if (int rc = upload(MI_T_DOWN_Q, HL, q3.data(), q3.size() * 4, "mtp down_proj qweight")) return rc;
+      if (int rc = upload(MI_T_DOWN_S, HL, s3.data(), s3.size() * 2, "mtp down_proj scales")) return rc;
+    }
     if (int rc = flush()) return rc;
   }
   // every tensor of the language model must have been bound (qzeros / g_idx are checked and

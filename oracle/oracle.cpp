@@ -1192,10 +1192,22 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
   orc_attn_reduce_v2(act, &md->attn, p, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
   linear(ly.o, attn_out.data());
   norm(part.data(), ly.o.S, ly.post_norm);
-  linear(ly.gate_up, x.data());
-  orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
-  linear(ly.down, hbuf.data());
-  norm(part.data(), ly.down.S, hd->final_norm);
+  if (md->experts) {  // an MoE model's head (spec 15e): one MoE layer of the model's shape
+    std::vector<float> lg(md->router_n);
+    orc_gemv_f16w(act, ly.router, x.data(), 1, H, md->router_n, md->router_ksplit, lg.data());
+    orc_moe_route r;
+    orc_moe_route_fn(act, lg.data(), md->experts, md->top_k, &r);
+    const size_t gub = size_t(2 * md->moe_inter / 16) * (H / 64) * 136;
+    const size_t dnb = size_t(H / 16) * (md->moe_inter / 64) * 136;
+    orc_moe_block(act, 1, md->experts, md->top_k, H, md->moe_inter, &r, x.data(), ly.moe_gu, nullptr, gub, 0,
+                  ly.moe_dn, nullptr, dnb, 0, 4, 2, nullptr, resid.data());
+    norm(nullptr, 0, hd->final_norm);
+  } else {
+    linear(ly.gate_up, x.data());
+    orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
+    linear(ly.down, hbuf.data());
+    norm(part.data(), ly.down.S, hd->final_norm);
+  }
   if (h_out) std::copy(x.begin(), x.end(), h_out);
   head_logits(act, md, x.data(), logits);
   return orc_argmax(logits, md->vocab, md->vocab_used);

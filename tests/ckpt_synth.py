@@ -125,10 +125,21 @@ class Synth:
                              "v": wbf(mp + "self_attn.v_proj.weight", KVH * HD, H),
                              "o": wbf(mp + "self_attn.o_proj.weight", H, QH * HD),
                              "in_norm": vec(mp + "input_layernorm.weight", H),
-                             "post_norm": vec(mp + "post_attention_layernorm.weight", H),
-                             "gate": wbf(mp + "mlp.gate_proj.weight", I, H),
-                             "up": wbf(mp + "mlp.up_proj.weight", I, H),
-                             "down": wbf(mp + "mlp.down_proj.weight", H, I)})
+                             "post_norm": vec(mp + "post_attention_layernorm.weight", H)})
+            if experts:  # an MoE model's head (spec 15e): one MoE layer, its linears in bf16
+                self.mtp["router"] = np.concatenate([O.bf16_bits_to_f32(wbf(mp + "mlp.gate.weight", experts, H)),
+                                                     O.bf16_bits_to_f32(wbf(mp + "mlp.shared_expert_gate.weight", 1,
+                                                                            H))])
+                self.mtp["experts"] = []
+                for e in range(experts + 1):
+                    ep = mp + (f"mlp.experts.{e}." if e < experts else "mlp.shared_expert.")
+                    self.mtp["experts"].append((wbf(ep + "gate_proj.weight", moe_inter, H),
+                                                wbf(ep + "up_proj.weight", moe_inter, H),
+                                                wbf(ep + "down_proj.weight", H, moe_inter)))
+            else:
+                self.mtp.update({"gate": wbf(mp + "mlp.gate_proj.weight", I, H),
+                                 "up": wbf(mp + "mlp.up_proj.weight", I, H),
+                                 "down": wbf(mp + "mlp.down_proj.weight", H, I)})
             if qk_norm:
                 self.mtp["q_norm"] = vec(mp + "self_attn.q_norm.weight", HD)
                 self.mtp["k_norm"] = vec(mp + "self_attn.k_norm.weight", HD)

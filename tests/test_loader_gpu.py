@@ -251,3 +251,64 @@ def test_mtp_head_loaded_and_drafts(tmp_path):
     with pytest.raises(mi.MiError, match="no mtp.fc"):
         e2.load(ppath)
     e2.close()
+
+
+def test_moe_mtp_head_loaded_and_drafts(tmp_path):
+    """An MoE model's head (spec 15e: one MoE layer of the model's shape) from bf16 mtp.*
+    tensors: the router as f16 tiles, every expert's linears quantised by rtn.h's rule into
+    layout-1 blocks, bitwise; the loaded head's drafts follow the oracle's head."""
+    from test_mtp_gpu import OracleHead, head_kv
+    H, E, MI = 512, 16, 128
+    syn = Synth(str(tmp_path / "mm"), layers=1, H=H, experts=E, top_k=4, moe_inter=MI, V=2048, mtp=True)
+    path = syn.write(split=2)
+    desc = mi.checkpoint_desc(path, max_len=512, max_rows=4)
+    desc.mtp = 1
+    eng = mi.Engine(desc, seed=5)
+    rep = eng.load(path)
+    print(f"engine_load {path} (MoE MTP head): {rep}", flush=True)
+    nq = 5 + 3 * (E + 1)  # fc, q, k, v, o and the experts' linears
+    assert f"MTP head: {12 + 2 + 3 * (E + 1)} tensors, {nq} linears quantised" in rep
+    li = eng.desc.layers
+    m = syn.mtp
+    rn = (E + 1 + 15) // 16 * 16
+    rows = np.zeros((rn, H), np.float32)
+    rows[:E + 1] = m["router"]
+    rt = np.empty(rn * H, np.uint16)
+    O.lib().orc_f16w_tile(O._p(O.f32_to_f16_bits(rows)), H, rn, O._p(rt))
+    assert np.array_equal(eng.to_host(mi.T_ROUTER, li, np.uint16), rt)
+    gu = eng.to_host(mi.T_MOE_GU, li, np.uint32)
+    dn = eng.to_host(mi.T_MOE_DN, li, np.uint32)
+    gub, dnb = (2 * MI // 16) * (H // 64) * 136, (H // 16) * (MI // 64) * 136
+
+    def rtn(b, K, N):
+        q = np.zeros((K // 8, N), np.uint32)
+        s = np.zeros((K // 64, N), np.uint16)
+        O.lib().orc_rtn_int4_g64(O._p(np.ascontiguousarray(b)), K, N, O._p(q), O._p(s))
+        return q, s
+
+    for e in (0, 9, E):
+        (gq, gs), (uq, us), (dq, ds) = rtn(m["experts"][e][0], H, MI), rtn(m["experts"][e][1], H, MI), \
+            rtn(m["experts"][e][2], MI, H)
+        want = np.empty(gub, np.uint32)
+        O.lib().orc_repack_layout1(O._p(np.ascontiguousarray(expect_interleave(gq, uq))),
+                                   O._p(np.ascontiguousarray(expect_interleave(gs, us))), H, 2 * MI, O._p(want))
+        assert np.array_equal(gu[e * gub:(e + 1) * gub], want), e
+        want = np.empty(dnb, np.uint32)
+        O.lib().orc_repack_layout1(O._p(dq), O._p(ds), MI, H, O._p(want))
+        assert np.array_equal(dn[e * dnb:(e + 1) * dnb], want), e
+    orc = OracleModel(eng)
+    oh = OracleHead(eng, orc)
+    eng.capture(1)
+    eng.reset(100, 7)
+    eng.generate(3)
+    c = eng.ctrl()
+    pos, cur = int(c[mi.CTRL_POS]), int(c[mi.CTRL_CUR])
+    hh0 = eng.to_host(mi.T_MTP_HH, 0, np.uint16)[:H].copy()
+    kk, vv = head_kv(eng)
+    drafts = eng.draft(3)
+    tok, h = cur, hh0
+    for i in range(3):
+        am, logits, hout = oh.run(tok, h, pos - 1 + i, kk, vv)
+        assert argmax_ok(int(drafts[i]), logits), (i, drafts[i], am)
+        tok, h = int(drafts[i]), hout
+    eng.close()

@@ -15,7 +15,7 @@ import pytest
 
 import oracle as O
 from mipkg import mi
-from test_engine_gpu import OracleModel, argmax_ok, close, small_desc
+from test_engine_gpu import OracleModel, argmax_ok, close, moe_small_desc, small_desc
 
 pytestmark = pytest.mark.gpu
 F16 = O.ORC_F16
@@ -36,14 +36,22 @@ class OracleHead:
             return a
 
         li = d.layers
+        moe = d.experts > 0
         S = [eng.linear_s(w) for w in range(4)]
         lins = []
         for w, (K, N) in enumerate([(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]):
+            if moe and w >= 2:  # an MoE model's head: its MoE layer instead of gate||up / down
+                lins.append(O.Linear(None, None, K, N, 1))
+                continue
             q = h(eng.to_host(2 * w, li, np.uint32))
             s = h(eng.to_host(2 * w + 1, li, np.uint16))
             lins.append(O.Linear(q.ctypes.data, s.ctypes.data, K, N, S[w]))
         L = O.Layer()
         L.qkv, L.o, L.gate_up, L.down = lins
+        if moe:
+            L.router = h(eng.to_host(mi.T_ROUTER, li, np.uint16)).ctypes.data
+            L.moe_gu = h(eng.to_host(mi.T_MOE_GU, li, np.uint32)).ctypes.data
+            L.moe_dn = h(eng.to_host(mi.T_MOE_DN, li, np.uint32)).ctypes.data
         L.in_norm = h(eng.to_host(mi.T_IN_NORM, li, np.float32)).ctypes.data
         L.post_norm = h(eng.to_host(mi.T_POST_NORM, li, np.float32)).ctypes.data
         if d.qk_norm:
@@ -81,16 +89,17 @@ def head_kv(eng):
         eng.to_host(mi.T_MTP_KV_V, 0, np.uint16).reshape(eng.desc.kv_heads, eng.desc.max_len, -1).copy()
 
 
-def make(seed=42, **kw):
-    eng = mi.Engine(small_desc(mtp=1, **kw), seed=seed)
+def make(seed=42, moe=False, **kw):
+    eng = mi.Engine((moe_small_desc if moe else small_desc)(mtp=1, **kw), seed=seed)
     orc = OracleModel(eng)
     return eng, orc, OracleHead(eng, orc)
 
 
-@pytest.mark.parametrize("kv8", [0, 1])
-def test_drafts_vs_oracle_head_chain(kv8):
-    # kv8: the main model over the int8 rotated cache (head_dim 256); the head keeps its own f16 cache
-    eng, orc, oh = make(**(dict(head_dim=256, kv_int8=1) if kv8 else {}))
+@pytest.mark.parametrize("kind", ["dense", "kv8", "moe"])
+def test_drafts_vs_oracle_head_chain(kind):
+    # kv8: the main model over the int8 rotated cache (head_dim 256); the head keeps its own f16
+    # cache. moe: an MoE model, whose head is one MoE layer (spec 15e)
+    eng, orc, oh = make(**{"dense": {}, "kv8": dict(head_dim=256, kv_int8=1), "moe": dict(moe=True)}[kind])
     H = eng.desc.hidden
     eng.capture(1)
     eng.reset(300, 7)
@@ -202,18 +211,19 @@ def test_prefill_fills_the_head_like_ingest():
         assert np.abs(x - y).max() <= 2e-2 * np.abs(y).max(), np.abs(x - y).max()
 
 
-@pytest.mark.parametrize("kv8", [0, 1])
-def test_speculative_loop_emits_the_greedy_tokens(kv8):
+@pytest.mark.parametrize("kind", ["dense", "kv8", "moe"])
+def test_speculative_loop_emits_the_greedy_tokens(kind):
     """draft(3) -> verify -> accept_greedy -> commit, repeated, against plain generate on a twin
     engine: the same token stream, bit for bit (verify rows are bitwise the plain steps); also
     with the main model over the int8 cache."""
     n = 14
-    kw = dict(head_dim=256, kv_int8=1) if kv8 else {}
-    plain = mi.Engine(small_desc(mtp=1, **kw), seed=31)
+    kw = dict(head_dim=256, kv_int8=1) if kind == "kv8" else {}
+    mk = moe_small_desc if kind == "moe" else small_desc
+    plain = mi.Engine(mk(mtp=1, **kw), seed=31)
     plain.capture(1)
     plain.reset(100, 5)
     want = list(plain.generate(n))
-    eng = mi.Engine(small_desc(mtp=1, **kw), seed=31)
+    eng = mi.Engine(mk(mtp=1, **kw), seed=31)
     eng.capture(1)
     eng.reset(100, 5)
     got, accepted = [], 0
