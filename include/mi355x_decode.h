@@ -460,7 +460,7 @@ typedef struct mi_model_desc {
    * [layers][kv_heads][max_len]; the step runs attn_prep_kv8 and the rotated reader pair. */
   uint32_t kv_int8;
   /* 1: the model's MTP head (loader::MtpHead; the draft lists of capture.cc:1772-1939): fc
-   * [2 hidden] -> hidden behind the embedding's and the hidden's norms, one dense decoder layer
+   * [2 hidden] -> hidden behind the embedding's and the hidden's norms, one decoder layer
    * at the model's shapes (mtp_intermediate = inter; an MoE model's head: one MoE layer of the
    * model's shape, spec 15e) with its own one-layer f16 KV cache, the head's final norm, the
    * shared embedding and lm_head (the main cache f16 or int8).
