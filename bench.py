@@ -320,15 +320,17 @@ def measure_lm_head_int8(st):
             "frac_of_peak": round(alg / t / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
 
 
-def measure_mtp(args):
+def measure_mtp(args, moe=False):
     """The MTP draft lists at the 27B shape (the head: one more dense layer at the model's
-    shapes, sharing the embedding and lm_head; random-init): the plain step with the head's K/V
-    fill, one draft list (the head at one row: front, attention over its own cache, MLP, head)
-    and the verify step at k = 3 (four rows, the fill over them), at context `--context`. The
-    weights are random, so the acceptance rate says nothing about a trained head; the time per
-    list is what the speculative loop pays."""
+    shapes, sharing the embedding and lm_head; random-init) or, moe, on the configs[3] MoE model
+    (the head: one MoE layer of its shape): the plain step with the head's K/V fill, one draft
+    list (the head at one row: front, attention over its own cache, FFN, head) and the verify
+    step at k = 3 (four rows, the fill over them), at context `--context`. The weights are
+    random, so the acceptance rate says nothing about a trained head; the time per list is what
+    the speculative loop pays."""
     ctx = args.context
-    desc = mi.desc_27b(max_len=((ctx + 64 + 1 + 63) // 64) * 64)
+    max_len = ((ctx + 64 + 1 + 63) // 64) * 64
+    desc = mi.desc_moe_cfg4(max_len=max_len) if moe else mi.desc_27b(max_len=max_len)
     desc.mtp = 1
     eng = mi.Engine(desc, seed=args.seed)  # the main model's weights are the bench engine's
     eng.capture(1)
@@ -354,7 +356,8 @@ def measure_mtp(args):
     assert c[mi.CTRL_DEBUG] == 0, (hex(c[mi.CTRL_DEBUG]), list(drafts), [hex(v) for v in c[:20]],
                                    [hex(v) for v in eng.to_host(mi.T_MTP_CTRL, 0, np.uint32)[:20]])
     eng.close()
-    return {"workload": f"27B shape with an MTP head (random-init), context {ctx}",
+    return {"workload": ("configs[3] MoE model" if moe else "27B shape") +
+                        f" with an MTP head (random-init), context {ctx}",
             "plain_step_with_fill_ms": round(plain / 1e3, 4),
             "draft_3_ms": round(t_draft3, 3), "draft_list_ms": round(t_draft3 / 3, 3),
             "verify_k3_ms": round(t_verify, 3),
@@ -700,7 +703,7 @@ def main():
         print(json.dumps({"lm_head_int8": measure_lm_head_int8(None)}), flush=True)
         return
     if args.only == "mtp":
-        print(json.dumps({"mtp": measure_mtp(args)}), flush=True)
+        print(json.dumps({"mtp": measure_mtp(args), "mtp_moe": measure_mtp(args, moe=True)}), flush=True)
         return
     if args.only == "moe_prefill":
         # the configs[3] MoE model's chunked prefill of a 2048-token prompt, three timed calls
@@ -824,6 +827,7 @@ def main():
         other["lm_head_int8"] = measure_lm_head_int8(None)
         log(f"bench: int8 lm_head {other['lm_head_int8']}")
         other["mtp"] = measure_mtp(args)
+        other["mtp_moe"] = measure_mtp(args, moe=True)
         log(f"bench: mtp {other['mtp']}")
 
     out = {
