@@ -185,14 +185,15 @@ def test_plain_steps_keep_the_head_filled():
         assert np.array_equal(hh[0], hh[1])  # committed at once
 
 
-def test_prefill_fills_the_head_like_ingest():
+@pytest.mark.parametrize("moe", [False, True])
+def test_prefill_fills_the_head_like_ingest(moe):
     """step_mtp_kv: a prefilled prompt leaves the head's K/V rows 0..n-2 and hh row 0 within the
     prefill's bar of the token-by-token ingest's (the prefill's hidden rows carry its own
-    roundings: rel 2e-2 of the rows' largest value)."""
+    roundings: rel 2e-2 of the rows' largest value); also on an MoE model."""
     ids = np.random.default_rng(4).integers(0, 4096, 40).astype(np.uint32)
     outs = []
     for way in ("prefill", "ingest"):
-        eng = mi.Engine(small_desc(mtp=1, max_rows=4), seed=77)
+        eng = mi.Engine((moe_small_desc if moe else small_desc)(mtp=1, max_rows=4), seed=77)
         eng.capture(1)
         eng.reset(0, int(ids[0]))
         print(f"mtp {way} of {ids.size} ids", flush=True)
