@@ -380,12 +380,13 @@ int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blo
  * work-groups after the down grid takes each row's norm from the new residual values, which
  * the down work-groups also publish through `handoff` ([M][hidden/2] hand-off words that hold
  * the empty pattern between launches: mi_gemv_handoff_init once; every launch leaves them
- * empty). A wait that never completes gives up after about a second and sets *status (may be
- * NULL) to MI_STATUS_HANDOFF_TIMEOUT. M <= 8. */
+ * empty). A wait that never completes gives up after poll_limit polls of a word (0 = 2^21,
+ * about a second) and sets *status (may be NULL) to MI_STATUS_HANDOFF_TIMEOUT. inject: 0 in
+ * normal use; bit 0 = the down work-groups publish nothing (tests of the timeout path). M <= 8. */
 int mi_moe_down_norm(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks,
                      uint16_t* resid, uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden,
                      uint32_t inter, const float* norm_w, uint16_t* x_out, float* rstd, float eps,
-                     uint32_t* handoff, uint32_t* status, void* stream);
+                     uint32_t* handoff, uint32_t* status, uint32_t poll_limit, uint32_t inject, void* stream);
 
 /* ---- the chunked prefill's kernels (src/kernels/prefill: pf_gemm_q4.cl, pf_flash_attn.cl,
  * pf_embed.cl) ---- */

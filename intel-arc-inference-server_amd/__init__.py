@@ -104,7 +104,7 @@ SIGNATURES = {
     "mi_moe_route": (i32, [vp, vp, u32, u32, u32, u32, vp]),
     "mi_moe_gate_up": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "mi_moe_gate_up_routed": (i32, [vp, u32, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
-    "mi_moe_down_norm": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp, vp, f32, vp, vp, vp]),
+    "mi_moe_down_norm": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp, vp, f32, vp, vp, u32, u32, vp]),
     "mi_moe_down": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
 }
 

@@ -522,7 +522,7 @@ struct mi_engine {
     MI_TRY(mi_moe_gate_up_routed(moe_logits, router_n, moe_route, x, L.moe_gu, moe_h, M, d.experts, d.top_k,
                                  d.hidden, d.moe_inter, stream));
     return mi_moe_down_norm(moe_route, moe_h, L.moe_dn, resid, M, d.experts, d.top_k, d.hidden, d.moe_inter, next_w,
-                            x, rstd, d.rms_eps, dn_words, ctrl + MI_CTRL_DEBUG, stream);
+                            x, rstd, d.rms_eps, dn_words, ctrl + MI_CTRL_DEBUG, 0, 0, stream);
   }
 
   // draft() (capture.cc:1849-1939): the whole head at one row on hctl, from (hctl's id, dh);

@@ -384,6 +384,7 @@ struct DownNorm {
   float eps;
   uint32_t* status;     // set to kStatusTimeout when a wait gives up (NULL: none)
   uint32_t poll_limit;
+  uint32_t inject;      // fault injection for tests: bit 0 = the down work-groups publish nothing
 };
 constexpr uint32_t kDnPollLimit = 1u << 21;
 
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
     const uint16_t o_b = f2h(h2f(r_b) + h2f(sh_b));
     const uint16_t nv = f2h(h2f(r_old) + h2f(o_b));
     *rp = nv;
-    if (dnm.x) {  // the pair (t, t + 1) as one hand-off word for the norm work-group
+    if (dnm.x && !(dnm.inject & 1u)) {  // the pair (t, t + 1) as one hand-off word for the norm work-group
       const uint16_t hi = (uint16_t)__shfl_down((int)nv, 1, 64);
       if ((t & 1u) == 0)
         st_agent(dnm.words + (size_t)m * (hidden / 2) + (nb * 16u + ch * 8u + t) / 2u, publishable_pair(nv, hi));
@@ -640,7 +641,7 @@ extern "C" int mi_moe_down(const uint32_t* route, const uint16_t* h, const uint3
 extern "C" int mi_moe_down_norm(const uint32_t* route, const uint16_t* h, const uint32_t* dn_blocks, uint16_t* resid,
                                 uint32_t M, uint32_t experts, uint32_t top_k, uint32_t hidden, uint32_t inter,
                                 const float* norm_w, uint16_t* x_out, float* rstd, float eps, uint32_t* handoff,
-                                uint32_t* status, void* stream) {
+                                uint32_t* status, uint32_t poll_limit, uint32_t inject, void* stream) {
   if (!route || !h || !dn_blocks || !resid || !norm_w || !x_out || !handoff)
     return mi_fail(MI_ERR_ARG, "moe_down_norm: null pointer");
   if (int e = check_moe(M, experts, top_k, hidden, inter)) return e;
@@ -648,7 +649,7 @@ extern "C" int mi_moe_down_norm(const uint32_t* route, const uint16_t* h, const 
   if (reinterpret_cast<uintptr_t>(dn_blocks) % 16 || reinterpret_cast<uintptr_t>(h) % 16)
     return mi_fail(MI_ERR_ARG, "moe_down_norm: dn_blocks and h need 16-byte alignment");
   const size_t lds = size_t(top_k + 1) * (inter / 64) * kHalfU32 * 4;
-  const DownNorm dnm{handoff, norm_w, x_out, rstd, eps, status, kDnPollLimit};
+  const DownNorm dnm{handoff, norm_w, x_out, rstd, eps, status, poll_limit ? poll_limit : kDnPollLimit, inject};
   moe_down_kernel<<<dim3(hidden / 8, M + 1), 256, lds, static_cast<hipStream_t>(stream)>>>(
       route, h, dn_blocks, resid, experts, top_k, hidden, inter, M, dnm);
   return mi_hip(static_cast<int>(hipGetLastError()), "moe_down_norm launch");

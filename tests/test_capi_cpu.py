@@ -58,8 +58,8 @@ def test_moe_argument_errors_without_a_gpu():
     assert L.mi_moe_route(8, 8, 1, 256, 8, 256, None) == -2      # router_n < experts + 1
     assert L.mi_moe_gate_up(8, 8, 8, 8, 1, 256, 8, 2000, 512, None) == -2  # hidden % 512
     assert L.mi_moe_gate_up_routed(None, 272, 8, 8, 8, 8, 1, 256, 8, 2048, 512, None) == -1
-    assert L.mi_moe_down_norm(8, 8, 8, 8, 1, 256, 8, 2048, 512, 8, 8, None, 1e-6, None, None, None) == -1
-    assert L.mi_moe_down_norm(16, 16, 16, 16, 9, 256, 8, 2048, 512, 16, 16, None, 1e-6, 16, None, None) == -2
+    assert L.mi_moe_down_norm(8, 8, 8, 8, 1, 256, 8, 2048, 512, 8, 8, None, 1e-6, None, None, 0, 0, None) == -1
+    assert L.mi_moe_down_norm(16, 16, 16, 16, 9, 256, 8, 2048, 512, 16, 16, None, 1e-6, 16, None, 0, 0, None) == -2
     assert L.mi_moe_gate_up_routed(8, 256, 8, 8, 8, 8, 1, 256, 8, 2048, 512, None) == -2  # router_n < E + 1
     assert L.mi_moe_gate_up_routed(8, 272, 8, 8, 8, 8, 1, 256, 8, 2000, 512, None) == -2  # hidden % 512
     assert L.mi_moe_down(8, 8, 8, 8, 1, 256, 8, 2048, 2048, None) == -2    # inter > 1024

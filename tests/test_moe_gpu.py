@@ -231,13 +231,22 @@ def test_down_norm_is_down_then_norm_rows(E, hidden, inter, M):
         mi.call("mi_moe_down", ptr(route), ptr(h), ptr(mo.d_dn), ptr(r1), rows, E, mo.top_k, hidden, inter, stream())
         mi.call("mi_norm_rows", ptr(r1), ptr(dw), ptr(x1), ptr(s1), rows, hidden, np.float32(1e-6), stream())
         mi.call("mi_moe_down_norm", ptr(route), ptr(h), ptr(mo.d_dn), ptr(r2), rows, E, mo.top_k, hidden, inter,
-                ptr(dw), ptr(x2), ptr(s2), np.float32(1e-6), ptr(handoff), ptr(status), stream())
+                ptr(dw), ptr(x2), ptr(s2), np.float32(1e-6), ptr(handoff), ptr(status), 0, 0, stream())
         sync()
         assert host(status, np.uint32)[0] == 0
         assert np.all(host(handoff, np.uint32) == 0xFFFFFFFF), "hand-off words not left empty"
         assert np.array_equal(host(r1, np.uint16), host(r2, np.uint16))
         assert np.array_equal(host(x1, np.uint16), host(x2, np.uint16))
         assert np.array_equal(host(s1, np.uint32), host(s2, np.uint32))
+    # the timeout path, forced from the host: the down work-groups publish nothing and the
+    # norm's waits give up after 64 polls; every kernel ends, the status word says so, and the
+    # hand-off words are left empty for the next launch
+    status = dev(np.zeros(1, np.uint32))
+    mi.call("mi_moe_down_norm", ptr(route), ptr(h), ptr(mo.d_dn), ptr(dev(resid)), rows, E, mo.top_k, hidden,
+            inter, ptr(dw), ptr(x2), ptr(s2), np.float32(1e-6), ptr(handoff), ptr(status), 64, 1, stream())
+    sync()
+    assert host(status, np.uint32)[0] == 0xDEAD0003
+    assert np.all(host(handoff, np.uint32) == 0xFFFFFFFF)
 
 
 def test_malformed_route_row_reads_the_shared_block():
