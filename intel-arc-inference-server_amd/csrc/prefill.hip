@@ -214,24 +214,26 @@ __device__ __forceinline__ uint32_t moe_slot_expert(const uint32_t* row, uint32_
   return id < E ? id : E;
 }
 
-// One work-group, a counting sort of the pairs p = t (top_k + 1) + s of T rows by expert: expert
-// e's pairs go to list[off_e ..], its row tiles to tiles[] as {e, first list index, pair count},
-// the tile count to tiles_n[0]. The order of the pairs within an expert comes from LDS atomics
-// and may differ between calls; it changes no result (an output row of the GEMM depends on its
-// own activation row only).
+// One work-group, a stable counting sort of the pairs p = t (top_k + 1) + s of T rows by expert:
+// expert e's pairs go to list[off_e ..] in ascending p (the reference's (token, slot) order), its
+// row tiles to tiles[] as {e, first list index, pair count}, the tile count to tiles_n[0]. Wave w
+// owns the pairs [w Q, (w + 1) Q): it counts them per expert, then places them 64 at a time, a
+// lane's rank among the lanes of its expert coming from a match mask built from 9 ballots (one per
+// bit of the expert index), so list[] is the same on every call.
 __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restrict__ route, uint32_t T,
                                                         uint32_t E, uint32_t top_k, uint32_t* __restrict__ list,
                                                         u4_t* __restrict__ tiles, uint32_t* __restrict__ tiles_n) {
   __shared__ uint16_t s_ex[kMoeMaxPairs];
-  __shared__ uint32_t s_cnt[257], s_off[257], s_toff[257], s_cur[257];
-  const uint32_t t = threadIdx.x, slots = top_k + 1, P = T * slots;
-  for (uint32_t e = t; e <= E; e += 256u) s_cnt[e] = s_cur[e] = 0;
+  __shared__ uint32_t s_wc[4][257], s_off[257], s_toff[257], s_cnt[257];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, slots = top_k + 1, P = T * slots;
+  for (uint32_t e = t; e <= E; e += 256u) s_wc[0][e] = s_wc[1][e] = s_wc[2][e] = s_wc[3][e] = 0;
+  for (uint32_t p = t; p < P; p += 256u)
+    s_ex[p] = (uint16_t)moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
   __syncthreads();
-  for (uint32_t p = t; p < P; p += 256u) {
-    const uint32_t e = moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
-    s_ex[p] = (uint16_t)e;
-    atomicAdd(&s_cnt[e], 1u);
-  }
+  const uint32_t Q = (P + 3u) / 4u, lo = min(P, wave * Q), hi = min(P, lo + Q);
+  for (uint32_t p = lo + lane; p < hi; p += 64u) atomicAdd(&s_wc[wave][s_ex[p]], 1u);  // counts only
+  __syncthreads();
+  for (uint32_t e = t; e <= E; e += 256u) s_cnt[e] = s_wc[0][e] + s_wc[1][e] + s_wc[2][e] + s_wc[3][e];
   __syncthreads();
   if (t == 0) {
     uint32_t o = 0, to = 0;
@@ -244,9 +246,32 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
     tiles_n[0] = to;
   }
   __syncthreads();
-  for (uint32_t p = t; p < P; p += 256u) {
-    const uint32_t e = s_ex[p];
-    list[s_off[e] + atomicAdd(&s_cur[e], 1u)] = p;
+  for (uint32_t e = t; e <= E; e += 256u) {  // s_wc becomes each wave's next list index per expert
+    uint32_t b = s_off[e];
+    for (uint32_t w = 0; w < 4u; ++w) {
+      const uint32_t c = s_wc[w][e];
+      s_wc[w][e] = b;
+      b += c;
+    }
+  }
+  __syncthreads();
+  const uint64_t below = lane ? (~0ull >> (64u - lane)) : 0ull;
+  for (uint32_t p0 = lo; p0 < hi; p0 += 64u) {
+    const uint32_t p = p0 + lane;
+    const bool valid = p < hi;
+    const uint32_t e = valid ? s_ex[p] : 511u;  // 511: no expert index (E <= 256)
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (uint32_t b = 0; b < 9u; ++b) {
+      const uint64_t bal = __ballot((e >> b) & 1u);
+      same &= ((e >> b) & 1u) ? bal : ~bal;
+    }
+    const uint32_t rank = (uint32_t)__popcll(same & below);
+    const uint32_t base = valid ? s_wc[wave][e] : 0u;
+    if (valid) list[base + rank] = p;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) s_wc[wave][e] = base + (uint32_t)__popcll(same);
+    __builtin_amdgcn_wave_barrier();
   }
   for (uint32_t e = t; e <= E; e += 256u) {
     const uint32_t n = s_cnt[e];

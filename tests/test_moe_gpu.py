@@ -336,9 +336,12 @@ def test_moe_prefill_matches_decode_kernels(T, bad):
     w = O.f16_bits_to_f32(orc).astype(np.float64)[ok]
     g = got[ok]
     assert np.all(np.abs(g - w) <= 2e-3 * np.abs(w) + 2e-3 * np.abs(w).max()), np.abs(g - w).max() / np.abs(w).max()
-    # every pair listed once, grouped by expert
+    # every pair listed once, grouped by expert in ascending (token, slot) order: the stable sort
+    # of the pairs by expert (a bad id reads the shared expert E)
     n_tiles = int(host(tiles_n, np.uint32)[0])
-    assert sorted(host(lst, np.uint32).tolist()) == list(range(P))
+    ids = rt_all[:, :K].astype(np.int64)
+    ex = np.concatenate([np.where(ids < E, ids, E), np.full((T, 1), E)], axis=1).ravel()
+    assert np.array_equal(host(lst, np.uint32), np.argsort(ex, kind="stable").astype(np.uint32))
     assert 1 <= n_tiles <= (P + 63) // 64 + E + 1
 
 
