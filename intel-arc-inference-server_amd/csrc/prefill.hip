@@ -216,24 +216,30 @@ __device__ __forceinline__ uint32_t moe_slot_expert(const uint32_t* row, uint32_
 
 // One work-group, a stable counting sort of the pairs p = t (top_k + 1) + s of T rows by expert:
 // expert e's pairs go to list[off_e ..] in ascending p (the reference's (token, slot) order), its
-// row tiles to tiles[] as {e, first list index, pair count}, the tile count to tiles_n[0]. Wave w
-// owns the pairs [w Q, (w + 1) Q): it counts them per expert, then places them 64 at a time, a
+// row tiles to tiles[] as {e, first list index, pair count}, the tile count to tiles_n[0]. Wave w (of
+// 16) owns the pairs [w Q, (w + 1) Q): it counts them per expert, then places them 64 at a time, a
 // lane's rank among the lanes of its expert coming from a match mask built from 9 ballots (one per
 // bit of the expert index), so list[] is the same on every call.
-__global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restrict__ route, uint32_t T,
+__global__ __launch_bounds__(1024) void moe_group_kernel(const uint32_t* __restrict__ route, uint32_t T,
                                                         uint32_t E, uint32_t top_k, uint32_t* __restrict__ list,
                                                         u4_t* __restrict__ tiles, uint32_t* __restrict__ tiles_n) {
   __shared__ uint16_t s_ex[kMoeMaxPairs];
-  __shared__ uint32_t s_wc[4][257], s_off[257], s_toff[257], s_cnt[257];
+  constexpr uint32_t kW = 16, kT = kW * 64;
+  __shared__ uint32_t s_wc[kW][257], s_off[257], s_toff[257], s_cnt[257];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, slots = top_k + 1, P = T * slots;
-  for (uint32_t e = t; e <= E; e += 256u) s_wc[0][e] = s_wc[1][e] = s_wc[2][e] = s_wc[3][e] = 0;
-  for (uint32_t p = t; p < P; p += 256u)
+  for (uint32_t e = t; e <= E; e += kT)
+    for (uint32_t w = 0; w < kW; ++w) s_wc[w][e] = 0;
+  for (uint32_t p = t; p < P; p += kT)
     s_ex[p] = (uint16_t)moe_slot_expert(route + (size_t)(p / slots) * kMoeRouteWords, p % slots, E, top_k);
   __syncthreads();
-  const uint32_t Q = (P + 3u) / 4u, lo = min(P, wave * Q), hi = min(P, lo + Q);
+  const uint32_t Q = (P + kW - 1u) / kW, lo = min(P, wave * Q), hi = min(P, lo + Q);
   for (uint32_t p = lo + lane; p < hi; p += 64u) atomicAdd(&s_wc[wave][s_ex[p]], 1u);  // counts only
   __syncthreads();
-  for (uint32_t e = t; e <= E; e += 256u) s_cnt[e] = s_wc[0][e] + s_wc[1][e] + s_wc[2][e] + s_wc[3][e];
+  for (uint32_t e = t; e <= E; e += kT) {
+    uint32_t c = 0;
+    for (uint32_t w = 0; w < kW; ++w) c += s_wc[w][e];
+    s_cnt[e] = c;
+  }
   __syncthreads();
   if (t == 0) {
     uint32_t o = 0, to = 0;
@@ -246,9 +252,9 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
     tiles_n[0] = to;
   }
   __syncthreads();
-  for (uint32_t e = t; e <= E; e += 256u) {  // s_wc becomes each wave's next list index per expert
+  for (uint32_t e = t; e <= E; e += kT) {  // s_wc becomes each wave's next list index per expert
     uint32_t b = s_off[e];
-    for (uint32_t w = 0; w < 4u; ++w) {
+    for (uint32_t w = 0; w < kW; ++w) {
       const uint32_t c = s_wc[w][e];
       s_wc[w][e] = b;
       b += c;
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const uint32_t* __restri
     if (valid && rank == 0) s_wc[wave][e] = base + (uint32_t)__popcll(same);
     __builtin_amdgcn_wave_barrier();
   }
-  for (uint32_t e = t; e <= E; e += 256u) {
+  for (uint32_t e = t; e <= E; e += kT) {
     const uint32_t n = s_cnt[e];
     for (uint32_t k = 0; k * kMoeRows < n; ++k)
       tiles[s_toff[e] + k] = u4_t{e, s_off[e] + k * kMoeRows, min(kMoeRows, n - k * kMoeRows), 0u};
@@ -897,7 +903,7 @@ int mi_moe_prefill(const uint32_t* route, const uint16_t* x, const uint32_t* gu_
   const size_t dn_block = (size_t)(hidden / 16u) * (inter / GBK) * kMoeTile;
   hipStream_t st = (hipStream_t)stream;
   u4_t* tl = reinterpret_cast<u4_t*>(tiles);
-  moe_group_kernel<<<1, 256, 0, st>>>(route, T, experts, top_k, list, tl, tiles_n);
+  moe_group_kernel<<<1, 1024, 0, st>>>(route, T, experts, top_k, list, tl, tiles_n);
   moe_gemm_kernel<true><<<dim3(2u * inter / 256u, max_tiles), 256, 0, st>>>(tl, tiles_n, list, gu_blocks, gu_block,
                                                                             x, T, h, nullptr, slots, hidden,
                                                                             2u * inter);
