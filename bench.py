@@ -442,9 +442,20 @@ def measure_cfg5(st):
 def time_prefill(eng, T):
     """ms of one T-token prefill from position 0 in one chunk (synthetic ids); the first call,
     which allocates the prefill scratch, is not timed."""
-    ids = np.random.default_rng(7).integers(0, eng.desc.vocab_used, T).astype(np.uint32)
-    eng.reset(0, 0)
-    eng.prefill(ids, T)
+    # the synthetic model's fp16 residual leaves the fp16 range on some prompts (the engine then
+    # fails the call): the prompt is the first seed's, from 7 on, whose logits stay finite
+    for seed in range(7, 39):
+        ids = np.random.default_rng(seed).integers(0, eng.desc.vocab_used, T).astype(np.uint32)
+        eng.reset(0, 0)
+        try:
+            eng.prefill(ids, T)
+            break
+        except mi.MiError as e:
+            if "not finite" not in str(e):
+                raise
+            log(f"bench: prefill prompt seed {seed} leaves the fp16 range; next seed")
+    else:
+        raise RuntimeError("no prompt seed keeps the fp16 prefill finite")
     eng.reset(0, 0)
     ev = Events(eng.stream)
     ev.start()

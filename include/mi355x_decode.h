@@ -32,6 +32,10 @@ extern "C" {
 /* The device status word's value after a fused launch's hand-off wait timed out
  * (mi_gemv_epilogue.status; the engine's control block word MI_CTRL_DEBUG). */
 #define MI_STATUS_HANDOFF_TIMEOUT 0xDEAD0003u
+/* The control block's MI_CTRL_DEBUG word after a step produced a logit that is not finite (an
+ * activation left the fp16 range): the argmax kernels set it when the word was 0, and the
+ * step's token is not to be used. */
+#define MI_STATUS_NONFINITE 0xDEAD0004u
 
 enum {
   MI_OK = 0,
@@ -499,7 +503,10 @@ enum {
   MI_T_MTP_FC_Q, MI_T_MTP_FC_S, MI_T_MTP_PRE_E, MI_T_MTP_PRE_H, MI_T_MTP_FINAL, MI_T_MTP_KV_K,
   MI_T_MTP_KV_V, MI_T_MTP_HH, MI_T_MTP_DH, MI_T_MTP_CTRL, MI_T_MTP_LOGITS,
   /* the int8 lm_head (lm_head_int8): its tiled int8 weight and fp32 row scales */
-  MI_T_LM_I8, MI_T_LM_I8_S
+  MI_T_LM_I8, MI_T_LM_I8_S,
+  /* MoE models: the hand-off words of mi_moe_down_norm [max_rows][hidden / 2] (0xFFFFFFFF
+   * between launches; emptied again by the engine after a step whose wait timed out) */
+  MI_T_MOE_HANDOFF
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's

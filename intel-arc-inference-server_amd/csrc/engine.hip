@@ -807,12 +807,22 @@ struct mi_engine {
   // MI_STATUS_HANDOFF_TIMEOUT in the debug word, and its hand-off words may hold values that
   // were published late. Those are emptied again here so the next step starts clean, and the
   // caller gets an error (the tokens of that call are not to be used). The word is cleared.
+  // A step whose logits were not finite (MI_STATUS_NONFINITE from the argmax) fails the call
+  // the same way.
   int check_handoff() {
     uint32_t c[MI_CTRL_WORDS];
     MI_TRY(read_ctrl(c));
+    if (c[MI_CTRL_DEBUG] == MI_STATUS_NONFINITE) {  // an activation left the fp16 range
+      ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
+      MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
+      MI_TRY(mi_stream_sync(stream));
+      return mi_fail(MI_ERR_STATE, "a logit of the step was not finite (an activation left the fp16 range); "
+                                   "the step's token is not to be used");
+    }
     if (c[MI_CTRL_DEBUG] != MI_STATUS_HANDOFF_TIMEOUT) return 0;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
+    if (dn_words) MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(d.max_rows) * (d.hidden / 2), stream));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
     if (step) MI_TRY(mi::step_plan_reset(step, stream));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
@@ -1070,6 +1080,7 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_MTP_LOGITS: *ptr = e->hlogits; b = size_t(m.vocab) * 4; break;
     case MI_T_LM_I8: *ptr = e->lm_i8; b = e->lm_i8 ? size_t(m.vocab) * m.hidden : 0; break;
     case MI_T_LM_I8_S: *ptr = e->lm_i8s; b = e->lm_i8s ? size_t(m.vocab) * 4 : 0; break;
+    case MI_T_MOE_HANDOFF: *ptr = e->dn_words; b = e->dn_words ? size_t(m.max_rows) * (m.hidden / 2) * 4 : 0; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;
@@ -1145,7 +1156,8 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
 
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk) {
   if (!e) return mi_fail(MI_ERR_ARG, "engine_prefill: null");
-  return e->prefill(ids, n, chunk);
+  MI_TRY(e->prefill(ids, n, chunk));
+  return e->check_handoff();  // the last position's logits: a non-finite one fails the call
 }
 
 int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs) {

@@ -573,8 +573,10 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
             bi = oi;
           }
         }
+        // a tile with a non-finite logit reports a NaN value, which argmax_stage2 flags
+        const bool bad = __ballot(n < epi.vocab_used && !__builtin_isfinite(v)) != 0ull;
         if (lane == 0)
-          epi.argmax_part[(size_t)row * ntiles + tile] = u2_t{__builtin_bit_cast(uint32_t, bv), bi};
+          epi.argmax_part[(size_t)row * ntiles + tile] = u2_t{bad ? kNanBits : __builtin_bit_cast(uint32_t, bv), bi};
       }
     }
   }

@@ -33,6 +33,8 @@ enum : uint32_t {
   CTRL_STEPS = 19,     // steps completed since the last reset (history index)
   CTRL_WORDS = 64
 };
+constexpr uint32_t kStatusNonFinite = 0xDEAD0004u;  // CTRL_DEBUG: a logit was not finite
+constexpr uint32_t kNanBits = 0x7FC00000u;          // the canonical fp32 NaN
 
 // threadIdx.x as a value the compiler cannot hoist: inside a loop over work-items of different
 // kinds (the persistent step), lane-derived addresses are then recomputed per item instead of

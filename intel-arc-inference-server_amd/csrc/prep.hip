@@ -456,15 +456,19 @@ __global__ __launch_bounds__(256) void argmax_stage1_kernel(const uint32_t* __re
   const float* row = logits + (size_t)m * vocab;
   float bv = -INFINITY;
   uint32_t bi = kNoIdx;
+  bool bad = false;  // a used logit that is not finite
   for (uint32_t k = k0 + lid; k < k1; k += kWG) {
     const float v = k < vocab_used ? row[k] : -INFINITY;
+    bad |= k < vocab_used && !__builtin_isfinite(v);
     if (better(v, k, bv, bi)) {
       bv = v;
       bi = k;
     }
   }
   argtree(bv, bi, sv, si);
-  if (lid == 0) part[(size_t)m * groups + g] = u2_t{__builtin_bit_cast(uint32_t, bv), bi};
+  bad = __syncthreads_or(bad);
+  // a chunk with a non-finite logit reports a NaN value, which stage 2 flags
+  if (lid == 0) part[(size_t)m * groups + g] = u2_t{bad ? kNanBits : __builtin_bit_cast(uint32_t, bv), bi};
 }
 
 // one work-group: fold each active row's chunk winners, write out_token[m], then
@@ -477,12 +481,14 @@ __global__ __launch_bounds__(256) void argmax_stage2_kernel(uint32_t* __restrict
   __shared__ uint32_t si[kWG];
   const uint32_t lid = threadIdx.x;
   const uint32_t n = ctrl[CTRL_NACT];
+  bool bad = false;  // a chunk winner is NaN: the chunk held a non-finite logit
   for (uint32_t m = 0; m < n; ++m) {
     float bv = -INFINITY;
     uint32_t bi = kNoIdx;
     for (uint32_t g = lid; g < groups; g += kWG) {
       const u2_t e = part[(size_t)m * groups + g];
       const float v = __builtin_bit_cast(float, e.x);
+      bad |= v != v;
       if (better(v, e.y, bv, bi)) {
         bv = v;
         bi = e.y;
@@ -491,6 +497,8 @@ __global__ __launch_bounds__(256) void argmax_stage2_kernel(uint32_t* __restrict
     argtree(bv, bi, sv, si);
     if (lid == 0) ctrl[CTRL_OUT + m] = bi;
   }
+  bad = __syncthreads_or(bad);
+  if (lid == 0 && bad && ctrl[CTRL_DEBUG] == 0u) ctrl[CTRL_DEBUG] = kStatusNonFinite;
   if (lid == 0 && n != 0u) {
     const uint32_t tok = ctrl[CTRL_OUT + n - 1u];
     ctrl[CTRL_CUR] = tok;

@@ -43,6 +43,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <memory>
+#include <cstdio>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -373,8 +374,9 @@ __device__ __forceinline__ void slice_item(const Stage& st, uint32_t i, const Sl
           bi = oi;
         }
       }
+      const bool bad = __ballot(n < st.vocab_used && !__builtin_isfinite(lv)) != 0ull;
       if (lane == 0) {
-        st_agent(st.am + 2u * tile, __builtin_bit_cast(uint32_t, publishable(bv)));
+        st_agent(st.am + 2u * tile, bad ? kNanBits : __builtin_bit_cast(uint32_t, publishable(bv)));
         st_agent(st.am + 2u * tile + 1u, bi);
       }
     }
@@ -606,6 +608,7 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
   const uint32_t groups = st.count ? st.tiles : 0u;  // the head GEMV's tiles
   float bv = -INFINITY;
   uint32_t bi = 0x7FFFFFFFu;
+  bool bad = false;  // a tile winner is NaN: the tile held a non-finite logit
   for (uint32_t g0 = 0; g0 < groups; g0 += 2048u) {
     const uint32_t ng = min(2048u, groups - g0);
     poll_lds_n(wt, st.am + 2u * g0, 2u * ng, t * 4u, 1024u, L.words, true);
@@ -613,6 +616,7 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
     for (uint32_t g = t; g < ng; g += 256u) {
       const float v = __builtin_bit_cast(float, L.words[2u * g]);
       const uint32_t ix = L.words[2u * g + 1u];
+      bad |= v != v;
       if ((v > bv) || (v == bv && ix < bi)) {
         bv = v;
         bi = ix;
@@ -637,6 +641,8 @@ __device__ __forceinline__ void finish_item(const StepArgs& a, const Stage& st, 
     }
     lds_barrier();
   }
+  bad = __syncthreads_or(bad);
+  if (t == 0 && bad && a.ctrl[CTRL_DEBUG] == 0u) a.ctrl[CTRL_DEBUG] = kStatusNonFinite;
   if (t == 0) {
     const uint32_t tok = si[0];
     a.ctrl[CTRL_OUT] = tok;
@@ -1021,6 +1027,9 @@ int step_plan_create(const StepModel& m, hipStream_t st, StepPlan** out) {
   if (std::getenv("MI_STEP_TRACE")) {  // diagnostics: item start/end times, [items][2] u32
     if (hipMalloc(&p->trace, (size_t)ufirst * 8) != hipSuccess) return mi_fail(MI_ERR_OOM, "step: trace");
     a.trace = p->trace;
+    for (const Stage& x : S)  // the unit ranges the trace is read against
+      std::fprintf(stderr, "step-stage kind %u epi %u ufirst %u units %u prod_units %u\n", x.kind, x.epi, x.ufirst,
+                   x.units, x.prod_units);
   }
   if (const char* env = std::getenv("MI_STEP_STOP")) {  // diagnostics: only the first n stages run
     const long n = std::strtol(env, nullptr, 10);

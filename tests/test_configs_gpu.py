@@ -46,7 +46,7 @@ def test_cfg2_full_27b_step_vs_oracle(eng27):
     err = np.abs(got.astype(np.float64) - want)
     print(f"27B step: max err / max logit {err.max() / np.abs(want).max():.3e}, argmax {got_tok} vs {am}",
           flush=True)
-    assert close(got, want)
+    assert close(got, want, abs_frac=5e-4, rel_big=2e-3)
     assert argmax_ok(got_tok, want)
     c = eng27.ctrl()
     assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_DEBUG] == 0
@@ -68,10 +68,20 @@ def test_cfg2_27b_verify_rows_bitwise_plain_steps(eng27, k):
     for m in range(k + 1):
         assert np.array_equal(got[m].view(np.uint32), lg[m].view(np.uint32)), m
     # a draft list with one wrong token: accept stops there and takes that row's argmax
+    # (the synthetic 27B model's fp16 residual overflows on some inputs, which the step flags and
+    # verify refuses: the wrong token is the first of toks[1] + 1, + 2, ... whose rows stay finite)
     bad = list(toks[:k])
-    bad[1] = (bad[1] + 1) % 151936
-    eng27.reset(P, t0)
-    rows = eng27.verify(bad)
+    for d in range(1, 9):
+        bad[1] = (toks[1] + d) % 151936
+        eng27.reset(P, t0)
+        try:
+            rows = eng27.verify(bad)
+            break
+        except mi.MiError as e:
+            assert "not finite" in str(e)
+            print(f"wrong token {bad[1]}: a row left the fp16 range, next", flush=True)
+    else:
+        pytest.fail("no finite wrong-token list in 8 tries")
     j, nxt = mi.accept_greedy(rows, bad)
     assert (j, nxt) == (1, toks[1]) and O.accept_greedy(rows, bad) == (j, nxt)
     eng27.commit(P, j, nxt)
@@ -147,3 +157,27 @@ def test_cfg3_131072_int8_paged():
                              O._p(want[i]))
     got = a[0].reshape(QH, HD)
     check_close(got[heads], want)
+
+
+def test_cfg4_full_moe_step_vs_oracle():
+    """BASELINE configs[3] at full size: the captured 40-layer MoE step (router GEMV, gate||up
+    with the routing in its prologue, down with the next norm, attention 16 / 2 heads of 256)
+    against the oracle's MoE step (moe_ref.h:144-152, 190-304) on the same weights and cache."""
+    print("cfg4: building the 40-layer MoE engine", flush=True)
+    eng = mi.Engine(mi.desc_moe_cfg4(max_len=4160), seed=1235)
+    eng.capture(1)
+    pos, tok = 4096, 1000
+    print("cfg4: oracle copies of the weights", flush=True)
+    orc = OracleModel(eng)
+    eng.reset(pos, tok)
+    got_tok = int(eng.generate(1)[0])
+    got = eng.logits(1)[0]
+    print("cfg4: the oracle's 40-layer step", flush=True)
+    am, want = orc.step(tok, pos)
+    print(f"cfg4 step: argmax {got_tok} vs {am}", flush=True)
+    assert close(got, want, abs_frac=5e-4, rel_big=2e-3)
+    assert argmax_ok(got_tok, want)
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_DEBUG] == 0
+    del orc
+    eng.close()

@@ -104,9 +104,22 @@ class OracleModel:
         return am, logits
 
 
-def close(got, want):
+def close(got, want, rel=2e-3, abs_frac=2e-3, rel_big=None):
+    """Logits against the oracle: every logit within rel * |want| + abs_frac * max|want|, and,
+    with rel_big, within rel_big * |want| element-wise on every logit of at least 5 % of the
+    largest. The two paths round the fp16 activations differently (the GEMV twins' summation
+    order differs from the MFMA order), so a small model's logits carry single-ulp flips of
+    its few activations: measured up to 4.5e-4 of max|want| there (the decode tests' bar 1e-3), and
+    5e-5 at the full 27B shape (bar 5e-4 there). The margins are printed."""
+    want = np.asarray(want, np.float64)
     err = np.abs(got.astype(np.float64) - want)
-    return np.all(err <= 2e-3 * np.abs(want) + 2e-3 * np.abs(want).max())
+    mx = np.abs(want).max()
+    big = np.abs(want) >= 0.05 * mx
+    rb = float((err[big] / np.abs(want[big])).max())
+    print(f"close: max err {err.max() / mx:.3e} of max|want| (bar {abs_frac}), max rel err {rb:.3e} on "
+          f"{int(big.sum())} logits >= 5% of max" + (f" (bar {rel_big})" if rel_big else ""), flush=True)
+    ok = bool(np.all(err <= rel * np.abs(want) + abs_frac * mx))
+    return ok and (rel_big is None or rb <= rel_big)
 
 
 def argmax_ok(gpu_tok, want_logits):
@@ -130,7 +143,7 @@ def test_decode_steps_vs_oracle_teacher_forced(qk_norm, lm8):
         got_tok = int(eng.generate(1)[0])
         got = eng.logits(1)[0]
         am, want = orc.step(tok, pos)
-        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert close(got, want, abs_frac=1e-3), f"step {step}: max err {np.abs(got - want).max()}"
         assert argmax_ok(got_tok, want)
         c = eng.ctrl()
         assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_CUR] == got_tok and c[mi.CTRL_OUT] == got_tok
@@ -159,7 +172,7 @@ def test_moe_decode_steps_vs_oracle(top_k):
         got_tok = int(eng.generate(1)[0])
         got = eng.logits(1)[0]
         am, want = orc.step(tok, pos)
-        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert close(got, want, abs_frac=1e-3), f"step {step}: max err {np.abs(got - want).max()}"
         assert argmax_ok(got_tok, want)
         assert eng.ctrl()[mi.CTRL_DEBUG] == 0
         tok, pos = got_tok, pos + 1
@@ -262,7 +275,7 @@ def test_int8_kv_decode_steps_vs_oracle(moe):
         got_tok = int(eng.generate(1)[0])
         got = eng.logits(1)[0]
         am, want = orc.step(tok, pos)
-        assert close(got, want), f"step {step}: max err {np.abs(got - want).max()}"
+        assert close(got, want, abs_frac=1e-3), f"step {step}: max err {np.abs(got - want).max()}"
         assert argmax_ok(got_tok, want)
         tok, pos = got_tok, pos + 1
     # the cache: rows the steps did not write unchanged; the written rows (from the device
@@ -302,4 +315,54 @@ def test_int8_kv_verify_rows_bitwise_plain_steps():
     got = eng.logits(3)
     for m in range(3):
         assert np.array_equal(got[m].view(np.uint32), lg[m].view(np.uint32))
+    eng.close()
+
+
+def test_moe_handoff_recovery_empties_down_norm_words():
+    """Engine::check_handoff after a timed-out wait on a MoE model: the down + norm launch's
+    hand-off words may hold a value a late down work-group published after its norm row gave up.
+    Forced from the host (stale full words, the timeout code in the debug word): the call fails,
+    every word reads empty afterwards and the next step is bitwise a clean engine's."""
+    eng = mi.Engine(moe_small_desc(), seed=21)
+    eng.capture(1)
+    P, t0 = 40, 9
+    eng.reset(P, t0)
+    want_tok = eng.generate(2)
+    want_lg = eng.logits(1)[0].copy()
+    words = eng.to_host(mi.T_MOE_HANDOFF, dtype=np.uint32)
+    assert words.size and np.all(words == 0xFFFFFFFF)
+    eng.from_host(mi.T_MOE_HANDOFF, np.full_like(words, 0x3C003C00))  # (1.0, 1.0): a full word
+    eng.reset(P, t0)
+    c = eng.ctrl()
+    c[mi.CTRL_DEBUG] = 0xDEAD0003
+    eng.from_host(mi.T_CTRL, c)
+    with pytest.raises(mi.MiError):
+        eng.generate(1)
+    assert np.all(eng.to_host(mi.T_MOE_HANDOFF, dtype=np.uint32) == 0xFFFFFFFF)
+    assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+    eng.reset(P, t0)
+    got = eng.generate(2)
+    assert np.array_equal(got, want_tok)
+    assert np.array_equal(eng.logits(1)[0].view(np.uint32), want_lg.view(np.uint32))
+    eng.close()
+
+
+@pytest.mark.parametrize("lm8", [0, 1])
+def test_nonfinite_logits_fail_the_call(lm8):
+    """A step whose activations leave the fp16 range (forced here with a final-norm weight of
+    1e30, so x is inf) sets MI_STATUS_NONFINITE from the argmax and the call fails; the word is
+    cleared and the engine steps normally once the weights are finite again."""
+    eng = mi.Engine(small_desc(lm_head_int8=lm8), seed=5)
+    eng.capture(1)
+    good = eng.to_host(mi.T_FINAL_NORM, dtype=np.float32).copy()
+    eng.reset(20, 3)
+    want = eng.generate(1)
+    eng.from_host(mi.T_FINAL_NORM, np.full_like(good, 1e30))
+    eng.reset(20, 3)
+    with pytest.raises(mi.MiError, match="not finite"):
+        eng.generate(1)
+    assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+    eng.from_host(mi.T_FINAL_NORM, good)
+    eng.reset(20, 3)
+    assert np.array_equal(eng.generate(1), want)
     eng.close()
