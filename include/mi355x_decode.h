@@ -84,6 +84,10 @@ int mi_fill_i8(int8_t* p, size_t n, uint64_t seed, int lo, int hi, void* stream)
 /* `tiles` int4 g64 layout-1 tiles of 136 u32 (common/repack.h:17-30): random nibble words and
  * fp16 scales uniform in [lo, hi) (synthetic expert weights) */
 int mi_fill_layout1(uint32_t* p, size_t tiles, uint64_t seed, float lo, float hi, void* stream);
+/* In place over n f16 values: mode 1 = to bf16 bits (round to nearest even, common/bf16.h:12-16);
+ * mode 2 = to the f16 encoding of that bf16 value (the bf16 activation mode's storage of the
+ * activations and the KV cache, mi_gemv_epilogue.act). */
+int mi_f16_to_bf16(uint16_t* p, size_t n, uint32_t mode, void* stream);
 
 /* ---- int4 GPTQ g64 unpack: replaces common::Int4Gptq::at (src/common/int4.h:19-23) as
  * a device pass; out[k][n] = (q - 8) * scale, fp32, exact ---- */
@@ -163,6 +167,13 @@ typedef struct mi_gemv_epilogue {
   uint32_t poll_limit;
   uint32_t inject;
   uint32_t* arrive;
+  /* The activation type (the reference's is bf16, common/bf16.h:8-43): 0 = f16 (every rounding
+   * above is rne_f16 and resid is f16). 1 = bf16: every rounding point rounds to bf16 instead
+   * (rne_bf16 where the reference has it); resid holds bf16 bits; x, x_next, h, out16 and the
+   * QKV kind's K/V rows hold the f16 encoding of bf16 values (exact for magnitudes in
+   * [2^-17, 65504]; a larger value is stored as inf, which the logits' finiteness check
+   * reports). The linears read those activations as they are. */
+  uint32_t act;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,
@@ -230,6 +241,10 @@ typedef struct mi_attn_shape {
   uint32_t qkv_n, k_off, v_off;
   float scale; /* score scale, fp32(1/sqrt(head_dim)) */
   float eps;   /* q/k RMSNorm epsilon */
+  /* the activation type, as mi_gemv_epilogue.act: 1 = bf16 roundings in attn_prep (q/k before
+   * and after the norm, the K/V rows as f16 encodings of bf16 values) and the reduce's output;
+   * the f16 cache kernels only (mi_attn_prep, mi_attn_decode, mi_attn_reduce) */
+  uint32_t act;
 } mi_attn_shape;
 
 /* attn_prep (attn.cl:361-372): fold the qkv partials [S][M][qkv_n], per-head q/k RMSNorm
@@ -323,6 +338,12 @@ int mi_argmax_finish(uint32_t* ctrl, const void* part, uint32_t groups, uint32_t
 int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w,
                   uint16_t* x_out, float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab,
                   float eps, void* stream);
+/* mi_embed_norm with the activation type act (mi_gemv_epilogue.act): 1 = the embedding table
+ * and resid hold bf16 bits, x the f16 encoding of the bf16-rounded norm (the reference's bf16
+ * embed_gather + prep_norm_finish, prep.cl:350-353). */
+int mi_embed_norm_act(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w,
+                      uint16_t* x_out, float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab, float eps,
+                      uint32_t act, void* stream);
 /* The norm of the residual as it stands, rows [M][hidden]: the sum of squares in 64-element
  * chunks added in chunk order, rstd = 1/sqrt(sum / hidden + eps), x = rne(r * rstd * w)
  * (prep_res_fold with S_PREV 0 then prep_norm_finish, prep.cl:288/350) - the norm after a
@@ -477,6 +498,13 @@ typedef struct mi_model_desc {
    * stages; a loaded checkpoint's 16-bit head is quantised at load (lm_head_int8.cc). 0: the
    * int4 g64 head. */
   uint32_t lm_head_int8;
+  /* 1: bf16 activations, the reference's own type (common/bf16.h:8-43): every rounding point
+   * of the step rounds to bf16, the embedding table and the residual stream hold bf16 bits, and
+   * the normed activations, the attention output, SwiGLU's output and the KV cache hold the f16
+   * encoding of bf16 values (mi_gemv_epilogue.act). The synthetic random-init 27B model's
+   * residual leaves the f16 range on some inputs; bf16's range holds it. Dense models with the
+   * f16-format cache, no MTP head; prefill refused (ingest). 0: f16 activations (BASELINE's). */
+  uint32_t act_bf16;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;

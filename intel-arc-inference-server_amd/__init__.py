@@ -36,6 +36,7 @@ SIGNATURES = {
     "mi_fill_f16": (i32, [vp, sz, u64, i32, f32, f32, vp]),
     "mi_fill_f32": (i32, [vp, sz, u64, i32, f32, f32, i32, vp]),
     "mi_fill_layout1": (i32, [vp, sz, u64, f32, f32, vp]),
+    "mi_f16_to_bf16": (i32, [vp, sz, u32, vp]),
     "mi_fill_i8": (i32, [vp, sz, u64, i32, i32, vp]),
     "mi_int4_dequant": (i32, [vp, vp, vp, u32, u32, vp]),
     "mi_gemv_w4a16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
@@ -64,6 +65,7 @@ SIGNATURES = {
     "mi_argmax_static": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
     "mi_argmax_finish": (i32, [vp, vp, u32, vp, u32, vp]),
     "mi_embed_norm": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, f32, vp]),
+    "mi_embed_norm_act": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, f32, u32, vp]),
     "mi_gemv_w4a16_ex": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp, vp]),
     "mi_engine_create": (vp, [vp, u64, vp]),
     "mi_checkpoint_desc": (i32, [C.c_char_p, u32, u32, vp]),
@@ -120,7 +122,7 @@ class GemvEpilogue(C.Structure):
                 ("ctrl", vp), ("shape", vp), ("q_norm", vp), ("k_norm", vp), ("rope", vp), ("attn_q", vp),
                 ("kv_k", vp), ("kv_v", vp), ("row_stride", sz), ("head_stride", sz), ("pages", vp),
                 ("page", u32), ("kv_len", u32), ("status", vp), ("poll_limit", u32), ("inject", u32),
-                ("arrive", vp)]
+                ("arrive", vp), ("act", u32)]
 
 
 STATUS_HANDOFF_TIMEOUT = 0xDEAD0003
@@ -176,7 +178,19 @@ class AttnShape(C.Structure):
     """mi_attn_shape: heads, head_dim, rotary dims, gate on/off, the fused qkv column map."""
     _fields_ = [("q_heads", u32), ("kv_heads", u32), ("head_dim", u32), ("rot_dim", u32),
                 ("gated", u32), ("qkv_n", u32), ("k_off", u32), ("v_off", u32), ("scale", f32),
-                ("eps", f32)]
+                ("eps", f32), ("act", u32)]
+
+
+def lib_shape(sh, act=0):
+    """An mi_attn_shape with the fields of `sh` (this package's AttnShape or the oracle's
+    orc_attn_shape, which has the same leading fields) and the activation type act."""
+    names = [f[0] for f in AttnShape._fields_ if f[0] != "act"]
+    return AttnShape(*[getattr(sh, n) for n in names], act)
+
+
+def shape_ref(sh, act=0):
+    """A pointer to lib_shape(sh, act), for the entries that take `const mi_attn_shape*`."""
+    return C.byref(lib_shape(sh, act))
 
 
 # ---- the decode loop (host-side mirror of src/runtime/engine.h) -------------------------
@@ -187,12 +201,12 @@ class ModelDesc(C.Structure):
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
                 ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
                 ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32),
-                ("mtp", u32), ("lm_head_int8", u32)]
+                ("mtp", u32), ("lm_head_int8", u32), ("act_bf16", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
                rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
-               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0, lm_head_int8=0):
+               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0, lm_head_int8=0, act_bf16=0):
     d = ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
                   head_dim if rot_dim is None else rot_dim, inter, vocab,
                   vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
@@ -200,6 +214,7 @@ def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_le
     d.kv_int8 = kv_int8
     d.mtp = mtp
     d.lm_head_int8 = lm_head_int8
+    d.act_bf16 = act_bf16
     return d
 
 
@@ -233,12 +248,12 @@ def desc_moe_cfg4(max_len=4096 + 512):
     return moe_desc(40, 2048, 16, 2, 256, 256, 8, 512, 151936, max_len)
 
 
-def desc_27b(max_len=4096 + 512):
+def desc_27b(max_len=4096 + 512, act_bf16=0):
     """the 27B-shape dense decoder (64 layers, hidden 5120, 40 q / 8 kv
     heads of 128, SwiGLU 17408, vocab 151936, RoPE theta 1e6). Attention blocks per kv head:
     64 (at context 4096, blocks of 128 positions: 8 x 33 work-groups, measured faster than
     128 blocks of 64 positions)."""
-    return dense_desc(64, 5120, 40, 8, 128, 17408, 151936, max_len, attn_tgt=64)
+    return dense_desc(64, 5120, 40, 8, 128, 17408, 151936, max_len, attn_tgt=64, act_bf16=act_bf16)
 
 
 # tensor kinds (mi_engine_tensor)

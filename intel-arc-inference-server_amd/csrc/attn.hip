@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
                                                           const float* __restrict__ attn_gate,
                                                           uint16_t* __restrict__ attn_out, uint32_t M,
                                                           uint32_t q_heads, uint32_t HD, uint32_t tgt,
-                                                          uint32_t gated, uint32_t kv_len) {
+                                                          uint32_t gated, uint32_t kv_len, uint32_t act) {
   __shared__ float fac[1024];
   __shared__ float s_sm;
   const uint32_t h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
     else
       r = f2h(o);
   } else {
-    r = merge_out(acc, s_sm, gated && attn_gate, gv);
+    r = merge_out(acc, s_sm, gated && attn_gate, gv, act);
   }
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
@@ -192,6 +192,7 @@ int mi_attn_prep_decode(uint32_t* ctrl, const float* partials, uint32_t S, uint3
   if (!ctrl || !partials || !shape || !rope || !kv_k || !kv_v || !attn_part || S == 0 || M == 0 || M > 8 ||
       tgt == 0)
     return mi_fail(MI_ERR_ARG, "attn_prep_decode: bad arguments (M <= 8)");
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: f16 activations only");
   const uint32_t HD = shape->head_dim;
   if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prep_decode: head_dim must be 128 or 256");
   const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
@@ -226,12 +227,13 @@ int mi_attn_reduce(const uint32_t* ctrl, const float* attn_part, const float* at
     return mi_fail(MI_ERR_ARG, "attn_reduce: bad arguments (tgt <= 1024)");
   const uint32_t HD = shape->head_dim;
   if (HD != 64 && HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_reduce: head_dim 64/128/256");
+  if (shape->act > 1) return mi_fail(MI_ERR_ARG, "attn_reduce: act is 0 (f16) or 1 (bf16)");
   if (tgt <= 64)
     attn_reduce_kernel<false, 64><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
-        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len, shape->act);
   else
     attn_reduce_kernel<false, 128><<<dim3(shape->q_heads, M), HD, 0, (hipStream_t)stream>>>(
-        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len);
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, HD, tgt, shape->gated, kv_len, shape->act);
   return mi_hip((int)hipGetLastError(), "attn_reduce");
 }
 
@@ -241,12 +243,13 @@ int mi_attn_reduce_kv8(const uint32_t* ctrl, const float* attn_part, const float
     return mi_fail(MI_ERR_ARG, "attn_reduce_kv8: bad arguments (tgt <= 1024)");
   if (shape->head_dim != 256)
     return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: the rotation is defined for head_dim 256 only");
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_reduce_kv8: f16 activations only");
   if (tgt <= 64)
     attn_reduce_kernel<true, 64><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
-        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len, 0u);
   else
     attn_reduce_kernel<true, 128><<<dim3(shape->q_heads, M), 256, 0, (hipStream_t)stream>>>(
-        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len);
+        ctrl, attn_part, attn_gate, attn_out, M, shape->q_heads, 256, tgt, shape->gated, kv_len, 0u);
   return mi_hip((int)hipGetLastError(), "attn_reduce_kv8");
 }
 

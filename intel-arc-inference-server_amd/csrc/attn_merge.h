@@ -40,10 +40,10 @@ __device__ __forceinline__ float merge_factors(uint32_t lane, uint32_t nb, MxOf 
   return wave_sum(sm);
 }
 
-// the merged value of one dim, rounded as attn_reduce writes it
-__device__ __forceinline__ uint16_t merge_out(float acc, float sm, bool gated, float gate) {
+// the merged value of one dim, rounded as attn_reduce writes it (act: mi_attn_shape.act)
+__device__ __forceinline__ uint16_t merge_out(float acc, float sm, bool gated, float gate, uint32_t act = 0u) {
   const float o = acc / sm;
-  return gated ? f2h(h2f(f2h(o)) * sigmoid_f32(gate)) : f2h(o);
+  return gated ? act_enc(act_round(o, act) * sigmoid_f32(gate), act) : act_enc(o, act);
 }
 
 }  // namespace mi

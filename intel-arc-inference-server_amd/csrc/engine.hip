@@ -224,7 +224,7 @@ struct mi_engine {
     const uint32_t R = m.max_rows;
     const uint32_t qkv_n = (QH + 2 * KVH) * HD;
     ash = mi_attn_shape{QH, KVH, HD, m.rot_dim, 0u, qkv_n, QH * HD, (QH + KVH) * HD,
-                        1.0f / std::sqrt(float(HD)), m.rms_eps};
+                        1.0f / std::sqrt(float(HD)), m.rms_eps, m.act_bf16};
     ash.scale = float(1.0 / std::sqrt(double(HD)));
     layer.resize(m.layers);
     size_t part_max = 0, part_ex_max = 1;
@@ -361,6 +361,7 @@ struct mi_engine {
       MI_TRY(init_linear(lm_head, seed));
     }
     MI_TRY(mi_fill_f16(embed, size_t(m.vocab) * H, seed++, 1, 0.0f, 1.0f, stream));
+    if (m.act_bf16) MI_TRY(mi_f16_to_bf16(embed, size_t(m.vocab) * H, 1, stream));  // the table in bf16
     MI_TRY(mi_fill_f32(final_norm, H, seed++, 1, 1.0f, 0.02f, 1, stream));
     if (m.kv_int8) {  // BASELINE config 3's int8 cache: uniform [-127, 127], scales U(0.005, 0.05)
       MI_TRY(mi_fill_i8(static_cast<int8_t*>(kv_k), kv_elems, seed++, -127, 127, stream));
@@ -370,6 +371,10 @@ struct mi_engine {
     } else {
       MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_k), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
       MI_TRY(mi_fill_f16(static_cast<uint16_t*>(kv_v), kv_elems, seed++, 1, 0.0f, 1.0f, stream));
+      if (m.act_bf16) {  // bf16 values, in the cache's f16 encoding
+        MI_TRY(mi_f16_to_bf16(static_cast<uint16_t*>(kv_k), kv_elems, 2, stream));
+        MI_TRY(mi_f16_to_bf16(static_cast<uint16_t*>(kv_v), kv_elems, 2, stream));
+      }
     }
     // the head last, so a model's own weights are the same with and without it
     if (m.mtp) {
@@ -432,6 +437,7 @@ struct mi_engine {
     e.eps = d.rms_eps;
     e.status = ctrl + MI_CTRL_DEBUG;
     e.arrive = use_arrive ? arrive : nullptr;
+    e.act = d.act_bf16;
     return e;
   }
 
@@ -447,7 +453,8 @@ struct mi_engine {
       mtp_fill_ctrl_kernel<<<1, 64, 0, stream>>>(ctrl, hctl, M);
       MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "mtp_fill_ctrl"));
     }
-    MI_TRY(mi_embed_norm(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps, stream));
+    MI_TRY(mi_embed_norm_act(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps,
+                             d.act_bf16, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
       MI_TRY(launch_qkv(li, M));
@@ -595,6 +602,7 @@ struct mi_engine {
     eq.kv_len = d.max_len;
     eq.status = ctrl + MI_CTRL_DEBUG;
     eq.arrive = use_arrive ? arrive : nullptr;
+    eq.act = d.act_bf16;
     return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream);
   }
   // the f16 cache's attention pair on control block c over the layer lk / lv: attn_prep first
@@ -626,6 +634,7 @@ struct mi_engine {
     eg.h = hbuf;
     eg.status = ctrl + MI_CTRL_DEBUG;
     eg.arrive = use_arrive ? arrive : nullptr;
+    eg.act = d.act_bf16;
     return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
                             stream);
   }
@@ -769,8 +778,9 @@ struct mi_engine {
       return 0;
     }
     if (!step) {
-      if (d.experts || d.kv_int8 || d.mtp || d.lm_head_int8)
-        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache and the int4 head only, no MTP head");
+      if (d.experts || d.kv_int8 || d.mtp || d.lm_head_int8 || d.act_bf16)
+        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache, f16 activations and the int4 "
+                                     "head only, no MTP head");
       std::vector<mi::StepLayerW> lw(d.layers);
       auto sl = [](const Linear& l) { return mi::StepLinear{l.q, l.s, l.K, l.N, l.S}; };
       for (uint32_t li = 0; li < d.layers; ++li) {
@@ -941,6 +951,7 @@ struct mi_engine {
 
   int prefill(const uint32_t* ids, uint32_t n, uint32_t chunk) {
     if (!ids || n == 0) return mi_fail(MI_ERR_ARG, "engine_prefill: no ids");
+    if (d.act_bf16) return mi_fail(MI_ERR_SHAPE, "engine_prefill: f16 activations only (ingest the prompt instead)");
     if (chunk == 0) chunk = std::min(kPrefillCap, d.max_len);
     if (chunk > kPrefillCap) return mi_fail(MI_ERR_ARG, "engine_prefill: chunk above the cap (2048)");
     for (uint32_t i = 0; i < n; ++i)
@@ -984,7 +995,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
-      m.mtp > 1 || m.lm_head_int8 > 1 ||
+      m.mtp > 1 || m.lm_head_int8 > 1 || m.act_bf16 > 1 || (m.act_bf16 && (m.experts || m.kv_int8 || m.mtp)) ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {
@@ -1015,6 +1026,7 @@ void mi_engine_destroy(mi_engine* e) { delete e; }
 void* mi_engine_stream(mi_engine* e) { return e ? e->stream : nullptr; }
 
 bool mi_engine_has_mtp(const mi_engine* e) { return e && e->d.mtp; }
+bool mi_engine_act_bf16(const mi_engine* e) { return e && e->d.act_bf16; }
 
 int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, size_t* bytes) {
   if (!e || !ptr) return mi_fail(MI_ERR_ARG, "engine_tensor: null");

@@ -112,6 +112,7 @@ struct GemvEpi {
   uint32_t extra_row;   // set by the launch: the fixed consumers are an extra grid row
   uint32_t* arrive;     // per-tile (QKV: per-head) arrival counts, zero between launches; NULL:
                         // the fixed consumers (slice S-1; QKV's extra row)
+  uint32_t act;         // 0: f16 activations; 1: bf16 (roundings to bf16, residual in bf16 bits)
 };
 
 // arrival words sit 128 bytes apart: no two tiles' counts share a cache line
@@ -271,12 +272,12 @@ __device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, 
   if (!is_q && !is_k) {
 #pragma unroll
     for (uint32_t k = 0; k < EPL; ++k)
-      epi.kv_v[crow * epi.row_stride + h * epi.head_stride + lane + 64u * k] = f2h(fr[lane + 64u * k]);
+      epi.kv_v[crow * epi.row_stride + h * epi.head_stride + lane + 64u * k] = act_enc(fr[lane + 64u * k], epi.act);
     return;
   }
   float xf[EPL], nv[EPL];
 #pragma unroll
-  for (uint32_t k = 0; k < EPL; ++k) xf[k] = h2f(f2h(fr[lane + 64u * k]));
+  for (uint32_t k = 0; k < EPL; ++k) xf[k] = act_round(fr[lane + 64u * k], epi.act);
   if (nw) {
     // tree_hd's order: the LDS steps (v[i] + v[i + st], st >= 64) are this lane's own
     // elements, then the 64-lane shuffle tree; lane 0's total is broadcast
@@ -291,7 +292,7 @@ __device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, 
     const float tot = __shfl(acc, 0, 64);
     const float rstd = 1.0f / sqrtf(tot / (float)HD + epi.qk_eps);
 #pragma unroll
-    for (uint32_t k = 0; k < EPL; ++k) nv[k] = h2f(f2h(xf[k] * rstd * wn[k]));
+    for (uint32_t k = 0; k < EPL; ++k) nv[k] = act_round(xf[k] * rstd * wn[k], epi.act);
   } else {
 #pragma unroll
     for (uint32_t k = 0; k < EPL; ++k) nv[k] = xf[k];
@@ -316,7 +317,7 @@ __device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, 
     if (is_q)
       epi.attn_q[((size_t)m * QH + h) * HD + e] = out;
     else
-      epi.kv_k[crow * epi.row_stride + h * epi.head_stride + e] = f2h(out);
+      epi.kv_k[crow * epi.row_stride + h * epi.head_stride + e] = act_enc(out, epi.act);
   }
 }
 
@@ -512,9 +513,9 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     for (int k = 0; k < (MR + kWaves - 1) / kWaves; ++k) {
       const uint32_t row = wave + kWaves * k;
       if (row >= M) break;
-      const uint16_t rb = f2h(h2f(r_pre[k]) + h2f(f2h(folded(row, lane))));
+      const uint16_t rb = res_rne(res_widen(r_pre[k], epi.act) + act_round(folded(row, lane), epi.act), epi.act);
       epi.resid[(size_t)row * N + n0 + lane] = rb;
-      const float v = h2f(rb);
+      const float v = res_widen(rb, epi.act);
       red[1][row][lane] = v;
       float a = __builtin_fmaf(v, v, 0.f);
 #pragma unroll
@@ -541,7 +542,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     }
     for (uint32_t row = wave; row < M; row += kWaves) {
       const uint32_t n = n0 + lane;
-      epi.x_next[(size_t)row * N + n] = f2h(red[1][row][lane] * s_rstd[row] * w_pre);
+      epi.x_next[(size_t)row * N + n] = act_enc(red[1][row][lane] * s_rstd[row] * w_pre, epi.act);
     }
     if (tile == 0 && t < M) epi.rstd[t] = s_rstd[t];
   } else if constexpr (EPI == EPI_SILU) {
@@ -549,13 +550,13 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     for (uint32_t i = t; i < 32u * M; i += 256u) {
       const uint32_t row = i / 32u, kk = i % 32u, k = tile * 32u + kk;
       const uint32_t gcol = (kk / 16u) * 32u + (kk % 16u);
-      const uint16_t g_b = f2h(folded(row, gcol)), u_b = f2h(folded(row, gcol + 16u));
-      const uint16_t s_b = f2h(silu_f32(h2f(g_b)));
-      epi.h[(size_t)row * (N / 2) + k] = f2h(h2f(s_b) * h2f(u_b));
+      const float g_r = act_round(folded(row, gcol), epi.act), u_r = act_round(folded(row, gcol + 16u), epi.act);
+      const float s_r = act_round(silu_f32(g_r), epi.act);
+      epi.h[(size_t)row * (N / 2) + k] = act_enc(s_r * u_r, epi.act);
     }
   } else if constexpr (EPI == EPI_F16OUT) {
     for (uint32_t i = t; i < total; i += 256u)
-      epi.out16[(size_t)(i / kCols) * N + n0 + i % kCols] = f2h(folded(i / kCols, i % kCols));
+      epi.out16[(size_t)(i / kCols) * N + n0 + i % kCols] = act_enc(folded(i / kCols, i % kCols), epi.act);
   } else if constexpr (EPI == EPI_LOGITS) {
     for (uint32_t row = wave; row < M; row += kWaves) {
       const uint32_t n = n0 + lane;
@@ -695,6 +696,8 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   e.poll_limit = ep->poll_limit ? ep->poll_limit : kPollLimit;
   e.inject = ep->inject;
   e.arrive = ep->arrive;
+  if (ep->act > 1) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: act is 0 (f16) or 1 (bf16)");
+  e.act = ep->act;
   int r;
   switch (ep->kind) {
     case MI_EPI_PARTIALS:
@@ -733,6 +736,7 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
         return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: N must be the q||k||v width of the shape");
       if (sh->rot_dim > HD || sh->rot_dim % 2) return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex QKV: bad rot_dim");
       if (ep->pages && ep->page == 0) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex QKV: page size 0");
+      if (sh->act != ep->act) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex QKV: the shape's act differs from the epilogue's");
       e.ctrl = ep->ctrl; e.rope = ep->rope; e.q_norm = ep->q_norm; e.k_norm = ep->k_norm;
       e.attn_q = ep->attn_q; e.kv_k = ep->kv_k; e.kv_v = ep->kv_v; e.pages = ep->pages;
       e.row_stride = ep->row_stride; e.head_stride = ep->head_stride; e.page = ep->page; e.kv_len = ep->kv_len;

@@ -667,7 +667,16 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   std::vector<uint16_t> scat;
   // embeddings
   if (!get_float(ck, pre + "embed_tokens.weight", size_t(V) * H, f32)) return fail_ck(ck);
-  if (!to_f16(ck, "embed_tokens", f32, f16)) return fail_ck(ck);
+  if (mi_engine_act_bf16(e)) {  // bf16 activations: the table in bf16 (common/bf16.h:12-16's rounding)
+    f16.resize(f32.size());
+    for (size_t i = 0; i < f32.size(); ++i) {
+      uint32_t u;
+      std::memcpy(&u, &f32[i], 4);
+      f16[i] = uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    }
+  } else if (!to_f16(ck, "embed_tokens", f32, f16)) {
+    return fail_ck(ck);
+  }
   f16.resize(size_t(Vp) * H, 0);
   if (int rc = upload(MI_T_EMBED, 0, f16.data(), f16.size() * 2, "embed_tokens")) return rc;
   if (!get_float(ck, pre + "norm.weight", H, f32)) return fail_ck(ck);

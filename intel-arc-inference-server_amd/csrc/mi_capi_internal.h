@@ -10,3 +10,5 @@ int mi_fail(int code, const char* msg);
 int mi_hip(int e, const char* where);
 // Whether the engine was created with an MTP head (its descriptor's mtp); for the loader.
 extern "C" bool mi_engine_has_mtp(const mi_engine* e);
+// Whether the engine runs bf16 activations (its descriptor's act_bf16); for the loader.
+extern "C" bool mi_engine_act_bf16(const mi_engine* e);

@@ -53,6 +53,28 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   asm("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, (half_t)f);
 }
+// bf16, the reference's activation type (common/bf16.h:8-16): widening is exact, narrowing is
+// round-to-nearest-even on the fp32 bits. A NaN stays a NaN (the bit formula alone can carry a
+// NaN with a full payload into a zero; finite values and infinities round as the formula says).
+__device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  asm("" : "+v"(f));
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if (f != f) return (uint16_t)0x7FC0u;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+// The activation type of a step: act 0 = f16, 1 = bf16. Under bf16 every rounding point of the
+// step rounds to bf16 (rne_bf16 where the reference has it), and the activations that feed a
+// linear or the attention (the normed x, SwiGLU's h, the attention output, the K/V rows) are
+// stored as the f16 encoding of that bf16 value: a bf16 value of magnitude in [2^-17, 65504]
+// is exact in f16 (8 significant bits), so the GEMV and attention kernels read the same
+// numbers either way; a larger one is stored as inf, which the logits' finiteness check then
+// reports. The residual stream, which grows past the f16 range, is stored as bf16 bits.
+__device__ __forceinline__ float act_round(float f, uint32_t act) { return act ? bf2f(f2bf(f)) : h2f(f2h(f)); }
+__device__ __forceinline__ uint16_t act_enc(float f, uint32_t act) { return act ? f2h(bf2f(f2bf(f))) : f2h(f); }
+__device__ __forceinline__ float res_widen(uint16_t b, uint32_t act) { return act ? bf2f(b) : h2f(b); }
+__device__ __forceinline__ uint16_t res_rne(float f, uint32_t act) { return act ? f2bf(f) : f2h(f); }
+
 __device__ __forceinline__ h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 

@@ -918,6 +918,7 @@ int mi_attn_prefill(const float* attn_q, const uint16_t* kv_k, const uint16_t* k
                     const mi_attn_shape* shape, uint16_t* attn_out, void* stream) {
   if (!attn_q || !kv_k || !kv_v || !attn_out || !shape || T == 0)
     return mi_fail(MI_ERR_ARG, "attn_prefill: bad arguments");
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_prefill: f16 activations only");
   const uint32_t HD = shape->head_dim;
   if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prefill: head_dim must be 128 or 256");
   const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
@@ -942,6 +943,7 @@ int mi_attn_prefill_kv8(const float* attn_q, const int8_t* kv_k, const int8_t* k
                         const mi_attn_shape* shape, float* out_rot, uint16_t* attn_out, void* stream) {
   if (!attn_q || !kv_k || !kv_v || !k_scale || !v_scale || !out_rot || !attn_out || !shape || T == 0)
     return mi_fail(MI_ERR_ARG, "attn_prefill_kv8: bad arguments");
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_prefill_kv8: f16 activations only");
   if (shape->head_dim != 256) return mi_fail(MI_ERR_SHAPE, "attn_prefill_kv8: the rotation is defined for head_dim 256");
   const uint32_t gqa = shape->kv_heads ? shape->q_heads / shape->kv_heads : 0;
   if (shape->kv_heads == 0 || shape->q_heads % shape->kv_heads ||
@@ -966,6 +968,7 @@ int mi_attn_prep_rows(const float* qkv, uint32_t T, uint32_t pos0, const mi_attn
                       size_t row_stride, size_t head_stride, const uint32_t* pages, uint32_t page, void* stream) {
   if (!qkv || !shape || !rope || !attn_q || !kv_k || !kv_v || T == 0)
     return mi_fail(MI_ERR_ARG, "attn_prep_rows: bad arguments");
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_prep_rows: f16 activations only");
   const uint32_t HD = shape->head_dim;
   if (HD != 128 && HD != 256) return mi_fail(MI_ERR_SHAPE, "attn_prep_rows: head_dim must be 128 or 256");
   if (shape->gated || shape->kv_heads == 0 || shape->k_off != shape->q_heads * HD ||

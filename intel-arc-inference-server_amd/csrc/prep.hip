@@ -176,6 +176,7 @@ struct AttnPrepArgs {
   uint16_t* k_scale;
   uint16_t* v_scale;
   size_t sc_row_stride, sc_head_stride;
+  uint32_t act;  // 0 f16, 1 bf16 roundings (the f16 cache only)
 };
 
 __device__ __forceinline__ size_t kv_row(uint32_t p, const uint32_t* pages, uint32_t page) {
@@ -234,12 +235,12 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   float vg = 0.f;
   if (!is_q) vg = qkv_sum((size_t)a.v_off + (size_t)h * HD + i);
   else if (a.gated && a.attn_gate) vg = qkv_sum(base + HD + i);
-  const float xf = h2f(f2h(qkv_sum(base + i)));
+  const float xf = act_round(qkv_sum(base + i), a.act);
   float nv;
   if (nw) {
     const float tot = tree_hd(xf * xf, red, HD);
     const float rstd = 1.0f / sqrtf(tot / (float)HD + a.eps);
-    nv = h2f(f2h(xf * rstd * wn));
+    nv = act_round(xf * rstd * wn, a.act);
   } else {
     nv = xf;
   }
@@ -289,10 +290,10 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
   } else {
     if (is_q) {
       a.attn_q[((size_t)m * a.q_heads + h) * HD + i] = outv;
-      if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = h2f(f2h(vg));
+      if (a.gated && a.attn_gate) a.attn_gate[((size_t)m * a.q_heads + h) * HD + i] = act_round(vg, a.act);
     } else {
-      a.kv_k[row * a.row_stride + h * a.head_stride + i] = f2h(outv);
-      a.kv_v[row * a.row_stride + h * a.head_stride + i] = f2h(vg);
+      a.kv_k[row * a.row_stride + h * a.head_stride + i] = act_enc(outv, a.act);
+      a.kv_v[row * a.row_stride + h * a.head_stride + i] = act_enc(vg, a.act);
     }
   }
 }
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
                                                          const float* __restrict__ norm_w,
                                                          uint16_t* __restrict__ x_out,
                                                          float* __restrict__ rstd_out, uint32_t hidden,
-                                                         uint32_t vocab, float eps) {
+                                                         uint32_t vocab, float eps, uint32_t act) {
   __shared__ float chunk[1024];
   // rows up to kHeld * 64 wide stay in registers between the two passes (with their norm weights,
   // loaded alongside), so a row takes one memory round trip; wider rows are read again
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
       const uint32_t c = c0 + 4 * u;
       if (c < nch) {
         if constexpr (GATHER) dst[c * 64 + lane] = v16[u];
-        const float v = h2f(v16[u]);
+        const float v = res_widen(v16[u], act);
         float a = __builtin_fmaf(v, v, 0.f);
 #pragma unroll
         for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
 #pragma unroll
       for (uint32_t u = 0; u < kPass; ++u) {
         const uint32_t c = wave + 4u * (kPass * it + u);
-        if (c < nch) x_out[(size_t)m * hidden + c * 64 + lane] = f2h(h2f(hv[it][u]) * r * hw[it][u]);
+        if (c < nch) x_out[(size_t)m * hidden + c * 64 + lane] = act_enc(res_widen(hv[it][u], act) * r * hw[it][u], act);
       }
     return;
   }
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(uint32_t* __restrict__ 
 #pragma unroll
     for (uint32_t u = 0; u < 8; ++u) {
       const uint32_t k = k0 + u * kWG;
-      if (k < hidden) x_out[(size_t)m * hidden + k] = f2h(h2f(v16[u]) * r * norm_w[k]);
+      if (k < hidden) x_out[(size_t)m * hidden + k] = act_enc(res_widen(v16[u], act) * r * norm_w[k], act);
     }
   }
 }
@@ -578,7 +579,8 @@ int mi_attn_prep(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t M,
   AttnPrepArgs a{ctrl, partials, q_norm, k_norm, rope, attn_q, attn_gate, kv_k, kv_v, pages, row_stride,
                  head_stride, page, S, M, shape->q_heads, shape->kv_heads, HD, shape->rot_dim,
                  shape->gated, shape->qkv_n, shape->k_off, shape->v_off, kv_len, shape->eps,
-                 nullptr, nullptr, 0, 0};
+                 nullptr, nullptr, 0, 0, shape->act};
+  if (shape->act > 1) return mi_fail(MI_ERR_ARG, "attn_prep: act is 0 (f16) or 1 (bf16)");
   attn_prep_kernel<false><<<dim3(shape->q_heads + shape->kv_heads, M), HD, 0, (hipStream_t)stream>>>(a);
   return mi_hip((int)hipGetLastError(), "attn_prep");
 }
@@ -603,7 +605,8 @@ int mi_attn_prep_kv8(uint32_t* ctrl, const float* partials, uint32_t S, uint32_t
                  reinterpret_cast<uint16_t*>(kv_k), reinterpret_cast<uint16_t*>(kv_v), pages, row_stride,
                  head_stride, page, S, M, shape->q_heads, shape->kv_heads, 256, shape->rot_dim,
                  shape->gated, shape->qkv_n, shape->k_off, shape->v_off, kv_len, shape->eps,
-                 k_scale, v_scale, sc_row_stride, sc_head_stride};
+                 k_scale, v_scale, sc_row_stride, sc_head_stride, 0u};
+  if (shape->act) return mi_fail(MI_ERR_SHAPE, "attn_prep_kv8: f16 activations only");
   attn_prep_kernel<true><<<dim3(shape->q_heads + shape->kv_heads, M), 256, 0, (hipStream_t)stream>>>(a);
   return mi_hip((int)hipGetLastError(), "attn_prep_kv8");
 }
@@ -621,8 +624,18 @@ int mi_embed_norm(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const 
   if (!ctrl || !embed || !resid || !norm_w || !x_out || M == 0 || M > 8 || hidden % 64 || hidden > 65536)
     return mi_fail(MI_ERR_ARG, "embed_norm: bad arguments (M <= 8, hidden a multiple of 64)");
   embed_norm_kernel<true><<<M, kWG, 0, (hipStream_t)stream>>>(ctrl, embed, resid, norm_w, x_out, rstd, hidden,
-                                                               vocab, eps);
+                                                               vocab, eps, 0u);
   return mi_hip((int)hipGetLastError(), "embed_norm");
+}
+
+int mi_embed_norm_act(uint32_t* ctrl, const uint16_t* embed, uint16_t* resid, const float* norm_w, uint16_t* x_out,
+                      float* rstd, uint32_t M, uint32_t hidden, uint32_t vocab, float eps, uint32_t act,
+                      void* stream) {
+  if (!ctrl || !embed || !resid || !norm_w || !x_out || M == 0 || M > 8 || hidden % 64 || hidden > 65536 || act > 1)
+    return mi_fail(MI_ERR_ARG, "embed_norm_act: bad arguments (M <= 8, hidden a multiple of 64, act 0 or 1)");
+  embed_norm_kernel<true><<<M, kWG, 0, (hipStream_t)stream>>>(ctrl, embed, resid, norm_w, x_out, rstd, hidden,
+                                                               vocab, eps, act);
+  return mi_hip((int)hipGetLastError(), "embed_norm_act");
 }
 
 int mi_norm_rows(const uint16_t* resid, const float* norm_w, uint16_t* x_out, float* rstd, uint32_t M,
@@ -630,7 +643,7 @@ int mi_norm_rows(const uint16_t* resid, const float* norm_w, uint16_t* x_out, fl
   if (!resid || !norm_w || !x_out || M == 0 || M > 16 || hidden % 64 || hidden > 65536)
     return mi_fail(MI_ERR_ARG, "norm_rows: bad arguments (M <= 16, hidden a multiple of 64)");
   embed_norm_kernel<false><<<M, kWG, 0, (hipStream_t)stream>>>(nullptr, nullptr, const_cast<uint16_t*>(resid),
-                                                                norm_w, x_out, rstd, hidden, 0, eps);
+                                                                norm_w, x_out, rstd, hidden, 0, eps, 0u);
   return mi_hip((int)hipGetLastError(), "norm_rows");
 }
 

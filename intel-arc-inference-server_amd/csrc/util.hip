@@ -47,6 +47,13 @@ __global__ void fill_f32_kernel(float* p, size_t n, uint64_t seed, int kind, flo
     p[i] = v;
   }
 }
+// mode 1: f16 -> bf16 bits; mode 2: f16 -> the f16 encoding of its bf16 rounding
+__global__ void f16_to_bf16_kernel(uint16_t* p, size_t n, uint32_t mode) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const uint16_t b = f2bf(h2f(p[i]));
+    p[i] = mode == 1u ? b : f2h(bf2f(b));
+  }
+}
 // int4 g64 layout-1 tiles (common/repack.h:17-30): 128 random nibble words, then 16 fp16
 // scales uniform in [lo, hi) packed two per word
 __global__ void fill_layout1_kernel(uint32_t* p, size_t n_words, uint64_t seed, float lo, float hi) {
@@ -123,6 +130,11 @@ int mi_fill_i8(int8_t* p, size_t n, uint64_t seed, int lo, int hi, void* stream)
 int mi_fill_layout1(uint32_t* p, size_t tiles, uint64_t seed, float lo, float hi, void* stream) {
   fill_layout1_kernel<<<grid_for(tiles * 136), 256, 0, (hipStream_t)stream>>>(p, tiles * 136, seed, lo, hi);
   return mi_hip((int)hipGetLastError(), "fill_layout1");
+}
+int mi_f16_to_bf16(uint16_t* p, size_t n, uint32_t mode, void* stream) {
+  if (!p || (mode != 1u && mode != 2u)) return mi_fail(MI_ERR_ARG, "f16_to_bf16: mode 1 or 2");
+  f16_to_bf16_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(p, n, mode);
+  return mi_hip((int)hipGetLastError(), "f16_to_bf16");
 }
 int mi_int4_dequant(const uint32_t* qweight, const uint16_t* scales, float* out, uint32_t K, uint32_t N,
                     void* stream) {

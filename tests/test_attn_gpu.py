@@ -46,7 +46,7 @@ def gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, pages=None, page=0):
     out = empty((M, QH * HD), np.uint16)
     dk, dv, dks, dvs, dq = dev(k), dev(v), dev(ks), dev(vs), dev(q)
     dpg = dev(pages)
-    shp = C.byref(sh)
+    shp = mi.shape_ref(sh)
     mi.call("mi_attn_decode", ptr(ctrl), ptr(dq), kind, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD,
             1, Lm, ptr(dpg), page, Lm, ptr(part), M, tgt, shp, stream())
     mi.call("mi_attn_reduce", ptr(ctrl), ptr(part), None, ptr(out), M, tgt, Lm, shp, stream())
@@ -189,7 +189,7 @@ def test_prep_decode_fused_is_prep_then_decode(QH, KVH, HD, rot, gated, qk, page
     c = np.zeros(64, np.uint32)
     c[0], c[1] = pos, n_act
     keep = [dev(part), dev(qn), dev(kn), dev(rope), dev(pages)]
-    shp = C.byref(sh)
+    shp = mi.shape_ref(sh)
     outs = []
     for fused in (False, True):
         ctrl = dev(c)

@@ -32,7 +32,7 @@ def verify(sh, q, k, v, pos, M, tgt, pages=None, page=0):
     part = empty((QH, tgt, M, HD + 2), np.float32)
     out = empty((M, QH * HD), np.uint16)
     dk, dv, dq, dpg = dev(k), dev(v), dev(q), dev(pages)
-    shp = C.byref(sh)
+    shp = mi.shape_ref(sh)
     mi.call("mi_attn_verify", ptr(ctrl), ptr(dq), ptr(dk), ptr(dv), HD, Lm * HD, ptr(dpg), page, Lm, ptr(part), M,
             tgt, shp, stream())
     mi.call("mi_attn_reduce", ptr(ctrl), ptr(part), None, ptr(out), M, tgt, Lm, shp, stream())
@@ -89,7 +89,7 @@ def test_verify_partial_rows_and_replay():
     part = empty((QH, tgt, 32, HD + 2), np.float32)
     out = dev(np.full((32, QH * HD), 0x7E00, np.uint16))
     dk, dv, dq = dev(k), dev(v), dev(q)
-    shp = C.byref(sh)
+    shp = mi.shape_ref(sh)
     res = []
     for _ in range(2):
         mi.call("mi_attn_verify", ptr(ctrl), ptr(dq), ptr(dk), ptr(dv), HD, Lm * HD, None, 0, Lm, ptr(part), 32, tgt,

@@ -84,12 +84,12 @@ def test_kv8_argument_errors_without_a_gpu():
     (src/common/kv8.h kHeadDim); the checks run before any launch."""
     L = mi.lib()
     sh = mi.AttnShape(40, 8, 128, 128, 0, 7168, 5120, 6144, 0.08838835, 1e-6)
-    assert L.mi_attn_reduce_kv8(8, 8, None, 8, 1, 8, 0, C.byref(sh), None) == -2
+    assert L.mi_attn_reduce_kv8(8, 8, None, 8, 1, 8, 0, mi.shape_ref(sh), None) == -2
     assert b"head_dim 256" in L.mi_last_error()
-    assert L.mi_attn_prep_kv8(8, 8, 1, 1, C.byref(sh), None, None, 8, 8, None, 8, 8, 8, 8, 128, 128, 1, 1,
+    assert L.mi_attn_prep_kv8(8, 8, 1, 1, mi.shape_ref(sh), None, None, 8, 8, None, 8, 8, 8, 8, 128, 128, 1, 1,
                               None, 0, 0, None) == -2
     sh.head_dim = 256
-    assert L.mi_attn_prep_kv8(8, 8, 1, 1, C.byref(sh), None, None, 8, 8, None, 8, 8, None, 8, 256, 256, 1, 1,
+    assert L.mi_attn_prep_kv8(8, 8, 1, 1, mi.shape_ref(sh), None, None, 8, 8, None, 8, 8, None, 8, 256, 256, 1, 1,
                               None, 0, 0, None) == -1   # no k_scale
 
 
@@ -110,11 +110,11 @@ def test_prefill_and_handoff_argument_errors_without_a_gpu():
     assert L.mi_gemm_w4a16(16, 16, 16, 16, 4, 128, 96, None) == -2       # N not a multiple of 128
     assert L.mi_gemm_w4a16_silu(None, 16, 16, 16, 4, 128, 128, None) == -1
     sh = O.attn_shape(8, 2, 64)
-    assert L.mi_attn_prefill(16, 16, 16, 64, 64, None, 0, 4, 0, C.byref(sh), 16, None) == -2  # head_dim 64
+    assert L.mi_attn_prefill(16, 16, 16, 64, 64, None, 0, 4, 0, mi.shape_ref(sh), 16, None) == -2  # head_dim 64
     sh = O.attn_shape(8, 2, 128, gated=True)
-    assert L.mi_attn_prep_rows(16, 4, 0, C.byref(sh), None, None, 16, 16, 16, 16, 128, 128, None, 0, None) == -2
+    assert L.mi_attn_prep_rows(16, 4, 0, mi.shape_ref(sh), None, None, 16, 16, 16, 16, 128, 128, None, 0, None) == -2
     sh = O.attn_shape(16, 2, 128)
-    assert L.mi_attn_prefill_kv8(16, 16, 16, 16, 16, 128, 128, 1, 128, None, 0, 4, 0, C.byref(sh), 16, 16,
+    assert L.mi_attn_prefill_kv8(16, 16, 16, 16, 16, 128, 128, 1, 128, None, 0, 4, 0, mi.shape_ref(sh), 16, 16,
                                  None) == -2  # the rotation needs head_dim 256
     assert L.mi_engine_prefill(None, None, 0, 0) == -1
 

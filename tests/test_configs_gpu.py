@@ -181,3 +181,32 @@ def test_cfg4_full_moe_step_vs_oracle():
     assert c[mi.CTRL_POS] == pos + 1 and c[mi.CTRL_DEBUG] == 0
     del orc
     eng.close()
+
+
+def test_cfg2_27b_bf16_step_vs_oracle():
+    """The 27B shape with bf16 activations (the reference's type) at seed 42, where the f16
+    activations of the same synthetic model leave the f16 range in the first step: the bf16 step
+    stays finite and matches the oracle's bf16 step."""
+    pos, tok = 4096, 1000
+    e16 = mi.Engine(mi.desc_27b(max_len=4160), seed=42)
+    e16.capture(1)
+    e16.reset(pos, tok)
+    with pytest.raises(mi.MiError, match="not finite"):
+        e16.generate(1)
+    print("27B seed 42, f16 activations: the step left the f16 range (flagged)", flush=True)
+    e16.close()
+    print("building the bf16 27B engine", flush=True)
+    eng = mi.Engine(mi.desc_27b(max_len=4160, act_bf16=1), seed=42)
+    eng.capture(1)
+    orc = OracleModel(eng)
+    eng.reset(pos, tok)
+    got_tok = int(eng.generate(1)[0])
+    got = eng.logits(1)[0]
+    print("27B bf16: the oracle's 64-layer step", flush=True)
+    am, want = orc.step(tok, pos)
+    assert np.all(np.isfinite(want)) and np.all(np.isfinite(got))
+    assert close(got, want, abs_frac=5e-4, rel_big=2e-3)
+    assert argmax_ok(got_tok, want)
+    assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+    del orc
+    eng.close()

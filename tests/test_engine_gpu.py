@@ -67,9 +67,12 @@ class OracleModel:
         lmq = self._h(eng.to_host(mi.T_LM_Q, 0, np.uint32))
         lms = self._h(eng.to_host(mi.T_LM_S, 0, np.uint16))
         self.kv8 = bool(d.kv_int8)
+        # bf16 activations: the engine's cache holds the f16 encoding of bf16 values, the
+        # oracle's holds the bf16 bits of the same values (exact either way)
+        self.act = O.ORC_BF16 if d.act_bf16 else F16
         kv_t = np.int8 if self.kv8 else np.uint16
-        self.kv_k = eng.to_host(mi.T_KV_K, 0, kv_t).copy()
-        self.kv_v = eng.to_host(mi.T_KV_V, 0, kv_t).copy()
+        self.kv_k = self._kv_in(eng.to_host(mi.T_KV_K, 0, kv_t).copy())
+        self.kv_v = self._kv_in(eng.to_host(mi.T_KV_V, 0, kv_t).copy())
         if self.kv8:
             self.kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
             self.kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
@@ -93,13 +96,26 @@ class OracleModel:
         self.keep.append(a)
         return a
 
+    def _kv_in(self, kv):
+        if self.act != O.ORC_BF16:
+            return kv
+        f = O.f16_bits_to_f32(kv).astype(np.float32)
+        b = (f.view(np.uint32) >> 16).astype(np.uint16)
+        assert np.array_equal(O.bf16_bits_to_f32(b), f)  # every cached value is a bf16 value
+        return b
+
+    def kv_values(self, which):
+        """The oracle's cache as fp32 values (to compare with the engine's)."""
+        kv = self.kv_k if which == "k" else self.kv_v
+        return O.widen(self.act, kv) if not self.kv8 else kv
+
     def step(self, tok, pos):
         logits = np.zeros(self.d.vocab, np.float32)
         if self.kv8:
             am = O.lib().orc_dense_step_kv8(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
                                             O._p(self.kv_ks), O._p(self.kv_vs), O._p(logits), self.d.layers)
         else:
-            am = O.lib().orc_dense_step(F16, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
+            am = O.lib().orc_dense_step(self.act, C.byref(self.m), tok, pos, O._p(self.kv_k), O._p(self.kv_v),
                                         O._p(logits), self.d.layers)
         return am, logits
 
@@ -122,12 +138,12 @@ def close(got, want, rel=2e-3, abs_frac=2e-3, rel_big=None):
     return ok and (rel_big is None or rb <= rel_big)
 
 
-def argmax_ok(gpu_tok, want_logits):
+def argmax_ok(gpu_tok, want_logits, abs_frac=2e-3):
     top = np.sort(want_logits)[::-1]
     if gpu_tok == int(np.argmax(want_logits)):
         return True
     # an oracle near-tie: the two leading logits closer than the tolerance
-    return (top[0] - want_logits[gpu_tok]) <= 2e-3 * np.abs(want_logits).max() * 2
+    return (top[0] - want_logits[gpu_tok]) <= abs_frac * np.abs(want_logits).max() * 2
 
 
 @pytest.mark.parametrize("qk_norm,lm8", [(1, 0), (0, 0), (1, 1)])
@@ -365,4 +381,75 @@ def test_nonfinite_logits_fail_the_call(lm8):
     eng.from_host(mi.T_FINAL_NORM, good)
     eng.reset(20, 3)
     assert np.array_equal(eng.generate(1), want)
+    eng.close()
+
+
+@pytest.mark.parametrize("qk_norm", [1, 0])
+def test_bf16_decode_steps_vs_oracle(qk_norm):
+    """bf16 activations (the reference's own type, common/bf16.h): the captured step against the
+    oracle's step under ORC_BF16 (rne_bf16 at every rounding point, bf16 embeddings, residual
+    and cache), teacher forced; the K/V rows the step writes equal the oracle's values."""
+    eng = mi.Engine(small_desc(qk_norm=qk_norm, act_bf16=1), seed=42)
+    orc = OracleModel(eng)
+    eng.capture(1)
+    pos, tok = 300, 7
+    eng.reset(pos, tok)
+    d = eng.desc
+    shp = (d.layers, d.kv_heads, d.max_len, d.head_dim)
+    for step in range(4):
+        got_tok = int(eng.generate(1)[0])
+        got = eng.logits(1)[0]
+        am, want = orc.step(tok, pos)
+        # bf16 keeps 8 significant bits: where the two GEMV orders round a fold to different sides
+        # of a bf16 tie, that activation differs by 2^-8 of itself (8x an f16 flip), and the
+        # logits by up to ~8e-3 of the largest (measured); bar 1.6e-2. Steps without such a
+        # flip come out bitwise (the bf16 x int4 products and their group sums are exact in fp32).
+        assert close(got, want, abs_frac=1.6e-2), f"step {step}"
+        assert argmax_ok(got_tok, want, abs_frac=1.6e-2)
+        for which, kind in (("k", mi.T_KV_K), ("v", mi.T_KV_V)):
+            g = O.f16_bits_to_f32(eng.to_host(kind, 0, np.uint16)).reshape(shp)[:, :, pos]
+            w = orc.kv_values(which).reshape(shp)[:, :, pos]
+            # the new rows: layer 0's (from the embedding row) the same bf16 values; a deeper
+            # layer's input carries the flips above, which move its rows by a few bf16 ulps
+            # (measured: 138 of 256 values of layer 1 at one step, at most 0.02 of the row's
+            # largest)
+            assert np.array_equal(g[0], w[0]), which
+            assert np.abs(g - w).max() <= 0.06 * np.abs(w).max(), which
+        tok, pos = got_tok, pos + 1
+    assert eng.ctrl()[mi.CTRL_DEBUG] == 0
+    eng.close()
+
+
+def test_bf16_verify_rows_bitwise_plain_steps():
+    """The bf16 step's verify rows (M = 3 through the fused QKV launch, M = 8 through attn_prep)
+    are bitwise the single-row steps at the same positions (property R)."""
+    eng = mi.Engine(small_desc(act_bf16=1, max_rows=8), seed=9)
+    eng.capture(1)
+    P, t0 = 60, 5
+    eng.reset(P, t0)
+    toks, lg = [], []
+    for _ in range(8):
+        toks.append(int(eng.generate(1)[0]))
+        lg.append(eng.logits(1)[0].copy())
+    for k in (2, 7):
+        eng.reset(P, t0)
+        rows = eng.verify(toks[:k])
+        assert list(rows) == toks[:k + 1]
+        got = eng.logits(k + 1)
+        for m in range(k + 1):
+            assert np.array_equal(got[m].view(np.uint32), lg[m].view(np.uint32)), (k, m)
+    eng.close()
+
+
+def test_bf16_refusals():
+    """What the bf16 mode does not serve is refused, not run in f16."""
+    with pytest.raises(mi.MiError):
+        mi.Engine(moe_small_desc(act_bf16=1), seed=1)
+    with pytest.raises(mi.MiError):
+        mi.Engine(small_desc(act_bf16=1, kv_int8=1, head_dim=256), seed=1)
+    eng = mi.Engine(small_desc(act_bf16=1), seed=1)
+    with pytest.raises(mi.MiError):
+        eng.prefill(np.arange(4, dtype=np.uint32))
+    with pytest.raises(mi.MiError):
+        eng.persistent(True)
     eng.close()

@@ -215,6 +215,7 @@ def test_qkv_epilogue_is_gemv_then_attn_prep(QH, KVH, HD, rot, M, n_act, paged, 
     """MI_EPI_QKV: attn_prep on the folded q||k||v inside the GEMV launch, bitwise the plain
     GEMV followed by mi_attn_prep (attn_q, the K/V cache rows written, nothing else touched)."""
     sh = O.attn_shape(QH, KVH, HD, rot_dim=rot)
+    msh = mi.lib_shape(sh)
     K, N = 64 * S * max(1, 16 // S), sh.qkv_n
     pos, Lm, P = 517, 1024, 64
     rng = np.random.default_rng(QH + M)
@@ -241,14 +242,14 @@ def test_qkv_epilogue_is_gemv_then_attn_prep(QH, KVH, HD, rot, M, n_act, paged, 
     mi.call("mi_gemv_w4a16", ptr(dq), ptr(ds), ptr(dx), ptr(part), M, K, N, S, stream())
     c1, aq1, k1, v1 = ctrl(), empty((M, QH, HD), np.float32), dev(kk), dev(vv)
     aq1.zero_()
-    mi.call("mi_attn_prep", ptr(c1), ptr(part), S, M, C.byref(sh), pnorm[0], pnorm[1], pnorm[2], ptr(aq1), None,
+    mi.call("mi_attn_prep", ptr(c1), ptr(part), S, M, mi.shape_ref(sh), pnorm[0], pnorm[1], pnorm[2], ptr(aq1), None,
             ptr(k1), ptr(v1), HD, Lm * HD, pnorm[3], P if paged else 0, Lm, stream())
     # the fused launch, twice (the hand-off words are empty again after the first)
     dpart = handoff(S * M * N)
     for rep in range(2):
         c2, aq2, k2, v2 = ctrl(), empty((M, QH, HD), np.float32), dev(kk), dev(vv)
         aq2.zero_()
-        ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(c2), shape=C.cast(C.pointer(sh), C.c_void_p),
+        ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(c2), shape=C.cast(C.pointer(msh), C.c_void_p),
                              q_norm=pnorm[0], k_norm=pnorm[1], rope=pnorm[2], attn_q=ptr(aq2), kv_k=ptr(k2),
                              kv_v=ptr(v2), row_stride=HD, head_stride=Lm * HD, pages=pnorm[3],
                              page=P if paged else 0, kv_len=Lm)
@@ -264,6 +265,7 @@ def test_qkv_epilogue_is_gemv_then_attn_prep(QH, KVH, HD, rot, M, n_act, paged, 
 def test_qkv_epilogue_past_the_cache():
     """A position at or past kv_len writes nothing and flags the step (attn_prep's rule)."""
     sh = O.attn_shape(40, 8, 128)
+    msh = mi.lib_shape(sh)
     K, N, S, Lm = 1024, sh.qkv_n, 4, 256
     qw, sc = rand_w(K, N, 7)
     x = O.f32_to_f16_bits(np.random.default_rng(7).standard_normal((1, K)).astype(np.float32))
@@ -276,7 +278,7 @@ def test_qkv_epilogue_past_the_cache():
     aq = dev(np.zeros((1, 40, 128), np.float32))
     dpart = handoff(S * N)
     dq, ds, dx = dev(qw), dev(sc), dev(x)
-    ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(dc), shape=C.cast(C.pointer(sh), C.c_void_p), rope=ptr(rope),
+    ep = mi.GemvEpilogue(kind=mi.EPI_QKV, ctrl=ptr(dc), shape=C.cast(C.pointer(msh), C.c_void_p), rope=ptr(rope),
                          attn_q=ptr(aq), kv_k=ptr(k2), kv_v=ptr(v2), row_stride=128, head_stride=Lm * 128,
                          kv_len=Lm)
     launch_ex(dq, ds, dx, dpart, 1, K, N, S, ep)

@@ -56,7 +56,7 @@ def gpu_prep_kv8(sh, part, S, M, pos, n_act, qn, kn, rope, k8, v8, ks, vs, pages
     dq.zero_(); dg.zero_()
     dk, dv, dks, dvs = dev(k8), dev(v8), dev(ks), dev(vs)
     keep = [dev(part), dev(qn), dev(kn), dev(rope), dev(pages)]
-    mi.call("mi_attn_prep_kv8", ptr(ctrl), ptr(keep[0]), S, M, C.byref(sh), ptr(keep[1]), ptr(keep[2]),
+    mi.call("mi_attn_prep_kv8", ptr(ctrl), ptr(keep[0]), S, M, mi.shape_ref(sh), ptr(keep[1]), ptr(keep[2]),
             ptr(keep[3]), ptr(dq), ptr(dg), ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm,
             ptr(keep[4]), page, Lm, stream())
     sync()
@@ -141,9 +141,9 @@ def test_writer_then_rotated_reader_vs_fp64(QH, KVH, gated):
     out = empty((M, QH * HD), np.uint16)
     print(f"kv8 reader QH={QH} KVH={KVH} gated={gated} pos={pos}", flush=True)
     mi.call("mi_attn_decode", ptr(ctrl), ptr(dq), 1, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm,
-            None, 0, Lm, ptr(dpart), M, tgt, C.byref(sh), stream())
+            None, 0, Lm, ptr(dpart), M, tgt, mi.shape_ref(sh), stream())
     mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(dpart), ptr(dg) if gated else None, ptr(out), M, tgt, Lm,
-            C.byref(sh), stream())
+            mi.shape_ref(sh), stream())
     sync()
     got = O.f16_bits_to_f32(host(out, np.uint16)[0]).astype(np.float64).reshape(QH, HD)
     G = QH // KVH
@@ -183,8 +183,8 @@ def test_reduce_kv8_is_reduce_then_unrotation():
     dp = dev(part)
     out = empty((1, QH * HD), np.uint16)
     plain = empty((1, QH * HD), np.uint16)
-    mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(dp), None, ptr(out), 1, tgt, 0, C.byref(sh), stream())
-    mi.call("mi_attn_reduce", ptr(ctrl), ptr(dp), None, ptr(plain), 1, tgt, 0, C.byref(sh), stream())
+    mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(dp), None, ptr(out), 1, tgt, 0, mi.shape_ref(sh), stream())
+    mi.call("mi_attn_reduce", ptr(ctrl), ptr(dp), None, ptr(plain), 1, tgt, 0, mi.shape_ref(sh), stream())
     sync()
     ref = np.zeros((1, QH * HD), np.uint16)
     L().orc_attn_reduce_v2_kv8(F16, C.byref(sh), pos, 1, 1, tgt, O._p(part), None, O._p(ref))

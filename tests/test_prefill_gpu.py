@@ -116,9 +116,9 @@ def test_attn_prep_rows_is_attn_prep(QH, KVH, HD, rot, qk, paged):
     q1, k1, v1 = empty((T, QH, HD), np.float32), dev(kk), dev(kk)
     q2, k2, v2 = empty((T, QH, HD), np.float32), dev(kk), dev(kk)
     print(f"attn_prep_rows {QH}/{KVH}x{HD}", flush=True)
-    mi.call("mi_attn_prep", ptr(ctrl), pp[0], 1, T, C.byref(sh), pp[1], pp[2], pp[3], ptr(q1), None, ptr(k1),
+    mi.call("mi_attn_prep", ptr(ctrl), pp[0], 1, T, mi.shape_ref(sh), pp[1], pp[2], pp[3], ptr(q1), None, ptr(k1),
             ptr(v1), HD, Lm * HD, pp[4], P if paged else 0, Lm, stream())
-    mi.call("mi_attn_prep_rows", pp[0], T, pos0, C.byref(sh), pp[1], pp[2], pp[3], ptr(q2), ptr(k2), ptr(v2), HD,
+    mi.call("mi_attn_prep_rows", pp[0], T, pos0, mi.shape_ref(sh), pp[1], pp[2], pp[3], ptr(q2), ptr(k2), ptr(v2), HD,
             Lm * HD, pp[4], P if paged else 0, stream())
     sync()
     assert np.array_equal(host(q2, np.uint32), host(q1, np.uint32))
@@ -138,7 +138,7 @@ def prefill_attention(sh, q, k, v, T, pos0, pages=None, page=0):
     Lm = k.shape[1]
     dq, dk, dv, dpg = dev(q), dev(k), dev(v), dev(pages)
     out = empty((T, QH * HD), np.uint16)
-    mi.call("mi_attn_prefill", ptr(dq), ptr(dk), ptr(dv), HD, Lm * HD, ptr(dpg), page, T, pos0, C.byref(sh),
+    mi.call("mi_attn_prefill", ptr(dq), ptr(dk), ptr(dv), HD, Lm * HD, ptr(dpg), page, T, pos0, mi.shape_ref(sh),
             ptr(out), stream())
     sync()
     return host(out, np.uint16)
@@ -344,7 +344,7 @@ def test_attn_prefill_kv8_rows_match_the_decode_reader():
     out = empty((T, QH * HD), np.uint16)
     print("attn_prefill_kv8", flush=True)
     mi.call("mi_attn_prefill_kv8", ptr(dq), ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm, None, 0, T,
-            pos0, C.byref(sh), ptr(rot), ptr(out), stream())
+            pos0, mi.shape_ref(sh), ptr(rot), ptr(out), stream())
     sync()
     got = O.f16_bits_to_f32(host(out, np.uint16)).astype(np.float64).reshape(T, QH, HD)
     tgt = 16
@@ -356,8 +356,8 @@ def test_attn_prefill_kv8_rows_match_the_decode_reader():
         part = empty((QH, tgt, 1, HD + 2), np.float32)
         want16 = empty((1, QH * HD), np.uint16)
         mi.call("mi_attn_decode", ptr(ctrl), ptr(qt), 1, ptr(dk), ptr(dv), ptr(dks), ptr(dvs), HD, Lm * HD, 1, Lm,
-                None, 0, Lm, ptr(part), 1, tgt, C.byref(sh), stream())
-        mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(part), None, ptr(want16), 1, tgt, Lm, C.byref(sh), stream())
+                None, 0, Lm, ptr(part), 1, tgt, mi.shape_ref(sh), stream())
+        mi.call("mi_attn_reduce_kv8", ptr(ctrl), ptr(part), None, ptr(want16), 1, tgt, Lm, mi.shape_ref(sh), stream())
         sync()
         want = O.f16_bits_to_f32(host(want16, np.uint16)).astype(np.float64).reshape(QH, HD)
         g = got[t]

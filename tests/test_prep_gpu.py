@@ -148,7 +148,7 @@ def test_attn_prep_without_qk_norm():
     dq = empty((M, QH, HD), np.float32)
     dk, dv = dev(kk), dev(vv)
     keep = [dev(part), dev(rope)]
-    mi.call("mi_attn_prep", ptr(ctrl), ptr(keep[0]), S, M, C.byref(sh), None, None, ptr(keep[1]),
+    mi.call("mi_attn_prep", ptr(ctrl), ptr(keep[0]), S, M, mi.shape_ref(sh), None, None, ptr(keep[1]),
             ptr(dq), None, ptr(dk), ptr(dv), HD, Lm * HD, None, 0, Lm, stream())
     sync()
     aq = np.zeros((M, QH, HD), np.float32)
