@@ -622,11 +622,11 @@ class CpuOracle:
             self.kv_ks = eng.to_host(mi.T_KV_KS, 0, np.uint16).copy()
             self.kv_vs = eng.to_host(mi.T_KV_VS, 0, np.uint16).copy()
         sh = O.attn_shape(QH, KVH, HD, rot_dim=d.rot_dim, eps=d.rms_eps)
+        self.lm = (h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab, S[4])
         self.model = O.DenseModel(d.layers, H, I, d.vocab, d.vocab_used, d.max_len, sh, d.rms_eps,
                                   C.cast(layers, C.c_void_p), h(mi.T_EMBED, 0, np.uint16),
                                   h(mi.T_FINAL_NORM, 0, np.float32),
-                                  O.Linear(h(mi.T_LM_Q, 0, np.uint32), h(mi.T_LM_S, 0, np.uint16), H, d.vocab,
-                                           S[4]),
+                                  O.Linear(*self.lm),
                                   h(mi.T_ROPE, 0, np.float32), d.attn_tgt, H // 64)
         if moe:
             m = self.model
@@ -655,6 +655,23 @@ class CpuOracle:
         if threads:
             O.lib().orc_set_threads(full)
         return dt, logits, int(am), int(used)
+
+
+    def head(self, threads=None):
+        """Seconds of the step's head alone (the lm_head GEMV in the twin order over a unit x)."""
+        O = self.O
+        q, sc, K, N, S = self.lm
+        xf = np.ones(K, np.float32)
+        out = np.zeros(N, np.float32)
+        full = O.lib().orc_threads()
+        if threads:
+            O.lib().orc_set_threads(threads)
+        t0 = time.perf_counter()
+        O.lib().orc_gemv_twin(0, q, sc, K, N, O._p(xf), 1, S, O._p(out))
+        dt = time.perf_counter() - t0
+        if threads:
+            O.lib().orc_set_threads(full)
+        return dt
 
 
 def cpu_oracle_step(eng, tok, pos):
@@ -780,11 +797,23 @@ def main():
         eng.reset(args.context, tok0)
         orc = CpuOracle(eng)
         dt, cpu_logits, cpu_am, threads = orc.step(tok0, args.context)
-        # 1 core, on a bounded sample: 1 and 3 layers + the head; per layer = the difference / 2
-        t1 = orc.step(tok0, args.context, layers=1, threads=1)[0]
-        t3 = orc.step(tok0, args.context, layers=3, threads=1)[0]
-        per_layer = max(t3 - t1, 0.0) / 2
-        one_core_step = (t1 - per_layer) + desc.layers * per_layer
+        # BASELINE.md's timing plan (median of >= 5 repetitions after a warm-up, which the full
+        # step above is) on a bounded sample: the step's first 4 and first 8 layers (a partial
+        # walk stops before the head) and the head alone, five times each; the layers cost the
+        # same, so per layer = (t8 - t4) / 4 and the step = t4 + (layers - 4) per layer + the
+        # head. 1 core: the same over 1 and 2 layers and the head, three times each.
+        def med(fn, reps):
+            return float(np.median([fn() for _ in range(reps)]))
+        t4 = med(lambda: orc.step(tok0, args.context, layers=4)[0], 5)
+        t8 = med(lambda: orc.step(tok0, args.context, layers=8)[0], 5)
+        th = med(lambda: orc.head(), 5)
+        per_layer_all = max(t8 - t4, 0.0) / 4
+        step_all = t4 + (desc.layers - 4) * per_layer_all + th
+        t1 = med(lambda: orc.step(tok0, args.context, layers=1, threads=1)[0], 3)
+        t2 = med(lambda: orc.step(tok0, args.context, layers=2, threads=1)[0], 3)
+        th1 = med(lambda: orc.head(threads=1), 3)
+        per_layer = max(t2 - t1, 0.0)
+        one_core_step = t1 + (desc.layers - 1) * per_layer + th1
         del orc
         eng.reset(args.context, tok0)
         gpu_tok = int(eng.generate(1)[0])
@@ -798,15 +827,19 @@ def main():
             "argmax_gpu": gpu_tok, "argmax_oracle": cpu_am,
         }
         cpu_name, cpu_avail, cpu_all = cpu_model()
-        cpu = {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"one full decode step of the same 64-layer model at context {args.context} "
-                         f"(oracle/oracle.cpp orc_dense_step, twin GEMV order, {threads} OpenMP threads), "
-                         f"{dt:.2f} s",
+        cpu = {"value": round(1.0 / step_all, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"the decode step of the same 64-layer model at context {args.context} (oracle/oracle.cpp "
+                         f"orc_dense_step, twin GEMV order, {threads} OpenMP threads): medians of 5 runs over the "
+                         f"first 4 layers ({t4:.3f} s), the first 8 ({t8:.3f} s) and the head ({th:.3f} s), per "
+                         f"layer {per_layer_all:.3f} s, so {step_all:.2f} s per step; the full 64-layer step of "
+                         f"the parity check (the warm-up) took {dt:.2f} s",
+               "full_step_s": round(dt, 3),
                "cpu_model": cpu_name, "threads_available": cpu_avail, "nproc": cpu_all,
                "one_core": {"value": round(1.0 / one_core_step, 5), "unit": "tokens/s", "cores": 1,
-                            "sample": f"1 thread: the step over 1 layer + head ({t1:.2f} s) and 3 layers + head "
-                                      f"({t3:.2f} s); per layer {per_layer:.2f} s, so the 64-layer step is "
-                                      f"{one_core_step:.1f} s"}}
+                            "sample": f"1 thread: medians of 3 runs over the first layer ({t1:.2f} s), the first 2 "
+                                      f"({t2:.2f} s) and the head ({th1:.2f} s); per layer {per_layer:.2f} s, so the "
+                                      f"64-layer step is {one_core_step:.1f} s (a full single-thread step is not run: "
+                                      f"it would hold the GPU box for minutes)"}}
         log(f"bench: cpu step {dt:.2f} s on {threads} threads; parity {parity}")
 
     eng.reset(args.context, tok0)

@@ -213,6 +213,11 @@ size_t mi_i8w_index(uint32_t K, uint32_t k, uint32_t n);
  * zero row s = 0, q = 0; into q_tiled (K N bytes, the layout above) and scales[N]. K a
  * multiple of 64, N of 16. */
 int mi_lm_head_int8_quantise(const float* w, uint32_t K, uint32_t N, int8_t* q_tiled, float* scales);
+/* A head the reference quantised (loader::quantise_int8_tiled, lm_head_int8.cc) is in its own
+ * layout, loader::int8_tiled_index (lm_head_int8.h:33: [N/16][K/16][16 k][16 n]). This copies
+ * it, on the device, into mi_i8w_index's layout (q_tiled, K N bytes, a separate buffer); its
+ * fp32 row scales are used as they are. K a multiple of 64, N of 16. */
+int mi_i8w_from_ref_tiles(const int8_t* ref_tiled, uint32_t K, uint32_t N, int8_t* q_tiled, void* stream);
 /* gemv_i8w: out fp32 [M][N] = (sum_k q[k][n] x[m][k]) * scales[n]; x f16 [M][K]; M <= 8, K a
  * multiple of 64, N of 64. */
 int mi_gemv_i8w(const int8_t* w, const float* scales, const uint16_t* x, float* out, uint32_t M,
@@ -520,10 +525,6 @@ enum {
   /* activations of the last step of the graph path (diagnostics): the residual [rows][hidden],
    * the normed input x, q fp32 [rows][q_heads][head_dim], the attention output, SwiGLU's output */
   MI_T_RESID, MI_T_X, MI_T_ATTN_Q, MI_T_ATTN_OUT, MI_T_HBUF,
-  /* the persistent step's work-item table, hand-off words and (with MI_STEP_TRACE set in the
-   * environment when the step is built) per-item start/end times (diagnostics; empty before
-   * mi_engine_persistent) */
-  MI_T_STEP_STAGES, MI_T_STEP_ARENA, MI_T_STEP_TRACE,
   /* the MTP head (mtp): its layer's tensors are the per-layer kinds at layer = layers; these
    * are its fc, its three norms, its KV layer [kv_heads][max_len][head_dim] f16, the hidden rows
    * hh [max_rows + 1][hidden] (row 0: the post-final-norm hidden of position pos - 1), the
@@ -572,13 +573,6 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
  * vocabulary, past the cache. Allocates its scratch on the first call (and for a larger chunk). */
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
-/* The single-row step as ONE persistent launch instead of the captured graph of launches
- * (Engine::replay, src/runtime/engine.cc:702-713, with capture.cc's list run as work-items of
- * one kernel): on = 1 makes replay(1), generate and ingest use it, on = 0 the graph again.
- * The first call builds its hand-off words (allocation happens here, not per step). The
- * results are bitwise the graph's. Dense layers with an f16 cache only (MI_ERR_SHAPE
- * otherwise). *wgs (may be NULL) receives the work-groups per launch. */
-int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs);
 /* Measurement (no reference counterpart: the role of the reference's per-kernel timing in
  * tools/bench): `reps` rounds of one linear's single-row step launch, exactly as the step
  * issues it (which = 0 qkv with attn_prep, 1 o + residual + norm, 2 gate||up + silu*up,

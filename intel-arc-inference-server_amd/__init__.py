@@ -90,13 +90,13 @@ SIGNATURES = {
     "mi_attn_prep_rows": (i32, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, vp]),
     "mi_attn_prefill_kv8": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, u32, vp, vp, vp, vp]),
     "mi_engine_bench_linear": (i32, [vp, u32, u32, vp]),
-    "mi_engine_persistent": (i32, [vp, u32, vp]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),
     "mi_engine_draft": (i32, [vp, u32, vp]),
     "mi_i8w_index": (sz, [u32, u32, u32]),
     "mi_lm_head_int8_quantise": (i32, [vp, u32, u32, vp, vp]),
+    "mi_i8w_from_ref_tiles": (i32, [vp, u32, u32, vp, vp]),
     "mi_gemv_i8w": (i32, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "mi_res_fold_ex": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "mi_norm_finish_ex": (i32, [vp, vp, vp, vp, sz, u32, u32, u32, f32, vp]),
@@ -260,9 +260,9 @@ def desc_27b(max_len=4096 + 512, act_bf16=0):
 (T_QKV_Q, T_QKV_S, T_O_Q, T_O_S, T_GU_Q, T_GU_S, T_DOWN_Q, T_DOWN_S, T_IN_NORM, T_POST_NORM,
  T_Q_NORM, T_K_NORM, T_ROUTER, T_MOE_GU, T_MOE_DN) = range(15)
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
- T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_STEP_STAGES,
- T_STEP_ARENA, T_STEP_TRACE, T_MTP_FC_Q, T_MTP_FC_S, T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K,
- T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS, T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF) = range(32, 66)
+ T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_MTP_FC_Q, T_MTP_FC_S,
+ T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K, T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS,
+ T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF) = range(32, 63)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 
@@ -351,13 +351,6 @@ class Engine:
         import numpy as np
         a = np.ascontiguousarray(ids, np.uint32)
         check(lib().mi_engine_prefill(self._h, a.ctypes.data, a.size, chunk), "engine_prefill")
-
-    def persistent(self, on=True):
-        """mi_engine_persistent: single-row steps as one persistent launch (on) or the captured
-        graph (off); returns the work-groups per launch."""
-        w = u32()
-        check(lib().mi_engine_persistent(self._h, 1 if on else 0, C.byref(w)), "engine_persistent")
-        return w.value
 
     def ctrl(self):
         import numpy as np

@@ -23,7 +23,7 @@ HIP_ONLY = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-
 
 # Per-file code generation options. attn.hip: the attention accumulators live in ordinary
 # VGPRs (they are rescaled by the vector ALUs between matrix-core products, which AGPRs would
-# turn into copies back and forth). step.hip holds the same attention code.
+# turn into copies back and forth).
 PER_FILE = {"attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 

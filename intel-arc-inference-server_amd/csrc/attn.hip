@@ -30,7 +30,7 @@ namespace {
 
 template <int HD, int KV8, int GQA, bool FP>
 __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a) {
-  attn_block<HD, KV8, GQA, FP, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, nullptr);
+  attn_block<HD, KV8, GQA, FP>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,

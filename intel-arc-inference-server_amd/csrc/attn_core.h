@@ -1,6 +1,6 @@
 // attn_core.h - the GQA decode attention block (attn_decode_v2, src/kernels/attn_v2.cl:172,
-// and its int8 reader, src/kernels/kv8.cl:535) as a device function, shared by the launch
-// form (attn.hip) and the persistent decode step (step.hip).
+// and its int8 reader, src/kernels/kv8.cl:535) as a device function of the launch form
+// (attn.hip).
 #pragma once
 #include "mi_common.h"
 #include "gemv_core.h"
@@ -40,8 +40,6 @@ struct AttnDecodeArgs {
   uint32_t* ctrl_w;
   uint32_t S, qkv_n, k_off, v_off, rot_dim, gated;
   float eps;
-  // the persistent step (PS): the new position's K/V rows as hand-off words [kv_heads][HD]
-  uint32_t* ps_new;
 };
 
 // 8 consecutive K elements of one row, raw (f16: 16 bytes; int8: 8 bytes)
@@ -107,21 +105,20 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 // attn_prep_kernel's chain operation for operation (the same fold order, the same 256-lane
 // norm tree, the same RoPE fma), so the partials, the cache rows and the gate are bitwise those
 // of attn_prep followed by the plain decode.
-template <int HD, int KV8, int GQA, bool FP, bool PS>
-__device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, uint32_t blk, uint32_t m,
-                                           Waiter* wt) {
+template <int HD, int KV8, int GQA, bool FP>
+__device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, uint32_t blk, uint32_t m) {
   constexpr uint32_t KK = HD / 32, NT = HD / 16;
   constexpr uint32_t EB = KV8 ? 1u : 2u, ROWB = HD * EB;  // bytes per row
   constexpr uint32_t VLD = ROWB / 64u;                     // 16-byte V loads per lane (4 lanes per row)
   constexpr uint32_t CW = 16u * EB;                        // bytes of one 16-dim column
-  constexpr bool PF = !PS && (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;  // (the persistent step keeps its registers)
+  constexpr bool PF = (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;
   constexpr uint32_t SV = 16u * ROWB;                      // one wave's staged V group
   constexpr uint32_t RED = 4u * GQA * HD * 4u;             // the end merge's accumulators
   __shared__ __align__(16) unsigned char s_buf[(4u * SV > RED ? 4u * SV : RED)];
   __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
   __shared__ uint32_t s_grow[kMaxBlockGroups];
   __shared__ h8_t s_q[2][KK][64];  // q as the B operand, per lane: f16 high and low parts
-  constexpr uint32_t FPQ = FP ? GQA * HD : 1u, FPN = FP ? 8u * HD : (PS ? HD : 1u), FPW = FP ? 4u * HD : 1u;
+  constexpr uint32_t FPQ = FP ? GQA * HD : 1u, FPN = FP ? 8u * HD : 1u, FPW = FP ? 4u * HD : 1u;
   __shared__ float s_q32[FPQ];                       // FP: the roped q of the GQA heads
   __shared__ __align__(16) uint16_t s_newk[FPN], s_newv[FPN];  // FP: new K/V rows, f16
   __shared__ float s_nrm[FPW];                       // FP: one wave's normed row (RoPE pairs)
@@ -130,7 +127,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   const uint32_t qi = lane & 15u, qq = lane >> 4;
   // q (plain form): wave 0's loads of the B operand go out before anything else, so waiting
   // for them later does not wait for the K/V loads issued after them (loads retire in order)
-  constexpr bool QE = !FP && !PS;
+  constexpr bool QE = !FP;
   f4_t qv[QE ? 2u * KK : 1u];
   if constexpr (QE) {
     if (wave == 0 && qi < GQA) {
@@ -343,22 +340,6 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
       a.ctrl_w[CTRL_DEBUG] = 0xDEAD0002u;  // attn_prep's flag: the row's position is past the cache
     lds_barrier();
   }
-  if constexpr (PS) {
-    // the step's new position, when this block holds it: its K and V rows come from the
-    // hand-off words the head work-items published (f16 pairs, K then V; this block is their
-    // only reader and empties them again), since the cache row is written in the same step
-    if (pos >= p_begin && pos < p_end) {  // uniform
-      if (t < HD) {
-        uint32_t* w = a.ps_new + (size_t)j * HD + t;  // [kv_heads][HD/2 K words | HD/2 V words]
-        const uint32_t v = wt->poll_word(w);
-        if (t < HD / 2u) reinterpret_cast<uint32_t*>(s_newk)[t] = v;
-        else reinterpret_cast<uint32_t*>(s_newv)[t - HD / 2u] = v;
-        st_agent(w, kEmpty);
-      }
-      pn0 = pos;
-    }
-    lds_barrier();
-  }
   // q as the MFMA B operand, staged once by wave 0: column qi = head (zero past GQA),
   // k = 32 kk + 8 qq + e; the waves read it from LDS per group rather than holding it
   if (wave == 0) {
@@ -369,9 +350,6 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
         if constexpr (FP) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = s_q32[qi * HD + 32 * kk + 8 * qq + e];
-        } else if constexpr (PS) {
-          // q from the head work-items' hand-off words (many readers: emptied later in the step)
-          wt->poll8(a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 32 * kk + 8 * qq, v);
         } else {
           const f4_t q0 = qv[2 * kk], q1 = qv[2 * kk + 1];
           v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
@@ -412,7 +390,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
       if (gi != wave && gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);  // (the first: above)
     }
     const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
-    if constexpr (FP || PS) {
+    if constexpr (FP) {
       // the step's new positions take the rows computed above (the cache may not hold them yet)
       const uint32_t p0 = p_begin + 16u * gi;
       if (p0 + glen > pn0) {  // uniform
@@ -540,18 +518,10 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
 #pragma unroll
     for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * GQA + g) * HD + dd], st_f[w2][g], v);
     float* out = a.attn_part + (((size_t)(j * GQA + g) * a.tgt + blk) * a.M + m) * (HD + 2);
-    if constexpr (PS) {  // hand-off words for the head's merge
-      st_agent(out + 2 + dd, publishable(v));
-      if (dd == 0) {
-        st_agent(out, publishable(st_hm[g]));
-        st_agent(out + 1, publishable(st_hs[g]));
-      }
-    } else {
-      *as_global(out + 2 + dd) = v;
-      if (dd == 0) {
-        out[0] = st_hm[g];
-        out[1] = st_hs[g];
-      }
+    *as_global(out + 2 + dd) = v;
+    if (dd == 0) {
+      out[0] = st_hm[g];
+      out[1] = st_hs[g];
     }
   }
 }

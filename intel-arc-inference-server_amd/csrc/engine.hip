@@ -30,7 +30,6 @@
 #include <vector>
 
 #include "mi_capi_internal.h"
-#include "step.h"
 
 namespace {
 
@@ -168,11 +167,8 @@ struct mi_engine {
   uint32_t* hhist = nullptr;  // [max_len] the drafted ids (the head's argmax history)
   float* hlogits = nullptr;   // [vocab] the last draft's logits
   hipGraphExec_t draft_graph = nullptr;
-  mi::StepPlan* step = nullptr;  // the persistent one-launch step (M = 1), when enabled
-  bool use_step = false;
 
   ~mi_engine() {
-    if (step) mi::step_plan_destroy(step);
     for (auto& g : graphs)
       if (g) (void)hipGraphExecDestroy(g);
     if (draft_graph) (void)hipGraphExecDestroy(draft_graph);
@@ -770,36 +766,6 @@ struct mi_engine {
                                                   stream)), "hh row 0");
   }
 
-  // The persistent step (step.h) for single-row steps: the same step as the M = 1 graph in one
-  // launch. Dense layers with an f16 cache only (MI_ERR_SHAPE otherwise).
-  int enable_step(bool on) {
-    if (!on) {
-      use_step = false;
-      return 0;
-    }
-    if (!step) {
-      if (d.experts || d.kv_int8 || d.mtp || d.lm_head_int8 || d.act_bf16)
-        return mi_fail(MI_ERR_SHAPE, "persistent step: dense layers with an f16 cache, f16 activations and the int4 "
-                                     "head only, no MTP head");
-      std::vector<mi::StepLayerW> lw(d.layers);
-      auto sl = [](const Linear& l) { return mi::StepLinear{l.q, l.s, l.K, l.N, l.S}; };
-      for (uint32_t li = 0; li < d.layers; ++li) {
-        const Layer& L = layer[li];
-        lw[li] = mi::StepLayerW{sl(L.qkv), sl(L.o), sl(L.gate_up), sl(L.down), L.in_norm, L.post_norm, L.q_norm, L.k_norm};
-      }
-      mi::StepModel sm{};
-      sm.layers = d.layers; sm.hidden = d.hidden; sm.inter = d.inter; sm.q_heads = d.q_heads;
-      sm.kv_heads = d.kv_heads; sm.head_dim = d.head_dim; sm.rot_dim = d.rot_dim; sm.vocab = d.vocab;
-      sm.vocab_used = d.vocab_used; sm.max_len = d.max_len; sm.tgt = d.attn_tgt; sm.eps = d.rms_eps;
-      sm.layer = lw.data(); sm.embed = embed; sm.final_norm = final_norm; sm.lm_head = sl(lm_head);
-      sm.rope = rope; sm.kv_k = static_cast<uint16_t*>(kv_k); sm.kv_v = static_cast<uint16_t*>(kv_v);
-      sm.ctrl = ctrl; sm.history = history; sm.logits = logits;
-      MI_TRY(mi::step_plan_create(sm, stream, &step));
-    }
-    use_step = true;
-    return 0;
-  }
-
   int set_rows(uint32_t pos, uint32_t n_act, const uint32_t* ids, uint32_t n_ids) {
     if (n_ids) {
       MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(ids_dev, ids, n_ids * 4, hipMemcpyHostToDevice, stream)),
@@ -834,7 +800,6 @@ struct mi_engine {
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
     if (dn_words) MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(d.max_rows) * (d.hidden / 2), stream));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
-    if (step) MI_TRY(mi::step_plan_reset(step, stream));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
     MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
     MI_TRY(mi_stream_sync(stream));
@@ -1076,9 +1041,6 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_ATTN_Q: *ptr = e->attn_q; b = size_t(m.max_rows) * m.q_heads * m.head_dim * 4; break;
     case MI_T_ATTN_OUT: *ptr = e->attn_out; b = size_t(m.max_rows) * m.q_heads * m.head_dim * 2; break;
     case MI_T_HBUF: *ptr = e->hbuf; b = size_t(m.max_rows) * m.inter * 2; break;
-    case MI_T_STEP_STAGES: mi::step_plan_debug(e->step, 0, ptr, &b); break;
-    case MI_T_STEP_ARENA: mi::step_plan_debug(e->step, 1, ptr, &b); break;
-    case MI_T_STEP_TRACE: mi::step_plan_debug(e->step, 2, ptr, &b); break;
     case MI_T_MTP_FC_Q: lin_q(e->mh.fc, ptr, &b); break;
     case MI_T_MTP_FC_S: lin_s(e->mh.fc, ptr, &b); break;
     case MI_T_MTP_PRE_E: *ptr = e->mh.pre_e; b = size_t(m.hidden) * 4; break;
@@ -1127,7 +1089,6 @@ int mi_engine_reset(mi_engine* e, uint32_t pos, uint32_t token) {
 }
 
 int mi_engine_replay(mi_engine* e, uint32_t M) {
-  if (e && M == 1 && e->use_step) return mi::step_plan_launch(e->step, e->stream);
   if (!e || M == 0 || M > e->d.max_rows || !e->graphs[M]) return mi_fail(MI_ERR_STATE, "engine_replay: not captured");
   return mi_hip(static_cast<int>(hipGraphLaunch(e->graphs[M], e->stream)), "hipGraphLaunch");
 }
@@ -1140,7 +1101,7 @@ int mi_engine_step_eager(mi_engine* e, uint32_t M) {
 }
 
 int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens) {
-  if (!e || (!e->graphs[1] && !e->use_step)) return mi_fail(MI_ERR_STATE, "engine_generate: capture(1) first");
+  if (!e || !e->graphs[1]) return mi_fail(MI_ERR_STATE, "engine_generate: capture(1) first");
   uint32_t c[MI_CTRL_WORDS];
   MI_TRY(e->read_ctrl(c));
   if (c[MI_CTRL_POS] + n > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_generate: past the KV cache");
@@ -1153,7 +1114,7 @@ int mi_engine_generate(mi_engine* e, uint32_t n, uint32_t* tokens) {
 }
 
 int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n) {
-  if (!e || (!e->graphs[1] && !e->use_step)) return mi_fail(MI_ERR_STATE, "engine_ingest: capture(1) first");
+  if (!e || !e->graphs[1]) return mi_fail(MI_ERR_STATE, "engine_ingest: capture(1) first");
   uint32_t c[MI_CTRL_WORDS];
   MI_TRY(e->read_ctrl(c));
   if (c[MI_CTRL_POS] + n > e->d.max_len) return mi_fail(MI_ERR_ARG, "engine_ingest: past the KV cache");
@@ -1170,13 +1131,6 @@ int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t ch
   if (!e) return mi_fail(MI_ERR_ARG, "engine_prefill: null");
   MI_TRY(e->prefill(ids, n, chunk));
   return e->check_handoff();  // the last position's logits: a non-finite one fails the call
-}
-
-int mi_engine_persistent(mi_engine* e, uint32_t on, uint32_t* wgs) {
-  if (!e) return mi_fail(MI_ERR_ARG, "engine_persistent: null");
-  MI_TRY(e->enable_step(on != 0));
-  if (wgs) *wgs = e->use_step ? mi::step_plan_wgs(e->step) : 0u;
-  return 0;
 }
 
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch) {

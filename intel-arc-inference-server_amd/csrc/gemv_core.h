@@ -1,6 +1,6 @@
-// gemv_core.h - the pieces of the W4A16 g64 linear shared by its launch form
-// (gemv_w4a16.hip) and the persistent decode step (step.hip): the register-local int4
-// dequantisation into MFMA operands and the hand-off words' empty pattern.
+// gemv_core.h - the pieces of the W4A16 g64 linear shared by its kernels (gemv_w4a16.hip, the
+// attention and MoE kernels' hand-offs): the register-local int4 dequantisation into MFMA
+// operands and the hand-off words' empty pattern.
 #pragma once
 #include "mi_common.h"
 
@@ -30,15 +30,12 @@ __device__ __forceinline__ h8_t perm_x(u4_t v) {
   return h8_t{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
 }
 
-// Keeps an MFMA source operand's registers intact until every MFMA of the batch that reads it
-// has been issued. Without it the register allocator may give the batch's last MFMA the shared
-// A operand's registers as its destination while the earlier MFMAs of the batch may still be
-// reading them; under register pressure (the persistent step's kernel) that corrupted the
-// middle products of a batch on gfx950.
-__device__ __forceinline__ void keep_mfma_operand(const h8_t& v) { asm volatile("" ::"v"(v)); }
-// The same for a batch of four MFMAs with one A operand: A, every B and every full result stay
-// in their own registers until the batch has been issued, so no destination overlaps a source
-// or another result of the batch.
+// Keeps a batch of four MFMAs with one A operand in distinct registers: A, every B and every
+// full result stay in their own registers until the batch has been issued, so no destination
+// overlaps a source or another result of the batch. Without it the register allocator may give
+// the batch's last MFMA the shared A operand's registers as its destination while the earlier
+// MFMAs may still be reading them; under register pressure that corrupted the middle products
+// of a batch on gfx950.
 __device__ __forceinline__ void keep_mfma_batch(const h8_t& a, const h8_t (&b)[4], const f4_t (&d)[4]) {
   asm volatile("" ::"v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
   asm volatile("" ::"v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]));
@@ -61,54 +58,5 @@ __device__ __forceinline__ uint32_t publishable_pair(uint16_t lo, uint16_t hi) {
 
 constexpr uint32_t kStatusTimeout = 0xDEAD0003u;  // the status word's value after a wait gave up
 
-// A bounded wait on hand-off words (the persistent step's work-items). A word is polled until
-// it is not empty or the thread's deadline (s_memrealtime ticks, 100 MHz) passes; the first
-// wait that gives up sets *status to kStatusTimeout, and every later wait of that thread takes
-// what it finds at once, so a step whose hand-offs break still ends promptly (with its output
-// marked invalid by the status word) instead of hanging.
-struct Waiter {
-  uint64_t deadline;
-  uint32_t* status;
-  bool dead;
-
-  __device__ __forceinline__ bool give_up() {
-    if (dead) return true;
-    if (__builtin_amdgcn_s_memrealtime() > deadline) {
-      dead = true;
-      if (status) st_agent(status, kStatusTimeout);
-    }
-    return dead;
-  }
-  __device__ __forceinline__ uint32_t poll_word(const uint32_t* p) {
-    uint32_t v = ld_agent(p);
-    while (v == kEmpty && !give_up()) {
-      __builtin_amdgcn_s_sleep(1);
-      v = ld_agent(p);
-    }
-    return v;
-  }
-  // eight consecutive fp32 words
-  __device__ __forceinline__ void poll8(const float* p, float (&v)[8]) {
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
-    uint32_t r[8];
-    uint32_t pending = 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      r[e] = ld_agent(w + e);
-      if (r[e] == kEmpty) pending |= 1u << e;
-    }
-    while (pending && !give_up()) {
-      __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (pending & (1u << e)) {
-          r[e] = ld_agent(w + e);
-          if (r[e] != kEmpty) pending &= ~(1u << e);
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(float, r[e]);
-  }
-};
 
 }  // namespace mi

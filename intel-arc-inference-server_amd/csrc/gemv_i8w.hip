@@ -78,6 +78,28 @@ __global__ __launch_bounds__(256) void gemv_i8w_kernel(const u4_t* __restrict__ 
   }
 }
 
+// One 16-byte unit of mi_i8w_index's layout per thread, gathered from the reference's
+// int8_tiled_index layout [N/16][K/16][16 k][16 n] (src/loader/lm_head_int8.h:33).
+__global__ __launch_bounds__(256) void i8w_from_ref_kernel(const int8_t* __restrict__ ref, int8_t* __restrict__ out,
+                                                           uint32_t K, uint32_t N) {
+  const size_t u = (size_t)blockIdx.x * 256u + threadIdx.x;  // unit (tile, chunk, lane)
+  const size_t units = (size_t)K * N / 16u;
+  if (u >= units) return;
+  const uint32_t lane = (uint32_t)(u % 64u), nc = K / 64u;
+  const uint32_t c = (uint32_t)((u / 64u) % nc), tile = (uint32_t)(u / 64u / nc);
+  const uint32_t n = tile * 16u + lane % 16u, q = lane / 16u;
+  uint32_t wv[4];
+#pragma unroll
+  for (uint32_t b = 0; b < 16u; ++b) {
+    const uint32_t k = c * 64u + (b / 8u) * 32u + q * 8u + b % 8u;
+    const size_t ri = ((size_t)(n / 16u) * (K / 16u) + k / 16u) * 256u + (k % 16u) * 16u + n % 16u;
+    const uint32_t v = (uint8_t)ref[ri];
+    if (b % 4u == 0) wv[b / 4u] = v;
+    else wv[b / 4u] |= v << (8u * (b % 4u));
+  }
+  *reinterpret_cast<u4_t*>(out + u * 16u) = u4_t{wv[0], wv[1], wv[2], wv[3]};
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -112,6 +134,14 @@ int mi_lm_head_int8_quantise(const float* w, uint32_t K, uint32_t N, int8_t* q_t
     }
   }
   return 0;
+}
+
+int mi_i8w_from_ref_tiles(const int8_t* ref_tiled, uint32_t K, uint32_t N, int8_t* q_tiled, void* stream) {
+  if (!ref_tiled || !q_tiled || ref_tiled == q_tiled || K == 0 || N == 0 || K % 64 || N % 16)
+    return mi_fail(MI_ERR_ARG, "i8w_from_ref_tiles: two buffers, K a multiple of 64, N of 16");
+  const size_t units = (size_t)K * N / 16u;
+  i8w_from_ref_kernel<<<(unsigned)((units + 255u) / 256u), 256, 0, (hipStream_t)stream>>>(ref_tiled, q_tiled, K, N);
+  return mi_hip((int)hipGetLastError(), "i8w_from_ref_tiles");
 }
 
 int mi_gemv_i8w(const int8_t* w, const float* scales, const uint16_t* x, float* out, uint32_t M, uint32_t K,

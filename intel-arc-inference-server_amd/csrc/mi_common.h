@@ -36,9 +36,8 @@ enum : uint32_t {
 constexpr uint32_t kStatusNonFinite = 0xDEAD0004u;  // CTRL_DEBUG: a logit was not finite
 constexpr uint32_t kNanBits = 0x7FC00000u;          // the canonical fp32 NaN
 
-// threadIdx.x as a value the compiler cannot hoist: inside a loop over work-items of different
-// kinds (the persistent step), lane-derived addresses are then recomputed per item instead of
-// being hoisted out of the loop, where every kind's would stay live (and in registers) at once.
+// threadIdx.x as a value the compiler cannot hoist: lane-derived addresses are then recomputed
+// where they are used instead of being hoisted out of a long loop and held in registers.
 __device__ __forceinline__ uint32_t opaque_tid() {
   uint32_t v = threadIdx.x;
   asm volatile("" : "+v"(v));

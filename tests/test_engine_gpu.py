@@ -450,6 +450,4 @@ def test_bf16_refusals():
     eng = mi.Engine(small_desc(act_bf16=1), seed=1)
     with pytest.raises(mi.MiError):
         eng.prefill(np.arange(4, dtype=np.uint32))
-    with pytest.raises(mi.MiError):
-        eng.persistent(True)
     eng.close()

@@ -55,3 +55,39 @@ def test_gemv_i8w_vs_oracle_and_fp64(M, K, N):
         prod = xf @ q.T.astype(np.float64)
         bound = (K * 2.0 ** -24 * (np.abs(xf) @ np.abs(q.T.astype(np.float64))) + 2.0 ** -24 * np.abs(prod)) * s
         assert np.all(np.abs(got - prod * s) <= bound + 2.0 ** -24 * np.abs(prod * s))
+
+
+def test_head_quantised_by_the_reference_retiles_bitwise():
+    """A head quantised by the reference's own quantise_int8_tiled (lm_head_int8.cc, in its
+    int8_tiled_index layout; compiled into oracle/_ref) re-tiled on the device by
+    mi_i8w_from_ref_tiles: every byte equals this library's own quantisation of the same head
+    in mi_i8w_index's layout, the scales are bitwise the same, and the GEMV over the re-tiled
+    head is bitwise the GEMV over the library's own."""
+    K, N, M = 512, 1024, 2
+    rng = np.random.default_rng(19)
+    w16 = O.f32_to_bf16_bits((0.05 * rng.standard_normal((N, K))).astype(np.float32))
+    w16[7] = 0  # a zero row: s = 0, q = 0
+    R = O.ref()
+    if R is None:
+        pytest.skip("oracle/_ref is not built (python __graft_entry__.py builds it where /root/reference is)")
+    q_ref = np.zeros(K * N, np.int8)
+    s_ref = np.zeros(N, np.float32)
+    R.ref_quantise_int8_tiled(O._p(w16), K, N, O._p(q_ref), O._p(s_ref))
+    q_own = np.zeros(K * N, np.int8)
+    s_own = np.zeros(N, np.float32)
+    mi.check(mi.lib().mi_lm_head_int8_quantise(O._p(np.ascontiguousarray(O.bf16_bits_to_f32(w16))), K, N,
+                                                 O._p(q_own), O._p(s_own)), "quantise")
+    assert np.array_equal(s_ref.view(np.uint32), s_own.view(np.uint32))
+    dref = dev(q_ref)
+    dq = empty((K * N,), np.int8)
+    mi.call("mi_i8w_from_ref_tiles", ptr(dref), K, N, ptr(dq), stream())
+    sync()
+    assert np.array_equal(host(dq, np.int8), q_own)
+    x = O.f32_to_f16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    dx, ds = dev(x), dev(s_ref)
+    a, b = empty((M, N), np.float32), empty((M, N), np.float32)
+    mi.call("mi_gemv_i8w", ptr(dq), ptr(ds), ptr(dx), ptr(a), M, K, N, stream())
+    dq_own, ds_own = dev(q_own), dev(s_own)  # (held: a temporary's memory could be reused at once)
+    mi.call("mi_gemv_i8w", ptr(dq_own), ptr(ds_own), ptr(dx), ptr(b), M, K, N, stream())
+    sync()
+    assert np.array_equal(host(a, np.uint32), host(b, np.uint32))
