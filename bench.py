@@ -21,6 +21,7 @@ Also printed in the same JSON line:
   parity       GPU vs oracle logits of that same step (rel 2e-3 bar) and their argmax.
 """
 import argparse
+import hashlib
 import ctypes as C
 import importlib
 import json
@@ -177,6 +178,91 @@ def gemv_roofline(eng, reps=3):
     }, alg
 
 
+GEMV_SOURCES = ("gemv_w4a16.hip", "gemv_core.h", "mi_common.h")
+
+
+def gemv_source_sha():
+    """sha256 (16 hex) of the GEMV kernel's sources: a traffic profile is reported only for the
+    kernel it measured."""
+    h = hashlib.sha256()
+    for f in GEMV_SOURCES:
+        with open(os.path.join(ROOT, "intel-arc-inference-server_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Reduces two rocprofv3 --pmc runs of `bench.py --only roofline` (FETCH_SIZE, then
+    WRITE_SIZE) to HBM bytes per GEMV launch: each counter (KiB per dispatch) is scaled by what
+    it reads for a kernel of known size in the same run - the 2 GiB stream read (fetch) and the
+    2 GiB fill (write). Writes profiles/gemv_w4a16_27b_step_traffic.json (the step's fused
+    launches) and profiles/gemv_w4a16_27b_traffic.json (the plain sweep), stamped with the
+    GEMV sources' hash, and prints the per-epilogue table."""
+    import csv
+    import glob
+    import re
+
+    def load(d, ctr):
+        path = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+        per, name, grid = {}, {}, {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != ctr:
+                    continue
+                k = r["Dispatch_Id"]
+                per[k] = per.get(k, 0.0) + float(r["Counter_Value"])
+                name[k], grid[k] = r["Kernel_Name"], int(r["Grid_Size"])
+        return per, name, grid
+    fe, fn, fg = load(fetch_dir, "FETCH_SIZE")
+    wr, wn, wg = load(write_dir, "WRITE_SIZE")
+    two = float(2 << 30)
+    fetch_factor = two / (1024.0 * max(v for k, v in fe.items() if "stream_read_kernel" in fn[k]))
+    write_factor = two / (1024.0 * max(v for k, v in wr.items() if "fill_u32_kernel" in wn[k]))
+
+    def epi(n):
+        m = re.search(r"gemv_w4a16_kernel<\s*\d+,\s*\d+,\s*(\d+)", n)
+        return None if m is None else int(m.group(1))
+    sha = gemv_source_sha()
+    split = {"qkv": 10, "o": 20, "gate_up": 10, "down": 34, "lm_head": 10}
+    shapes = {"qkv": (5120, 7168, 5), "o": (5120, 5120, 1), "gate_up": (5120, 34816, 2), "down": (17408, 5120, 1),
+              "lm_head": (5120, 151936, 3)}
+    per_step = {"qkv": 64, "o": 64, "gate_up": 64, "down": 64, "lm_head": 1}
+    lines = [f"fetch factor {fetch_factor:.4f} (a 2 GiB stream read), write factor {write_factor:.4f} (a 2 GiB "
+             f"fill), GEMV sources {sha}", "",
+             "| launches | linear | EPI | S | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic MB | "
+             "algorithmic MB | traffic / algorithmic |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for fused, fname, what in ((True, "gemv_w4a16_27b_step_traffic.json",
+                                "27B-shape step GEMVs, the step's fused launches (EPI 1 RESID, 2 SILU, 3 LOGITS, 5 QKV)"),
+                               (False, "gemv_w4a16_27b_traffic.json", "27B-shape GEMV sweep, plain launches (EPI 0)")):
+        tot_t = tot_a = 0.0
+        for lin, (K, N, e) in shapes.items():
+            S = split[lin]
+            e_run = e if fused else 0
+            rows_g = S + 1 if fused and e in (1, 5) else S
+            grid = N // 64 * rows_g * 256
+            F = [v for k, v in fe.items() if epi(fn[k]) == e_run and fg[k] == grid]
+            W = [v for k, v in wr.items() if epi(wn[k]) == e_run and wg[k] == grid]
+            fk, wk = sum(F) / len(F), sum(W) / len(W)
+            t = fk * 1024 * fetch_factor + wk * 1024 * write_factor
+            a = K * N // 2 + (K // 64) * N * 2 + 2 * K + 4 * N
+            tot_t += t * per_step[lin]
+            tot_a += a * per_step[lin]
+            lines.append(f"| {'fused' if fused else 'plain'} | {lin} | {e_run} | {S} | {len(F)} | {fk:.1f} | {wk:.1f} | "
+                         f"{t / 1e6:.2f} | {a / 1e6:.2f} | {t / a:.3f} |")
+        n = sum(per_step.values())
+        lines.append(f"| {'fused' if fused else 'plain'} | per launch of the step's {n} | | | | | | "
+                     f"{tot_t / n / 1e6:.3f} | {tot_a / n / 1e6:.3f} | {tot_t / tot_a:.3f} |")
+        prof = {"kernel": "gemv_w4a16_kernel", "workload": what, "traffic_bytes_per_launch": int(tot_t / n),
+                "alg_bytes_per_launch": int(tot_a / n), "fetch_factor": round(fetch_factor, 4),
+                "write_factor": round(write_factor, 4), "split_k": split,
+                "source_sha": sha, "sources": list(GEMV_SOURCES),
+                "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) -- python3 bench.py --only roofline; "
+                           "python3 bench.py --pmc-summary FETCH_DIR WRITE_DIR"}
+        with open(os.path.join(ROOT, "profiles", fname), "w") as f:
+            json.dump(prof, f, indent=1)
+    print("\n".join(lines))
+
+
 def profiled_traffic(eng, name="gemv_w4a16_27b_traffic.json"):
     """HBM bytes per GEMV launch from a committed PMC summary under profiles/ (FETCH_SIZE and
     WRITE_SIZE runs of the launches, each scaled by a kernel of known size), provided it was
@@ -190,6 +276,9 @@ def profiled_traffic(eng, name="gemv_w4a16_27b_traffic.json"):
     mine = dict(zip(["qkv", "o", "gate_up", "down", "lm_head"], [eng.linear_s(w) for w in range(5)]))
     if prof.get("split_k") != mine:
         log(f"bench: profiled traffic was measured at S {prof.get('split_k')}, engine uses {mine}: not reported")
+        return None
+    if prof.get("source_sha") != gemv_source_sha():
+        log(f"bench: profiled traffic ({name}) was measured on other GEMV sources: not reported")
         return None
     return prof["traffic_bytes_per_launch"]
 
@@ -714,6 +803,9 @@ def main():
                     help="enqueue each step kernel by kernel instead of replaying the captured graph "
                          "(no capture, no CPU step); with --steps 0 only the GEMV roofline sweep and "
                          "the stream-read probe run, which is the command the kernel profiles use")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two rocprofv3 --pmc output folders of `--only roofline` (FETCH_SIZE, WRITE_SIZE) "
+                         "into profiles/gemv_w4a16_27b_*traffic.json")
     ap.add_argument("--only", choices=["cfg1", "cfg3", "cfg4", "cfg5", "prefill", "moe_prefill", "roofline",
                                        "lm8", "mtp"],
                     default=None,
@@ -729,6 +821,9 @@ def main():
         print(json.dumps({"prefill": measure_prefill(eng)}), flush=True)
         eng.close()
         return
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.only == "roofline":
         # the GEMV roofline's launches alone (the command the GEMV kernel profiles use): the
         # step's fused launches per linear, then the plain sweep
@@ -737,7 +832,9 @@ def main():
         roof, _ = step_gemv_roofline(eng)
         plain, _ = gemv_roofline(eng)
         eng.close()
-        print(json.dumps({"roofline": roof, "plain_sweep": plain}), flush=True)
+        # the calibration kernels of the PMC passes: a 2 GiB fill and 2 GiB stream reads
+        stream = stream_read_rate(None)
+        print(json.dumps({"roofline": roof, "plain_sweep": plain, "stream_read_gbs": round(stream, 1)}), flush=True)
         return
     if args.only == "cfg4" and args.eager:
         # the configs[3] MoE decode step enqueued kernel by kernel (the MoE kernel profiles'
