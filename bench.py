@@ -454,7 +454,7 @@ def measure_mtp(args, moe=False):
                     "synchronisation per call); the plain step is HIP-event timed"}
 
 
-def measure_cfg3(st, ctx):
+def measure_cfg3(st, ctx, tgt=64):
     """one layer's decode attention at context `ctx`, 40 q / 8 kv heads
     of 128, int8 K/V uniform [-127, 127] with fp16 scales U(0.005, 0.05) per (pos, kv head),
     64-token pages in a shuffled table; attn_decode + attn_reduce per call at 64 blocks per kv
@@ -462,7 +462,7 @@ def measure_cfg3(st, ctx):
     through enough cache copies (at least 4, at least 640 MB in all) that none is still in
     the 256 MB MALL when it is read again."""
     L, D = mi.lib(), Dev()
-    QH, KVH, HD, P, tgt = 40, 8, 128, 64, 64  # tgt 64: the fastest blocking at 32k and 128k (a 24..128 sweep)
+    QH, KVH, HD, P = 40, 8, 128, 64
     rng = np.random.default_rng(ctx)
     copy_bytes = 2 * KVH * ctx * HD + 2 * KVH * ctx * 2
     copies = max(4, -(-640 * 2**20 // copy_bytes))
@@ -494,7 +494,7 @@ def measure_cfg3(st, ctx):
     t = time_calls(st, call, 50)
     D.free()
     alg = 2 * KVH * HD * ctx + 2 * KVH * ctx * 2
-    return {"context": ctx, "us_per_layer": round(t, 2), "alg_bytes": alg, "gbs": round(alg / t / 1e3, 1),
+    return {"context": ctx, "tgt": tgt, "us_per_layer": round(t, 2), "alg_bytes": alg, "gbs": round(alg / t / 1e3, 1),
             "frac_of_peak": round(alg / t / 1e3 / HBM_PEAK_GBS, 4), "cache_copies": copies}
 
 
@@ -869,7 +869,7 @@ def main():
         return
     if args.only:
         fn = {"cfg1": lambda: measure_cfg1(None),
-              "cfg3": lambda: [measure_cfg3(None, L) for L in (32768, 131072)],
+              "cfg3": lambda: [measure_cfg3(None, L, args.attn_tgt or 64) for L in (32768, 131072)],
               "cfg5": lambda: measure_cfg5(None)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return
