@@ -55,16 +55,24 @@ constexpr uint32_t kFoldWords = 2304;  // a consumer's polled partials: S * 64 (
 
 struct ChainStage {
   uint32_t kind, first, count;
+  uint32_t items;  // SLICE: product items
   // the linear this stage produces (SLICE) or consumes (RESID / SILU / HEAD)
   const uint32_t* qw;
   const uint16_t* sc;
   uint32_t K, N, S, gps, tiles;
   const uint16_t* x_plain;  // SLICE input from an earlier launch, f16 [K]
   const uint32_t* x_words;  // or hand-off words, f16 pairs [K / 2]
+  // or (n_sums set) x is the RMSNorm of a residual handed over as words (x_words: residual
+  // pairs [K / 2]) with its per-tile sums of squares n_sums [K / 64] and weights n_w [K]
+  const float* n_sums;
+  const float* n_w;
   float* part;              // [S][N] hand-off partials
   // RESID
   const uint16_t* r_in_plain;  // the residual in (one of the two)
   uint32_t* r_in_words;
+  uint32_t r_in_take;          // r_in_words has this consumer as its only reader
+  float* sum_pub;              // set: publish the tile's sum of squares here [tiles] and stop
+                               // (the next linear's slices form the norm); else the full norm
   uint16_t* r_out_plain;       // the residual out (either or both)
   uint32_t* r_out_words;
   float* sumsq;                // [tiles][tiles], consumer c's copy at row c
@@ -157,25 +165,53 @@ __device__ __forceinline__ void poll_lds_n(const ChainArgs& a, const void* base,
 // ---- a product item: one tile of one slice (gemv_w4a16_kernel<1, 2, EPI> at M = 1) ----
 // Wave w takes the slice's k-groups w and w + 4; each an MFMA batch scaled per column, summed
 // in group order; the waves' sums added in wave order: the launch kernel's slice partial.
-__device__ __forceinline__ void slice_item(const ChainArgs& a, const ChainStage& st, uint32_t u, Lds& L) {
+__device__ __forceinline__ void slice_item(const ChainArgs& a, const ChainStage& st, uint32_t u, Lds& L, uint32_t si,
+                                           uint32_t& inv_for) {
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, c4 = lane & 15u, q = lane >> 4;
-  const uint32_t tiles = st.tiles, N = st.N, gps = st.gps;
+  const uint32_t tiles = st.tiles, N = st.N, gps = st.gps, act = a.act;
   const uint32_t s = u / tiles, tile = u - s * tiles, n0 = tile * 64u, ncol = n0 + 4u * c4;
-  // the weights first (they do not depend on anything), then the input
+  // the weights first (they do not depend on anything), then the input; every load goes out
+  // unconditionally (a wave with no second group re-reads its first) so none waits for a branch
   u4_t wv[2][2];
   u2_t sv[2];
 #pragma unroll
   for (uint32_t k = 0; k < 2; ++k) {
     const uint32_t gl = wave + 4u * k;
-    if (gl < gps) {
-      const uint32_t g = s * gps + gl;
+    const uint32_t g = s * gps + (gl < gps ? gl : wave % gps);
 #pragma unroll
-      for (uint32_t h = 0; h < 2; ++h) wv[k][h] = load_stream16(st.qw + (size_t)(g * 8u + 4u * h + q) * N + ncol);
-      sv[k] = *as_global(reinterpret_cast<const u2_t*>(st.sc + (size_t)g * N + ncol));
-    }
+    for (uint32_t h = 0; h < 2; ++h) wv[k][h] = load_stream16(st.qw + (size_t)(g * 8u + 4u * h + q) * N + ncol);
+    sv[k] = *as_global(reinterpret_cast<const u2_t*>(st.sc + (size_t)g * N + ncol));
   }
   const uint32_t nw = gps * 32u;  // the slice's input words
-  if (st.x_words) {
+  if (st.n_sums) {
+    // x = RMSNorm(residual) formed here, as the norm's consumer forms it: the tile sums added
+    // in tile order from +0 (once per stage and work-group), then (v * inv) * w per element
+    float w0 = 0.f, w1 = 0.f;
+    if (t < nw) {
+      w0 = st.n_w[2u * (s * nw + t)];
+      w1 = st.n_w[2u * (s * nw + t) + 1u];
+    }
+    poll_lds<1>(a, st.x_words + s * nw, nw, t * 4u, 0u, L.xw, false);
+    if (inv_for != si) {
+      const uint32_t nt = st.K / 64u;
+      poll_lds<1>(a, st.n_sums, nt, t * 4u, 0u, L.words, false);
+      lds_barrier();
+      if (t == 0) {
+        float tot = 0.f;
+        for (uint32_t g = 0; g < nt; ++g) tot += __builtin_bit_cast(float, L.words[g]);
+        L.misc[1] = 1.0f / sqrtf(tot / (float)st.K + a.eps);
+      }
+      inv_for = si;
+    }
+    lds_barrier();
+    if (t < nw) {
+      const float inv = L.misc[1];
+      const uint32_t rw = L.xw[t];
+      const uint16_t x0 = act_enc(res_widen((uint16_t)(rw & 0xFFFFu), act) * inv * w0, act);
+      const uint16_t x1 = act_enc(res_widen((uint16_t)(rw >> 16), act) * inv * w1, act);
+      L.xw[t] = publishable_pair(x0, x1);
+    }
+  } else if (st.x_words) {
     poll_lds<1>(a, st.x_words + s * nw, nw, t * 4u, 0u, L.xw, false);
   } else if (t < nw) {
     L.xw[t] = *as_global(reinterpret_cast<const uint32_t*>(st.x_plain) + s * nw + t);
@@ -246,9 +282,9 @@ __device__ __forceinline__ void resid_item(const ChainArgs& a, const ChainStage&
   float w_pre = 0.f;
   if (wave == 0) {  // the residual (plain input) and the norm weight go out before the fold
     if (!st.r_in_words) r_pre = st.r_in_plain[n0 + lane];
-    w_pre = st.norm_w[n0 + lane];
+    if (!st.sum_pub) w_pre = st.norm_w[n0 + lane];  // (no norm here in the publishing form)
   }
-  if (st.r_in_words) poll_lds<1>(a, st.r_in_words + tile * 32u, 32u, t * 4u, 0u, L.rw, true);
+  if (st.r_in_words) poll_lds<1>(a, st.r_in_words + tile * 32u, 32u, t * 4u, 0u, L.rw, st.r_in_take != 0);
   fold_tile(a, st, tile, L);
   if (wave == 0) {
     if (st.r_in_words) {
@@ -265,7 +301,15 @@ __device__ __forceinline__ void resid_item(const ChainArgs& a, const ChainStage&
 #pragma unroll
     for (int sst = 32; sst > 0; sst >>= 1) s2 += __shfl_down(s2, sst, 64);
     s2 = publishable(__shfl(s2, 0, 64));
-    for (uint32_t c = lane; c < tiles; c += 64u) st_agent(st.sumsq + (size_t)c * tiles + tile, s2);
+    if (st.sum_pub) {
+      if (lane == 0) st_agent(st.sum_pub + tile, s2);
+    } else {
+      for (uint32_t c = lane; c < tiles; c += 64u) st_agent(st.sumsq + (size_t)c * tiles + tile, s2);
+    }
+  }
+  if (st.sum_pub) {  // the next linear's slices form the norm from the residual and the sums
+    lds_barrier();
+    return;
   }
   // every tile's sum (this consumer's copy), added in ascending tile order
   poll_lds<1>(a, st.sumsq + (size_t)tile * tiles, tiles, t * 4u, 0u, L.words, true);
@@ -397,18 +441,20 @@ __device__ __forceinline__ void head_item(const ChainArgs& a, const ChainStage& 
 }
 
 template <int HD>
-__global__ __launch_bounds__(256, 4) void chain_kernel(ChainArgs a) {
+__global__ __launch_bounds__(256, 4) void chain_kernel(ChainArgs a, const ChainStage* __restrict__ stages) {
   __shared__ Lds L;
   // the set of many-reader words the previous launch used: every reader of it has finished
   for (uint32_t k = blockIdx.x * 256u + threadIdx.x; k < a.jan_words; k += gridDim.x * 256u) st_agent(a.jan + k, kEmpty);
-  uint32_t si = 0;
+  uint32_t si = 0, inv_for = ~0u;
   for (uint32_t i = blockIdx.x; i < a.total; i += gridDim.x) {
-    while (i >= a.stages[si].first + a.stages[si].count) ++si;
-    const ChainStage& st = a.stages[si];
+    // the stage table as its own __restrict__ parameter: scalar loads into SGPRs (a vector load
+    // of the fields would put a dependent memory round trip in front of every item)
+    while (i >= stages[si].first + stages[si].count) ++si;
+    const ChainStage& st = stages[si];
     const uint32_t u = i - st.first;
     const uint32_t t0 = a.trace ? (uint32_t)__builtin_amdgcn_s_memrealtime() : 0u;
     switch (st.kind) {
-      case CS_SLICE: slice_item(a, st, u, L); break;
+      case CS_SLICE: slice_item(a, st, u, L, si, inv_for); break;
       case CS_RESID: resid_item(a, st, u, L); break;
       case CS_SILU: silu_item(a, st, u, L); break;
       default: head_item<HD>(a, st, u, L); break;
@@ -485,12 +531,16 @@ int chain_plan_create(const ChainModel& m, hipStream_t st, ChainPlan** out) {
     return o;
   };
   const uint32_t tilesH = H / 64;
-  size_t x_post[2], hw[2], x_in[2], set_begin[2], set_end[2];
+  // per set: the residual after o and its tile sums (read by gate||up's slices and down's
+  // consumers), SwiGLU's h, the residual after down and its sums (the next q||k||v's slices)
+  size_t r_post[2], s_post[2], hw[2], r_next[2], s_next[2], set_begin[2], set_end[2];
   for (int k = 0; k < 2; ++k) {
     set_begin[k] = off;
-    x_post[k] = take(H / 2);
+    r_post[k] = take(H / 2);
+    s_post[k] = take(tilesH);
     hw[k] = take(I / 2);
-    x_in[k] = take(H / 2);
+    r_next[k] = take(H / 2);
+    s_next[k] = take(tilesH);
     set_end[k] = off;
   }
   uint32_t So = 0, Sg = 0, Sd = 0, Sq = 0;
@@ -502,8 +552,7 @@ int chain_plan_create(const ChainModel& m, hipStream_t st, ChainPlan** out) {
   }
   const size_t part_o = take((size_t)So * H), part_g = take((size_t)Sg * 2 * I), part_d = take((size_t)Sd * H);
   const size_t part_q = take((size_t)Sq * qkv_n);
-  const size_t sum_o = take((size_t)tilesH * tilesH), sum_d = take((size_t)tilesH * tilesH);
-  const size_t r_mid = take(H / 2);
+  const size_t sum_d = take((size_t)tilesH * tilesH);  // the last layer's final norm (all-to-all sums)
   p->arena_words = off;
   if (hipMalloc(&p->arena, off * 4) != hipSuccess) return mi_fail(MI_ERR_OOM, "chain: hand-off words");
   if (int e = mi_gemv_handoff_init(reinterpret_cast<float*>(p->arena), off, st)) return e;
@@ -535,44 +584,57 @@ int chain_plan_create(const ChainModel& m, hipStream_t st, ChainPlan** out) {
       s.S = l.S;
       s.gps = l.K / 64 / l.S;
       s.tiles = l.N / 64;
-      s.count = s.tiles * l.S;
+      s.items = s.tiles * l.S;
+      s.count = s.items;
       s.x_plain = xp;
       s.x_words = xw;
       s.part = part;
       return s;
     };
-    // o, then its consumers: the residual (plain in, words out), the post-attention norm
+    // o, then its consumers: the residual (plain in, words out) and its tile sums
     add(slice(L.o, m.attn_out, nullptr, F(part_o)));
     ChainStage ro = all.back();
     ro.kind = CS_RESID;
     ro.count = tilesH;
     ro.r_in_plain = m.resid;
-    ro.r_out_words = W(r_mid);
-    ro.sumsq = F(sum_o);
-    ro.norm_w = L.post_norm;
-    ro.x_out_words = W(x_post[k]);
+    ro.r_out_words = W(r_post[k]);
+    ro.sum_pub = F(s_post[k]);
     add(ro);
-    add(slice(L.gate_up, nullptr, W(x_post[k]), F(part_g)));
+    // gate||up on the post-attention norm of that residual, formed by its slices
+    ChainStage gu = slice(L.gate_up, nullptr, W(r_post[k]), F(part_g));
+    gu.n_sums = F(s_post[k]);
+    gu.n_w = L.post_norm;
+    add(gu);
     ChainStage sg = all.back();
     sg.kind = CS_SILU;
     sg.count = (2 * I) / 64;
+    sg.n_sums = nullptr;
     sg.h_words = W(hw[k]);
     add(sg);
     add(slice(L.down, nullptr, W(hw[k]), F(part_d)));
     ChainStage rd = all.back();
     rd.kind = CS_RESID;
     rd.count = tilesH;
-    rd.r_in_words = W(r_mid);
+    rd.r_in_words = W(r_post[k]);
+    rd.r_in_take = 0;
     rd.r_out_plain = m.resid;
-    rd.sumsq = F(sum_d);
-    rd.norm_w = last ? m.final_norm : m.layer[li + 1].in_norm;
-    rd.x_out_plain = m.x;  // the lm_head's input after the last layer (and a plain copy otherwise)
-    rd.x_out_words = last ? nullptr : W(x_in[k]);
+    if (last) {  // the final norm, whole, for the head's launch
+      rd.sumsq = F(sum_d);
+      rd.norm_w = m.final_norm;
+      rd.x_out_plain = m.x;
+    } else {
+      rd.r_out_words = W(r_next[k]);
+      rd.sum_pub = F(s_next[k]);
+    }
     add(rd);
     if (!last) {  // the next layer's q||k||v and attn_prep
       const ChainLayer& N1 = m.layer[li + 1];
-      add(slice(N1.qkv, nullptr, W(x_in[k]), F(part_q)));
+      ChainStage qs = slice(N1.qkv, nullptr, W(r_next[k]), F(part_q));
+      qs.n_sums = F(s_next[k]);
+      qs.n_w = N1.in_norm;
+      add(qs);
       ChainStage hq = all.back();
+      hq.n_sums = nullptr;
       hq.kind = CS_HEAD;
       hq.count = QH + 2 * KVH;
       hq.q_norm = N1.q_norm;
@@ -629,8 +691,8 @@ int chain_plan_create(const ChainModel& m, hipStream_t st, ChainPlan** out) {
 
 int chain_launch(const ChainPlan* p, uint32_t layer, hipStream_t st) {
   if (!p || layer >= p->args.size()) return mi_fail(MI_ERR_ARG, "chain: layer out of range");
-  if (p->m.head_dim == 128) chain_kernel<128><<<p->wgs, 256, 0, st>>>(p->args[layer]);
-  else chain_kernel<256><<<p->wgs, 256, 0, st>>>(p->args[layer]);
+  if (p->m.head_dim == 128) chain_kernel<128><<<p->wgs, 256, 0, st>>>(p->args[layer], p->args[layer].stages);
+  else chain_kernel<256><<<p->wgs, 256, 0, st>>>(p->args[layer], p->args[layer].stages);
   return mi_hip((int)hipGetLastError(), "chain launch");
 }
 
