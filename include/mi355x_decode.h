@@ -535,10 +535,7 @@ enum {
   MI_T_LM_I8, MI_T_LM_I8_S,
   /* MoE models: the hand-off words of mi_moe_down_norm [max_rows][hidden / 2] (0xFFFFFFFF
    * between launches; emptied again by the engine after a step whose wait timed out) */
-  MI_T_MOE_HANDOFF,
-  /* the chain launches' per-item start / end times [layers][items][2] u32 (s_memrealtime; with
-   * MI_CHAIN_TRACE set in the environment when mi_engine_chain first builds them; diagnostics) */
-  MI_T_CHAIN_TRACE
+  MI_T_MOE_HANDOFF
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's
@@ -576,16 +573,6 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
  * vocabulary, past the cache. Allocates its scratch on the first call (and for a larger chunk). */
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
-/* The single-row step with one launch per layer for the layer's linears (no counterpart in the
- * reference, which records them launch by launch, capture.cc:1247, 997, 1370): on = 1 makes
- * replay(1), generate and ingest run, per layer, the attention pair and ONE launch holding o with
- * the residual and the post-attention norm, gate||up with SwiGLU, down with the residual and the
- * next norm, and the next layer's q||k||v with attn_prep, all as one list of work-items handed
- * on through the hand-off words; on = 0 the launch-per-linear graph again. The results are
- * bitwise the graph's. Dense models with the f16-format cache, no MTP head (MI_ERR_SHAPE
- * otherwise); allocation happens at the first on = 1, and a captured single-row graph is
- * recorded again. *wgs (may be NULL) receives the work-groups per chain launch. */
-int mi_engine_chain(mi_engine* e, uint32_t on, uint32_t* wgs);
 /* Measurement (no reference counterpart: the role of the reference's per-kernel timing in
  * tools/bench): `reps` rounds of one linear's single-row step launch, exactly as the step
  * issues it (which = 0 qkv with attn_prep, 1 o + residual + norm, 2 gate||up + silu*up,

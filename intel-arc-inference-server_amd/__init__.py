@@ -89,7 +89,6 @@ SIGNATURES = {
     "mi_moe_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp]),
     "mi_attn_prep_rows": (i32, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, vp]),
     "mi_attn_prefill_kv8": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, u32, vp, vp, vp, vp]),
-    "mi_engine_chain": (i32, [vp, u32, vp]),
     "mi_engine_bench_linear": (i32, [vp, u32, u32, vp]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
@@ -263,7 +262,7 @@ def desc_27b(max_len=4096 + 512, act_bf16=0):
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_MTP_FC_Q, T_MTP_FC_S,
  T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K, T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS,
- T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF, T_CHAIN_TRACE) = range(32, 64)
+ T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF) = range(32, 63)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
 
 
@@ -352,13 +351,6 @@ class Engine:
         import numpy as np
         a = np.ascontiguousarray(ids, np.uint32)
         check(lib().mi_engine_prefill(self._h, a.ctypes.data, a.size, chunk), "engine_prefill")
-
-    def chain(self, on=True):
-        """mi_engine_chain: single-row steps with one launch per layer for its linears (on) or
-        the launch-per-linear graph (off); returns the work-groups per chain launch."""
-        w = u32()
-        check(lib().mi_engine_chain(self._h, 1 if on else 0, C.byref(w)), "engine_chain")
-        return w.value
 
     def ctrl(self):
         import numpy as np

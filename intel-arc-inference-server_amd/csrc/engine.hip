@@ -30,7 +30,6 @@
 #include <vector>
 
 #include "mi_capi_internal.h"
-#include "chain.h"
 
 namespace {
 
@@ -168,11 +167,8 @@ struct mi_engine {
   uint32_t* hhist = nullptr;  // [max_len] the drafted ids (the head's argmax history)
   float* hlogits = nullptr;   // [vocab] the last draft's logits
   hipGraphExec_t draft_graph = nullptr;
-  mi::ChainPlan* chain = nullptr;  // the layer chain launches (single-row steps), when built
-  bool use_chain = false;
 
   ~mi_engine() {
-    if (chain) mi::chain_destroy(chain);
     for (auto& g : graphs)
       if (g) (void)hipGraphExecDestroy(g);
     if (draft_graph) (void)hipGraphExecDestroy(draft_graph);
@@ -455,19 +451,6 @@ struct mi_engine {
     }
     MI_TRY(mi_embed_norm_act(ctrl, embed, resid, layer[0].in_norm, x, rstd, M, d.hidden, d.vocab, d.rms_eps,
                              d.act_bf16, stream));
-    if (use_chain && M == 1) {
-      // layer 0's q||k||v, then per layer the attention pair and the chain launch (o, gate||up,
-      // down and the next layer's q||k||v with their epilogues), then the head
-      MI_TRY(launch_qkv(0, 1));
-      const size_t layer_kv16 = size_t(d.kv_heads) * d.max_len * d.head_dim;
-      for (uint32_t li = 0; li < d.layers; ++li) {
-        MI_TRY(attn_pair(layer[li], ctrl, static_cast<uint16_t*>(kv_k) + li * layer_kv16,
-                         static_cast<uint16_t*>(kv_v) + li * layer_kv16, 1, false));
-        MI_TRY(mi::chain_launch(chain, li, stream));
-      }
-      MI_TRY(mi::chain_finish(chain, stream));
-      return head(ctrl, M, x, logits, history);
-    }
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
       MI_TRY(launch_qkv(li, M));
@@ -783,39 +766,6 @@ struct mi_engine {
                                                   stream)), "hh row 0");
   }
 
-  // The layer chain (chain.h) for single-row steps: the same step as the launch-per-linear graph,
-  // bitwise, with one launch per layer for its linears and their epilogues. Dense layers with
-  // the f16-format cache, no MTP head (MI_ERR_SHAPE otherwise). A captured single-row graph is
-  // recorded again.
-  int set_chain(bool on) {
-    if (on && !chain) {
-      if (d.experts || d.kv_int8 || d.mtp)
-        return mi_fail(MI_ERR_SHAPE, "chain: dense layers with the f16-format cache, no MTP head");
-      std::vector<mi::ChainLayer> lw(d.layers);
-      auto cl = [](const Linear& l) { return mi::ChainLinear{l.q, l.s, l.K, l.N, l.S}; };
-      for (uint32_t li = 0; li < d.layers; ++li) {
-        const Layer& L = layer[li];
-        lw[li] = mi::ChainLayer{cl(L.qkv), cl(L.o), cl(L.gate_up), cl(L.down), L.in_norm, L.post_norm, L.q_norm,
-                                L.k_norm};
-      }
-      mi::ChainModel cm{};
-      cm.layers = d.layers; cm.hidden = d.hidden; cm.inter = d.inter; cm.q_heads = d.q_heads;
-      cm.kv_heads = d.kv_heads; cm.head_dim = d.head_dim; cm.rot_dim = d.rot_dim; cm.max_len = d.max_len;
-      cm.act = d.act_bf16; cm.eps = d.rms_eps; cm.layer = lw.data(); cm.final_norm = final_norm; cm.rope = rope;
-      cm.kv_k = static_cast<uint16_t*>(kv_k); cm.kv_v = static_cast<uint16_t*>(kv_v); cm.ctrl = ctrl;
-      cm.status = ctrl + MI_CTRL_DEBUG; cm.resid = resid; cm.x = x; cm.attn_out = attn_out; cm.attn_q = attn_q;
-      MI_TRY(mi::chain_plan_create(cm, stream, &chain));
-    }
-    if (on == use_chain) return 0;
-    use_chain = on;
-    if (graphs[1]) {
-      (void)hipGraphExecDestroy(graphs[1]);
-      graphs[1] = nullptr;
-      return capture(1);
-    }
-    return 0;
-  }
-
   int set_rows(uint32_t pos, uint32_t n_act, const uint32_t* ids, uint32_t n_ids) {
     if (n_ids) {
       MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(ids_dev, ids, n_ids * 4, hipMemcpyHostToDevice, stream)),
@@ -848,7 +798,6 @@ struct mi_engine {
     if (c[MI_CTRL_DEBUG] != MI_STATUS_HANDOFF_TIMEOUT) return 0;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
-    if (chain) MI_TRY(mi::chain_reset(chain, stream));
     if (dn_words) MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(d.max_rows) * (d.hidden / 2), stream));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
@@ -1092,7 +1041,6 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_ATTN_Q: *ptr = e->attn_q; b = size_t(m.max_rows) * m.q_heads * m.head_dim * 4; break;
     case MI_T_ATTN_OUT: *ptr = e->attn_out; b = size_t(m.max_rows) * m.q_heads * m.head_dim * 2; break;
     case MI_T_HBUF: *ptr = e->hbuf; b = size_t(m.max_rows) * m.inter * 2; break;
-    case MI_T_CHAIN_TRACE: mi::chain_debug(e->chain, ptr, &b); break;
     case MI_T_MTP_FC_Q: lin_q(e->mh.fc, ptr, &b); break;
     case MI_T_MTP_FC_S: lin_s(e->mh.fc, ptr, &b); break;
     case MI_T_MTP_PRE_E: *ptr = e->mh.pre_e; b = size_t(m.hidden) * 4; break;
@@ -1183,13 +1131,6 @@ int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t ch
   if (!e) return mi_fail(MI_ERR_ARG, "engine_prefill: null");
   MI_TRY(e->prefill(ids, n, chunk));
   return e->check_handoff();  // the last position's logits: a non-finite one fails the call
-}
-
-int mi_engine_chain(mi_engine* e, uint32_t on, uint32_t* wgs) {
-  if (!e) return mi_fail(MI_ERR_ARG, "engine_chain: null");
-  MI_TRY(e->set_chain(on != 0));
-  if (wgs) *wgs = e->use_chain ? mi::chain_wgs(e->chain) : 0u;
-  return 0;
 }
 
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch) {
