@@ -174,6 +174,21 @@ typedef struct mi_gemv_epilogue {
    * [2^-17, 65504]; a larger value is stored as inf, which the logits' finiteness check
    * reports). The linears read those activations as they are. */
   uint32_t act;
+  /* The RMSNorm split across two launches (no reference counterpart: the reference forms the
+   * norm in res_norm, capture.cc:997, a launch of its own): RESID with sums_out set writes
+   * resid and the 64-column tiles' sums of squares, sums_out [M][N/64] (plain stores),
+   * followed by M words set to 0xFFFFFFFF, and nothing else (sumsq, rstd, next_norm_w, x_next
+   * unused); the launch that reads the norm then forms it: with in_sums set (the PARTIALS,
+   * SILU or QKV kind; K a multiple of 256 up to 16384, at most 8 k-groups per slice) x is
+   * that residual [M][K] and the input is rne(x * rstd * in_norm_w), rstd = 1/sqrt(sum_g
+   * in_sums[m][g] / K + in_eps) with the sums added in ascending g from +0 - RESID's x_next
+   * bit for bit. in_sums has the same layout: the M words after the sums hold 0xFFFFFFFF or
+   * the rstd of these sums (the launch's work-groups share the rstd through them, so the
+   * first ones form it and the later ones read it). */
+  float* sums_out;
+  const float* in_sums;
+  const float* in_norm_w;
+  float in_eps;
 } mi_gemv_epilogue;
 int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales, const uint16_t* x,
                      float* partials, uint32_t M, uint32_t K, uint32_t N, uint32_t S,

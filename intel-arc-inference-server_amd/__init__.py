@@ -122,7 +122,8 @@ class GemvEpilogue(C.Structure):
                 ("ctrl", vp), ("shape", vp), ("q_norm", vp), ("k_norm", vp), ("rope", vp), ("attn_q", vp),
                 ("kv_k", vp), ("kv_v", vp), ("row_stride", sz), ("head_stride", sz), ("pages", vp),
                 ("page", u32), ("kv_len", u32), ("status", vp), ("poll_limit", u32), ("inject", u32),
-                ("arrive", vp), ("act", u32)]
+                ("arrive", vp), ("act", u32), ("sums_out", vp), ("in_sums", vp), ("in_norm_w", vp),
+                ("in_eps", f32)]
 
 
 STATUS_HANDOFF_TIMEOUT = 0xDEAD0003

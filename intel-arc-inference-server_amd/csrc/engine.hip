@@ -147,6 +147,7 @@ struct mi_engine {
   float* logits = nullptr;
   void* argmax_part = nullptr;
   float* rstd = nullptr;
+  float* nsum = nullptr;  // a residual's tile sums of squares [M][hidden / 64] and M rstd words, for the next launch's norm
   float* moe_logits = nullptr;   // [max_rows][router_n]
   uint32_t* moe_route = nullptr; // [max_rows][MI_MOE_ROUTE_WORDS]
   uint16_t* moe_h = nullptr;     // [max_rows][top_k + 1][moe_inter]
@@ -326,6 +327,7 @@ struct mi_engine {
     MI_TRY(alloc(&logits, size_t(R) * m.vocab));
     MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * (m.vocab / 64 + mi_argmax_groups(m.vocab))));
     MI_TRY(alloc(&rstd, R));
+    MI_TRY(alloc(&nsum, size_t(R) * (m.hidden / 64 + 1)));
     if (moe) {
       MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
       MI_TRY(alloc(&moe_route, size_t(R) * MI_MOE_ROUTE_WORDS));
@@ -422,14 +424,32 @@ struct mi_engine {
   }
   uint32_t router_ksplit() const { return router_ksplit_of(d.hidden); }
 
-  mi_gemv_epilogue resid_epi(const float* next_w) const {
+  // The dense layers split each RMSNorm between two launches: o's and down's consumers write
+  // the residual and its tile sums (nsum) only, and gate||up (the next qkv) forms the norm
+  // itself for its slice, bitwise the x the consumers would have written; that spares the
+  // consumers' all-to-all exchange of tile sums. The last layer's down (the head's input, which
+  // the MTP head copies too) and MoE layers (the router and the experts read x) keep x.
+  // (The launches that form the norm take at most 8 k-groups per slice and 256 tile sums: a
+  // model whose split-K widths leave more keeps x throughout.)
+  bool split_norm() const {
+    if (d.experts || d.hidden / 64 > 256 || (d.hidden / 64) % 4) return false;
+    auto ok = [](const Linear& l) { return (l.K / 64) / l.S <= 8; };
+    for (uint32_t li = 0; li < d.layers; ++li)
+      if (!ok(layer[li].qkv) || !ok(layer[li].gate_up)) return false;
+    return !d.mtp || ok(mh.L.gate_up);
+  }
+  mi_gemv_epilogue resid_epi(const float* next_w, bool sums_only) const {
     mi_gemv_epilogue e{};
     e.kind = MI_EPI_RESID;
     e.resid = resid;
-    e.sumsq = sumsq;
-    e.rstd = rstd;
-    e.next_norm_w = next_w;
-    e.x_next = x;
+    if (sums_only) {
+      e.sums_out = nsum;
+    } else {
+      e.sumsq = sumsq;
+      e.rstd = rstd;
+      e.next_norm_w = next_w;
+      e.x_next = x;
+    }
     e.eps = d.rms_eps;
     e.status = ctrl + MI_CTRL_DEBUG;
     e.arrive = use_arrive ? arrive : nullptr;
@@ -453,7 +473,7 @@ struct mi_engine {
                              d.act_bf16, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      MI_TRY(launch_qkv(li, M));
+      MI_TRY(launch_qkv(li, M, li > 0 && split_norm()));
       if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
         int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
         int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
@@ -483,7 +503,7 @@ struct mi_engine {
         continue;
       }
       MI_TRY(launch_gate_up(L, M));
-      MI_TRY(launch_down(L, M, next_w));
+      MI_TRY(launch_down(L, M, next_w, split_norm() && li + 1 < d.layers));
     }
     MI_TRY(head(ctrl, M, x, logits, history));
     if (d.mtp) {
@@ -538,7 +558,7 @@ struct mi_engine {
       MI_TRY(moe_block(mh.L, 1, mh.final_n));
     } else {
       MI_TRY(launch_gate_up(mh.L, 1));
-      MI_TRY(launch_down(mh.L, 1, mh.final_n));
+      MI_TRY(launch_down(mh.L, 1, mh.final_n, false));
     }
     MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(dh, x, size_t(d.hidden) * 2, hipMemcpyDeviceToDevice, stream)),
                   "dh"));
@@ -566,19 +586,33 @@ struct mi_engine {
 
   // the qkv GEMV of layer li; with the f16 cache and M <= 4, attn_prep inside it (one consumer
   // work-group per head), else plain partials for mi_attn_prep / mi_attn_prep_kv8
-  int launch_qkv(uint32_t li, uint32_t M) {
+  // the qkv GEMV's input: x, or (ni) the residual with nsum, the layer's input norm formed by
+  // the launch
+  int qkv_plain(const Layer& L, uint32_t M, bool ni) {
+    if (!ni) return mi_gemv_w4a16(L.qkv.q, L.qkv.s, x, part, M, L.qkv.K, L.qkv.N, L.qkv.S, stream);
+    mi_gemv_epilogue ep{};
+    ep.kind = MI_EPI_PARTIALS;
+    norm_in(ep, L.in_norm);
+    return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, resid, part, M, L.qkv.K, L.qkv.N, L.qkv.S, &ep, stream);
+  }
+  void norm_in(mi_gemv_epilogue& e, const float* w) const {
+    e.in_sums = nsum;
+    e.in_norm_w = w;
+    e.in_eps = d.rms_eps;
+    e.act = d.act_bf16;
+  }
+  int launch_qkv(uint32_t li, uint32_t M, bool ni) {
     const size_t layer_kv = size_t(d.kv_heads) * d.max_len * d.head_dim;
-    if (d.kv_int8) return mi_gemv_w4a16(layer[li].qkv.q, layer[li].qkv.s, x, part, M, layer[li].qkv.K,
-                                        layer[li].qkv.N, layer[li].qkv.S, stream);
+    if (d.kv_int8) return qkv_plain(layer[li], M, ni);
     return launch_qkv_on(layer[li], ctrl, static_cast<uint16_t*>(kv_k) + li * layer_kv,
-                         static_cast<uint16_t*>(kv_v) + li * layer_kv, M, false);
+                         static_cast<uint16_t*>(kv_v) + li * layer_kv, M, false, ni);
   }
   // layer L's qkv on control block c, K/V rows into the f16 layer lk / lv; prep: run attn_prep
-  // here too when it is not fused (M > 4)
-  int launch_qkv_on(const Layer& L, uint32_t* c, uint16_t* lk, uint16_t* lv, uint32_t M, bool prep) {
+  // here too when it is not fused (M > 4); ni: the input norm formed by the launch
+  int launch_qkv_on(const Layer& L, uint32_t* c, uint16_t* lk, uint16_t* lv, uint32_t M, bool prep, bool ni = false) {
     const uint32_t HD = d.head_dim;
     if (!qkv_is_fused(M)) {
-      MI_TRY(mi_gemv_w4a16(L.qkv.q, L.qkv.s, x, part, M, L.qkv.K, L.qkv.N, L.qkv.S, stream));
+      MI_TRY(qkv_plain(L, M, ni));
       return prep ? mi_attn_prep(c, part, L.qkv.S, M, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr, lk, lv, HD,
                                  size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream)
                   : 0;
@@ -599,7 +633,8 @@ struct mi_engine {
     eq.status = ctrl + MI_CTRL_DEBUG;
     eq.arrive = use_arrive ? arrive : nullptr;
     eq.act = d.act_bf16;
-    return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream);
+    if (ni) norm_in(eq, L.in_norm);
+    return mi_gemv_w4a16_ex(L.qkv.q, L.qkv.s, ni ? resid : x, part_ex, M, L.qkv.K, L.qkv.N, L.qkv.S, &eq, stream);
   }
   // the f16 cache's attention pair on control block c over the layer lk / lv: attn_prep first
   // when `prep` (the qkv launch did not fuse it); verify_attn.h's rule picks the many-row kernel for
@@ -620,7 +655,7 @@ struct mi_engine {
   }
   // o with the residual fold and the post-attention norm
   int launch_o(const Layer& L, uint32_t M) {
-    const mi_gemv_epilogue eo = resid_epi(L.post_norm);
+    const mi_gemv_epilogue eo = resid_epi(L.post_norm, split_norm());
     return mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream);
   }
   // gate||up with silu * up
@@ -631,12 +666,14 @@ struct mi_engine {
     eg.status = ctrl + MI_CTRL_DEBUG;
     eg.arrive = use_arrive ? arrive : nullptr;
     eg.act = d.act_bf16;
-    return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, x, part_ex, M, L.gate_up.K, L.gate_up.N, L.gate_up.S, &eg,
-                            stream);
+    if (split_norm()) norm_in(eg, L.post_norm);
+    return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, split_norm() ? resid : x, part_ex, M, L.gate_up.K,
+                            L.gate_up.N, L.gate_up.S, &eg, stream);
   }
-  // down with the residual fold and the next norm (the next layer's, the final one, the head's)
-  int launch_down(const Layer& L, uint32_t M, const float* next_w) {
-    const mi_gemv_epilogue ed = resid_epi(next_w);
+  // down with the residual fold and the next norm (the next layer's, the final one, the head's);
+  // sums_only: the residual and its tile sums only (the next qkv forms the norm)
+  int launch_down(const Layer& L, uint32_t M, const float* next_w, bool sums_only) {
+    const mi_gemv_epilogue ed = resid_epi(next_w, sums_only);
     return mi_gemv_w4a16_ex(L.down.q, L.down.s, hbuf, part_ex, M, L.down.K, L.down.N, L.down.S, &ed, stream);
   }
   // the int4 lm_head with the logits and the per-tile argmax
@@ -661,10 +698,10 @@ struct mi_engine {
       return mi_fail(MI_ERR_SHAPE, "engine_bench_linear: an MoE model has no dense gate_up / down");
     auto one = [&](uint32_t li) -> int {
       switch (which) {
-        case 0: return launch_qkv(li, 1);
+        case 0: return launch_qkv(li, 1, li > 0 && split_norm());
         case 1: return launch_o(layer[li], 1);
         case 2: return launch_gate_up(layer[li], 1);
-        case 3: return launch_down(layer[li], 1, next_norm(li));
+        case 3: return launch_down(layer[li], 1, next_norm(li), split_norm() && li + 1 < d.layers);
         default:
           return d.lm_head_int8 ? mi_gemv_i8w(lm_i8, lm_i8s, x, logits, 1, d.hidden, d.vocab, stream)
                                 : launch_lm_head(1, x, logits);

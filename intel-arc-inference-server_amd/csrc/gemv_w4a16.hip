@@ -113,6 +113,13 @@ struct GemvEpi {
   uint32_t* arrive;     // per-tile (QKV: per-head) arrival counts, zero between launches; NULL:
                         // the fixed consumers (slice S-1; QKV's extra row)
   uint32_t act;         // 0: f16 activations; 1: bf16 (roundings to bf16, residual in bf16 bits)
+  // the norm split across two launches: RESID with sums_out writes the residual and its tiles'
+  // sums of squares [M][N/64] only; a launch with in_sums ([M][K/64]) reads x as that residual
+  // and forms rne(x * rstd * in_norm_w) itself
+  float* sums_out;
+  const float* in_sums;
+  const float* in_norm_w;
+  float in_eps;
 };
 
 // arrival words sit 128 bytes apart: no two tiles' counts share a cache line
@@ -321,8 +328,44 @@ __device__ __forceinline__ void qkv_consumer(const float* partials, uint32_t M, 
   }
 }
 
-// MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue.
-template <int MR, int U, int EPI>
+// sum_{g < n} p[g] from +0 in ascending g, p in LDS: the words read 32 / 16 / 4 at a time in
+// 16-byte reads (p 16-byte aligned, n % 4 == 0), so the chain of adds waits on the LDS a few
+// times rather than once per pair of words
+__device__ __forceinline__ float lds_seq_sum(const float* p, uint32_t n) {
+  float tot = 0.f;
+  uint32_t g = 0;
+  const f4_t* p4 = reinterpret_cast<const f4_t*>(p);
+  auto add4 = [&](const f4_t& v) {
+    tot += v[0];
+    tot += v[1];
+    tot += v[2];
+    tot += v[3];
+  };
+  for (; g + 32u <= n; g += 32u) {
+    f4_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = p4[g / 4u + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) add4(v[j]);
+  }
+  if (g + 16u <= n) {
+    f4_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = p4[g / 4u + j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) add4(v[j]);
+    g += 16u;
+  }
+  for (; g < n; g += 4u) add4(p4[g / 4u]);
+  return tot;
+}
+
+// MR: row capacity (1, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue;
+// NI: the input is the RMSNorm of a residual, formed by each work-group for its slice (while
+// its first weight loads are in flight): every row's rstd from the residual's tile sums, added in
+// tile order from +0 as the RESID consumers add them, then rne((r * rstd) * w) per element -
+// the RESID kind's x_next bit for bit - into LDS, where the slice reads it.
+template <int MR, int U, int EPI, bool NI = false>
 __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ x,
@@ -353,9 +396,109 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
 #pragma unroll
     for (int r = 0; r < RR; ++r) acc[c][r] = 0.f;
 
+  u4_t wv[U][2];
+  u2_t sv[U];
+  auto load_w = [&](uint32_t g0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = g0 + u * kWaves;
+      if (g < g_end) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) wv[u][h] = load_stream16(qweight + (size_t)(g * 8u + 4u * h + q) * N + ncol);
+        sv[u] = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + ncol);
+      }
+    }
+  };
+  // NI: the slice's input rows, f16 pairs [M][gps * 32] (the tile sums pass through first)
+  constexpr uint32_t XIN = NI ? (uint32_t)MR * 256u : 1u;
+  __shared__ __align__(16) uint32_t s_xin[XIN];
+  __shared__ __align__(16) float s_nsum[NI && MR == 1 ? 256 : 1];  // one row's tile sums
+  if constexpr (NI) {
+    if (!xrow_c) {  // uniform: the extra consumer row has no slice
+      const uint32_t t = threadIdx.x, nt = K / 64u, kw = gps * 32u, nwords = M * kw;
+      const uint32_t k0 = s * gps * 64u;
+      float sm[MR];
+      uint32_t rw[MR];
+      float w0[MR], w1[MR];
+      // the rows' rstd, when a work-group of this launch has already formed it: the words
+      // after the sums (empty until then)
+      const uint32_t* rcache = reinterpret_cast<const uint32_t*>(epi.in_sums) + M * nt;
+      const uint32_t rc = ld_agent(rcache + (MR == 1 ? 0u : min(t, M - 1u)));
+#pragma unroll
+      for (int u = 0; u < MR; ++u) {
+        const uint32_t e = t + 256u * u;
+        if (e < M * nt) sm[u] = epi.in_sums[e];
+        if (e < nwords) {
+          const uint32_t row = e / kw, k = k0 + 2u * (e - row * kw);
+          rw[u] = *reinterpret_cast<const uint32_t*>(x + (size_t)row * K + k);
+          w0[u] = epi.in_norm_w[k];
+          w1[u] = epi.in_norm_w[k + 1u];
+        }
+      }
+      // then the first batch's weights: the waits for the loads above (retired in order) do
+      // not wait for them
+      // (unconditionally, a missing group re-reading the slice's last: a load under a branch
+      // makes every later wait a wait for everything)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t g = min(g_begin + u * kWaves, g_end - 1u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) wv[u][h] = load_stream16(qweight + (size_t)(g * 8u + 4u * h + q) * N + ncol);
+        sv[u] = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + ncol);
+      }
+#pragma unroll
+      for (int u = 0; u < MR; ++u)
+        if (t + 256u * u < M * nt) {
+          if constexpr (MR == 1) s_nsum[t] = sm[u];
+          else s_xin[t + 256u * u] = __builtin_bit_cast(uint32_t, sm[u]);
+        }
+      __syncthreads();
+      // the rows' rstd: at one row every thread adds the sums itself (one broadcast LDS read
+      // per word for a whole wave), so no barrier waits for one thread's chain of adds, and
+      // the sums keep their own words; at more rows thread m adds row m's
+      float rs1 = 0.f;
+      __shared__ float s_rstd_in[MR];
+      // (a pure function of the sums; the grid's first work-group stores it: stores from every
+      // work-group to one word would queue behind each other for tens of microseconds)
+      uint32_t* rcw = const_cast<uint32_t*>(rcache);
+      const bool keeper = blockIdx.x == 0 && blockIdx.y == 0;
+      if constexpr (MR == 1) {
+        if (rc != kEmpty) {
+          rs1 = __builtin_bit_cast(float, rc);
+        } else {
+          rs1 = 1.0f / sqrtf(lds_seq_sum(s_nsum, nt) / (float)K + epi.in_eps);
+          if (keeper && t == 0) st_agent(rcw, __builtin_bit_cast(uint32_t, rs1));
+        }
+      } else {
+        if (t < M) {
+          float r;
+          if (rc != kEmpty) {
+            r = __builtin_bit_cast(float, rc);
+          } else {
+            const float* sp = reinterpret_cast<const float*>(s_xin) + t * nt;
+            r = 1.0f / sqrtf(lds_seq_sum(sp, nt) / (float)K + epi.in_eps);
+            if (keeper) st_agent(rcw + t, __builtin_bit_cast(uint32_t, r));
+          }
+          s_rstd_in[t] = r;
+        }
+        __syncthreads();  // (also: the sums' words are overwritten with x below)
+      }
+#pragma unroll
+      for (int u = 0; u < MR; ++u) {
+        const uint32_t e = t + 256u * u;
+        if (e < nwords) {
+          const float rs = MR == 1 ? rs1 : s_rstd_in[e / kw];
+          const uint16_t x0 = act_enc(res_widen((uint16_t)(rw[u] & 0xFFFFu), epi.act) * rs * w0[u], epi.act);
+          const uint16_t x1 = act_enc(res_widen((uint16_t)(rw[u] >> 16), epi.act) * rs * w1[u], epi.act);
+          s_xin[e] = (uint32_t)x0 | ((uint32_t)x1 << 16);
+        }
+      }
+      __syncthreads();
+    }
+  }
+
   for (uint32_t g0 = g_begin; g0 < g_end; g0 += kWaves * U) {
-    u4_t wv[U][2];
-    u2_t sv[U];
+    if (!NI || g0 != g_begin) load_w(g0);
     u4_t xv[U][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -363,14 +506,13 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       if (g < g_end) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const uint32_t row = g * 8u + 4u * h + q;
-          wv[u][h] = load_stream16(qweight + (size_t)row * N + ncol);
-          if (xrow)
-            xv[u][h] = *reinterpret_cast<const u4_t*>(x + (size_t)c4 * K + g * 64u + 32u * h + 8u * q);
-          else
+          if (!xrow)
             xv[u][h] = u4_t{0u, 0u, 0u, 0u};
+          else if constexpr (NI)
+            xv[u][h] = *reinterpret_cast<const u4_t*>(s_xin + c4 * (gps * 32u) + (g - s * gps) * 32u + 16u * h + 4u * q);
+          else
+            xv[u][h] = *reinterpret_cast<const u4_t*>(x + (size_t)c4 * K + g * 64u + 32u * h + 8u * q);
         }
-        sv[u] = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + ncol);
       }
     }
 #pragma unroll
@@ -469,7 +611,7 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       const uint32_t row = wave + kWaves * k;
       if (row < M) r_pre[k] = epi.resid[(size_t)row * N + n0 + lane];
     }
-    w_pre = epi.next_w[n0 + lane];
+    if (!epi.sums_out) w_pre = epi.next_w[n0 + lane];  // (the split form has no norm weights)
   }
   constexpr int kFoldBuf = fold_buf<MR, EPI>();
   __shared__ float s_fold[kFoldBuf];
@@ -521,8 +663,16 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
 #pragma unroll
       for (int st = 32; st > 0; st >>= 1) a += __shfl_down(a, st, 64);
       a = publishable(__shfl(a, 0, 64));
+      if (epi.sums_out) {  // the next launch forms the norm
+        if (lane == 0) epi.sums_out[(size_t)row * ntiles + tile] = a;
+        continue;
+      }
       // every consumer c gets its own copy: sumsq[c][row][tile]
       for (uint32_t c = lane; c < ntiles; c += 64u) st_agent(epi.sumsq + ((size_t)c * M + row) * ntiles + tile, a);
+    }
+    if (epi.sums_out) {  // uniform; the rstd words after the sums are empty again
+      if (tile == 0 && t < M) reinterpret_cast<uint32_t*>(epi.sums_out)[(size_t)M * ntiles + t] = kEmpty;
+      return;
     }
     // all tiles' sums of this launch: sumsq[tile][row][g], g ascending, polled in rounds of rows
     __shared__ float s_rstd[16];
@@ -610,6 +760,12 @@ int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float
   GemvEpi e = epi;
   e.extra_row = EPI == EPI_RESID && !epi.arrive && kExtraRow;
   dim3 grid(N / kCols, (EPI == EPI_QKV || e.extra_row) && !epi.arrive ? S + 1 : S);
+  if constexpr (EPI == EPI_PARTIALS || EPI == EPI_SILU || EPI == EPI_QKV) {
+    if (epi.in_sums) {
+      gemv_w4a16_kernel<MR, 2, EPI, true><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
+      return (int)hipGetLastError();
+    }
+  }
   if (gps >= 16)
     gemv_w4a16_kernel<MR, 4, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
   else
@@ -698,14 +854,26 @@ extern "C" int mi_gemv_w4a16_ex(const uint32_t* qweight, const uint16_t* scales,
   e.arrive = ep->arrive;
   if (ep->act > 1) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: act is 0 (f16) or 1 (bf16)");
   e.act = ep->act;
+  e.sums_out = ep->sums_out;
+  e.in_sums = ep->in_sums;
+  e.in_norm_w = ep->in_norm_w;
+  e.in_eps = ep->in_eps;
+  if (e.in_sums) {
+    if (!e.in_norm_w) return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex: in_sums needs in_norm_w");
+    if (ep->kind != MI_EPI_PARTIALS && ep->kind != MI_EPI_SILU && ep->kind != MI_EPI_QKV)
+      return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex: in_sums with the PARTIALS, SILU or QKV kind only");
+    if (K / 64 > 256 || (K / 64) % 4 || (K / 64) / S > 8)
+      return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex: in_sums needs K a multiple of 256 up to 16384 and at most 8 "
+                                   "k-groups per slice");
+  }
   int r;
   switch (ep->kind) {
     case MI_EPI_PARTIALS:
       r = launch_rows<EPI_PARTIALS>(qweight, scales, x, partials, M, K, N, S, e, st);
       break;
     case MI_EPI_RESID:
-      if (!e.resid || !e.sumsq || !e.rstd || !e.next_w || !e.x_next)
-        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex RESID: resid, sumsq, rstd, next_norm_w and x_next are required");
+      if (!e.resid || (!e.sums_out && (!e.sumsq || !e.rstd || !e.next_w || !e.x_next)))
+        return mi_fail(MI_ERR_ARG, "gemv_w4a16_ex RESID: resid, and sums_out or sumsq, rstd, next_norm_w and x_next are required");
       if (N > 16384)  // every tile's consumer must be resident at once (N/64 <= 256 work-groups)
         return mi_fail(MI_ERR_SHAPE, "gemv_w4a16_ex RESID: N must be <= 16384");
       r = launch_rows<EPI_RESID>(qweight, scales, x, partials, M, K, N, S, e, st);
