@@ -46,7 +46,11 @@ enum {
 };
 
 /* Control block word indices (src/runtime/control.h:13-24: pos, n_active, cur_token[8],
- * out_token[8], debug_flag), plus the step counter this library keeps after them. */
+ * out_token[8], debug_flag), plus the step counter this library keeps after them; and the
+ * many-row lists' id slots at the reference's offsets (control.h:35-42): a list of 9..16 rows
+ * reads its ids at MI_CTRL_WIDE_CUR and writes its argmaxes at MI_CTRL_WIDE_OUT, a list of
+ * 17..64 rows at MI_CTRL_DEEP_CUR / MI_CTRL_DEEP_OUT; lists of up to 8 rows at MI_CTRL_CUR /
+ * MI_CTRL_OUT. Every list leaves its last row's argmax at MI_CTRL_CUR. */
 enum {
   MI_CTRL_POS = 0,
   MI_CTRL_NACT = 1,
@@ -54,7 +58,11 @@ enum {
   MI_CTRL_OUT = 10,
   MI_CTRL_DEBUG = 18,
   MI_CTRL_STEPS = 19,
-  MI_CTRL_WORDS = 64
+  MI_CTRL_WIDE_CUR = 32,
+  MI_CTRL_WIDE_OUT = 48,
+  MI_CTRL_DEEP_CUR = 64,
+  MI_CTRL_DEEP_OUT = 128,
+  MI_CTRL_WORDS = 192
 };
 
 const char* mi_last_error(void);
@@ -493,7 +501,8 @@ typedef struct mi_model_desc {
   uint32_t layers, hidden, q_heads, kv_heads, head_dim, rot_dim, inter, vocab, vocab_used;
   uint32_t max_len;  /* KV cache rows per layer (positions) */
   uint32_t qk_norm;  /* 1: per-head RMSNorm on q and k (attn.cl attn_prep) */
-  uint32_t max_rows; /* largest verify step (rows) the engine captures, 1..8 */
+  uint32_t max_rows; /* largest verify step (rows) the engine captures, 1..64 (above 8: no
+                      * MTP head; such lists run as row chunks of 8, see mi_engine_verify) */
   uint32_t attn_tgt; /* attention blocks per kv head (the v2 grid's TGT) */
   float rope_theta, rms_eps;
   /* experts > 0: every layer's MLP is a mixture-of-experts block (moe.cl) of `experts`
@@ -596,7 +605,11 @@ int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
  * the step's state: reset the engine (mi_engine_reset) before generating again. */
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
- * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. With the MTP head
+ * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. k + 1 <= max_rows;
+ * a list of more than 8 rows (the reference's wide and deep lists, verify_attn.h:65-92) runs
+ * every layer's linears, attn_prep and the head in row chunks of 8 and the attention over all
+ * rows at once (mi_attn_verify where mi_attn_verify_binds, else the decode kernel per chunk):
+ * each row's logits are those of the same row in a list of at most 8 rows. With the MTP head
  * the rows' post-final-norm hidden goes to hh rows 1..k+1 and the head's K/V are filled over
  * hh rows 0..k at positions pos - 1 .. pos + k - 1 (capture.cc:362-370); k > 0 needs pos >= 1. */
 int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t* argmax_rows);

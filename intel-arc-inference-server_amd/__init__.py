@@ -264,7 +264,8 @@ def desc_27b(max_len=4096 + 512, act_bf16=0):
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_MTP_FC_Q, T_MTP_FC_S,
  T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K, T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS,
  T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF) = range(32, 63)
-CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 64
+CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 192
+CTRL_WIDE_CUR, CTRL_WIDE_OUT, CTRL_DEEP_CUR, CTRL_DEEP_OUT = 32, 48, 64, 128
 
 
 class Engine:

@@ -59,6 +59,16 @@ struct Layer {
 __global__ void ctrl_set_kernel(uint32_t* ctrl, uint32_t word, uint32_t value) {
   if (threadIdx.x == 0) ctrl[word] = value;
 }
+// A list's id and argmax slots (control.h:35-42): up to 8 rows at cur_token / out_token, 9..16
+// at wide_cur / wide_out, 17..64 at deep_cur / deep_out.
+__host__ __device__ inline uint32_t ctrl_cur_at(uint32_t M) {
+  return M <= 8 ? MI_CTRL_CUR : M <= 16 ? MI_CTRL_WIDE_CUR : MI_CTRL_DEEP_CUR;
+}
+__host__ __device__ inline uint32_t ctrl_out_at(uint32_t M) {
+  return M <= 8 ? MI_CTRL_OUT : M <= 16 ? MI_CTRL_WIDE_OUT : MI_CTRL_DEEP_OUT;
+}
+constexpr uint32_t kRowChunk = 8;  // rows per launch in a list of more than 8 rows
+
 __global__ void ctrl_set_rows_kernel(uint32_t* ctrl, uint32_t pos, uint32_t n_act, const uint32_t* ids,
                                      uint32_t n_ids) {
   const uint32_t t = threadIdx.x;
@@ -66,7 +76,47 @@ __global__ void ctrl_set_rows_kernel(uint32_t* ctrl, uint32_t pos, uint32_t n_ac
     ctrl[MI_CTRL_POS] = pos;
     ctrl[MI_CTRL_NACT] = n_act;
   }
-  if (t < n_ids) ctrl[MI_CTRL_CUR + t] = ids[t];
+  if (t < n_ids) ctrl[ctrl_cur_at(n_ids) + t] = ids[t];
+}
+
+
+// A many-row list's row chunks: chunk c's control block (cctl + c MI_CTRL_WORDS) holds the
+// position pos + 8 c, its active rows and its ids, so every launch of the chunk reads its rows
+// as an up-to-8-row list does. One thread per chunk.
+__global__ void chunk_ctrl_kernel(const uint32_t* ctrl, uint32_t* cctl, uint32_t M) {
+  const uint32_t c = threadIdx.x, nc = (M + kRowChunk - 1) / kRowChunk;
+  if (c >= nc) return;
+  uint32_t* cc = cctl + c * MI_CTRL_WORDS;
+  const uint32_t pos = ctrl[MI_CTRL_POS], n = ctrl[MI_CTRL_NACT], r0 = c * kRowChunk;
+  cc[MI_CTRL_POS] = pos + r0;
+  cc[MI_CTRL_NACT] = n > r0 ? min(n - r0, kRowChunk) : 0u;
+  cc[MI_CTRL_DEBUG] = 0u;
+  cc[MI_CTRL_STEPS] = 0u;
+  for (uint32_t i = 0; i < kRowChunk; ++i)
+    cc[MI_CTRL_CUR + i] = r0 + i < M ? ctrl[ctrl_cur_at(M) + r0 + i] : 0u;
+}
+// After the chunks' heads: their argmaxes into the list's out slots, then what argmax_stage2
+// does for a list (the last row's argmax as cur_token, the history entry, the step count, pos
+// advanced by the active rows), and the first flag a chunk raised.
+__global__ void chunk_gather_kernel(uint32_t* ctrl, const uint32_t* cctl, uint32_t M, uint32_t* history,
+                                    uint32_t history_len) {
+  const uint32_t t = threadIdx.x, n = ctrl[MI_CTRL_NACT], oo = ctrl_out_at(M);
+  if (t < M) ctrl[oo + t] = cctl[(t / kRowChunk) * MI_CTRL_WORDS + MI_CTRL_OUT + t % kRowChunk];
+  __syncthreads();
+  if (t == 0) {
+    for (uint32_t c = 0; c * kRowChunk < M; ++c) {
+      const uint32_t f = cctl[c * MI_CTRL_WORDS + MI_CTRL_DEBUG];
+      if (f && ctrl[MI_CTRL_DEBUG] == 0u) ctrl[MI_CTRL_DEBUG] = f;
+    }
+    if (n != 0u) {
+      const uint32_t tok = ctrl[oo + min(n, M) - 1u];
+      ctrl[MI_CTRL_CUR] = tok;
+      const uint32_t step = ctrl[MI_CTRL_STEPS];
+      if (history && step < history_len) history[step] = tok;
+      ctrl[MI_CTRL_STEPS] = step + 1u;
+      ctrl[MI_CTRL_POS] += n;
+    }
+  }
 }
 
 // The MTP head's control block for the K/V fill over a step's M rows (capture.cc:362-370):
@@ -155,7 +205,8 @@ struct mi_engine {
   uint32_t router_n = 0;
   size_t gu_block = 0, dn_block = 0;  // u32 per expert block
   mi_attn_shape ash{};
-  hipGraphExec_t graphs[17] = {};
+  hipGraphExec_t graphs[65] = {};
+  uint32_t* cctl = nullptr;  // a many-row list's row chunks' control blocks [8][MI_CTRL_WORDS]
   // the MTP head (d.mtp): weights, its one-layer KV cache, the hidden rows, the draft chain
   MtpHead mh;
   uint16_t* hkv_k = nullptr;  // [kv_heads][max_len][head_dim] f16
@@ -219,6 +270,9 @@ struct mi_engine {
     const mi_model_desc& m = d;
     const uint32_t H = m.hidden, HD = m.head_dim, QH = m.q_heads, KVH = m.kv_heads;
     const uint32_t R = m.max_rows;
+    // rows per launch: a list of more than 8 rows runs its launches in row chunks of 8, so the
+    // per-launch scratch (split-K partials, hand-off words, argmax parts) holds RL rows
+    const uint32_t RL = std::min(R, kRowChunk);
     const uint32_t qkv_n = (QH + 2 * KVH) * HD;
     ash = mi_attn_shape{QH, KVH, HD, m.rot_dim, 0u, qkv_n, QH * HD, (QH + KVH) * HD,
                         1.0f / std::sqrt(float(HD)), m.rms_eps, m.act_bf16};
@@ -248,10 +302,10 @@ struct mi_engine {
         MI_TRY(alloc(&L.q_norm, HD));
         MI_TRY(alloc(&L.k_norm, HD));
       }
-      if (L.qkv.q) part_max = std::max(part_max, size_t(L.qkv.S) * R * L.qkv.N);
+      if (L.qkv.q) part_max = std::max(part_max, size_t(L.qkv.S) * RL * L.qkv.N);
       for (const Linear* l : {&L.o, &L.gate_up, &L.down})
-        if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S) * R * l->N);
-      part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(R, 4u) * L.qkv.N);  // QKV: all S slices
+        if (l->q) part_ex_max = std::max(part_ex_max, size_t(l->S) * RL * l->N);
+      part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(RL, 4u) * L.qkv.N);  // QKV: all S slices
     }
     if (m.mtp) {  // the head: fc (plain partials) and a dense layer at the model's shapes
       MI_TRY(alloc_linear(mh.fc, 2 * H, H, 0));
@@ -289,7 +343,7 @@ struct mi_engine {
       MI_TRY(alloc(&lm_i8s, m.vocab));
     } else {
       MI_TRY(alloc_linear(lm_head, H, m.vocab, MI_EPI_LOGITS));
-      part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * R * m.vocab);
+      part_ex_max = std::max(part_ex_max, size_t(lm_head.S) * RL * m.vocab);
     }
     MI_TRY(alloc(&embed, size_t(m.vocab) * H));
     MI_TRY(alloc(&final_norm, H));
@@ -307,7 +361,8 @@ struct mi_engine {
     }
     MI_TRY(alloc(&ctrl, MI_CTRL_WORDS));
     MI_TRY(alloc(&history, m.max_len));
-    MI_TRY(alloc(&ids_dev, 32));
+    MI_TRY(alloc(&ids_dev, 64));
+    if (R > kRowChunk) MI_TRY(alloc(&cctl, size_t(kRowChunk) * MI_CTRL_WORDS));
     MI_TRY(alloc(&resid, size_t(R) * H));
     MI_TRY(alloc(&x, size_t(R) * std::max(H, QH * HD)));
     MI_TRY(alloc(&hbuf, size_t(R) * m.inter));
@@ -316,7 +371,7 @@ struct mi_engine {
     MI_TRY(alloc(&part_ex, part_ex_max));
     part_ex_n = part_ex_max;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_max, stream));
-    sumsq_n = size_t(H / 64) * R * (H / 64);
+    sumsq_n = size_t(H / 64) * RL * (H / 64);
     MI_TRY(alloc(&sumsq, sumsq_n));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
     arrive_n = 32 * std::max<size_t>({m.vocab / 64, 2 * m.inter / 64, qkv_n / 64, H / 64});
@@ -325,15 +380,15 @@ struct mi_engine {
     MI_TRY(alloc(&attn_q, size_t(R) * QH * HD));
     MI_TRY(alloc(&attn_part, size_t(QH) * m.attn_tgt * R * (HD + 2)));
     MI_TRY(alloc(&logits, size_t(R) * m.vocab));
-    MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(R) * (m.vocab / 64 + mi_argmax_groups(m.vocab))));
+    MI_TRY(alloc(reinterpret_cast<uint64_t**>(&argmax_part), size_t(RL) * (m.vocab / 64 + mi_argmax_groups(m.vocab))));
     MI_TRY(alloc(&rstd, R));
     MI_TRY(alloc(&nsum, size_t(R) * (m.hidden / 64 + 1)));
     if (moe) {
       MI_TRY(alloc(&moe_logits, size_t(R) * router_n));
       MI_TRY(alloc(&moe_route, size_t(R) * MI_MOE_ROUTE_WORDS));
       MI_TRY(alloc(&moe_h, size_t(R) * (m.top_k + 1) * m.moe_inter));
-      MI_TRY(alloc(&dn_words, size_t(R) * (H / 2)));
-      MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(R) * (H / 2), stream));
+      MI_TRY(alloc(&dn_words, size_t(RL) * (H / 2)));
+      MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(RL) * (H / 2), stream));
     }
 
     // synthetic weights (BASELINE config 2's distributions)
@@ -463,6 +518,7 @@ struct mi_engine {
   // gate||up GEMV with silu*up fused; down GEMV with the residual fold + next norm fused.
   // (The int8 cache or M > 4: the qkv partials and attn_prep apart.)
   int enqueue_step(uint32_t M) {
+    if (M > kRowChunk) return enqueue_wide(M);
     const uint32_t HD = d.head_dim, KVH = d.kv_heads;
     const size_t layer_kv = size_t(KVH) * d.max_len * HD;
     if (d.mtp) {  // the head's control block for this step's K/V fill, before argmax moves ctrl
@@ -519,6 +575,125 @@ struct mi_engine {
                       "hh commit"));
     }
     return 0;
+  }
+
+  // Row chunk c of a many-row list: while the guard lives, the row buffers point at the chunk's
+  // rows and ctrl at the chunk's control block, so the launches serve a chunk exactly as they
+  // serve a list of up to 8 rows.
+  struct RowShift {
+    mi_engine& e;
+    uint32_t* ctrl;
+    uint16_t *x, *resid, *attn_out, *hbuf, *moe_h;
+    float *rstd, *nsum, *attn_q, *logits, *moe_logits;
+    uint32_t* moe_route;
+    RowShift(mi_engine& en, uint32_t c)
+        : e(en), ctrl(en.ctrl), x(en.x), resid(en.resid), attn_out(en.attn_out), hbuf(en.hbuf), moe_h(en.moe_h),
+          rstd(en.rstd), nsum(en.nsum), attn_q(en.attn_q), logits(en.logits), moe_logits(en.moe_logits),
+          moe_route(en.moe_route) {
+      const mi_model_desc& d = en.d;
+      const size_t r0 = size_t(c) * kRowChunk, qd = size_t(d.q_heads) * d.head_dim;
+      e.ctrl = en.cctl + size_t(c) * MI_CTRL_WORDS;
+      e.x += r0 * d.hidden;
+      e.resid += r0 * d.hidden;
+      e.rstd += r0;
+      e.nsum += r0 * (d.hidden / 64 + 1);
+      e.attn_q += r0 * qd;
+      e.attn_out += r0 * qd;
+      e.hbuf += r0 * d.inter;
+      e.logits += r0 * d.vocab;
+      if (e.moe_logits) {
+        e.moe_logits += r0 * en.router_n;
+        e.moe_route += r0 * MI_MOE_ROUTE_WORDS;
+        e.moe_h += r0 * (d.top_k + 1) * d.moe_inter;
+      }
+    }
+    ~RowShift() {
+      e.ctrl = ctrl; e.x = x; e.resid = resid; e.attn_out = attn_out; e.hbuf = hbuf; e.moe_h = moe_h;
+      e.rstd = rstd; e.nsum = nsum; e.attn_q = attn_q; e.logits = logits; e.moe_logits = moe_logits;
+      e.moe_route = moe_route;
+    }
+  };
+
+  // A list of 9..64 rows (the reference's wide and deep verify lists, control.h:35-42,
+  // verify_attn.h:65-92): per layer the qkv GEMV and attn_prep chunk by chunk (8 rows each, at
+  // positions pos + 8 c ..), then the attention over all rows at once - mi_attn_verify where
+  // the rule binds it, else the decode kernel chunk by chunk (the K/V rows of every chunk are
+  // written by then) - then o, gate||up and down chunk by chunk; the head per chunk; then the
+  // chunks' argmaxes into the list's out slots and pos advanced (chunk_gather_kernel). Every
+  // row is the same row of an up-to-8-row list: the GEMV rows do not depend on the launch's
+  // rows (property R), nor do attn_prep's or the decode kernel's.
+  int enqueue_wide(uint32_t M) {
+    const uint32_t HD = d.head_dim, KVH = d.kv_heads, nc = (M + kRowChunk - 1) / kRowChunk;
+    const size_t layer_kv = size_t(KVH) * d.max_len * HD;
+    auto rows = [&](uint32_t c) { return std::min(kRowChunk, M - c * kRowChunk); };
+    chunk_ctrl_kernel<<<1, 64, 0, stream>>>(ctrl, cctl, M);
+    MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "chunk_ctrl"));
+    for (uint32_t c = 0; c < nc; ++c) {
+      RowShift r(*this, c);
+      MI_TRY(mi_embed_norm_act(ctrl, embed, resid, layer[0].in_norm, x, rstd, rows(c), d.hidden, d.vocab, d.rms_eps,
+                               d.act_bf16, stream));
+    }
+    const bool verify_attn = !d.kv_int8 && mi_attn_verify_binds(M, 0, d.q_heads, d.kv_heads);
+    for (uint32_t li = 0; li < d.layers; ++li) {
+      const Layer& L = layer[li];
+      const bool ni = li > 0 && split_norm();
+      void* lk = d.kv_int8 ? static_cast<void*>(static_cast<int8_t*>(kv_k) + li * layer_kv)
+                           : static_cast<void*>(static_cast<uint16_t*>(kv_k) + li * layer_kv);
+      void* lv = d.kv_int8 ? static_cast<void*>(static_cast<int8_t*>(kv_v) + li * layer_kv)
+                           : static_cast<void*>(static_cast<uint16_t*>(kv_v) + li * layer_kv);
+      uint16_t* lks = d.kv_int8 ? kv_ks + size_t(li) * KVH * d.max_len : nullptr;
+      uint16_t* lvs = d.kv_int8 ? kv_vs + size_t(li) * KVH * d.max_len : nullptr;
+      for (uint32_t c = 0; c < nc; ++c) {
+        RowShift r(*this, c);
+        const uint32_t Mc = rows(c);
+        if (d.kv_int8) {
+          MI_TRY(qkv_plain(L, Mc, ni));
+          MI_TRY(mi_attn_prep_kv8(ctrl, part, L.qkv.S, Mc, &ash, L.q_norm, L.k_norm, rope, attn_q, nullptr,
+                                  static_cast<int8_t*>(lk), static_cast<int8_t*>(lv), lks, lvs, HD,
+                                  size_t(d.max_len) * HD, 1, d.max_len, nullptr, 0, d.max_len, stream));
+        } else {
+          MI_TRY(launch_qkv_on(L, ctrl, static_cast<uint16_t*>(lk), static_cast<uint16_t*>(lv), Mc, !qkv_is_fused(Mc),
+                               ni));
+        }
+      }
+      if (verify_attn) {
+        MI_TRY(mi_attn_verify(ctrl, attn_q, static_cast<uint16_t*>(lk), static_cast<uint16_t*>(lv), HD,
+                              size_t(d.max_len) * HD, nullptr, 0, d.max_len, attn_part, M, d.attn_tgt, &ash, stream));
+        MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, M, d.attn_tgt, d.max_len, &ash, stream));
+      } else {
+        for (uint32_t c = 0; c < nc; ++c) {
+          RowShift r(*this, c);
+          const uint32_t Mc = rows(c);
+          if (d.kv_int8) {
+            MI_TRY(mi_attn_decode(ctrl, attn_q, 1, lk, lv, lks, lvs, HD, size_t(d.max_len) * HD, 1, d.max_len, nullptr,
+                                  0, d.max_len, attn_part, Mc, d.attn_tgt, &ash, stream));
+            MI_TRY(mi_attn_reduce_kv8(ctrl, attn_part, nullptr, attn_out, Mc, d.attn_tgt, d.max_len, &ash, stream));
+          } else {
+            MI_TRY(mi_attn_decode(ctrl, attn_q, 0, lk, lv, nullptr, nullptr, HD, size_t(d.max_len) * HD, 0, 0, nullptr,
+                                  0, d.max_len, attn_part, Mc, d.attn_tgt, &ash, stream));
+            MI_TRY(mi_attn_reduce(ctrl, attn_part, nullptr, attn_out, Mc, d.attn_tgt, d.max_len, &ash, stream));
+          }
+        }
+      }
+      const float* next_w = next_norm(li);
+      for (uint32_t c = 0; c < nc; ++c) {
+        RowShift r(*this, c);
+        const uint32_t Mc = rows(c);
+        MI_TRY(launch_o(L, Mc));
+        if (d.experts) {
+          MI_TRY(moe_block(L, Mc, next_w));
+        } else {
+          MI_TRY(launch_gate_up(L, Mc));
+          MI_TRY(launch_down(L, Mc, next_w, split_norm() && li + 1 < d.layers));
+        }
+      }
+    }
+    for (uint32_t c = 0; c < nc; ++c) {
+      RowShift r(*this, c);
+      MI_TRY(head(ctrl, rows(c), x, logits, nullptr));
+    }
+    chunk_gather_kernel<<<1, 64, 0, stream>>>(ctrl, cctl, M, history, d.max_len);
+    return mi_hip(static_cast<int>(hipGetLastError()), "chunk_gather");
   }
 
   // ---- the MTP head (capture.cc:1772-1939) ----
@@ -835,7 +1010,7 @@ struct mi_engine {
     if (c[MI_CTRL_DEBUG] != MI_STATUS_HANDOFF_TIMEOUT) return 0;
     MI_TRY(mi_gemv_handoff_init(part_ex, part_ex_n, stream));
     MI_TRY(mi_gemv_handoff_init(sumsq, sumsq_n, stream));
-    if (dn_words) MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(d.max_rows) * (d.hidden / 2), stream));
+    if (dn_words) MI_TRY(mi_gemv_handoff_init(reinterpret_cast<float*>(dn_words), size_t(std::min(d.max_rows, kRowChunk)) * (d.hidden / 2), stream));
     MI_TRY(mi_hip(static_cast<int>(hipMemsetAsync(arrive, 0, arrive_n * 4, stream)), "arrive clear"));
     ctrl_set_kernel<<<1, 64, 0, stream>>>(ctrl, MI_CTRL_DEBUG, 0u);
     MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set"));
@@ -995,7 +1170,8 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
   const mi_model_desc& m = *desc;
   if (m.layers == 0 || m.hidden % 256 || m.hidden > 65536 || (m.head_dim != 128 && m.head_dim != 256) || m.kv_heads == 0 ||
       m.q_heads % m.kv_heads || m.q_heads / m.kv_heads > 8 || m.inter % 64 || m.vocab % 64 ||
-      m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 8 || m.rot_dim > m.head_dim ||
+      m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 64 || (m.max_rows > 8 && m.mtp) ||
+      m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
       m.mtp > 1 || m.lm_head_int8 > 1 || m.act_bf16 > 1 || (m.act_bf16 && (m.experts || m.kv_int8 || m.mtp)) ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
@@ -1091,7 +1267,7 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_MTP_LOGITS: *ptr = e->hlogits; b = size_t(m.vocab) * 4; break;
     case MI_T_LM_I8: *ptr = e->lm_i8; b = e->lm_i8 ? size_t(m.vocab) * m.hidden : 0; break;
     case MI_T_LM_I8_S: *ptr = e->lm_i8s; b = e->lm_i8s ? size_t(m.vocab) * 4 : 0; break;
-    case MI_T_MOE_HANDOFF: *ptr = e->dn_words; b = e->dn_words ? size_t(m.max_rows) * (m.hidden / 2) * 4 : 0; break;
+    case MI_T_MOE_HANDOFF: *ptr = e->dn_words; b = e->dn_words ? size_t(std::min(m.max_rows, kRowChunk)) * (m.hidden / 2) * 4 : 0; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }
   if (bytes) *bytes = b;
@@ -1197,7 +1373,7 @@ int mi_engine_verify(mi_engine* e, const uint32_t* drafts, uint32_t k, uint32_t*
   uint32_t c2[MI_CTRL_WORDS];
   MI_TRY(e->read_ctrl(c2));
   MI_TRY(e->check_handoff());
-  if (argmax_rows) std::memcpy(argmax_rows, c2 + MI_CTRL_OUT, (k + 1) * 4);
+  if (argmax_rows) std::memcpy(argmax_rows, c2 + ctrl_out_at(k + 1), (k + 1) * 4);
   // leave pos at the verify position until commit (Engine::commit decides the advance)
   return e->set_rows(c[MI_CTRL_POS], 1, nullptr, 0);
 }

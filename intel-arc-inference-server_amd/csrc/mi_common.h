@@ -31,7 +31,11 @@ enum : uint32_t {
   CTRL_OUT = 10,       // out_token[8]: the step's argmax per row
   CTRL_DEBUG = 18,     // 0xDEAD0001: an id outside the embedding table
   CTRL_STEPS = 19,     // steps completed since the last reset (history index)
-  CTRL_WORDS = 64
+  CTRL_WIDE_CUR = 32,  // wide_cur[16] / wide_out[16]: a 9..16-row list's ids (control.h:35-38)
+  CTRL_WIDE_OUT = 48,
+  CTRL_DEEP_CUR = 64,  // deep_cur[64] / deep_out[64]: a 17..64-row list's (control.h:39-42)
+  CTRL_DEEP_OUT = 128,
+  CTRL_WORDS = 192
 };
 constexpr uint32_t kStatusNonFinite = 0xDEAD0004u;  // CTRL_DEBUG: a logit was not finite
 constexpr uint32_t kNanBits = 0x7FC00000u;          // the canonical fp32 NaN
