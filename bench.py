@@ -409,9 +409,10 @@ def measure_lm_head_int8(st):
             "frac_of_peak": round(alg / t / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
 
 
-def measure_mtp(args, moe=False):
+def measure_mtp(args, moe=False, w16=False):
     """The MTP draft lists at the 27B shape (the head: one more dense layer at the model's
-    shapes, sharing the embedding and lm_head; random-init) or, moe, on the configs[3] MoE model
+    shapes, sharing the embedding and lm_head; random-init; w16: its linears in 16 bits as the
+    reference keeps a dense head, else int4) or, moe, on the configs[3] MoE model
     (the head: one MoE layer of its shape): the plain step with the head's K/V fill, one draft
     list (the head at one row: front, attention over its own cache, FFN, head) and the verify
     step at k = 3 (four rows, the fill over them), at context `--context`. The weights are
@@ -421,6 +422,7 @@ def measure_mtp(args, moe=False):
     max_len = ((ctx + 64 + 1 + 63) // 64) * 64
     desc = mi.desc_moe_cfg4(max_len=max_len) if moe else mi.desc_27b(max_len=max_len)
     desc.mtp = 1
+    desc.mtp_w16 = 1 if w16 else 0
     eng = mi.Engine(desc, seed=args.seed)  # the main model's weights are the bench engine's
     eng.capture(1)
     eng.capture(4)
@@ -437,19 +439,33 @@ def measure_mtp(args, moe=False):
         eng.draft(3)
     t_draft3 = (time.perf_counter() - t0) / reps * 1e3
     drafts = eng.draft(3)
-    t0 = time.perf_counter()
+    # the random-init model's fp16 activations can leave the range on some rows (the verify
+    # call then fails loudly, after its step ran): the time is the same, the flag says so
+    finite = True
+    c0 = eng.ctrl()
+    t_verify = 0.0
     for _ in range(reps):
-        eng.verify(drafts)
-    t_verify = (time.perf_counter() - t0) / reps * 1e3
+        eng.reset(int(c0[mi.CTRL_POS]), int(c0[mi.CTRL_CUR]))  # (a failed verify leaves no valid cur)
+        t0 = time.perf_counter()
+        try:
+            eng.verify(drafts)
+        except mi.MiError as ex:
+            if "not finite" not in str(ex):
+                raise
+            finite = False
+        t_verify += time.perf_counter() - t0
+    t_verify = t_verify / reps * 1e3
+    eng.reset(int(c0[mi.CTRL_POS]), int(c0[mi.CTRL_CUR]))
     c = eng.ctrl()
     assert c[mi.CTRL_DEBUG] == 0, (hex(c[mi.CTRL_DEBUG]), list(drafts), [hex(v) for v in c[:20]],
                                    [hex(v) for v in eng.to_host(mi.T_MTP_CTRL, 0, np.uint32)[:20]])
     eng.close()
     return {"workload": ("configs[3] MoE model" if moe else "27B shape") +
-                        f" with an MTP head (random-init), context {ctx}",
+                        f" with an MTP head ({'16-bit' if w16 else 'int4' if not moe else 'MoE'} linears, "
+                        f"random-init), context {ctx}",
             "plain_step_with_fill_ms": round(plain / 1e3, 4),
             "draft_3_ms": round(t_draft3, 3), "draft_list_ms": round(t_draft3 / 3, 3),
-            "verify_k3_ms": round(t_verify, 3),
+            "verify_k3_ms": round(t_verify, 3), "verify_logits_finite": finite,
             "note": "draft and verify times are host wall clock around each call (one "
                     "synchronisation per call); the plain step is HIP-event timed"}
 
@@ -855,7 +871,8 @@ def main():
         print(json.dumps({"lm_head_int8": measure_lm_head_int8(None)}), flush=True)
         return
     if args.only == "mtp":
-        print(json.dumps({"mtp": measure_mtp(args), "mtp_moe": measure_mtp(args, moe=True)}), flush=True)
+        print(json.dumps({"mtp": measure_mtp(args), "mtp_w16": measure_mtp(args, w16=True),
+                          "mtp_moe": measure_mtp(args, moe=True)}), flush=True)
         return
     if args.only == "moe_prefill":
         # the configs[3] MoE model's chunked prefill of a 2048-token prompt, three timed calls
@@ -997,6 +1014,7 @@ def main():
         other["lm_head_int8"] = measure_lm_head_int8(None)
         log(f"bench: int8 lm_head {other['lm_head_int8']}")
         other["mtp"] = measure_mtp(args)
+        other["mtp_w16"] = measure_mtp(args, w16=True)
         other["mtp_moe"] = measure_mtp(args, moe=True)
         log(f"bench: mtp {other['mtp']}")
 

@@ -534,6 +534,13 @@ typedef struct mi_model_desc {
    * residual leaves the f16 range on some inputs; bf16's range holds it. Dense models with the
    * f16-format cache, no MTP head; prefill refused (ingest). 0: f16 activations (BASELINE's). */
   uint32_t act_bf16;
+  /* With a dense MTP head (mtp = 1, experts = 0): 1 keeps the head's five linears (fc, q||k||v,
+   * o, gate||up, down) in 16 bits as the reference's loader does (loader.cc:586-597,
+   * repack_bf16_tiled), run by the 16-bit GEMV (mi_gemv_f16w, gemv_bf16's order) with the
+   * standalone fold, norm, SwiGLU and attn_prep kernels; a loaded checkpoint's bf16 head
+   * weights are held as f16 (exact in f16's range; a weight outside it is refused). 0: the
+   * head's linears quantised to int4 g64 at load (rtn.h's rule) and run as the layers'. */
+  uint32_t mtp_w16;
 } mi_model_desc;
 
 typedef struct mi_engine mi_engine;
@@ -559,7 +566,10 @@ enum {
   MI_T_LM_I8, MI_T_LM_I8_S,
   /* MoE models: the hand-off words of mi_moe_down_norm [max_rows][hidden / 2] (0xFFFFFFFF
    * between launches; emptied again by the engine after a step whose wait timed out) */
-  MI_T_MOE_HANDOFF
+  MI_T_MOE_HANDOFF,
+  /* the 16-bit MTP head (mtp_w16): fc, q||k||v, o, gate||up (interleaved in 16-column blocks),
+   * down, each f16 in mi_gemv_f16w's tile layout [N/16][K/8][8][16] */
+  MI_T_MTP_W16_FC, MI_T_MTP_W16_QKV, MI_T_MTP_W16_O, MI_T_MTP_W16_GU, MI_T_MTP_W16_DN
 };
 
 /* Allocates weights (random-init on the device from `seed`, BASELINE config 2's

@@ -202,12 +202,12 @@ class ModelDesc(C.Structure):
                 ("vocab_used", u32), ("max_len", u32), ("qk_norm", u32), ("max_rows", u32),
                 ("attn_tgt", u32), ("rope_theta", f32), ("rms_eps", f32),
                 ("experts", u32), ("top_k", u32), ("moe_inter", u32), ("kv_int8", u32),
-                ("mtp", u32), ("lm_head_int8", u32), ("act_bf16", u32)]
+                ("mtp", u32), ("lm_head_int8", u32), ("act_bf16", u32), ("mtp_w16", u32)]
 
 
 def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_len, *,
                rot_dim=None, vocab_used=None, qk_norm=1, max_rows=8, attn_tgt=128,
-               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0, lm_head_int8=0, act_bf16=0):
+               rope_theta=1e6, rms_eps=1e-6, kv_int8=0, mtp=0, lm_head_int8=0, act_bf16=0, mtp_w16=0):
     d = ModelDesc(layers, hidden, q_heads, kv_heads, head_dim,
                   head_dim if rot_dim is None else rot_dim, inter, vocab,
                   vocab if vocab_used is None else vocab_used, max_len, qk_norm, max_rows,
@@ -216,6 +216,7 @@ def dense_desc(layers, hidden, q_heads, kv_heads, head_dim, inter, vocab, max_le
     d.mtp = mtp
     d.lm_head_int8 = lm_head_int8
     d.act_bf16 = act_bf16
+    d.mtp_w16 = mtp_w16
     return d
 
 
@@ -263,7 +264,8 @@ def desc_27b(max_len=4096 + 512, act_bf16=0):
 (T_EMBED, T_FINAL_NORM, T_LM_Q, T_LM_S, T_ROPE, T_KV_K, T_KV_V, T_LOGITS, T_CTRL,
  T_HISTORY, T_KV_KS, T_KV_VS, T_RESID, T_X, T_ATTN_Q, T_ATTN_OUT, T_HBUF, T_MTP_FC_Q, T_MTP_FC_S,
  T_MTP_PRE_E, T_MTP_PRE_H, T_MTP_FINAL, T_MTP_KV_K, T_MTP_KV_V, T_MTP_HH, T_MTP_DH, T_MTP_CTRL, T_MTP_LOGITS,
- T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF) = range(32, 63)
+ T_LM_I8, T_LM_I8_S, T_MOE_HANDOFF, T_MTP_W16_FC, T_MTP_W16_QKV, T_MTP_W16_O, T_MTP_W16_GU,
+ T_MTP_W16_DN) = range(32, 68)
 CTRL_POS, CTRL_NACT, CTRL_CUR, CTRL_OUT, CTRL_DEBUG, CTRL_STEPS, CTRL_WORDS = 0, 1, 2, 10, 18, 19, 192
 CTRL_WIDE_CUR, CTRL_WIDE_OUT, CTRL_DEEP_CUR, CTRL_DEEP_OUT = 32, 48, 64, 128
 

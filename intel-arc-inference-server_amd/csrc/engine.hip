@@ -153,6 +153,8 @@ constexpr uint32_t kMaxDraft = 3;       // draft lists per iteration (MtpBuffers
 struct MtpHead {
   Linear fc;
   Layer L;
+  // the 16-bit head (mtp_w16): f16 in gemv_f16w's tiles; the int4 linears above stay empty
+  uint16_t *fc16 = nullptr, *qkv16 = nullptr, *o16 = nullptr, *gu16 = nullptr, *dn16 = nullptr;
   float* pre_e = nullptr;
   float* pre_h = nullptr;
   float* final_n = nullptr;
@@ -308,15 +310,24 @@ struct mi_engine {
       part_ex_max = std::max(part_ex_max, size_t(L.qkv.S) * std::min(RL, 4u) * L.qkv.N);  // QKV: all S slices
     }
     if (m.mtp) {  // the head: fc (plain partials) and a dense layer at the model's shapes
-      MI_TRY(alloc_linear(mh.fc, 2 * H, H, 0));
       Layer& L = mh.L;
-      MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_QKV));
-      MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
+      if (m.mtp_w16) {  // the 16-bit head: its GEMVs write [rows][N] fp32 into `part`
+        MI_TRY(alloc(&mh.fc16, size_t(2 * H) * H));
+        MI_TRY(alloc(&mh.qkv16, size_t(H) * qkv_n));
+        MI_TRY(alloc(&mh.o16, size_t(QH * HD) * H));
+        MI_TRY(alloc(&mh.gu16, size_t(H) * 2 * m.inter));
+        MI_TRY(alloc(&mh.dn16, size_t(m.inter) * H));
+        part_max = std::max({part_max, size_t(R) * H, size_t(R) * qkv_n, size_t(R) * 2 * m.inter});
+      } else {
+        MI_TRY(alloc_linear(mh.fc, 2 * H, H, 0));
+        MI_TRY(alloc_linear(L.qkv, H, qkv_n, MI_EPI_QKV));
+        MI_TRY(alloc_linear(L.o, QH * HD, H, MI_EPI_RESID));
+      }
       if (moe) {  // an MoE model's head (spec 15e): one MoE layer of the model's shape
         MI_TRY(alloc(&L.router, size_t(router_n) * H));
         MI_TRY(alloc(&L.moe_gu, (m.experts + 1) * gu_block));
         MI_TRY(alloc(&L.moe_dn, (m.experts + 1) * dn_block));
-      } else {
+      } else if (!m.mtp_w16) {
         MI_TRY(alloc_linear(L.gate_up, H, 2 * m.inter, MI_EPI_SILU));
         MI_TRY(alloc_linear(L.down, m.inter, H, MI_EPI_RESID));
       }
@@ -325,7 +336,7 @@ struct mi_engine {
         MI_TRY(alloc(&L.q_norm, HD));
         MI_TRY(alloc(&L.k_norm, HD));
       }
-      part_max = std::max({part_max, size_t(mh.fc.S) * R * H, size_t(L.qkv.S) * R * L.qkv.N});
+      if (!m.mtp_w16) part_max = std::max({part_max, size_t(mh.fc.S) * R * H, size_t(L.qkv.S) * R * L.qkv.N});
       MI_TRY(alloc(&hkv_k, size_t(KVH) * m.max_len * HD));
       MI_TRY(alloc(&hkv_v, size_t(KVH) * m.max_len * HD));
       MI_TRY(alloc(&hh, size_t(R + 1) * H));
@@ -439,6 +450,14 @@ struct mi_engine {
         MI_TRY(mi_fill_u32(l->q, size_t(l->K / 8) * l->N, seed++, stream));
         MI_TRY(mi_fill_f16(l->s, size_t(l->K / 64) * l->N, seed++, 0, 0.0005f, 0.005f, stream));
       }
+      // the 16-bit head: N(0, 0.01), about the int4 head's weights' spread at its scales
+      for (uint16_t* w : {mh.fc16, mh.qkv16, mh.o16, mh.gu16, mh.dn16}) {
+        if (!w) continue;
+        const size_t n = w == mh.fc16 ? size_t(2 * H) * H : w == mh.qkv16 ? size_t(H) * qkv_n
+                       : w == mh.o16 ? size_t(QH * HD) * H : w == mh.gu16 ? size_t(H) * 2 * m.inter
+                                                                          : size_t(m.inter) * H;
+        MI_TRY(mi_fill_f16(w, n, seed++, 1, 0.0f, 0.01f, stream));
+      }
       if (m.experts) {  // the MoE head's router as the layers', its experts at the head's scales
         MI_TRY(mi_fill_f16(mh.L.router, size_t(router_n) * H, seed++, 1, 0.0f, 0.02f, stream));
         MI_TRY(mi_fill_layout1(mh.L.moe_gu, (m.experts + 1) * gu_block / 136, seed++, 0.0005f, 0.005f, stream));
@@ -491,7 +510,7 @@ struct mi_engine {
     auto ok = [](const Linear& l) { return (l.K / 64) / l.S <= 8; };
     for (uint32_t li = 0; li < d.layers; ++li)
       if (!ok(layer[li].qkv) || !ok(layer[li].gate_up)) return false;
-    return !d.mtp || ok(mh.L.gate_up);
+    return !d.mtp || d.mtp_w16 || ok(mh.L.gate_up);
   }
   mi_gemv_epilogue resid_epi(const float* next_w, bool sums_only) const {
     mi_gemv_epilogue e{};
@@ -708,10 +727,32 @@ struct mi_engine {
     MI_TRY(mi_norm_finish_ex(hsumsq, resid, mh.pre_e, hx2, size_t(2) * H, M, H, G, d.rms_eps, stream));
     MI_TRY(mi_res_fold(nullptr, hid, hsumsq, M, H, 0, G, stream));
     MI_TRY(mi_norm_finish_ex(hsumsq, hid, mh.pre_h, hx2 + H, size_t(2) * H, M, H, G, d.rms_eps, stream));
+    if (d.mtp_w16) {  // the 16-bit head: one [M][N] output per linear (S = 1 for the folds)
+      const uint32_t HD = d.head_dim, qkv_n = (d.q_heads + 2 * d.kv_heads) * HD;
+      MI_TRY(mi_gemv_f16w(mh.fc16, hx2, part, M, 2 * H, H, router_ksplit_of(2 * H), stream));
+      MI_TRY(mi_res_fold_ex(part, resid, hsumsq, M, H, 1, G, 1, stream));
+      MI_TRY(mi_norm_finish(hsumsq, resid, mh.L.in_norm, x, M, H, G, d.rms_eps, stream));
+      MI_TRY(mi_gemv_f16w(mh.qkv16, x, part, M, H, qkv_n, router_ksplit_of(H), stream));
+      return mi_attn_prep(hctl, part, 1, M, &ash, mh.L.q_norm, mh.L.k_norm, rope, attn_q, nullptr, hkv_k, hkv_v, HD,
+                          size_t(d.max_len) * HD, nullptr, 0, d.max_len, stream);
+    }
     MI_TRY(mi_gemv_w4a16(mh.fc.q, mh.fc.s, hx2, part, M, mh.fc.K, mh.fc.N, mh.fc.S, stream));
     MI_TRY(mi_res_fold_ex(part, resid, hsumsq, M, H, mh.fc.S, G, 1, stream));
     MI_TRY(mi_norm_finish(hsumsq, resid, mh.L.in_norm, x, M, H, G, d.rms_eps, stream));
     return launch_qkv_on(mh.L, hctl, hkv_k, hkv_v, M, true);
+  }
+  // the 16-bit head's o with the residual and the post-attention norm, its MLP, and its final
+  // norm into x (one row): the standalone kernels on the GEMV's [1][N] output (S = 1)
+  int draft_tail16() {
+    const uint32_t H = d.hidden, G = H / 64, QD = d.q_heads * d.head_dim, I = d.inter;
+    MI_TRY(mi_gemv_f16w(mh.o16, attn_out, part, 1, QD, H, router_ksplit_of(QD), stream));
+    MI_TRY(mi_res_fold(part, resid, hsumsq, 1, H, 1, G, stream));
+    MI_TRY(mi_norm_finish(hsumsq, resid, mh.L.post_norm, x, 1, H, G, d.rms_eps, stream));
+    MI_TRY(mi_gemv_f16w(mh.gu16, x, part, 1, H, 2 * I, router_ksplit_of(H), stream));
+    MI_TRY(mi_silu_mul(part, hbuf, 1, I, 1, stream));
+    MI_TRY(mi_gemv_f16w(mh.dn16, hbuf, part, 1, I, H, router_ksplit_of(I), stream));
+    MI_TRY(mi_res_fold(part, resid, hsumsq, 1, H, 1, G, stream));
+    return mi_norm_finish(hsumsq, resid, mh.final_n, x, 1, H, G, d.rms_eps, stream);
   }
   // an MoE layer's FFN on x (rows M): router || shared gate, route + gate||up, down + combine
   // into the residual with the next norm (weights next_w) into x
@@ -728,12 +769,16 @@ struct mi_engine {
   int enqueue_draft() {
     MI_TRY(head_front(dh, 1));
     MI_TRY(attn_pair(mh.L, hctl, hkv_k, hkv_v, 1, false));
-    MI_TRY(launch_o(mh.L, 1));
-    if (d.experts) {  // an MoE model's head: its MoE layer (capture.cc:1913's moe_block)
-      MI_TRY(moe_block(mh.L, 1, mh.final_n));
+    if (d.mtp_w16) {
+      MI_TRY(draft_tail16());
     } else {
-      MI_TRY(launch_gate_up(mh.L, 1));
-      MI_TRY(launch_down(mh.L, 1, mh.final_n, false));
+      MI_TRY(launch_o(mh.L, 1));
+      if (d.experts) {  // an MoE model's head: its MoE layer (capture.cc:1913's moe_block)
+        MI_TRY(moe_block(mh.L, 1, mh.final_n));
+      } else {
+        MI_TRY(launch_gate_up(mh.L, 1));
+        MI_TRY(launch_down(mh.L, 1, mh.final_n, false));
+      }
     }
     MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(dh, x, size_t(d.hidden) * 2, hipMemcpyDeviceToDevice, stream)),
                   "dh"));
@@ -1173,7 +1218,7 @@ mi_engine* mi_engine_create(const mi_model_desc* desc, uint64_t seed, void* stre
       m.vocab_used > m.vocab || m.max_len == 0 || m.max_rows == 0 || m.max_rows > 64 || (m.max_rows > 8 && m.mtp) ||
       m.rot_dim > m.head_dim ||
       m.attn_tgt == 0 || (m.q_heads * m.head_dim) % 64 || m.kv_int8 > 1 || (m.kv_int8 && m.head_dim != 256) ||
-      m.mtp > 1 || m.lm_head_int8 > 1 || m.act_bf16 > 1 || (m.act_bf16 && (m.experts || m.kv_int8 || m.mtp)) ||
+      m.mtp > 1 || m.mtp_w16 > 1 || (m.mtp_w16 && (!m.mtp || m.experts)) || m.lm_head_int8 > 1 || m.act_bf16 > 1 || (m.act_bf16 && (m.experts || m.kv_int8 || m.mtp)) ||
       (m.experts && (m.experts < 16 || m.experts > 256 || (m.experts & (m.experts - 1)) || m.top_k < 1 ||
                      m.top_k > 8 || m.moe_inter % 128 || m.moe_inter == 0 || m.moe_inter > 1024 ||
                      m.hidden % 512 || m.hidden > 4096))) {
@@ -1267,6 +1312,14 @@ int mi_engine_tensor(mi_engine* e, uint32_t kind, uint32_t layer, void** ptr, si
     case MI_T_MTP_LOGITS: *ptr = e->hlogits; b = size_t(m.vocab) * 4; break;
     case MI_T_LM_I8: *ptr = e->lm_i8; b = e->lm_i8 ? size_t(m.vocab) * m.hidden : 0; break;
     case MI_T_LM_I8_S: *ptr = e->lm_i8s; b = e->lm_i8s ? size_t(m.vocab) * 4 : 0; break;
+    case MI_T_MTP_W16_FC: *ptr = e->mh.fc16; b = e->mh.fc16 ? size_t(2 * m.hidden) * m.hidden * 2 : 0; break;
+    case MI_T_MTP_W16_QKV:
+      *ptr = e->mh.qkv16;
+      b = e->mh.qkv16 ? size_t(m.hidden) * (m.q_heads + 2 * m.kv_heads) * m.head_dim * 2 : 0;
+      break;
+    case MI_T_MTP_W16_O: *ptr = e->mh.o16; b = e->mh.o16 ? size_t(m.q_heads) * m.head_dim * m.hidden * 2 : 0; break;
+    case MI_T_MTP_W16_GU: *ptr = e->mh.gu16; b = e->mh.gu16 ? size_t(m.hidden) * 2 * m.inter * 2 : 0; break;
+    case MI_T_MTP_W16_DN: *ptr = e->mh.dn16; b = e->mh.dn16 ? size_t(m.inter) * m.hidden * 2 : 0; break;
     case MI_T_MOE_HANDOFF: *ptr = e->dn_words; b = e->dn_words ? size_t(std::min(m.max_rows, kRowChunk)) * (m.hidden / 2) * 4 : 0; break;
     default: return mi_fail(MI_ERR_ARG, "engine_tensor: unknown kind");
   }

@@ -632,6 +632,14 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
     if (int rc = mi_engine_tensor(e, MI_T_LM_I8, 0, &p8, &b8)) return rc;
     head_i8 = b8 != 0;
   }
+  // the MTP head's form (its descriptor's mtp_w16): whether it holds 16-bit linears
+  bool head_w16 = false;
+  {
+    void* p16 = nullptr;
+    size_t b16 = 0;
+    if (int rc = mi_engine_tensor(e, MI_T_MTP_W16_FC, 0, &p16, &b16)) return rc;
+    head_w16 = b16 != 0;
+  }
   const std::string pre = lm_prefix(ck);
   const uint32_t H = want.hidden, QH = want.q_heads, KVH = want.kv_heads, HD = want.head_dim;
   const uint32_t I = want.inter, Vp = want.vocab;
@@ -842,15 +850,57 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
     };
     std::vector<uint32_t> q1, q2, q3;
     std::vector<uint16_t> s1, s2, s3;
-    if (!mtp_linear("mtp.fc", 2 * H, H, q1, s1)) return fail_ck(ck);
-    if (int rc = upload(MI_T_MTP_FC_Q, 0, q1.data(), q1.size() * 4, "mtp.fc qweight")) return rc;
-    if (int rc = upload(MI_T_MTP_FC_S, 0, s1.data(), s1.size() * 2, "mtp.fc scales")) return rc;
+    // the 16-bit head (desc.mtp_w16, loader.cc:586-597): the linears' [N][K] weights (q||k||v
+    // and gate||up by output rows, gate/up interleaved in 16-row blocks) as f16 in gemv_f16w's
+    // tiles
+    const bool w16 = head_w16;
+    auto mtp_w16 = [&](const std::vector<std::string>& bases, const std::vector<uint32_t>& ns, uint32_t K, bool gu,
+                       uint32_t kind) -> int {
+      std::vector<float> all;
+      uint32_t N = 0;
+      for (size_t i = 0; i < bases.size(); ++i) {
+        ++rep.mtp_tensors;
+        if (!ck.find(bases[i] + ".weight")) {
+          ck.fail("engine_load: a 16-bit MTP head needs " + bases[i] + ".weight (the checkpoint's head is not 16-bit)");
+          return fail_ck(ck);
+        }
+        if (!get_float(ck, bases[i] + ".weight", size_t(ns[i]) * K, f32)) return fail_ck(ck);
+        all.insert(all.end(), f32.begin(), f32.end());
+        N += ns[i];
+      }
+      if (gu) {  // repack.h's interleave16 by rows: row n is gate row (n / 32) 16 + n % 16 (n % 32 < 16), else up's
+        const uint32_t I2 = N / 2;
+        std::vector<float> r(all.size());
+        for (uint32_t n = 0; n < N; ++n) {
+          const uint32_t src = (n % 32 < 16 ? 0u : I2) + (n / 32) * 16 + n % 16;
+          std::memcpy(&r[size_t(n) * K], &all[size_t(src) * K], size_t(K) * 4);
+        }
+        all.swap(r);
+      }
+      std::vector<uint16_t> h16, tiles;
+      if (!to_f16(ck, bases[0], all, h16)) return fail_ck(ck);
+      tiles.resize(h16.size());
+      f16w_tile(h16.data(), K, N, tiles.data());
+      return upload(kind, 0, tiles.data(), tiles.size() * 2, bases[0].c_str());
+    };
+    if (w16) {
+      if (int rc = mtp_w16({"mtp.fc"}, {H}, 2 * H, false, MI_T_MTP_W16_FC)) return rc;
+    } else {
+      if (!mtp_linear("mtp.fc", 2 * H, H, q1, s1)) return fail_ck(ck);
+      if (int rc = upload(MI_T_MTP_FC_Q, 0, q1.data(), q1.size() * 4, "mtp.fc qweight")) return rc;
+      if (int rc = upload(MI_T_MTP_FC_S, 0, s1.data(), s1.size() * 2, "mtp.fc scales")) return rc;
+    }
     if (int rc = mtp_norm("mtp.pre_fc_norm_embedding.weight", H, MI_T_MTP_PRE_E, 0)) return rc;
     if (int rc = mtp_norm("mtp.pre_fc_norm_hidden.weight", H, MI_T_MTP_PRE_H, 0)) return rc;
     if (int rc = mtp_norm("mtp.norm.weight", H, MI_T_MTP_FINAL, 0)) return rc;
     if (int rc = flush()) return rc;
     const std::string lp = "mtp.layers.0.";
-    {
+    if (w16) {
+      if (int rc = mtp_w16({lp + "self_attn.q_proj", lp + "self_attn.k_proj", lp + "self_attn.v_proj"},
+                          {QH * HD, KVH * HD, KVH * HD}, H, false, MI_T_MTP_W16_QKV))
+        return rc;
+      if (int rc = mtp_w16({lp + "self_attn.o_proj"}, {H}, QH * HD, false, MI_T_MTP_W16_O)) return rc;
+    } else {
       std::vector<uint32_t> qq, kq, vq;
       std::vector<uint16_t> qs, ks, vs;
       if (!mtp_linear(lp + "self_attn.q_proj", H, QH * HD, qq, qs) ||
@@ -861,10 +911,10 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
       concat_cols<uint16_t>({{qs.data(), QH * HD}, {ks.data(), KVH * HD}, {vs.data(), KVH * HD}}, H / 64, scat);
       if (int rc = upload(MI_T_QKV_Q, HL, qcat.data(), qcat.size() * 4, "mtp q||k||v qweight")) return rc;
       if (int rc = upload(MI_T_QKV_S, HL, scat.data(), scat.size() * 2, "mtp q||k||v scales")) return rc;
+      if (!mtp_linear(lp + "self_attn.o_proj", QH * HD, H, q1, s1)) return fail_ck(ck);
+      if (int rc = upload(MI_T_O_Q, HL, q1.data(), q1.size() * 4, "mtp o_proj qweight")) return rc;
+      if (int rc = upload(MI_T_O_S, HL, s1.data(), s1.size() * 2, "mtp o_proj scales")) return rc;
     }
-    if (!mtp_linear(lp + "self_attn.o_proj", QH * HD, H, q1, s1)) return fail_ck(ck);
-    if (int rc = upload(MI_T_O_Q, HL, q1.data(), q1.size() * 4, "mtp o_proj qweight")) return rc;
-    if (int rc = upload(MI_T_O_S, HL, s1.data(), s1.size() * 2, "mtp o_proj scales")) return rc;
     if (int rc = mtp_norm(lp + "input_layernorm.weight", H, MI_T_IN_NORM, HL)) return rc;
     if (int rc = mtp_norm(lp + "post_attention_layernorm.weight", H, MI_T_POST_NORM, HL)) return rc;
     if (want.qk_norm) {
@@ -875,6 +925,9 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
     if (moe) {  // an MoE model's head (spec 15e): one MoE layer in the main layers' device form
       if (int rc = load_moe_ffn(lp, HL, true)) return rc;
       rep.mtp_tensors += 2 + 3 * (size_t(E) + 1);  // router, shared gate, the experts' linears
+    } else if (w16) {
+      if (int rc = mtp_w16({lp + "mlp.gate_proj", lp + "mlp.up_proj"}, {I, I}, H, true, MI_T_MTP_W16_GU)) return rc;
+      if (int rc = mtp_w16({lp + "mlp.down_proj"}, {H}, I, false, MI_T_MTP_W16_DN)) return rc;
     } else {
       if (!mtp_linear(lp + "mlp.gate_proj", H, I, q1, s1) || !mtp_linear(lp + "mlp.up_proj", H, I, q2, s2) ||
           !mtp_linear(lp + "mlp.down_proj", I, H, q3, s3))
@@ -906,11 +959,11 @@ int mi_engine_load(mi_engine* e, const char* dir, char* report, size_t report_le
   if (report && report_len) {
     std::snprintf(report, report_len,
                   "loaded %zu int4 linears; dropped %zu qzeros + %zu g_idx (invariants asserted); %zu subnormal "
-                  "scales kept; lm_head %s; MTP head: %zu tensors, %zu linears quantised to int4 g64 at load",
+                  "scales kept; lm_head %s; MTP head: %zu tensors, %zu linears quantised to int4 g64 at load%s",
                   rep.linears, rep.qzeros, rep.g_idx, rep.subnormal_scales,
                   rep.quantised_head ? (head_i8 ? "quantised to int8 rows at load" : "quantised to int4 g64 at load")
                                      : "int4 as shipped",
-                  rep.mtp_tensors, rep.mtp_quantised);
+                  rep.mtp_tensors, rep.mtp_quantised, head_w16 ? " (its linears kept 16-bit)" : "");
   }
   return 0;
 }

@@ -181,7 +181,8 @@ class Layer(C.Structure):
 class MtpHead(C.Structure):
     """orc_mtp_head: the MTP head's fc, its decoder layer and its three norms."""
     _fields_ = [("fc", Linear), ("layer", Layer), ("pre_e", C.c_void_p), ("pre_h", C.c_void_p),
-                ("final_norm", C.c_void_p)]
+                ("final_norm", C.c_void_p), ("w16_fc", C.c_void_p), ("w16_qkv", C.c_void_p),
+                ("w16_o", C.c_void_p), ("w16_gu", C.c_void_p), ("w16_dn", C.c_void_p)]
 
 
 class DenseModel(C.Structure):

@@ -1144,17 +1144,28 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
   const Act A{act};
   const uint32_t H = md->hidden, HD = md->attn.head_dim, QH = md->attn.q_heads, L = md->max_len;
   const uint32_t G = H / 64;
-  if (p >= L || hd->fc.K != 2 * H || hd->fc.N != H) return 0xFFFFFFFFu;
+  if (p >= L || (!hd->w16_fc && (hd->fc.K != 2 * H || hd->fc.N != H))) return 0xFFFFFFFFu;
   std::vector<uint16_t> resid(H), hrow(h, h + H), x2(size_t(2) * H), x(H), attn_out(size_t(QH) * HD);
   std::vector<uint16_t> hbuf(md->inter);
   std::vector<float> sumsq(G), part, attn_q(size_t(QH) * HD), attn_part;
   std::vector<float> xf(std::max<size_t>({size_t(2) * H, size_t(QH) * HD, size_t(md->inter)}));
   const orc_layer& ly = hd->layer;
-  auto linear = [&](const orc_linear& l, const uint16_t* in) {
+  // one linear into `part`: the int4 twin's S slices, or (w16) the 16-bit GEMV's one slice;
+  // returns the slice count the fold that follows takes
+  auto linear = [&](const orc_linear& l, const uint16_t* w16, uint32_t K, uint32_t N, const uint16_t* in) {
+    if (w16) {
+      uint32_t ks = 16;
+      while (ks > 1 && (K / 8) % ks) ks /= 2;
+      part.assign(N, 0.f);
+      orc_gemv_f16w(act, w16, in, 1, K, N, ks, part.data());
+      return 1u;
+    }
     for (uint32_t i = 0; i < l.K; ++i) xf[i] = A.w(in[i]);
     part.assign(size_t(l.S) * l.N, 0.f);
     orc_gemv_twin_partials(0, l.qweight, l.scales, l.K, l.N, xf.data(), 1, l.S, part.data());
+    return l.S;
   };
+  const uint32_t qkv_n = (QH + 2 * md->attn.kv_heads) * HD;
   auto norm = [&](const float* partials, uint32_t s_prev, const float* w) {  // as orc_dense_step's
     if (md->norm_g == 0) {
       orc_res_norm(act, partials, resid.data(), w, x.data(), 1, H, s_prev, md->rms_eps);
@@ -1171,17 +1182,17 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
   orc_norm_finish(act, sumsq.data(), resid.data(), hd->pre_e, x2.data(), 1, H, G, md->rms_eps);
   orc_res_fold(act, nullptr, hrow.data(), sumsq.data(), 1, H, 0, G);
   orc_norm_finish(act, sumsq.data(), hrow.data(), hd->pre_h, x2.data() + H, 1, H, G, md->rms_eps);
-  linear(hd->fc, x2.data());
+  const uint32_t s_fc = linear(hd->fc, hd->w16_fc, 2 * H, H, x2.data());
   // ZERO_RESID (prep.cl:308-309): the residual stream starts at fc's output, rne(sum_s partials)
   for (uint32_t k = 0; k < H; ++k) {
     float acc = 0.f;
-    for (uint32_t s = 0; s < hd->fc.S; ++s) acc += part[size_t(s) * H + k];
+    for (uint32_t s = 0; s < s_fc; ++s) acc += part[size_t(s) * H + k];
     resid[k] = A.rne(acc);
   }
   orc_res_fold(act, nullptr, resid.data(), sumsq.data(), 1, H, 0, G);
   orc_norm_finish(act, sumsq.data(), resid.data(), ly.in_norm, x.data(), 1, H, G, md->rms_eps);
-  linear(ly.qkv, x.data());
-  orc_attn_prep(act, &md->attn, p, 1, 1, part.data(), ly.qkv.S, ly.q_norm, ly.k_norm, md->rope, attn_q.data(),
+  const uint32_t s_qkv = linear(ly.qkv, hd->w16_qkv, H, qkv_n, x.data());
+  orc_attn_prep(act, &md->attn, p, 1, 1, part.data(), s_qkv, ly.q_norm, ly.k_norm, md->rope, attn_q.data(),
                 nullptr, kv_k, kv_v, HD, size_t(L) * HD, nullptr, 0);
   if (!full) return 0;
   // draft(): the attention pair over the head's keys 0..p, o and the post-attention norm, the MLP,
@@ -1190,8 +1201,8 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
   orc_attn_decode_v2(act, &md->attn, p, 1, 1, md->tgt, attn_q.data(), 0, kv_k, kv_v, nullptr, nullptr, HD,
                      size_t(L) * HD, 0, 0, nullptr, 0, attn_part.data());
   orc_attn_reduce_v2(act, &md->attn, p, 1, 1, md->tgt, attn_part.data(), nullptr, attn_out.data());
-  linear(ly.o, attn_out.data());
-  norm(part.data(), ly.o.S, ly.post_norm);
+  const uint32_t s_o = linear(ly.o, hd->w16_o, QH * HD, H, attn_out.data());
+  norm(part.data(), s_o, ly.post_norm);
   if (md->experts) {  // an MoE model's head (spec 15e): one MoE layer of the model's shape
     std::vector<float> lg(md->router_n);
     orc_gemv_f16w(act, ly.router, x.data(), 1, H, md->router_n, md->router_ksplit, lg.data());
@@ -1203,10 +1214,10 @@ uint32_t orc_mtp_head_step(int act, const orc_dense_model* md, const orc_mtp_hea
                   ly.moe_dn, nullptr, dnb, 0, 4, 2, nullptr, resid.data());
     norm(nullptr, 0, hd->final_norm);
   } else {
-    linear(ly.gate_up, x.data());
-    orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, ly.gate_up.S);
-    linear(ly.down, hbuf.data());
-    norm(part.data(), ly.down.S, hd->final_norm);
+    const uint32_t s_gu = linear(ly.gate_up, hd->w16_gu, H, 2 * md->inter, x.data());
+    orc_silu_mul(act, part.data(), hbuf.data(), 1, md->inter, s_gu);
+    const uint32_t s_dn = linear(ly.down, hd->w16_dn, md->inter, H, hbuf.data());
+    norm(part.data(), s_dn, hd->final_norm);
   }
   if (h_out) std::copy(x.begin(), x.end(), h_out);
   head_logits(act, md, x.data(), logits);

@@ -238,6 +238,15 @@ typedef struct orc_mtp_head {
   const float* pre_e; /* the embedding's norm */
   const float* pre_h; /* the hidden's norm */
   const float* final_norm;
+  /* the 16-bit head (loader.cc:586-597 keeps a dense head's linears in bf16): when set, fc,
+   * q||k||v, o, gate||up and down are these [N][K] 16-bit matrices in orc_f16w_tile's layout,
+   * each run by orc_gemv_f16w (gemv_bf16's order; ksplit the largest power of two <= 16
+   * dividing K/8) as one slice, and the orc_linear fields above are unused */
+  const uint16_t* w16_fc;
+  const uint16_t* w16_qkv;
+  const uint16_t* w16_o;
+  const uint16_t* w16_gu;
+  const uint16_t* w16_dn;
 } orc_mtp_head;
 /* One head row at head position p for token `tok` and hidden h (act [hidden]: the main model's
  * post-final-norm hidden of position p, or the head's own output of the previous draft):

@@ -253,6 +253,56 @@ def test_mtp_head_loaded_and_drafts(tmp_path):
     e2.close()
 
 
+def test_mtp_head_16bit_loaded_and_drafts(tmp_path):
+    """desc.mtp_w16: the checkpoint's bf16 head linears kept in 16 bits as the reference's loader
+    keeps a dense head (loader.cc:586-597), each the f16 of the bf16 weight in gemv_f16w's tiles
+    (q||k||v and gate||up by output rows, gate / up interleaved in 16-row blocks), bitwise; the
+    loaded head's drafts follow the oracle's 16-bit head on the same weights."""
+    from test_mtp_gpu import OracleHead, head_kv
+    syn = Synth(str(tmp_path / "mtp16"), layers=2, V=2048, mtp=True)
+    path = syn.write(split=2)
+    desc = mi.checkpoint_desc(path, max_len=512, max_rows=4)
+    desc.mtp, desc.mtp_w16 = 1, 1
+    eng = mi.Engine(desc, seed=5)
+    rep = eng.load(path)
+    print(f"engine_load {path} (16-bit MTP head): {rep}", flush=True)
+    assert "MTP head: 15 tensors, 0 linears quantised" in rep and "kept 16-bit" in rep
+    d = eng.desc
+    H, I, QH, KVH, HD = d.hidden, d.inter, d.q_heads, d.kv_heads, d.head_dim
+
+    def tiled(w_bf16_rows):
+        w = O.f32_to_f16_bits(O.bf16_bits_to_f32(np.ascontiguousarray(w_bf16_rows)))
+        N, K = w.shape
+        t = np.zeros_like(w)
+        O.lib().orc_f16w_tile(O._p(w), K, N, O._p(t))
+        return t.ravel()
+
+    m = syn.mtp
+    n = np.arange(2 * I)
+    gu_rows = np.where(n % 32 < 16, 0, I) + (n // 32) * 16 + n % 16
+    want = {mi.T_MTP_W16_FC: m["fc"], mi.T_MTP_W16_QKV: np.concatenate([m["q"], m["k"], m["v"]]),
+            mi.T_MTP_W16_O: m["o"], mi.T_MTP_W16_GU: np.concatenate([m["gate"], m["up"]])[gu_rows],
+            mi.T_MTP_W16_DN: m["down"]}
+    for kind, w in want.items():
+        assert np.array_equal(eng.to_host(kind, 0, np.uint16), tiled(w)), kind
+    orc = OracleModel(eng)
+    oh = OracleHead(eng, orc)
+    eng.capture(1)
+    eng.reset(100, 7)
+    eng.generate(3)
+    c = eng.ctrl()
+    pos, cur = int(c[mi.CTRL_POS]), int(c[mi.CTRL_CUR])
+    hh0 = eng.to_host(mi.T_MTP_HH, 0, np.uint16)[:H].copy()
+    kk, vv = head_kv(eng)
+    drafts = eng.draft(3)
+    tok, h = cur, hh0
+    for i in range(3):
+        am, logits, hout = oh.run(tok, h, pos - 1 + i, kk, vv)
+        assert argmax_ok(int(drafts[i]), logits), (i, drafts[i], am)
+        tok, h = int(drafts[i]), hout
+    eng.close()
+
+
 def test_moe_mtp_head_loaded_and_drafts(tmp_path):
     """An MoE model's head (spec 15e: one MoE layer of the model's shape) from bf16 mtp.*
     tensors: the router as f16 tiles, every expert's linears quantised by rtn.h's rule into

@@ -37,10 +37,11 @@ class OracleHead:
 
         li = d.layers
         moe = d.experts > 0
+        w16 = bool(d.mtp_w16)  # the 16-bit head: its f16 tiles, the int4 fields unused
         S = [eng.linear_s(w) for w in range(4)]
         lins = []
         for w, (K, N) in enumerate([(H, (QH + 2 * KVH) * HD), (QH * HD, H), (H, 2 * I), (I, H)]):
-            if moe and w >= 2:  # an MoE model's head: its MoE layer instead of gate||up / down
+            if (moe and w >= 2) or w16:  # an MoE model's head: its MoE layer instead of gate||up / down
                 lins.append(O.Linear(None, None, K, N, 1))
                 continue
             q = h(eng.to_host(2 * w, li, np.uint32))
@@ -57,13 +58,19 @@ class OracleHead:
         if d.qk_norm:
             L.q_norm = h(eng.to_host(mi.T_Q_NORM, li, np.float32)).ctypes.data
             L.k_norm = h(eng.to_host(mi.T_K_NORM, li, np.float32)).ctypes.data
-        fcq = h(eng.to_host(mi.T_MTP_FC_Q, 0, np.uint32))
-        fcs = h(eng.to_host(mi.T_MTP_FC_S, 0, np.uint16))
-        fc = O.Linear(fcq.ctypes.data, fcs.ctypes.data, 2 * H, H, eng.linear_s(5))
         pe = h(eng.to_host(mi.T_MTP_PRE_E, 0, np.float32))
         ph = h(eng.to_host(mi.T_MTP_PRE_H, 0, np.float32))
         fn = h(eng.to_host(mi.T_MTP_FINAL, 0, np.float32))
-        self.head = O.MtpHead(fc, L, pe.ctypes.data, ph.ctypes.data, fn.ctypes.data)
+        if w16:
+            fc = O.Linear(None, None, 0, 0, 0)
+            w16s = [h(eng.to_host(k, 0, np.uint16)).ctypes.data for k in
+                    (mi.T_MTP_W16_FC, mi.T_MTP_W16_QKV, mi.T_MTP_W16_O, mi.T_MTP_W16_GU, mi.T_MTP_W16_DN)]
+        else:
+            fcq = h(eng.to_host(mi.T_MTP_FC_Q, 0, np.uint32))
+            fcs = h(eng.to_host(mi.T_MTP_FC_S, 0, np.uint16))
+            fc = O.Linear(fcq.ctypes.data, fcs.ctypes.data, 2 * H, H, eng.linear_s(5))
+            w16s = []
+        self.head = O.MtpHead(fc, L, pe.ctypes.data, ph.ctypes.data, fn.ctypes.data, *w16s)
         keep.append(L)
 
     def run(self, tok, h16, p, kk, vv, full=1):
@@ -95,11 +102,13 @@ def make(seed=42, moe=False, **kw):
     return eng, orc, OracleHead(eng, orc)
 
 
-@pytest.mark.parametrize("kind", ["dense", "kv8", "moe"])
+@pytest.mark.parametrize("kind", ["dense", "kv8", "moe", "w16"])
 def test_drafts_vs_oracle_head_chain(kind):
     # kv8: the main model over the int8 rotated cache (head_dim 256); the head keeps its own f16
-    # cache. moe: an MoE model, whose head is one MoE layer (spec 15e)
-    eng, orc, oh = make(**{"dense": {}, "kv8": dict(head_dim=256, kv_int8=1), "moe": dict(moe=True)}[kind])
+    # cache. moe: an MoE model, whose head is one MoE layer (spec 15e). w16: the dense head's
+    # linears in 16 bits (the reference's bf16 head, loader.cc:586-597)
+    eng, orc, oh = make(**{"dense": {}, "kv8": dict(head_dim=256, kv_int8=1), "moe": dict(moe=True),
+                           "w16": dict(mtp_w16=1)}[kind])
     H = eng.desc.hidden
     eng.capture(1)
     eng.reset(300, 7)
@@ -130,8 +139,9 @@ def test_drafts_vs_oracle_head_chain(kind):
     assert eng.ctrl()[mi.CTRL_POS] == pos  # the main model's state is untouched
 
 
-def test_verify_fills_the_head_and_commit_moves_the_hidden():
-    eng, orc, oh = make(seed=5)
+@pytest.mark.parametrize("w16", [0, 1])
+def test_verify_fills_the_head_and_commit_moves_the_hidden(w16):
+    eng, orc, oh = make(seed=5, mtp_w16=w16)
     H = eng.desc.hidden
     eng.capture(1)
     eng.reset(200, 11)
@@ -212,13 +222,13 @@ def test_prefill_fills_the_head_like_ingest(moe):
         assert np.abs(x - y).max() <= 2e-2 * np.abs(y).max(), np.abs(x - y).max()
 
 
-@pytest.mark.parametrize("kind", ["dense", "kv8", "moe"])
+@pytest.mark.parametrize("kind", ["dense", "kv8", "moe", "w16"])
 def test_speculative_loop_emits_the_greedy_tokens(kind):
     """draft(3) -> verify -> accept_greedy -> commit, repeated, against plain generate on a twin
     engine: the same token stream, bit for bit (verify rows are bitwise the plain steps); also
-    with the main model over the int8 cache."""
+    with the main model over the int8 cache, and with the 16-bit head."""
     n = 14
-    kw = dict(head_dim=256, kv_int8=1) if kind == "kv8" else {}
+    kw = dict(head_dim=256, kv_int8=1) if kind == "kv8" else dict(mtp_w16=1) if kind == "w16" else {}
     mk = moe_small_desc if kind == "moe" else small_desc
     plain = mi.Engine(mk(mtp=1, **kw), seed=31)
     plain.capture(1)

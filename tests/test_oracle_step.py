@@ -464,13 +464,21 @@ class TinyMtp(TinyModel):
     layer with its own one-layer KV cache, the embedding / hidden / final norms; the head
     shares the model's embedding and lm_head."""
 
-    def __init__(self, seed, **kw):
+    def __init__(self, seed, w16=False, **kw):
         super().__init__(seed, **kw)
         d = self.d
         H, QH, KVH, HD, I, L = d["H"], d["QH"], d["KVH"], d["HD"], d["I"], d["L"]
         rng = np.random.default_rng(seed + 500)
+        w16s = []  # w16: the linears' f16 [N][K] matrices in orc_f16w_tile's layout
 
         def lin(K, N, S=2):
+            if w16:
+                w = f16(rng.standard_normal((N, K)) * 0.06)
+                t = np.zeros_like(w)
+                O.lib().orc_f16w_tile(O._p(w), K, N, O._p(t))
+                self.keep.append(t)
+                w16s.append(t.ctypes.data)
+                return O.Linear(None, None, 0, 0, 0), O.f16_bits_to_f32(w).astype(np.float64).T
             q = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32)
             sc = f16(rng.uniform(0.004, 0.03, (K // 64, N)))
             self.keep += [q, sc]
@@ -496,7 +504,7 @@ class TinyMtp(TinyModel):
         if d["qk_norm"]:
             Ly.q_norm, Ly.k_norm = self.hn["q_norm"].ctypes.data, self.hn["k_norm"].ctypes.data
         self.head = O.MtpHead(fc, Ly, self.hn["pre_e"].ctypes.data, self.hn["pre_h"].ctypes.data,
-                              self.hn["final"].ctypes.data)
+                              self.hn["final"].ctypes.data, *w16s)
         self.hkv_k = f16(rng.standard_normal((KVH, L, HD)))
         self.hkv_v = f16(rng.standard_normal((KVH, L, HD)))
 
@@ -568,13 +576,15 @@ def _head_case(m, tok, p, seed):
     return h, f16(h)
 
 
-@pytest.mark.parametrize("seed,p,qk_norm", [(1, 0, True), (2, 29, True), (3, 63, False)])
-def test_mtp_head_vs_independent_fp64_forward(seed, p, qk_norm):
+@pytest.mark.parametrize("seed,p,qk_norm,w16", [(1, 0, True, False), (2, 29, True, False), (3, 63, False, False),
+                                                (4, 0, True, True), (5, 40, True, True), (6, 63, False, True)])
+def test_mtp_head_vs_independent_fp64_forward(seed, p, qk_norm, w16):
     """orc_mtp_head_step against an fp64 forward of the head written here: the draft's logits,
     its output hidden and the K/V row it writes at the head position, and two chained drafts
     (the second fed the first's id and output hidden), at the dense step's bar; the fill form
-    (full = 0) writes the same K/V row and nothing else."""
-    m = TinyMtp(seed, qk_norm=qk_norm)
+    (full = 0) writes the same K/V row and nothing else. w16: the head's linears as 16-bit
+    matrices (the reference's bf16 head, loader.cc:586-597) through orc_gemv_f16w."""
+    m = TinyMtp(seed, w16=w16, qk_norm=qk_norm)
     tok = (seed * 131) % m.d["V"]
     h, h16 = _head_case(m, tok, p, seed)
     kk, vv = m.hkv_k.copy(), m.hkv_v.copy()
@@ -606,12 +616,13 @@ def test_mtp_head_vs_independent_fp64_forward(seed, p, qk_norm):
     assert np.array_equal(kf[:, mask], m.hkv_k[:, mask]) and np.array_equal(vf[:, mask], m.hkv_v[:, mask])
 
 
+@pytest.mark.parametrize("w16", [False, True])
 @pytest.mark.parametrize("mistake", ["cat_swap", "stale_resid", "head_pos", "no_final_norm"])
-def test_mtp_bar_rejects_plausible_wiring_mistakes(mistake):
+def test_mtp_bar_rejects_plausible_wiring_mistakes(mistake, w16):
     """The head's comparison is not vacuous: the fp64 forward with one plausible mistake (the
     concat halves swapped, the fc output added to a stale residual, the head's RoPE one
     position off, the final norm dropped) misses the bar."""
-    m = TinyMtp(2)
+    m = TinyMtp(2, w16=w16)
     h, h16 = _head_case(m, 77, 29, 2)
     _, got, _ = m.oracle_head(77, h16, 29, m.hkv_k.copy(), m.hkv_v.copy())
     kc = O.f16_bits_to_f32(m.hkv_k).astype(np.float64)
