@@ -5,6 +5,11 @@
 #include "mi_common.h"
 #include "gemv_core.h"
 
+// groups in flight per wave for the int8 head_dim-128 reader
+#ifndef MI_ATTN_PD8
+#define MI_ATTN_PD8 3
+#endif
+
 namespace mi {
 
 __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
@@ -96,7 +101,9 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 //           swizzle that keeps the four row groups on distinct banks; B = the weights (times the
 //           row's V scale for int8), split into f16 high and low parts like q. The int8 (or f16)
 //           V values are exact in f16.
-// Prefetch (PF): the next group's K and V registers are loaded before the current group is used.
+// Prefetch: a ring of PD groups' K and V registers per wave (PD = 3 for int8 rows of 128, 2 for
+// fp16 rows of 128 or int8 rows of 256, 1 otherwise); a group's registers take the group 4 PD
+// ahead as soon as it has been used.
 // FP (fused prep, f16 cache): the kernel also does attn_prep's work (attn.cl:361-372) for the
 // rows it needs: q of its GQA heads from the qkv partials (fold, q-norm, RoPE), and the K and V
 // rows of the step's new positions that fall in its block (fold, k-norm, RoPE, f16), which it
@@ -111,7 +118,10 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   constexpr uint32_t EB = KV8 ? 1u : 2u, ROWB = HD * EB;  // bytes per row
   constexpr uint32_t VLD = ROWB / 64u;                     // 16-byte V loads per lane (4 lanes per row)
   constexpr uint32_t CW = 16u * EB;                        // bytes of one 16-dim column
-  constexpr bool PF = (KK * (KV8 ? 2u : 4u) + VLD * 4u) <= 32u;
+  // groups in flight per wave: a ring of PD register buffers (VGPRs per group: K 2 KK (int8) or
+  // 4 KK (f16), V 4 VLD, the two int8 scales)
+  constexpr uint32_t GREG = KK * (KV8 ? 2u : 4u) + VLD * 4u;
+  constexpr uint32_t PD = GREG <= 16u ? MI_ATTN_PD8 : (GREG <= 32u ? 2u : 1u);
   constexpr uint32_t SV = 16u * ROWB;                      // one wave's staged V group
   constexpr uint32_t RED = 4u * GQA * HD * 4u;             // the end merge's accumulators
   __shared__ __align__(16) unsigned char s_buf[(4u * SV > RED ? 4u * SV : RED)];
@@ -160,54 +170,43 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   };
   const uint32_t vrow = lane >> 2, vpart = lane & 3u;  // the V row and quarter this lane loads
   // group gi whose first cache row is rb (uniform)
+  // Every lane loads whatever the group's length: rows past it re-read the group's last row
+  // (their scores are masked to -inf and their weights are 0), so no load sits under a branch
+  // and the waits for one group's loads never wait for the later groups' loads.
   auto load_group = [&](uint32_t gi, uint32_t rb, Group& g) {
     const uint32_t p0 = p_begin + 16u * gi;
-    const uint32_t glen = min(16u, p_end - p0);
-    if (qi < glen) {
-      const size_t row = (size_t)rb + qi;
+    const uint32_t glast = min(16u, p_end - p0) - 1u;
+    const size_t row = (size_t)rb + min(qi, glast);
 #pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) {
-        const size_t off = row * a.row_stride + hoff + 32 * kk + 8 * qq;
-        if constexpr (KV8 == 0)
-          g.k[kk].w = *as_global(reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(a.kv_k) + off));
-        else
-          g.k[kk].w = *as_global(reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(a.kv_k) + off));
-      }
-      if constexpr (KV8 == 1) {
-        g.ks = *as_global(a.k_scale + row * a.sc_row_stride + shoff);
-        g.vs = *as_global(a.v_scale + row * a.sc_row_stride + shoff);
-      }
-    } else {
-#pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) zero_chunk<KV8>(g.k[kk]);
-      g.ks = 0;
-      g.vs = 0;
+    for (uint32_t kk = 0; kk < KK; ++kk) {
+      const size_t off = row * a.row_stride + hoff + 32 * kk + 8 * qq;
+      if constexpr (KV8 == 0)
+        g.k[kk].w = *as_global(reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(a.kv_k) + off));
+      else
+        g.k[kk].w = *as_global(reinterpret_cast<const u2_t*>(static_cast<const int8_t*>(a.kv_k) + off));
     }
-    if (vrow < glen) {
-      const unsigned char* vb = static_cast<const unsigned char*>(a.kv_v) +
-                                (((size_t)rb + vrow) * a.row_stride + hoff) * EB + vpart * (ROWB / 4u);
-#pragma unroll
-      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = *as_global(reinterpret_cast<const u4_t*>(vb + 16u * i));
-    } else {
-#pragma unroll
-      for (uint32_t i = 0; i < VLD; ++i) g.v[i] = u4_t{0u, 0u, 0u, 0u};
+    if constexpr (KV8 == 1) {
+      g.ks = *as_global(a.k_scale + row * a.sc_row_stride + shoff);
+      g.vs = *as_global(a.v_scale + row * a.sc_row_stride + shoff);
     }
+    const unsigned char* vb = static_cast<const unsigned char*>(a.kv_v) +
+                              (((size_t)rb + min(vrow, glast)) * a.row_stride + hoff) * EB + vpart * (ROWB / 4u);
+#pragma unroll
+    for (uint32_t i = 0; i < VLD; ++i) g.v[i] = *as_global(reinterpret_cast<const u4_t*>(vb + 16u * i));
   };
 
 
   // this wave's first group goes out before anything else: its row straight from the page
   // table, the later groups' rows staged in LDS below
   // (PF: its second group too, so both are in flight while q is staged)
-  Group cur, nxt;
-  uint32_t gi = wave;
+  Group buf[PD];
   auto direct_row = [&](uint32_t g) -> uint32_t {
     const uint32_t p0 = p_begin + 16u * g;
     return __builtin_amdgcn_readfirstlane(a.pages ? a.pages[p0 / a.page] * a.page + p0 % a.page : p0);
   };
-  if (gi < ng) load_group(gi, direct_row(gi), cur);
-  if constexpr (PF) {
-    if (gi + 4u < ng) load_group(gi + 4u, direct_row(gi + 4u), nxt);
-  }
+#pragma unroll
+  for (uint32_t d = 0; d < PD; ++d)
+    if (wave + 4u * d < ng) load_group(wave + 4u * d, direct_row(wave + 4u * d), buf[d]);
   // A paged cache: a page holds whole 16-position groups, so a group's rows are consecutive.
   // Each group's first cache row is looked up once, into LDS (the only divisions by the page
   // size), so no later K/V load waits on a page-table load.
@@ -385,100 +384,100 @@ __device__ __forceinline__ void attn_block(const AttnDecodeArgs& a, uint32_t j, 
   auto group_row = [&](uint32_t g) -> uint32_t {
     return __builtin_amdgcn_readfirstlane(a.pages ? s_grow[g] : p_begin + 16u * g);
   };
-  for (; gi < ng; gi += 4u) {
-    if constexpr (PF) {
-      if (gi != wave && gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), nxt);  // (the first: above)
-    }
-    const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
-    if constexpr (FP) {
-      // the step's new positions take the rows computed above (the cache may not hold them yet)
-      const uint32_t p0 = p_begin + 16u * gi;
-      if (p0 + glen > pn0) {  // uniform
-        if (qi < glen && p0 + qi >= pn0) {
-          const uint16_t* nk = s_newk + (p0 + qi - pn0) * HD;
+  // the ring: group gi = gb + 4 ri sits in buf[ri]; once used, buf[ri] takes group gi + 4 PD
+  for (uint32_t gb = wave; gb < ng; gb += 4u * PD) {
 #pragma unroll
-          for (uint32_t kk = 0; kk < KK; ++kk) cur.k[kk].w = *reinterpret_cast<const u4_t*>(nk + 32 * kk + 8 * qq);
-        }
-        if (vrow < glen && p0 + vrow >= pn0) {
-          const unsigned char* nv = reinterpret_cast<const unsigned char*>(s_newv + (p0 + vrow - pn0) * HD);
-#pragma unroll
-          for (uint32_t i = 0; i < VLD; ++i) cur.v[i] = *reinterpret_cast<const u4_t*>(nv + vpart * (ROWB / 4u) + 16u * i);
+    for (uint32_t ri = 0; ri < PD; ++ri) {
+      const uint32_t gi = gb + 4u * ri;
+      if (gi >= ng) break;  // uniform
+      Group& cur = buf[ri];
+      const uint32_t glen = min(16u, p_end - (p_begin + 16u * gi));
+      if constexpr (FP) {
+        // the step's new positions take the rows computed above (the cache may not hold them yet)
+        const uint32_t p0 = p_begin + 16u * gi;
+        if (p0 + glen > pn0) {  // uniform
+          if (qi < glen && p0 + qi >= pn0) {
+            const uint16_t* nk = s_newk + (p0 + qi - pn0) * HD;
+  #pragma unroll
+            for (uint32_t kk = 0; kk < KK; ++kk) cur.k[kk].w = *reinterpret_cast<const u4_t*>(nk + 32 * kk + 8 * qq);
+          }
+          if (vrow < glen && p0 + vrow >= pn0) {
+            const unsigned char* nv = reinterpret_cast<const unsigned char*>(s_newv + (p0 + vrow - pn0) * HD);
+  #pragma unroll
+            for (uint32_t i = 0; i < VLD; ++i) cur.v[i] = *reinterpret_cast<const u4_t*>(nv + vpart * (ROWB / 4u) + 16u * i);
+          }
         }
       }
-    }
-    // stage this group's V rows (the previous group's reads of this wave's area are done:
-    // one wave's LDS operations complete in order, and the fence keeps the compiler's too)
-    wave_lds_sync();
-#pragma unroll
-    for (uint32_t i = 0; i < VLD; ++i) {
-      const uint32_t byte = vpart * (ROWB / 4u) + 16u * i;  // within the row
-      *reinterpret_cast<u4_t*>(sv + sv_off(vrow, byte / CW) + byte % CW) = cur.v[i];
-    }
-    wave_lds_sync();
-    // scores S^T[position 4 qq + r][head qi]
-    f4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (uint32_t kk = 0; kk < KK; ++kk) {
-      const h8_t kh = chunk_h8<KV8>(cur.k[kk]);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[0][kk][lane], d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[1][kk][lane], d, 0, 0, 0);
-    }
-    float sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t r = 0; r < 4; ++r) {
-      float rs = a.scale;
-      if constexpr (KV8 == 1) rs = a.scale * h2f((uint16_t)__shfl((int)cur.ks, (int)(4u * qq + r), 64));
-      sc[r] = 4u * qq + r < glen ? d[r] * rs : -INFINITY;
-      mx = fmaxf(mx, sc[r]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = expf(m_run - m_new);  // 0 on the first group (m_run = -inf)
-    float w[4];
-#pragma unroll
-    for (uint32_t r = 0; r < 4; ++r) w[r] = expf(sc[r] - m_new);
-    l_run = __builtin_fmaf(l_run, alpha, (w[0] + w[1]) + (w[2] + w[3]));
-    m_run = m_new;
-    if (__ballot(alpha != 1.0f)) {  // a head's max moved (a factor of 1 leaves acc unchanged)
-#pragma unroll
-      for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
-    }
-    // B operand: the weights (int8: times the row's V scale), f16 high and low parts
-    h4_t bh, bl;
-#pragma unroll
-    for (uint32_t r = 0; r < 4; ++r) {
-      float wv = w[r];
-      if constexpr (KV8 == 1) wv *= h2f((uint16_t)__shfl((int)cur.vs, (int)(4u * qq + r), 64));
-      const half_t h = (half_t)wv;
-      bh[r] = h;
-      bl[r] = (half_t)(wv - (float)h);
-    }
-    // P V per 16-dim tile: A[dim qi][position 4 qq + jj] from the staged rows
-#pragma unroll
-    for (uint32_t tt = 0; tt < NT; ++tt) {
-      h4_t av;
-      if constexpr (KV8 == 1) {
-        uint32_t b[4];
-#pragma unroll
-        for (uint32_t jj = 0; jj < 4; ++jj) b[jj] = sv[sv_off(4u * qq + jj, tt) + qi];
-        const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
-        const h2_t lo = as_h2((b[0] | (b[1] << 16)) ^ 0x64806480u) - bias;
-        const h2_t hi = as_h2((b[2] | (b[3] << 16)) ^ 0x64806480u) - bias;
-        av = h4_t{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-#pragma unroll
-        for (uint32_t jj = 0; jj < 4; ++jj)
-          av[jj] = *reinterpret_cast<const half_t*>(sv + sv_off(4u * qq + jj, tt) + 2u * qi);
+      // stage this group's V rows (the previous group's reads of this wave's area are done:
+      // one wave's LDS operations complete in order, and the fence keeps the compiler's too)
+      wave_lds_sync();
+  #pragma unroll
+      for (uint32_t i = 0; i < VLD; ++i) {
+        const uint32_t byte = vpart * (ROWB / 4u) + 16u * i;  // within the row
+        *reinterpret_cast<u4_t*>(sv + sv_off(vrow, byte / CW) + byte % CW) = cur.v[i];
       }
-      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, acc[tt], 0, 0, 0);
-      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, acc[tt], 0, 0, 0);
-    }
-    if constexpr (PF) {
-      cur = nxt;
-    } else {
-      if (gi + 4u < ng) load_group(gi + 4u, group_row(gi + 4u), cur);
+      wave_lds_sync();
+      // scores S^T[position 4 qq + r][head qi]
+      f4_t d = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (uint32_t kk = 0; kk < KK; ++kk) {
+        const h8_t kh = chunk_h8<KV8>(cur.k[kk]);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[0][kk][lane], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, s_q[1][kk][lane], d, 0, 0, 0);
+      }
+      float sc[4];
+      float mx = -INFINITY;
+  #pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) {
+        float rs = a.scale;
+        if constexpr (KV8 == 1) rs = a.scale * h2f((uint16_t)__shfl((int)cur.ks, (int)(4u * qq + r), 64));
+        sc[r] = 4u * qq + r < glen ? d[r] * rs : -INFINITY;
+        mx = fmaxf(mx, sc[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = expf(m_run - m_new);  // 0 on the first group (m_run = -inf)
+      float w[4];
+  #pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) w[r] = expf(sc[r] - m_new);
+      l_run = __builtin_fmaf(l_run, alpha, (w[0] + w[1]) + (w[2] + w[3]));
+      m_run = m_new;
+      if (__ballot(alpha != 1.0f)) {  // a head's max moved (a factor of 1 leaves acc unchanged)
+  #pragma unroll
+        for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
+      }
+      // B operand: the weights (int8: times the row's V scale), f16 high and low parts
+      h4_t bh, bl;
+  #pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) {
+        float wv = w[r];
+        if constexpr (KV8 == 1) wv *= h2f((uint16_t)__shfl((int)cur.vs, (int)(4u * qq + r), 64));
+        const half_t h = (half_t)wv;
+        bh[r] = h;
+        bl[r] = (half_t)(wv - (float)h);
+      }
+      // P V per 16-dim tile: A[dim qi][position 4 qq + jj] from the staged rows
+  #pragma unroll
+      for (uint32_t tt = 0; tt < NT; ++tt) {
+        h4_t av;
+        if constexpr (KV8 == 1) {
+          uint32_t b[4];
+  #pragma unroll
+          for (uint32_t jj = 0; jj < 4; ++jj) b[jj] = sv[sv_off(4u * qq + jj, tt) + qi];
+          const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+          const h2_t lo = as_h2((b[0] | (b[1] << 16)) ^ 0x64806480u) - bias;
+          const h2_t hi = as_h2((b[2] | (b[3] << 16)) ^ 0x64806480u) - bias;
+          av = h4_t{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+  #pragma unroll
+          for (uint32_t jj = 0; jj < 4; ++jj)
+            av[jj] = *reinterpret_cast<const half_t*>(sv + sv_off(4u * qq + jj, tt) + 2u * qi);
+        }
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bh, acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl, acc[tt], 0, 0, 0);
+      }
+      if (gi + 4u * PD < ng) load_group(gi + 4u * PD, group_row(gi + 4u * PD), cur);
     }
   }
   // merge the four waves: M = max m_w, f_w = exp(m_w - M), sum and acc weighted by f_w in
