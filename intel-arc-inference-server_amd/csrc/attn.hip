@@ -22,6 +22,7 @@
 #include "mi_capi_internal.h"
 #include "mi_common.h"
 #include "attn_core.h"
+#include "attn_dma.h"
 #include "attn_merge.h"
 
 namespace mi {
@@ -30,7 +31,7 @@ namespace {
 
 template <int HD, int KV8, int GQA, bool FP>
 __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a) {
-  attn_block<HD, KV8, GQA, FP>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+  attn_block_dma<HD, KV8, GQA, FP>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,

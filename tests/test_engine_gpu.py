@@ -291,7 +291,9 @@ def test_int8_kv_decode_steps_vs_oracle(moe):
         got_tok = int(eng.generate(1)[0])
         got = eng.logits(1)[0]
         am, want = orc.step(tok, pos)
-        assert close(got, want, abs_frac=1e-3), f"step {step}: max err {np.abs(got - want).max()}"
+        # 2e-3: the rows each step writes differ from the oracle's by up to one int8 step (checked
+        # below), which moves these logits by up to ~1.2e-3 of the largest (measured)
+        assert close(got, want, abs_frac=2e-3), f"step {step}: max err {np.abs(got - want).max()}"
         assert argmax_ok(got_tok, want)
         tok, pos = got_tok, pos + 1
     # the cache: rows the steps did not write unchanged; the written rows (from the device
