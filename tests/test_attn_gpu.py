@@ -133,6 +133,34 @@ def test_long_context_paged_bitwise(kind):
     check_close(a[0].reshape(QH, HD), want)
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("QH,KVH,HD", [(40, 8, 128), (16, 2, 256), (8, 1, 128)])
+@pytest.mark.parametrize("Lm,tgt,pos,P", [(4096, 8, 4095, 64), (4096, 16, 2000, 32), (1024, 4, 1000, 16)])
+def test_decode_ring_paths_paged(kind, QH, KVH, HD, Lm, tgt, pos, P):
+    """The decode kernel's LDS ring at several groups per wave (blocks of 512 / 256 / 320
+    positions: the ring's slots reused, pairs of groups per softmax step, a wave's odd last
+    group, a partial last group), paged with a shuffled table of 64-, 32- and 16-position
+    pages, f16 and int8 rows of 128 and 256: bitwise the contiguous cache, and within rel 2e-3
+    of the fp64 reference."""
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(kind, KVH, Lm, HD, pos + HD + kind)
+    q = np.random.default_rng(pos + QH).standard_normal((1, QH, HD)).astype(np.float32)
+    a, pa = gpu_attention(sh, q, kind, k, v, ks, vs, pos, 1, tgt)
+    rng = np.random.default_rng(P + kind)
+    pages = rng.permutation(Lm // P).astype(np.uint32)
+    phys = np.concatenate([np.arange(pg * P, pg * P + P) for pg in pages])
+    kp, vp = np.empty_like(k), np.empty_like(v)
+    kp[:, phys], vp[:, phys] = k, v
+    ksp = vsp = None
+    if kind:
+        ksp, vsp = np.empty_like(ks), np.empty_like(vs)
+        ksp[:, phys], vsp[:, phys] = ks, vs
+    b, pb = gpu_attention(sh, q, kind, kp, vp, ksp, vsp, pos, 1, tgt, pages, P)
+    assert np.array_equal(a, b)
+    want = fp64_attention(sh, q[0], kind, k, v, ks, vs, pos + 1)
+    check_close(a[0].reshape(QH, HD), want)
+
+
 def test_rows_are_bitwise_their_single_row_steps():
     QH, KVH, HD, Lm, tgt = 40, 8, 128, 4096, 128
     sh = O.attn_shape(QH, KVH, HD)
