@@ -100,12 +100,17 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
   __shared__ uint32_t s_grow[kMaxBlockGroups];
   __shared__ h8_t s_q[2][KK][64];
-  // FP: the new K/V rows (f16); the roped q of the GQA heads and the waves' normed rows live in
-  // the ring, which the fused form starts to load only after its prologue
+  // FP: the new K/V rows (f16), the roped q of the GQA heads and the waves' normed rows. At
+  // rows of 256 the last two live in the ring (LDS is short), which the fused form then starts
+  // to load only after its prologue; at rows of 128 they have arrays of their own and the ring's
+  // first groups go out first, as in the plain form.
   constexpr uint32_t FPN = FP ? 8u * HD : 1u;
   __shared__ __align__(16) uint16_t s_newk[FPN], s_newv[FPN];
-  static_assert(!FP || C::RING >= (GQA * HD + 4u * HD) * 4u, "prologue area");
-  float* const s_q32 = reinterpret_cast<float*>(s_ring);
+  constexpr bool kEarly = !FP || HD == 128;
+  constexpr uint32_t FPQ = FP && kEarly ? GQA * HD + 4u * HD : 1u;
+  __shared__ float s_fpq[FPQ];
+  static_assert(kEarly || C::RING >= (GQA * HD + 4u * HD) * 4u, "prologue area");
+  float* const s_q32 = kEarly ? s_fpq : reinterpret_cast<float*>(s_ring);
   float* const s_nrm = s_q32 + GQA * HD;
 
   const uint32_t t = opaque_tid(), lane = t & 63u;
@@ -182,7 +187,7 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
       }
     }
   };
-  if constexpr (!FP) issue_first();
+  if constexpr (kEarly) issue_first();
   // q of the GQA heads (plain form: wave 0 loads it)
   f4_t qv[FP ? 1u : 2u * KK];
   if constexpr (!FP) {
@@ -360,7 +365,7 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   }
   wait_vm<0>();   // (the compiler's waits above have seen to this already)
   lds_barrier();  // s_grow, s_q
-  if constexpr (FP) issue_first();
+  if constexpr (!kEarly) issue_first();
 
   // the running state in log2 units: scores are scaled by log2(e) so every exponential is one
   // v_exp_f32 (exp2); the partial's max goes out in natural units
