@@ -51,6 +51,31 @@ __global__ __launch_bounds__(256) void gemv_f16w_kernel(const uint16_t* __restri
 #pragma unroll
   for (uint32_t r = 0; r < R; ++r) acc[r] = 0.f;
   uint32_t k8 = 0;
+  if constexpr (R == 1) {
+    // one row: a chunk of up to 16 k8 blocks' weights and activations is loaded before any of
+    // it is used (one memory round trip per chunk; the sum's order is unchanged)
+    constexpr uint32_t CH = 16;
+    for (; k8 < per; k8 += CH) {
+      uint16_t wv[CH][8];
+      u4_t xv[CH];
+#pragma unroll
+      for (uint32_t u = 0; u < CH; ++u) {
+        const uint32_t kk = min(k8 + u, per - 1u);  // (past the slice: re-read, not added)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) wv[u][j] = tile[(size_t)kk * 128 + j * 16];
+        xv[u] = *reinterpret_cast<const u4_t*>(xr + (size_t)kk * 8);
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < CH; ++u) {
+        if (k8 + u < per) {
+          const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+          for (uint32_t j = 0; j < 8; ++j)
+            acc[0] += h2f(wv[u][j]) * h2f((uint16_t)(xw[j / 2] >> (16 * (j % 2))));
+        }
+      }
+    }
+  }
   for (; k8 + 4 <= per; k8 += 4) {
     uint16_t wv[4][8];
 #pragma unroll
