@@ -608,11 +608,12 @@ int mi_engine_ingest(mi_engine* e, const uint32_t* ids, uint32_t n);
 int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t chunk);
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
 /* Measurement (no reference counterpart: the role of the reference's per-kernel timing in
- * tools/bench): `reps` rounds of one linear's single-row step launch, exactly as the step
- * issues it (which = 0 qkv with attn_prep, 1 o + residual + norm, 2 gate||up + silu*up,
- * 3 down + residual + norm: each layer's in turn; 4 the lm_head + argmax parts), back to back
- * on the engine's stream; *ms_per_launch = the HIP-event time per launch. The launches rewrite
- * the step's state: reset the engine (mi_engine_reset) before generating again. */
+ * tools/bench): `reps` rounds of one linear's step launch, exactly as the step issues it
+ * (which bits 0-7 = 0 qkv with attn_prep, 1 o + residual + norm, 2 gate||up + silu*up,
+ * 3 down + residual + norm: each layer's in turn; 4 the lm_head + argmax parts; bits 8-15 =
+ * the rows M, 1..8, 0 meaning 1), back to back on the engine's stream; *ms_per_launch = the
+ * HIP-event time per launch. The launches rewrite the step's state: reset the engine
+ * (mi_engine_reset) before generating again. */
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
  * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. k + 1 <= max_rows;

@@ -504,8 +504,13 @@ struct mi_engine {
   // consumers' all-to-all exchange of tile sums. The last layer's down (the head's input, which
   // the MTP head copies too) and MoE layers (the router and the experts read x) keep x.
   // (The launches that form the norm take at most 8 k-groups per slice and 256 tile sums: a
-  // model whose split-K widths leave more keeps x throughout.)
-  bool split_norm() const {
+  // model whose split-K widths leave more keeps x throughout.) Single-row steps only: at 2..8
+  // rows every work-group of gate||up forming its rows' norm costs more than the exchange it
+  // spares (measured at the 27B shape, rows 2 / 4 / 8: 5.30 / 6.13 / 8.83 ms split against
+  // 5.01 / 5.51 / 6.65 ms with x written by the consumers; one row: 4.22 ms either way or
+  // better split).
+  bool split_norm(uint32_t M) const {
+    if (M > 1) return false;
     if (d.experts || d.hidden / 64 > 256 || (d.hidden / 64) % 4) return false;
     auto ok = [](const Linear& l) { return (l.K / 64) / l.S <= 8; };
     for (uint32_t li = 0; li < d.layers; ++li)
@@ -548,7 +553,7 @@ struct mi_engine {
                              d.act_bf16, stream));
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      MI_TRY(launch_qkv(li, M, li > 0 && split_norm()));
+      MI_TRY(launch_qkv(li, M, li > 0 && split_norm(M)));
       if (d.kv_int8) {  // capture.cc fa_layer under --kv-cache int8: kv8.cl's writer and reader pair
         int8_t* lk = static_cast<int8_t*>(kv_k) + li * layer_kv;
         int8_t* lv = static_cast<int8_t*>(kv_v) + li * layer_kv;
@@ -578,7 +583,7 @@ struct mi_engine {
         continue;
       }
       MI_TRY(launch_gate_up(L, M));
-      MI_TRY(launch_down(L, M, next_w, split_norm() && li + 1 < d.layers));
+      MI_TRY(launch_down(L, M, next_w, split_norm(M) && li + 1 < d.layers));
     }
     MI_TRY(head(ctrl, M, x, logits, history));
     if (d.mtp) {
@@ -655,7 +660,7 @@ struct mi_engine {
     const bool verify_attn = !d.kv_int8 && mi_attn_verify_binds(M, 0, d.q_heads, d.kv_heads);
     for (uint32_t li = 0; li < d.layers; ++li) {
       const Layer& L = layer[li];
-      const bool ni = li > 0 && split_norm();
+      const bool ni = li > 0 && split_norm(kRowChunk);
       void* lk = d.kv_int8 ? static_cast<void*>(static_cast<int8_t*>(kv_k) + li * layer_kv)
                            : static_cast<void*>(static_cast<uint16_t*>(kv_k) + li * layer_kv);
       void* lv = d.kv_int8 ? static_cast<void*>(static_cast<int8_t*>(kv_v) + li * layer_kv)
@@ -703,7 +708,7 @@ struct mi_engine {
           MI_TRY(moe_block(L, Mc, next_w));
         } else {
           MI_TRY(launch_gate_up(L, Mc));
-          MI_TRY(launch_down(L, Mc, next_w, split_norm() && li + 1 < d.layers));
+          MI_TRY(launch_down(L, Mc, next_w, split_norm(kRowChunk) && li + 1 < d.layers));
         }
       }
     }
@@ -875,7 +880,7 @@ struct mi_engine {
   }
   // o with the residual fold and the post-attention norm
   int launch_o(const Layer& L, uint32_t M) {
-    const mi_gemv_epilogue eo = resid_epi(L.post_norm, split_norm());
+    const mi_gemv_epilogue eo = resid_epi(L.post_norm, split_norm(M));
     return mi_gemv_w4a16_ex(L.o.q, L.o.s, attn_out, part_ex, M, L.o.K, L.o.N, L.o.S, &eo, stream);
   }
   // gate||up with silu * up
@@ -886,8 +891,8 @@ struct mi_engine {
     eg.status = ctrl + MI_CTRL_DEBUG;
     eg.arrive = use_arrive ? arrive : nullptr;
     eg.act = d.act_bf16;
-    if (split_norm()) norm_in(eg, L.post_norm);
-    return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, split_norm() ? resid : x, part_ex, M, L.gate_up.K,
+    if (split_norm(M)) norm_in(eg, L.post_norm);
+    return mi_gemv_w4a16_ex(L.gate_up.q, L.gate_up.s, split_norm(M) ? resid : x, part_ex, M, L.gate_up.K,
                             L.gate_up.N, L.gate_up.S, &eg, stream);
   }
   // down with the residual fold and the next norm (the next layer's, the final one, the head's);
@@ -912,19 +917,21 @@ struct mi_engine {
   // turn; 4 the lm_head) back to back on the stream, HIP events around; *ms = the average per
   // launch. The launches rewrite the step's buffers (residual, KV row at pos, logits): the
   // caller resets the engine afterwards.
-  int bench_linear(uint32_t which, uint32_t reps, float* ms) {
-    if (which > 4 || reps == 0 || !ms) return mi_fail(MI_ERR_ARG, "engine_bench_linear: which 0..4, reps > 0");
+  int bench_linear(uint32_t which_rows, uint32_t reps, float* ms) {
+    const uint32_t which = which_rows & 0xFFu, M = (which_rows >> 8) ? (which_rows >> 8) : 1u;
+    if (which > 4 || reps == 0 || !ms || M > kRowChunk || M > d.max_rows)
+      return mi_fail(MI_ERR_ARG, "engine_bench_linear: which 0..4, rows 1..8, reps > 0");
     if (d.experts && (which == 2 || which == 3))
       return mi_fail(MI_ERR_SHAPE, "engine_bench_linear: an MoE model has no dense gate_up / down");
     auto one = [&](uint32_t li) -> int {
       switch (which) {
-        case 0: return launch_qkv(li, 1, li > 0 && split_norm());
-        case 1: return launch_o(layer[li], 1);
-        case 2: return launch_gate_up(layer[li], 1);
-        case 3: return launch_down(layer[li], 1, next_norm(li), split_norm() && li + 1 < d.layers);
+        case 0: return launch_qkv(li, M, li > 0 && split_norm(M));
+        case 1: return launch_o(layer[li], M);
+        case 2: return launch_gate_up(layer[li], M);
+        case 3: return launch_down(layer[li], M, next_norm(li), split_norm(M) && li + 1 < d.layers);
         default:
-          return d.lm_head_int8 ? mi_gemv_i8w(lm_i8, lm_i8s, x, logits, 1, d.hidden, d.vocab, stream)
-                                : launch_lm_head(1, x, logits);
+          return d.lm_head_int8 ? mi_gemv_i8w(lm_i8, lm_i8s, x, logits, M, d.hidden, d.vocab, stream)
+                                : launch_lm_head(M, x, logits);
       }
     };
     const uint32_t per_round = which == 4 ? 1u : d.layers;
