@@ -120,6 +120,7 @@ struct GemvEpi {
   const float* in_sums;
   const float* in_norm_w;
   float in_eps;
+  uint32_t row_cons;  // set by the launch: RESID's extra consumers are one grid row per row m
 };
 
 // arrival words sit 128 bytes apart: no two tiles' counts share a cache line
@@ -384,7 +385,11 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   const uint32_t g_begin = s * gps + wave;
   // QKV's fixed consumer row (s = S) has no slice of its own
   // an extra consumer row (QKV always; the others when epi.extra_row) has no slice of its own
-  const bool xrow_c = (EPI == EPI_QKV || epi.extra_row) && !dyn && s + 1 == gridDim.y;
+  // RESID over several rows (row_cons): one consumer work-group per (tile, row), in grid rows
+  // S_p .. S_p + M - 1 after the S_p producer rows
+  const bool rowc = MR > 1 && EPI == EPI_RESID && epi.row_cons;
+  const uint32_t S_p = (K / 64u) / gps;
+  const bool xrow_c = (EPI == EPI_QKV || epi.extra_row) && !dyn && (rowc ? s >= S_p : s + 1 == gridDim.y);
   const uint32_t g_end = xrow_c ? 0u : (s + 1) * gps;
   const bool xrow = c4 < M;  // this lane feeds activation row c4 of the A operand
 
@@ -565,8 +570,10 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     }
   }
   const uint32_t total = M * kCols;
-  const uint32_t S = gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
-  const bool consumer = EPI != EPI_PARTIALS && EPI != EPI_QKV && !dyn && s + 1 == S;
+  const uint32_t S = rowc ? S_p + 1u : gridDim.y, tile = blockIdx.x, ntiles = gridDim.x;
+  const bool consumer = EPI != EPI_PARTIALS && EPI != EPI_QKV && !dyn && (rowc ? s >= S_p : s + 1 == S);
+  // the rows a consumer folds and finishes: all M, or its own row
+  const uint32_t r_lo = rowc ? s - S_p : 0u, r_n = rowc ? 1u : M, rs = rowc ? M : 1u;
   for (uint32_t i = threadIdx.x; i < total; i += 256u) {
     const uint32_t row = i / kCols, col = i % kCols;
     float v = red[0][row][col];
@@ -608,8 +615,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   if constexpr (EPI == EPI_RESID) {
 #pragma unroll
     for (int k = 0; k < (MR + kWaves - 1) / kWaves; ++k) {
-      const uint32_t row = wave + kWaves * k;
-      if (row < M) r_pre[k] = epi.resid[(size_t)row * N + n0 + lane];
+      const uint32_t row = r_lo + wave + kWaves * k;
+      if (row < r_lo + r_n) r_pre[k] = epi.resid[(size_t)row * N + n0 + lane];
     }
     if (!epi.sums_out) w_pre = epi.next_w[n0 + lane];  // (the split form has no norm weights)
   }
@@ -619,30 +626,33 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
   {
     // sum_s partials[s][row][n] from 0.f in ascending s, polled in rounds of `per_round`
     // slices (the fixed consumer's own slice S-1 is the last term, from red[0])
-    // (thread t folds elements t + 256 u of the tile's M x 64)
+    // (thread t folds elements t + 256 u of the consumer's r_n x 64)
     constexpr int EL = MR * kCols / 256 > 0 ? MR * kCols / 256 : 1;
-    const uint32_t per_round = kFoldBuf / total;
+    const uint32_t ctot = r_n * kCols;
+    const uint32_t per_round = kFoldBuf / ctot;
     float a[EL];
 #pragma unroll
     for (int u = 0; u < EL; ++u) a[u] = 0.f;
     for (uint32_t s0 = 0; s0 < npoll; s0 += per_round) {
       const uint32_t ns = min(per_round, npoll - s0);
-      // element e: row-slice e / 64 of slices s0.., column e % 64 (e / 64 = t / 64 + 4 u)
-      poll_into<kFoldBuf>(s_fold, ns * total, partials + (size_t)s0 * M * N,
-                          ((t / kCols) * N + n0 + t % kCols) * 4u, 4u * N * 4u, epi.status, epi.poll_limit);
+      // element e: row-slice e / 64 of slices s0.. (its row at e / 64 rows of rs apart from
+      // row r_lo), column e % 64 (e / 64 = t / 64 + 4 u)
+      poll_into<kFoldBuf>(s_fold, ns * ctot, partials + (size_t)s0 * M * N,
+                          ((t / kCols) * rs * N + r_lo * N + n0 + t % kCols) * 4u, 4u * rs * N * 4u, epi.status,
+                          epi.poll_limit);
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < EL; ++u) {
         const uint32_t i = t + 256u * u;
-        if (i < total)
-          for (uint32_t j = 0; j < ns; ++j) a[u] += s_fold[j * total + i];
+        if (i < ctot)
+          for (uint32_t j = 0; j < ns; ++j) a[u] += s_fold[j * ctot + i];
       }
       __syncthreads();
     }
 #pragma unroll
     for (int u = 0; u < EL; ++u) {
       const uint32_t i = t + 256u * u;
-      if (i < total) red[0][i / kCols][i % kCols] = own ? a[u] + red[0][i / kCols][i % kCols] : a[u];
+      if (i < ctot) red[0][r_lo + i / kCols][i % kCols] = own ? a[u] + red[0][i / kCols][i % kCols] : a[u];
     }
     __syncthreads();
   }
@@ -653,8 +663,8 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
     // 256-lane tree over a 64-element chunk (lanes 64..255 add exact zeros)
 #pragma unroll
     for (int k = 0; k < (MR + kWaves - 1) / kWaves; ++k) {
-      const uint32_t row = wave + kWaves * k;
-      if (row >= M) break;
+      const uint32_t row = r_lo + wave + kWaves * k;
+      if (row >= r_lo + r_n) break;
       const uint16_t rb = res_rne(res_widen(r_pre[k], epi.act) + act_round(folded(row, lane), epi.act), epi.act);
       epi.resid[(size_t)row * N + n0 + lane] = rb;
       const float v = res_widen(rb, epi.act);
@@ -671,14 +681,14 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       for (uint32_t c = lane; c < ntiles; c += 64u) st_agent(epi.sumsq + ((size_t)c * M + row) * ntiles + tile, a);
     }
     if (epi.sums_out) {  // uniform; the rstd words after the sums are empty again
-      if (tile == 0 && t < M) reinterpret_cast<uint32_t*>(epi.sums_out)[(size_t)M * ntiles + t] = kEmpty;
+      if (tile == 0 && t < r_n) reinterpret_cast<uint32_t*>(epi.sums_out)[(size_t)M * ntiles + r_lo + t] = kEmpty;
       return;
     }
     // all tiles' sums of this launch: sumsq[tile][row][g], g ascending, polled in rounds of rows
     __shared__ float s_rstd[16];
     const uint32_t rows_per_round = kFoldBuf / ntiles;
-    for (uint32_t r0 = 0; r0 < M; r0 += rows_per_round) {
-      const uint32_t nr = min(rows_per_round, M - r0);
+    for (uint32_t r0 = r_lo; r0 < r_lo + r_n; r0 += rows_per_round) {
+      const uint32_t nr = min(rows_per_round, r_lo + r_n - r0);
       poll_into<kFoldBuf>(s_fold, nr * ntiles, epi.sumsq + ((size_t)tile * M + r0) * ntiles, t * 4u, 1024u,
                           epi.status, epi.poll_limit);
       __syncthreads();
@@ -690,11 +700,11 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       }
       __syncthreads();
     }
-    for (uint32_t row = wave; row < M; row += kWaves) {
+    for (uint32_t row = r_lo + wave; row < r_lo + r_n; row += kWaves) {
       const uint32_t n = n0 + lane;
       epi.x_next[(size_t)row * N + n] = act_enc(red[1][row][lane] * s_rstd[row] * w_pre, epi.act);
     }
-    if (tile == 0 && t < M) epi.rstd[t] = s_rstd[t];
+    if (tile == 0 && t < r_n) epi.rstd[r_lo + t] = s_rstd[r_lo + t];
   } else if constexpr (EPI == EPI_SILU) {
     // 64 interleave16 columns = 32 outputs k = 32 tile + i (gate at gflat, up at gflat + 16)
     for (uint32_t i = t; i < 32u * M; i += 256u) {
@@ -759,7 +769,8 @@ int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float
   // extra_row), or slice S-1
   GemvEpi e = epi;
   e.extra_row = EPI == EPI_RESID && !epi.arrive && kExtraRow;
-  dim3 grid(N / kCols, (EPI == EPI_QKV || e.extra_row) && !epi.arrive ? S + 1 : S);
+  e.row_cons = e.extra_row && M > 1;
+  dim3 grid(N / kCols, (EPI == EPI_QKV || e.extra_row) && !epi.arrive ? S + (e.row_cons ? M : 1u) : S);
   if constexpr (EPI == EPI_PARTIALS || EPI == EPI_SILU || EPI == EPI_QKV) {
     if (epi.in_sums) {
       gemv_w4a16_kernel<MR, 2, EPI, true><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
