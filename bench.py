@@ -470,6 +470,22 @@ def measure_mtp(args, moe=False, w16=False):
                     "synchronisation per call); the plain step is HIP-event timed"}
 
 
+def measure_verify_steps(eng, ctx, tok0, rows=(1, 2, 3, 4, 5, 6, 7, 8), reps=20):
+    """The small-M verify step (the reference's gemm_sm lists, docs/12-kernels.md:409-412): the
+    captured M-row step with all M rows live at context `ctx` (mi_engine_bench_verify: per step
+    the rows' control reset and the graph, HIP-event timed), and its cost in plain steps."""
+    ms = {}
+    for M in rows:
+        eng.reset(ctx, tok0)
+        t = C.c_float()
+        mi.check(mi.lib().mi_engine_bench_verify(eng._h, M, reps, C.byref(t)), "engine_bench_verify")
+        ms[M] = float(t.value)
+    eng.reset(ctx, tok0)
+    return {"workload": f"27B-shape verify step, M live rows at context {ctx} (ids: the current token in each)",
+            "ms": {str(M): round(v, 4) for M, v in ms.items()},
+            "plain_steps": {str(M): round(v / ms[1], 3) for M, v in ms.items()}}
+
+
 def measure_cfg3(st, ctx, tgt=64):
     """one layer's decode attention at context `ctx`, 40 q / 8 kv heads
     of 128, int8 K/V uniform [-127, 127] with fp16 scales U(0.005, 0.05) per (pos, kv head),
@@ -978,6 +994,10 @@ def main():
         tok_s = 1000.0 / ms_per_step
         log(f"bench: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms wall -> {tok_s:.1f} tok/s")
 
+    verify = None
+    if not args.eager and not args.no_other:
+        verify = measure_verify_steps(eng, args.context, tok0)
+        log(f"bench: verify steps {verify}")
     roof, alg_gemv = step_gemv_roofline(eng)
     plain, _ = gemv_roofline(eng)
     roof["plain_sweep"] = {k: plain[k] for k in ("achieved", "frac", "gemv_ms_per_step", "avg_launch_us")}
@@ -1006,6 +1026,7 @@ def main():
         other["cfg5_small_m_gemv"] = measure_cfg5(None)
         log(f"bench: cfg5 {other['cfg5_small_m_gemv']}")
         other["prefill_27b"] = prefill
+        other["verify_steps_27b"] = verify
         other["bf16_27b_step"] = measure_bf16_step(args)
         log(f"bench: bf16 {other['bf16_27b_step']}")
         other["cfg4_moe_step"] = measure_cfg4(args)

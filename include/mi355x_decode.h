@@ -615,6 +615,14 @@ int mi_engine_read_ctrl(mi_engine* e, uint32_t* out /* MI_CTRL_WORDS */);
  * HIP-event time per launch. The launches rewrite the step's state: reset the engine
  * (mi_engine_reset) before generating again. */
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch);
+/* Measurement (no reference counterpart: the role of the reference's verify-step timing,
+ * docs/12-kernels.md:409-412): `reps` M-row verify steps at the current position with all M
+ * rows live (ids: cur_token in each), M = bits 0-7 of rows_mode; each step = the rows' control
+ * reset + the captured M-row graph (captured here if not yet; bit 8 set: the same step
+ * enqueued kernel by kernel, for kernel tracers), back to back on the engine's stream;
+ * *ms_per_step = the HIP-event time per step. pos and cur_token are left as they were
+ * (n_active 1); the cache rows pos .. pos + M - 1 are overwritten. */
+int mi_engine_bench_verify(mi_engine* e, uint32_t rows_mode, uint32_t reps, float* ms_per_step);
 /* Engine::verify (engine.cc:868-926): one (k+1)-row step over [cur_token, drafts];
  * argmax_rows gets the k+1 row argmaxes; pos stays at the verify position. k + 1 <= max_rows;
  * a list of more than 8 rows (the reference's wide and deep lists, verify_attn.h:65-92) runs

@@ -90,6 +90,7 @@ SIGNATURES = {
     "mi_attn_prep_rows": (i32, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp, u32, vp]),
     "mi_attn_prefill_kv8": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, sz, vp, u32, u32, u32, vp, vp, vp, vp]),
     "mi_engine_bench_linear": (i32, [vp, u32, u32, vp]),
+    "mi_engine_bench_verify": (i32, [vp, u32, u32, vp]),
     "mi_engine_read_ctrl": (i32, [vp, vp]),
     "mi_engine_verify": (i32, [vp, vp, u32, vp]),
     "mi_engine_commit": (i32, [vp, u32, u32, u32]),

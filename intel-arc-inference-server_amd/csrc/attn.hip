@@ -173,7 +173,7 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
   a.pages = pages; a.attn_part = attn_part; a.row_stride = row_stride; a.head_stride = head_stride;
   a.sc_row_stride = sc_row_stride; a.sc_head_stride = sc_head_stride; a.page = page; a.M = M;
   a.q_heads = shape->q_heads; a.kv_heads = shape->kv_heads; a.tgt = tgt; a.kv_len = kv_len; a.scale = shape->scale;
-  dim3 grid(shape->kv_heads, tgt, M);
+  dim3 grid(shape->kv_heads, tgt, attn_row_groups(M, gqa));
   hipStream_t st = (hipStream_t)stream;
   if (HD == 128) {
     if (kv_kind == 0) launch_decode<128, 0, false>(a, gqa, grid, st);

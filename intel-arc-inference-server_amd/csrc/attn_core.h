@@ -12,6 +12,18 @@ __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
   return p < 64u ? 64u : p;
 }
 
+// list rows one decode work-group takes: the 16 columns of the matrix products hold
+// 16 / GQA rows' q heads (the fused prep: one row)
+__host__ __device__ constexpr uint32_t attn_rows_per_wg(uint32_t gqa, bool fused_prep) {
+  return fused_prep || gqa == 0 || gqa > 16 ? 1u : 16u / gqa;
+}
+// work-groups over the rows of an M-row list: RPW at a time, plus one for the split where the
+// block size changes
+__host__ inline uint32_t attn_row_groups(uint32_t M, uint32_t gqa) {
+  const uint32_t rpw = attn_rows_per_wg(gqa, false);
+  return (M + rpw - 1) / rpw + (M > 1 && rpw > 1 ? 1u : 0u);
+}
+
 // 16-position groups whose cache rows one work-group stages for a paged cache (a block of
 // ppw positions holds ppw / 16 groups; ppw is a multiple of 64)
 constexpr uint32_t kMaxBlockGroups = 512;

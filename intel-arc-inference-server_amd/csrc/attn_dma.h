@@ -2,9 +2,16 @@
 // src/kernels/attn_v2.cl:172, and its int8 reader, src/kernels/kv8.cl:535) with the K/V rows
 // streamed into LDS by gfx950's direct global-to-LDS loads.
 //
-// Per work-group (kv head j, block blk, row m) the block's 16-position groups are dealt to the
-// four waves round-robin, as in attn_block; each wave keeps its own online softmax and the
-// waves merge once at the end into the block's partial {max, sum, acc[HD]}.
+// Per work-group (kv head j, block blk, rows r_lo .. r_hi - 1) the block's 16-position groups
+// are dealt to the four waves round-robin; each wave keeps its own online softmax and the
+// waves merge once at the end into each (row, head)'s partial {max, sum, acc[HD]}.
+//
+// Rows. The matrix products have 16 columns, one per (row, q head): a plain launch gives a
+// work-group RPW = 16 / GQA consecutive rows of the list that share the block size (column
+// c = GQA rr + g is row r_lo + rr, head j GQA + g), so the block's K/V rows are read once for
+// all of them. Row r sees positions < pos + r + 1: its scores past that are -inf and a group
+// that holds none of its positions leaves its state untouched (alpha 1, weights 0), so each
+// column's values are, operation for operation, those of a one-row work-group for its row.
 //
 // Loads. A wave owns a ring of NB group slots in LDS. A group's 16 K rows and 16 V rows go
 // into a slot with global_load_lds_dwordx4: one instruction moves 1 KB, lane L writing LDS
@@ -89,12 +96,13 @@ __device__ __forceinline__ void wait_group(uint32_t after) {  // after: groups i
 }
 
 template <int HD, int KV8, int GQA, bool FP>
-__device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t j, uint32_t blk, uint32_t m) {
+__device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t j, uint32_t blk, uint32_t zg) {
   static_assert(!FP || KV8 == 0, "the fused prep writes the f16 cache");
   using C = AttnDmaCfg<HD, KV8>;
   constexpr uint32_t KK = HD / 32, NT = HD / 16;
   constexpr uint32_t ROWB = C::ROWB, CPR = C::CPR, GB = C::GB, NB = C::NB, SLOT = C::SLOT;
-  constexpr uint32_t RED = 4u * GQA * HD * 4u;  // the end merge's accumulators
+  constexpr uint32_t RPW = attn_rows_per_wg(GQA, FP), NC = RPW * GQA;  // rows, live columns
+  constexpr uint32_t RED = 4u * NC * HD * 4u;  // the end merge's accumulators
   static_assert(C::RING >= RED, "merge area");
   __shared__ __align__(16) unsigned char s_ring[C::RING];
   __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
@@ -116,16 +124,43 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   const uint32_t t = opaque_tid(), lane = t & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const uint32_t qi = lane & 15u, qq = lane >> 4;
-  const uint32_t n_act = a.ctrl[CTRL_NACT];
-  if (m >= n_act) return;
+  const uint32_t n_act = min(a.ctrl[CTRL_NACT], a.M);
   const uint32_t pos = a.ctrl[CTRL_POS];
-  uint32_t L = pos + m + 1;
-  if (a.kv_len && L > a.kv_len) L = a.kv_len;
+  auto row_len = [&](uint32_t r) {  // the keys row r sees
+    const uint32_t len = pos + r + 1u;
+    return a.kv_len && len > a.kv_len ? a.kv_len : len;
+  };
+  // this work-group's rows [r_lo, r_hi): the list's rows split where the block size changes
+  // (row b on; the size is non-decreasing in the row and, rounded to 64 positions of
+  // ceil(len / tgt), changes at most once over 64 consecutive rows), then RPW at a time
+  uint32_t r_lo, r_hi;
+  if constexpr (RPW == 1) {
+    r_lo = zg;
+    r_hi = zg + 1u;
+    if (zg >= n_act) return;
+  } else {
+    const uint32_t s0 = v2_ppw(row_len(0), a.tgt);
+    uint32_t b = n_act;
+    for (uint32_t r = 1; r < n_act; ++r)
+      if (v2_ppw(row_len(r), a.tgt) != s0) {
+        b = r;
+        break;
+      }
+    const uint32_t za = (b + RPW - 1u) / RPW;
+    r_lo = zg < za ? zg * RPW : b + (zg - za) * RPW;
+    r_hi = min(r_lo + RPW, zg < za ? b : n_act);
+    if (r_lo >= r_hi) return;
+  }
+  const uint32_t m = r_lo;  // the fused prep's row (RPW = 1)
+  const uint32_t L = row_len(r_hi - 1u);
   const uint32_t s = v2_ppw(L, a.tgt);
   uint32_t nb = (L - 1) / s + 1;
   if (nb > a.tgt) nb = a.tgt;
   if (blk >= nb) return;
   const uint32_t p_begin = blk * s, p_end = min(p_begin + s, L);
+  // this lane's column: its row's end in the block (p_begin: no column, or the row ends before)
+  const uint32_t crow = r_lo + qi / GQA;
+  const uint32_t pe_col = qi < NC && crow < r_hi ? max(min(p_begin + s, row_len(crow)), p_begin) : p_begin;
   const uint32_t ng = (p_end - p_begin + 15u) / 16u;
   const uint32_t ngw = wave < ng ? (ng - wave + 3u) / 4u : 0u;  // this wave's groups
 
@@ -191,8 +226,8 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   // q of the GQA heads (plain form: wave 0 loads it)
   f4_t qv[FP ? 1u : 2u * KK];
   if constexpr (!FP) {
-    if (wave == 0 && qi < GQA) {
-      const float* qp = a.attn_q + ((size_t)m * a.q_heads + j * GQA + qi) * HD + 8 * qq;
+    if (wave == 0 && qi < NC && crow < r_hi) {
+      const float* qp = a.attn_q + ((size_t)crow * a.q_heads + j * GQA + qi % GQA) * HD + 8 * qq;
 #pragma unroll
       for (uint32_t kk = 0; kk < KK; ++kk) {
         qv[2 * kk] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk));
@@ -339,7 +374,7 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
 #pragma unroll
     for (uint32_t kk = 0; kk < KK; ++kk) {
       float v[8];
-      if (qi < GQA) {
+      if (qi < NC && crow < r_hi) {
         if constexpr (FP) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = s_q32[qi * HD + 32 * kk + 8 * qq + e];
@@ -400,12 +435,13 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
     const bool has1 = NG == 2 && tw + 1 < ngw;
     const uint32_t last = has1 ? tw + 1 : tw;
     wait_group<NB, C::DG>(min(ngw, tw + NB) - last - 1u);
-    uint32_t glen[NG], slot[NG];
+    uint32_t glen[NG], slot[NG], p0g[NG];
 #pragma unroll
     for (uint32_t u = 0; u < NG; ++u) {
       const uint32_t tg = u && has1 ? tw + 1 : tw;  // a missing second group reads the first's slot
       slot[u] = ring_lds + (tg % NB) * SLOT;
-      glen[u] = u && !has1 ? 0u : min(16u, p_end - (p_begin + 16u * (wave + 4u * tg)));
+      p0g[u] = p_begin + 16u * (wave + 4u * tg);
+      glen[u] = u && !has1 ? 0u : min(16u, p_end - p0g[u]);
       if constexpr (FP) {
         // the step's new positions take the rows computed above (the cache may not hold them
         // yet): they overwrite the group's loaded rows in the slot, chunk c at c ^ f(row)
@@ -507,19 +543,21 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
           rs = qscale * h2f((uint16_t)(((er + kpar0) & 1u) ? kw[u][r] >> 16 : kw[u][r] & 0xFFFFu));
           vsv[u][r] = h2f((uint16_t)(((er + vpar0) & 1u) ? vw[u][r] >> 16 : vw[u][r] & 0xFFFFu));
         }
-        sc[u][r] = 4u * qq + r < glen[u] ? (dh[u][r] + dl[u][r]) * rs : -INFINITY;
+        sc[u][r] = 4u * qq + r < glen[u] && p0g[u] + 4u * qq + r < pe_col ? (dh[u][r] + dl[u][r]) * rs : -INFINITY;
         mx = fmaxf(mx, sc[u][r]);
       }
     }
     mx = head_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first group
+    // a column none of whose positions are in these groups keeps its state
+    const bool colive = p0g[0] < pe_col;
+    const float m_new = colive ? fmaxf(m_run, mx) : m_run;
+    const float alpha = colive ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 on the first group
     float w[NG][4];
     float wsum = 0.f;
 #pragma unroll
     for (uint32_t u = 0; u < NG; ++u) {
 #pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) w[u][r] = __builtin_amdgcn_exp2f(sc[u][r] - m_new);
+      for (uint32_t r = 0; r < 4; ++r) w[u][r] = colive ? __builtin_amdgcn_exp2f(sc[u][r] - m_new) : 0.f;
       wsum += (w[u][0] + w[u][1]) + (w[u][2] + w[u][3]);
     }
     l_run = __builtin_fmaf(l_run, alpha, wsum);
@@ -580,14 +618,15 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
     st_l[wave][qi] = l;
   }
   lds_barrier();  // every wave is done with its ring, which the merge reuses
-  float* red = reinterpret_cast<float*>(s_ring);  // [4][GQA][HD]
-  if (qi < GQA) {
+  float* red = reinterpret_cast<float*>(s_ring);  // [4][NC][HD]
+  const uint32_t nlc = (r_hi - r_lo) * GQA;  // the live columns
+  if (qi < nlc) {
 #pragma unroll
     for (uint32_t tt = 0; tt < NT; ++tt)
 #pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) red[(wave * GQA + qi) * HD + 16u * tt + 4u * qq + r] = acc[tt][r];
+      for (uint32_t r = 0; r < 4; ++r) red[(wave * NC + qi) * HD + 16u * tt + 4u * qq + r] = acc[tt][r];
   }
-  if (t < GQA) {
+  if (t < nlc) {
     float M = st_m[0][t];
 #pragma unroll
     for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][t]);
@@ -602,12 +641,14 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
     st_hs[t] = sm;
   }
   lds_barrier();
-  for (uint32_t idx = t; idx < GQA * HD; idx += 256u) {
-    const uint32_t g = idx / HD, dd = idx % HD;
+  for (uint32_t idx = t; idx < nlc * HD; idx += 256u) {
+    const uint32_t g = idx / HD, dd = idx % HD, row = r_lo + g / GQA;
+    // a row whose keys end before this block has no partial here
+    if (blk * s >= row_len(row)) continue;
     float v = 0.f;
 #pragma unroll
-    for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * GQA + g) * HD + dd], st_f[w2][g], v);
-    float* out = a.attn_part + (((size_t)(j * GQA + g) * a.tgt + blk) * a.M + m) * (HD + 2);
+    for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * NC + g) * HD + dd], st_f[w2][g], v);
+    float* out = a.attn_part + (((size_t)(j * GQA + g % GQA) * a.tgt + blk) * a.M + row) * (HD + 2);
     *as_global(out + 2 + dd) = v;
     if (dd == 0) {
       out[0] = st_hm[g];

@@ -952,6 +952,47 @@ struct mi_engine {
     return check_handoff();
   }
 
+  // `reps` verify steps of M live rows at the current position (ids: cur_token in every row),
+  // each the rows' control reset (one one-thread kernel) and the captured M-row graph (bit 8 of
+  // rows_mode: the same step enqueued kernel by kernel, for kernel tracers), back to
+  // back on the engine's stream; *ms = the HIP-event time per step. Leaves pos and cur as they
+  // were, n_active 1; the cache rows pos .. pos + M - 1 hold the last step's K/V.
+  int bench_verify(uint32_t rows_mode, uint32_t reps, float* ms) {
+    const uint32_t M = rows_mode & 0xFFu;
+    const bool eager = rows_mode & 0x100u;
+    if (M == 0 || M > d.max_rows || reps == 0 || !ms || (rows_mode >> 9))
+      return mi_fail(MI_ERR_ARG, "engine_bench_verify: bad args");
+    if (!eager) MI_TRY(capture(M));
+    uint32_t c[MI_CTRL_WORDS];
+    MI_TRY(read_ctrl(c));
+    const uint32_t pos = c[MI_CTRL_POS], cur = c[MI_CTRL_CUR];
+    if (pos + M > d.max_len) return mi_fail(MI_ERR_ARG, "engine_bench_verify: past the KV cache");
+    const std::vector<uint32_t> ids(M, cur);
+    MI_TRY(mi_hip(static_cast<int>(hipMemcpyAsync(ids_dev, ids.data(), M * 4, hipMemcpyHostToDevice, stream)),
+                  "ids upload"));
+    auto one = [&]() -> int {
+      ctrl_set_rows_kernel<<<1, 64, 0, stream>>>(ctrl, pos, M, ids_dev, M);
+      MI_TRY(mi_hip(static_cast<int>(hipGetLastError()), "ctrl_set_rows"));
+      if (eager) return enqueue_step(M);
+      return mi_hip(static_cast<int>(hipGraphLaunch(graphs[M], stream)), "hipGraphLaunch");
+    };
+    for (int w = 0; w < 3; ++w) MI_TRY(one());
+    hipEvent_t a, b;
+    MI_TRY(mi_hip(static_cast<int>(hipEventCreate(&a)), "event"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventCreate(&b)), "event"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventRecord(a, stream)), "event record"));
+    for (uint32_t r = 0; r < reps; ++r) MI_TRY(one());
+    MI_TRY(mi_hip(static_cast<int>(hipEventRecord(b, stream)), "event record"));
+    MI_TRY(mi_hip(static_cast<int>(hipEventSynchronize(b)), "event sync"));
+    float t = 0.f;
+    MI_TRY(mi_hip(static_cast<int>(hipEventElapsedTime(&t, a, b)), "event elapsed"));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *ms = t / float(reps);
+    MI_TRY(check_handoff());
+    return set_rows(pos, 1, &cur, 1);
+  }
+
   int capture(uint32_t M) {
     if (graphs[M]) return 0;
     hipGraph_t g = nullptr;
@@ -1409,6 +1450,11 @@ int mi_engine_prefill(mi_engine* e, const uint32_t* ids, uint32_t n, uint32_t ch
 int mi_engine_bench_linear(mi_engine* e, uint32_t which, uint32_t reps, float* ms_per_launch) {
   if (!e) return mi_fail(MI_ERR_ARG, "engine_bench_linear: null");
   return e->bench_linear(which, reps, ms_per_launch);
+}
+
+int mi_engine_bench_verify(mi_engine* e, uint32_t rows_mode, uint32_t reps, float* ms_per_step) {
+  if (!e) return mi_fail(MI_ERR_ARG, "engine_bench_verify: null");
+  return e->bench_verify(rows_mode, reps, ms_per_step);
 }
 
 int mi_engine_read_ctrl(mi_engine* e, uint32_t* out) {

@@ -37,13 +37,13 @@ def make_kv(kind, KVH, Lm, HD, seed):
     return k, v, ks, vs
 
 
-def gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, pages=None, page=0):
+def gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, pages=None, page=0, n_act=None):
     HD, QH = sh.head_dim, sh.q_heads
     Lm = k.shape[1]
     print(f"attn kind={kind} HD={HD} QH={QH} pos={pos} M={M} tgt={tgt} paged={pages is not None}", flush=True)
-    ctrl = ctrl_dev(pos, M)
+    ctrl = ctrl_dev(pos, M if n_act is None else n_act)
     part = empty((QH, tgt, M, HD + 2), np.float32)
-    out = empty((M, QH * HD), np.uint16)
+    out = dev(np.full((M, QH * HD), 0xFFFF, np.uint16))
     dk, dv, dks, dvs, dq = dev(k), dev(v), dev(ks), dev(vs), dev(q)
     dpg = dev(pages)
     shp = mi.shape_ref(sh)
@@ -161,17 +161,31 @@ def test_decode_ring_paths_paged(kind, QH, KVH, HD, Lm, tgt, pos, P):
     check_close(a[0].reshape(QH, HD), want)
 
 
-def test_rows_are_bitwise_their_single_row_steps():
-    QH, KVH, HD, Lm, tgt = 40, 8, 128, 4096, 128
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("QH,KVH,HD", [(40, 8, 128), (16, 2, 256), (8, 8, 128), (8, 2, 128), (8, 4, 128),
+                                      (12, 2, 128)])
+@pytest.mark.parametrize("Lm,tgt,pos,M,n_act", [
+    (4096, 128, 2045, 4, 4),   # one block size, 4 rows
+    (512, 4, 252, 8, 8),       # the block size changes at row 4 (ppw 64 -> 128)
+    (512, 4, 250, 16, 13),     # 16 rows, 13 live, the change at row 6
+    (1024, 8, 700, 3, 3),      # several groups per wave, rows ending inside the last group
+    (1024, 8, 761, 7, 7),      # rows whose last block is new to the later rows
+])
+def test_rows_are_bitwise_their_single_row_steps(kind, QH, KVH, HD, Lm, tgt, pos, M, n_act):
+    """Several rows per work-group (16 / GQA rows' heads in the product columns): every live
+    row's output and partials bitwise the one-row launch at pos + m; replays bitwise; rows past
+    n_act untouched."""
     sh = O.attn_shape(QH, KVH, HD)
-    k, v, ks, vs = make_kv(0, KVH, Lm, HD, 3)
-    M, pos = 4, 2045  # rows straddle the 2048-key stride change of ppw at tgt 32 ... and 128
-    q = np.random.default_rng(4).standard_normal((M, QH, HD)).astype(np.float32)
-    full, _ = gpu_attention(sh, q, 0, k, v, ks, vs, pos, M, tgt)
-    for m in range(M):
-        one, _ = gpu_attention(sh, np.ascontiguousarray(q[m:m + 1]), 0, k, v, ks, vs, pos + m, 1, tgt)
-        assert np.array_equal(one[0], full[m])
-    again, _ = gpu_attention(sh, q, 0, k, v, ks, vs, pos, M, tgt)
+    k, v, ks, vs = make_kv(kind, KVH, Lm, HD, 3 + kind)
+    q = np.random.default_rng(4 + M).standard_normal((M, QH, HD)).astype(np.float32)
+    full, pf = gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, n_act=n_act)
+    for m in range(n_act):
+        one, p1 = gpu_attention(sh, np.ascontiguousarray(q[m:m + 1]), kind, k, v, ks, vs, pos + m, 1, tgt)
+        assert np.array_equal(one[0], full[m]), m
+        nb = (pos + m) // mi.lib().mi_attn_ppw(pos + m + 1, tgt) + 1
+        assert np.array_equal(p1[:, :nb, 0].view(np.uint32), pf[:, :nb, m].view(np.uint32)), m
+    assert np.all(full[n_act:] == 0xFFFF)
+    again, _ = gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt, n_act=n_act)
     assert np.array_equal(full, again)
 
 

@@ -260,6 +260,28 @@ def test_verify_rows_bitwise_plain_steps_and_accept():
     eng.close()
 
 
+def test_bench_verify_runs_live_rows_and_restores_control():
+    """mi_engine_bench_verify: M live rows per step (their argmaxes are verify's over the same
+    ids, bitwise), pos / cur / n_active as before the call."""
+    eng = mi.Engine(small_desc(), seed=11)
+    eng.capture(1)
+    P, t0, M = 200, 9, 3
+    eng.reset(P, t0)
+    want = eng.verify([t0] * (M - 1))
+    lg = eng.logits(M).copy()
+    eng.reset(P, t0)
+    ms = C.c_float()
+    mi.check(mi.lib().mi_engine_bench_verify(eng._h, M, 4, C.byref(ms)), "engine_bench_verify")
+    assert ms.value > 0
+    c = eng.ctrl()
+    assert c[mi.CTRL_POS] == P and c[mi.CTRL_CUR] == t0 and c[mi.CTRL_NACT] == 1
+    assert np.array_equal(eng.logits(M).view(np.uint32), lg.view(np.uint32))
+    assert list(c[mi.CTRL_OUT:mi.CTRL_OUT + M]) == list(want)
+    with pytest.raises(mi.MiError):
+        mi.check(mi.lib().mi_engine_bench_verify(eng._h, 0, 4, C.byref(ms)), "engine_bench_verify")
+    eng.close()
+
+
 def test_ingest_then_generate():
     eng = mi.Engine(small_desc(), seed=5)
     eng.capture(1)
