@@ -29,9 +29,9 @@ namespace mi {
 namespace {
 
 
-template <int HD, int KV8, int GQA, bool FP>
+template <int HD, int KV8, int GQA, bool FP, int CT>
 __global__ __launch_bounds__(256) void attn_decode_wave_kernel(AttnDecodeArgs a) {
-  attn_block_dma<HD, KV8, GQA, FP>(a, blockIdx.x, blockIdx.y, blockIdx.z);
+  attn_block_dma<HD, KV8, GQA, FP, CT>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // attn_v2.cl:383-428's merge of a row's nb block partials, as one common max M = max mx_b,
@@ -120,15 +120,29 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const uint32_t* __rest
   attn_out[(size_t)m * q_heads * HD + (size_t)h * HD + d] = r;
 }
 
+template <int HD, int KV8, int GQA, bool FP>
+void launch_decode_ct(const AttnDecodeArgs& a, uint32_t ct, dim3 grid, hipStream_t st) {
+  // the tiles an M-row list can use: GQA at most (16 rows), and attn_ct_cap
+  constexpr int CAP = (int)attn_ct_cap(HD, KV8);
+  constexpr int CTMAX = FP ? 1 : (GQA < CAP ? GQA : CAP);
+  if (CTMAX >= 3 && ct == 3)
+    attn_decode_wave_kernel<HD, KV8, GQA, FP, (CTMAX >= 3 ? 3 : 1)><<<grid, 256, 0, st>>>(a);
+  else if (CTMAX >= 2 && ct == 2)
+    attn_decode_wave_kernel<HD, KV8, GQA, FP, (CTMAX >= 2 ? 2 : 1)><<<grid, 256, 0, st>>>(a);
+  else
+    attn_decode_wave_kernel<HD, KV8, GQA, FP, 1><<<grid, 256, 0, st>>>(a);
+}
+
+// ct: the column tiles (attn_col_tiles; the fused prep: 1), grid z already sized for them
 template <int HD, int KV8, bool FP>
-int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, dim3 grid, hipStream_t st) {
+int launch_decode(const AttnDecodeArgs& a, uint32_t gqa, uint32_t ct, dim3 grid, hipStream_t st) {
   switch (gqa) {
-    case 1: attn_decode_wave_kernel<HD, KV8, 1, FP><<<grid, 256, 0, st>>>(a); break;
-    case 2: attn_decode_wave_kernel<HD, KV8, 2, FP><<<grid, 256, 0, st>>>(a); break;
-    case 4: attn_decode_wave_kernel<HD, KV8, 4, FP><<<grid, 256, 0, st>>>(a); break;
-    case 5: attn_decode_wave_kernel<HD, KV8, 5, FP><<<grid, 256, 0, st>>>(a); break;
-    case 6: attn_decode_wave_kernel<HD, KV8, 6, FP><<<grid, 256, 0, st>>>(a); break;
-    case 8: attn_decode_wave_kernel<HD, KV8, 8, FP><<<grid, 256, 0, st>>>(a); break;
+    case 1: launch_decode_ct<HD, KV8, 1, FP>(a, ct, grid, st); break;
+    case 2: launch_decode_ct<HD, KV8, 2, FP>(a, ct, grid, st); break;
+    case 4: launch_decode_ct<HD, KV8, 4, FP>(a, ct, grid, st); break;
+    case 5: launch_decode_ct<HD, KV8, 5, FP>(a, ct, grid, st); break;
+    case 6: launch_decode_ct<HD, KV8, 6, FP>(a, ct, grid, st); break;
+    case 8: launch_decode_ct<HD, KV8, 8, FP>(a, ct, grid, st); break;
     default: return -1;
   }
   return 0;
@@ -173,14 +187,15 @@ int mi_attn_decode(const uint32_t* ctrl, const float* attn_q, uint32_t kv_kind, 
   a.pages = pages; a.attn_part = attn_part; a.row_stride = row_stride; a.head_stride = head_stride;
   a.sc_row_stride = sc_row_stride; a.sc_head_stride = sc_head_stride; a.page = page; a.M = M;
   a.q_heads = shape->q_heads; a.kv_heads = shape->kv_heads; a.tgt = tgt; a.kv_len = kv_len; a.scale = shape->scale;
-  dim3 grid(shape->kv_heads, tgt, attn_row_groups(M, gqa));
+  const uint32_t ct = attn_col_tiles(M, gqa, HD, kv_kind);
+  dim3 grid(shape->kv_heads, tgt, attn_row_groups(M, gqa, ct));
   hipStream_t st = (hipStream_t)stream;
   if (HD == 128) {
-    if (kv_kind == 0) launch_decode<128, 0, false>(a, gqa, grid, st);
-    else launch_decode<128, 1, false>(a, gqa, grid, st);
+    if (kv_kind == 0) launch_decode<128, 0, false>(a, gqa, ct, grid, st);
+    else launch_decode<128, 1, false>(a, gqa, ct, grid, st);
   } else {
-    if (kv_kind == 0) launch_decode<256, 0, false>(a, gqa, grid, st);
-    else launch_decode<256, 1, false>(a, gqa, grid, st);
+    if (kv_kind == 0) launch_decode<256, 0, false>(a, gqa, ct, grid, st);
+    else launch_decode<256, 1, false>(a, gqa, ct, grid, st);
   }
   return mi_hip((int)hipGetLastError(), "attn_decode");
 }
@@ -217,8 +232,8 @@ int mi_attn_prep_decode(uint32_t* ctrl, const float* partials, uint32_t S, uint3
   a.rot_dim = shape->rot_dim; a.gated = shape->gated; a.eps = shape->eps;
   dim3 grid(shape->kv_heads, tgt, M);
   hipStream_t st = (hipStream_t)stream;
-  if (HD == 128) launch_decode<128, 0, true>(a, gqa, grid, st);
-  else launch_decode<256, 0, true>(a, gqa, grid, st);
+  if (HD == 128) launch_decode<128, 0, true>(a, gqa, 1, grid, st);
+  else launch_decode<256, 0, true>(a, gqa, 1, grid, st);
   return mi_hip((int)hipGetLastError(), "attn_prep_decode");
 }
 

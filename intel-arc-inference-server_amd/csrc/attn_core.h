@@ -12,15 +12,25 @@ __device__ __forceinline__ uint32_t v2_ppw(uint32_t len, uint32_t tgt) {
   return p < 64u ? 64u : p;
 }
 
-// list rows one decode work-group takes: the 16 columns of the matrix products hold
-// 16 / GQA rows' q heads (the fused prep: one row)
-__host__ __device__ constexpr uint32_t attn_rows_per_wg(uint32_t gqa, bool fused_prep) {
-  return fused_prep || gqa == 0 || gqa > 16 ? 1u : 16u / gqa;
+// list rows one decode work-group takes: the ct tiles of 16 columns of the matrix products
+// hold 16 ct / GQA rows' q heads (the fused prep: one row)
+__host__ __device__ constexpr uint32_t attn_rows_per_wg(uint32_t gqa, bool fused_prep, uint32_t ct) {
+  return fused_prep || gqa == 0 || gqa > 16u * ct ? 1u : 16u * ct / gqa;
+}
+// column tiles for an M-row list: enough for every row's heads, at most 3 (f16 rows of 128) or
+// 2 (int8 rows of 128, rows of 256: a third tile's accumulators would not leave two waves per
+// SIMD, or any, the registers)
+__host__ __device__ constexpr uint32_t attn_ct_cap(uint32_t hd, uint32_t kv8) {
+  return hd == 128u && kv8 == 0u ? 3u : 2u;
+}
+__host__ inline uint32_t attn_col_tiles(uint32_t M, uint32_t gqa, uint32_t hd, uint32_t kv8) {
+  const uint32_t need = (M * gqa + 15u) / 16u, cap = attn_ct_cap(hd, kv8);
+  return need < 1u ? 1u : (need > cap ? cap : need);
 }
 // work-groups over the rows of an M-row list: RPW at a time, plus one for the split where the
 // block size changes
-__host__ inline uint32_t attn_row_groups(uint32_t M, uint32_t gqa) {
-  const uint32_t rpw = attn_rows_per_wg(gqa, false);
+__host__ inline uint32_t attn_row_groups(uint32_t M, uint32_t gqa, uint32_t ct) {
+  const uint32_t rpw = attn_rows_per_wg(gqa, false, ct);
   return (M + rpw - 1) / rpw + (M > 1 && rpw > 1 ? 1u : 0u);
 }
 

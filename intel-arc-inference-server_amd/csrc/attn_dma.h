@@ -6,10 +6,10 @@
 // are dealt to the four waves round-robin; each wave keeps its own online softmax and the
 // waves merge once at the end into each (row, head)'s partial {max, sum, acc[HD]}.
 //
-// Rows. The matrix products have 16 columns, one per (row, q head): a plain launch gives a
-// work-group RPW = 16 / GQA consecutive rows of the list that share the block size (column
-// c = GQA rr + g is row r_lo + rr, head j GQA + g), so the block's K/V rows are read once for
-// all of them. Row r sees positions < pos + r + 1: its scores past that are -inf and a group
+// Rows. The matrix products' columns are (row, q head) pairs, 16 per tile: a plain launch gives
+// a work-group RPW = 16 CT / GQA consecutive rows of the list that share the block size (column
+// c = 16 ct + qi = GQA rr + g is row r_lo + rr, head j GQA + g), so the block's K/V rows are
+// read once for all of them; the CT tiles share every LDS read of K and V^T. Row r sees positions < pos + r + 1: its scores past that are -inf and a group
 // that holds none of its positions leaves its state untouched (alpha 1, weights 0), so each
 // column's values are, operation for operation, those of a one-row work-group for its row.
 //
@@ -95,19 +95,29 @@ __device__ __forceinline__ void wait_group(uint32_t after) {  // after: groups i
   else wait_vm<(NB > 3 ? 3 * DG : 0)>();
 }
 
-template <int HD, int KV8, int GQA, bool FP>
+template <int HD, int KV8, int GQA, bool FP, int CT>
 __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t j, uint32_t blk, uint32_t zg) {
   static_assert(!FP || KV8 == 0, "the fused prep writes the f16 cache");
   using C = AttnDmaCfg<HD, KV8>;
   constexpr uint32_t KK = HD / 32, NT = HD / 16;
-  constexpr uint32_t ROWB = C::ROWB, CPR = C::CPR, GB = C::GB, NB = C::NB, SLOT = C::SLOT;
-  constexpr uint32_t RPW = attn_rows_per_wg(GQA, FP), NC = RPW * GQA;  // rows, live columns
-  constexpr uint32_t RED = 4u * NC * HD * 4u;  // the end merge's accumulators
-  static_assert(C::RING >= RED, "merge area");
-  __shared__ __align__(16) unsigned char s_ring[C::RING];
+  constexpr uint32_t ROWB = C::ROWB, CPR = C::CPR, GB = C::GB, SLOT = C::SLOT;
+  static_assert(!FP || CT == 1, "the fused prep takes one row");
+  constexpr uint32_t RPW = attn_rows_per_wg(GQA, FP, CT), NC = RPW * GQA;  // rows, live columns
+  constexpr uint32_t RED = 4u * 16u * HD * 4u;  // the end merge's accumulators (one tile at a time)
+  // groups per softmax step: two for int8 rows of 128 (two independent chains of products), else
+  // one (f16 rows of 128 measured faster with one, the ring prefetching the next group); the same
+  // for every CT, since the step's rounding depends on it
+  constexpr uint32_t NG = HD == 128 && KV8 ? 2u : 1u;
+  // slots per wave: several tiles take the fewest (a multiple of NG) that hold the merge, which
+  // leaves LDS for the tiles' q
+  constexpr uint32_t NBMIN = (RED + 4u * SLOT - 1u) / (4u * SLOT);
+  constexpr uint32_t NB = CT == 1 ? C::NB : (NBMIN + NG - 1u) / NG * NG;
+  constexpr uint32_t RING = 4u * NB * SLOT;
+  static_assert(RING >= RED, "merge area");
+  __shared__ __align__(16) unsigned char s_ring[RING];
   __shared__ float st_m[4][16], st_l[4][16], st_f[4][16], st_hm[16], st_hs[16];
   __shared__ uint32_t s_grow[kMaxBlockGroups];
-  __shared__ h8_t s_q[2][KK][64];
+  __shared__ h8_t s_q[CT][2][KK][64];
   // FP: the new K/V rows (f16), the roped q of the GQA heads and the waves' normed rows. At
   // rows of 256 the last two live in the ring (LDS is short), which the fused form then starts
   // to load only after its prologue; at rows of 128 they have arrays of their own and the ring's
@@ -117,7 +127,7 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   constexpr bool kEarly = !FP || HD == 128;
   constexpr uint32_t FPQ = FP && kEarly ? GQA * HD + 4u * HD : 1u;
   __shared__ float s_fpq[FPQ];
-  static_assert(kEarly || C::RING >= (GQA * HD + 4u * HD) * 4u, "prologue area");
+  static_assert(kEarly || RING >= (GQA * HD + 4u * HD) * 4u, "prologue area");
   float* const s_q32 = kEarly ? s_fpq : reinterpret_cast<float*>(s_ring);
   float* const s_nrm = s_q32 + GQA * HD;
 
@@ -158,9 +168,15 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   if (nb > a.tgt) nb = a.tgt;
   if (blk >= nb) return;
   const uint32_t p_begin = blk * s, p_end = min(p_begin + s, L);
-  // this lane's column: its row's end in the block (p_begin: no column, or the row ends before)
-  const uint32_t crow = r_lo + qi / GQA;
-  const uint32_t pe_col = qi < NC && crow < r_hi ? max(min(p_begin + s, row_len(crow)), p_begin) : p_begin;
+  // this lane's column 16 ct + qi of each tile: its row, and the row's end in the block
+  // (p_begin: no column, or the row ends before the block)
+  uint32_t crow[CT], pe_col[CT];
+#pragma unroll
+  for (uint32_t ct = 0; ct < CT; ++ct) {
+    const uint32_t c = 16u * ct + qi;
+    crow[ct] = r_lo + c / GQA;
+    pe_col[ct] = c < NC && crow[ct] < r_hi ? max(min(p_begin + s, row_len(crow[ct])), p_begin) : p_begin;
+  }
   const uint32_t ng = (p_end - p_begin + 15u) / 16u;
   const uint32_t ngw = wave < ng ? (ng - wave + 3u) / 4u : 0u;  // this wave's groups
 
@@ -224,16 +240,18 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   };
   if constexpr (kEarly) issue_first();
   // q of the GQA heads (plain form: wave 0 loads it)
-  f4_t qv[FP ? 1u : 2u * KK];
+  f4_t qv[CT][FP ? 1u : 2u * KK];
   if constexpr (!FP) {
-    if (wave == 0 && qi < NC && crow < r_hi) {
-      const float* qp = a.attn_q + ((size_t)crow * a.q_heads + j * GQA + qi % GQA) * HD + 8 * qq;
 #pragma unroll
-      for (uint32_t kk = 0; kk < KK; ++kk) {
-        qv[2 * kk] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk));
-        qv[2 * kk + 1] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk + 4));
+    for (uint32_t ct = 0; ct < CT; ++ct)
+      if (wave == 0 && pe_col[ct] > p_begin) {
+        const float* qp = a.attn_q + ((size_t)crow[ct] * a.q_heads + j * GQA + (16u * ct + qi) % GQA) * HD + 8 * qq;
+#pragma unroll
+        for (uint32_t kk = 0; kk < KK; ++kk) {
+          qv[ct][2 * kk] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk));
+          qv[ct][2 * kk + 1] = *as_global(reinterpret_cast<const f4_t*>(qp + 32 * kk + 4));
+        }
       }
-    }
   }
   // the later groups' first cache rows (a page holds whole groups), staged in LDS
   if (a.pages) {
@@ -372,14 +390,16 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   // q as the MFMA B operand (f16 high and low parts), staged by wave 0
   if (wave == 0) {
 #pragma unroll
+    for (uint32_t ct = 0; ct < CT; ++ct)
+#pragma unroll
     for (uint32_t kk = 0; kk < KK; ++kk) {
       float v[8];
-      if (qi < NC && crow < r_hi) {
+      if (pe_col[ct] > p_begin) {
         if constexpr (FP) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = s_q32[qi * HD + 32 * kk + 8 * qq + e];
         } else {
-          const f4_t q0 = qv[2 * kk], q1 = qv[2 * kk + 1];
+          const f4_t q0 = qv[ct][2 * kk], q1 = qv[ct][2 * kk + 1];
           v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
           v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
         }
@@ -394,8 +414,8 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
         hi[e] = h;
         lo[e] = (half_t)(v[e] - (float)h);
       }
-      s_q[0][kk][lane] = hi;
-      s_q[1][kk][lane] = lo;
+      s_q[ct][0][kk][lane] = hi;
+      s_q[ct][1][kk][lane] = lo;
     }
   }
   wait_vm<0>();   // (the compiler's waits above have seen to this already)
@@ -406,10 +426,15 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
   // v_exp_f32 (exp2); the partial's max goes out in natural units
   constexpr float kLog2e = 1.4426950408889634f;
   const float qscale = a.scale * kLog2e;
-  float m_run = -INFINITY, l_run = 0.f;
-  f4_t acc[NT];
+  float m_run[CT], l_run[CT];
+  f4_t acc[CT][NT];
 #pragma unroll
-  for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t ct = 0; ct < CT; ++ct) {
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.f;
+#pragma unroll
+    for (uint32_t tt = 0; tt < NT; ++tt) acc[ct][tt] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
   // the scales' halves: an element's word half is bit 1 of its address
   const uint32_t kpar0 = (uint32_t)(((uintptr_t)a.k_scale >> 1) + (size_t)j * a.sc_head_stride);
   const uint32_t vpar0 = (uint32_t)(((uintptr_t)a.v_scale >> 1) + (size_t)j * a.sc_head_stride);
@@ -424,8 +449,6 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(b0), "+v"(b1));
     return fmaxf(b0, b1);
   };
-  // groups per iteration: two for rows of 128 (two independent chains of products), one for 256
-  constexpr uint32_t NG = HD == 128 ? 2u : 1u;
   static_assert(NB % NG == 0, "ring");
   typedef int v2i_t __attribute__((ext_vector_type(2)));
   typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -515,89 +538,101 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
         vw[u][0] = v4.x; vw[u][1] = v4.y; vw[u][2] = v4.z; vw[u][3] = v4.w;
       }
     }
-    // scores S^T[position 4 qq + r][head qi]: the f16 high and low parts of q on two chains
-    f4_t dh[NG], dl[NG];
-#pragma unroll
-    for (uint32_t u = 0; u < NG; ++u) dh[u] = dl[u] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (uint32_t kk = 0; kk < KK; ++kk)
-#pragma unroll
-      for (uint32_t u = 0; u < NG; ++u) {
-        const h8_t k8 = KV8 ? chunk_h8<1>(kc[u][kk]) : kh[u][kk];
-        dh[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k8, s_q[0][kk][lane], dh[u], 0, 0, 0);
-        dl[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k8, s_q[1][kk][lane], dl[u], 0, 0, 0);
-      }
-    float sc[NG][4], vsv[NG][4];
-    float mx = -INFINITY;
+    // the int8 rows' score and V scales (shared by the tiles)
+    float rsc[NG][4], vsv[NG][4];
 #pragma unroll
     for (uint32_t u = 0; u < NG; ++u) {
       uint32_t rb = 0;
       if constexpr (KV8 == 1) rb = group_row(wave + 4u * (u && has1 ? tw + 1 : tw));
 #pragma unroll
       for (uint32_t r = 0; r < 4; ++r) {
-        float rs = qscale;
+        rsc[u][r] = qscale;
         vsv[u][r] = 1.0f;
         if constexpr (KV8 == 1) {
           const uint32_t rr = glen[u] ? min(4u * qq + r, glen[u] - 1u) : 0u;
           const uint32_t er = (uint32_t)((size_t)(rb + rr) * a.sc_row_stride);
-          rs = qscale * h2f((uint16_t)(((er + kpar0) & 1u) ? kw[u][r] >> 16 : kw[u][r] & 0xFFFFu));
+          rsc[u][r] = qscale * h2f((uint16_t)(((er + kpar0) & 1u) ? kw[u][r] >> 16 : kw[u][r] & 0xFFFFu));
           vsv[u][r] = h2f((uint16_t)(((er + vpar0) & 1u) ? vw[u][r] >> 16 : vw[u][r] & 0xFFFFu));
         }
-        sc[u][r] = 4u * qq + r < glen[u] && p0g[u] + 4u * qq + r < pe_col ? (dh[u][r] + dl[u][r]) * rs : -INFINITY;
-        mx = fmaxf(mx, sc[u][r]);
       }
     }
-    mx = head_max(mx);
-    // a column none of whose positions are in these groups keeps its state
-    const bool colive = p0g[0] < pe_col;
-    const float m_new = colive ? fmaxf(m_run, mx) : m_run;
-    const float alpha = colive ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 on the first group
-    float w[NG][4];
-    float wsum = 0.f;
 #pragma unroll
-    for (uint32_t u = 0; u < NG; ++u) {
+    for (uint32_t ct = 0; ct < CT; ++ct) {
+      // scores S^T[position 4 qq + r][column 16 ct + qi]: the f16 high and low parts of q on
+      // two chains
+      f4_t dh[NG], dl[NG];
 #pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) w[u][r] = colive ? __builtin_amdgcn_exp2f(sc[u][r] - m_new) : 0.f;
-      wsum += (w[u][0] + w[u][1]) + (w[u][2] + w[u][3]);
-    }
-    l_run = __builtin_fmaf(l_run, alpha, wsum);
-    m_run = m_new;
-    if (__ballot(alpha != 1.0f)) {
+      for (uint32_t u = 0; u < NG; ++u) dh[u] = dl[u] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (uint32_t tt = 0; tt < NT; ++tt) acc[tt] *= alpha;
-    }
-    // B operands: the weights (int8: times the row's V scale), f16 high and low parts
-    h4_t bh[NG], bl[NG];
+      for (uint32_t kk = 0; kk < KK; ++kk)
 #pragma unroll
-    for (uint32_t u = 0; u < NG; ++u)
+        for (uint32_t u = 0; u < NG; ++u) {
+          const h8_t k8 = KV8 ? chunk_h8<1>(kc[u][kk]) : kh[u][kk];
+          dh[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k8, s_q[ct][0][kk][lane], dh[u], 0, 0, 0);
+          dl[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k8, s_q[ct][1][kk][lane], dl[u], 0, 0, 0);
+        }
+      float sc[NG][4];
+      float mx = -INFINITY;
 #pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) {
-        const float wv = w[u][r] * vsv[u][r];
-        const half_t h = (half_t)wv;
-        bh[u][r] = h;
-        bl[u][r] = (half_t)(wv - (float)h);
-      }
-    // P V per 16-dim tile
+      for (uint32_t u = 0; u < NG; ++u)
 #pragma unroll
-    for (uint32_t i = 0; i < NTR; ++i) {
+        for (uint32_t r = 0; r < 4; ++r) {
+          sc[u][r] = 4u * qq + r < glen[u] && p0g[u] + 4u * qq + r < pe_col[ct] ? (dh[u][r] + dl[u][r]) * rsc[u][r]
+                                                                                : -INFINITY;
+          mx = fmaxf(mx, sc[u][r]);
+        }
+      mx = head_max(mx);
+      // a column none of whose positions are in these groups keeps its state
+      const bool colive = p0g[0] < pe_col[ct];
+      const float m_new = colive ? fmaxf(m_run[ct], mx) : m_run[ct];
+      const float alpha = colive ? __builtin_amdgcn_exp2f(m_run[ct] - m_new) : 1.0f;  // 0 on the first group
+      float w[NG][4];
+      float wsum = 0.f;
 #pragma unroll
       for (uint32_t u = 0; u < NG; ++u) {
-        if constexpr (KV8 == 0) {
-          acc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u][i], bh[u], acc[i], 0, 0, 0);
-          acc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u][i], bl[u], acc[i], 0, 0, 0);
-        } else {
-          const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
-          const uint32_t x0 = (uint32_t)raw[u][i].x ^ 0x80808080u, x1 = (uint32_t)raw[u][i].y ^ 0x80808080u;
-          const uint32_t hi = 0x64646464u;
-          const h2_t p0 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04010400u)) - bias;
-          const h2_t p1 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04030402u)) - bias;
-          const h2_t p2 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04010400u)) - bias;
-          const h2_t p3 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04030402u)) - bias;
-          const h4_t a0 = h4_t{p0[0], p0[1], p1[0], p1[1]}, a1 = h4_t{p2[0], p2[1], p3[0], p3[1]};
-          acc[2 * i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, bh[u], acc[2 * i], 0, 0, 0);
-          acc[2 * i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, bl[u], acc[2 * i], 0, 0, 0);
-          acc[2 * i + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, bh[u], acc[2 * i + 1], 0, 0, 0);
-          acc[2 * i + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, bl[u], acc[2 * i + 1], 0, 0, 0);
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) w[u][r] = colive ? __builtin_amdgcn_exp2f(sc[u][r] - m_new) : 0.f;
+        wsum += (w[u][0] + w[u][1]) + (w[u][2] + w[u][3]);
+      }
+      l_run[ct] = __builtin_fmaf(l_run[ct], alpha, wsum);
+      m_run[ct] = m_new;
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (uint32_t tt = 0; tt < NT; ++tt) acc[ct][tt] *= alpha;
+      }
+      // B operands: the weights (int8: times the row's V scale), f16 high and low parts
+      h4_t bh[NG], bl[NG];
+#pragma unroll
+      for (uint32_t u = 0; u < NG; ++u)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) {
+          const float wv = w[u][r] * vsv[u][r];
+          const half_t h = (half_t)wv;
+          bh[u][r] = h;
+          bl[u][r] = (half_t)(wv - (float)h);
+        }
+      // P V per 16-dim tile
+#pragma unroll
+      for (uint32_t i = 0; i < NTR; ++i) {
+#pragma unroll
+        for (uint32_t u = 0; u < NG; ++u) {
+          if constexpr (KV8 == 0) {
+            acc[ct][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u][i], bh[u], acc[ct][i], 0, 0, 0);
+            acc[ct][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[u][i], bl[u], acc[ct][i], 0, 0, 0);
+          } else {
+            const h2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+            const uint32_t x0 = (uint32_t)raw[u][i].x ^ 0x80808080u, x1 = (uint32_t)raw[u][i].y ^ 0x80808080u;
+            const uint32_t hi = 0x64646464u;
+            const h2_t p0 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04010400u)) - bias;
+            const h2_t p1 = as_h2(__builtin_amdgcn_perm(hi, x0, 0x04030402u)) - bias;
+            const h2_t p2 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04010400u)) - bias;
+            const h2_t p3 = as_h2(__builtin_amdgcn_perm(hi, x1, 0x04030402u)) - bias;
+            const h4_t a0 = h4_t{p0[0], p0[1], p1[0], p1[1]}, a1 = h4_t{p2[0], p2[1], p3[0], p3[1]};
+            acc[ct][2 * i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, bh[u], acc[ct][2 * i], 0, 0, 0);
+            acc[ct][2 * i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, bl[u], acc[ct][2 * i], 0, 0, 0);
+            acc[ct][2 * i + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, bh[u], acc[ct][2 * i + 1], 0, 0, 0);
+            acc[ct][2 * i + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, bl[u], acc[ct][2 * i + 1], 0, 0, 0);
+          }
         }
       }
     }
@@ -607,52 +642,58 @@ __device__ __forceinline__ void attn_block_dma(const AttnDecodeArgs& a, uint32_t
       if (tw + u + NB < ngw) issue(tw + u + NB, group_row(wave + 4u * (tw + u + NB)));
   }
   wait_vm<0>();
-  // the state in natural units for the partial: max * ln 2
-  m_run *= 0.6931471805599453f;
-  // merge the four waves: M = max m_w, f_w = exp(m_w - M), sum and acc weighted by f_w in
-  // wave order
-  float l = l_run + __shfl_xor(l_run, 16, 64);
-  l = l + __shfl_xor(l, 32, 64);
-  if (qq == 0) {
-    st_m[wave][qi] = m_run;
-    st_l[wave][qi] = l;
-  }
   lds_barrier();  // every wave is done with its ring, which the merge reuses
-  float* red = reinterpret_cast<float*>(s_ring);  // [4][NC][HD]
-  const uint32_t nlc = (r_hi - r_lo) * GQA;  // the live columns
-  if (qi < nlc) {
+  // merge the four waves per tile of columns: M = max m_w, f_w = exp(m_w - M), sum and acc
+  // weighted by f_w in wave order (the state's max in natural units: max * ln 2)
+  float* red = reinterpret_cast<float*>(s_ring);  // [4][16][HD]
+  const uint32_t ncols = (r_hi - r_lo) * GQA;      // the live columns
 #pragma unroll
-    for (uint32_t tt = 0; tt < NT; ++tt)
-#pragma unroll
-      for (uint32_t r = 0; r < 4; ++r) red[(wave * NC + qi) * HD + 16u * tt + 4u * qq + r] = acc[tt][r];
-  }
-  if (t < nlc) {
-    float M = st_m[0][t];
-#pragma unroll
-    for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][t]);
-    float sm = 0.f;
-#pragma unroll
-    for (uint32_t w2 = 0; w2 < 4; ++w2) {
-      const float f = expf(st_m[w2][t] - M);
-      sm = __builtin_fmaf(st_l[w2][t], f, sm);
-      st_f[w2][t] = f;
+  for (uint32_t ct = 0; ct < CT; ++ct) {
+    const uint32_t nlc = ncols > 16u * ct ? min(ncols - 16u * ct, 16u) : 0u;  // this tile's
+    if (nlc == 0) break;  // uniform
+    if (ct) lds_barrier();  // the previous tile's merge is done with red and the st arrays
+    const float mr = m_run[ct] * 0.6931471805599453f;
+    float l = l_run[ct] + __shfl_xor(l_run[ct], 16, 64);
+    l = l + __shfl_xor(l, 32, 64);
+    if (qq == 0) {
+      st_m[wave][qi] = mr;
+      st_l[wave][qi] = l;
     }
-    st_hm[t] = M;
-    st_hs[t] = sm;
-  }
-  lds_barrier();
-  for (uint32_t idx = t; idx < nlc * HD; idx += 256u) {
-    const uint32_t g = idx / HD, dd = idx % HD, row = r_lo + g / GQA;
-    // a row whose keys end before this block has no partial here
-    if (blk * s >= row_len(row)) continue;
-    float v = 0.f;
+    if (qi < nlc) {
 #pragma unroll
-    for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * NC + g) * HD + dd], st_f[w2][g], v);
-    float* out = a.attn_part + (((size_t)(j * GQA + g % GQA) * a.tgt + blk) * a.M + row) * (HD + 2);
-    *as_global(out + 2 + dd) = v;
-    if (dd == 0) {
-      out[0] = st_hm[g];
-      out[1] = st_hs[g];
+      for (uint32_t tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) red[(wave * 16u + qi) * HD + 16u * tt + 4u * qq + r] = acc[ct][tt][r];
+    }
+    lds_barrier();
+    if (t < nlc) {
+      float M = st_m[0][t];
+#pragma unroll
+      for (uint32_t w2 = 1; w2 < 4; ++w2) M = fmaxf(M, st_m[w2][t]);
+      float sm = 0.f;
+#pragma unroll
+      for (uint32_t w2 = 0; w2 < 4; ++w2) {
+        const float f = expf(st_m[w2][t] - M);
+        sm = __builtin_fmaf(st_l[w2][t], f, sm);
+        st_f[w2][t] = f;
+      }
+      st_hm[t] = M;
+      st_hs[t] = sm;
+    }
+    lds_barrier();
+    for (uint32_t idx = t; idx < nlc * HD; idx += 256u) {
+      const uint32_t g = idx / HD, dd = idx % HD, c = 16u * ct + g, row = r_lo + c / GQA;
+      // a row whose keys end before this block has no partial here
+      if (blk * s >= row_len(row)) continue;
+      float v = 0.f;
+#pragma unroll
+      for (uint32_t w2 = 0; w2 < 4; ++w2) v = __builtin_fmaf(red[(w2 * 16u + g) * HD + dd], st_f[w2][g], v);
+      float* out = a.attn_part + (((size_t)(j * GQA + c % GQA) * a.tgt + blk) * a.M + row) * (HD + 2);
+      *as_global(out + 2 + dd) = v;
+      if (dd == 0) {
+        out[0] = st_hm[g];
+        out[1] = st_hs[g];
+      }
     }
   }
 }
