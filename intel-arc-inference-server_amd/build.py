@@ -23,8 +23,11 @@ HIP_ONLY = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-
 
 # Per-file code generation options. attn.hip: the attention accumulators live in ordinary
 # VGPRs (they are rescaled by the vector ALUs between matrix-core products, which AGPRs would
-# turn into copies back and forth).
+# turn into copies back and forth). gemv_w4a16.hip: each product's result is scaled into the
+# fp32 accumulators by the vector ALUs at once, so it too is kept out of AGPRs (no copies out of
+# them: 27B step 4.23 -> 4.13 ms, verify steps at 2..8 rows 0.5-2 % faster).
 PER_FILE = {"attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+            "gemv_w4a16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 
