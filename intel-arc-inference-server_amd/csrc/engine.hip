@@ -504,13 +504,12 @@ struct mi_engine {
   // consumers' all-to-all exchange of tile sums. The last layer's down (the head's input, which
   // the MTP head copies too) and MoE layers (the router and the experts read x) keep x.
   // (The launches that form the norm take at most 8 k-groups per slice and 256 tile sums: a
-  // model whose split-K widths leave more keeps x throughout.) Single-row steps only: at 2..8
-  // rows every work-group of gate||up forming its rows' norm costs more than the exchange it
-  // spares (measured at the 27B shape, rows 2 / 4 / 8: 5.30 / 6.13 / 8.83 ms split against
-  // 5.01 / 5.51 / 6.65 ms with x written by the consumers; one row: 4.22 ms either way or
-  // better split).
+  // model whose split-K widths leave more keeps x throughout.) Up to 4 rows: at 5..8 rows
+  // (the 16-row kernel) every work-group of gate||up forming its rows' norm costs more than the
+  // exchange it spares (27B shape, per layer at 8 rows: gate||up 47.2 against 27.7 us, o and
+  // down 26.1 against 32.6; at 4 rows 28.1 against 24.7 and 23.8 against 28.9).
   bool split_norm(uint32_t M) const {
-    if (M > 1) return false;
+    if (M > 4) return false;
     if (d.experts || d.hidden / 64 > 256 || (d.hidden / 64) % 4) return false;
     auto ok = [](const Linear& l) { return (l.K / 64) / l.S <= 8; };
     for (uint32_t li = 0; li < d.layers; ++li)

@@ -429,16 +429,17 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
       // after the sums (empty until then)
       const uint32_t* rcache = reinterpret_cast<const uint32_t*>(epi.in_sums) + M * nt;
       const uint32_t rc = ld_agent(rcache + (MR == 1 ? 0u : min(t, M - 1u)));
+      // (every load unconditional, at a clamped index: a load under a branch leaves its value
+      // in a register that the join copies, and the copy waits for the load at once)
 #pragma unroll
       for (int u = 0; u < MR; ++u) {
         const uint32_t e = t + 256u * u;
-        if (e < M * nt) sm[u] = epi.in_sums[e];
-        if (e < nwords) {
-          const uint32_t row = e / kw, k = k0 + 2u * (e - row * kw);
-          rw[u] = *reinterpret_cast<const uint32_t*>(x + (size_t)row * K + k);
-          w0[u] = epi.in_norm_w[k];
-          w1[u] = epi.in_norm_w[k + 1u];
-        }
+        sm[u] = epi.in_sums[min(e, M * nt - 1u)];
+        const uint32_t ec = min(e, nwords - 1u), row = ec / kw, k = k0 + 2u * (ec - row * kw);
+        rw[u] = *reinterpret_cast<const uint32_t*>(x + (size_t)row * K + k);
+        const f2_t w = *reinterpret_cast<const f2_t*>(epi.in_norm_w + k);
+        w0[u] = w.x;
+        w1[u] = w.y;
       }
       // then the first batch's weights: the waits for the loads above (retired in order) do
       // not wait for them
@@ -451,12 +452,12 @@ __global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restr
         for (int h = 0; h < 2; ++h) wv[u][h] = load_stream16(qweight + (size_t)(g * 8u + 4u * h + q) * N + ncol);
         sv[u] = *reinterpret_cast<const u2_t*>(scales + (size_t)g * N + ncol);
       }
+      // (unconditional too: the words past the M * nt sums are never read)
 #pragma unroll
-      for (int u = 0; u < MR; ++u)
-        if (t + 256u * u < M * nt) {
-          if constexpr (MR == 1) s_nsum[t] = sm[u];
-          else s_xin[t + 256u * u] = __builtin_bit_cast(uint32_t, sm[u]);
-        }
+      for (int u = 0; u < MR; ++u) {
+        if constexpr (MR == 1) s_nsum[t] = sm[u];
+        else s_xin[t + 256u * u] = __builtin_bit_cast(uint32_t, sm[u]);
+      }
       __syncthreads();
       // the rows' rstd: at one row every thread adds the sums itself (one broadcast LDS read
       // per word for a whole wave), so no barrier waits for one thread's chain of adds, and
