@@ -169,11 +169,17 @@ __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base,
   constexpr int kSc1 = 16;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7FFFFFFF, 0x00020000);
   const uint32_t t = threadIdx.x;
+  // Every load is issued unconditionally: an element past cnt (or, re-polling, one already
+  // read) takes an offset past the resource's range, which the buffer unit answers with 0 and
+  // no memory access. (A load under a branch leaves its value in a register that the branch's
+  // join copies, and the copy waits for that load at once: one round trip per word.)
+  constexpr uint32_t kOob = 0x80000000u;
   uint32_t v[PER];
   uint32_t pending = 0;  // bit u: element t + 256 u still empty
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (t + 256u * u < cnt) v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, u * ustride, kSc1);
+    v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, t + 256u * u < cnt ? voff + u * ustride : kOob, 0, kSc1);
+  __builtin_amdgcn_sched_barrier(0);  // (all of them before the first use)
 #pragma unroll
   for (int u = 0; u < PER; ++u)
     if (t + 256u * u < cnt && v[u] == kEmpty) pending |= 1u << u;
@@ -181,8 +187,12 @@ __device__ __forceinline__ void poll_into(float* dst, uint32_t cnt, float* base,
   for (uint32_t n = 0; pending && n < limit; ++n) {
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int u = 0; u < PER; ++u)
-      if (pending & (1u << u)) v[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, u * ustride, kSc1);
+    for (int u = 0; u < PER; ++u) {
+      const bool p = pending & (1u << u);
+      const uint32_t nv = __builtin_amdgcn_raw_buffer_load_b32(rs, p ? voff + u * ustride : kOob, 0, kSc1);
+      v[u] = p ? nv : v[u];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < PER; ++u)
       if ((pending & (1u << u)) && v[u] != kEmpty) pending &= ~(1u << u);
