@@ -274,13 +274,15 @@ __device__ __forceinline__ void put_f16(float* dst, const u4_t (&v)[PER], uint32
     }
   }
 }
+// (every load unconditional, pieces past n re-reading the last: a load under a branch leaves
+// its value in a register that the branch's join copies, and the copy waits for it at once)
 template <int PER>
 __device__ __forceinline__ void get_f16(u4_t (&v)[PER], const uint16_t* src, uint32_t n) {
   const uint32_t n8 = n / 8u;
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const uint32_t i = threadIdx.x + 256u * u;
-    if (i < n8) v[u] = *reinterpret_cast<const u4_t*>(src + 8u * i);
+    const uint32_t i = min(threadIdx.x + 256u * u, n8 - 1u);
+    v[u] = *reinterpret_cast<const u4_t*>(src + 8u * i);
   }
 }
 
@@ -514,7 +516,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint32_t* __restric
   for (uint32_t k = 0; k < 8; ++k) wk[k] = k < top_k ? __builtin_bit_cast(float, row[R_W + k]) : 0.f;
   const float sg = __builtin_bit_cast(float, row[R_SG]);
   uint16_t* rp = resid + (size_t)m * hidden + nb * 16 + ch * 8 + (t & 7u);
-  const uint16_t r_old = t < 8u ? *rp : (uint16_t)0;
+  const uint16_t r_old = *rp;  // (every lane: lanes 8.. read lane t % 8's element, unused)
   constexpr int HP = kMaxSlotsInter / 8 / 256 + 1;  // h pieces per thread (<= 1152 pieces)
   u4_t hv[HP];
   get_f16<HP>(hv, h + (size_t)m * slots * inter, slots * inter);
