@@ -821,20 +821,27 @@ int check_gemv(const uint32_t* qweight, const uint16_t* scales, const uint16_t* 
 
 using namespace mi;
 
-extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
-  // The split-K width for a plain launch (measured on MI355X over the 27B shapes at M = 1):
-  // the smallest S | K/64 that gives at most 8 k-groups per split and at least 2048
-  // work-groups, never going below 4 k-groups per split.
+namespace {
+// the smallest S | K/64 that gives at most 8 k-groups per split and at least 2048 work-groups,
+// never going below min_gps k-groups per split
+uint32_t pick_split(uint32_t K, uint32_t N, uint32_t min_gps) {
   const uint32_t G = K / 64, tiles = N / kCols;
   uint32_t best = 1;
   for (uint32_t S = 1; S <= G; ++S) {
     if (G % S) continue;
     const uint32_t gps = G / S;
-    if (gps < 4 && S > 1) break;
+    if (gps < min_gps && S > 1) break;
     best = S;
     if (gps <= 8 && tiles * S >= 2048) break;
   }
   return best;
+}
+}  // namespace
+
+extern "C" uint32_t mi_gemv_pick_s(uint32_t K, uint32_t N) {
+  // The split-K width for a plain launch (measured on MI355X over the 27B shapes at M = 1):
+  // at least 4 k-groups per split.
+  return pick_split(K, N, 4u);
 }
 
 extern "C" uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue) {
@@ -843,6 +850,9 @@ extern "C" uint32_t mi_gemv_pick_s_ex(uint32_t K, uint32_t N, uint32_t epilogue)
   // over the 27B shapes: o 20, gate_up 10 and down 34 beat the largest S <= 8). QKV's head
   // consumers fold a whole head over every slice: there the smallest S | K/64 with at most 8
   // k-groups per slice (27B qkv: 10, measured ahead of 5, 8, 16 and 20).
+  // RESID: at least 5 k-groups per split (27B o: 16 rather than 20, step 4.07 -> 4.03 ms;
+  // down keeps 34).
+  if (epilogue == MI_EPI_RESID) return pick_split(K, N, 5u);
   if (epilogue == MI_EPI_QKV) {
     const uint32_t G = K / 64;
     for (uint32_t S = 1; S <= G; ++S)

@@ -33,14 +33,16 @@ def test_argument_errors_are_reported_without_a_gpu():
 
 def test_split_k_choices_for_the_27b_shapes():
     """Measured best S on MI355X at M = 1 (qkv, o, gate_up, down, lm_head), plain and fused
-    alike; S always divides K/64."""
+    alike except RESID (at least 5 k-groups per split: o 16); S always divides K/64."""
     L = mi.lib()
     shapes = [(5120, 7168, 20), (5120, 5120, 20), (5120, 34816, 10), (17408, 5120, 34), (5120, 151936, 10)]
     for K, N, want in shapes:
         assert L.mi_gemv_pick_s(K, N) == want
         assert L.mi_gemv_pick_s_ex(K, N, mi.EPI_PARTIALS) == want
-        for epi in (mi.EPI_RESID, mi.EPI_SILU, mi.EPI_LOGITS, mi.EPI_F16OUT):
+        for epi in (mi.EPI_SILU, mi.EPI_LOGITS, mi.EPI_F16OUT):
             assert L.mi_gemv_pick_s_ex(K, N, epi) == want
+    assert L.mi_gemv_pick_s_ex(5120, 5120, mi.EPI_RESID) == 16  # the 27B o
+    assert L.mi_gemv_pick_s_ex(17408, 5120, mi.EPI_RESID) == 34  # the 27B down
     assert L.mi_gemv_pick_s_ex(5120, 7168, mi.EPI_QKV) == 10  # the 27B qkv, fused with attn_prep
     assert L.mi_gemv_pick_s_ex(2048, 4608, mi.EPI_QKV) == 4
     for K in (64, 128, 512, 1024, 3072, 8192, 17408):
