@@ -223,9 +223,10 @@ def pmc_summary(fetch_dir, write_dir):
         m = re.search(r"gemv_w4a16_kernel<\s*\d+,\s*\d+,\s*(\d+)", n)
         return None if m is None else int(m.group(1))
     sha = gemv_source_sha()
-    split = {"qkv": 10, "o": 20, "gate_up": 10, "down": 34, "lm_head": 10}
     shapes = {"qkv": (5120, 7168, 5), "o": (5120, 5120, 1), "gate_up": (5120, 34816, 2), "down": (17408, 5120, 1),
               "lm_head": (5120, 151936, 3)}
+    # the engine's split-K widths (its fused epilogues' choice; the plain sweep launches at the same S)
+    split = {lin: int(mi.lib().mi_gemv_pick_s_ex(K, N, e)) for lin, (K, N, e) in shapes.items()}
     per_step = {"qkv": 64, "o": 64, "gate_up": 64, "down": 64, "lm_head": 1}
     lines = [f"fetch factor {fetch_factor:.4f} (a 2 GiB stream read), write factor {write_factor:.4f} (a 2 GiB "
              f"fill), GEMV sources {sha}", "",
