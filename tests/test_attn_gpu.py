@@ -189,6 +189,33 @@ def test_rows_are_bitwise_their_single_row_steps(kind, QH, KVH, HD, Lm, tgt, pos
     assert np.array_equal(full, again)
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("QH,KVH,HD", [(40, 8, 128), (16, 2, 256)])
+def test_rows_paged_bitwise_contiguous(kind, QH, KVH, HD):
+    """Several rows per work-group over a paged cache (32-position pages, shuffled table):
+    bitwise the contiguous cache, and each row bitwise its one-row launch."""
+    Lm, tgt, pos, M, P = 1024, 8, 761, 8, 32
+    sh = O.attn_shape(QH, KVH, HD)
+    k, v, ks, vs = make_kv(kind, KVH, Lm, HD, 11 + kind)
+    q = np.random.default_rng(12).standard_normal((M, QH, HD)).astype(np.float32)
+    a, _ = gpu_attention(sh, q, kind, k, v, ks, vs, pos, M, tgt)
+    rng = np.random.default_rng(13)
+    pages = rng.permutation(Lm // P).astype(np.uint32)
+    phys = np.concatenate([np.arange(pg * P, pg * P + P) for pg in pages])
+    kp, vp = np.empty_like(k), np.empty_like(v)
+    kp[:, phys], vp[:, phys] = k, v
+    ksp = vsp = None
+    if kind:
+        ksp, vsp = np.empty_like(ks), np.empty_like(vs)
+        ksp[:, phys], vsp[:, phys] = ks, vs
+    b, _ = gpu_attention(sh, q, kind, kp, vp, ksp, vsp, pos, M, tgt, pages, P)
+    assert np.array_equal(a, b)
+    for m in (0, M - 1):
+        one, _ = gpu_attention(sh, np.ascontiguousarray(q[m:m + 1]), kind, kp, vp, ksp, vsp, pos + m, 1, tgt,
+                               pages, P)
+        assert np.array_equal(one[0], b[m]), m
+
+
 def test_reduce_matches_oracle_merge_on_device_partials():
     """attn_reduce_v2's merge on the GPU's own partials: within 1 fp16 ulp of the oracle's
     sequential merge (the device forms the same sum with a common max; exp differs by <= 1
