@@ -9,9 +9,10 @@
 // Rows. The matrix products' columns are (row, q head) pairs, 16 per tile: a plain launch gives
 // a work-group RPW = 16 CT / GQA consecutive rows of the list that share the block size (column
 // c = 16 ct + qi = GQA rr + g is row r_lo + rr, head j GQA + g), so the block's K/V rows are
-// read once for all of them; the CT tiles share every LDS read of K and V^T. Row r sees positions < pos + r + 1: its scores past that are -inf and a group
-// that holds none of its positions leaves its state untouched (alpha 1, weights 0), so each
-// column's values are, operation for operation, those of a one-row work-group for its row.
+// read once for all of them; the CT tiles share every LDS read of K and V^T. Row r sees
+// positions < pos + r + 1: its scores past that are -inf and a group that holds none of its
+// positions leaves its state untouched (alpha 1, weights 0), so each column's values are,
+// operation for operation, those of a one-row work-group for its row.
 //
 // Loads. A wave owns a ring of NB group slots in LDS. A group's 16 K rows and 16 V rows go
 // into a slot with global_load_lds_dwordx4: one instruction moves 1 KB, lane L writing LDS
@@ -26,7 +27,7 @@
 // loads it issued after that group; the loads are issued from inline assembly, which the
 // compiler's own wait insertion does not see, so no load of its own is left outstanding
 // across the loop and every wait inside the loop is this code's.
-// Products, per group, on the matrix cores as in attn_block:
+// Products, per group, on the matrix cores:
 //   scores  S^T = K Q^T (v_mfma_f32_16x16x32_f16): A = 16 K rows read from LDS (lane l: row
 //           l % 16, dims 8 (l / 16) + 32 kk; int8 widened exactly to f16), B = q in f16 high
 //           and low parts;
@@ -36,8 +37,9 @@
 //           positions 4 g .. 4 g + 3 (f16); ds_read_b64_tr_b8 gives the same for two tiles at
 //           once (int8, widened exactly to f16) - and B = the weights (int8: times the row's V
 //           scale) in f16 high and low parts.
-// Every score, weight and product is the one attn_block forms, in the same order; only where
-// the operands come from differs.
+// Each wave's online softmax takes its groups in ascending order, NG groups per step, and the
+// waves merge in wave order; the results are checked against attn_decode_v2's restatement and
+// fp64 attention.
 #pragma once
 #include "attn_core.h"
 
