@@ -371,7 +371,7 @@ __device__ __forceinline__ float lds_seq_sum(const float* p, uint32_t n) {
   return tot;
 }
 
-// MR: row capacity (1, 2, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue;
+// MR: row capacity (1, 2, 3, 4 or 16); U: k-groups whose loads are issued together; EPI: epilogue;
 // NI: the input is the RMSNorm of a residual, formed by each work-group for its slice (while
 // its first weight loads are in flight): every row's rstd from the residual's tile sums, added in
 // tile order from +0 as the RESID consumers add them, then rne((r * rstd) * w) per element -
@@ -799,9 +799,11 @@ template <int EPI>
 int launch_rows(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float* part, uint32_t M,
                 uint32_t K, uint32_t N, uint32_t S, const GemvEpi& epi, hipStream_t st) {
   if (M == 1) return launch_gemv<1, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
-  // two rows: a kernel of their own (94 VGPRs, five waves per SIMD, against the 4-row kernel's
-  // 102 and four: 27B verify step at 2 rows 4.81 -> 4.44 ms)
+  // two and three rows: kernels of their own (94 / 96-99 VGPRs, five waves per SIMD where they
+  // fit 96, against the 4-row kernel's 102 and four: 27B verify step at 2 rows 4.81 -> 4.44 ms,
+  // at 3 rows 5.06 -> 4.88)
   if (M == 2) return launch_gemv<2, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
+  if (M == 3) return launch_gemv<3, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
   if (M <= 4) return launch_gemv<4, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
   return launch_gemv<16, EPI>(qw, sc, x, part, M, K, N, S, epi, st);
 }
