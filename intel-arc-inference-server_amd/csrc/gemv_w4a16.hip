@@ -790,6 +790,8 @@ int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float
   }
   if (gps >= 16)
     gemv_w4a16_kernel<MR, 4, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
+  else if (MR >= 3)  // one k-group per wave at a time: five or six waves per SIMD instead of four
+    gemv_w4a16_kernel<MR, 1, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
   else
     gemv_w4a16_kernel<MR, 2, EPI><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
   return (int)hipGetLastError();
