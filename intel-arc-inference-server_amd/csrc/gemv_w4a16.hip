@@ -784,7 +784,7 @@ int launch_gemv(const uint32_t* qw, const uint16_t* sc, const uint16_t* x, float
   dim3 grid(N / kCols, (EPI == EPI_QKV || e.extra_row) && !epi.arrive ? S + (e.row_cons ? M : 1u) : S);
   if constexpr (EPI == EPI_PARTIALS || EPI == EPI_SILU || EPI == EPI_QKV) {
     if (epi.in_sums) {
-      gemv_w4a16_kernel<MR, 2, EPI, true><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
+      gemv_w4a16_kernel<MR, (MR >= 3 ? 1 : 2), EPI, true><<<grid, 256, 0, st>>>(qw, sc, x, part, M, K, N, gps, e);
       return (int)hipGetLastError();
     }
   }
