@@ -376,8 +376,11 @@ __device__ __forceinline__ float lds_seq_sum(const float* p, uint32_t n) {
 // its first weight loads are in flight): every row's rstd from the residual's tile sums, added in
 // tile order from +0 as the RESID consumers add them, then rne((r * rstd) * w) per element -
 // the RESID kind's x_next bit for bit - into LDS, where the slice reads it.
+// The 16-row kernel with one k-group per wave asks for six waves per SIMD, which it meets in
+// 80 VGPRs without spilling (27B verify at 8 rows 6.47 -> 6.42 ms; at 3 rows the same request
+// measured slower).
 template <int MR, int U, int EPI, bool NI = false>
-__global__ __launch_bounds__(256) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
+__global__ __launch_bounds__(256, (MR == 16 && U == 1 ? 6 : 1)) void gemv_w4a16_kernel(const uint32_t* __restrict__ qweight,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ x,
                                                          float* __restrict__ partials, uint32_t M,
